@@ -1,0 +1,334 @@
+"""Benchmark of the thinker MoE block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Headline workload: one MoE block prefill of 512 tokens (hidden 2048, 64 routed experts of 1408 plus a
+shared expert, softmax top-6, router bias ~ N(0, 0.5) for ragged expert loads). A step is the whole
+block on inputs already resident in HBM: RMSNorm -> router -> align -> grouped gate/up -> down ->
+combine + residual, replayed from one hipGraph. `value` is tokens/s over exactly K timed steps.
+
+Also measured and reported under "extra": decode of 1 token (bf16) as a hipGraph step and per kernel,
+int8 decode at batch 1/2/4/8, the 2048-token Zipf prefill, and the full 28-layer synthetic decode step
+(+ LM head) in one hipGraph. The roofline of the dominant kernel (prefill gate/up) is its algorithmic
+bytes over its average duration from HIP events on its own stream; the CPU baseline is the oracle's
+torch path on a bounded sample of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "ming-voice_amd"), ROOT]
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of extra workloads to run (decode,int8,zipf,full)")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def graph_of(fn, stream):
+    """Captures fn() once into a hipGraph on `stream` (after one eager warm call)."""
+    with torch.cuda.stream(stream):
+        fn()
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    return g
+
+
+def time_graph(g, stream, reps, warmup=2):
+    """Average ms per replay, from HIP events recorded on the replay stream."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_ms(fn, stream, reps=20):
+    """Average duration of the launch(es) in fn: `reps` copies captured in one graph, timed with events."""
+    g = graph_of(lambda: [fn() for _ in range(reps)], stream)
+    return time_graph(g, stream, 5) / reps
+
+
+# ----------------------------------------------------------------------------------------------- prefill
+
+def prefill_setup(b, n, bias, seed):
+    import fused_moe
+    import fused_ops
+    import workloads as W
+    x = W.tokens(n, seed=seed, device="cuda")
+    E1, I, H = b["w_gu"].shape[0], b["w_d"].shape[-1], b["w_d"].shape[1]
+    sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device)
+    st = {}
+
+    def step():
+        xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+        ids, wts, _ = fused_ops.route(xn, b["w32"], bias, top_k=W.TOP_K, scoring="softmax")
+        st["xn"], st["ids"], st["wts"] = xn, ids, wts
+        return fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x, scratch=sc)
+
+    step()
+    torch.cuda.synchronize()
+    return x, sc, st, step
+
+
+def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70):
+    import fused_moe
+    import _mingmoe
+    import workloads as W
+    x, sc, st, step = prefill_setup(b, n, bias, seed)
+    g = graph_of(step, stream)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        stream.synchronize()
+        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    ids = st["ids"]
+    counts = torch.bincount(ids.reshape(-1), minlength=b["w_gu"].shape[0]).cpu()
+    used = int((counts > 0).sum())
+    P = ids.numel()
+
+    def phase(p):
+        return lambda: fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], ids, st["wts"], residual=x,
+                                                   scratch=sc, phases=p, align=False)
+    gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream)
+    dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream)
+    cb_ms = kernel_ms(phase(_mingmoe.MM_PHASE_COMBINE), stream)
+    H, I = W.HIDDEN, W.INTER
+    gu_bytes = used * 2 * I * H * 2 + n * H * 2 + P * I * 2
+    dn_bytes = used * H * I * 2 + P * I * 2 + P * H * 4
+    flops = P * W.flops_per_pair()
+    moe_ms = gu_ms + dn_ms
+    return {
+        "tokens": n, "ms_per_step": ms, "tokens_per_s": n / ms * 1e3, "wall_s": wall,
+        "experts_used": used, "top3_share": float(counts[:-1].sort(descending=True).values[:3].sum() / P),
+        "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3, "combine_us": cb_ms * 1e3,
+        "gate_up_GBs": gu_bytes / gu_ms / 1e6, "down_GBs": dn_bytes / dn_ms / 1e6, "gate_up_bytes": gu_bytes,
+        "mfma_pct": flops / (moe_ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 100,
+        "hbm_pct_weights": used * W.expert_bytes() / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+    }
+
+
+# ------------------------------------------------------------------------------------------------ decode
+
+def decode_metrics(b, n, stream, int8=False, seed=40):
+    import fused_moe
+    import fused_ops
+    import _mingmoe
+    import workloads as W
+    x = W.tokens(n, seed=seed + n, device="cuda")
+    w_gu, w_d = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
+    sgu, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
+    E = b["w32"].shape[0]
+    logits = torch.empty(n, E, device="cuda")
+    ids = torch.empty(n, W.TOP_K + 1, device="cuda", dtype=torch.long)
+    wts = torch.empty(n, W.TOP_K + 1, device="cuda")
+    a_buf = torch.empty(n * (W.TOP_K + 1), W.INTER, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(n, W.HIDDEN, device="cuda", dtype=torch.bfloat16)
+    st = {}
+
+    def step():
+        xn = st["xn"] = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+        fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, ids, wts, scoring="softmax")
+        fused_moe.fused_moe_decode(xn, w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu, s_d=sd, residual=x)
+
+    g = graph_of(step, stream)
+    ms = time_graph(g, stream, 200)
+
+    def phase(p):
+        return lambda: fused_moe.fused_moe_decode(st["xn"], w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu,
+                                                  s_d=sd, residual=x, phases=p)
+    gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream, 50)
+    dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream, 50)
+    uniq = int(torch.unique(ids).numel())
+    H, I = W.HIDDEN, W.INTER
+    es = 1 if int8 else 2
+    sb = 2 if int8 else 0
+    gu_bytes = uniq * (2 * I * H * es + 2 * I * sb)
+    dn_bytes = uniq * (H * I * es + H * sb)
+    return {
+        "tokens": n, "int8": int8, "unique_experts": uniq, "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / n,
+        "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
+        "gate_up_TBs": gu_bytes / gu_ms / 1e9, "down_TBs": dn_bytes / dn_ms / 1e9,
+        "moe_TBs": (gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e9,
+        "layer_TBs": (gu_bytes + dn_bytes) / ms / 1e9,
+        "moe_hbm_pct": (gu_bytes + dn_bytes) / ((gu_ms + dn_ms) * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+    }
+
+
+# ------------------------------------------------------------------------------------- full decode step
+
+def full_decode_metrics(stream, layers=28):
+    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1."""
+    import fastlinear
+    import fused_moe
+    import fused_ops
+    import workloads as W
+    H, dev = W.HIDDEN, "cuda"
+    L = []
+    for li in range(layers):
+        s = 1000 + 16 * li
+        L.append({
+            "ln1": W.normal((H,), 0.02, s, dev, mean=1.0), "q": W.normal((H, H), 0.02, s + 1, dev),
+            "k": W.normal((256, H), 0.02, s + 2, dev), "v": W.normal((256, H), 0.02, s + 3, dev),
+            "o": W.normal((H, H), 0.02, s + 4, dev), "blk": W.block(seed=s + 5, device=dev),
+        })
+    fn = W.normal((H,), 0.02, 999, dev, mean=1.0)
+    head = W.normal((W.VOCAB, H), 0.02, 998, dev)
+    x0 = W.tokens(1, seed=997, device=dev)
+    E = W.EXPERTS
+    logits = torch.empty(1, E, device=dev)
+    ids = torch.empty(1, W.TOP_K + 1, device=dev, dtype=torch.long)
+    wts = torch.empty(1, W.TOP_K + 1, device=dev)
+    a_buf = torch.empty(W.TOP_K + 1, W.INTER, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        h = x0
+        for p in L:
+            xn = fused_ops.rms_norm(h, p["ln1"], W.EPS)
+            q = fastlinear.small_linear(xn, p["q"])
+            fastlinear.small_linear(xn, p["k"])
+            fastlinear.small_linear(xn, p["v"])
+            h = fastlinear.small_linear(q, p["o"], residual=h)  # attention itself is outside the MoE path
+            b = p["blk"]
+            xn = fused_ops.rms_norm(h, b["norm_w"], W.EPS)
+            fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, ids, wts, scoring="softmax")
+            h = fused_moe.fused_moe_decode(xn, b["w_gu"], b["w_d"], ids, wts, a_buf=a_buf, residual=h)
+        return fastlinear.small_linear(h, head, norm=(fn, W.EPS))
+
+    g = graph_of(step, stream)
+    ms = time_graph(g, stream, 20)
+    proj = 28 * (2 * H * H + 2 * 256 * H) * 2
+    moe = 28 * 7 * W.expert_bytes()
+    router = 28 * E * H * 4
+    total = proj + moe + router + W.VOCAB * H * 2
+    del L, head
+    return {"layers": layers, "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
+            "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100}
+
+
+# -------------------------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(b, bias, n_sample=64, reps=2):
+    """The oracle's torch CPU path (RMSNorm, router, per-expert MoE loop, combine) on the first n_sample
+    tokens of the 512-token workload; returns tokens/s and the threads used."""
+    from oracle import moe_oracle as O
+    import workloads as W
+    cpu = {k: b[k].cpu() for k in ("norm_w", "w32", "w_gu", "w_d")}
+    x = W.tokens(512, seed=70, device="cuda")[:n_sample].cpu()
+    bias_c = bias.cpu()
+
+    def run():
+        xn = O.rms_norm(x, cpu["norm_w"], W.EPS)
+        ids, wts = O.router_select(O.router_logits(xn, cpu["w32"]), bias_c, scoring="softmax", top_k=W.TOP_K)
+        return O.moe(xn, cpu["w_gu"], cpu["w_d"], ids, wts, residual=x)
+
+    run()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t)
+    t = sorted(ts)[len(ts) // 2]
+    return {"value": n_sample / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {n_sample} of the 512 tokens, median of {reps} runs after 1 warmup, "
+                      f"{platform.processor() or platform.machine()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the MoE block path has no multi-GPU code in this build "
+              "(use --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import _mingmoe
+    import workloads as W
+    _mingmoe.load()
+    torch.manual_seed(0)
+    stream = torch.cuda.Stream()
+    t0 = time.time()
+    b = W.block(seed=0, device="cuda")
+    bias = W.ragged_bias(device="cuda")
+    torch.cuda.synchronize()
+    log(f"[bench] block ready {time.time() - t0:.1f}s")
+    head = prefill_metrics(b, 512, bias, args.steps, args.warmup, stream)
+    log(f"[bench] prefill 512: {head['tokens_per_s']:.0f} tok/s, gate/up {head['gate_up_us']:.1f} us")
+    extra = {"prefill_512": head}
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda k: not args.quick and (not only or k in only))
+    if want("decode"):
+        extra["decode_bf16_b1"] = decode_metrics(b, 1, stream)
+        log(f"[bench] decode bf16: {extra['decode_bf16_b1']}")
+    if want("int8"):
+        W.quantize_block(b, torch.bfloat16)
+        for n in (1, 2, 4, 8):
+            extra[f"decode_int8_b{n}"] = decode_metrics(b, n, stream, int8=True)
+            log(f"[bench] decode int8 b{n}: {extra[f'decode_int8_b{n}']}")
+        for k in ("q_gu", "q_d", "s_gu", "s_d"):
+            b.pop(k)
+    if want("zipf"):
+        extra["prefill_2048_zipf"] = prefill_metrics(b, 2048, W.zipf_bias(device="cuda"), 10, 2, stream, seed=90)
+        log(f"[bench] zipf: {extra['prefill_2048_zipf']}")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(b, bias)
+        log(f"[bench] cpu baseline: {cpu}")
+    if want("full"):
+        del b
+        torch.cuda.empty_cache()
+        extra["full_decode_28l"] = full_decode_metrics(stream)
+        log(f"[bench] full decode: {extra['full_decode_28l']}")
+    gu_s = head["gate_up_us"] * 1e-6
+    achieved = head["gate_up_bytes"] / gu_s / 1e9
+    line = {
+        "metric": "MoE layer decode us/token + achieved HBM TB/s; MoE prefill tokens/s + MFMA %",
+        "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "thinker MoE block prefill, 512 tokens, hidden 2048, 64+1 experts x 1408, "
+                               "softmax top-6, ragged router bias", "tokens": 512, "hidden": 2048, "experts": 64,
+                   "inter": 1408, "top_k": 6, "graph": True},
+        "roofline": {"bound": "hbm", "kernel": "prefill_gate_up_kernel", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,172 @@
+/*
+ * mingmoe.h — C ABI of libmingmoe.so, the MI355X (gfx950) kernels of the Ming thinker MoE block.
+ *
+ * Every entry point takes raw device pointers, element counts, row strides (in elements), dtype codes,
+ * scalars and a hipStream_t (passed as void*), enqueues its kernels on that stream and returns an int
+ * status (0 = ok). Nothing here allocates, frees or synchronises: scratch buffers are passed in by the
+ * caller, so every call can be captured into a hipGraph. On a nonzero status, mm_last_error() gives
+ * the message of the last failure on the calling thread; launch failures contain the text "HIP error".
+ *
+ * Each entry point names the reference Python interface it replaces (file:line in the Ming Voice
+ * sources); the Python modules fused_ops.py, fused_moe.py and fastlinear.py of this package keep
+ * those signatures and call these functions through ctypes.
+ */
+#ifndef MINGMOE_H
+#define MINGMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MM_ABI_VERSION 1
+
+/* status codes */
+#define MM_OK 0
+#define MM_ERR_ARG 1     /* bad shape, dtype, stride, alignment or null pointer */
+#define MM_ERR_HIP 2     /* a HIP launch failed; message starts with "HIP error" */
+
+/* dtype codes (torch dtypes of the tensors behind the pointers) */
+#define MM_BF16 0
+#define MM_FP16 1
+#define MM_FP32 2
+#define MM_INT8 3
+#define MM_INT32 4
+#define MM_INT64 5
+
+/* router scoring modes */
+#define MM_SCORE_SIGMOID_GROUP 0 /* sigmoid + bias, group-limited top-k (the Ming thinker router) */
+#define MM_SCORE_SOFTMAX 1       /* softmax over (logits + bias), top-k, renormalised */
+
+/* phase masks of mm_moe_decode / mm_moe_prefill (0 = every phase). A later phase run alone reuses the
+ * scratch (a_buf, o_buf) left by an earlier call with the same arguments; this lets a profiler or a
+ * benchmark bracket one kernel with events. */
+#define MM_PHASE_ALL 0
+#define MM_PHASE_GATE_UP 1
+#define MM_PHASE_DOWN 2
+#define MM_PHASE_COMBINE 4
+
+/* small_linear activations */
+#define MM_ACT_NONE 0
+#define MM_ACT_GELU_TANH 1
+#define MM_ACT_SILU 2
+
+/* Stacked expert weights, as the thinker lays them out (engine.py:150-188, 313-391):
+ *   w_gu [n_slots, 2*inter, hidden]  rows 0..inter-1 = gate, inter..2*inter-1 = up
+ *   w_d  [n_slots, hidden, inter]
+ * with the shared expert in the last slot. The last dim must be contiguous and every row 16-byte
+ * aligned. For int8 weights (w_dtype = MM_INT8) s_gu [n_slots, 2*inter] and s_d [n_slots, hidden]
+ * hold one scale per output row (s_dtype MM_FP32 or MM_BF16); for bf16 weights they are NULL. */
+typedef struct mm_experts {
+  const void* w_gu;
+  const void* w_d;
+  const void* s_gu;
+  const void* s_d;
+  int32_t w_dtype;
+  int32_t s_dtype;
+  int64_t n_slots;
+  int64_t hidden;
+  int64_t inter;
+  int64_t gu_stride_e, gu_stride_n; /* element strides of w_gu dims 0 and 1 */
+  int64_t d_stride_e, d_stride_n;   /* element strides of w_d dims 0 and 1 */
+  int64_t sgu_stride_e, sd_stride_e; /* element strides of s_gu / s_d dim 0 */
+} mm_experts;
+
+/* ABI version (MM_ABI_VERSION) and the last error message of this thread (returns its length). */
+int mm_version(void);
+size_t mm_last_error(char* buf, size_t len);
+
+/* RMSNorm, one row per token: y = (w * bf16(x * rsqrt(mean(x^2) + eps))) cast to y_dtype.
+ * Replaces fused_ops.rms_norm / _rms_norm (fused_ops.py:16-37). x, w, y: bf16 / fp16 / fp32. */
+int mm_rms_norm(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t x_row_stride,
+                const void* w, int w_dtype, float eps,
+                void* y, int y_dtype, int64_t y_row_stride, void* stream);
+
+/* MoE router for n_tokens rows: logits = x . w32^T in fp32, then top_k selection and weights.
+ * Replaces fused_ops.moe_route / _gate_gemv / _route (fused_ops.py:40-103) and the multi-token gate
+ * forward (engine.py:326-333).
+ *   scoring MM_SCORE_SIGMOID_GROUP: s = sigmoid(logit); r = s + bias; groups of n_experts/n_group rank
+ *     by the sum of their two largest r; the topk_group best groups stay; top_k of r (ties: lowest
+ *     index); weight = s / (sum s + 1e-20) * scale.
+ *   scoring MM_SCORE_SOFTMAX (n_group must be 1): z = logit + bias; top_k of z (ties: lowest index);
+ *     p = softmax(z); weight = p / (sum p_selected + 1e-20) * scale.
+ * append_shared != 0 writes id n_experts with weight 1.0 after the top_k routed ones (the shared
+ * expert), so each output row holds top_k + 1 entries. bias may be NULL. ids: MM_INT32 / MM_INT64.
+ * logits [n_tokens, n_experts] fp32 (row stride n_experts); ids / wts rows of stride out_row_stride. */
+int mm_router(const void* x, int x_dtype, int64_t n_tokens, int64_t hidden, int64_t x_row_stride,
+              const float* w32, int64_t n_experts, const float* bias,
+              int scoring, int n_group, int topk_group, int top_k, float scale, int append_shared,
+              float* logits, void* ids, int ids_dtype, float* wts, int64_t out_row_stride,
+              void* stream);
+
+/* Selection half of mm_router on logits already in device memory (same semantics and outputs). */
+int mm_router_select(const float* logits, int64_t n_tokens, int64_t n_experts, const float* bias,
+                     int scoring, int n_group, int topk_group, int top_k, float scale, int append_shared,
+                     void* ids, int ids_dtype, float* wts, int64_t out_row_stride, void* stream);
+
+/* Stable counting sort of the P (token, slot) pairs by expert, each expert's run padded to block_m.
+ * Replaces fused_moe._align_blocks (fused_moe.py:154-173), bit-exact:
+ *   sorted_ids [nb*block_m] int32: pair indices grouped by expert in ascending pair order, pad = P;
+ *   bexp [nb] int32: expert of each block, -1 past the last used block;
+ *   nb must equal ceil((P + n_slots*(block_m-1)) / block_m).
+ *   expert_offsets (optional, may be NULL) [n_slots+1] int32: padded start row of each expert and,
+ *   in the last entry, the number of used rows.
+ * flat: MM_INT32 / MM_INT64 expert ids; ids outside [0, n_slots) are dropped. P <= 2^30. */
+int mm_align_blocks(const void* flat, int flat_dtype, int64_t P, int32_t n_slots, int32_t block_m,
+                    int32_t* sorted_ids, int32_t* bexp, int64_t nb, int32_t* expert_offsets,
+                    void* stream);
+
+/* Decode MoE for 1..8 tokens: for each token t and slot k (expert e = ids[t,k]):
+ *   g = bf16(x_t . Wg[e]^T [* s]), u = bf16(x_t . Wu[e]^T [* s]), a = bf16(bf16(silu(g)) * u)
+ *   y_t = bf16(sum_k wts[t,k] * bf16(a . Wd[e]^T [* s]))          (fp32 sum in slot order)
+ *   with residual: y_t = bf16(y_t + residual_t)
+ * Each distinct expert of the batch is streamed from HBM once. Replaces fused_moe.fused_moe_decode /
+ * _moe_gate_up / _moe_down (fused_moe.py:13-83) and, for 2..8 tokens, the prefill kernels the
+ * reference falls back to (engine.py:379-382). n_tokens * nk <= 64.
+ * x, residual, y: bf16. ids: MM_INT32 / MM_INT64 [n_tokens, nk]; wts fp32 [n_tokens, nk].
+ * a_buf: bf16 scratch [n_tokens*nk, inter] (row p = t*nk + k), also an output of the call. */
+int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
+                  const void* ids, int ids_dtype, int64_t nk, int64_t ids_row_stride,
+                  const float* wts, int64_t wts_row_stride,
+                  const void* residual, int64_t res_row_stride,
+                  void* a_buf, void* y, int64_t y_row_stride, int phases, void* stream);
+
+/* Grouped prefill MoE over the blocks produced by mm_align_blocks (same math as mm_moe_decode).
+ * Replaces fused_moe.fused_moe_prefill / _moe_gu_grouped / _moe_down_grouped (fused_moe.py:92-196).
+ * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs
+ * p = t*nk + k whose id lies outside [0, n_slots) contribute nothing); wts fp32 [n_tokens*nk];
+ * sorted_ids / bexp / nb / block_m from mm_align_blocks; a_buf bf16 [n_tokens*nk, inter] and
+ * o_buf fp32 [n_tokens*nk, hidden] are scratch; y bf16 [n_tokens, hidden]. */
+int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
+                   int64_t nk, const void* ids, int ids_dtype, const float* wts,
+                   const int32_t* sorted_ids, const int32_t* bexp, int64_t nb, int32_t block_m,
+                   const void* residual, int64_t res_row_stride,
+                   void* a_buf, float* o_buf, void* y, int64_t y_row_stride, int phases, void* stream);
+
+/* y = act(norm?(x) . W^T + b) [+ residual] for M <= 16 rows.
+ * Replaces fastlinear.small_linear / _small_m_linear (fastlinear.py:123-174) including the rounding
+ * points of its epilogue: bf16 before the activation and before the residual add.
+ * x, w, b, residual, norm_g, y: bf16. norm_g (optional): RMSNorm prologue with norm_eps,
+ * x -> bf16(bf16(x * rstd) * g). b, residual, norm_g may be NULL. act: MM_ACT_*.
+ * xn_buf: bf16 scratch [M, K] used when a norm prologue is given (may be NULL otherwise). */
+int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride,
+                    const void* w, int64_t N, int64_t w_row_stride,
+                    const void* b, int act, const void* residual, int64_t res_row_stride,
+                    const void* norm_g, float norm_eps, void* xn_buf,
+                    void* y, int64_t y_row_stride, void* stream);
+
+/* Symmetric per-row int8: amax = max(max|w|, 1e-8); scale = amax / 127;
+ * q = clamp(round_half_even(w / scale), -127, 127).
+ * Replaces fused_moe.quantize_rows_int8 (fused_moe.py:199-204). w: bf16 / fp16 / fp32 [rows, K];
+ * q int8 [rows, K]; scale [rows] in MM_FP32 (reference) or MM_BF16 (then the scale is rounded to bf16
+ * first and q divides by the rounded value). */
+int mm_quantize_rows_int8(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t w_row_stride,
+                          int8_t* q, int64_t q_row_stride, void* scale, int scale_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINGMOE_H */

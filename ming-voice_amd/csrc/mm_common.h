@@ -1,0 +1,145 @@
+// Shared host and device helpers of libmingmoe (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "mingmoe.h"
+
+// ------------------------------------------------------------------------------------------ host side
+
+namespace mm {
+
+// Records a printf-style message as this thread's last error and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks hipGetLastError() after a launch; returns MM_OK or MM_ERR_HIP with "HIP error: ..." recorded.
+int check_launch(const char* what);
+
+// Size in bytes of a dtype code, 0 when unknown.
+size_t dtype_size(int dtype);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Number of compute units of the current device (queried once per device, thread-safe).
+int cu_count();
+
+}  // namespace mm
+
+#define MM_REQUIRE(cond, ...)                                 \
+  do {                                                        \
+    if (!(cond)) return ::mm::set_error(MM_ERR_ARG, __VA_ARGS__); \
+  } while (0)
+
+#define MM_STREAM(s) (reinterpret_cast<hipStream_t>(s))
+
+// ---------------------------------------------------------------------------------------- device side
+
+namespace mmd {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+// Round-to-nearest-even float -> bf16 (a single v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// Round a float through bf16 and back, the `.to(bfloat16).to(float32)` of the reference kernels.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Typed scalar load / store through dtype tags.
+struct BF16 { typedef uint16_t T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+              static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); } };
+struct FP16 { typedef uint16_t T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return f16_to_f32(p[i]); }
+              static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); } };
+struct FP32 { typedef float T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
+              static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = v; } };
+
+// Scale loads for int8 weights (fp32 or bf16 scale tensors).
+__device__ __forceinline__ float load_scale(const void* s, int s_dtype, int64_t i) {
+  return s_dtype == MM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(s)[i]) : static_cast<const float*>(s)[i];
+}
+
+__device__ __forceinline__ int64_t load_id(const void* ids, int ids_dtype, int64_t i) {
+  return ids_dtype == MM_INT64 ? static_cast<const int64_t*>(ids)[i] : static_cast<int64_t>(static_cast<const int32_t*>(ids)[i]);
+}
+
+// 2 x bf16 (packed in a dword) dot 2 x bf16, accumulated in fp32 (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+// Dot of 8 bf16 weights (uint4) with 8 bf16 activations (uint4).
+__device__ __forceinline__ float dot8_bf16(const uint4& w, const uint4& x, float acc) {
+  acc = dot2_bf16(w.x, x.x, acc);
+  acc = dot2_bf16(w.y, x.y, acc);
+  acc = dot2_bf16(w.z, x.z, acc);
+  acc = dot2_bf16(w.w, x.w, acc);
+  return acc;
+}
+
+// Signed byte b (0..3) of a dword as float (a single SDWA v_cvt_f32_i32 on gfx950).
+__device__ __forceinline__ float sbyte(uint32_t v, int b) { return static_cast<float>(static_cast<int8_t>(v >> (8 * b))); }
+
+// Dot of 4 int8 weights (one dword) with 4 activations given as two packed bf16 pairs.
+__device__ __forceinline__ float dot4_i8_bf16(uint32_t w, uint32_t x01, uint32_t x23, float acc) {
+  acc = fmaf(sbyte(w, 0), __uint_as_float(x01 << 16), acc);
+  acc = fmaf(sbyte(w, 1), __uint_as_float(x01 & 0xffff0000u), acc);
+  acc = fmaf(sbyte(w, 2), __uint_as_float(x23 << 16), acc);
+  acc = fmaf(sbyte(w, 3), __uint_as_float(x23 & 0xffff0000u), acc);
+  return acc;
+}
+
+// Dot of 16 int8 weights (uint4) with 16 bf16 activations (two uint4).
+__device__ __forceinline__ float dot16_i8_bf16(const uint4& w, const uint4& xa, const uint4& xb, float acc) {
+  acc = dot4_i8_bf16(w.x, xa.x, xa.y, acc);
+  acc = dot4_i8_bf16(w.y, xa.z, xa.w, acc);
+  acc = dot4_i8_bf16(w.z, xb.x, xb.y, acc);
+  acc = dot4_i8_bf16(w.w, xb.z, xb.w, acc);
+  return acc;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Butterfly sum over the lanes of a wave (all lanes get the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Arg-max over a wave: largest value, lowest index among equal values. Every lane gets the winner.
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, kWave);
+    int oi = __shfl_xor(idx, o, kWave);
+    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+  }
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+}  // namespace mmd

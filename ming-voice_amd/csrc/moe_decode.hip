@@ -1,0 +1,419 @@
+// Decode MoE for 1..8 tokens (fused_moe.py:13-83): expert-gathered GEMV pair, HBM-bound.
+//
+// Kernel A (gate/up): grid (row tiles of I, distinct experts). Each workgroup finds the distinct experts of
+// the batch from the ids (in first-appearance order), takes the one given by blockIdx.y, and streams its
+// gate and up rows once with 16-byte loads, dotting them with every token routed to that expert.
+//   a[p, r] = bf16(bf16(silu(bf16(g))) * bf16(u)),  g/u = x_t . row (* row scale for int8)
+// Kernel B (down + combine): grid (row tiles of H). Each wave streams the down rows of one distinct
+// expert for the tile, dots them with a[p] of every pair routed there, rounds to bf16 (after the row
+// scale for int8) and parks the result in LDS; the workgroup then sums over slots in order per token:
+//   y[t, h] = bf16(sum_k wts[t,k] * part[t*nk+k, h]) (+ residual, rounded again)
+#include "mm_common.h"
+
+namespace {
+
+using namespace mmd;
+
+constexpr int kMaxPairs = 64;
+
+struct DecodeArgs {
+  const uint16_t* x;
+  int64_t xs;
+  int n_tokens, nk, P;
+  const void* ids;
+  int ids_dtype;
+  int64_t ids_rs;
+  const float* wts;
+  int64_t wts_rs;
+  const void* w_gu;
+  const void* w_d;
+  const void* s_gu;
+  const void* s_d;
+  int s_dtype;
+  int E1;
+  int64_t H, I;
+  int64_t gu_se, gu_sn, d_se, d_sn, sgu_se, sd_se;
+  const uint16_t* res;
+  int64_t res_rs;
+  uint16_t* a_buf;
+  uint16_t* y;
+  int64_t ys;
+};
+
+// Distinct experts of the batch. Lane p < P holds pair p's expert; returns the expert of distinct slot u
+// (or -1 when the batch has fewer distinct experts) and the mask of pairs routed to it.
+__device__ __forceinline__ int distinct_expert(const DecodeArgs& a, int u, unsigned long long& pairs) {
+  const int lane = lane_id();
+  int64_t id = -1;
+  if (lane < a.P) {
+    const int t = lane / a.nk, k = lane - t * a.nk;
+    id = load_id(a.ids, a.ids_dtype, t * a.ids_rs + k);
+    if (id < 0 || id >= a.E1) id = -1;
+  }
+  const int my = static_cast<int>(id);
+  bool first = my >= 0;
+  for (int q = 0; q < a.P; ++q) {
+    const int oq = __shfl(my, q, kWave);
+    if (q < lane && oq == my) first = false;
+  }
+  const unsigned long long fm = __ballot(first);
+  const unsigned long long below = lane == 0 ? 0ull : (fm & ((1ull << lane) - 1ull));
+  const int rank = __popcll(below);
+  const unsigned long long pick = __ballot(first && rank == u);
+  if (pick == 0ull) {
+    pairs = 0ull;
+    return -1;
+  }
+  const int src = __ffsll(static_cast<long long>(pick)) - 1;
+  const int e = __shfl(my, src, kWave);
+  pairs = __ballot(my == e);
+  return e;
+}
+
+// 16-byte chunk c of a weight row holds CE elements; the matching activation chunk is CE bf16 values.
+template <bool Q>
+struct Act {
+  uint4 v[Q ? 2 : 1];
+};
+
+template <bool Q>
+__device__ __forceinline__ void load_act(Act<Q>& o, const uint16_t* row, int64_t c, bool ok) {
+  if (!ok) {
+    o.v[0] = make_uint4(0, 0, 0, 0);
+    if (Q) o.v[Q ? 1 : 0] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const uint4* p = reinterpret_cast<const uint4*>(row + c * (Q ? 16 : 8));
+  o.v[0] = p[0];
+  if (Q) o.v[Q ? 1 : 0] = p[1];
+}
+
+template <bool Q>
+__device__ __forceinline__ float dot_chunk(const uint4& w, const Act<Q>& x, float acc) {
+  if constexpr (Q) return dot16_i8_bf16(w, x.v[0], x.v[Q ? 1 : 0], acc);
+  else return dot8_bf16(w, x.v[0], acc);
+}
+
+__device__ __forceinline__ uint4 load_w(const void* base, int64_t byte_off, bool ok) {
+  if (!ok) return make_uint4(0, 0, 0, 0);
+  return *reinterpret_cast<const uint4*>(static_cast<const char*>(base) + byte_off);
+}
+
+// ------------------------------------------------------------------------------------------- kernel A
+
+template <bool Q, int LPR, int NC, int R, int MAXT>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
+  unsigned long long pairs;
+  const int e = distinct_expert(a, blockIdx.y, pairs);
+  if (e < 0) return;
+  constexpr int ES = Q ? 1 : 2;        // weight bytes per element
+  constexpr int GPW = kWave / LPR;      // row pairs per wave per step
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  const int g = lane / LPR, s = lane % LPR;
+  const int64_t nch = a.H * ES / 16;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GPW * R);
+  const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
+
+  while (pairs) {
+    // up to MAXT pairs of this expert
+    int pid[MAXT];
+    int cntp = 0;
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) {
+      pid[t] = -1;
+      if (pairs) {
+        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+        pairs &= pairs - 1ull;
+        pid[t] = p;
+        cntp = t + 1;
+      }
+    }
+    float accg[R][MAXT], accu[R][MAXT];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) accg[i][t] = accu[i][t] = 0.f;
+    // one pass over the row unless it is longer than LPR * NC chunks
+    for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {
+      Act<Q> xa[MAXT][NC];
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        const int tok = pid[t] >= 0 ? pid[t] / a.nk : 0;
+        const uint16_t* xr = a.x + tok * a.xs;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+          load_act<Q>(xa[t][j], xr, c, t < cntp && c < nch);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+        const bool rok = r < a.I;
+        uint4 wg[NC], wu[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+          const bool ok = rok && c < nch;
+          wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
+          wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
+        }
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+          if (t < cntp) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+              accg[i][t] = dot_chunk<Q>(wg[j], xa[t][j], accg[i][t]);
+              accu[i][t] = dot_chunk<Q>(wu[j], xa[t][j], accu[i][t]);
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+      const bool rok = r < a.I;
+      float sg = 1.f, su = 1.f;
+      if (Q && rok) {
+        sg = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + r);
+        su = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + a.I + r);
+      }
+#pragma unroll
+      for (int t = 0; t < MAXT; ++t) {
+        if (t < cntp) {
+          float ag = group_sum<LPR>(accg[i][t]);
+          float au = group_sum<LPR>(accu[i][t]);
+          if (s == 0 && rok) {
+            if (Q) { ag *= sg; au *= su; }
+            const float gg = round_bf16(ag), uu = round_bf16(au);
+            const float act = round_bf16(silu(gg));
+            a.a_buf[static_cast<int64_t>(pid[t]) * a.I + r] = f32_to_bf16(act * uu);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------- kernel B
+
+constexpr int kDownWaves = 8;
+
+template <bool Q, int LPR, int NC>
+__global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs a) {
+  constexpr int ES = Q ? 1 : 2;
+  constexpr int RW = kWave / LPR;  // output rows per workgroup
+  __shared__ float part[kMaxPairs][RW];
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  const int g = lane / LPR, s = lane % LPR;
+  const int64_t h = static_cast<int64_t>(blockIdx.x) * RW + g;
+  const bool hok = h < a.H;
+  const int64_t nch = a.I * ES / 16;
+
+  for (int i = threadIdx.x; i < kMaxPairs * RW; i += blockDim.x) (&part[0][0])[i] = 0.f;
+  __syncthreads();
+
+  for (int u = wave;; u += kDownWaves) {
+    unsigned long long pairs;
+    const int e = distinct_expert(a, u, pairs);
+    if (e < 0) break;
+    const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
+    float sc = 1.f;
+    if (Q && hok) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + h);
+    if (nch <= static_cast<int64_t>(LPR) * NC) {
+      // the whole row fits one pass: load the weights once for every pair of the expert
+      uint4 w[NC];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t c = s + static_cast<int64_t>(LPR) * j;
+        w[j] = load_w(wbase, h * a.d_sn * ES + c * 16, hok && c < nch);
+      }
+      while (pairs) {
+        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+        pairs &= pairs - 1ull;
+        const uint16_t* ar = a.a_buf + static_cast<int64_t>(p) * a.I;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int64_t c = s + static_cast<int64_t>(LPR) * j;
+          Act<Q> av;
+          load_act<Q>(av, ar, c, c < nch);
+          acc = dot_chunk<Q>(w[j], av, acc);
+        }
+        acc = group_sum<LPR>(acc);
+        if (s == 0 && hok) part[p][g] = round_bf16(Q ? acc * sc : acc);
+      }
+    } else {
+      // long rows: passes of LPR * NC chunks per pair (weights re-read from cache for later pairs)
+      while (pairs) {
+        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+        pairs &= pairs - 1ull;
+        const uint16_t* ar = a.a_buf + static_cast<int64_t>(p) * a.I;
+        float acc = 0.f;
+        for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+            const uint4 w = load_w(wbase, h * a.d_sn * ES + c * 16, hok && c < nch);
+            Act<Q> av;
+            load_act<Q>(av, ar, c, c < nch);
+            acc = dot_chunk<Q>(w, av, acc);
+          }
+        }
+        acc = group_sum<LPR>(acc);
+        if (s == 0 && hok) part[p][g] = round_bf16(Q ? acc * sc : acc);
+      }
+    }
+  }
+  __syncthreads();
+
+  // combine: one thread per (token, row), slots summed in order
+  const int tid = threadIdx.x;
+  if (tid < a.n_tokens * RW) {
+    const int t = tid / RW, r = tid % RW;
+    const int64_t hh = static_cast<int64_t>(blockIdx.x) * RW + r;
+    if (hh < a.H) {
+      float acc = 0.f;
+      for (int k = 0; k < a.nk; ++k) acc = fmaf(a.wts[t * a.wts_rs + k], part[t * a.nk + k][r], acc);
+      float out = round_bf16(acc);
+      if (a.res) out = out + bf16_to_f32(a.res[t * a.res_rs + hh]);
+      a.y[t * a.ys + hh] = f32_to_bf16(out);
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------------- launch
+
+template <bool Q, int LPR, int NC, int R, int MAXT>
+int launch_a(const DecodeArgs& a, hipStream_t st) {
+  constexpr int rows_per_wg = 4 * (kWave / LPR) * R;
+  dim3 grid(static_cast<unsigned>((a.I + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(min(a.P, a.E1)));
+  hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT>), grid, dim3(256), 0, st, a);
+  return mm::check_launch("moe_decode gate_up");
+}
+
+template <bool Q, int LPR, int NC>
+int launch_b(const DecodeArgs& a, hipStream_t st) {
+  constexpr int RW = kWave / LPR;
+  dim3 grid(static_cast<unsigned>((a.H + RW - 1) / RW));
+  hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC>), grid, dim3(kDownWaves * 64), 0, st, a);
+  return mm::check_launch("moe_decode down");
+}
+
+// Template choice. A row of nch 16-byte chunks is split over LPR lanes with NC chunks per lane per
+// pass; rows longer than LPR * NC chunks take several passes, so a few instances cover every shape.
+template <bool Q, int LPR, int NC>
+int dispatch_a_t(const DecodeArgs& a, hipStream_t st) {
+  const int maxt = a.n_tokens;  // pairs of one expert: one per token unless a token repeats an expert
+  if (maxt <= 1) return launch_a<Q, LPR, NC, 2, 1>(a, st);
+  if (maxt <= 2) return launch_a<Q, LPR, NC, 2, 2>(a, st);
+  if (maxt <= 4) return launch_a<Q, LPR, NC, 1, 4>(a, st);
+  return launch_a<Q, LPR, NC, 1, 8>(a, st);
+}
+
+template <bool Q>
+int dispatch_a(const DecodeArgs& a, hipStream_t st) {
+  const int64_t nch = a.H * (Q ? 1 : 2) / 16;  // gate/up rows run over the hidden dim
+  if (nch < 64) return dispatch_a_t<Q, 16, 4>(a, st);
+  if (nch <= 128) return dispatch_a_t<Q, 64, 2>(a, st);
+  if (nch <= 192) return dispatch_a_t<Q, 64, 3>(a, st);
+  return dispatch_a_t<Q, 64, 4>(a, st);
+}
+
+template <bool Q>
+int dispatch_b(const DecodeArgs& a, hipStream_t st) {
+  const int64_t nch = a.I * (Q ? 1 : 2) / 16;  // down rows run over the intermediate dim
+  if (nch >= 128) return launch_b<Q, 16, 12>(a, st);
+  if (nch > 32) return launch_b<Q, 8, 12>(a, st);
+  return launch_b<Q, 8, 4>(a, st);
+}
+
+}  // namespace
+
+namespace mm {
+
+// Validates the stacked expert descriptor for the 16-byte-chunk kernels.
+int check_experts(const char* who, const mm_experts* ex) {
+  MM_REQUIRE(ex, "%s: null expert descriptor", who);
+  MM_REQUIRE(ex->w_dtype == MM_BF16 || ex->w_dtype == MM_INT8, "%s: expert weights must be bf16 or int8", who);
+  const int64_t es = ex->w_dtype == MM_INT8 ? 1 : 2;
+  MM_REQUIRE(ex->w_gu && ex->w_d, "%s: null expert weights", who);
+  MM_REQUIRE(ex->n_slots >= 1 && ex->hidden > 0 && ex->inter > 0, "%s: bad expert shape", who);
+  MM_REQUIRE((ex->hidden * es) % 16 == 0 && (ex->inter * es) % 16 == 0,
+             "%s: hidden=%lld and inter=%lld must be multiples of %lld elements (16-byte rows)", who,
+             (long long)ex->hidden, (long long)ex->inter, (long long)(16 / es));
+  MM_REQUIRE(ex->gu_stride_n >= ex->hidden && ex->gu_stride_e >= 2 * ex->inter * ex->gu_stride_n,
+             "%s: w_gu strides do not describe [E, 2I, H] with a contiguous last dim", who);
+  MM_REQUIRE(ex->d_stride_n >= ex->inter && ex->d_stride_e >= ex->hidden * ex->d_stride_n,
+             "%s: w_d strides do not describe [E, H, I] with a contiguous last dim", who);
+  MM_REQUIRE(aligned16(ex->w_gu) && aligned16(ex->w_d) && (ex->gu_stride_n * es) % 16 == 0 &&
+                 (ex->gu_stride_e * es) % 16 == 0 && (ex->d_stride_n * es) % 16 == 0 && (ex->d_stride_e * es) % 16 == 0,
+             "%s: expert weight rows must be 16-byte aligned", who);
+  if (ex->w_dtype == MM_INT8) {
+    MM_REQUIRE(ex->s_gu && ex->s_d, "%s: int8 experts need s_gu and s_d", who);
+    MM_REQUIRE(ex->s_dtype == MM_FP32 || ex->s_dtype == MM_BF16, "%s: scales must be fp32 or bf16", who);
+    MM_REQUIRE(ex->sgu_stride_e >= 2 * ex->inter && ex->sd_stride_e >= ex->hidden, "%s: bad scale strides", who);
+  }
+  return MM_OK;
+}
+
+}  // namespace mm
+
+extern "C" int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
+                             const void* ids, int ids_dtype, int64_t nk, int64_t ids_row_stride, const float* wts,
+                             int64_t wts_row_stride, const void* residual, int64_t res_row_stride, void* a_buf, void* y,
+                             int64_t y_row_stride, int phases, void* stream) {
+  int rc = mm::check_experts("moe_decode", ex);
+  if (rc) return rc;
+  MM_REQUIRE(n_tokens >= 1 && nk >= 1 && n_tokens * nk <= kMaxPairs,
+             "moe_decode: n_tokens * nk must be in [1, %d] (got %lld x %lld)", kMaxPairs, (long long)n_tokens,
+             (long long)nk);
+  MM_REQUIRE(x && ids && wts && a_buf && y, "moe_decode: null pointer");
+  MM_REQUIRE(ids_dtype == MM_INT32 || ids_dtype == MM_INT64, "moe_decode: ids must be int32 or int64");
+  MM_REQUIRE(x_row_stride >= ex->hidden && y_row_stride >= ex->hidden, "moe_decode: row stride smaller than hidden");
+  MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0, "moe_decode: x rows must be 16-byte aligned");
+  MM_REQUIRE(mm::aligned16(a_buf), "moe_decode: a_buf must be 16-byte aligned");
+  MM_REQUIRE(ids_row_stride >= nk && wts_row_stride >= nk, "moe_decode: ids/wts row stride smaller than nk");
+  MM_REQUIRE(!residual || res_row_stride >= ex->hidden, "moe_decode: residual row stride smaller than hidden");
+  MM_REQUIRE(ex->n_slots <= 0x7fffffff && ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "moe_decode: shape too large");
+  DecodeArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.xs = x_row_stride;
+  a.n_tokens = static_cast<int>(n_tokens);
+  a.nk = static_cast<int>(nk);
+  a.P = static_cast<int>(n_tokens * nk);
+  a.ids = ids;
+  a.ids_dtype = ids_dtype;
+  a.ids_rs = ids_row_stride;
+  a.wts = wts;
+  a.wts_rs = wts_row_stride;
+  a.w_gu = ex->w_gu;
+  a.w_d = ex->w_d;
+  a.s_gu = ex->s_gu;
+  a.s_d = ex->s_d;
+  a.s_dtype = ex->s_dtype;
+  a.E1 = static_cast<int>(ex->n_slots);
+  a.H = ex->hidden;
+  a.I = ex->inter;
+  a.gu_se = ex->gu_stride_e;
+  a.gu_sn = ex->gu_stride_n;
+  a.d_se = ex->d_stride_e;
+  a.d_sn = ex->d_stride_n;
+  a.sgu_se = ex->sgu_stride_e;
+  a.sd_se = ex->sd_stride_e;
+  a.res = static_cast<const uint16_t*>(residual);
+  a.res_rs = res_row_stride;
+  a.a_buf = static_cast<uint16_t*>(a_buf);
+  a.y = static_cast<uint16_t*>(y);
+  a.ys = y_row_stride;
+  hipStream_t st = MM_STREAM(stream);
+  const bool q = ex->w_dtype == MM_INT8;
+  if (phases == MM_PHASE_ALL) phases = MM_PHASE_GATE_UP | MM_PHASE_DOWN;
+  if (phases & MM_PHASE_GATE_UP) {
+    rc = q ? dispatch_a<true>(a, st) : dispatch_a<false>(a, st);
+    if (rc) return rc;
+  }
+  if (phases & MM_PHASE_DOWN) return q ? dispatch_b<true>(a, st) : dispatch_b<false>(a, st);
+  return MM_OK;
+}

@@ -1,0 +1,361 @@
+// MoE router: fp32 logits GEMV/GEMM and top-k selection (fused_ops.py:40-103, engine.py:326-333).
+#include "mm_common.h"
+
+namespace {
+
+using namespace mmd;
+
+constexpr int kMaxExperts = 1024;      // per-lane slots = kMaxExperts / 64
+constexpr int kSlots = kMaxExperts / kWave;
+
+template <class TX>
+__device__ __forceinline__ float4 load4(const typename TX::T* p, int64_t i) {
+  return make_float4(TX::ld(p, i), TX::ld(p, i + 1), TX::ld(p, i + 2), TX::ld(p, i + 3));
+}
+
+// logits for up to 8 tokens: one wave per expert, lanes stride over the hidden dim 4 floats at a time.
+template <class TX>
+__global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
+                                                          int64_t xs, const float* __restrict__ w32, int E,
+                                                          float* __restrict__ logits) {
+  const int e = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (e >= E) return;
+  const int lane = lane_id();
+  const float* wr = w32 + static_cast<int64_t>(e) * H;
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+  const bool vec = (H & 3) == 0;
+  if (vec) {
+    for (int64_t h = 4 * lane; h < H; h += 4 * kWave) {
+      const float4 wv = *reinterpret_cast<const float4*>(wr + h);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (t < n_tokens) {
+          const float4 xv = load4<TX>(x + t * xs, h);
+          acc[t] = fmaf(xv.x, wv.x, acc[t]);
+          acc[t] = fmaf(xv.y, wv.y, acc[t]);
+          acc[t] = fmaf(xv.z, wv.z, acc[t]);
+          acc[t] = fmaf(xv.w, wv.w, acc[t]);
+        }
+      }
+    }
+  } else {
+    for (int64_t h = lane; h < H; h += kWave) {
+      const float wv = wr[h];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (t < n_tokens) acc[t] = fmaf(TX::ld(x + t * xs, h), wv, acc[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < n_tokens) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) logits[static_cast<int64_t>(t) * E + e] = v;
+    }
+  }
+}
+
+// logits for many tokens: 64 tokens x 64 experts per workgroup, fp32 register tiles over LDS k-slabs.
+constexpr int kTM = 64, kTE = 64, kTK = 16;
+
+template <class TX>
+__global__ __launch_bounds__(256) void router_gemm_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
+                                                          int64_t xs, const float* __restrict__ w32, int E,
+                                                          float* __restrict__ logits) {
+  __shared__ float xsm[kTK][kTM + 4];
+  __shared__ float wsm[kTK][kTE + 4];
+  const int t0 = blockIdx.y * kTM, e0 = blockIdx.x * kTE;
+  const int tid = threadIdx.x;
+  const int ty = tid / 16, tx = tid % 16;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  for (int64_t k0 = 0; k0 < H; k0 += kTK) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int idx = tid + 256 * r;  // 0..1023 over a 64 x 16 tile
+      const int row = idx / kTK, kk = idx % kTK;
+      const int64_t k = k0 + kk;
+      const int t = t0 + row, e = e0 + row;
+      xsm[kk][row] = (t < n_tokens && k < H) ? TX::ld(x + static_cast<int64_t>(t) * xs, k) : 0.f;
+      wsm[kk][row] = (e < E && k < H) ? w32[static_cast<int64_t>(e) * H + k] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kTK; ++kk) {
+      float xv[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[i] = xsm[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[j] = wsm[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = t0 + ty * 4 + i;
+    if (t >= n_tokens) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = e0 + tx * 4 + j;
+      if (e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i][j];
+    }
+  }
+}
+
+struct SelectArgs {
+  const float* logits;
+  int n_tokens, E;
+  const float* bias;
+  int scoring, n_group, topk_group, top_k;
+  float scale;
+  int append_shared;
+  void* ids;
+  int ids_dtype;
+  float* wts;
+  int64_t out_stride;
+};
+
+// Arg-max over the lane-held slots then across the wave; lowest expert index wins ties.
+__device__ __forceinline__ void slots_argmax(const float (&v)[kSlots], int nslots, float& best, int& bidx) {
+  // Slot 0 seeds the search so that an all -inf input still yields the lowest index, as an
+  // arg-max with first-index ties does. Slots past the valid range hold -inf and larger indices.
+  const int lane = lane_id();
+  best = v[0];
+  bidx = lane;
+#pragma unroll
+  for (int j = 1; j < kSlots; ++j) {
+    if (j < nslots && v[j] > best) { best = v[j]; bidx = lane + kWave * j; }
+  }
+  wave_argmax(best, bidx);
+}
+
+// One wave per token: selection, weights and the optional shared-expert slot.
+__global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
+  __shared__ float rbuf[4][kMaxExperts];
+  const int wv = threadIdx.x / kWave;
+  const int t = blockIdx.x * 4 + wv;
+  if (t >= a.n_tokens) return;
+  const int lane = lane_id();
+  const int E = a.E;
+  const int nslots = (E + kWave - 1) / kWave;
+  const float* lg = a.logits + static_cast<int64_t>(t) * E;
+  float score[kSlots], key[kSlots];  // score: weight source; key: selection value
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const int e = lane + kWave * j;
+    score[j] = 0.f;
+    key[j] = -INFINITY;
+    if (j < nslots && e < E) {
+      const float l = lg[e];
+      const float b = a.bias ? a.bias[e] : 0.f;
+      if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
+        score[j] = 1.0f / (1.0f + __expf(-l));
+        key[j] = score[j] + b;
+      } else {
+        key[j] = l + b;
+      }
+    }
+  }
+  if (a.scoring == MM_SCORE_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) m = fmaxf(m, key[j]);
+    m = wave_max(m);
+    float den = 0.f;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E) {
+        score[j] = __expf(key[j] - m);
+        den += score[j];
+      }
+    }
+    den = wave_sum(den);
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) score[j] = score[j] / den;
+  } else if (a.n_group > 1) {
+    // group score = sum of the two largest keys of the group (first max excluded once)
+    const int G = a.n_group, GS = E / G;
+    float* r = rbuf[wv];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E) r[e] = key[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float gscore[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int g = lane + kWave * j;
+      gscore[j] = -INFINITY;
+      if (g < G) {
+        float m1 = -INFINITY;
+        int a1 = 0;
+        for (int i = 0; i < GS; ++i) {
+          const float v = r[g * GS + i];
+          if (v > m1 || i == 0) { m1 = v; a1 = i; }
+        }
+        float m2 = -INFINITY;
+        for (int i = 0; i < GS; ++i)
+          if (i != a1) m2 = fmaxf(m2, r[g * GS + i]);
+        gscore[j] = m1 + m2;
+      }
+    }
+    // keep the topk_group best groups (iterative arg-max, lowest group index on ties)
+    bool keep[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) keep[j] = false;
+    for (int it = 0; it < a.topk_group; ++it) {
+      float bv;
+      int bi;
+      slots_argmax(gscore, kSlots, bv, bi);
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j)
+        if (lane + kWave * j == bi) { keep[j] = true; gscore[j] = -INFINITY; }
+    }
+    // broadcast the kept-group flags through LDS and mask the keys of dropped groups
+    __builtin_amdgcn_wave_barrier();
+    float* kf = rbuf[wv];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int g = lane + kWave * j;
+      if (g < G) kf[g] = keep[j] ? 1.f : 0.f;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E && kf[e / GS] == 0.f) key[j] = -INFINITY;
+    }
+  }
+  // top_k by iterative arg-max on the keys; weights come from the scores
+  float sel_w = 0.f;  // lane k holds the score of the k-th pick
+  int sel_e = 0;
+  float total = 0.f;
+  for (int k = 0; k < a.top_k; ++k) {
+    float bv;
+    int bi;
+    slots_argmax(key, nslots, bv, bi);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j)
+      if (lane + kWave * j == bi) { s = score[j]; key[j] = -INFINITY; }
+    s = wave_sum(s);  // exactly one lane contributes
+    total += s;
+    if (lane == k) { sel_w = s; sel_e = bi; }
+  }
+  const int64_t o = static_cast<int64_t>(t) * a.out_stride;
+  float w = 0.f;
+  int id = 0;
+  bool write = false;
+  if (lane < a.top_k) {
+    w = sel_w / (total + 1e-20f) * a.scale;
+    id = sel_e;
+    write = true;
+  } else if (lane == a.top_k && a.append_shared) {
+    w = 1.0f;
+    id = E;
+    write = true;
+  }
+  if (write) {
+    a.wts[o + lane] = w;
+    if (a.ids_dtype == MM_INT64) static_cast<int64_t*>(a.ids)[o + lane] = id;
+    else static_cast<int32_t*>(a.ids)[o + lane] = id;
+  }
+}
+
+int check_select(int64_t n_tokens, int64_t E, int scoring, int n_group, int topk_group, int top_k, int append_shared,
+                 const void* ids, int ids_dtype, const float* wts, int64_t out_row_stride) {
+  MM_REQUIRE(n_tokens >= 0 && n_tokens <= 0x7fffffffLL, "router: bad token count %lld", (long long)n_tokens);
+  MM_REQUIRE(E >= 1 && E <= kMaxExperts, "router: n_experts must be in [1, %d], got %lld", kMaxExperts, (long long)E);
+  MM_REQUIRE(top_k >= 1 && top_k <= E && top_k + (append_shared ? 1 : 0) <= kWave,
+             "router: top_k=%d out of range for %lld experts", top_k, (long long)E);
+  MM_REQUIRE(scoring == MM_SCORE_SIGMOID_GROUP || scoring == MM_SCORE_SOFTMAX, "router: unknown scoring mode %d", scoring);
+  MM_REQUIRE(n_group >= 1 && E % n_group == 0 && n_group <= kMaxExperts, "router: n_group=%d must divide n_experts=%lld",
+             n_group, (long long)E);
+  MM_REQUIRE(scoring == MM_SCORE_SIGMOID_GROUP || n_group == 1, "router: softmax scoring takes n_group=1 (got %d)", n_group);
+  MM_REQUIRE(topk_group >= 1 && topk_group <= n_group, "router: topk_group=%d must be in [1, n_group=%d]", topk_group, n_group);
+  MM_REQUIRE(static_cast<int64_t>(topk_group) * (E / n_group) >= top_k,
+             "router: top_k=%d exceeds the experts of the kept groups (%lld)", top_k,
+             (long long)(static_cast<int64_t>(topk_group) * (E / n_group)));
+  MM_REQUIRE(ids_dtype == MM_INT32 || ids_dtype == MM_INT64, "router: ids dtype must be int32 or int64");
+  MM_REQUIRE(ids && wts, "router: null output pointer");
+  MM_REQUIRE(out_row_stride >= top_k + (append_shared ? 1 : 0), "router: output row stride %lld too small",
+             (long long)out_row_stride);
+  return MM_OK;
+}
+
+int launch_select(const float* logits, int64_t n_tokens, int64_t E, const float* bias, int scoring, int n_group,
+                  int topk_group, int top_k, float scale, int append_shared, void* ids, int ids_dtype, float* wts,
+                  int64_t out_row_stride, hipStream_t s) {
+  SelectArgs a{logits, static_cast<int>(n_tokens), static_cast<int>(E), bias, scoring, n_group, topk_group, top_k,
+               scale, append_shared, ids, ids_dtype, wts, out_row_stride};
+  const unsigned blocks = static_cast<unsigned>((n_tokens + 3) / 4);
+  hipLaunchKernelGGL(router_select_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return mm::check_launch("router_select");
+}
+
+template <class TX>
+int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const float* w32, int64_t E, float* logits,
+                  hipStream_t s) {
+  const auto* xp = static_cast<const typename TX::T*>(x);
+  if (n_tokens <= 8) {
+    hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>((E + 3) / 4)), dim3(256), 0, s, xp,
+                       static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits);
+  } else {
+    dim3 grid(static_cast<unsigned>((E + kTE - 1) / kTE), static_cast<unsigned>((n_tokens + kTM - 1) / kTM));
+    hipLaunchKernelGGL(router_gemm_kernel<TX>, grid, dim3(256), 0, s, xp, static_cast<int>(n_tokens), H, xs, w32,
+                       static_cast<int>(E), logits);
+  }
+  return mm::check_launch("router_logits");
+}
+
+}  // namespace
+
+extern "C" int mm_router_select(const float* logits, int64_t n_tokens, int64_t n_experts, const float* bias, int scoring,
+                                int n_group, int topk_group, int top_k, float scale, int append_shared, void* ids,
+                                int ids_dtype, float* wts, int64_t out_row_stride, void* stream) {
+  int rc = check_select(n_tokens, n_experts, scoring, n_group, topk_group, top_k, append_shared, ids, ids_dtype, wts,
+                        out_row_stride);
+  if (rc) return rc;
+  MM_REQUIRE(logits, "router_select: null logits");
+  if (n_tokens == 0) return MM_OK;
+  return launch_select(logits, n_tokens, n_experts, bias, scoring, n_group, topk_group, top_k, scale, append_shared,
+                       ids, ids_dtype, wts, out_row_stride, MM_STREAM(stream));
+}
+
+extern "C" int mm_router(const void* x, int x_dtype, int64_t n_tokens, int64_t hidden, int64_t x_row_stride,
+                         const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                         int topk_group, int top_k, float scale, int append_shared, float* logits, void* ids,
+                         int ids_dtype, float* wts, int64_t out_row_stride, void* stream) {
+  int rc = check_select(n_tokens, n_experts, scoring, n_group, topk_group, top_k, append_shared, ids, ids_dtype, wts,
+                        out_row_stride);
+  if (rc) return rc;
+  MM_REQUIRE(x && w32 && logits, "router: null pointer");
+  MM_REQUIRE(hidden > 0 && x_row_stride >= hidden, "router: bad hidden size %lld / stride %lld", (long long)hidden,
+             (long long)x_row_stride);
+  if (n_tokens == 0) return MM_OK;
+  hipStream_t s = MM_STREAM(stream);
+  switch (x_dtype) {
+    case MM_BF16: rc = launch_logits<BF16>(x, n_tokens, hidden, x_row_stride, w32, n_experts, logits, s); break;
+    case MM_FP16: rc = launch_logits<FP16>(x, n_tokens, hidden, x_row_stride, w32, n_experts, logits, s); break;
+    case MM_FP32: rc = launch_logits<FP32>(x, n_tokens, hidden, x_row_stride, w32, n_experts, logits, s); break;
+    default: return mm::set_error(MM_ERR_ARG, "router: unsupported x dtype %d", x_dtype);
+  }
+  if (rc) return rc;
+  return launch_select(logits, n_tokens, n_experts, bias, scoring, n_group, topk_group, top_k, scale, append_shared, ids,
+                       ids_dtype, wts, out_row_stride, s);
+}

@@ -1,0 +1,217 @@
+"""Fused MoE for the Ming thinker on hand-written gfx950 HIP kernels (drop-in for the reference fused_moe.py).
+
+Experts (plus the shared expert, stored as expert index E) live in stacked tensors w_gu [E+1, 2I, H]
+(gate rows, then up rows) and w_d [E+1, H, I], bf16 or int8 with per-output-row scales.
+
+  fused_moe_decode   1..8 tokens: expert-gathered GEMV pair streaming each distinct expert once
+                     (fused_moe.py:67-83)
+  fused_moe_prefill  N tokens: on-GPU align into 64-row expert blocks, grouped MFMA gate/up and down GEMMs,
+                     ordered per-token combine (fused_moe.py:176-196); N <= 8 takes the decode kernels
+  _align_blocks      the stable counting sort behind prefill, bit-exact with the reference (fused_moe.py:154-173)
+  quantize_rows_int8 symmetric per-row int8 (fused_moe.py:199-204)
+
+CFG and GCFG are kept for callers that read or tune them; the HIP kernels choose their own tiles, so the
+values are advisory.
+"""
+import time
+
+import torch
+
+import _mingmoe as _mm
+
+__all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "CFG", "GCFG"]
+
+CFG = dict(A=dict(BN=16, BK=256, num_warps=4), B=dict(BN=16, BK=256, num_warps=4))
+GCFG = dict(A=dict(BM=64, BN=64, BK=64, num_warps=4), B=dict(BM=64, BN=128, BK=64, num_warps=4))
+
+BLOCK_M = 64        # rows per expert block in prefill (align padding)
+MAX_DECODE_TOKENS = 8
+_MAX_PAIRS = 64
+
+
+def _flat_ids(ids):
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"ids must be int32 or int64 (got {ids.dtype})")
+    return ids if ids.is_contiguous() else ids.contiguous()
+
+
+def fused_moe_decode(x, w_gu, w_d, ids, weights, a_buf=None, out=None, s_gu=None, s_d=None, *, residual=None,
+                     phases=_mm.MM_PHASE_ALL):
+    """x: [1, H] bf16 ([N, H] with N <= 8 also accepted); ids: [NK] (or [N, NK]) expert ids, shared expert
+    included; weights: same shape, fp32. w_gu/w_d are bf16, or int8 with row scales s_gu [E+1, 2I] /
+    s_d [E+1, H] (fp32 or bf16). Returns y [N, H] bf16 = sum_k weights[k] * expert_k(x) (+ residual).
+    phases (default all) selects the gate/up and/or down kernel, for timing one of them."""
+    _mm.require_gpu(x, w_gu, w_d, ids, weights, a_buf, out, s_gu, s_d, residual)
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    N = x2.shape[0]
+    ids2 = _flat_ids(ids).reshape(N, -1)
+    NK = ids2.shape[1]
+    if weights.dtype != torch.float32:
+        weights = weights.float()
+    wts2 = weights.reshape(N, NK)
+    if not wts2.is_contiguous():
+        wts2 = wts2.contiguous()
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"fused_moe_decode: x must be bf16 (got {x.dtype})")
+    if N * NK > _MAX_PAIRS:
+        raise ValueError(f"fused_moe_decode: {N} tokens x {NK} slots exceeds {_MAX_PAIRS} pairs")
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d)
+    I = ex.inter
+    a = torch.empty(N * NK, I, device=x.device, dtype=torch.bfloat16) if a_buf is None else a_buf
+    if a.dtype != torch.bfloat16 or a.numel() < N * NK * I or not a.is_contiguous():
+        raise ValueError(f"fused_moe_decode: a_buf must be a contiguous bf16 buffer of {N * NK}x{I}")
+    y = torch.empty(N, H, device=x.device, dtype=torch.bfloat16) if out is None else out
+    if y.dtype != torch.bfloat16 or y.numel() != N * H or not y.is_contiguous():
+        raise ValueError(f"fused_moe_decode: out must be a contiguous bf16 [{N}, {H}] tensor")
+    r2 = None
+    if residual is not None:
+        r2 = residual.reshape(N, H)
+        if r2.dtype != torch.bfloat16:
+            raise ValueError("fused_moe_decode: residual must be bf16")
+        if not r2.is_contiguous():
+            r2 = r2.contiguous()
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_moe_decode(_mm.ptr(x2), N, x2.stride(0), ex, _mm.ptr(ids2), _mm.dtype_code(ids2), NK,
+                                    ids2.stride(0), _mm.ptr(wts2), wts2.stride(0), _mm.ptr(r2),
+                                    r2.stride(0) if r2 is not None else 0, _mm.ptr(a), _mm.ptr(y), H, phases,
+                                    _mm.stream_of(x)), "fused_moe_decode")
+    return y.view(N, H)
+
+
+def _num_blocks(P, E1, BM):
+    return (P + E1 * (BM - 1) + BM - 1) // BM
+
+
+def _align_blocks(flat, E1, BM, expert_offsets=None, out=None):
+    """Sort pair indices by expert, padding each expert's run to a multiple of BM (GPU only, no sync).
+    Returns sorted pair ids (P = padding) and the expert of each BM block (-1 = unused), and nb.
+    expert_offsets (int32 [E1+1]) receives each expert's padded start row and the used row count;
+    out = (sorted_ids, bexp) reuses caller buffers."""
+    _mm.require_gpu(flat)
+    flat = _flat_ids(flat).reshape(-1)
+    P = flat.numel()
+    nb = _num_blocks(P, E1, BM)
+    if out is not None:
+        sorted_ids, bexp = out
+        if sorted_ids.numel() != nb * BM or bexp.numel() != nb or sorted_ids.dtype != torch.int32 \
+                or bexp.dtype != torch.int32:
+            raise ValueError("_align_blocks: out buffers do not match the block count")
+    else:
+        sorted_ids = torch.empty(nb * BM, dtype=torch.int32, device=flat.device)
+        bexp = torch.empty(nb, dtype=torch.int32, device=flat.device)
+    if expert_offsets is not None and (expert_offsets.dtype != torch.int32 or expert_offsets.numel() != E1 + 1):
+        raise ValueError("_align_blocks: expert_offsets must be int32 with E1 + 1 elements")
+    lib = _mm.load()
+    with _mm.on_device(flat):
+        _mm.check(lib.mm_align_blocks(_mm.ptr(flat), _mm.dtype_code(flat), P, int(E1), int(BM), _mm.ptr(sorted_ids),
+                                      _mm.ptr(bexp), nb, _mm.ptr(expert_offsets), _mm.stream_of(flat)),
+                  "_align_blocks")
+    return sorted_ids, bexp, nb
+
+
+class PrefillScratch:
+    """Device buffers of one prefill call (align output and intermediates), reusable across calls of the
+    same shape so that a caller can keep them outside the timed or captured region."""
+
+    def __init__(self, N, KP1, E1, H, I, device):
+        P = N * KP1
+        self.nb = _num_blocks(P, E1, BLOCK_M)
+        self.sorted_ids = torch.empty(self.nb * BLOCK_M, dtype=torch.int32, device=device)
+        self.bexp = torch.empty(self.nb, dtype=torch.int32, device=device)
+        self.offsets = torch.empty(E1 + 1, dtype=torch.int32, device=device)
+        self.a = torch.empty(P, I, device=device, dtype=torch.bfloat16)
+        self.o = torch.empty(P, H, device=device, dtype=torch.float32)
+        self.y = torch.empty(N, H, device=device, dtype=torch.bfloat16)
+
+
+def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residual=None, scratch=None,
+                      phases=_mm.MM_PHASE_ALL, align=True):
+    """x: [N, H] bf16; ids: [N, K+1] expert ids per token (shared expert included); weights: [N, K+1] fp32.
+    Returns [N, H] bf16 = sum_k weights[:, k] * expert_k(x) (+ residual).
+    scratch (a PrefillScratch) supplies the buffers; phases / align=False run part of the pipeline on
+    scratch left by an earlier call, for timing one kernel."""
+    _mm.require_gpu(x, w_gu, w_d, ids, weights, s_gu, s_d, residual)
+    N, H = x.shape
+    KP1 = ids.shape[-1]
+    if N == 0:
+        return torch.empty(0, H, device=x.device, dtype=x.dtype)
+    if N <= MAX_DECODE_TOKENS and N * KP1 <= _MAX_PAIRS:  # decode-sized batches stream each expert once
+        return fused_moe_decode(x, w_gu, w_d, ids, weights, s_gu=s_gu, s_d=s_d, residual=residual,
+                                phases=phases & (_mm.MM_PHASE_GATE_UP | _mm.MM_PHASE_DOWN))
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"fused_moe_prefill: x must be bf16 (got {x.dtype})")
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d)
+    E1, I = ex.n_slots, ex.inter
+    x2 = x if x.is_contiguous() else x.contiguous()
+    flat = _flat_ids(ids).reshape(-1)
+    P = flat.numel()
+    if P != N * KP1:
+        raise ValueError("fused_moe_prefill: ids must be [N, K+1]")
+    wts = weights.reshape(-1).float().contiguous()
+    sc = scratch if scratch is not None else PrefillScratch(N, KP1, E1, H, I, x.device)
+    if sc.a.shape != (P, I) or sc.y.shape != (N, H) or sc.offsets.numel() != E1 + 1:
+        raise ValueError("fused_moe_prefill: scratch was made for another shape")
+    nb = sc.nb
+    if align:
+        _align_blocks(flat, E1, BLOCK_M, expert_offsets=sc.offsets, out=(sc.sorted_ids, sc.bexp))
+    sorted_ids, bexp, a, o, y = sc.sorted_ids, sc.bexp, sc.a, sc.o, sc.y
+    r2 = None
+    if residual is not None:
+        r2 = residual.reshape(N, H)
+        if r2.dtype != torch.bfloat16:
+            raise ValueError("fused_moe_prefill: residual must be bf16")
+        if not r2.is_contiguous():
+            r2 = r2.contiguous()
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_moe_prefill(_mm.ptr(x2), N, x2.stride(0), ex, KP1, _mm.ptr(flat), _mm.dtype_code(flat),
+                                     _mm.ptr(wts), _mm.ptr(sorted_ids), _mm.ptr(bexp), nb, BLOCK_M, _mm.ptr(r2),
+                                     r2.stride(0) if r2 is not None else 0, _mm.ptr(a), _mm.ptr(o), _mm.ptr(y), H,
+                                     phases, _mm.stream_of(x)), "fused_moe_prefill")
+    return y
+
+
+def quantize_rows_int8(w, *, scale_dtype=torch.float32):
+    """Symmetric per-output-row int8: w [..., N, K] -> (int8 [..., N, K], scales [..., N]).
+    scale_dtype torch.float32 (the reference) or torch.bfloat16 (q then divides by the rounded scale)."""
+    _mm.require_gpu(w)
+    if scale_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("quantize_rows_int8: scale_dtype must be torch.float32 or torch.bfloat16")
+    K = w.shape[-1]
+    w2 = w.reshape(-1, K)
+    if not w2.is_contiguous():
+        w2 = w2.contiguous()
+    rows = w2.shape[0]
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    s = torch.empty(w.shape[:-1], dtype=scale_dtype, device=w.device)
+    lib = _mm.load()
+    with _mm.on_device(w):
+        _mm.check(lib.mm_quantize_rows_int8(_mm.ptr(w2), _mm.dtype_code(w2), rows, K, w2.stride(0), _mm.ptr(q), K,
+                                            _mm.ptr(s), _mm.dtype_code(s), _mm.stream_of(w)), "quantize_rows_int8")
+    return q, s
+
+
+def _graph_us(fn, reps=50, inner=20):
+    """Microseconds per call of fn, captured `inner` times in one hipGraph and replayed `reps` times."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(inner):
+                fn()
+        g.replay()
+        s.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            g.replay()
+        s.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    return (time.perf_counter() - t) / reps / inner * 1e6

@@ -1,0 +1,106 @@
+"""CPU checks of the C ABI: the library loads and exports every entry point of include/mingmoe.h, the
+ctypes struct matches the C layout, and argument validation fails with a message before any GPU work."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+import _mingmoe as mm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mingmoe.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(mm_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert _declared() == sorted(mm.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = mm.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.mm_version() == mm.ABI_VERSION
+
+
+def test_experts_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "mingmoe.h"\n'
+                   'int main(void){printf("%zu", sizeof(mm_experts));'
+                   + "".join(f'printf(" %zu", offsetof(mm_experts, {f}));' for f, _ in mm.Experts._fields_)
+                   + 'return 0;}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(mm.Experts)
+    assert vals[1:] == [getattr(mm.Experts, f).offset for f, _ in mm.Experts._fields_]
+
+
+def _err(rc):
+    assert rc == mm.MM_ERR_ARG
+    return mm.last_error()
+
+
+def test_argument_validation_reports_messages():
+    lib = mm.load()
+    P = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    assert "bad shape" in _err(lib.mm_rms_norm(P, mm.MM_BF16, -1, 64, 64, P, mm.MM_BF16, 1e-6, P, mm.MM_BF16, 64, None))
+    assert "top_k" in _err(lib.mm_router(P, mm.MM_BF16, 1, 64, 64, P, 64, None, mm.MM_SCORE_SOFTMAX, 1, 1, 65, 1.0, 1,
+                                         P, P, mm.MM_INT64, P, 66, None))
+    assert "n_group" in _err(lib.mm_router(P, mm.MM_BF16, 1, 64, 64, P, 64, None, mm.MM_SCORE_SOFTMAX, 2, 1, 6, 1.0, 1,
+                                           P, P, mm.MM_INT64, P, 7, None))
+    assert "nb=" in _err(lib.mm_align_blocks(P, mm.MM_INT64, 100, 65, 64, P, P, 3, None, None))
+    assert "n_slots" in _err(lib.mm_align_blocks(P, mm.MM_INT64, 100, 300, 64, P, P, 400, None, None))
+    assert "null expert descriptor" in _err(lib.mm_moe_decode(P, 1, 64, None, P, mm.MM_INT64, 7, 7, P, 7, None, 0, P,
+                                                              P, 64, 0, None))
+    ex = mm.Experts()
+    ex.w_gu, ex.w_d, ex.w_dtype, ex.n_slots, ex.hidden, ex.inter = 16, 16, mm.MM_BF16, 65, 2048, 1408
+    ex.gu_stride_e, ex.gu_stride_n, ex.d_stride_e, ex.d_stride_n = 2816 * 2048, 2048, 2048 * 1408, 1408
+    assert "n_tokens * nk" in _err(lib.mm_moe_decode(P, 10, 2048, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None,
+                                                     0, P, P, 2048, 0, None))
+    ex.w_gu = 18  # misaligned rows
+    assert "16-byte aligned" in _err(lib.mm_moe_decode(P, 1, 2048, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None,
+                                                       0, P, P, 2048, 0, None))
+    ex.w_gu, ex.hidden = 16, 2047
+    assert "multiples" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, 10, 64,
+                                                  None, 0, P, P, P, 2048, 0, None))
+    ex.hidden = 2048
+    assert "block_m" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, 10, 32,
+                                                None, 0, P, P, P, 2048, 0, None))
+    assert "M=17" in _err(lib.mm_small_linear(P, 17, 64, 64, P, 64, 64, None, 0, None, 0, None, 0.0, None, P, 64, None))
+    assert "scale dtype" in _err(lib.mm_quantize_rows_int8(P, mm.MM_BF16, 4, 64, 64, P, 64, P, mm.MM_INT8, None))
+
+
+def test_wrappers_refuse_cpu_tensors():
+    import fused_moe
+    import fused_ops
+    import fastlinear
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU path"):
+        fused_ops.rms_norm(x, torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="no CPU path"):
+        fused_moe.quantize_rows_int8(x)
+    with pytest.raises(ValueError, match="no CPU path"):
+        fastlinear.small_linear(x, torch.zeros(8, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="no CPU path"):
+        fused_moe._align_blocks(torch.zeros(7, dtype=torch.long), 65, 64)
+
+
+def test_reference_module_surface_is_kept():
+    import fused_moe
+    import fused_ops
+    import fastlinear
+    for mod, names in ((fused_moe, ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "_align_blocks",
+                                    "CFG", "GCFG", "_graph_us"]),
+                       (fused_ops, ["rms_norm", "moe_route"]),
+                       (fastlinear, ["small_linear", "save_cache", "_graph_time", "CACHE_FILE", "_best"])):
+        for n in names:
+            assert hasattr(mod, n), f"{mod.__name__}.{n}"
+    fastlinear.save_cache()  # nothing tuned: writes nothing
