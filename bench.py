@@ -130,7 +130,7 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70):
     cb_ms = kernel_ms(phase(_mingmoe.MM_PHASE_COMBINE), stream)
     H, I = W.HIDDEN, W.INTER
     gu_bytes = used * 2 * I * H * 2 + n * H * 2 + P * I * 2
-    dn_bytes = used * H * I * 2 + P * I * 2 + P * H * 4
+    dn_bytes = used * H * I * 2 + P * I * 2 + P * H * 2
     flops = P * W.flops_per_pair()
     moe_ms = gu_ms + dn_ms
     return {

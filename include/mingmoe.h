@@ -137,13 +137,14 @@ int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const m
  * Replaces fused_moe.fused_moe_prefill / _moe_gu_grouped / _moe_down_grouped (fused_moe.py:92-196).
  * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs
  * p = t*nk + k whose id lies outside [0, n_slots) contribute nothing); wts fp32 [n_tokens*nk];
- * sorted_ids / bexp / nb / block_m from mm_align_blocks; a_buf bf16 [n_tokens*nk, inter] and
- * o_buf fp32 [n_tokens*nk, hidden] are scratch; y bf16 [n_tokens, hidden]. */
+ * sorted_ids / bexp / expert_offsets / nb / block_m (64) from mm_align_blocks; a_buf bf16
+ * [n_tokens*nk, inter] and part_buf bf16 [n_tokens*nk, hidden] (per-pair expert outputs bf16(a . Wd^T),
+ * before the slot weight) are scratch; y bf16 [n_tokens, hidden]. */
 int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
                    int64_t nk, const void* ids, int ids_dtype, const float* wts,
-                   const int32_t* sorted_ids, const int32_t* bexp, int64_t nb, int32_t block_m,
-                   const void* residual, int64_t res_row_stride,
-                   void* a_buf, float* o_buf, void* y, int64_t y_row_stride, int phases, void* stream);
+                   const int32_t* sorted_ids, const int32_t* bexp, const int32_t* expert_offsets,
+                   int64_t nb, int32_t block_m, const void* residual, int64_t res_row_stride,
+                   void* a_buf, void* part_buf, void* y, int64_t y_row_stride, int phases, void* stream);
 
 /* y = act(norm?(x) . W^T + b) [+ residual] for M <= 16 rows.
  * Replaces fastlinear.small_linear / _small_m_linear (fastlinear.py:123-174) including the rounding

@@ -44,8 +44,8 @@ SIGNATURES = {
     "mm_align_blocks": ([_P, _I32, _I64, ctypes.c_int32, ctypes.c_int32, _P, _P, _I64, _P, _P], ctypes.c_int),
     "mm_moe_decode": ([_P, _I64, _I64, ctypes.POINTER(Experts), _P, _I32, _I64, _I64, _P, _I64, _P, _I64, _P, _P,
                        _I64, _I32, _P], ctypes.c_int),
-    "mm_moe_prefill": ([_P, _I64, _I64, ctypes.POINTER(Experts), _I64, _P, _I32, _P, _P, _P, _I64, ctypes.c_int32,
-                        _P, _I64, _P, _P, _P, _I64, _I32, _P], ctypes.c_int),
+    "mm_moe_prefill": ([_P, _I64, _I64, ctypes.POINTER(Experts), _I64, _P, _I32, _P, _P, _P, _P, _I64,
+                        ctypes.c_int32, _P, _I64, _P, _P, _P, _I64, _I32, _P], ctypes.c_int),
     "mm_small_linear": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64, _P, _F32, _P, _P, _I64, _P],
                         ctypes.c_int),
     "mm_quantize_rows_int8": ([_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P], ctypes.c_int),

@@ -101,97 +101,151 @@ __device__ __forceinline__ uint4 load_w(const void* base, int64_t byte_off, bool
 
 // ------------------------------------------------------------------------------------------- kernel A
 
-template <bool Q, int LPR, int NC, int R, int MAXT>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
-  unsigned long long pairs;
-  const int e = distinct_expert(a, blockIdx.y, pairs);
-  if (e < 0) return;
-  constexpr int ES = Q ? 1 : 2;        // weight bytes per element
-  constexpr int GPW = kWave / LPR;      // row pairs per wave per step
-  const int lane = lane_id(), wave = threadIdx.x / kWave;
+// Epilogue of one gate/up row pair for one pair p: scales (int8), bf16 rounding points, SiLU, product.
+template <bool Q>
+__device__ __forceinline__ void gate_up_store(const DecodeArgs& a, int e, int64_t r, int p, float ag, float au) {
+  if (Q) {
+    ag *= load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + r);
+    au *= load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + a.I + r);
+  }
+  const float gg = round_bf16(ag), uu = round_bf16(au);
+  const float act = round_bf16(silu(gg));
+  a.a_buf[static_cast<int64_t>(p) * a.I + r] = f32_to_bf16(act * uu);
+}
+
+// One token per expert (batch 1, or a batch whose tokens chose distinct experts): the token's activation
+// chunks stay in registers for all rows of the wave.
+template <bool Q, int LPR, int NC, int R>
+__device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, const char* wbase, int64_t row0) {
+  constexpr int ES = Q ? 1 : 2;
+  constexpr int GPW = kWave / LPR;
+  const int lane = lane_id();
   const int g = lane / LPR, s = lane % LPR;
   const int64_t nch = a.H * ES / 16;
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GPW * R);
-  const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
-
-  while (pairs) {
-    // up to MAXT pairs of this expert
-    int pid[MAXT];
-    int cntp = 0;
+  const uint16_t* xr = a.x + static_cast<int64_t>(p / a.nk) * a.xs;
+  float accg[R], accu[R];
 #pragma unroll
-    for (int t = 0; t < MAXT; ++t) {
-      pid[t] = -1;
-      if (pairs) {
-        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
-        pairs &= pairs - 1ull;
-        pid[t] = p;
-        cntp = t + 1;
-      }
-    }
-    float accg[R][MAXT], accu[R][MAXT];
+  for (int i = 0; i < R; ++i) accg[i] = accu[i] = 0.f;
+  for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {  // one pass unless H is long
+    Act<Q> xa[NC];
 #pragma unroll
-    for (int i = 0; i < R; ++i)
-#pragma unroll
-      for (int t = 0; t < MAXT; ++t) accg[i][t] = accu[i][t] = 0.f;
-    // one pass over the row unless it is longer than LPR * NC chunks
-    for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {
-      Act<Q> xa[MAXT][NC];
-#pragma unroll
-      for (int t = 0; t < MAXT; ++t) {
-        const int tok = pid[t] >= 0 ? pid[t] / a.nk : 0;
-        const uint16_t* xr = a.x + tok * a.xs;
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
-          load_act<Q>(xa[t][j], xr, c, t < cntp && c < nch);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
-        const bool rok = r < a.I;
-        uint4 wg[NC], wu[NC];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
-          const bool ok = rok && c < nch;
-          wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
-          wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
-        }
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-          if (t < cntp) {
-#pragma unroll
-            for (int j = 0; j < NC; ++j) {
-              accg[i][t] = dot_chunk<Q>(wg[j], xa[t][j], accg[i][t]);
-              accu[i][t] = dot_chunk<Q>(wu[j], xa[t][j], accu[i][t]);
-            }
-          }
-        }
-      }
+    for (int j = 0; j < NC; ++j) {
+      const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+      load_act<Q>(xa[j], xr, c, c < nch);
     }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
       const bool rok = r < a.I;
-      float sg = 1.f, su = 1.f;
-      if (Q && rok) {
-        sg = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + r);
-        su = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + a.I + r);
+      uint4 wg[NC], wu[NC];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+        const bool ok = rok && c < nch;
+        wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
+        wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
       }
 #pragma unroll
-      for (int t = 0; t < MAXT; ++t) {
-        if (t < cntp) {
-          float ag = group_sum<LPR>(accg[i][t]);
-          float au = group_sum<LPR>(accu[i][t]);
-          if (s == 0 && rok) {
-            if (Q) { ag *= sg; au *= su; }
-            const float gg = round_bf16(ag), uu = round_bf16(au);
-            const float act = round_bf16(silu(gg));
-            a.a_buf[static_cast<int64_t>(pid[t]) * a.I + r] = f32_to_bf16(act * uu);
-          }
-        }
+      for (int j = 0; j < NC; ++j) {
+        accg[i] = dot_chunk<Q>(wg[j], xa[j], accg[i]);
+        accu[i] = dot_chunk<Q>(wu[j], xa[j], accu[i]);
       }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+    const float ag = group_sum<LPR>(accg[i]), au = group_sum<LPR>(accu[i]);
+    if (s == 0 && r < a.I) gate_up_store<Q>(a, e, r, p, ag, au);
+  }
+}
+
+// Several tokens per expert: their activation rows are staged in LDS (bf16). Each weight row pair is loaded
+// once into registers and dotted with every staged row in turn, so registers hold only the weight chunks.
+// Needs the row in one pass (nch <= LPR * NC); the caller takes gate_up_one per token otherwise.
+template <bool Q, int LPR, int NC, int R, int MAXT>
+__device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cntp, const int* spid, const char* wbase,
+                                             int64_t row0, uint16_t* xs) {
+  constexpr int ES = Q ? 1 : 2;
+  constexpr int GPW = kWave / LPR;
+  const int lane = lane_id();
+  const int g = lane / LPR, s = lane % LPR;
+  const int64_t nch = a.H * ES / 16;
+  // stage the rows of this group's tokens (whole workgroup; the group is uniform across it)
+  const int64_t row_chunks = a.H / 8;  // 16-byte chunks of one bf16 row
+  for (int64_t i = threadIdx.x; i < cntp * row_chunks; i += blockDim.x) {
+    const int t = static_cast<int>(i / row_chunks);
+    const int64_t c = i % row_chunks;
+    reinterpret_cast<uint4*>(xs + t * a.H)[c] =
+        reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(spid[t] / a.nk) * a.xs)[c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+    const bool rok = r < a.I;
+    uint4 wg[NC], wu[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t c = s + static_cast<int64_t>(LPR) * j;
+      const bool ok = rok && c < nch;
+      wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
+      wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
+    }
+    for (int t = 0; t < cntp; ++t) {
+      float ag = 0.f, au = 0.f;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t c = s + static_cast<int64_t>(LPR) * j;
+        Act<Q> xv;
+        load_act<Q>(xv, xs + t * a.H, c, c < nch);
+        ag = dot_chunk<Q>(wg[j], xv, ag);
+        au = dot_chunk<Q>(wu[j], xv, au);
+      }
+      ag = group_sum<LPR>(ag);
+      au = group_sum<LPR>(au);
+      if (s == 0 && rok) gate_up_store<Q>(a, e, r, spid[t], ag, au);
+    }
+  }
+  __syncthreads();  // the staging buffer is reused by the next group
+}
+
+template <bool Q, int LPR, int NC, int R, int MAXT>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
+  extern __shared__ uint4 xs_raw[];  // MAXT bf16 rows of the hidden dim (MAXT > 1 only)
+  __shared__ int spid[MAXT];
+  unsigned long long pairs;
+  const int e = distinct_expert(a, blockIdx.y, pairs);
+  if (e < 0) return;
+  constexpr int ES = Q ? 1 : 2;
+  constexpr int GPW = kWave / LPR;  // row pairs per wave per step
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GPW * R);
+  const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
+  if constexpr (MAXT == 1) {
+    while (pairs) {
+      const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+      pairs &= pairs - 1ull;
+      gate_up_one<Q, LPR, NC, R>(a, e, p, wbase, row0);
+    }
+  } else {
+    const bool one_pass = a.H * ES / 16 <= static_cast<int64_t>(LPR) * NC;
+    while (pairs) {
+      if (!one_pass || __popcll(pairs) == 1) {
+        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+        pairs &= pairs - 1ull;
+        gate_up_one<Q, LPR, NC, R>(a, e, p, wbase, row0);
+        continue;
+      }
+      int cntp = 0;
+      while (pairs && cntp < MAXT) {  // the next MAXT pairs of this expert, in pair order
+        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+        pairs &= pairs - 1ull;
+        if (threadIdx.x == 0) spid[cntp] = p;
+        ++cntp;
+      }
+      __syncthreads();
+      gate_up_many<Q, LPR, NC, R, MAXT>(a, e, cntp, spid, wbase, row0, reinterpret_cast<uint16_t*>(xs_raw));
     }
   }
 }
@@ -289,7 +343,8 @@ template <bool Q, int LPR, int NC, int R, int MAXT>
 int launch_a(const DecodeArgs& a, hipStream_t st) {
   constexpr int rows_per_wg = 4 * (kWave / LPR) * R;
   dim3 grid(static_cast<unsigned>((a.I + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(min(a.P, a.E1)));
-  hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT>), grid, dim3(256), 0, st, a);
+  const size_t lds = MAXT > 1 ? static_cast<size_t>(MAXT) * a.H * 2 : 0;
+  hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT>), grid, dim3(256), lds, st, a);
   return mm::check_launch("moe_decode gate_up");
 }
 
@@ -305,11 +360,14 @@ int launch_b(const DecodeArgs& a, hipStream_t st) {
 // pass; rows longer than LPR * NC chunks take several passes, so a few instances cover every shape.
 template <bool Q, int LPR, int NC>
 int dispatch_a_t(const DecodeArgs& a, hipStream_t st) {
-  const int maxt = a.n_tokens;  // pairs of one expert: one per token unless a token repeats an expert
+  // tokens staged per group: one per token of the batch (a token naming an expert twice adds groups),
+  // bounded so that the staged rows fit 64 KB of LDS
+  int maxt = a.n_tokens;
+  while (maxt > 1 && static_cast<int64_t>(maxt) * a.H * 2 > 65536) maxt /= 2;
   if (maxt <= 1) return launch_a<Q, LPR, NC, 2, 1>(a, st);
   if (maxt <= 2) return launch_a<Q, LPR, NC, 2, 2>(a, st);
-  if (maxt <= 4) return launch_a<Q, LPR, NC, 1, 4>(a, st);
-  return launch_a<Q, LPR, NC, 1, 8>(a, st);
+  if (maxt <= 4) return launch_a<Q, LPR, NC, 2, 4>(a, st);
+  return launch_a<Q, LPR, NC, 2, 8>(a, st);
 }
 
 template <bool Q>
@@ -324,9 +382,14 @@ int dispatch_a(const DecodeArgs& a, hipStream_t st) {
 template <bool Q>
 int dispatch_b(const DecodeArgs& a, hipStream_t st) {
   const int64_t nch = a.I * (Q ? 1 : 2) / 16;  // down rows run over the intermediate dim
-  if (nch >= 128) return launch_b<Q, 16, 12>(a, st);
-  if (nch > 32) return launch_b<Q, 8, 12>(a, st);
-  return launch_b<Q, 8, 4>(a, st);
+  if constexpr (Q) {  // int8 chunks carry 32-byte activation chunks: fewer chunks per lane
+    if (nch > 48) return launch_b<Q, 16, 6>(a, st);
+    return launch_b<Q, 8, 6>(a, st);
+  } else {
+    if (nch >= 128) return launch_b<Q, 16, 12>(a, st);
+    if (nch > 32) return launch_b<Q, 8, 12>(a, st);
+    return launch_b<Q, 8, 4>(a, st);
+  }
 }
 
 }  // namespace

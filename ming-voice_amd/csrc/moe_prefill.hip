@@ -1,22 +1,30 @@
 // Grouped prefill MoE on bf16 MFMA (fused_moe.py:92-196).
 //
-// Pairs are grouped by expert into blocks of 64 rows by mm_align_blocks. Kernel GU computes, for one block
-// and 64 columns of I, the gate and up projections of the 64 gathered token rows with
-// v_mfma_f32_16x16x32_bf16 over LDS-staged k-slabs and writes a = bf16(bf16(silu(bf16(g))) * bf16(u)) per
-// pair. Kernel DOWN computes o[pair] = f32(bf16(a . Wd^T [* s])) * w_pair for 128 columns of H. Kernel
-// COMBINE sums the slots of each token in order (fp32) and rounds to bf16, adding the residual if given.
-// int8 weights are widened to bf16 (exact for |q| <= 127) on their way into LDS; the row scale multiplies
-// the fp32 accumulator before the bf16 rounding, as in the reference.
+// mm_align_blocks groups the (token, slot) pairs by expert into blocks of 64 rows and reports each expert's
+// padded row range. A tile is (expert block of 64 pairs) x (256 output columns):
+//   GATE_UP: columns are 128 gate + the matching 128 up rows of W_gu[e]; the epilogue writes
+//            a[pair] = bf16(bf16(silu(bf16(g))) * bf16(u)) (int8: row scale on the fp32 accumulator first).
+//   DOWN:    columns are 256 rows of W_d[e]; the epilogue writes part[pair] = bf16(a . Wd^T [* s]).
+//   COMBINE: y[t] = bf16(sum_k w[t,k] * part[t*nk+k]) (fp32, slots in order) (+ residual, rounded again),
+//            the reference's f32(bf16(acc)) * w summed over slots (fused_moe.py:147-148, 196).
+// Tiles are ordered expert-major, then column tile, then block, and dealt out to the 8 XCDs in contiguous
+// runs, so the blocks that share a weight tile run together on one XCD and hit its L2. The k loop copies
+// 64-wide slabs of the activation rows and of the weight rows straight into LDS (global_load_lds, 3-4
+// slabs in flight) and feeds v_mfma_f32_16x16x32_bf16 from there. int8 weights stay int8 in LDS and are
+// widened to bf16 (exact for |q| <= 127) as fragments are read.
+#include <mutex>
+
 #include "mm_common.h"
 
 namespace {
 
 using namespace mmd;
 
-constexpr int kBM = 64;        // rows (pairs) per block, = align block_m
-constexpr int kBK = 64;        // k-slab
-constexpr int kLdsK = kBK + 8; // padded LDS row (elements) against bank conflicts
-constexpr int kThreads = 256;
+constexpr int kBM = 64;          // rows (pairs) per block, = align block_m
+constexpr int kBN = 256;         // output columns per tile
+constexpr int kBK = 64;          // k-slab (bf16 elements): rows of 128 bytes = 8 chunks of 16 bytes
+constexpr int kThreads = 256;    // 4 waves, each 64 rows x 64 columns
+constexpr int kXcds = 8;
 
 struct PrefillArgs {
   const uint16_t* x;
@@ -27,7 +35,7 @@ struct PrefillArgs {
   const float* wts;
   const int32_t* sorted_ids;
   const int32_t* bexp;
-  int nb;
+  const int32_t* offsets;  // [E1+1] padded start row of each expert, used rows last
   const void* w_gu;
   const void* w_d;
   const void* s_gu;
@@ -38,132 +46,248 @@ struct PrefillArgs {
   const uint16_t* res;
   int64_t res_rs;
   uint16_t* a_buf;
-  float* o_buf;
+  uint16_t* part;
   uint16_t* y;
   int64_t ys;
 };
 
+// Tile of this workgroup: expert e, block blk (rows blk*64 ..), column tile nt. False: no tile.
+__device__ __forceinline__ bool map_tile(const PrefillArgs& a, int NT, int& e, int& blk, int& nt) {
+  const int used_blocks = a.offsets[a.E1] / kBM;
+  const int G = used_blocks * NT;
+  const int per = (G + kXcds - 1) / kXcds;
+  const int w = blockIdx.x;
+  const int idx = w / kXcds, xcd = w % kXcds;  // workgroups are dealt to XCDs round robin
+  if (idx >= per) return false;
+  const int L = xcd * per + idx;
+  if (L >= G) return false;
+  e = a.bexp[L / NT];
+  const int b0 = a.offsets[e] / kBM, nblk = a.offsets[e + 1] / kBM - b0;
+  const int local = L - b0 * NT;
+  nt = local / nblk;
+  blk = b0 + local % nblk;
+  return true;
+}
+
 // 16 int8 -> 16 bf16 (exact), as two uint4 of packed bf16 pairs.
 __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
-  uint32_t in[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t in[4] = {q.x, q.y, q.z, q.w};
   uint32_t out[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t v = in[i];
-    const uint32_t b0 = f32_to_bf16(sbyte(v, 0)), b1 = f32_to_bf16(sbyte(v, 1));
-    const uint32_t b2 = f32_to_bf16(sbyte(v, 2)), b3 = f32_to_bf16(sbyte(v, 3));
-    out[2 * i] = b0 | (b1 << 16);
-    out[2 * i + 1] = b2 | (b3 << 16);
+    out[2 * i] = static_cast<uint32_t>(f32_to_bf16(sbyte(v, 0))) | (static_cast<uint32_t>(f32_to_bf16(sbyte(v, 1))) << 16);
+    out[2 * i + 1] = static_cast<uint32_t>(f32_to_bf16(sbyte(v, 2))) | (static_cast<uint32_t>(f32_to_bf16(sbyte(v, 3))) << 16);
   }
   lo = make_uint4(out[0], out[1], out[2], out[3]);
   hi = make_uint4(out[4], out[5], out[6], out[7]);
 }
 
-// Stage `rows` weight rows x kBK k-values (bf16 in LDS) starting at k0. Row r of the tile is weight row
-// row_of(r); rows past `nrows` or k past K are zero.
-template <bool Q, int ROWS, class RowFn>
-__device__ __forceinline__ void stage_w(uint16_t (*lds)[kLdsK], const char* wbase, int64_t row_stride_el, int64_t K,
-                                        int64_t k0, RowFn row_of) {
-  constexpr int ES = Q ? 1 : 2;
-  constexpr int CPR = kBK * ES / 16;  // 16-byte chunks per row of the slab
-  constexpr int TOTAL = ROWS * CPR;
-  for (int i = threadIdx.x; i < TOTAL; i += kThreads) {
-    const int r = i / CPR, c = i % CPR;
-    const int64_t wr = row_of(r);
-    const int64_t k = k0 + static_cast<int64_t>(c) * (16 / ES);
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (wr >= 0 && k < K) v = *reinterpret_cast<const uint4*>(wbase + (wr * row_stride_el + k) * ES);
-    if constexpr (Q) {
-      uint4 lo, hi;
-      widen_i8(v, lo, hi);
-      *reinterpret_cast<uint4*>(&lds[r][c * 16]) = lo;
-      *reinterpret_cast<uint4*>(&lds[r][c * 16 + 8]) = hi;
-    } else {
-      *reinterpret_cast<uint4*>(&lds[r][c * 8]) = v;
+// ---------------------------------------------------------------------------------- k-slab pipeline
+//
+// Each k-slab (64 k) of the tile is copied global -> LDS by global_load_lds_dwordx4: one wave instruction
+// fills 1 KB of LDS in lane order, and each lane picks the 16-byte global chunk that belongs at its LDS
+// position. Rows and k past the operand (padding pairs, columns past the weight, the k tail) read a
+// zero chunk. NS slabs are in flight; the wave waits on vmcnt for the oldest and a barrier makes it
+// visible to every wave. Layouts (bytes) keep the 16 rows that one MFMA fragment reads on distinct banks:
+//   bf16 rows (A, and B for bf16 weights): 128 B = 8 chunks, chunk c of row r at r*128 + (c ^ (r & 7))*16
+//   int8 weight rows: 64 B = 4 chunks of 16 k, chunk c of row r at r*64 + (c ^ ((r >> 1) & 3))*16
+// A lane's MFMA k-chunk for step ks of lane quarter lq is ks*4 + lq (bf16 weights) or 2*lq + ks (int8
+// weights, so that one 16-byte int8 chunk widens into the two steps); A follows the same choice.
+
+__device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes for masked lanes
+
+template <bool Q>
+struct Geo {
+  static constexpr int ROWB = Q ? 64 : 128;           // weight bytes per row per slab
+  static constexpr int A_BYTES = kBM * 128;            // 8 KB
+  static constexpr int B_BYTES = kBN * ROWB;           // 32 KB bf16, 16 KB int8
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int NS = Q ? 4 : 3;                 // slabs in flight
+  static constexpr size_t LDS = static_cast<size_t>(NS) * STAGE;
+  static constexpr int A_INSTR = A_BYTES / 1024 / 4;  // per wave per slab: 2
+  static constexpr int B_INSTR = B_BYTES / 1024 / 4;  // 8 bf16, 4 int8
+  static constexpr int LOADS = A_INSTR + B_INSTR;
+};
+
+__device__ __forceinline__ int pos_bf16(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+__device__ __forceinline__ int pos_i8(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+__device__ __forceinline__ void load_lds16(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+// Wait until at most n vector-memory loads of this wave are outstanding (n a compile-time constant).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Per-thread source rows of the direct loads: for A instruction j the lane fills tile row ra[j], logical
+// chunk ca[j]; for B instruction j tile row rb[j], logical chunk cb[j].
+template <bool Q>
+struct LoadMap {
+  int ra[Geo<Q>::A_INSTR], ca[Geo<Q>::A_INSTR];
+  int rb[Geo<Q>::B_INSTR], cb[Geo<Q>::B_INSTR];
+  __device__ __forceinline__ LoadMap() {
+    const int w = threadIdx.x / kWave, l = lane_id();
+#pragma unroll
+    for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+      ra[j] = (w * Geo<Q>::A_INSTR + j) * 8 + l / 8;
+      ca[j] = (l % 8) ^ (ra[j] & 7);
+    }
+#pragma unroll
+    for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+      if constexpr (Q) {
+        rb[j] = (w * Geo<Q>::B_INSTR + j) * 16 + l / 4;
+        cb[j] = (l % 4) ^ ((rb[j] >> 1) & 3);
+      } else {
+        rb[j] = (w * Geo<Q>::B_INSTR + j) * 8 + l / 8;
+        cb[j] = (l % 8) ^ (rb[j] & 7);
+      }
     }
   }
-}
+};
 
-// Stage kBM activation rows x kBK (bf16) from rows given by src_row(r) (nullptr = zero row).
-template <class SrcFn>
-__device__ __forceinline__ void stage_a(uint16_t (*lds)[kLdsK], int64_t K, int64_t k0, SrcFn src_row) {
-  constexpr int CPR = kBK / 8;
-  for (int i = threadIdx.x; i < kBM * CPR; i += kThreads) {
-    const int r = i / CPR, c = i % CPR;
-    const uint16_t* src = src_row(r);
-    const int64_t k = k0 + c * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (src && k < K) v = *reinterpret_cast<const uint4*>(src + k);
-    *reinterpret_cast<uint4*>(&lds[r][c * 8]) = v;
+// Issues the direct loads of slab kt into LDS stage `st` (arow/brow: this thread's source row starts,
+// null for masked rows; k counted in elements).
+template <bool Q>
+__device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K, const LoadMap<Q>& m,
+                                           const uint16_t* const* arow, const char* const* brow) {
+  constexpr int ES = Q ? 1 : 2;
+  char* sa = lds + st * Geo<Q>::STAGE;
+  char* sb = sa + Geo<Q>::A_BYTES;
+  const int w = threadIdx.x / kWave;
+  const int64_t k0 = static_cast<int64_t>(kt) * kBK;
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+    const int64_t k = k0 + m.ca[j] * 8;
+    const void* src = (arow[j] && k < K) ? static_cast<const void*>(arow[j] + k) : static_cast<const void*>(g_zero_chunk);
+    load_lds16(src, sa + (w * Geo<Q>::A_INSTR + j) * 1024);
+  }
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+    const int64_t k = k0 + m.cb[j] * (16 / ES);
+    const void* src = (brow[j] && k < K) ? static_cast<const void*>(brow[j] + k * ES) : static_cast<const void*>(g_zero_chunk);
+    load_lds16(src, sb + (w * Geo<Q>::B_INSTR + j) * 1024);
   }
 }
 
-__device__ __forceinline__ bf16x8_t lds_frag(const uint16_t (*lds)[kLdsK], int row, int k) {
-  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(&lds[row][k]));
+__device__ __forceinline__ bf16x8_t lds_frag16(const char* base, int pos) {
+  return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(base + pos));
+}
+
+// The shared GEMM body: acc[i][j] (i: 16-row fragment 0..3, j: 16-column fragment 0..3 of this wave's 64
+// columns) over K, with the tile row of the wave's column fragment j given by bcol(j).
+template <bool Q, class BColFn>
+__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[4][4], int64_t K, const uint16_t* const* arow,
+                                          const char* const* brow, char* lds, BColFn bcol) {
+  constexpr int NS = Geo<Q>::NS;
+  constexpr int LOADS = Geo<Q>::LOADS;
+  const int lane = lane_id();
+  const int lr = lane & 15, lq = lane >> 4;
+  const LoadMap<Q> m;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int nk = static_cast<int>((K + kBK - 1) / kBK);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue_slab<Q>(lds, s, s, K, m, arow, brow);
+  for (int kt = 0; kt < nk; ++kt) {
+    // slabs issued after kt so far: min(nk - 1 - kt, NS - 2); wait for kt's own loads
+    const int pending = min(nk - 1 - kt, NS - 2);
+    if (pending >= 2) wait_vmcnt<2 * LOADS>();
+    else if (pending == 1) wait_vmcnt<LOADS>();
+    else wait_vmcnt<0>();
+    // slab kt visible to all waves; every wave is done with slab kt-1. A plain barrier: the loads of
+    // slab kt were waited for above, and a memory fence would also wait for the later slabs' loads.
+    __builtin_amdgcn_s_barrier();
+    if (kt + NS - 1 < nk) issue_slab<Q>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow);
+    const char* sa = lds + (kt % NS) * Geo<Q>::STAGE;
+    const char* sb = sa + Geo<Q>::A_BYTES;
+    if constexpr (Q) {
+      // one 16-byte int8 chunk per lane and fragment feeds both 32-wide steps
+      bf16x8_t fb[2][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = bcol(j) + lr;
+        uint4 lo, hi;
+        widen_i8(*reinterpret_cast<const uint4*>(sb + pos_i8(r, lq)), lo, hi);
+        fb[0][j] = __builtin_bit_cast(bf16x8_t, lo);
+        fb[1][j] = __builtin_bit_cast(bf16x8_t, hi);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        bf16x8_t fa[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[i] = lds_frag16(sa, pos_bf16(16 * i + lr, 2 * lq + ks));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int ch = ks * 4 + lq;
+        bf16x8_t fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[i] = lds_frag16(sa, pos_bf16(16 * i + lr, ch));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fb[j] = lds_frag16(sb, pos_bf16(bcol(j) + lr, ch));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------- gate / up
 
 template <bool Q>
 __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a) {
-  constexpr int ES = Q ? 1 : 2;
-  const int blk = blockIdx.x;
-  const int e = a.bexp[blk];
-  if (e < 0) return;
-  __shared__ uint16_t sa[kBM][kLdsK];
-  __shared__ uint16_t sb[128][kLdsK];  // rows 0..63 gate, 64..127 up
+  extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
-  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int NT = static_cast<int>((a.I + kBN / 2 - 1) / (kBN / 2));
+  int e, blk, nt;
+  if (!map_tile(a, NT, e, blk, nt)) return;
+  constexpr int ES = Q ? 1 : 2;
+  const int64_t I = a.I, n0 = static_cast<int64_t>(nt) * (kBN / 2);
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
-  const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
-  const int lane = lane_id(), wave = threadIdx.x / kWave;
-  const int wm = wave / 2, wn = wave % 2;
-  floatx4 accg[2][2], accu[2][2];
+  // source rows of this thread's direct loads
+  const LoadMap<Q> m;
+  const uint16_t* arow[Geo<Q>::A_INSTR];
+  const char* brow[Geo<Q>::B_INSTR];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      accg[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-      accu[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-  const int64_t I = a.I;
-  for (int64_t k0 = 0; k0 < a.H; k0 += kBK) {
-    stage_a(sa, a.H, k0, [&](int r) -> const uint16_t* {
-      const int p = spair[r];
-      return p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
-    });
-    stage_w<Q, 128>(sb, wbase, a.gu_sn, a.H, k0, [&](int r) -> int64_t {
-      const int64_t col = n0 + (r & 63);
-      if (col >= I) return -1;
-      return r < 64 ? col : I + col;
-    });
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 32) {
-      const int kk = ks + 8 * (lane / 16);
-      bf16x8_t fa[2], fg[2], fu[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = lds_frag(sa, 32 * wm + 16 * i + (lane % 16), kk);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        fg[j] = lds_frag(sb, 32 * wn + 16 * j + (lane % 16), kk);
-        fu[j] = lds_frag(sb, 64 + 32 * wn + 16 * j + (lane % 16), kk);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fg[j], accg[i][j], 0, 0, 0);
-          accu[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fu[j], accu[i][j], 0, 0, 0);
-        }
-    }
-    __syncthreads();
+  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+    const int p = spair[m.ra[j]];
+    arow[j] = p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
   }
-  // epilogue: D[row = 4*(lane/16) + v][col = lane%16] of each 16x16 tile
+  const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+    const int r = m.rb[j];  // tile row: 0..127 gate, 128..255 up
+    const int64_t col = n0 + (r & 127);
+    brow[j] = col < I ? wbase + ((r < 128 ? col : I + col) * a.gu_sn) * ES : nullptr;
+  }
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  floatx4 acc[4][4];  // j = 0,1 gate fragments, 2,3 the matching up fragments
+  tile_gemm<Q>(acc, a.H, arow, brow, reinterpret_cast<char*>(lds_raw),
+               [&](int j) { return (j < 2 ? 0 : 128) + 32 * wave + 16 * (j & 1); });
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + 32 * wn + 16 * j + (lane % 16);
+    const int64_t col = n0 + 32 * wave + 16 * j + (lane & 15);
     if (col >= I) continue;
     float sg = 1.f, su = 1.f;
     if (Q) {
@@ -171,13 +295,12 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
       su = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + I + col);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = 32 * wm + 16 * i + 4 * (lane / 16) + v;
-        const int p = spair[row];
+        const int p = spair[16 * i + 4 * (lane >> 4) + v];  // D[row = 4*(lane/16) + v][col = lane%16]
         if (p >= a.P) continue;
-        float g = accg[i][j][v], u = accu[i][j][v];
+        float g = acc[i][j][v], u = acc[i][j + 2][v];
         if (Q) { g *= sg; u *= su; }
         const float gg = round_bf16(g), uu = round_bf16(u);
         a.a_buf[static_cast<int64_t>(p) * I + col] = f32_to_bf16(round_bf16(silu(gg)) * uu);
@@ -189,86 +312,131 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
 
 template <bool Q>
 __global__ __launch_bounds__(kThreads) void prefill_down_kernel(PrefillArgs a) {
-  constexpr int ES = Q ? 1 : 2;
-  const int blk = blockIdx.x;
-  const int e = a.bexp[blk];
-  if (e < 0) return;
-  __shared__ uint16_t sa[kBM][kLdsK];
-  __shared__ uint16_t sb[128][kLdsK];
+  extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
-  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 128;
+  const int NT = static_cast<int>((a.H + kBN - 1) / kBN);
+  int e, blk, nt;
+  if (!map_tile(a, NT, e, blk, nt)) return;
+  constexpr int ES = Q ? 1 : 2;
+  const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * kBN;
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
-  const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
-  const int lane = lane_id(), wave = threadIdx.x / kWave;
-  const int wm = wave / 2, wn = wave % 2;  // wave tile: 32 rows x 64 cols
-  floatx4 acc[2][4];
+  const LoadMap<Q> m;
+  const uint16_t* arow[Geo<Q>::A_INSTR];
+  const char* brow[Geo<Q>::B_INSTR];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int64_t H = a.H, I = a.I;
-  for (int64_t k0 = 0; k0 < I; k0 += kBK) {
-    stage_a(sa, I, k0, [&](int r) -> const uint16_t* {
-      const int p = spair[r];
-      return p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
-    });
-    stage_w<Q, 128>(sb, wbase, a.d_sn, I, k0, [&](int r) -> int64_t {
-      const int64_t h = n0 + r;
-      return h < H ? h : -1;
-    });
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 32) {
-      const int kk = ks + 8 * (lane / 16);
-      bf16x8_t fa[2], fb[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = lds_frag(sa, 32 * wm + 16 * i + (lane % 16), kk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) fb[j] = lds_frag(sb, 64 * wn + 16 * j + (lane % 16), kk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
+  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+    const int p = spair[m.ra[j]];
+    arow[j] = p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
   }
+  const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+    const int64_t h = h0 + m.rb[j];
+    brow[j] = h < H ? wbase + (h * a.d_sn) * ES : nullptr;
+  }
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  floatx4 acc[4][4];
+  tile_gemm<Q>(acc, I, arow, brow, reinterpret_cast<char*>(lds_raw), [&](int j) { return 64 * wave + 16 * j; });
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t h = n0 + 64 * wn + 16 * j + (lane % 16);
+    const int64_t h = h0 + 64 * wave + 16 * j + (lane & 15);
     if (h >= H) continue;
     float sc = 1.f;
     if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + h);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = 32 * wm + 16 * i + 4 * (lane / 16) + v;
-        const int p = spair[row];
+        const int p = spair[16 * i + 4 * (lane >> 4) + v];
         if (p >= a.P) continue;
-        float val = acc[i][j][v];
-        if (Q) val *= sc;
-        a.o_buf[static_cast<int64_t>(p) * H + h] = round_bf16(val) * a.wts[p];
+        const float val = Q ? acc[i][j][v] * sc : acc[i][j][v];
+        a.part[static_cast<int64_t>(p) * H + h] = f32_to_bf16(val);
       }
   }
 }
 
 // -------------------------------------------------------------------------------------------- combine
 
+// One thread per 8 consecutive outputs of a token: y = bf16(sum_k w_k * part_k) (+ residual, rounded again).
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
+  const int64_t H8 = a.H / 8;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(a.n_tokens) * a.H;
-  if (idx >= total) return;
-  const int64_t t = idx / a.H, h = idx % a.H;
-  const float* o = a.o_buf + t * a.nk * a.H + h;
-  float acc = 0.f;
+  if (idx >= static_cast<int64_t>(a.n_tokens) * H8) return;
+  const int64_t t = idx / H8, h = (idx % H8) * 8;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   for (int k = 0; k < a.nk; ++k) {
-    const int64_t id = load_id(a.ids, a.ids_dtype, t * a.nk + k);
-    if (id >= 0 && id < a.E1) acc += o[static_cast<int64_t>(k) * a.H];  // dropped pairs have no row
+    const int64_t p = t * a.nk + k;
+    const int64_t id = load_id(a.ids, a.ids_dtype, p);
+    if (id < 0 || id >= a.E1) continue;  // dropped pairs have no row
+    const float w = a.wts[p];
+    const uint4 v = *reinterpret_cast<const uint4*>(a.part + p * a.H + h);
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = fmaf(w, __uint_as_float(u[i] << 16), acc[2 * i]);
+      acc[2 * i + 1] = fmaf(w, __uint_as_float(u[i] & 0xffff0000u), acc[2 * i + 1]);
+    }
   }
-  float out = round_bf16(acc);
-  if (a.res) out += bf16_to_f32(a.res[t * a.res_rs + h]);
-  a.y[t * a.ys + h] = f32_to_bf16(out);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float lo = round_bf16(acc[2 * i]), hi = round_bf16(acc[2 * i + 1]);
+    if (a.res) {
+      lo += bf16_to_f32(a.res[t * a.res_rs + h + 2 * i]);
+      hi += bf16_to_f32(a.res[t * a.res_rs + h + 2 * i + 1]);
+    }
+    o[i] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  }
+  uint16_t* yr = a.y + t * a.ys + h;
+  if ((reinterpret_cast<uintptr_t>(yr) & 15) == 0) {
+    *reinterpret_cast<uint4*>(yr) = make_uint4(o[0], o[1], o[2], o[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      yr[2 * i] = static_cast<uint16_t>(o[i] & 0xffff);
+      yr[2 * i + 1] = static_cast<uint16_t>(o[i] >> 16);
+    }
+  }
+}
+
+// Dynamic LDS above the default limit needs an opt-in per kernel and device (done once each).
+template <class K>
+int allow_lds(K kernel, size_t bytes, const char* what) {
+  static std::mutex mu;
+  static bool done[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!done[dev]) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(bytes));
+    if (e != hipSuccess) return mm::set_error(MM_ERR_HIP, "HIP error setting LDS size of %s: %s", what, hipGetErrorString(e));
+    done[dev] = true;
+  }
+  return MM_OK;
+}
+
+template <bool Q>
+int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
+  int rc;
+  if (phases & MM_PHASE_GATE_UP) {
+    const int64_t nt = (a.I + kBN / 2 - 1) / (kBN / 2);
+    const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
+    if ((rc = allow_lds(prefill_gate_up_kernel<Q>, Geo<Q>::LDS, "prefill_gate_up"))) return rc;
+    hipLaunchKernelGGL(prefill_gate_up_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
+    if ((rc = mm::check_launch("moe_prefill gate_up"))) return rc;
+  }
+  if (phases & MM_PHASE_DOWN) {
+    const int64_t nt = (a.H + kBN - 1) / kBN;
+    const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
+    if ((rc = allow_lds(prefill_down_kernel<Q>, Geo<Q>::LDS, "prefill_down"))) return rc;
+    hipLaunchKernelGGL(prefill_down_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
+    if ((rc = mm::check_launch("moe_prefill down"))) return rc;
+  }
+  return MM_OK;
 }
 
 }  // namespace
@@ -278,20 +446,23 @@ int check_experts(const char* who, const mm_experts* ex);
 }
 
 extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex, int64_t nk,
-                              const void* ids, int ids_dtype, const float* wts, const int32_t* sorted_ids, const int32_t* bexp, int64_t nb,
-                              int32_t block_m, const void* residual, int64_t res_row_stride, void* a_buf, float* o_buf,
-                              void* y, int64_t y_row_stride, int phases, void* stream) {
+                              const void* ids, int ids_dtype, const float* wts, const int32_t* sorted_ids,
+                              const int32_t* bexp, const int32_t* expert_offsets, int64_t nb, int32_t block_m,
+                              const void* residual, int64_t res_row_stride, void* a_buf, void* part_buf, void* y,
+                              int64_t y_row_stride, int phases, void* stream) {
   int rc = mm::check_experts("moe_prefill", ex);
   if (rc) return rc;
   MM_REQUIRE(block_m == kBM, "moe_prefill: block_m must be %d (got %d)", kBM, block_m);
   MM_REQUIRE(n_tokens >= 0 && nk >= 1 && n_tokens * nk <= (1LL << 30), "moe_prefill: bad token/slot counts");
-  MM_REQUIRE(nb >= 0 && nb <= 0x7fffffffLL / kBM, "moe_prefill: bad block count");
+  MM_REQUIRE(nb >= 0 && nb * 16 <= 0x7fffffffLL, "moe_prefill: bad block count");
+  MM_REQUIRE(ex->n_slots <= 0x7fffffff && ex->hidden % 8 == 0, "moe_prefill: hidden must be a multiple of 8");
   if (n_tokens == 0) return MM_OK;
   MM_REQUIRE(ids_dtype == MM_INT32 || ids_dtype == MM_INT64, "moe_prefill: ids must be int32 or int64");
-  MM_REQUIRE(x && ids && wts && sorted_ids && bexp && a_buf && o_buf && y, "moe_prefill: null pointer");
+  MM_REQUIRE(x && ids && wts && sorted_ids && bexp && expert_offsets && a_buf && part_buf && y,
+             "moe_prefill: null pointer");
   MM_REQUIRE(x_row_stride >= ex->hidden && y_row_stride >= ex->hidden, "moe_prefill: row stride smaller than hidden");
   MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0, "moe_prefill: x rows must be 16-byte aligned");
-  MM_REQUIRE(mm::aligned16(a_buf), "moe_prefill: a_buf must be 16-byte aligned");
+  MM_REQUIRE(mm::aligned16(a_buf) && mm::aligned16(part_buf), "moe_prefill: a_buf and part_buf must be 16-byte aligned");
   MM_REQUIRE(!residual || res_row_stride >= ex->hidden, "moe_prefill: residual row stride smaller than hidden");
   PrefillArgs a;
   a.x = static_cast<const uint16_t*>(x);
@@ -305,7 +476,7 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   a.wts = wts;
   a.sorted_ids = sorted_ids;
   a.bexp = bexp;
-  a.nb = static_cast<int>(nb);
+  a.offsets = expert_offsets;
   a.w_gu = ex->w_gu;
   a.w_d = ex->w_d;
   a.s_gu = ex->s_gu;
@@ -322,28 +493,17 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   a.res = static_cast<const uint16_t*>(residual);
   a.res_rs = res_row_stride;
   a.a_buf = static_cast<uint16_t*>(a_buf);
-  a.o_buf = o_buf;
+  a.part = static_cast<uint16_t*>(part_buf);
   a.y = static_cast<uint16_t*>(y);
   a.ys = y_row_stride;
   hipStream_t st = MM_STREAM(stream);
-  const bool q = ex->w_dtype == MM_INT8;
   if (phases == MM_PHASE_ALL) phases = MM_PHASE_GATE_UP | MM_PHASE_DOWN | MM_PHASE_COMBINE;
-  if (nb > 0 && (phases & MM_PHASE_GATE_UP)) {
-    dim3 g1(static_cast<unsigned>(nb), static_cast<unsigned>((a.I + 63) / 64));
-    if (q) hipLaunchKernelGGL(prefill_gate_up_kernel<true>, g1, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL(prefill_gate_up_kernel<false>, g1, dim3(kThreads), 0, st, a);
-    rc = mm::check_launch("moe_prefill gate_up");
-    if (rc) return rc;
-  }
-  if (nb > 0 && (phases & MM_PHASE_DOWN)) {
-    dim3 g2(static_cast<unsigned>(nb), static_cast<unsigned>((a.H + 127) / 128));
-    if (q) hipLaunchKernelGGL(prefill_down_kernel<true>, g2, dim3(kThreads), 0, st, a);
-    else hipLaunchKernelGGL(prefill_down_kernel<false>, g2, dim3(kThreads), 0, st, a);
-    rc = mm::check_launch("moe_prefill down");
+  if (nb > 0) {
+    rc = ex->w_dtype == MM_INT8 ? launch_gemms<true>(a, nb, phases, st) : launch_gemms<false>(a, nb, phases, st);
     if (rc) return rc;
   }
   if (!(phases & MM_PHASE_COMBINE)) return MM_OK;
-  const int64_t total = n_tokens * a.H;
+  const int64_t total = n_tokens * (a.H / 8);
   hipLaunchKernelGGL(prefill_combine_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, st, a);
   return mm::check_launch("moe_prefill combine");
 }

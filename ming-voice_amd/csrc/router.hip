@@ -1,4 +1,6 @@
 // MoE router: fp32 logits GEMV/GEMM and top-k selection (fused_ops.py:40-103, engine.py:326-333).
+#include <algorithm>
+
 #include "mm_common.h"
 
 namespace {
@@ -13,21 +15,21 @@ __device__ __forceinline__ float4 load4(const typename TX::T* p, int64_t i) {
   return make_float4(TX::ld(p, i), TX::ld(p, i + 1), TX::ld(p, i + 2), TX::ld(p, i + 3));
 }
 
-// logits for up to 8 tokens: one wave per expert, lanes stride over the hidden dim 4 floats at a time.
+// logits for up to 8 tokens: one workgroup per expert, its 4 waves split the hidden dim (float4 loads of
+// the fp32 router row), partial sums reduced through LDS in wave order.
 template <class TX>
 __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
                                                           int64_t xs, const float* __restrict__ w32, int E,
                                                           float* __restrict__ logits) {
-  const int e = blockIdx.x * 4 + threadIdx.x / kWave;
-  if (e >= E) return;
-  const int lane = lane_id();
+  __shared__ float red[4][8];
+  const int e = blockIdx.x;
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
   const float* wr = w32 + static_cast<int64_t>(e) * H;
   float acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.f;
-  const bool vec = (H & 3) == 0;
-  if (vec) {
-    for (int64_t h = 4 * lane; h < H; h += 4 * kWave) {
+  if ((H & 3) == 0) {
+    for (int64_t h = 4 * static_cast<int64_t>(threadIdx.x); h < H; h += 4 * 256) {
       const float4 wv = *reinterpret_cast<const float4*>(wr + h);
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
@@ -41,7 +43,7 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
       }
     }
   } else {
-    for (int64_t h = lane; h < H; h += kWave) {
+    for (int64_t h = threadIdx.x; h < H; h += 256) {
       const float wv = wr[h];
 #pragma unroll
       for (int t = 0; t < 8; ++t)
@@ -52,63 +54,62 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
   for (int t = 0; t < 8; ++t) {
     if (t < n_tokens) {
       const float v = wave_sum(acc[t]);
-      if (lane == 0) logits[static_cast<int64_t>(t) * E + e] = v;
+      if (lane == 0) red[wave][t] = v;
     }
   }
+  __syncthreads();
+  if (threadIdx.x < n_tokens)
+    logits[static_cast<int64_t>(threadIdx.x) * E + e] =
+        ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
 }
 
-// logits for many tokens: 64 tokens x 64 experts per workgroup, fp32 register tiles over LDS k-slabs.
-constexpr int kTM = 64, kTE = 64, kTK = 16;
-
+// logits for many tokens on fp32 MFMA (v_mfma_f32_16x16x4_f32): a workgroup computes 16 tokens x 16
+// experts; its 4 waves and, inside a wave, the 4 lane quarters each own a contiguous run of the hidden dim
+// (any k order is valid as long as the token and expert operands of a lane agree). The 4 wave partials
+// are summed through LDS in wave order.
 template <class TX>
-__global__ __launch_bounds__(256) void router_gemm_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
+__global__ __launch_bounds__(256) void router_mfma_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
                                                           int64_t xs, const float* __restrict__ w32, int E,
                                                           float* __restrict__ logits) {
-  __shared__ float xsm[kTK][kTM + 4];
-  __shared__ float wsm[kTK][kTE + 4];
-  const int t0 = blockIdx.y * kTM, e0 = blockIdx.x * kTE;
-  const int tid = threadIdx.x;
-  const int ty = tid / 16, tx = tid % 16;
-  float acc[4][4];
+  __shared__ float red[4][16][17];
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  const int row = lane % 16, q = lane / 16;
+  const int t = t0 + row, e = e0 + row;
+  const bool tok = t < n_tokens, exp_ok = e < E;
+  // this lane's run of the hidden dim: S consecutive k, S a multiple of 4
+  const int64_t S = ((H + 63) / 64) * 4;
+  const int64_t kb = (static_cast<int64_t>(wave) * 4 + q) * S;
+  const typename TX::T* xr = x + static_cast<int64_t>(tok ? t : 0) * xs;
+  const float* wr = w32 + static_cast<int64_t>(exp_ok ? e : 0) * H;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  const bool vec = (H & 3) == 0;
+  for (int64_t s = 0; s < S; s += 4) {
+    const int64_t k = kb + s;
+    float a[4], b[4];
+    if (vec && k + 4 <= H) {
+      const float4 wv = exp_ok ? *reinterpret_cast<const float4*>(wr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 xv = tok ? load4<TX>(xr, k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      a[0] = xv.x; a[1] = xv.y; a[2] = xv.z; a[3] = xv.w;
+      b[0] = wv.x; b[1] = wv.y; b[2] = wv.z; b[3] = wv.w;
+    } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (int64_t k0 = 0; k0 < H; k0 += kTK) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int idx = tid + 256 * r;  // 0..1023 over a 64 x 16 tile
-      const int row = idx / kTK, kk = idx % kTK;
-      const int64_t k = k0 + kk;
-      const int t = t0 + row, e = e0 + row;
-      xsm[kk][row] = (t < n_tokens && k < H) ? TX::ld(x + static_cast<int64_t>(t) * xs, k) : 0.f;
-      wsm[kk][row] = (e < E && k < H) ? w32[static_cast<int64_t>(e) * H + k] : 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const bool in = k + i < H;
+        a[i] = (tok && in) ? TX::ld(xr, k + i) : 0.f;
+        b[i] = (exp_ok && in) ? wr[k + i] : 0.f;
+      }
     }
-    __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < kTK; ++kk) {
-      float xv[4], wv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[i] = xsm[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) wv[j] = wsm[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
-    }
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[i], acc, 0, 0, 0);
   }
+  // D[token = 4*(lane/16) + v][expert = lane % 16]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = t0 + ty * 4 + i;
-    if (t >= n_tokens) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = e0 + tx * 4 + j;
-      if (e < E) logits[static_cast<int64_t>(t) * E + e] = acc[i][j];
-    }
-  }
+  for (int v = 0; v < 4; ++v) red[wave][4 * q + v][row] = acc[v];
+  __syncthreads();
+  const int i = threadIdx.x / 16, j = threadIdx.x % 16;
+  if (t0 + i < n_tokens && e0 + j < E)
+    logits[static_cast<int64_t>(t0 + i) * E + e0 + j] = ((red[0][i][j] + red[1][i][j]) + red[2][i][j]) + red[3][i][j];
 }
 
 struct SelectArgs {
@@ -125,22 +126,24 @@ struct SelectArgs {
 };
 
 // Arg-max over the lane-held slots then across the wave; lowest expert index wins ties.
-__device__ __forceinline__ void slots_argmax(const float (&v)[kSlots], int nslots, float& best, int& bidx) {
+template <int NS>
+__device__ __forceinline__ void slots_argmax(const float (&v)[NS], int nslots, float& best, int& bidx) {
   // Slot 0 seeds the search so that an all -inf input still yields the lowest index, as an
   // arg-max with first-index ties does. Slots past the valid range hold -inf and larger indices.
   const int lane = lane_id();
   best = v[0];
   bidx = lane;
 #pragma unroll
-  for (int j = 1; j < kSlots; ++j) {
+  for (int j = 1; j < NS; ++j) {
     if (j < nslots && v[j] > best) { best = v[j]; bidx = lane + kWave * j; }
   }
   wave_argmax(best, bidx);
 }
 
 // One wave per token: selection, weights and the optional shared-expert slot.
+template <int NS>
 __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
-  __shared__ float rbuf[4][kMaxExperts];
+  __shared__ float rbuf[4][NS * kWave];
   const int wv = threadIdx.x / kWave;
   const int t = blockIdx.x * 4 + wv;
   if (t >= a.n_tokens) return;
@@ -148,9 +151,9 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
   const int E = a.E;
   const int nslots = (E + kWave - 1) / kWave;
   const float* lg = a.logits + static_cast<int64_t>(t) * E;
-  float score[kSlots], key[kSlots];  // score: weight source; key: selection value
+  float score[NS], key[NS];  // score: weight source; key: selection value
 #pragma unroll
-  for (int j = 0; j < kSlots; ++j) {
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + kWave * j;
     score[j] = 0.f;
     key[j] = -INFINITY;
@@ -168,11 +171,11 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
   if (a.scoring == MM_SCORE_SOFTMAX) {
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) m = fmaxf(m, key[j]);
+    for (int j = 0; j < NS; ++j) m = fmaxf(m, key[j]);
     m = wave_max(m);
     float den = 0.f;
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
+    for (int j = 0; j < NS; ++j) {
       const int e = lane + kWave * j;
       if (j < nslots && e < E) {
         score[j] = __expf(key[j] - m);
@@ -181,22 +184,22 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
     }
     den = wave_sum(den);
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) score[j] = score[j] / den;
+    for (int j = 0; j < NS; ++j) score[j] = score[j] / den;
   } else if (a.n_group > 1) {
     // group score = sum of the two largest keys of the group (first max excluded once)
     const int G = a.n_group, GS = E / G;
     float* r = rbuf[wv];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
+    for (int j = 0; j < NS; ++j) {
       const int e = lane + kWave * j;
       if (j < nslots && e < E) r[e] = key[j];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float gscore[kSlots];
+    float gscore[NS];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
+    for (int j = 0; j < NS; ++j) {
       const int g = lane + kWave * j;
       gscore[j] = -INFINITY;
       if (g < G) {
@@ -213,22 +216,22 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
       }
     }
     // keep the topk_group best groups (iterative arg-max, lowest group index on ties)
-    bool keep[kSlots];
+    bool keep[NS];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) keep[j] = false;
+    for (int j = 0; j < NS; ++j) keep[j] = false;
     for (int it = 0; it < a.topk_group; ++it) {
       float bv;
       int bi;
-      slots_argmax(gscore, kSlots, bv, bi);
+      slots_argmax(gscore, NS, bv, bi);
 #pragma unroll
-      for (int j = 0; j < kSlots; ++j)
+      for (int j = 0; j < NS; ++j)
         if (lane + kWave * j == bi) { keep[j] = true; gscore[j] = -INFINITY; }
     }
     // broadcast the kept-group flags through LDS and mask the keys of dropped groups
     __builtin_amdgcn_wave_barrier();
     float* kf = rbuf[wv];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
+    for (int j = 0; j < NS; ++j) {
       const int g = lane + kWave * j;
       if (g < G) kf[g] = keep[j] ? 1.f : 0.f;
     }
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
+    for (int j = 0; j < NS; ++j) {
       const int e = lane + kWave * j;
       if (j < nslots && e < E && kf[e / GS] == 0.f) key[j] = -INFINITY;
     }
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
     slots_argmax(key, nslots, bv, bi);
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j)
+    for (int j = 0; j < NS; ++j)
       if (lane + kWave * j == bi) { s = score[j]; key[j] = -INFINITY; }
     s = wave_sum(s);  // exactly one lane contributes
     total += s;
@@ -304,7 +307,12 @@ int launch_select(const float* logits, int64_t n_tokens, int64_t E, const float*
   SelectArgs a{logits, static_cast<int>(n_tokens), static_cast<int>(E), bias, scoring, n_group, topk_group, top_k,
                scale, append_shared, ids, ids_dtype, wts, out_row_stride};
   const unsigned blocks = static_cast<unsigned>((n_tokens + 3) / 4);
-  hipLaunchKernelGGL(router_select_kernel, dim3(blocks), dim3(256), 0, s, a);
+  // lane-held slots: enough for the experts and (sigmoid mode) the groups
+  const int64_t need = std::max<int64_t>(E, n_group);
+  if (need <= 64) hipLaunchKernelGGL(router_select_kernel<1>, dim3(blocks), dim3(256), 0, s, a);
+  else if (need <= 128) hipLaunchKernelGGL(router_select_kernel<2>, dim3(blocks), dim3(256), 0, s, a);
+  else if (need <= 256) hipLaunchKernelGGL(router_select_kernel<4>, dim3(blocks), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(router_select_kernel<kSlots>, dim3(blocks), dim3(256), 0, s, a);
   return mm::check_launch("router_select");
 }
 
@@ -313,11 +321,11 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
                   hipStream_t s) {
   const auto* xp = static_cast<const typename TX::T*>(x);
   if (n_tokens <= 8) {
-    hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>((E + 3) / 4)), dim3(256), 0, s, xp,
+    hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xp,
                        static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits);
   } else {
-    dim3 grid(static_cast<unsigned>((E + kTE - 1) / kTE), static_cast<unsigned>((n_tokens + kTM - 1) / kTM));
-    hipLaunchKernelGGL(router_gemm_kernel<TX>, grid, dim3(256), 0, s, xp, static_cast<int>(n_tokens), H, xs, w32,
+    dim3 grid(static_cast<unsigned>((E + 15) / 16), static_cast<unsigned>((n_tokens + 15) / 16));
+    hipLaunchKernelGGL(router_mfma_kernel<TX>, grid, dim3(256), 0, s, xp, static_cast<int>(n_tokens), H, xs, w32,
                        static_cast<int>(E), logits);
   }
   return mm::check_launch("router_logits");

@@ -124,7 +124,7 @@ class PrefillScratch:
         self.bexp = torch.empty(self.nb, dtype=torch.int32, device=device)
         self.offsets = torch.empty(E1 + 1, dtype=torch.int32, device=device)
         self.a = torch.empty(P, I, device=device, dtype=torch.bfloat16)
-        self.o = torch.empty(P, H, device=device, dtype=torch.float32)
+        self.part = torch.empty(P, H, device=device, dtype=torch.bfloat16)
         self.y = torch.empty(N, H, device=device, dtype=torch.bfloat16)
 
 
@@ -158,7 +158,7 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
     nb = sc.nb
     if align:
         _align_blocks(flat, E1, BLOCK_M, expert_offsets=sc.offsets, out=(sc.sorted_ids, sc.bexp))
-    sorted_ids, bexp, a, o, y = sc.sorted_ids, sc.bexp, sc.a, sc.o, sc.y
+    sorted_ids, bexp, a, part, y = sc.sorted_ids, sc.bexp, sc.a, sc.part, sc.y
     r2 = None
     if residual is not None:
         r2 = residual.reshape(N, H)
@@ -169,8 +169,9 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
     lib = _mm.load()
     with _mm.on_device(x):
         _mm.check(lib.mm_moe_prefill(_mm.ptr(x2), N, x2.stride(0), ex, KP1, _mm.ptr(flat), _mm.dtype_code(flat),
-                                     _mm.ptr(wts), _mm.ptr(sorted_ids), _mm.ptr(bexp), nb, BLOCK_M, _mm.ptr(r2),
-                                     r2.stride(0) if r2 is not None else 0, _mm.ptr(a), _mm.ptr(o), _mm.ptr(y), H,
+                                     _mm.ptr(wts), _mm.ptr(sorted_ids), _mm.ptr(bexp), _mm.ptr(sc.offsets), nb,
+                                     BLOCK_M, _mm.ptr(r2), r2.stride(0) if r2 is not None else 0, _mm.ptr(a),
+                                     _mm.ptr(part), _mm.ptr(y), H,
                                      phases, _mm.stream_of(x)), "fused_moe_prefill")
     return y
 

@@ -69,11 +69,11 @@ def test_argument_validation_reports_messages():
     assert "16-byte aligned" in _err(lib.mm_moe_decode(P, 1, 2048, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None,
                                                        0, P, P, 2048, 0, None))
     ex.w_gu, ex.hidden = 16, 2047
-    assert "multiples" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, 10, 64,
-                                                  None, 0, P, P, P, 2048, 0, None))
+    assert "multiples" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10,
+                                                  64, None, 0, P, P, P, 2048, 0, None))
     ex.hidden = 2048
-    assert "block_m" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, 10, 32,
-                                                None, 0, P, P, P, 2048, 0, None))
+    assert "block_m" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10,
+                                                32, None, 0, P, P, P, 2048, 0, None))
     assert "M=17" in _err(lib.mm_small_linear(P, 17, 64, 64, P, 64, 64, None, 0, None, 0, None, 0.0, None, P, 64, None))
     assert "scale dtype" in _err(lib.mm_quantize_rows_int8(P, mm.MM_BF16, 4, 64, 64, P, 64, P, mm.MM_INT8, None))
 

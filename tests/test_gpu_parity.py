@@ -241,6 +241,30 @@ def test_prefill_zipf_2048_subset_and_histogram(blk):
     close(y.cpu()[sub], _oracle_moe(cpu, xn[sub.to(DEV)], ids[sub.to(DEV)], wts[sub.to(DEV)]))
 
 
+@pytest.mark.parametrize("int8", [False, True])
+def test_prefill_and_decode_ragged_shapes(int8):
+    """Tails on every tiled dim: hidden 1536 (6 column tiles of 256), inter 208 (partial 128-column tile and a
+    partial 64-wide k slab), 129 expert slots (the Ming thinker's 128 + shared), top-8."""
+    H, I, E, K = 1536, 208, 128, 8
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 130, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 131, DEV)
+    g = torch.Generator().manual_seed(132)
+    for n in (3, 77):
+        sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
+        ids = torch.cat([sel, torch.full((n, 1), E)], 1).to(DEV)
+        wts = torch.cat([torch.rand(n, K, generator=g), torch.ones(n, 1)], 1).to(DEV)
+        x = W.normal((n, H), 1.0, 133 + n, DEV)
+        if int8:
+            q_gu, s_gu = fused_moe.quantize_rows_int8(w_gu, scale_dtype=torch.bfloat16)
+            q_d, s_d = fused_moe.quantize_rows_int8(w_d, scale_dtype=torch.bfloat16)
+            y = fused_moe.fused_moe_prefill(x, q_gu, q_d, ids, wts, s_gu=s_gu, s_d=s_d)
+            ref = O.moe(x.cpu(), q_gu.cpu(), q_d.cpu(), ids.cpu(), wts.cpu(), s_gu.cpu(), s_d.cpu())
+        else:
+            y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
+            ref = O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu())
+        close(y, ref)
+
+
 def test_prefill_equals_per_token_decode(blk):
     b, _ = blk
     x = W.tokens(24, seed=95, device=DEV)
