@@ -1,15 +1,15 @@
 // Grouped prefill MoE on bf16 MFMA (fused_moe.py:92-196).
 //
 // mm_align_blocks groups the (token, slot) pairs by expert into blocks of 64 rows and reports each expert's
-// padded row range. A tile is (expert block of 64 pairs) x (256 output columns):
-//   GATE_UP: columns are 128 gate + the matching 128 up rows of W_gu[e]; the epilogue writes
+// padded row range. A tile is (expert block of 64 pairs) x (BN = 128 or 256 output columns):
+//   GATE_UP: columns are BN/2 gate + the matching BN/2 up rows of W_gu[e]; the epilogue writes
 //            a[pair] = bf16(bf16(silu(bf16(g))) * bf16(u)) (int8: row scale on the fp32 accumulator first).
-//   DOWN:    columns are 256 rows of W_d[e]; the epilogue writes part[pair] = bf16(a . Wd^T [* s]).
+//   DOWN:    columns are BN rows of W_d[e]; the epilogue writes part[pair] = bf16(a . Wd^T [* s]).
 //   COMBINE: y[t] = bf16(sum_k w[t,k] * part[t*nk+k]) (fp32, slots in order) (+ residual, rounded again),
 //            the reference's f32(bf16(acc)) * w summed over slots (fused_moe.py:147-148, 196).
 // Tiles are ordered expert-major, then column tile, then block, and dealt out to the 8 XCDs in contiguous
 // runs, so the blocks that share a weight tile run together on one XCD and hit its L2. The k loop copies
-// 64-wide slabs of the activation rows and of the weight rows straight into LDS (global_load_lds, 3-4
+// 64-wide slabs of the activation rows and of the weight rows straight into LDS (global_load_lds, several
 // slabs in flight) and feeds v_mfma_f32_16x16x32_bf16 from there. int8 weights stay int8 in LDS and are
 // widened to bf16 (exact for |q| <= 127) as fragments are read.
 #include <mutex>
@@ -21,10 +21,30 @@ namespace {
 using namespace mmd;
 
 constexpr int kBM = 64;          // rows (pairs) per block, = align block_m
-constexpr int kBN = 256;         // output columns per tile
 constexpr int kBK = 64;          // k-slab (bf16 elements): rows of 128 bytes = 8 chunks of 16 bytes
-constexpr int kThreads = 256;    // 4 waves, each 64 rows x 64 columns
+constexpr int kThreads = 256;    // 4 waves
 constexpr int kXcds = 8;
+// Tile shape per weight type: output columns per tile, LDS stages (k-slabs in flight) and wave rows
+// (1: each wave 64 rows x BN/4 columns; 2: 32 rows x BN/2 columns). LDS = stages x (8 KB + BN x 128 B
+// bf16 / BN x 64 B int8); fewer stages let more workgroups share a CU.
+#ifndef MM_PREFILL_BN_BF16
+#define MM_PREFILL_BN_BF16 128
+#endif
+#ifndef MM_PREFILL_SLABS_BF16
+#define MM_PREFILL_SLABS_BF16 3
+#endif
+#ifndef MM_PREFILL_WM_BF16
+#define MM_PREFILL_WM_BF16 1
+#endif
+#ifndef MM_PREFILL_BN_INT8
+#define MM_PREFILL_BN_INT8 256
+#endif
+#ifndef MM_PREFILL_SLABS_INT8
+#define MM_PREFILL_SLABS_INT8 2
+#endif
+#ifndef MM_PREFILL_WM_INT8
+#define MM_PREFILL_WM_INT8 1
+#endif
 
 struct PrefillArgs {
   const uint16_t* x;
@@ -99,15 +119,21 @@ __device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes
 
 template <bool Q>
 struct Geo {
+  static constexpr int BN = Q ? MM_PREFILL_BN_INT8 : MM_PREFILL_BN_BF16;     // output columns per tile
+  static constexpr int NS = Q ? MM_PREFILL_SLABS_INT8 : MM_PREFILL_SLABS_BF16;  // slabs in flight
+  static constexpr int WM = Q ? MM_PREFILL_WM_INT8 : MM_PREFILL_WM_BF16;     // wave rows
+  static constexpr int WN = 4 / WM;                   // wave columns
+  static constexpr int FM = kBM / WM / 16;            // 16-row fragments per wave
+  static constexpr int FN = BN / WN / 16;             // 16-column fragments per wave
   static constexpr int ROWB = Q ? 64 : 128;           // weight bytes per row per slab
-  static constexpr int A_BYTES = kBM * 128;            // 8 KB
-  static constexpr int B_BYTES = kBN * ROWB;           // 32 KB bf16, 16 KB int8
+  static constexpr int A_BYTES = kBM * 128;           // 8 KB
+  static constexpr int B_BYTES = BN * ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int NS = Q ? 4 : 3;                 // slabs in flight
   static constexpr size_t LDS = static_cast<size_t>(NS) * STAGE;
-  static constexpr int A_INSTR = A_BYTES / 1024 / 4;  // per wave per slab: 2
-  static constexpr int B_INSTR = B_BYTES / 1024 / 4;  // 8 bf16, 4 int8
+  static constexpr int A_INSTR = A_BYTES / 1024 / 4;  // direct-load instructions per wave per slab
+  static constexpr int B_INSTR = B_BYTES / 1024 / 4;
   static constexpr int LOADS = A_INSTR + B_INSTR;
+  static_assert((BN == 128 || BN == 256) && (WM == 1 || WM == 2) && FN % 2 == 0, "tile shape");
 };
 
 __device__ __forceinline__ int pos_bf16(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
@@ -181,20 +207,20 @@ __device__ __forceinline__ bf16x8_t lds_frag16(const char* base, int pos) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(base + pos));
 }
 
-// The shared GEMM body: acc[i][j] (i: 16-row fragment 0..3, j: 16-column fragment 0..3 of this wave's 64
-// columns) over K, with the tile row of the wave's column fragment j given by bcol(j).
+// The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
+// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j.
 template <bool Q, class BColFn>
-__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[4][4], int64_t K, const uint16_t* const* arow,
-                                          const char* const* brow, char* lds, BColFn bcol) {
-  constexpr int NS = Geo<Q>::NS;
-  constexpr int LOADS = Geo<Q>::LOADS;
+__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN], int64_t K,
+                                          const uint16_t* const* arow, const char* const* brow, char* lds, int r0,
+                                          BColFn bcol) {
+  constexpr int NS = Geo<Q>::NS, LOADS = Geo<Q>::LOADS, FM = Geo<Q>::FM, FN = Geo<Q>::FN;
   const int lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
   const LoadMap<Q> m;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   const int nk = static_cast<int>((K + kBK - 1) / kBK);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
@@ -202,9 +228,14 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[4][4], int64_t K, const
   for (int kt = 0; kt < nk; ++kt) {
     // slabs issued after kt so far: min(nk - 1 - kt, NS - 2); wait for kt's own loads
     const int pending = min(nk - 1 - kt, NS - 2);
-    if (pending >= 2) wait_vmcnt<2 * LOADS>();
-    else if (pending == 1) wait_vmcnt<LOADS>();
-    else wait_vmcnt<0>();
+    static_assert(NS >= 2 && NS <= 6 && (NS - 2) * LOADS < 64, "slab count");
+    switch (pending) {
+      case 4: wait_vmcnt<(NS >= 6 ? 4 : 0) * LOADS>(); break;
+      case 3: wait_vmcnt<(NS >= 5 ? 3 : 0) * LOADS>(); break;
+      case 2: wait_vmcnt<(NS >= 4 ? 2 : 0) * LOADS>(); break;
+      case 1: wait_vmcnt<LOADS>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
     // slab kt visible to all waves; every wave is done with slab kt-1. A plain barrier: the loads of
     // slab kt were waited for above, and a memory fence would also wait for the later slabs' loads.
     __builtin_amdgcn_s_barrier();
@@ -213,39 +244,38 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[4][4], int64_t K, const
     const char* sb = sa + Geo<Q>::A_BYTES;
     if constexpr (Q) {
       // one 16-byte int8 chunk per lane and fragment feeds both 32-wide steps
-      bf16x8_t fb[2][4];
+      bf16x8_t fb[2][FN];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = bcol(j) + lr;
+      for (int j = 0; j < FN; ++j) {
         uint4 lo, hi;
-        widen_i8(*reinterpret_cast<const uint4*>(sb + pos_i8(r, lq)), lo, hi);
+        widen_i8(*reinterpret_cast<const uint4*>(sb + pos_i8(bcol(j) + lr, lq)), lo, hi);
         fb[0][j] = __builtin_bit_cast(bf16x8_t, lo);
         fb[1][j] = __builtin_bit_cast(bf16x8_t, hi);
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        bf16x8_t fa[4];
+        bf16x8_t fa[FM];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fa[i] = lds_frag16(sa, pos_bf16(16 * i + lr, 2 * lq + ks));
+        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_bf16(r0 + 16 * i + lr, 2 * lq + ks));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int ch = ks * 4 + lq;
-        bf16x8_t fa[4], fb[4];
+        bf16x8_t fa[FM], fb[FN];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fa[i] = lds_frag16(sa, pos_bf16(16 * i + lr, ch));
+        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_bf16(r0 + 16 * i + lr, ch));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) fb[j] = lds_frag16(sb, pos_bf16(bcol(j) + lr, ch));
+        for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_bf16(bcol(j) + lr, ch));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
       }
     }
@@ -256,38 +286,44 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[4][4], int64_t K, const
 
 template <bool Q>
 __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a) {
+  using G = Geo<Q>;
+  constexpr int HALF = G::BN / 2;  // gate columns per tile (and as many up columns)
   extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
-  const int NT = static_cast<int>((a.I + kBN / 2 - 1) / (kBN / 2));
+  const int NT = static_cast<int>((a.I + HALF - 1) / HALF);
   int e, blk, nt;
   if (!map_tile(a, NT, e, blk, nt)) return;
   constexpr int ES = Q ? 1 : 2;
-  const int64_t I = a.I, n0 = static_cast<int64_t>(nt) * (kBN / 2);
+  const int64_t I = a.I, n0 = static_cast<int64_t>(nt) * HALF;
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
   // source rows of this thread's direct loads
   const LoadMap<Q> m;
-  const uint16_t* arow[Geo<Q>::A_INSTR];
-  const char* brow[Geo<Q>::B_INSTR];
+  const uint16_t* arow[G::A_INSTR];
+  const char* brow[G::B_INSTR];
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+  for (int j = 0; j < G::A_INSTR; ++j) {
     const int p = spair[m.ra[j]];
     arow[j] = p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
   }
   const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
-    const int r = m.rb[j];  // tile row: 0..127 gate, 128..255 up
-    const int64_t col = n0 + (r & 127);
-    brow[j] = col < I ? wbase + ((r < 128 ? col : I + col) * a.gu_sn) * ES : nullptr;
+  for (int j = 0; j < G::B_INSTR; ++j) {
+    const int r = m.rb[j];  // tile row: gate rows first, then the matching up rows
+    const int64_t col = n0 + (r % HALF);
+    brow[j] = col < I ? wbase + ((r < HALF ? col : I + col) * a.gu_sn) * ES : nullptr;
   }
   const int wave = threadIdx.x / kWave, lane = lane_id();
-  floatx4 acc[4][4];  // j = 0,1 gate fragments, 2,3 the matching up fragments
-  tile_gemm<Q>(acc, a.H, arow, brow, reinterpret_cast<char*>(lds_raw),
-               [&](int j) { return (j < 2 ? 0 : 128) + 32 * wave + 16 * (j & 1); });
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  const int r0 = wm * (kBM / G::WM);
+  constexpr int FG = G::FN / 2;      // gate fragments of the wave; the next FG are the matching up ones
+  const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
+  floatx4 acc[G::FM][G::FN];
+  tile_gemm<Q>(acc, a.H, arow, brow, reinterpret_cast<char*>(lds_raw), r0,
+               [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); });
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t col = n0 + 32 * wave + 16 * j + (lane & 15);
+  for (int j = 0; j < FG; ++j) {
+    const int64_t col = n0 + g0 + 16 * j + (lane & 15);
     if (col >= I) continue;
     float sg = 1.f, su = 1.f;
     if (Q) {
@@ -295,12 +331,12 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
       su = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + I + col);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::FM; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int p = spair[16 * i + 4 * (lane >> 4) + v];  // D[row = 4*(lane/16) + v][col = lane%16]
+        const int p = spair[r0 + 16 * i + 4 * (lane >> 4) + v];  // D[row = 4*(lane/16) + v][col = lane%16]
         if (p >= a.P) continue;
-        float g = acc[i][j][v], u = acc[i][j + 2][v];
+        float g = acc[i][j][v], u = acc[i][j + FG][v];
         if (Q) { g *= sg; u *= su; }
         const float gg = round_bf16(g), uu = round_bf16(u);
         a.a_buf[static_cast<int64_t>(p) * I + col] = f32_to_bf16(round_bf16(silu(gg)) * uu);
@@ -312,43 +348,47 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
 
 template <bool Q>
 __global__ __launch_bounds__(kThreads) void prefill_down_kernel(PrefillArgs a) {
+  using G = Geo<Q>;
   extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
-  const int NT = static_cast<int>((a.H + kBN - 1) / kBN);
+  const int NT = static_cast<int>((a.H + G::BN - 1) / G::BN);
   int e, blk, nt;
   if (!map_tile(a, NT, e, blk, nt)) return;
   constexpr int ES = Q ? 1 : 2;
-  const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * kBN;
+  const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * G::BN;
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
   const LoadMap<Q> m;
-  const uint16_t* arow[Geo<Q>::A_INSTR];
-  const char* brow[Geo<Q>::B_INSTR];
+  const uint16_t* arow[G::A_INSTR];
+  const char* brow[G::B_INSTR];
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+  for (int j = 0; j < G::A_INSTR; ++j) {
     const int p = spair[m.ra[j]];
     arow[j] = p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
   }
   const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+  for (int j = 0; j < G::B_INSTR; ++j) {
     const int64_t h = h0 + m.rb[j];
     brow[j] = h < H ? wbase + (h * a.d_sn) * ES : nullptr;
   }
   const int wave = threadIdx.x / kWave, lane = lane_id();
-  floatx4 acc[4][4];
-  tile_gemm<Q>(acc, I, arow, brow, reinterpret_cast<char*>(lds_raw), [&](int j) { return 64 * wave + 16 * j; });
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  const int r0 = wm * (kBM / G::WM);
+  const int c0 = wn * G::FN * 16;
+  floatx4 acc[G::FM][G::FN];
+  tile_gemm<Q>(acc, I, arow, brow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t h = h0 + 64 * wave + 16 * j + (lane & 15);
+  for (int j = 0; j < G::FN; ++j) {
+    const int64_t h = h0 + c0 + 16 * j + (lane & 15);
     if (h >= H) continue;
     float sc = 1.f;
     if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + h);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::FM; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int p = spair[16 * i + 4 * (lane >> 4) + v];
+        const int p = spair[r0 + 16 * i + 4 * (lane >> 4) + v];
         if (p >= a.P) continue;
         const float val = Q ? acc[i][j][v] * sc : acc[i][j][v];
         a.part[static_cast<int64_t>(p) * H + h] = f32_to_bf16(val);
@@ -423,14 +463,14 @@ template <bool Q>
 int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
   int rc;
   if (phases & MM_PHASE_GATE_UP) {
-    const int64_t nt = (a.I + kBN / 2 - 1) / (kBN / 2);
+    const int64_t nt = (a.I + Geo<Q>::BN / 2 - 1) / (Geo<Q>::BN / 2);
     const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
     if ((rc = allow_lds(prefill_gate_up_kernel<Q>, Geo<Q>::LDS, "prefill_gate_up"))) return rc;
     hipLaunchKernelGGL(prefill_gate_up_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
     if ((rc = mm::check_launch("moe_prefill gate_up"))) return rc;
   }
   if (phases & MM_PHASE_DOWN) {
-    const int64_t nt = (a.H + kBN - 1) / kBN;
+    const int64_t nt = (a.H + Geo<Q>::BN - 1) / Geo<Q>::BN;
     const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
     if ((rc = allow_lds(prefill_down_kernel<Q>, Geo<Q>::LDS, "prefill_down"))) return rc;
     hipLaunchKernelGGL(prefill_down_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
