@@ -167,7 +167,14 @@ def decode_metrics(b, n, stream, int8=False, seed=40):
         fused_moe.fused_moe_decode(xn, w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu, s_d=sd, residual=x)
 
     g = graph_of(step, stream)
-    ms = time_graph(g, stream, 200)
+    ms_unfused = time_graph(g, stream, 200)
+
+    def fused_step():
+        fused_moe.moe_block_decode(x, b["norm_w"], W.EPS, b["w32"], w_gu, w_d, top_k=W.TOP_K, s_gu=sgu, s_d=sd,
+                                   logits=logits, ids=ids, wts=wts, a_buf=a_buf, out=out)
+
+    gf = graph_of(fused_step, stream)
+    ms = time_graph(gf, stream, 200)
 
     def phase(p):
         return lambda: fused_moe.fused_moe_decode(st["xn"], w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu,
@@ -182,6 +189,7 @@ def decode_metrics(b, n, stream, int8=False, seed=40):
     dn_bytes = uniq * (H * I * es + H * sb)
     return {
         "tokens": n, "int8": int8, "unique_experts": uniq, "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / n,
+        "us_per_step_unfused": ms_unfused * 1e3,
         "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
         "gate_up_TBs": gu_bytes / gu_ms / 1e9, "down_TBs": dn_bytes / dn_ms / 1e9,
         "moe_TBs": (gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e9,
@@ -225,9 +233,8 @@ def full_decode_metrics(stream, layers=28):
             fastlinear.small_linear(xn, p["v"])
             h = fastlinear.small_linear(q, p["o"], residual=h)  # attention itself is outside the MoE path
             b = p["blk"]
-            xn = fused_ops.rms_norm(h, b["norm_w"], W.EPS)
-            fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, ids, wts, scoring="softmax")
-            h = fused_moe.fused_moe_decode(xn, b["w_gu"], b["w_d"], ids, wts, a_buf=a_buf, residual=h)
+            h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
+                                           logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
         return fastlinear.small_linear(h, head, norm=(fn, W.EPS))
 
     g = graph_of(step, stream)

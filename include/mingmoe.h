@@ -133,6 +133,23 @@ int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const m
                   const void* residual, int64_t res_row_stride,
                   void* a_buf, void* y, int64_t y_row_stride, int phases, void* stream);
 
+/* One decode MoE block for 1..8 bf16 tokens in four kernels:
+ *   router:  xn = RMSNorm(x; norm_w bf16, eps) on the fly (bit-identical to mm_rms_norm), logits = xn . w32^T,
+ *            xn stored to the workspace;
+ *   select:  as mm_router's selection (shared expert n_experts appended with weight 1), into ids / wts;
+ *   gate/up, down: as mm_moe_decode on xn, y = MoE(xn) (+ x when add_residual).
+ * Same results as mm_rms_norm -> mm_router -> mm_moe_decode(residual = x). No single call of the reference
+ * does this: it fuses the per-layer sequence of engine.py:229, 284-297, 371-386.
+ * ex->n_slots must be n_experts + 1. logits fp32 [n_tokens, n_experts], ids [n_tokens, top_k+1]
+ * (MM_INT32 / MM_INT64), wts fp32 [n_tokens, top_k+1], a_buf bf16 [n_tokens*(top_k+1), inter],
+ * y bf16 [n_tokens, hidden] (must not alias x when add_residual). workspace: 16-byte aligned device
+ * scratch of n_tokens * hidden bf16 (the normalised rows); calls that share one workspace must not overlap. */
+int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                        const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                        int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                        void* ids, int ids_dtype, float* wts, void* a_buf, void* workspace, int add_residual,
+                        void* y, int64_t y_row_stride, void* stream);
+
 /* Grouped prefill MoE over the blocks produced by mm_align_blocks (same math as mm_moe_decode).
  * Replaces fused_moe.fused_moe_prefill / _moe_gu_grouped / _moe_down_grouped (fused_moe.py:92-196).
  * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs

@@ -46,6 +46,8 @@ SIGNATURES = {
                        _I64, _I32, _P], ctypes.c_int),
     "mm_moe_prefill": ([_P, _I64, _I64, ctypes.POINTER(Experts), _I64, _P, _I32, _P, _P, _P, _P, _I64,
                         ctypes.c_int32, _P, _I64, _P, _P, _P, _I64, _I32, _P], ctypes.c_int),
+    "mm_moe_block_decode": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
+                             ctypes.POINTER(Experts), _P, _P, _I32, _P, _P, _P, _I32, _P, _I64, _P], ctypes.c_int),
     "mm_small_linear": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64, _P, _F32, _P, _P, _I64, _P],
                         ctypes.c_int),
     "mm_quantize_rows_int8": ([_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P], ctypes.c_int),

@@ -1,0 +1,256 @@
+// Router selection for one token on one wave (fused_ops.py:53-93 and the softmax router of the configs).
+// Shared by the router kernels (logits + selection for small batches, selection alone), so every path
+// picks identical experts.
+#pragma once
+
+#include "mm_common.h"
+
+namespace mmd {
+
+struct SelectParams {
+  const float* bias;  // [E] or null
+  int E, scoring, n_group, topk_group, top_k;
+  float scale;
+  int append_shared;
+};
+
+// Arg-max over the lane-held slots then across the wave; lowest expert index wins ties. Slot 0 seeds the
+// search so that an all -inf input still yields the lowest index, as an arg-max with first-index ties
+// does; slots past the valid range hold -inf and larger indices.
+template <int NS>
+__device__ __forceinline__ void slots_argmax(const float (&v)[NS], int nslots, float& best, int& bidx) {
+  const int lane = lane_id();
+  best = v[0];
+  bidx = lane;
+#pragma unroll
+  for (int j = 1; j < NS; ++j) {
+    if (j < nslots && v[j] > best) { best = v[j]; bidx = lane + kWave * j; }
+  }
+  wave_argmax(best, bidx);
+}
+
+// Fast path of select_token for at most 64 experts without group limits: one expert per lane, every lane
+// ranks its key against all others (value descending, index ascending, through scalar lane reads), so the
+// picks need no chain of cross-lane reductions. Same picks, order and arithmetic as the general path.
+__device__ __forceinline__ void select_token64(const SelectParams& a, const float* lg, int& id, float& w, bool& has) {
+  const int lane = lane_id();
+  const int E = a.E;
+  const bool valid = lane < E;
+  float score = 0.f, key = -INFINITY;
+  if (valid) {
+    const float l = lg[lane];
+    const float b = a.bias ? a.bias[lane] : 0.f;
+    if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
+      score = 1.0f / (1.0f + __expf(-l));
+      key = score + b;
+    } else {
+      key = l + b;
+    }
+  }
+  if (a.scoring == MM_SCORE_SOFTMAX) {
+    const float m = wave_max(key);
+    if (valid) score = __expf(key - m);
+    const float den = wave_sum(valid ? score : 0.f);
+    score = score / den;
+  }
+  // rank = lanes ahead of this one: larger key, or equal key and lower index
+  int rank = 0;
+  const int kb = __float_as_int(key);
+  for (int j = 0; j < kWave; ++j) {
+    const float kj = __int_as_float(__builtin_amdgcn_readlane(kb, j));
+    rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
+  }
+  // lane k gathers the k-th pick; the weights' sum runs over the picks in order
+  float total = 0.f, sel_w = 0.f;
+  int sel_e = 0;
+  const int sb = __float_as_int(score);
+  for (int k = 0; k < a.top_k; ++k) {
+    const int src = __ffsll(static_cast<long long>(__ballot(rank == k))) - 1;
+    const float s = __int_as_float(__builtin_amdgcn_readlane(sb, src));
+    total += s;
+    if (lane == k) { sel_w = s; sel_e = src; }
+  }
+  has = false;
+  w = 0.f;
+  id = 0;
+  if (lane < a.top_k) {
+    w = sel_w / (total + 1e-20f) * a.scale;
+    id = sel_e;
+    has = true;
+  } else if (lane == a.top_k && a.append_shared) {
+    w = 1.0f;
+    id = E;
+    has = true;
+  }
+}
+
+// Selects the experts of one token from its logits `lg` (whole wave). On return lane k < top_k holds the
+// k-th pick (id, weight), lane top_k the shared expert when append_shared; `has` tells which lanes hold
+// an entry. rbuf: NS*64 floats of LDS private to this wave.
+//   sigmoid: s = sigmoid(l); key = s + bias; group-limited (n_group > 1: groups ranked by the sum of
+//            their two largest keys, topk_group kept); top_k by key; w = s / (sum s + 1e-20) * scale
+//   softmax: key = l + bias; top_k by key; p = softmax(key); w = p / (sum p_sel + 1e-20) * scale
+template <int NS>
+__device__ __forceinline__ void select_token(const SelectParams& a, const float* lg, float* rbuf, int& id, float& w,
+                                             bool& has) {
+  const int lane = lane_id();
+  const int E = a.E;
+  const int nslots = (E + kWave - 1) / kWave;
+  float score[NS], key[NS];  // score: weight source; key: selection value
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int e = lane + kWave * j;
+    score[j] = 0.f;
+    key[j] = -INFINITY;
+    if (j < nslots && e < E) {
+      const float l = lg[e];
+      const float b = a.bias ? a.bias[e] : 0.f;
+      if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
+        score[j] = 1.0f / (1.0f + __expf(-l));
+        key[j] = score[j] + b;
+      } else {
+        key[j] = l + b;
+      }
+    }
+  }
+  if (a.scoring == MM_SCORE_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) m = fmaxf(m, key[j]);
+    m = wave_max(m);
+    float den = 0.f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E) {
+        score[j] = __expf(key[j] - m);
+        den += score[j];
+      }
+    }
+    den = wave_sum(den);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) score[j] = score[j] / den;
+  } else if (a.n_group > 1) {
+    // group score = sum of the two largest keys of the group (first max excluded once)
+    const int G = a.n_group, GS = E / G;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E) rbuf[e] = key[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float gscore[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int g = lane + kWave * j;
+      gscore[j] = -INFINITY;
+      if (g < G) {
+        float m1 = -INFINITY;
+        int a1 = 0;
+        for (int i = 0; i < GS; ++i) {
+          const float v = rbuf[g * GS + i];
+          if (v > m1 || i == 0) { m1 = v; a1 = i; }
+        }
+        float m2 = -INFINITY;
+        for (int i = 0; i < GS; ++i)
+          if (i != a1) m2 = fmaxf(m2, rbuf[g * GS + i]);
+        gscore[j] = m1 + m2;
+      }
+    }
+    // keep the topk_group best groups (iterative arg-max, lowest group index on ties)
+    bool keep[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) keep[j] = false;
+    for (int it = 0; it < a.topk_group; ++it) {
+      float bv;
+      int bi;
+      slots_argmax(gscore, NS, bv, bi);
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        if (lane + kWave * j == bi) { keep[j] = true; gscore[j] = -INFINITY; }
+    }
+    // broadcast the kept-group flags through LDS and mask the keys of dropped groups
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int g = lane + kWave * j;
+      if (g < G) rbuf[g] = keep[j] ? 1.f : 0.f;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int e = lane + kWave * j;
+      if (j < nslots && e < E && rbuf[e / GS] == 0.f) key[j] = -INFINITY;
+    }
+    __builtin_amdgcn_wave_barrier();  // rbuf may be reused by the caller
+  }
+  // top_k by iterative arg-max on the keys; weights come from the scores
+  float sel_w = 0.f;  // lane k holds the score of the k-th pick
+  int sel_e = 0;
+  float total = 0.f;
+  for (int k = 0; k < a.top_k; ++k) {
+    float bv;
+    int bi;
+    slots_argmax(key, nslots, bv, bi);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+      if (lane + kWave * j == bi) { s = score[j]; key[j] = -INFINITY; }
+    s = wave_sum(s);  // exactly one lane contributes
+    total += s;
+    if (lane == k) { sel_w = s; sel_e = bi; }
+  }
+  has = false;
+  w = 0.f;
+  id = 0;
+  if (lane < a.top_k) {
+    w = sel_w / (total + 1e-20f) * a.scale;
+    id = sel_e;
+    has = true;
+  } else if (lane == a.top_k && a.append_shared) {
+    w = 1.0f;
+    id = E;
+    has = true;
+  }
+}
+
+// Selection entry used by every kernel: the one-expert-per-lane path when it applies, else the general one.
+template <int NS>
+__device__ __forceinline__ void select_any(const SelectParams& a, const float* lg, float* rbuf, int& id, float& w,
+                                           bool& has) {
+  if (a.E <= kWave && a.n_group <= 1) select_token64(a, lg, id, w, has);
+  else select_token<NS>(a, lg, rbuf, id, w, has);
+}
+
+// Slots per lane (NS) needed for E experts and G groups.
+inline int select_slots(int64_t E, int64_t G) {
+  const int64_t need = E > G ? E : G;
+  return need <= 64 ? 1 : need <= 128 ? 2 : need <= 256 ? 4 : 16;
+}
+
+// 1 / sqrt(mean(x^2) + eps) of one row, computed the same way by every kernel that normalises a row (so
+// fused and standalone RMSNorm produce identical bits): threads 0..255 take strided partial sums, each of
+// their 4 waves reduces by butterflies, and waves 0..3 are summed in order. Every thread of the workgroup
+// (256 or more) must call it; every thread gets the result. red: 4 floats of LDS.
+template <class TX>
+__device__ __forceinline__ float row_rstd256(const typename TX::T* xr, int64_t n, float eps, float* red) {
+  if (threadIdx.x < 256) {
+    float ss = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+      const float v = TX::ld(xr, i);
+      ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane_id() == 0) red[threadIdx.x / kWave] = ss;
+  }
+  __syncthreads();
+  const float t = ((red[0] + red[1]) + red[2]) + red[3];
+  __syncthreads();
+  return rsqrtf(t / static_cast<float>(n) + eps);
+}
+
+}  // namespace mmd

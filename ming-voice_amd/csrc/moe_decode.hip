@@ -9,6 +9,7 @@
 // scale for int8) and parks the result in LDS; the workgroup then sums over slots in order per token:
 //   y[t, h] = bf16(sum_k wts[t,k] * part[t*nk+k, h]) (+ residual, rounded again)
 #include "mm_common.h"
+#include "mm_select.h"
 
 namespace {
 
@@ -122,7 +123,7 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
   const int lane = lane_id();
   const int g = lane / LPR, s = lane % LPR;
   const int64_t nch = a.H * ES / 16;
-  const uint16_t* xr = a.x + static_cast<int64_t>(p / a.nk) * a.xs;
+  const int tok = p / a.nk;
   float accg[R], accu[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) accg[i] = accu[i] = 0.f;
@@ -131,7 +132,7 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
-      load_act<Q>(xa[j], xr, c, c < nch);
+      load_act<Q>(xa[j], a.x + tok * a.xs, c, c < nch);
     }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -176,8 +177,8 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
   for (int64_t i = threadIdx.x; i < cntp * row_chunks; i += blockDim.x) {
     const int t = static_cast<int>(i / row_chunks);
     const int64_t c = i % row_chunks;
-    reinterpret_cast<uint4*>(xs + t * a.H)[c] =
-        reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(spid[t] / a.nk) * a.xs)[c];
+    const int tok = spid[t] / a.nk;
+    reinterpret_cast<uint4*>(xs + t * a.H)[c] = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(tok) * a.xs)[c];
   }
   __syncthreads();
 #pragma unroll
@@ -209,6 +210,8 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
   }
   __syncthreads();  // the staging buffer is reused by the next group
 }
+
+constexpr int kMaxTokens = 8;
 
 template <bool Q, int LPR, int NC, int R, int MAXT>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
@@ -479,4 +482,75 @@ extern "C" int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stri
   }
   if (phases & MM_PHASE_DOWN) return q ? dispatch_b<true>(a, st) : dispatch_b<false>(a, st);
   return MM_OK;
+}
+
+namespace mm {
+int check_router_args(int64_t n_tokens, int64_t E, int scoring, int n_group, int topk_group, int top_k,
+                      int append_shared, const void* ids, int ids_dtype, const float* wts, int64_t out_row_stride);
+int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
+                 const float* w32, const mmd::SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
+                 int64_t out_row_stride, void* xn_out, hipStream_t s);
+}  // namespace mm
+
+// Whole MoE block for 1..8 tokens in four launches: router logits (RMSNorm fused; the normalised rows go
+// to the workspace), selection, gate/up on the normalised rows, down + combine with the raw rows as
+// residual. The ids / weights it writes are the ones the unfused chain produces.
+extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                                   const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                                   int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                                   void* ids, int ids_dtype, float* wts, void* a_buf, void* workspace,
+                                   int add_residual, void* y, int64_t y_row_stride, void* stream) {
+  int rc = mm::check_experts("moe_block_decode", ex);
+  if (rc) return rc;
+  const int64_t nk = static_cast<int64_t>(top_k) + 1;
+  rc = mm::check_router_args(n_tokens, n_experts, scoring, n_group, topk_group, top_k, 1, ids, ids_dtype, wts, nk);
+  if (rc) return rc;
+  MM_REQUIRE(n_tokens >= 1 && n_tokens <= kMaxTokens && n_tokens * nk <= kMaxPairs,
+             "moe_block_decode: 1..%d tokens with (top_k + 1) * tokens <= %d", kMaxTokens, kMaxPairs);
+  MM_REQUIRE(ex->n_slots == n_experts + 1, "moe_block_decode: expert slots (%lld) must be n_experts + 1 (shared last)",
+             (long long)ex->n_slots);
+  MM_REQUIRE(x && norm_w && w32 && logits && a_buf && workspace && y, "moe_block_decode: null pointer");
+  MM_REQUIRE(x_row_stride >= ex->hidden && y_row_stride >= ex->hidden, "moe_block_decode: row stride smaller than hidden");
+  MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0 && mm::aligned16(a_buf) && mm::aligned16(workspace),
+             "moe_block_decode: x, a_buf and workspace must be 16-byte aligned");
+  MM_REQUIRE(ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "moe_block_decode: shape too large");
+  hipStream_t st = MM_STREAM(stream);
+  const mmd::SelectParams sp{bias, static_cast<int>(n_experts), scoring, n_group, topk_group, top_k, scale, 1};
+  rc = mm::router_front(x, n_tokens, ex->hidden, x_row_stride, norm_w, eps, w32, sp, logits, ids, ids_dtype, wts, nk,
+                        workspace, st);
+  if (rc) return rc;
+  DecodeArgs a;
+  a.x = static_cast<const uint16_t*>(workspace);
+  a.xs = ex->hidden;
+  a.n_tokens = static_cast<int>(n_tokens);
+  a.nk = static_cast<int>(nk);
+  a.P = static_cast<int>(n_tokens * nk);
+  a.ids = ids;
+  a.ids_dtype = ids_dtype;
+  a.ids_rs = nk;
+  a.wts = wts;
+  a.wts_rs = nk;
+  a.w_gu = ex->w_gu;
+  a.w_d = ex->w_d;
+  a.s_gu = ex->s_gu;
+  a.s_d = ex->s_d;
+  a.s_dtype = ex->s_dtype;
+  a.E1 = static_cast<int>(ex->n_slots);
+  a.H = ex->hidden;
+  a.I = ex->inter;
+  a.gu_se = ex->gu_stride_e;
+  a.gu_sn = ex->gu_stride_n;
+  a.d_se = ex->d_stride_e;
+  a.d_sn = ex->d_stride_n;
+  a.sgu_se = ex->sgu_stride_e;
+  a.sd_se = ex->sd_stride_e;
+  a.res = add_residual ? static_cast<const uint16_t*>(x) : nullptr;
+  a.res_rs = x_row_stride;
+  a.a_buf = static_cast<uint16_t*>(a_buf);
+  a.y = static_cast<uint16_t*>(y);
+  a.ys = y_row_stride;
+  const bool q = ex->w_dtype == MM_INT8;
+  rc = q ? dispatch_a<true>(a, st) : dispatch_a<false>(a, st);
+  if (rc) return rc;
+  return q ? dispatch_b<true>(a, st) : dispatch_b<false>(a, st);
 }

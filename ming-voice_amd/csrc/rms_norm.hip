@@ -1,30 +1,13 @@
 // RMSNorm over the last dim, one workgroup per row (fused_ops.py:16-37).
 //   var = mean(x_f32^2); y = bf16(x * rsqrt(var + eps)); out = (w_f32 * y) cast to the output dtype.
 #include "mm_common.h"
+#include "mm_select.h"
 
 namespace {
 
 using namespace mmd;
 
 constexpr int kThreads = 256;
-
-// Sum of squares of one row across the workgroup; every thread gets the total.
-template <class TX>
-__device__ __forceinline__ float row_sumsq(const typename TX::T* xr, int64_t n, float* red) {
-  float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += kThreads) {
-    float v = TX::ld(xr, i);
-    ss = fmaf(v, v, ss);
-  }
-  ss = wave_sum(ss);
-  const int w = threadIdx.x / kWave;
-  if (lane_id() == 0) red[w] = ss;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int j = 0; j < kThreads / kWave; ++j) t += red[j];
-  return t;
-}
 
 template <class TX, class TW, class TY>
 __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const typename TX::T* __restrict__ x, int64_t n, int64_t xs,
@@ -33,8 +16,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const typename TX::T
   __shared__ float red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const typename TX::T* xr = x + row * xs;
-  const float ss = row_sumsq<TX>(xr, n, red);
-  const float rstd = rsqrtf(ss / static_cast<float>(n) + eps);
+  const float rstd = row_rstd256<TX>(xr, n, eps, red);
   typename TY::T* yr = y + row * ys;
   for (int64_t i = threadIdx.x; i < n; i += kThreads) {
     const float v = round_bf16(TX::ld(xr, i) * rstd);

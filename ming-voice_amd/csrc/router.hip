@@ -1,7 +1,6 @@
 // MoE router: fp32 logits GEMV/GEMM and top-k selection (fused_ops.py:40-103, engine.py:326-333).
-#include <algorithm>
-
 #include "mm_common.h"
+#include "mm_select.h"
 
 namespace {
 
@@ -16,25 +15,59 @@ __device__ __forceinline__ float4 load4(const typename TX::T* p, int64_t i) {
 }
 
 // logits for up to 8 tokens: one workgroup per expert, its 4 waves split the hidden dim (float4 loads of
-// the fp32 router row), partial sums reduced through LDS in wave order.
+// the fp32 router row), partial sums reduced through LDS in wave order. (A router row is 4-8 KB: spread
+// over E workgroups the rows stream at full-chip bandwidth; one CU alone keeps too few misses in flight.)
+// With norm_w (bf16) the rows are RMS-normalised on the fly exactly as mm_rms_norm writes them,
+// xn = bf16(w * bf16(x * rstd)); workgroup 0 then stores xn to xn_out ([n_tokens, H], bf16) when given.
 template <class TX>
 __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
                                                           int64_t xs, const float* __restrict__ w32, int E,
-                                                          float* __restrict__ logits) {
+                                                          float* __restrict__ logits,
+                                                          const uint16_t* __restrict__ norm_w, float eps,
+                                                          uint16_t* __restrict__ xn_out) {
   __shared__ float red[4][8];
+  __shared__ float red4[4];
   const int e = blockIdx.x;
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   const float* wr = w32 + static_cast<int64_t>(e) * H;
+  float rstd[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) rstd[t] = 1.f;
+  if (norm_w) {
+    for (int t = 0; t < n_tokens; ++t) {
+      const float r = row_rstd256<TX>(x + t * xs, H, eps, red4);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q == t) rstd[q] = r;
+    }
+  }
+  const bool store_xn = xn_out && blockIdx.x == 0;
   float acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.f;
   if ((H & 3) == 0) {
     for (int64_t h = 4 * static_cast<int64_t>(threadIdx.x); h < H; h += 4 * 256) {
       const float4 wv = *reinterpret_cast<const float4*>(wr + h);
+      float4 nw = make_float4(1.f, 1.f, 1.f, 1.f);
+      if (norm_w) nw = make_float4(bf16_to_f32(norm_w[h]), bf16_to_f32(norm_w[h + 1]), bf16_to_f32(norm_w[h + 2]),
+                                   bf16_to_f32(norm_w[h + 3]));
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         if (t < n_tokens) {
-          const float4 xv = load4<TX>(x + t * xs, h);
+          float4 xv = load4<TX>(x + t * xs, h);
+          if (norm_w) {
+            xv.x = round_bf16(nw.x * round_bf16(xv.x * rstd[t]));
+            xv.y = round_bf16(nw.y * round_bf16(xv.y * rstd[t]));
+            xv.z = round_bf16(nw.z * round_bf16(xv.z * rstd[t]));
+            xv.w = round_bf16(nw.w * round_bf16(xv.w * rstd[t]));
+            if (store_xn) {
+              uint16_t* o = xn_out + t * H + h;
+              o[0] = f32_to_bf16(xv.x);
+              o[1] = f32_to_bf16(xv.y);
+              o[2] = f32_to_bf16(xv.z);
+              o[3] = f32_to_bf16(xv.w);
+            }
+          }
           acc[t] = fmaf(xv.x, wv.x, acc[t]);
           acc[t] = fmaf(xv.y, wv.y, acc[t]);
           acc[t] = fmaf(xv.z, wv.z, acc[t]);
@@ -45,9 +78,18 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
   } else {
     for (int64_t h = threadIdx.x; h < H; h += 256) {
       const float wv = wr[h];
+      const float nw = norm_w ? bf16_to_f32(norm_w[h]) : 1.f;
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        if (t < n_tokens) acc[t] = fmaf(TX::ld(x + t * xs, h), wv, acc[t]);
+      for (int t = 0; t < 8; ++t) {
+        if (t < n_tokens) {
+          float xv = TX::ld(x + t * xs, h);
+          if (norm_w) {
+            xv = round_bf16(nw * round_bf16(xv * rstd[t]));
+            if (store_xn) xn_out[t * H + h] = f32_to_bf16(xv);
+          }
+          acc[t] = fmaf(xv, wv, acc[t]);
+        }
+      }
     }
   }
 #pragma unroll
@@ -125,21 +167,6 @@ struct SelectArgs {
   int64_t out_stride;
 };
 
-// Arg-max over the lane-held slots then across the wave; lowest expert index wins ties.
-template <int NS>
-__device__ __forceinline__ void slots_argmax(const float (&v)[NS], int nslots, float& best, int& bidx) {
-  // Slot 0 seeds the search so that an all -inf input still yields the lowest index, as an
-  // arg-max with first-index ties does. Slots past the valid range hold -inf and larger indices.
-  const int lane = lane_id();
-  best = v[0];
-  bidx = lane;
-#pragma unroll
-  for (int j = 1; j < NS; ++j) {
-    if (j < nslots && v[j] > best) { best = v[j]; bidx = lane + kWave * j; }
-  }
-  wave_argmax(best, bidx);
-}
-
 // One wave per token: selection, weights and the optional shared-expert slot.
 template <int NS>
 __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
@@ -148,135 +175,16 @@ __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
   const int t = blockIdx.x * 4 + wv;
   if (t >= a.n_tokens) return;
   const int lane = lane_id();
-  const int E = a.E;
-  const int nslots = (E + kWave - 1) / kWave;
-  const float* lg = a.logits + static_cast<int64_t>(t) * E;
-  float score[NS], key[NS];  // score: weight source; key: selection value
-#pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int e = lane + kWave * j;
-    score[j] = 0.f;
-    key[j] = -INFINITY;
-    if (j < nslots && e < E) {
-      const float l = lg[e];
-      const float b = a.bias ? a.bias[e] : 0.f;
-      if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
-        score[j] = 1.0f / (1.0f + __expf(-l));
-        key[j] = score[j] + b;
-      } else {
-        key[j] = l + b;
-      }
-    }
-  }
-  if (a.scoring == MM_SCORE_SOFTMAX) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < NS; ++j) m = fmaxf(m, key[j]);
-    m = wave_max(m);
-    float den = 0.f;
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int e = lane + kWave * j;
-      if (j < nslots && e < E) {
-        score[j] = __expf(key[j] - m);
-        den += score[j];
-      }
-    }
-    den = wave_sum(den);
-#pragma unroll
-    for (int j = 0; j < NS; ++j) score[j] = score[j] / den;
-  } else if (a.n_group > 1) {
-    // group score = sum of the two largest keys of the group (first max excluded once)
-    const int G = a.n_group, GS = E / G;
-    float* r = rbuf[wv];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int e = lane + kWave * j;
-      if (j < nslots && e < E) r[e] = key[j];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float gscore[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int g = lane + kWave * j;
-      gscore[j] = -INFINITY;
-      if (g < G) {
-        float m1 = -INFINITY;
-        int a1 = 0;
-        for (int i = 0; i < GS; ++i) {
-          const float v = r[g * GS + i];
-          if (v > m1 || i == 0) { m1 = v; a1 = i; }
-        }
-        float m2 = -INFINITY;
-        for (int i = 0; i < GS; ++i)
-          if (i != a1) m2 = fmaxf(m2, r[g * GS + i]);
-        gscore[j] = m1 + m2;
-      }
-    }
-    // keep the topk_group best groups (iterative arg-max, lowest group index on ties)
-    bool keep[NS];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) keep[j] = false;
-    for (int it = 0; it < a.topk_group; ++it) {
-      float bv;
-      int bi;
-      slots_argmax(gscore, NS, bv, bi);
-#pragma unroll
-      for (int j = 0; j < NS; ++j)
-        if (lane + kWave * j == bi) { keep[j] = true; gscore[j] = -INFINITY; }
-    }
-    // broadcast the kept-group flags through LDS and mask the keys of dropped groups
-    __builtin_amdgcn_wave_barrier();
-    float* kf = rbuf[wv];
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int g = lane + kWave * j;
-      if (g < G) kf[g] = keep[j] ? 1.f : 0.f;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int e = lane + kWave * j;
-      if (j < nslots && e < E && kf[e / GS] == 0.f) key[j] = -INFINITY;
-    }
-  }
-  // top_k by iterative arg-max on the keys; weights come from the scores
-  float sel_w = 0.f;  // lane k holds the score of the k-th pick
-  int sel_e = 0;
-  float total = 0.f;
-  for (int k = 0; k < a.top_k; ++k) {
-    float bv;
-    int bi;
-    slots_argmax(key, nslots, bv, bi);
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-      if (lane + kWave * j == bi) { s = score[j]; key[j] = -INFINITY; }
-    s = wave_sum(s);  // exactly one lane contributes
-    total += s;
-    if (lane == k) { sel_w = s; sel_e = bi; }
-  }
-  const int64_t o = static_cast<int64_t>(t) * a.out_stride;
-  float w = 0.f;
-  int id = 0;
-  bool write = false;
-  if (lane < a.top_k) {
-    w = sel_w / (total + 1e-20f) * a.scale;
-    id = sel_e;
-    write = true;
-  } else if (lane == a.top_k && a.append_shared) {
-    w = 1.0f;
-    id = E;
-    write = true;
-  }
-  if (write) {
-    a.wts[o + lane] = w;
-    if (a.ids_dtype == MM_INT64) static_cast<int64_t*>(a.ids)[o + lane] = id;
-    else static_cast<int32_t*>(a.ids)[o + lane] = id;
+  const SelectParams sp{a.bias, a.E, a.scoring, a.n_group, a.topk_group, a.top_k, a.scale, a.append_shared};
+  int id;
+  float w;
+  bool has;
+  select_any<NS>(sp, a.logits + static_cast<int64_t>(t) * a.E, rbuf[wv], id, w, has);
+  if (has) {
+    const int64_t o = static_cast<int64_t>(t) * a.out_stride + lane;
+    a.wts[o] = w;
+    if (a.ids_dtype == MM_INT64) static_cast<int64_t*>(a.ids)[o] = id;
+    else static_cast<int32_t*>(a.ids)[o] = id;
   }
 }
 
@@ -307,12 +215,12 @@ int launch_select(const float* logits, int64_t n_tokens, int64_t E, const float*
   SelectArgs a{logits, static_cast<int>(n_tokens), static_cast<int>(E), bias, scoring, n_group, topk_group, top_k,
                scale, append_shared, ids, ids_dtype, wts, out_row_stride};
   const unsigned blocks = static_cast<unsigned>((n_tokens + 3) / 4);
-  // lane-held slots: enough for the experts and (sigmoid mode) the groups
-  const int64_t need = std::max<int64_t>(E, n_group);
-  if (need <= 64) hipLaunchKernelGGL(router_select_kernel<1>, dim3(blocks), dim3(256), 0, s, a);
-  else if (need <= 128) hipLaunchKernelGGL(router_select_kernel<2>, dim3(blocks), dim3(256), 0, s, a);
-  else if (need <= 256) hipLaunchKernelGGL(router_select_kernel<4>, dim3(blocks), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(router_select_kernel<kSlots>, dim3(blocks), dim3(256), 0, s, a);
+  switch (select_slots(E, n_group)) {  // lane-held slots: enough for the experts and the groups
+    case 1: hipLaunchKernelGGL(router_select_kernel<1>, dim3(blocks), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(router_select_kernel<2>, dim3(blocks), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(router_select_kernel<4>, dim3(blocks), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(router_select_kernel<kSlots>, dim3(blocks), dim3(256), 0, s, a); break;
+  }
   return mm::check_launch("router_select");
 }
 
@@ -322,7 +230,7 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
   const auto* xp = static_cast<const typename TX::T*>(x);
   if (n_tokens <= 8) {
     hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xp,
-                       static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits);
+                       static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nullptr, 0.f, nullptr);
   } else {
     dim3 grid(static_cast<unsigned>((E + 15) / 16), static_cast<unsigned>((n_tokens + 15) / 16));
     hipLaunchKernelGGL(router_mfma_kernel<TX>, grid, dim3(256), 0, s, xp, static_cast<int>(n_tokens), H, xs, w32,
@@ -332,6 +240,33 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
 }
 
 }  // namespace
+
+namespace mm {
+
+// Router of the decode block front for 1..8 bf16 tokens: logits with the RMSNorm (norm_w bf16, eps)
+// applied on the fly, the normalised rows stored to xn_out ([n_tokens, H] bf16), then the selection with
+// the shared expert appended.
+int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
+                 const float* w32, const SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
+                 int64_t out_row_stride, void* xn_out, hipStream_t s) {
+  MM_REQUIRE(n_tokens >= 1 && n_tokens <= 8, "router: the fused norm path takes 1..8 tokens");
+  hipLaunchKernelGGL(router_gemv_kernel<BF16>, dim3(static_cast<unsigned>(sp.E)), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), static_cast<int>(n_tokens), H, xs, w32, sp.E, logits,
+                     static_cast<const uint16_t*>(norm_w), eps, static_cast<uint16_t*>(xn_out));
+  const int rc = check_launch("router_logits");
+  if (rc) return rc;
+  return launch_select(logits, n_tokens, sp.E, sp.bias, sp.scoring, sp.n_group, sp.topk_group, sp.top_k, sp.scale,
+                       sp.append_shared, ids, ids_dtype, wts, out_row_stride, s);
+}
+
+int check_router_args(int64_t n_tokens, int64_t E, int scoring, int n_group, int topk_group, int top_k,
+                      int append_shared, const void* ids, int ids_dtype, const float* wts, int64_t out_row_stride) {
+  return check_select(n_tokens, E, scoring, n_group, topk_group, top_k, append_shared, ids, ids_dtype, wts,
+                      out_row_stride);
+}
+
+
+}  // namespace mm
 
 extern "C" int mm_router_select(const float* logits, int64_t n_tokens, int64_t n_experts, const float* bias, int scoring,
                                 int n_group, int topk_group, int top_k, float scale, int append_shared, void* ids,

@@ -82,6 +82,57 @@ def fused_moe_decode(x, w_gu, w_d, ids, weights, a_buf=None, out=None, s_gu=None
     return y.view(N, H)
 
 
+_SCORING = {"sigmoid": _mm.MM_SCORE_SIGMOID_GROUP, "softmax": _mm.MM_SCORE_SOFTMAX}
+
+
+def moe_block_decode(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scoring="softmax", n_group=1,
+                     topk_group=1, scale=1.0, s_gu=None, s_d=None, residual=True, logits=None, ids=None, wts=None,
+                     a_buf=None, out=None, workspace=None):
+    """One decode MoE block for 1..8 bf16 tokens in four kernels: the router GEMV with the RMSNorm (norm_w, eps)
+    applied on the fly (the normalised rows go to `workspace`, bf16 [N, H]); the expert selection (shared
+    expert appended); the gate/up GEMV; the down GEMV with the combine and the residual add of x.
+    Same results as rms_norm -> moe_route -> fused_moe_decode(residual=x). Returns (y [N, H], ids, wts,
+    logits); the optional buffers make the call allocation-free."""
+    _mm.require_gpu(x, norm_w, w32, w_gu, w_d, bias, s_gu, s_d, logits, ids, wts, a_buf, out, workspace)
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    N, E = x2.shape[0], w32.shape[0]
+    NK = top_k + 1
+    for name, t, dt in (("x", x2, torch.bfloat16), ("norm_w", norm_w, torch.bfloat16), ("w32", w32, torch.float32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"moe_block_decode: {name} must be contiguous {dt}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E or not bias.is_contiguous()):
+        raise ValueError("moe_block_decode: bias must be a contiguous fp32 [E] tensor")
+    if scoring not in _SCORING:
+        raise ValueError(f"moe_block_decode: scoring must be one of {sorted(_SCORING)}")
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d)
+    dev = x.device
+    logits = torch.empty(N, E, device=dev, dtype=torch.float32) if logits is None else logits
+    ids = torch.empty(N, NK, device=dev, dtype=torch.int64) if ids is None else ids
+    wts = torch.empty(N, NK, device=dev, dtype=torch.float32) if wts is None else wts
+    a = torch.empty(N * NK, ex.inter, device=dev, dtype=torch.bfloat16) if a_buf is None else a_buf
+    y = torch.empty(N, H, device=dev, dtype=torch.bfloat16) if out is None else out
+    for name, t, n, dt in (("logits", logits, N * E, torch.float32), ("wts", wts, N * NK, torch.float32),
+                           ("a_buf", a, N * NK * ex.inter, torch.bfloat16), ("out", y, N * H, torch.bfloat16)):
+        if t.dtype != dt or t.numel() < n or not t.is_contiguous():
+            raise ValueError(f"moe_block_decode: {name} must be a contiguous {dt} buffer of {n} elements")
+    if ids.dtype not in (torch.int32, torch.int64) or ids.numel() != N * NK or not ids.is_contiguous():
+        raise ValueError(f"moe_block_decode: ids must be a contiguous int32/int64 [{N}, {NK}] tensor")
+    ws = torch.empty(N, H, device=dev, dtype=torch.bfloat16) if workspace is None else workspace
+    if ws.numel() * ws.element_size() < N * H * 2 or not ws.is_contiguous():
+        raise ValueError(f"moe_block_decode: workspace must be a contiguous buffer of at least {N * H * 2} bytes")
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_moe_block_decode(_mm.ptr(x2), N, x2.stride(0), _mm.ptr(norm_w), float(eps), _mm.ptr(w32), E,
+                                          _mm.ptr(bias), _SCORING[scoring], int(n_group), int(topk_group), int(top_k),
+                                          float(scale), ex, _mm.ptr(logits), _mm.ptr(ids), _mm.dtype_code(ids),
+                                          _mm.ptr(wts), _mm.ptr(a), _mm.ptr(ws), 1 if residual else 0, _mm.ptr(y),
+                                          H, _mm.stream_of(x)), "moe_block_decode")
+    return y.view(N, H), ids.view(N, NK), wts.view(N, NK), logits.view(N, E)
+
+
 def _num_blocks(P, E1, BM):
     return (P + E1 * (BM - 1) + BM - 1) // BM
 

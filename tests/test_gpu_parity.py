@@ -201,6 +201,45 @@ def test_decode_int8_batches(blk, n, sdt):
     close(y, _oracle_moe(c, xn, ids, wts, int8=True))
 
 
+@pytest.mark.parametrize("n,int8", [(1, False), (3, False), (1, True), (2, True), (4, True), (8, True)])
+def test_moe_block_decode_matches_unfused_and_oracle(blk, n, int8):
+    """The three-kernel decode block equals rms_norm -> moe_route -> fused_moe_decode(residual=x) bit for bit
+    (same rstd reduction, same logits order, same picks), and the oracle within tolerance."""
+    b, cpu = blk
+    x = W.tokens(n, seed=140 + n, device=DEV)
+    wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
+    sg, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
+    y, ids, wts, logits = fused_moe.moe_block_decode(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=6, s_gu=sg, s_d=sd)
+    xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+    l2 = torch.empty(n, 64, device=DEV)
+    i2 = torch.empty(n, 7, device=DEV, dtype=torch.long)
+    w2 = torch.empty(n, 7, device=DEV)
+    fused_ops.moe_route(xn, b["w32"], None, 1, 1, 6, 1.0, l2, i2, w2, scoring="softmax")
+    y2 = fused_moe.fused_moe_decode(xn, wg, wd, i2, w2, s_gu=sg, s_d=sd, residual=x)
+    assert torch.equal(logits, l2) and torch.equal(ids, i2) and torch.equal(wts, w2)
+    assert torch.equal(y, y2)
+    close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
+
+
+def test_moe_block_decode_sigmoid_group_thinker_router():
+    """The Ming thinker's router (128 experts, 8 groups, top 4 groups, top 8, scale 2.5) on the fused path."""
+    H, I, E = 1536, 512, 128
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 150, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 151, DEV)
+    w32 = W.normal((E, H), 0.02, 152, DEV, dtype=torch.float32)
+    bias = W.normal((E,), 0.05, 153, DEV, dtype=torch.float32)
+    nw = W.normal((H,), 0.02, 154, DEV, mean=1.0)
+    x = W.tokens(1, seed=155, device=DEV, hidden=H)
+    y, ids, wts, logits = fused_moe.moe_block_decode(x, nw, 1e-6, w32, w_gu, w_d, top_k=8, bias=bias, scoring="sigmoid",
+                                                     n_group=8, topk_group=4, scale=2.5)
+    ref_ids, ref_w = O.router_select(logits.cpu(), bias.cpu(), scoring="sigmoid", n_group=8, topk_group=4, top_k=8,
+                                     scale=2.5)
+    assert torch.equal(ids.cpu(), ref_ids)
+    torch.testing.assert_close(wts.cpu(), ref_w, rtol=1e-5, atol=1e-6)
+    xn = O.rms_norm(x.cpu(), nw.cpu(), 1e-6)
+    close(y, O.moe(xn, w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu(), residual=x.cpu()))
+
+
 @pytest.mark.parametrize("n", [2, 5, 8])
 def test_decode_bf16_batches_and_repeated_experts(blk, n):
     b, cpu = blk
