@@ -80,18 +80,15 @@ def kernel_ms(fn, stream, reps=20):
 
 def prefill_setup(b, n, bias, seed):
     import fused_moe
-    import fused_ops
     import workloads as W
     x = W.tokens(n, seed=seed, device="cuda")
     E1, I, H = b["w_gu"].shape[0], b["w_d"].shape[-1], b["w_d"].shape[1]
-    sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device)
-    st = {}
+    sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True)
+    st = {"xn": sc.xn, "ids": sc.ids, "wts": sc.wts}
 
-    def step():
-        xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
-        ids, wts, _ = fused_ops.route(xn, b["w32"], bias, top_k=W.TOP_K, scoring="softmax")
-        st["xn"], st["ids"], st["wts"] = xn, ids, wts
-        return fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x, scratch=sc)
+    def step():  # the whole block: RMSNorm + router + select + align + gate/up + down + combine (+ x)
+        return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
+                                           bias=bias, scoring="softmax", scratch=sc)[0]
 
     step()
     torch.cuda.synchronize()

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 1
+#define MM_ABI_VERSION 2
 
 /* status codes */
 #define MM_OK 0
@@ -162,6 +162,23 @@ int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const 
                    const int32_t* sorted_ids, const int32_t* bexp, const int32_t* expert_offsets,
                    int64_t nb, int32_t block_m, const void* residual, int64_t res_row_stride,
                    void* a_buf, void* part_buf, void* y, int64_t y_row_stride, int phases, void* stream);
+
+/* One MoE block for a prefill batch (any n_tokens >= 1): xn = RMSNorm(x; norm_w bf16, eps) (stored;
+ * fused into the router GEMV up to 8 tokens, bit-identical to mm_rms_norm), router logits of xn, the
+ * selection (shared expert n_experts appended with weight 1), mm_align_blocks, then mm_moe_prefill on xn
+ * with x as residual when add_residual. Same results as mm_rms_norm -> mm_router -> mm_align_blocks ->
+ * mm_moe_prefill(residual = x). No single call of the reference does this: it fuses the per-layer
+ * sequence of engine.py:229, 284-309.
+ * ex->n_slots must be n_experts + 1. logits fp32 [n_tokens, n_experts]; ids [n_tokens, top_k+1]
+ * (MM_INT32 / MM_INT64); wts fp32 [n_tokens, top_k+1]; xn bf16 [n_tokens, hidden] (16-byte aligned);
+ * sorted_ids / bexp / expert_offsets / nb sized as for mm_align_blocks with block_m 64; a_buf / part_buf
+ * as for mm_moe_prefill; y bf16 [n_tokens, hidden] (must not alias x when add_residual). */
+int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                         const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                         int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                         void* ids, int ids_dtype, float* wts, void* xn, int32_t* sorted_ids, int32_t* bexp,
+                         int32_t* expert_offsets, int64_t nb, void* a_buf, void* part_buf, int add_residual,
+                         void* y, int64_t y_row_stride, void* stream);
 
 /* y = act(norm?(x) . W^T + b) [+ residual] for M <= 16 rows.
  * Replaces fastlinear.small_linear / _small_m_linear (fastlinear.py:123-174) including the rounding

@@ -56,11 +56,11 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) { return static_cast<flo
 __device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
 
 // Typed scalar load / store through dtype tags.
-struct BF16 { typedef uint16_t T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+struct BF16 { typedef uint16_t T; static constexpr bool kBf16 = true; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
               static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); } };
-struct FP16 { typedef uint16_t T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return f16_to_f32(p[i]); }
+struct FP16 { typedef uint16_t T; static constexpr bool kBf16 = false; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return f16_to_f32(p[i]); }
               static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); } };
-struct FP32 { typedef float T; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
+struct FP32 { typedef float T; static constexpr bool kBf16 = false; static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
               static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = v; } };
 
 // Scale loads for int8 weights (fp32 or bf16 scale tensors).
@@ -109,25 +109,50 @@ __device__ __forceinline__ float dot16_i8_bf16(const uint4& w, const uint4& xa, 
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// Butterfly sum over the lanes of a wave (all lanes get the total).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+// Cross-lane moves inside rows of 16 lanes by DPP (no LDS round trip).
+template <int ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
 }
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]: lane i <-> i ^ 1
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]: lane i <-> i ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
 
-// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
+// Sum over aligned groups of `width` lanes (a power of two <= 64); every lane of a group gets the group's
+// total, with one fixed association: pairs, then quads, then halves and rows of 16 (each step adds a lane
+// of the partner group, whose lanes hold equal values by then), then the row totals as (r0 + r1) + (r2 + r3).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  static_assert(width >= 1 && width <= 64 && (width & (width - 1)) == 0, "group width");
+  if constexpr (width >= 2) v += dpp_f32<kDppXor1>(v);
+  if constexpr (width >= 4) v += dpp_f32<kDppXor2>(v);
+  if constexpr (width >= 8) v += dpp_f32<kDppHalfMirror>(v);
+  if constexpr (width >= 16) v += dpp_f32<kDppMirror>(v);
+  if constexpr (width == 32) {
+    v += __shfl_xor(v, 16, kWave);
+  } else if constexpr (width == 64) {
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    v = (r0 + r1) + (r2 + r3);
+  }
   return v;
 }
 
+// Sum over the lanes of a wave (all lanes get the total).
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f32<kDppMirror>(v));
+  const int b = __float_as_int(v);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)), __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
 }
 
 // Arg-max over a wave: largest value, lowest index among equal values. Every lane gets the winner.

@@ -232,17 +232,52 @@ inline int select_slots(int64_t E, int64_t G) {
   return need <= 64 ? 1 : need <= 128 ? 2 : need <= 256 ? 4 : 16;
 }
 
+// Sum of squares of elements 8c .. 8c+7 (those below n) of a row, added to ss in element order.
+template <class TX>
+__device__ __forceinline__ float chunk_ss(const typename TX::T* xr, int64_t c, int64_t n, float ss) {
+  const int64_t i0 = c * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (i0 + i < n) {
+      const float v = TX::ld(xr, i0 + i);
+      ss = fmaf(v, v, ss);
+    }
+  }
+  return ss;
+}
+
+// The same for a whole, 16-byte aligned chunk of bf16 (one load, same order).
+__device__ __forceinline__ float chunk_ss_bf16x8(const uint4& v, float ss) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xffff0000u);
+    ss = fmaf(lo, lo, ss);
+    ss = fmaf(hi, hi, ss);
+  }
+  return ss;
+}
+
+// Whether rows of TX at xr with n elements (row stride xs) can be read in whole aligned bf16 chunks.
+template <class TX>
+__device__ __forceinline__ bool rows_bf16x8(const typename TX::T* xr, int64_t n, int64_t xs) {
+  return TX::kBf16 && (n & 7) == 0 && (xs & 7) == 0 && (reinterpret_cast<uintptr_t>(xr) & 15) == 0;
+}
+
 // 1 / sqrt(mean(x^2) + eps) of one row, computed the same way by every kernel that normalises a row (so
-// fused and standalone RMSNorm produce identical bits): threads 0..255 take strided partial sums, each of
-// their 4 waves reduces by butterflies, and waves 0..3 are summed in order. Every thread of the workgroup
-// (256 or more) must call it; every thread gets the result. red: 4 floats of LDS.
+// fused and standalone RMSNorm produce identical bits): thread i < 256 sums the 8-element chunks i,
+// i + 256, ... (elements in order), each of the 4 waves reduces by butterflies, and waves 0..3 are summed
+// in order. Every thread of the workgroup (256 or more) must call it; every thread gets the result.
+// red: 4 floats of LDS.
 template <class TX>
 __device__ __forceinline__ float row_rstd256(const typename TX::T* xr, int64_t n, float eps, float* red) {
   if (threadIdx.x < 256) {
     float ss = 0.f;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-      const float v = TX::ld(xr, i);
-      ss = fmaf(v, v, ss);
+    if (rows_bf16x8<TX>(xr, n, 8)) {
+      for (int64_t c = threadIdx.x; c * 8 < n; c += 256)
+        ss = chunk_ss_bf16x8(reinterpret_cast<const uint4*>(xr)[c], ss);
+    } else {
+      for (int64_t c = threadIdx.x; c * 8 < n; c += 256) ss = chunk_ss<TX>(xr, c, n, ss);
     }
     ss = wave_sum(ss);
     if (lane_id() == 0) red[threadIdx.x / kWave] = ss;

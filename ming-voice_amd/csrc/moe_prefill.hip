@@ -15,20 +15,27 @@
 #include <mutex>
 
 #include "mm_common.h"
+#include "mm_select.h"
 
 namespace {
 
 using namespace mmd;
 
 constexpr int kBM = 64;          // rows (pairs) per block, = align block_m
-constexpr int kBK = 64;          // k-slab (bf16 elements): rows of 128 bytes = 8 chunks of 16 bytes
 constexpr int kThreads = 256;    // 4 waves
 constexpr int kXcds = 8;
-// Tile shape per weight type: output columns per tile, LDS stages (k-slabs in flight) and wave rows
-// (1: each wave 64 rows x BN/4 columns; 2: 32 rows x BN/2 columns). LDS = stages x (8 KB + BN x 128 B
-// bf16 / BN x 64 B int8); fewer stages let more workgroups share a CU.
+// Tile shape per weight type: output columns per tile, k-slab width (k elements per LDS stage: each
+// weight row is fetched in segments of BK elements, and HBM streams longer segments better), LDS stages
+// (k-slabs in flight) and wave rows (1: each wave 64 rows x BN/4 columns; 2: 32 rows x BN/2 columns).
+// LDS = stages x (64 x BK x 2 B + BN x BK x weight bytes); fewer stages let more workgroups share a CU.
 #ifndef MM_PREFILL_BN_BF16
 #define MM_PREFILL_BN_BF16 128
+#endif
+#ifndef MM_PREFILL_BK_BF16
+#define MM_PREFILL_BK_BF16 64
+#endif
+#ifndef MM_PREFILL_BK_INT8
+#define MM_PREFILL_BK_INT8 64
 #endif
 #ifndef MM_PREFILL_SLABS_BF16
 #define MM_PREFILL_SLABS_BF16 3
@@ -105,39 +112,51 @@ __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
 
 // ---------------------------------------------------------------------------------- k-slab pipeline
 //
-// Each k-slab (64 k) of the tile is copied global -> LDS by global_load_lds_dwordx4: one wave instruction
+// Each k-slab (BK k) of the tile is copied global -> LDS by global_load_lds_dwordx4: one wave instruction
 // fills 1 KB of LDS in lane order, and each lane picks the 16-byte global chunk that belongs at its LDS
 // position. Rows and k past the operand (padding pairs, columns past the weight, the k tail) read a
 // zero chunk. NS slabs are in flight; the wave waits on vmcnt for the oldest and a barrier makes it
-// visible to every wave. Layouts (bytes) keep the 16 rows that one MFMA fragment reads on distinct banks:
-//   bf16 rows (A, and B for bf16 weights): 128 B = 8 chunks, chunk c of row r at r*128 + (c ^ (r & 7))*16
-//   int8 weight rows: 64 B = 4 chunks of 16 k, chunk c of row r at r*64 + (c ^ ((r >> 1) & 3))*16
-// A lane's MFMA k-chunk for step ks of lane quarter lq is ks*4 + lq (bf16 weights) or 2*lq + ks (int8
-// weights, so that one 16-byte int8 chunk widens into the two steps); A follows the same choice.
+// visible to every wave. Rows of R bytes (bf16: 2*BK, int8 weights: BK) hold R/16 chunks; chunk c of row
+// r sits at r*R + (c ^ s(r))*16 with s(r) = (r / rows-per-256-bytes) mod min(R/16, 16), so the 16 rows
+// that one MFMA fragment reads (same logical chunk) fall on distinct bank groups.
+// A lane's MFMA k-chunk for step ks of lane quarter lq is ks*4 + lq (bf16 weights) or, for int8 weights
+// (one 16-byte int8 chunk widens into two steps), 8g + 2lq + ks in 64-k group g; A follows the same choice.
 
 __device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes for masked lanes
 
 template <bool Q>
 struct Geo {
   static constexpr int BN = Q ? MM_PREFILL_BN_INT8 : MM_PREFILL_BN_BF16;     // output columns per tile
+  static constexpr int BK = Q ? MM_PREFILL_BK_INT8 : MM_PREFILL_BK_BF16;     // k elements per slab
   static constexpr int NS = Q ? MM_PREFILL_SLABS_INT8 : MM_PREFILL_SLABS_BF16;  // slabs in flight
   static constexpr int WM = Q ? MM_PREFILL_WM_INT8 : MM_PREFILL_WM_BF16;     // wave rows
   static constexpr int WN = 4 / WM;                   // wave columns
   static constexpr int FM = kBM / WM / 16;            // 16-row fragments per wave
   static constexpr int FN = BN / WN / 16;             // 16-column fragments per wave
-  static constexpr int ROWB = Q ? 64 : 128;           // weight bytes per row per slab
-  static constexpr int A_BYTES = kBM * 128;           // 8 KB
+  static constexpr int AROW = BK * 2;                 // activation (bf16) bytes per row per slab
+  static constexpr int ROWB = Q ? BK : BK * 2;        // weight bytes per row per slab
+  static constexpr int A_BYTES = kBM * AROW;
   static constexpr int B_BYTES = BN * ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr size_t LDS = static_cast<size_t>(NS) * STAGE;
   static constexpr int A_INSTR = A_BYTES / 1024 / 4;  // direct-load instructions per wave per slab
   static constexpr int B_INSTR = B_BYTES / 1024 / 4;
   static constexpr int LOADS = A_INSTR + B_INSTR;
-  static_assert((BN == 128 || BN == 256) && (WM == 1 || WM == 2) && FN % 2 == 0, "tile shape");
+  static constexpr int KSTEPS = BK / 32;              // MFMA k-steps per slab
+  static_assert((BN == 64 || BN == 128 || BN == 256) && (WM == 1 || WM == 2) && FN % 2 == 0, "tile shape");
+  static_assert(BK == 64 || BK == 128, "slab width");
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "slab must split over 4 waves in 1 KB pieces");
 };
 
-__device__ __forceinline__ int pos_bf16(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-__device__ __forceinline__ int pos_i8(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+// LDS byte position of 16-byte chunk c of row r in a slab with rows of `rowb` bytes. The XOR swizzle puts
+// the 16 rows read by one MFMA fragment (same logical chunk) on distinct 16-byte bank groups.
+template <int rowb>
+__device__ __forceinline__ int pos_row(int r, int c) {
+  constexpr int ch = rowb / 16;                     // chunks per row
+  constexpr int rp = rowb >= 256 ? 1 : 256 / rowb;  // rows per 256 bytes (one pass over the banks)
+  constexpr int mask = ch < 16 ? ch - 1 : 15;
+  return r * rowb + ((c ^ ((r / rp) & mask)) << 4);
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -160,21 +179,20 @@ struct LoadMap {
   int ra[Geo<Q>::A_INSTR], ca[Geo<Q>::A_INSTR];
   int rb[Geo<Q>::B_INSTR], cb[Geo<Q>::B_INSTR];
   __device__ __forceinline__ LoadMap() {
+    using G = Geo<Q>;
+    constexpr int ACH = G::AROW / 16, BCH = G::ROWB / 16;  // chunks per row
     const int w = threadIdx.x / kWave, l = lane_id();
 #pragma unroll
-    for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
-      ra[j] = (w * Geo<Q>::A_INSTR + j) * 8 + l / 8;
-      ca[j] = (l % 8) ^ (ra[j] & 7);
+    for (int j = 0; j < G::A_INSTR; ++j) {
+      ra[j] = (w * G::A_INSTR + j) * (64 / ACH) + l / ACH;
+      // the lane's LDS position holds physical chunk l % ACH; the swizzle is an involution, so the
+      // logical chunk is the position the swizzle gives that physical chunk
+      ca[j] = (pos_row<G::AROW>(ra[j], l % ACH) - ra[j] * G::AROW) >> 4;
     }
 #pragma unroll
-    for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
-      if constexpr (Q) {
-        rb[j] = (w * Geo<Q>::B_INSTR + j) * 16 + l / 4;
-        cb[j] = (l % 4) ^ ((rb[j] >> 1) & 3);
-      } else {
-        rb[j] = (w * Geo<Q>::B_INSTR + j) * 8 + l / 8;
-        cb[j] = (l % 8) ^ (rb[j] & 7);
-      }
+    for (int j = 0; j < G::B_INSTR; ++j) {
+      rb[j] = (w * G::B_INSTR + j) * (64 / BCH) + l / BCH;
+      cb[j] = (pos_row<G::ROWB>(rb[j], l % BCH) - rb[j] * G::ROWB) >> 4;
     }
   }
 };
@@ -188,7 +206,7 @@ __device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K,
   char* sa = lds + st * Geo<Q>::STAGE;
   char* sb = sa + Geo<Q>::A_BYTES;
   const int w = threadIdx.x / kWave;
-  const int64_t k0 = static_cast<int64_t>(kt) * kBK;
+  const int64_t k0 = static_cast<int64_t>(kt) * Geo<Q>::BK;
 #pragma unroll
   for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
     const int64_t k = k0 + m.ca[j] * 8;
@@ -209,19 +227,24 @@ __device__ __forceinline__ bf16x8_t lds_frag16(const char* base, int pos) {
 
 // The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
 // 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j.
-template <bool Q, class BColFn>
-__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN], int64_t K,
-                                          const uint16_t* const* arow, const char* const* brow, char* lds, int r0,
-                                          BColFn bcol) {
+template <bool Q, class XRowFn, class WRowFn, class BColFn>
+__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN], int64_t K, XRowFn xrow,
+                                          WRowFn wrow, char* lds, int r0, BColFn bcol) {
   constexpr int NS = Geo<Q>::NS, LOADS = Geo<Q>::LOADS, FM = Geo<Q>::FM, FN = Geo<Q>::FN;
   const int lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
   const LoadMap<Q> m;
+  const uint16_t* arow[Geo<Q>::A_INSTR];
+  const char* brow[Geo<Q>::B_INSTR];
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) arow[j] = xrow(m.ra[j]);
+#pragma unroll
+  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) brow[j] = wrow(m.rb[j]);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int nk = static_cast<int>((K + kBK - 1) / kBK);
+  const int nk = static_cast<int>((K + Geo<Q>::BK - 1) / Geo<Q>::BK);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nk) issue_slab<Q>(lds, s, s, K, m, arow, brow);
@@ -243,35 +266,40 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN]
     const char* sa = lds + (kt % NS) * Geo<Q>::STAGE;
     const char* sb = sa + Geo<Q>::A_BYTES;
     if constexpr (Q) {
-      // one 16-byte int8 chunk per lane and fragment feeds both 32-wide steps
-      bf16x8_t fb[2][FN];
+      // one 16-byte int8 chunk (16 k) per lane and fragment feeds two 32-wide steps: in 64-k group g the
+      // lane quarter lq takes int8 chunk 4g + lq, i.e. bf16 activation chunks 8g + 2lq (+1)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        uint4 lo, hi;
-        widen_i8(*reinterpret_cast<const uint4*>(sb + pos_i8(bcol(j) + lr, lq)), lo, hi);
-        fb[0][j] = __builtin_bit_cast(bf16x8_t, lo);
-        fb[1][j] = __builtin_bit_cast(bf16x8_t, hi);
-      }
+      for (int g = 0; g < Geo<Q>::BK / 64; ++g) {
+        bf16x8_t fb[2][FN];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        bf16x8_t fa[FM];
+        for (int j = 0; j < FN; ++j) {
+          uint4 lo, hi;
+          widen_i8(*reinterpret_cast<const uint4*>(sb + pos_row<Geo<Q>::ROWB>(bcol(j) + lr, 4 * g + lq)), lo, hi);
+          fb[0][j] = __builtin_bit_cast(bf16x8_t, lo);
+          fb[1][j] = __builtin_bit_cast(bf16x8_t, hi);
+        }
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_bf16(r0 + 16 * i + lr, 2 * lq + ks));
+        for (int ks = 0; ks < 2; ++ks) {
+          bf16x8_t fa[FM];
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+          for (int i = 0; i < FM; ++i)
+            fa[i] = lds_frag16(sa, pos_row<Geo<Q>::AROW>(r0 + 16 * i + lr, 8 * g + 2 * lq + ks));
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
+        }
       }
     } else {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < Geo<Q>::KSTEPS; ++ks) {
         const int ch = ks * 4 + lq;
         bf16x8_t fa[FM], fb[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_bf16(r0 + 16 * i + lr, ch));
+        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_row<Geo<Q>::AROW>(r0 + 16 * i + lr, ch));
 #pragma unroll
-        for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_bf16(bcol(j) + lr, ch));
+        for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_row<Geo<Q>::ROWB>(bcol(j) + lr, ch));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -297,29 +325,24 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
   const int64_t I = a.I, n0 = static_cast<int64_t>(nt) * HALF;
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
-  // source rows of this thread's direct loads
-  const LoadMap<Q> m;
-  const uint16_t* arow[G::A_INSTR];
-  const char* brow[G::B_INSTR];
-#pragma unroll
-  for (int j = 0; j < G::A_INSTR; ++j) {
-    const int p = spair[m.ra[j]];
-    arow[j] = p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
-  }
+  // activation row of tile row r (token of pair spair[r]); weight row of tile column r (gate columns
+  // first, then the matching up rows); null = masked
+  auto xrow = [&](int r) -> const uint16_t* {
+    const int p = spair[r];
+    return p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
+  };
   const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
-#pragma unroll
-  for (int j = 0; j < G::B_INSTR; ++j) {
-    const int r = m.rb[j];  // tile row: gate rows first, then the matching up rows
+  auto wrow = [&](int r) -> const char* {
     const int64_t col = n0 + (r % HALF);
-    brow[j] = col < I ? wbase + ((r < HALF ? col : I + col) * a.gu_sn) * ES : nullptr;
-  }
+    return col < I ? wbase + ((r < HALF ? col : I + col) * a.gu_sn) * ES : nullptr;
+  };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
   const int r0 = wm * (kBM / G::WM);
   constexpr int FG = G::FN / 2;      // gate fragments of the wave; the next FG are the matching up ones
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
-  tile_gemm<Q>(acc, a.H, arow, brow, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<Q>(acc, a.H, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); });
 #pragma unroll
   for (int j = 0; j < FG; ++j) {
@@ -358,26 +381,21 @@ __global__ __launch_bounds__(kThreads) void prefill_down_kernel(PrefillArgs a) {
   const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * G::BN;
   if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
   __syncthreads();
-  const LoadMap<Q> m;
-  const uint16_t* arow[G::A_INSTR];
-  const char* brow[G::B_INSTR];
-#pragma unroll
-  for (int j = 0; j < G::A_INSTR; ++j) {
-    const int p = spair[m.ra[j]];
-    arow[j] = p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
-  }
+  auto xrow = [&](int r) -> const uint16_t* {
+    const int p = spair[r];
+    return p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
+  };
   const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
-#pragma unroll
-  for (int j = 0; j < G::B_INSTR; ++j) {
-    const int64_t h = h0 + m.rb[j];
-    brow[j] = h < H ? wbase + (h * a.d_sn) * ES : nullptr;
-  }
+  auto wrow = [&](int r) -> const char* {
+    const int64_t h = h0 + r;
+    return h < H ? wbase + (h * a.d_sn) * ES : nullptr;
+  };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
   const int r0 = wm * (kBM / G::WM);
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
-  tile_gemm<Q>(acc, I, arow, brow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
+  tile_gemm<Q>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
 #pragma unroll
   for (int j = 0; j < G::FN; ++j) {
     const int64_t h = h0 + c0 + 16 * j + (lane & 15);
@@ -546,4 +564,43 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   const int64_t total = n_tokens * (a.H / 8);
   hipLaunchKernelGGL(prefill_combine_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, st, a);
   return mm::check_launch("moe_prefill combine");
+}
+
+namespace mm {
+int check_router_args(int64_t n_tokens, int64_t E, int scoring, int n_group, int topk_group, int top_k,
+                      int append_shared, const void* ids, int ids_dtype, const float* wts, int64_t out_row_stride);
+int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
+                 const float* w32, const mmd::SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
+                 int64_t out_row_stride, void* xn_out, hipStream_t s);
+}  // namespace mm
+
+// Whole MoE block for a prefill batch: RMSNorm into xn, router logits, selection, align, gate/up and down
+// over the expert blocks, combine with the raw rows as residual.
+extern "C" int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                                    const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                                    int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                                    void* ids, int ids_dtype, float* wts, void* xn, int32_t* sorted_ids, int32_t* bexp,
+                                    int32_t* expert_offsets, int64_t nb, void* a_buf, void* part_buf, int add_residual,
+                                    void* y, int64_t y_row_stride, void* stream) {
+  int rc = mm::check_experts("moe_block_prefill", ex);
+  if (rc) return rc;
+  const int64_t nk = static_cast<int64_t>(top_k) + 1;
+  rc = mm::check_router_args(n_tokens, n_experts, scoring, n_group, topk_group, top_k, 1, ids, ids_dtype, wts, nk);
+  if (rc) return rc;
+  MM_REQUIRE(ex->n_slots == n_experts + 1, "moe_block_prefill: expert slots (%lld) must be n_experts + 1 (shared last)",
+             (long long)ex->n_slots);
+  MM_REQUIRE(x && norm_w && w32 && logits && xn, "moe_block_prefill: null pointer");
+  MM_REQUIRE(mm::aligned16(xn), "moe_block_prefill: xn must be 16-byte aligned");
+  if (n_tokens == 0) return MM_OK;
+  hipStream_t st = MM_STREAM(stream);
+  const mmd::SelectParams sp{bias, static_cast<int>(n_experts), scoring, n_group, topk_group, top_k, scale, 1};
+  rc = mm::router_front(x, n_tokens, ex->hidden, x_row_stride, norm_w, eps, w32, sp, logits, ids, ids_dtype, wts, nk, xn,
+                        st);
+  if (rc) return rc;
+  rc = mm_align_blocks(ids, ids_dtype, n_tokens * nk, static_cast<int32_t>(ex->n_slots), kBM, sorted_ids, bexp, nb,
+                       expert_offsets, stream);
+  if (rc) return rc;
+  return mm_moe_prefill(xn, n_tokens, ex->hidden, ex, nk, ids, ids_dtype, wts, sorted_ids, bexp, expert_offsets, nb, kBM,
+                        add_residual ? x : nullptr, x_row_stride, a_buf, part_buf, y, y_row_stride, MM_PHASE_ALL,
+                        stream);
 }

@@ -14,6 +14,21 @@ __device__ __forceinline__ float4 load4(const typename TX::T* p, int64_t i) {
   return make_float4(TX::ld(p, i), TX::ld(p, i + 1), TX::ld(p, i + 2), TX::ld(p, i + 3));
 }
 
+__device__ __attribute__((aligned(16))) float g_zero4[4];  // zero source for masked vector loads
+
+// 4 consecutive elements from an address aligned to 4 elements, in one load.
+template <class TX>
+__device__ __forceinline__ float4 load4v(const typename TX::T* p) {
+  if constexpr (sizeof(typename TX::T) == 4) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    const typename TX::T h[4] = {static_cast<typename TX::T>(v.x & 0xffff), static_cast<typename TX::T>(v.x >> 16),
+                                 static_cast<typename TX::T>(v.y & 0xffff), static_cast<typename TX::T>(v.y >> 16)};
+    return make_float4(TX::ld(h, 0), TX::ld(h, 1), TX::ld(h, 2), TX::ld(h, 3));
+  }
+}
+
 // logits for up to 8 tokens: one workgroup per expert, its 4 waves split the hidden dim (float4 loads of
 // the fp32 router row), partial sums reduced through LDS in wave order. (A router row is 4-8 KB: spread
 // over E workgroups the rows stream at full-chip bandwidth; one CU alone keeps too few misses in flight.)
@@ -105,53 +120,81 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
         ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
 }
 
-// logits for many tokens on fp32 MFMA (v_mfma_f32_16x16x4_f32): a workgroup computes 16 tokens x 16
-// experts; its 4 waves and, inside a wave, the 4 lane quarters each own a contiguous run of the hidden dim
-// (any k order is valid as long as the token and expert operands of a lane agree). The 4 wave partials
-// are summed through LDS in wave order.
+// logits for many tokens on fp32 MFMA (v_mfma_f32_16x16x4_f32): a workgroup of 16 waves computes 16
+// tokens x 16 experts, each wave a contiguous run of the hidden dim. In a wave the lane (row r = lane % 16,
+// quarter q = lane / 16) takes k = run + 16j + 4q + i of token row r and router row r, so the 4 quarters
+// of a row read adjacent 16-byte pieces; MFMA step i of group j takes element i (any k order is valid
+// while the token and expert operands of a lane agree). Each lane fetches its groups in batches of 8 before
+// issuing their MFMAs; the 16 wave partials are summed through LDS in wave order.
+constexpr int kRouterWaves = 16;
+
 template <class TX>
-__global__ __launch_bounds__(256) void router_mfma_kernel(const typename TX::T* __restrict__ x, int n_tokens, int64_t H,
-                                                          int64_t xs, const float* __restrict__ w32, int E,
-                                                          float* __restrict__ logits) {
-  __shared__ float red[4][16][17];
+__global__ __launch_bounds__(kRouterWaves * 64) void router_mfma_kernel(const typename TX::T* __restrict__ x,
+                                                                        int n_tokens, int64_t H, int64_t xs,
+                                                                        const float* __restrict__ w32, int E,
+                                                                        float* __restrict__ logits) {
+  constexpr int U = 8;  // 16-k groups in flight per lane
+  __shared__ float red[kRouterWaves][16][17];
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
   const int row = lane % 16, q = lane / 16;
   const int t = t0 + row, e = e0 + row;
   const bool tok = t < n_tokens, exp_ok = e < E;
-  // this lane's run of the hidden dim: S consecutive k, S a multiple of 4
-  const int64_t S = ((H + 63) / 64) * 4;
-  const int64_t kb = (static_cast<int64_t>(wave) * 4 + q) * S;
+  // this wave's run of the hidden dim: KW consecutive k, KW a multiple of 16
+  const int64_t KW = (H + kRouterWaves * 16 - 1) / (kRouterWaves * 16) * 16;
+  const int64_t kw0 = static_cast<int64_t>(wave) * KW;
   const typename TX::T* xr = x + static_cast<int64_t>(tok ? t : 0) * xs;
   const float* wr = w32 + static_cast<int64_t>(exp_ok ? e : 0) * H;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  const bool vec = (H & 3) == 0;
-  for (int64_t s = 0; s < S; s += 4) {
-    const int64_t k = kb + s;
-    float a[4], b[4];
-    if (vec && k + 4 <= H) {
-      const float4 wv = exp_ok ? *reinterpret_cast<const float4*>(wr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 xv = tok ? load4<TX>(xr, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      a[0] = xv.x; a[1] = xv.y; a[2] = xv.z; a[3] = xv.w;
-      b[0] = wv.x; b[1] = wv.y; b[2] = wv.z; b[3] = wv.w;
-    } else {
+  // vector path: whole 4-element pieces at aligned addresses, loads made unconditional (masked pieces read
+  // zeros) so that no load sits in a divergent branch
+  const bool vec = (H & 3) == 0 && (xs & 3) == 0 &&
+                   (reinterpret_cast<uintptr_t>(x) & (4 * sizeof(typename TX::T) - 1)) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w32) & 15) == 0;
+  if (vec) {
+    const typename TX::T* xz = reinterpret_cast<const typename TX::T*>(g_zero4);
+    for (int64_t j0 = 0; j0 < KW; j0 += 16 * U) {
+      float4 av[U], bv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t k = kw0 + j0 + 16 * u + 4 * q;
+        const bool in = j0 + 16 * u < KW && k < H;  // H % 4 == 0: a piece is whole or out
+        bv[u] = *reinterpret_cast<const float4*>(in && exp_ok ? wr + k : g_zero4);
+        av[u] = load4v<TX>(in && tok ? xr + k : xz);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].x, bv[u].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].y, bv[u].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].z, bv[u].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u].w, bv[u].w, acc, 0, 0, 0);
+      }
+    }
+  } else {
+    for (int64_t j = 0; j < KW; j += 16) {
+      const int64_t k = kw0 + j + 4 * q;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool in = k + i < H;
-        a[i] = (tok && in) ? TX::ld(xr, k + i) : 0.f;
-        b[i] = (exp_ok && in) ? wr[k + i] : 0.f;
+        const float a1 = (tok && in) ? TX::ld(xr, k + i) : 0.f;
+        const float b1 = (exp_ok && in) ? wr[k + i] : 0.f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc, 0, 0, 0);
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[i], acc, 0, 0, 0);
   }
   // D[token = 4*(lane/16) + v][expert = lane % 16]
 #pragma unroll
   for (int v = 0; v < 4; ++v) red[wave][4 * q + v][row] = acc[v];
   __syncthreads();
-  const int i = threadIdx.x / 16, j = threadIdx.x % 16;
-  if (t0 + i < n_tokens && e0 + j < E)
-    logits[static_cast<int64_t>(t0 + i) * E + e0 + j] = ((red[0][i][j] + red[1][i][j]) + red[2][i][j]) + red[3][i][j];
+  if (threadIdx.x < 256) {
+    const int i = threadIdx.x / 16, jj = threadIdx.x % 16;
+    if (t0 + i < n_tokens && e0 + jj < E) {
+      float sum = red[0][i][jj];
+#pragma unroll
+      for (int w = 1; w < kRouterWaves; ++w) sum += red[w][i][jj];
+      logits[static_cast<int64_t>(t0 + i) * E + e0 + jj] = sum;
+    }
+  }
 }
 
 struct SelectArgs {
@@ -226,15 +269,17 @@ int launch_select(const float* logits, int64_t n_tokens, int64_t E, const float*
 
 template <class TX>
 int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const float* w32, int64_t E, float* logits,
-                  hipStream_t s) {
+                  hipStream_t s, const void* norm_w = nullptr, float eps = 0.f, void* xn_out = nullptr) {
   const auto* xp = static_cast<const typename TX::T*>(x);
-  if (n_tokens <= 8) {
+  const auto* nw = static_cast<const uint16_t*>(norm_w);
+  auto* xo = static_cast<uint16_t*>(xn_out);
+  if (n_tokens <= 8) {  // the RMSNorm is fused only here; larger batches take normalised rows
     hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xp,
-                       static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nullptr, 0.f, nullptr);
+                       static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
   } else {
     dim3 grid(static_cast<unsigned>((E + 15) / 16), static_cast<unsigned>((n_tokens + 15) / 16));
-    hipLaunchKernelGGL(router_mfma_kernel<TX>, grid, dim3(256), 0, s, xp, static_cast<int>(n_tokens), H, xs, w32,
-                       static_cast<int>(E), logits);
+    hipLaunchKernelGGL(router_mfma_kernel<TX>, grid, dim3(kRouterWaves * 64), 0, s, xp, static_cast<int>(n_tokens), H,
+                       xs, w32, static_cast<int>(E), logits);
   }
   return mm::check_launch("router_logits");
 }
@@ -243,17 +288,22 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
 
 namespace mm {
 
-// Router of the decode block front for 1..8 bf16 tokens: logits with the RMSNorm (norm_w bf16, eps)
-// applied on the fly, the normalised rows stored to xn_out ([n_tokens, H] bf16), then the selection with
-// the shared expert appended.
+// Router of the MoE block front for bf16 tokens: RMSNorm (norm_w bf16, eps) into xn_out ([n_tokens, H]
+// bf16), logits of the normalised rows, then the selection with the shared expert appended. Up to 8 tokens
+// the norm runs inside the logits kernel; larger batches normalise first (mm_rms_norm), which is faster
+// than repeating the row reduction in every router workgroup. Either way xn is bit-identical.
 int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
                  const float* w32, const SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
                  int64_t out_row_stride, void* xn_out, hipStream_t s) {
-  MM_REQUIRE(n_tokens >= 1 && n_tokens <= 8, "router: the fused norm path takes 1..8 tokens");
-  hipLaunchKernelGGL(router_gemv_kernel<BF16>, dim3(static_cast<unsigned>(sp.E)), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(x), static_cast<int>(n_tokens), H, xs, w32, sp.E, logits,
-                     static_cast<const uint16_t*>(norm_w), eps, static_cast<uint16_t*>(xn_out));
-  const int rc = check_launch("router_logits");
+  MM_REQUIRE(n_tokens >= 1 && n_tokens <= 0x7fffffffLL, "router: bad token count");
+  int rc;
+  if (n_tokens <= 8) {
+    rc = launch_logits<BF16>(x, n_tokens, H, xs, w32, sp.E, logits, s, norm_w, eps, xn_out);
+  } else {
+    rc = mm_rms_norm(x, MM_BF16, n_tokens, H, xs, norm_w, MM_BF16, eps, xn_out, MM_BF16, H, s);
+    if (rc) return rc;
+    rc = launch_logits<BF16>(xn_out, n_tokens, H, H, w32, sp.E, logits, s);
+  }
   if (rc) return rc;
   return launch_select(logits, n_tokens, sp.E, sp.bias, sp.scoring, sp.n_group, sp.topk_group, sp.top_k, sp.scale,
                        sp.append_shared, ids, ids_dtype, wts, out_row_stride, s);

@@ -168,7 +168,7 @@ class PrefillScratch:
     """Device buffers of one prefill call (align output and intermediates), reusable across calls of the
     same shape so that a caller can keep them outside the timed or captured region."""
 
-    def __init__(self, N, KP1, E1, H, I, device):
+    def __init__(self, N, KP1, E1, H, I, device, block=False):
         P = N * KP1
         self.nb = _num_blocks(P, E1, BLOCK_M)
         self.sorted_ids = torch.empty(self.nb * BLOCK_M, dtype=torch.int32, device=device)
@@ -177,6 +177,11 @@ class PrefillScratch:
         self.a = torch.empty(P, I, device=device, dtype=torch.bfloat16)
         self.part = torch.empty(P, H, device=device, dtype=torch.bfloat16)
         self.y = torch.empty(N, H, device=device, dtype=torch.bfloat16)
+        if block:  # router outputs and normalised rows of moe_block_prefill
+            self.logits = torch.empty(N, E1 - 1, device=device, dtype=torch.float32)
+            self.ids = torch.empty(N, KP1, device=device, dtype=torch.int64)
+            self.wts = torch.empty(N, KP1, device=device, dtype=torch.float32)
+            self.xn = torch.empty(N, H, device=device, dtype=torch.bfloat16)
 
 
 def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residual=None, scratch=None,
@@ -225,6 +230,45 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
                                      _mm.ptr(part), _mm.ptr(y), H,
                                      phases, _mm.stream_of(x)), "fused_moe_prefill")
     return y
+
+
+def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scoring="softmax", n_group=1,
+                      topk_group=1, scale=1.0, s_gu=None, s_d=None, residual=True, scratch=None):
+    """One prefill MoE block: RMSNorm (norm_w, eps; normalised rows kept in the scratch), router, expert
+    selection (shared expert appended), align, gate/up, down, combine (+ x).
+    Same results as rms_norm -> route -> fused_moe_prefill(residual=x). Returns (y [N, H], ids, wts,
+    logits), views of `scratch` (a PrefillScratch made with block=True; allocated when None)."""
+    _mm.require_gpu(x, norm_w, w32, w_gu, w_d, bias, s_gu, s_d)
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    N, E = x2.shape[0], w32.shape[0]
+    NK = top_k + 1
+    for name, t, dt in (("x", x2, torch.bfloat16), ("norm_w", norm_w, torch.bfloat16), ("w32", w32, torch.float32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"moe_block_prefill: {name} must be contiguous {dt}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E or not bias.is_contiguous()):
+        raise ValueError("moe_block_prefill: bias must be a contiguous fp32 [E] tensor")
+    if scoring not in _SCORING:
+        raise ValueError(f"moe_block_prefill: scoring must be one of {sorted(_SCORING)}")
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d)
+    sc = scratch if scratch is not None else PrefillScratch(N, NK, ex.n_slots, H, ex.inter, x.device, block=True)
+    if not hasattr(sc, "xn") or sc.xn.shape != (N, H) or sc.ids.shape != (N, NK) or sc.logits.shape != (N, E) \
+            or sc.a.shape != (N * NK, ex.inter) or sc.offsets.numel() != ex.n_slots + 1:
+        raise ValueError("moe_block_prefill: scratch was made for another shape (or without block=True)")
+    if N == 0:
+        return sc.y, sc.ids, sc.wts, sc.logits
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_moe_block_prefill(_mm.ptr(x2), N, x2.stride(0), _mm.ptr(norm_w), float(eps), _mm.ptr(w32), E,
+                                           _mm.ptr(bias), _SCORING[scoring], int(n_group), int(topk_group),
+                                           int(top_k), float(scale), ex, _mm.ptr(sc.logits), _mm.ptr(sc.ids),
+                                           _mm.dtype_code(sc.ids), _mm.ptr(sc.wts), _mm.ptr(sc.xn),
+                                           _mm.ptr(sc.sorted_ids), _mm.ptr(sc.bexp), _mm.ptr(sc.offsets), sc.nb,
+                                           _mm.ptr(sc.a), _mm.ptr(sc.part), 1 if residual else 0, _mm.ptr(sc.y), H,
+                                           _mm.stream_of(x)), "moe_block_prefill")
+    return sc.y, sc.ids, sc.wts, sc.logits
 
 
 def quantize_rows_int8(w, *, scale_dtype=torch.float32):

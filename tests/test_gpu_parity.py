@@ -268,6 +268,28 @@ def test_prefill_int8(blk, n):
     close(y, _oracle_moe(cpu, xn, ids, wts, int8=True))
 
 
+@pytest.mark.parametrize("n,int8", [(512, False), (100, True), (20, False), (5, False)])
+def test_moe_block_prefill_matches_unfused_and_oracle(blk, n, int8):
+    """The prefill block (norm fused into the router GEMM) equals rms_norm -> route -> fused_moe_prefill
+    (residual=x) bit for bit above the decode sizes, and the oracle within tolerance."""
+    b, cpu = blk
+    bias = W.ragged_bias(device=DEV)
+    x = W.tokens(n, seed=160 + n, device=DEV)
+    wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
+    sg, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
+    sc = fused_moe.PrefillScratch(n, 7, 65, W.HIDDEN, W.INTER, DEV, block=True)
+    y, ids, wts, logits = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=6, bias=bias,
+                                                      s_gu=sg, s_d=sd, scratch=sc)
+    xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+    assert torch.equal(sc.xn, xn)
+    i2, w2, l2 = fused_ops.route(xn, b["w32"], bias, top_k=6, scoring="softmax")
+    assert torch.equal(logits, l2) and torch.equal(ids, i2.long()) and torch.equal(wts, w2)
+    if n > fused_moe.MAX_DECODE_TOKENS:  # the unfused call takes the same prefill kernels
+        y2 = fused_moe.fused_moe_prefill(xn, wg, wd, i2, w2, s_gu=sg, s_d=sd, residual=x)
+        assert torch.equal(y, y2)
+    close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
+
+
 def test_prefill_zipf_2048_subset_and_histogram(blk):
     b, cpu = blk
     x = W.tokens(2048, seed=90, device=DEV)
