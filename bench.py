@@ -14,10 +14,15 @@ bytes over its average duration from HIP events on its own stream; the CPU basel
 torch path on a bounded sample of the same workload on this host.
 """
 import argparse
+import csv
+import glob
 import json
 import os
 import platform
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -37,6 +42,8 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of extra workloads to run (decode,int8,zipf,full)")
+    ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 counter passes (traffic = null)")
+    ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -138,6 +145,75 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70):
         "mfma_pct": flops / (moe_ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 100,
         "hbm_pct_weights": used * W.expert_bytes() / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
     }
+
+
+# ------------------------------------------------------------------------------- HBM traffic (counters)
+
+PROBE_LAUNCHES = 5
+COPY_BYTES = 512 << 20  # calibration copy: reads and writes this many bytes, twice the last-level cache
+
+
+def pmc_probe():
+    """Child run under `rocprofv3 --pmc <counter>`: the headline gate/up kernel PROBE_LAUNCHES times on the
+    512-token workload, then a plain device copy of COPY_BYTES as many times (counter calibration)."""
+    import fused_moe
+    import _mingmoe
+    import workloads as W
+    _mingmoe.load()
+    b = W.block(seed=0, device="cuda")
+    x, sc, st, step = prefill_setup(b, 512, W.ragged_bias(device="cuda"), 70)
+    for _ in range(PROBE_LAUNCHES):
+        fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], st["ids"], st["wts"], residual=x, scratch=sc,
+                                    phases=_mingmoe.MM_PHASE_GATE_UP, align=False)
+    torch.cuda.synchronize()
+    del b
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(PROBE_LAUNCHES):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[probe] done", flush=True)
+
+
+def _counter_per_dispatch(path, counter):
+    """{kernel name: [counter value of each dispatch]} from a rocprofv3 counter_collection.csv."""
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") == counter:
+                out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def pmc_traffic(timeout=90):
+    """HBM bytes per launch of the gate/up kernel: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two
+    rocprofv3 --pmc passes over pmc_probe(), each scaled by bytes / counter of the calibration copy."""
+    tool = shutil.which("rocprofv3")
+    if tool is None:
+        return None, {"error": "rocprofv3 not found"}
+    detail = {}
+    total = 0.0
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="mm_pmc_")
+        cmd = ["timeout", "-s", "KILL", str(timeout), tool, "--pmc", counter, "--output-format", "csv", "-d", out,
+               "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--pmc-probe"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            shutil.rmtree(out, ignore_errors=True)
+            return None, {"error": f"{counter} pass exited {r.returncode} without counters", "stderr": r.stderr[-400:]}
+        per = _counter_per_dispatch(files[0], counter)
+        shutil.rmtree(out, ignore_errors=True)
+        gu = [v for k, vs in per.items() if "prefill_gate_up_kernel" in k for v in vs]
+        cp = [v for k, vs in per.items() if "copy" in k.lower() for v in vs]
+        if not gu or not cp:
+            return None, {"error": f"{counter}: kernels not found in {sorted(per)}"}
+        gu_kib, cp_kib = sum(gu) / len(gu), sum(cp) / len(cp)
+        factor = COPY_BYTES / (cp_kib * 1024.0)
+        detail[counter] = {"gate_up_KiB": gu_kib, "copy_KiB": cp_kib, "copy_bytes": COPY_BYTES, "factor": factor,
+                           "bytes": gu_kib * 1024.0 * factor}
+        total += gu_kib * 1024.0 * factor
+    return total, detail
 
 
 # ------------------------------------------------------------------------------------------------ decode
@@ -275,6 +351,9 @@ def cpu_baseline(b, bias, n_sample=64, reps=2):
 
 def main():
     args = parse()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE block path has no multi-GPU code in this build "
               "(use --gpus 1)", file=sys.stderr)
@@ -318,6 +397,11 @@ def main():
         log(f"[bench] full decode: {extra['full_decode_28l']}")
     gu_s = head["gate_up_us"] * 1e-6
     achieved = head["gate_up_bytes"] / gu_s / 1e9
+    traffic = None
+    if not args.no_pmc:
+        traffic, detail = pmc_traffic()
+        extra["gate_up_traffic"] = dict(detail, algorithmic_bytes=head["gate_up_bytes"])
+        log(f"[bench] gate/up traffic: {traffic} ({detail})")
     line = {
         "metric": "MoE layer decode us/token + achieved HBM TB/s; MoE prefill tokens/s + MFMA %",
         "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -327,7 +411,7 @@ def main():
                                "softmax top-6, ragged router bias", "tokens": 512, "hidden": 2048, "experts": 64,
                    "inter": 1408, "top_k": 6, "graph": True},
         "roofline": {"bound": "hbm", "kernel": "prefill_gate_up_kernel", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
         "cpu_baseline": cpu,
         "extra": extra,
     }
