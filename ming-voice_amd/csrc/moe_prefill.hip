@@ -22,35 +22,29 @@ namespace {
 using namespace mmd;
 
 constexpr int kBM = 64;          // rows (pairs) per block, = align block_m
-constexpr int kThreads = 256;    // 4 waves
 constexpr int kXcds = 8;
-// Tile shape per weight type: output columns per tile, k-slab width (k elements per LDS stage: each
-// weight row is fetched in segments of BK elements, and HBM streams longer segments better), LDS stages
-// (k-slabs in flight) and wave rows (1: each wave 64 rows x BN/4 columns; 2: 32 rows x BN/2 columns).
-// LDS = stages x (64 x BK x 2 B + BN x BK x weight bytes); fewer stages let more workgroups share a CU.
-#ifndef MM_PREFILL_BN_BF16
-#define MM_PREFILL_BN_BF16 128
+// Tile shape per weight type and GEMM: output columns per tile (BN) and waves per workgroup. The k-slab is
+// 64 elements; 128-column bf16 tiles keep 3 slabs in flight, int8 and 256-column tiles 2 (LDS = slabs x
+// (8 KB + BN x 64 x weight bytes), two workgroups per CU). Waves split the 64 x BN tile as 1 x 4 (4 waves,
+// each 64 rows x BN/4) or 2 x NW/2 (8 waves, or 64-column tiles). Measured on the 512-token block: 8-wave
+// 128-column bf16 tiles are the fastest of 64/128/256 columns x 4/8 waves x 2/3 slabs.
+#ifndef MM_PREFILL_GU_BN_BF16
+#define MM_PREFILL_GU_BN_BF16 128
 #endif
-#ifndef MM_PREFILL_BK_BF16
-#define MM_PREFILL_BK_BF16 64
+#ifndef MM_PREFILL_DOWN_BN_BF16
+#define MM_PREFILL_DOWN_BN_BF16 128
 #endif
-#ifndef MM_PREFILL_BK_INT8
-#define MM_PREFILL_BK_INT8 64
+#ifndef MM_PREFILL_GU_BN_INT8
+#define MM_PREFILL_GU_BN_INT8 256
 #endif
-#ifndef MM_PREFILL_SLABS_BF16
-#define MM_PREFILL_SLABS_BF16 3
+#ifndef MM_PREFILL_DOWN_BN_INT8
+#define MM_PREFILL_DOWN_BN_INT8 256
 #endif
-#ifndef MM_PREFILL_WM_BF16
-#define MM_PREFILL_WM_BF16 1
+#ifndef MM_PREFILL_GU_WAVES_BF16
+#define MM_PREFILL_GU_WAVES_BF16 8
 #endif
-#ifndef MM_PREFILL_BN_INT8
-#define MM_PREFILL_BN_INT8 256
-#endif
-#ifndef MM_PREFILL_SLABS_INT8
-#define MM_PREFILL_SLABS_INT8 2
-#endif
-#ifndef MM_PREFILL_WM_INT8
-#define MM_PREFILL_WM_INT8 1
+#ifndef MM_PREFILL_DOWN_WAVES_BF16
+#define MM_PREFILL_DOWN_WAVES_BF16 8
 #endif
 
 struct PrefillArgs {
@@ -124,13 +118,15 @@ __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
 
 __device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes for masked lanes
 
-template <bool Q>
+template <bool Quant, int TileN, int Waves = 4>
 struct Geo {
-  static constexpr int BN = Q ? MM_PREFILL_BN_INT8 : MM_PREFILL_BN_BF16;     // output columns per tile
-  static constexpr int BK = Q ? MM_PREFILL_BK_INT8 : MM_PREFILL_BK_BF16;     // k elements per slab
-  static constexpr int NS = Q ? MM_PREFILL_SLABS_INT8 : MM_PREFILL_SLABS_BF16;  // slabs in flight
-  static constexpr int WM = Q ? MM_PREFILL_WM_INT8 : MM_PREFILL_WM_BF16;     // wave rows
-  static constexpr int WN = 4 / WM;                   // wave columns
+  static constexpr bool Q = Quant;
+  static constexpr int BN = TileN;                    // output columns per tile
+  static constexpr int NW = Waves;                    // waves per workgroup
+  static constexpr int BK = 64;                       // k elements per slab
+  static constexpr int NS = Q || BN >= 256 ? 2 : 3;   // slabs in flight
+  static constexpr int WM = (BN <= 64 || NW == 8) ? 2 : 1;  // wave rows
+  static constexpr int WN = NW / WM;                  // wave columns
   static constexpr int FM = kBM / WM / 16;            // 16-row fragments per wave
   static constexpr int FN = BN / WN / 16;             // 16-column fragments per wave
   static constexpr int AROW = BK * 2;                 // activation (bf16) bytes per row per slab
@@ -139,13 +135,12 @@ struct Geo {
   static constexpr int B_BYTES = BN * ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr size_t LDS = static_cast<size_t>(NS) * STAGE;
-  static constexpr int A_INSTR = A_BYTES / 1024 / 4;  // direct-load instructions per wave per slab
-  static constexpr int B_INSTR = B_BYTES / 1024 / 4;
+  static constexpr int A_INSTR = A_BYTES / 1024 / NW;  // direct-load instructions per wave per slab
+  static constexpr int B_INSTR = B_BYTES / 1024 / NW;
   static constexpr int LOADS = A_INSTR + B_INSTR;
   static constexpr int KSTEPS = BK / 32;              // MFMA k-steps per slab
-  static_assert((BN == 64 || BN == 128 || BN == 256) && (WM == 1 || WM == 2) && FN % 2 == 0, "tile shape");
-  static_assert(BK == 64 || BK == 128, "slab width");
-  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "slab must split over 4 waves in 1 KB pieces");
+  static_assert((BN == 64 || BN == 128 || BN == 256) && (NW == 4 || NW == 8) && FN % 2 == 0, "tile shape");
+  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "slab must split over the waves in 1 KB pieces");
 };
 
 // LDS byte position of 16-byte chunk c of row r in a slab with rows of `rowb` bytes. The XOR swizzle puts
@@ -174,12 +169,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Per-thread source rows of the direct loads: for A instruction j the lane fills tile row ra[j], logical
 // chunk ca[j]; for B instruction j tile row rb[j], logical chunk cb[j].
-template <bool Q>
+template <class G>
 struct LoadMap {
-  int ra[Geo<Q>::A_INSTR], ca[Geo<Q>::A_INSTR];
-  int rb[Geo<Q>::B_INSTR], cb[Geo<Q>::B_INSTR];
+  int ra[G::A_INSTR], ca[G::A_INSTR];
+  int rb[G::B_INSTR], cb[G::B_INSTR];
   __device__ __forceinline__ LoadMap() {
-    using G = Geo<Q>;
     constexpr int ACH = G::AROW / 16, BCH = G::ROWB / 16;  // chunks per row
     const int w = threadIdx.x / kWave, l = lane_id();
 #pragma unroll
@@ -199,25 +193,25 @@ struct LoadMap {
 
 // Issues the direct loads of slab kt into LDS stage `st` (arow/brow: this thread's source row starts,
 // null for masked rows; k counted in elements).
-template <bool Q>
-__device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K, const LoadMap<Q>& m,
+template <class G>
+__device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K, const LoadMap<G>& m,
                                            const uint16_t* const* arow, const char* const* brow) {
-  constexpr int ES = Q ? 1 : 2;
-  char* sa = lds + st * Geo<Q>::STAGE;
-  char* sb = sa + Geo<Q>::A_BYTES;
+  constexpr int ES = G::Q ? 1 : 2;
+  char* sa = lds + st * G::STAGE;
+  char* sb = sa + G::A_BYTES;
   const int w = threadIdx.x / kWave;
-  const int64_t k0 = static_cast<int64_t>(kt) * Geo<Q>::BK;
+  const int64_t k0 = static_cast<int64_t>(kt) * G::BK;
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) {
+  for (int j = 0; j < G::A_INSTR; ++j) {
     const int64_t k = k0 + m.ca[j] * 8;
     const void* src = (arow[j] && k < K) ? static_cast<const void*>(arow[j] + k) : static_cast<const void*>(g_zero_chunk);
-    load_lds16(src, sa + (w * Geo<Q>::A_INSTR + j) * 1024);
+    load_lds16(src, sa + (w * G::A_INSTR + j) * 1024);
   }
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) {
+  for (int j = 0; j < G::B_INSTR; ++j) {
     const int64_t k = k0 + m.cb[j] * (16 / ES);
     const void* src = (brow[j] && k < K) ? static_cast<const void*>(brow[j] + k * ES) : static_cast<const void*>(g_zero_chunk);
-    load_lds16(src, sb + (w * Geo<Q>::B_INSTR + j) * 1024);
+    load_lds16(src, sb + (w * G::B_INSTR + j) * 1024);
   }
 }
 
@@ -227,27 +221,27 @@ __device__ __forceinline__ bf16x8_t lds_frag16(const char* base, int pos) {
 
 // The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
 // 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j.
-template <bool Q, class XRowFn, class WRowFn, class BColFn>
-__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN], int64_t K, XRowFn xrow,
+template <class G, class XRowFn, class WRowFn, class BColFn>
+__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t K, XRowFn xrow,
                                           WRowFn wrow, char* lds, int r0, BColFn bcol) {
-  constexpr int NS = Geo<Q>::NS, LOADS = Geo<Q>::LOADS, FM = Geo<Q>::FM, FN = Geo<Q>::FN;
+  constexpr int NS = G::NS, LOADS = G::LOADS, FM = G::FM, FN = G::FN;
   const int lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
-  const LoadMap<Q> m;
-  const uint16_t* arow[Geo<Q>::A_INSTR];
-  const char* brow[Geo<Q>::B_INSTR];
+  const LoadMap<G> m;
+  const uint16_t* arow[G::A_INSTR];
+  const char* brow[G::B_INSTR];
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::A_INSTR; ++j) arow[j] = xrow(m.ra[j]);
+  for (int j = 0; j < G::A_INSTR; ++j) arow[j] = xrow(m.ra[j]);
 #pragma unroll
-  for (int j = 0; j < Geo<Q>::B_INSTR; ++j) brow[j] = wrow(m.rb[j]);
+  for (int j = 0; j < G::B_INSTR; ++j) brow[j] = wrow(m.rb[j]);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int nk = static_cast<int>((K + Geo<Q>::BK - 1) / Geo<Q>::BK);
+  const int nk = static_cast<int>((K + G::BK - 1) / G::BK);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue_slab<Q>(lds, s, s, K, m, arow, brow);
+    if (s < nk) issue_slab<G>(lds, s, s, K, m, arow, brow);
   for (int kt = 0; kt < nk; ++kt) {
     // slabs issued after kt so far: min(nk - 1 - kt, NS - 2); wait for kt's own loads
     const int pending = min(nk - 1 - kt, NS - 2);
@@ -262,19 +256,19 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN]
     // slab kt visible to all waves; every wave is done with slab kt-1. A plain barrier: the loads of
     // slab kt were waited for above, and a memory fence would also wait for the later slabs' loads.
     __builtin_amdgcn_s_barrier();
-    if (kt + NS - 1 < nk) issue_slab<Q>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow);
-    const char* sa = lds + (kt % NS) * Geo<Q>::STAGE;
-    const char* sb = sa + Geo<Q>::A_BYTES;
-    if constexpr (Q) {
+    if (kt + NS - 1 < nk) issue_slab<G>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow);
+    const char* sa = lds + (kt % NS) * G::STAGE;
+    const char* sb = sa + G::A_BYTES;
+    if constexpr (G::Q) {
       // one 16-byte int8 chunk (16 k) per lane and fragment feeds two 32-wide steps: in 64-k group g the
       // lane quarter lq takes int8 chunk 4g + lq, i.e. bf16 activation chunks 8g + 2lq (+1)
 #pragma unroll
-      for (int g = 0; g < Geo<Q>::BK / 64; ++g) {
+      for (int g = 0; g < G::BK / 64; ++g) {
         bf16x8_t fb[2][FN];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           uint4 lo, hi;
-          widen_i8(*reinterpret_cast<const uint4*>(sb + pos_row<Geo<Q>::ROWB>(bcol(j) + lr, 4 * g + lq)), lo, hi);
+          widen_i8(*reinterpret_cast<const uint4*>(sb + pos_row<G::ROWB>(bcol(j) + lr, 4 * g + lq)), lo, hi);
           fb[0][j] = __builtin_bit_cast(bf16x8_t, lo);
           fb[1][j] = __builtin_bit_cast(bf16x8_t, hi);
         }
@@ -283,7 +277,7 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN]
           bf16x8_t fa[FM];
 #pragma unroll
           for (int i = 0; i < FM; ++i)
-            fa[i] = lds_frag16(sa, pos_row<Geo<Q>::AROW>(r0 + 16 * i + lr, 8 * g + 2 * lq + ks));
+            fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, 8 * g + 2 * lq + ks));
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -293,13 +287,13 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN]
       }
     } else {
 #pragma unroll
-      for (int ks = 0; ks < Geo<Q>::KSTEPS; ++ks) {
+      for (int ks = 0; ks < G::KSTEPS; ++ks) {
         const int ch = ks * 4 + lq;
         bf16x8_t fa[FM], fb[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_row<Geo<Q>::AROW>(r0 + 16 * i + lr, ch));
+        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, ch));
 #pragma unroll
-        for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_row<Geo<Q>::ROWB>(bcol(j) + lr, ch));
+        for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_row<G::ROWB>(bcol(j) + lr, ch));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -312,9 +306,9 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[Geo<Q>::FM][Geo<Q>::FN]
 
 // ------------------------------------------------------------------------------------------- gate / up
 
-template <bool Q>
-__global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a) {
-  using G = Geo<Q>;
+template <bool Q, int BN, int NW>
+__global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a) {
+  using G = Geo<Q, BN, NW>;
   constexpr int HALF = G::BN / 2;  // gate columns per tile (and as many up columns)
   extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
@@ -342,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
   constexpr int FG = G::FN / 2;      // gate fragments of the wave; the next FG are the matching up ones
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
-  tile_gemm<Q>(acc, a.H, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<G>(acc, a.H, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); });
 #pragma unroll
   for (int j = 0; j < FG; ++j) {
@@ -369,9 +363,9 @@ __global__ __launch_bounds__(kThreads) void prefill_gate_up_kernel(PrefillArgs a
 
 // ----------------------------------------------------------------------------------------------- down
 
-template <bool Q>
-__global__ __launch_bounds__(kThreads) void prefill_down_kernel(PrefillArgs a) {
-  using G = Geo<Q>;
+template <bool Q, int BN, int NW>
+__global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
+  using G = Geo<Q, BN, NW>;
   extern __shared__ uint4 lds_raw[];
   __shared__ int spair[kBM];
   const int NT = static_cast<int>((a.H + G::BN - 1) / G::BN);
@@ -395,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void prefill_down_kernel(PrefillArgs a) {
   const int r0 = wm * (kBM / G::WM);
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
-  tile_gemm<Q>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
+  tile_gemm<G>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
 #pragma unroll
   for (int j = 0; j < G::FN; ++j) {
     const int64_t h = h0 + c0 + 16 * j + (lane & 15);
@@ -477,23 +471,37 @@ int allow_lds(K kernel, size_t bytes, const char* what) {
   return MM_OK;
 }
 
+template <bool Q, int BN, int NW>
+int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
+  using G = Geo<Q, BN, NW>;
+  const int64_t nt = (a.I + G::BN / 2 - 1) / (G::BN / 2);
+  const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
+  int rc = allow_lds(prefill_gate_up_kernel<Q, BN, NW>, G::LDS, "prefill_gate_up");
+  if (rc) return rc;
+  hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  return mm::check_launch("moe_prefill gate_up");
+}
+
+template <bool Q, int BN, int NW>
+int launch_down(const PrefillArgs& a, int64_t nb, hipStream_t st) {
+  using G = Geo<Q, BN, NW>;
+  const int64_t nt = (a.H + G::BN - 1) / G::BN;
+  const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
+  int rc = allow_lds(prefill_down_kernel<Q, BN, NW>, G::LDS, "prefill_down");
+  if (rc) return rc;
+  hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  return mm::check_launch("moe_prefill down");
+}
+
 template <bool Q>
 int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
+  constexpr int GU_BN = Q ? MM_PREFILL_GU_BN_INT8 : MM_PREFILL_GU_BN_BF16;
+  constexpr int DOWN_BN = Q ? MM_PREFILL_DOWN_BN_INT8 : MM_PREFILL_DOWN_BN_BF16;
+  constexpr int GU_NW = Q ? 4 : MM_PREFILL_GU_WAVES_BF16;
+  constexpr int DOWN_NW = Q ? 4 : MM_PREFILL_DOWN_WAVES_BF16;
   int rc;
-  if (phases & MM_PHASE_GATE_UP) {
-    const int64_t nt = (a.I + Geo<Q>::BN / 2 - 1) / (Geo<Q>::BN / 2);
-    const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-    if ((rc = allow_lds(prefill_gate_up_kernel<Q>, Geo<Q>::LDS, "prefill_gate_up"))) return rc;
-    hipLaunchKernelGGL(prefill_gate_up_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
-    if ((rc = mm::check_launch("moe_prefill gate_up"))) return rc;
-  }
-  if (phases & MM_PHASE_DOWN) {
-    const int64_t nt = (a.H + Geo<Q>::BN - 1) / Geo<Q>::BN;
-    const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-    if ((rc = allow_lds(prefill_down_kernel<Q>, Geo<Q>::LDS, "prefill_down"))) return rc;
-    hipLaunchKernelGGL(prefill_down_kernel<Q>, dim3(static_cast<unsigned>(g)), dim3(kThreads), Geo<Q>::LDS, st, a);
-    if ((rc = mm::check_launch("moe_prefill down"))) return rc;
-  }
+  if ((phases & MM_PHASE_GATE_UP) && (rc = launch_gate_up<Q, GU_BN, GU_NW>(a, nb, st))) return rc;
+  if ((phases & MM_PHASE_DOWN) && (rc = launch_down<Q, DOWN_BN, DOWN_NW>(a, nb, st))) return rc;
   return MM_OK;
 }
 
