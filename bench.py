@@ -274,7 +274,9 @@ def decode_metrics(b, n, stream, int8=False, seed=40):
 # ------------------------------------------------------------------------------------- full decode step
 
 def full_decode_metrics(stream, layers=28):
-    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1."""
+    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1; and the
+    28 MoE blocks alone (median of 5 timings): the decode MoE layer with every layer's experts read from
+    HBM, as in a real forward pass (the single-layer decode figures can hit the 256 MB last-level cache)."""
     import fastlinear
     import fused_moe
     import fused_ops
@@ -312,13 +314,27 @@ def full_decode_metrics(stream, layers=28):
 
     g = graph_of(step, stream)
     ms = time_graph(g, stream, 20)
+
+    def moe_only():  # the 28 MoE blocks alone, distinct weights per layer (no reuse from the last-level cache)
+        h = x0
+        for p in L:
+            b = p["blk"]
+            h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
+                                           logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
+        return h
+
+    gm = graph_of(moe_only, stream)
+    moe_ms = sorted(time_graph(gm, stream, 20) for _ in range(5))[2]
     proj = 28 * (2 * H * H + 2 * 256 * H) * 2
     moe = 28 * 7 * W.expert_bytes()
     router = 28 * E * H * 4
     total = proj + moe + router + W.VOCAB * H * 2
+    moe_layer_bytes = 7 * W.expert_bytes() + E * H * 4
     del L, head
     return {"layers": layers, "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
-            "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100}
+            "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+            "moe_us_per_layer": moe_ms * 1e3 / layers, "moe_layer_bytes": moe_layer_bytes,
+            "moe_TBs": moe_layer_bytes * layers / moe_ms / 1e9}
 
 
 # -------------------------------------------------------------------------------------------- CPU baseline

@@ -361,13 +361,23 @@ int launch_b(const DecodeArgs& a, hipStream_t st) {
 
 // Template choice. A row of nch 16-byte chunks is split over LPR lanes with NC chunks per lane per
 // pass; rows longer than LPR * NC chunks take several passes, so a few instances cover every shape.
+// Row pairs per wave of the single-token gate/up kernel: one (more, smaller workgroups) measured best over
+// 28 distinct layers against two to four.
+#ifndef MM_GU_R_BF16
+#define MM_GU_R_BF16 1
+#endif
+#ifndef MM_GU_R_I8
+#define MM_GU_R_I8 1
+#endif
+
 template <bool Q, int LPR, int NC>
 int dispatch_a_t(const DecodeArgs& a, hipStream_t st) {
   // tokens staged per group: one per token of the batch (a token naming an expert twice adds groups),
   // bounded so that the staged rows fit 64 KB of LDS
   int maxt = a.n_tokens;
   while (maxt > 1 && static_cast<int64_t>(maxt) * a.H * 2 > 65536) maxt /= 2;
-  if (maxt <= 1) return launch_a<Q, LPR, NC, 2, 1>(a, st);
+  constexpr int R = Q ? MM_GU_R_I8 : MM_GU_R_BF16;  // row pairs per wave
+  if (maxt <= 1) return launch_a<Q, LPR, NC, R, 1>(a, st);
   if (maxt <= 2) return launch_a<Q, LPR, NC, 2, 2>(a, st);
   if (maxt <= 4) return launch_a<Q, LPR, NC, 2, 4>(a, st);
   return launch_a<Q, LPR, NC, 2, 8>(a, st);
@@ -382,14 +392,26 @@ int dispatch_a(const DecodeArgs& a, hipStream_t st) {
   return dispatch_a_t<Q, 64, 4>(a, st);
 }
 
+// Lanes per row and chunks per lane of the down kernel for rows of the benchmarked size (1408 inter):
+// 32 lanes read 512 contiguous bytes of a row per instruction; measured over 28 distinct layers, 32 lanes
+// beat 16 (256-byte pieces) and 64 (one row per wave step, too little work per wave).
+#ifndef MM_DOWN_BF16_LPR
+#define MM_DOWN_BF16_LPR 32
+#define MM_DOWN_BF16_NC 6
+#endif
+#ifndef MM_DOWN_I8_LPR
+#define MM_DOWN_I8_LPR 32
+#define MM_DOWN_I8_NC 3
+#endif
+
 template <bool Q>
 int dispatch_b(const DecodeArgs& a, hipStream_t st) {
   const int64_t nch = a.I * (Q ? 1 : 2) / 16;  // down rows run over the intermediate dim
   if constexpr (Q) {  // int8 chunks carry 32-byte activation chunks: fewer chunks per lane
-    if (nch > 48) return launch_b<Q, 16, 6>(a, st);
+    if (nch > 48) return launch_b<Q, MM_DOWN_I8_LPR, MM_DOWN_I8_NC>(a, st);
     return launch_b<Q, 8, 6>(a, st);
   } else {
-    if (nch >= 128) return launch_b<Q, 16, 12>(a, st);
+    if (nch >= 128) return launch_b<Q, MM_DOWN_BF16_LPR, MM_DOWN_BF16_NC>(a, st);
     if (nch > 32) return launch_b<Q, 8, 12>(a, st);
     return launch_b<Q, 8, 4>(a, st);
   }
@@ -494,7 +516,8 @@ int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const v
 
 // Whole MoE block for 1..8 tokens in four launches: router logits (RMSNorm fused; the normalised rows go
 // to the workspace), selection, gate/up on the normalised rows, down + combine with the raw rows as
-// residual. The ids / weights it writes are the ones the unfused chain produces.
+// residual. (Selecting in the router's last-finishing workgroup instead costs more in device-wide fences
+// than the launch it saves.) The ids / weights it writes are the ones the unfused chain produces.
 extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
                                    const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
                                    int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
@@ -516,11 +539,12 @@ extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_ro
   MM_REQUIRE(ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "moe_block_decode: shape too large");
   hipStream_t st = MM_STREAM(stream);
   const mmd::SelectParams sp{bias, static_cast<int>(n_experts), scoring, n_group, topk_group, top_k, scale, 1};
+  void* xn = workspace;
   rc = mm::router_front(x, n_tokens, ex->hidden, x_row_stride, norm_w, eps, w32, sp, logits, ids, ids_dtype, wts, nk,
-                        workspace, st);
+                        xn, st);
   if (rc) return rc;
   DecodeArgs a;
-  a.x = static_cast<const uint16_t*>(workspace);
+  a.x = static_cast<const uint16_t*>(xn);
   a.xs = ex->hidden;
   a.n_tokens = static_cast<int>(n_tokens);
   a.nk = static_cast<int>(nk);

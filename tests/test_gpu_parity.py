@@ -422,3 +422,39 @@ def test_gpu_argument_errors():
         fused_moe.fused_moe_decode(torch.zeros(9, 2048, device=DEV, dtype=BF), torch.zeros(2, 16, 2048, device=DEV,
                                    dtype=BF), torch.zeros(2, 2048, 8, device=DEV, dtype=BF),
                                    torch.zeros(9, 8, device=DEV, dtype=torch.long), torch.zeros(9, 8, device=DEV))
+
+
+def test_block_decode_graph_replays_follow_new_inputs(blk):
+    """The fused decode block captured once and replayed on new token rows: every replay equals an eager
+    call on the same rows."""
+    b, _ = blk
+    x = W.tokens(2, seed=130, device=DEV)
+    logits = torch.empty(2, 64, device=DEV)
+    ids = torch.empty(2, 7, device=DEV, dtype=torch.long)
+    wts = torch.empty(2, 7, device=DEV)
+    a_buf = torch.empty(14, 1408, device=DEV, dtype=BF)
+    out = torch.empty(2, 2048, device=DEV, dtype=BF)
+    ws = torch.empty(2, 2048, device=DEV, dtype=BF)
+
+    def step():
+        fused_moe.moe_block_decode(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=6, logits=logits,
+                                   ids=ids, wts=wts, a_buf=a_buf, out=out, workspace=ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for i in range(4):
+        x.copy_(W.tokens(2, seed=131 + i, device=DEV))
+        want, want_ids, _, _ = fused_moe.moe_block_decode(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"],
+                                                          top_k=6)
+        torch.cuda.synchronize()
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids, want_ids) and torch.equal(out, want), f"replay {i}"
