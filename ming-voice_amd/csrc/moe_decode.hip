@@ -42,7 +42,9 @@ struct DecodeArgs {
 };
 
 // Distinct experts of the batch. Lane p < P holds pair p's expert; returns the expert of distinct slot u
-// (or -1 when the batch has fewer distinct experts) and the mask of pairs routed to it.
+// (or -1 when the batch has fewer distinct experts) and the mask of pairs routed to it. Distinct experts
+// are enumerated in first-appearance order: the lowest remaining lane leads, and one ballot takes every
+// pair of its expert (one readlane + one ballot per distinct expert, no per-pair shuffles).
 __device__ __forceinline__ int distinct_expert(const DecodeArgs& a, int u, unsigned long long& pairs) {
   const int lane = lane_id();
   int64_t id = -1;
@@ -52,23 +54,19 @@ __device__ __forceinline__ int distinct_expert(const DecodeArgs& a, int u, unsig
     if (id < 0 || id >= a.E1) id = -1;
   }
   const int my = static_cast<int>(id);
-  bool first = my >= 0;
-  for (int q = 0; q < a.P; ++q) {
-    const int oq = __shfl(my, q, kWave);
-    if (q < lane && oq == my) first = false;
+  unsigned long long remaining = __ballot(my >= 0);
+  for (int i = 0; remaining; ++i) {
+    const int leader = __ffsll(static_cast<long long>(remaining)) - 1;
+    const int e = __builtin_amdgcn_readlane(my, leader);
+    const unsigned long long same = __ballot(my == e);
+    if (i == u) {
+      pairs = same;
+      return e;
+    }
+    remaining &= ~same;
   }
-  const unsigned long long fm = __ballot(first);
-  const unsigned long long below = lane == 0 ? 0ull : (fm & ((1ull << lane) - 1ull));
-  const int rank = __popcll(below);
-  const unsigned long long pick = __ballot(first && rank == u);
-  if (pick == 0ull) {
-    pairs = 0ull;
-    return -1;
-  }
-  const int src = __ffsll(static_cast<long long>(pick)) - 1;
-  const int e = __shfl(my, src, kWave);
-  pairs = __ballot(my == e);
-  return e;
+  pairs = 0ull;
+  return -1;
 }
 
 // 16-byte chunk c of a weight row holds CE elements; the matching activation chunk is CE bf16 values.
