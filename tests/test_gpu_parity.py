@@ -290,6 +290,16 @@ def test_moe_block_prefill_matches_unfused_and_oracle(blk, n, int8):
     close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
 
 
+def test_prefill_zipf_2048_int8_subset(blk):
+    """Hot experts of the Zipf batch on the int8 path: block pairs as 128-row tiles, odd last blocks alone."""
+    b, cpu = blk
+    x = W.tokens(2048, seed=91, device=DEV)
+    xn, ids, wts = _route_tokens(b, x, W.zipf_bias(device=DEV))
+    y = fused_moe.fused_moe_prefill(xn, b["q_gu"], b["q_d"], ids, wts, s_gu=b["s_gu"], s_d=b["s_d"])
+    sub = torch.randperm(2048, generator=torch.Generator().manual_seed(1))[:160]
+    close(y.cpu()[sub], _oracle_moe(cpu, xn[sub.to(DEV)], ids[sub.to(DEV)], wts[sub.to(DEV)], int8=True))
+
+
 def test_prefill_zipf_2048_subset_and_histogram(blk):
     b, cpu = blk
     x = W.tokens(2048, seed=90, device=DEV)
@@ -305,12 +315,13 @@ def test_prefill_zipf_2048_subset_and_histogram(blk):
 @pytest.mark.parametrize("int8", [False, True])
 def test_prefill_and_decode_ragged_shapes(int8):
     """Tails on every tiled dim: hidden 1536 (6 column tiles of 256), inter 208 (partial 128-column tile and a
-    partial 64-wide k slab), 129 expert slots (the Ming thinker's 128 + shared), top-8."""
+    partial 64-wide k slab), 129 expert slots (the Ming thinker's 128 + shared), top-8. 1100 tokens put
+    about 69 pairs on each expert: the 128-row tiles (block pairs) and the odd last blocks."""
     H, I, E, K = 1536, 208, 128, 8
     w_gu = W.normal((E + 1, 2 * I, H), 0.02, 130, DEV)
     w_d = W.normal((E + 1, H, I), 0.02, 131, DEV)
     g = torch.Generator().manual_seed(132)
-    for n in (3, 77):
+    for n in (3, 77, 1100):
         sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
         ids = torch.cat([sel, torch.full((n, 1), E)], 1).to(DEV)
         wts = torch.cat([torch.rand(n, K, generator=g), torch.ones(n, 1)], 1).to(DEV)
