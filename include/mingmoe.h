@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 2
+#define MM_ABI_VERSION 3
 
 /* status codes */
 #define MM_OK 0
@@ -199,6 +199,41 @@ int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride,
  * first and q divides by the rounded value). */
 int mm_quantize_rows_int8(const void* w, int w_dtype, int64_t rows, int64_t K, int64_t w_row_stride,
                           int8_t* q, int64_t q_row_stride, void* scale, int scale_dtype, void* stream);
+
+/* ---- Talker kernels (fast_talker.py). bf16 activations; latency-bound, a few KB to a few 100 KB per call. */
+
+/* Rotary attention over seq <= 8 tokens per (batch, head), for the Talker's DiT and aggregator blocks.
+ * Replaces fast_talker.rope_attn / _tiny_rope_attn (fast_talker.py:34-79).
+ * qkv bf16 [batch, seq, 3*dim] contiguous (q | k | v, head h at columns h*hd .. h*hd+hd-1 of each part);
+ * cos_t, sin_t fp32 [seq, hd/2] (one angle per interleaved pair); out bf16 [batch, seq, dim].
+ * Pair (x[2p], x[2p+1]) is rotated by angle p and rounded to bf16 for q and k; scores are scaled by
+ * 1/sqrt(hd); the softmax weights are rounded to bf16 before p . v. hd = dim/heads must be even, <= 256. */
+int mm_rope_attn(const void* qkv, int64_t batch, int64_t seq, int64_t dim, int heads, const float* cos_t,
+                 const float* sin_t, void* out, void* stream);
+
+/* Bytes of fp32 workspace mm_qwen_decode_attn needs: nh * ceil(max_len/64) * (hd + 2) * 4 (0 if invalid). */
+int64_t mm_decode_attn_workspace(int nh, int hd, int64_t max_len);
+
+/* Single-token GQA decode attention of the Talker's Qwen2 over its static KV cache.
+ * Replaces fast_talker._qwen_decode_attn (fast_talker.py:165-212, launched at :255-256).
+ * qkv bf16 [(nh + 2*nkv) * hd] (q heads, then k heads, then v heads); k_cache, v_cache bf16
+ * [nkv, max_len, hd] (one layer of StaticQwen2's cache, engine.py:1258-1259); pos: device scalar
+ * (MM_INT64 / MM_INT32), the position of this token; inv_freq fp32 [hd/2]; out bf16 [nh * hd].
+ * Rotary (rotate-half form, cos / sin of pos * inv_freq rounded to bf16) is applied to q and k, rounded to
+ * bf16; k and v are written into the caches at row pos; out = softmax(scale * q . K[0..pos]) . V[0..pos].
+ * A pos outside [0, max_len) writes nothing to the caches and sets the output to NaN.
+ * nh must be a multiple of nkv with nh/nkv <= 16; hd a multiple of 32 in [32, 256]; max_len <= 65536.
+ * workspace: at least mm_decode_attn_workspace(nh, hd, max_len) bytes of device memory, 16-byte aligned;
+ * its contents need no initialisation. Two kernels, both on `stream`. */
+int mm_qwen_decode_attn(const void* qkv, int nh, int nkv, int hd, void* k_cache, void* v_cache, int64_t max_len,
+                        const void* pos, int pos_dtype, const float* inv_freq, float scale, void* out,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out = bf16(bf16(silu(g)) * u) for rows of gu = [g | u], each 2*inter wide.
+ * Replaces fast_talker._silu_mul (fast_talker.py:215-222, launched at :259-260). gu, out bf16;
+ * rows <= 65535; row strides in elements. */
+int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stride, void* out,
+                int64_t out_row_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ MM_OK, MM_ERR_ARG, MM_ERR_HIP = 0, 1, 2
 MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -54,6 +54,11 @@ SIGNATURES = {
     "mm_small_linear": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64, _P, _F32, _P, _P, _I64, _P],
                         ctypes.c_int),
     "mm_quantize_rows_int8": ([_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P], ctypes.c_int),
+    "mm_rope_attn": ([_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
+    "mm_decode_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),
+    "mm_qwen_decode_attn": ([_P, _I32, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F32, _P, _P, _I64, _P],
+                            ctypes.c_int),
+    "mm_silu_mul": ([_P, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
 }
 
 _lib = None

@@ -1,0 +1,179 @@
+"""The Talker's per-token work on hand-written gfx950 HIP kernels (drop-in for the reference fast_talker.py).
+
+  rope_attn(qkv, cos, sin, heads)      interleaved-rotary attention over 2-3 tokens per (batch, head), the
+                                       DiT / aggregator blocks' attention (fast_talker.py:34-79)
+  qwen_decode_attn(qkv, k, v, pos, ...) single-token GQA decode attention over StaticQwen2's KV cache,
+                                       writing this token's k / v at `pos` (fast_talker.py:165-212)
+  silu_mul(gu, out=None)               bf16(bf16(silu(g)) * u) of the Qwen2 MLP (fast_talker.py:215-222)
+  FastQwen2Step                        the Talker LLM decode step built from small_linear and the kernels
+                                       above (fast_talker.py:225-262)
+
+Every op runs on torch's current stream, allocates only with torch (so it can be captured in a graph),
+and raises if the HIP library is missing: there is no CPU or Triton path.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+import _mingmoe as _mm
+from fastlinear import small_linear
+
+__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "FastQwen2Step", "decode_attn_workspace"]
+
+
+def rope_attn(qkv, cos, sin, heads):
+    """qkv [B, S, 3D] bf16 (q | k | v); cos, sin [S, HD/2] fp32 (one angle per interleaved pair, as
+    _rope_tables builds them). Returns the attention output [B, S, D] bf16 (fast_talker.py:72-79).
+    S <= 8; HD = D / heads even and <= 256."""
+    _mm.require_gpu(qkv, cos, sin)
+    if qkv.dim() != 3 or qkv.shape[-1] % 3:
+        raise ValueError(f"rope_attn: qkv must be [B, S, 3D] (got {tuple(qkv.shape)})")
+    B, S, D3 = qkv.shape
+    D = D3 // 3
+    if D % heads:
+        raise ValueError(f"rope_attn: dim {D} is not divisible by heads={heads}")
+    P = D // heads // 2
+    if qkv.dtype != torch.bfloat16:
+        raise ValueError(f"rope_attn: qkv must be bf16 (got {qkv.dtype})")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or t.numel() != S * P:
+            raise ValueError(f"rope_attn: {name} must be fp32 [S={S}, HD/2={P}] (got {t.dtype} {tuple(t.shape)})")
+    qkv = qkv if qkv.is_contiguous() else qkv.contiguous()
+    cos = cos if cos.is_contiguous() else cos.contiguous()
+    sin = sin if sin.is_contiguous() else sin.contiguous()
+    out = torch.empty(B, S, D, device=qkv.device, dtype=qkv.dtype)
+    lib = _mm.load()
+    with _mm.on_device(qkv):
+        _mm.check(lib.mm_rope_attn(_mm.ptr(qkv), B, S, D, int(heads), _mm.ptr(cos), _mm.ptr(sin), _mm.ptr(out),
+                                   _mm.stream_of(qkv)), "rope_attn")
+    return out
+
+
+def decode_attn_workspace(nh, hd, max_len, device):
+    """The fp32 workspace qwen_decode_attn needs (no initialisation needed); reusable across calls and layers
+    on one stream."""
+    n = _mm.load().mm_decode_attn_workspace(int(nh), int(hd), int(max_len))
+    if n <= 0:
+        raise ValueError(f"decode_attn_workspace: bad shape nh={nh} hd={hd} max_len={max_len}")
+    return torch.empty((n + 3) // 4, dtype=torch.float32, device=device)
+
+
+def qwen_decode_attn(qkv, k_cache, v_cache, pos, inv_freq, out, max_len, scale, nh, nkv, hd, workspace=None):
+    """One decode token of the Talker's Qwen2 attention (fast_talker.py:165-212, launched at :255-256).
+
+    qkv: [1, (nh + 2 nkv) hd] bf16 (the fused q | k | v projection); k_cache, v_cache: one layer of
+    StaticQwen2's cache, [1, nkv, max_len, hd] bf16, written at row pos; pos: [1] int64 (or int32) device
+    tensor; inv_freq: [hd/2] fp32; out: [1, nh hd] bf16 or None (allocated). Returns out.
+    A pos outside [0, max_len) leaves the caches untouched and gives NaN outputs."""
+    _mm.require_gpu(qkv, k_cache, v_cache, pos, inv_freq, out, workspace)
+    nh, nkv, hd, max_len = int(nh), int(nkv), int(hd), int(max_len)
+    if qkv.dtype != torch.bfloat16 or qkv.numel() != (nh + 2 * nkv) * hd or not qkv.is_contiguous():
+        raise ValueError(f"qwen_decode_attn: qkv must be contiguous bf16 with (nh + 2 nkv) hd = "
+                         f"{(nh + 2 * nkv) * hd} elements (got {qkv.dtype} {tuple(qkv.shape)})")
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if c.dtype != torch.bfloat16 or c.numel() != nkv * max_len * hd or not c.is_contiguous():
+            raise ValueError(f"qwen_decode_attn: {name} must be contiguous bf16 [nkv, max_len, hd] = "
+                             f"[{nkv}, {max_len}, {hd}] (got {c.dtype} {tuple(c.shape)})")
+    if pos.numel() != 1 or pos.dtype not in (torch.int64, torch.int32):
+        raise ValueError("qwen_decode_attn: pos must be a one-element int64 or int32 tensor")
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != hd // 2 or not inv_freq.is_contiguous():
+        raise ValueError(f"qwen_decode_attn: inv_freq must be contiguous fp32 [{hd // 2}]")
+    if out is None:
+        out = torch.empty(1, nh * hd, device=qkv.device, dtype=torch.bfloat16)
+    elif out.dtype != torch.bfloat16 or out.numel() != nh * hd or not out.is_contiguous():
+        raise ValueError(f"qwen_decode_attn: out must be contiguous bf16 with nh hd = {nh * hd} elements")
+    if workspace is None:
+        workspace = decode_attn_workspace(nh, hd, max_len, qkv.device)
+    lib = _mm.load()
+    with _mm.on_device(qkv):
+        _mm.check(lib.mm_qwen_decode_attn(_mm.ptr(qkv), nh, nkv, hd, _mm.ptr(k_cache), _mm.ptr(v_cache), max_len,
+                                          _mm.ptr(pos), _mm.dtype_code(pos), _mm.ptr(inv_freq), float(scale),
+                                          _mm.ptr(out), _mm.ptr(workspace),
+                                          workspace.numel() * workspace.element_size(), _mm.stream_of(qkv)),
+                  "qwen_decode_attn")
+    return out
+
+
+def silu_mul(gu, out=None):
+    """gu [..., 2I] bf16 = [g | u] -> bf16(bf16(silu(g)) * u) [..., I] (fast_talker.py:215-222)."""
+    _mm.require_gpu(gu, out)
+    if gu.dtype != torch.bfloat16 or gu.shape[-1] % 2:
+        raise ValueError(f"silu_mul: gu must be bf16 with an even last dim (got {gu.dtype} {tuple(gu.shape)})")
+    I = gu.shape[-1] // 2
+    g2 = gu.reshape(-1, 2 * I)
+    if g2.stride(-1) != 1:
+        g2 = g2.contiguous()
+    if out is None:
+        out = torch.empty(*gu.shape[:-1], I, device=gu.device, dtype=gu.dtype)
+    o2 = out.reshape(-1, I)
+    if o2.shape[0] != g2.shape[0] or out.dtype != torch.bfloat16 or o2.stride(-1) != 1 or o2.data_ptr() != out.data_ptr():
+        raise ValueError("silu_mul: out must be bf16 [..., I] with the rows of gu and a contiguous last dim")
+    lib = _mm.load()
+    with _mm.on_device(gu):
+        _mm.check(lib.mm_silu_mul(_mm.ptr(g2), g2.shape[0], I, g2.stride(0), _mm.ptr(o2), o2.stride(0),
+                                  _mm.stream_of(gu)), "silu_mul")
+    return out
+
+
+def _fuse(mods, attr="weight"):
+    """One contiguous tensor holding the `attr` of each Linear in mods, stacked along dim 0; each module's
+    parameter becomes a view into it, so the weights are held once (fast_talker.py:21-31)."""
+    parts = [getattr(m, attr) for m in mods]
+    fused = torch.cat([p.detach() for p in parts], dim=0).contiguous()
+    row = 0
+    for p in parts:
+        p.data = fused[row:row + p.shape[0]]
+        row += p.shape[0]
+    return fused
+
+
+class FastQwen2Step:
+    """Single-token decode of the Talker's Qwen2 over StaticQwen2's static KV cache (fast_talker.py:225-262).
+
+    Per layer: small_linear(RMSNorm -> fused q|k|v + bias), qwen_decode_attn (rotary, cache write at pos,
+    attention), small_linear(o_proj + residual), small_linear(RMSNorm -> fused gate|up), silu_mul,
+    small_linear(down_proj + residual); the final norm is torch's rms_norm as in the reference."""
+
+    def __init__(self, static_llm):
+        m = static_llm.m
+        self.sl = static_llm
+        self.nh, self.nkv, self.hd = static_llm.nh, static_llm.nkv, static_llm.hd
+        self.scale = 1.0 / math.sqrt(self.hd)
+        self.layers = []
+        for layer in m.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            self.layers.append({
+                "wqkv": _fuse([at.q_proj, at.k_proj, at.v_proj]),
+                "bqkv": _fuse([at.q_proj, at.k_proj, at.v_proj], "bias"),
+                "wo": at.o_proj.weight,
+                "wgu": _fuse([mlp.gate_proj, mlp.up_proj]),
+                "wd": mlp.down_proj.weight,
+                "n1": (layer.input_layernorm.weight, layer.input_layernorm.variance_epsilon),
+                "n2": (layer.post_attention_layernorm.weight, layer.post_attention_layernorm.variance_epsilon),
+            })
+        self.norm = (m.norm.weight, m.norm.variance_epsilon)
+        self._ws = {}
+
+    def _workspace(self, device):
+        ws = self._ws.get(device)
+        if ws is None:
+            ws = decode_attn_workspace(self.nh, self.hd, self.sl.max_len, device)
+            self._ws[device] = ws
+        return ws
+
+    def __call__(self, x, pos):
+        """x: [1, 1, H] input embedding; pos: [1] long device tensor (position of x).
+        Returns the final-normed hidden state [1, 1, H]."""
+        H = x.shape[-1]
+        h = x.reshape(1, H)
+        sl = self.sl
+        ws = self._workspace(h.device)
+        for i, L in enumerate(self.layers):
+            qkv = small_linear(h, L["wqkv"], L["bqkv"], norm=L["n1"])
+            a = qwen_decode_attn(qkv, sl.k[i], sl.v[i], pos, sl.inv_freq, None, sl.max_len, self.scale, self.nh,
+                                 self.nkv, self.hd, workspace=ws)
+            h = small_linear(a, L["wo"], None, residual=h)
+            act = silu_mul(small_linear(h, L["wgu"], None, norm=L["n2"]))
+            h = small_linear(act, L["wd"], None, residual=h)
+        return F.rms_norm(h, (H,), self.norm[0], self.norm[1]).reshape(1, 1, H)

@@ -1,0 +1,105 @@
+"""CPU oracle of the Talker's three small kernels — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as
+the checker (or the timed CPU baseline); the product path (ming-voice_amd/) never calls it.
+
+It restates in plain torch (fp32 on the CPU) the algorithm of fast_talker.py's Triton kernels, with their
+rounding points. How each function is pinned (closed forms, the unfused torch path of engine.py's
+StaticQwen2, complex-number rotation, torch's scaled_dot_product_attention and silu) is in
+tests/test_talker_oracle.py.
+"""
+import math
+
+import torch
+
+BF16 = torch.bfloat16
+
+
+def _bf(t):
+    """Round an fp32 tensor through bf16 (round to nearest even) and back to fp32."""
+    return t.to(BF16).float()
+
+
+def rope_attn(qkv, cos, sin, heads):
+    """fast_talker.py:34-79. qkv [B, S, 3D] bf16; cos, sin [S, HD/2] fp32 (one angle per pair).
+    Interleaved pairs (x[2p], x[2p+1]) -> (xe c - xo s, xo c + xe s), rounded to bf16 for q and k (:53-57);
+    scores = (sum over pairs of qe'ke' + qo'ko') * HD^-1/2 (:58-59); softmax over the S keys (:60-63); p rounded
+    to bf16 (:64); out = p . v rounded to bf16 (:65-69). Returns [B, S, D] bf16."""
+    B, S, D3 = qkv.shape
+    D = D3 // 3
+    HD = D // heads
+    P = HD // 2
+    x = qkv.float().reshape(B, S, 3, heads, P, 2)
+    c = cos.float()[None, :, None, :]
+    s = sin.float()[None, :, None, :]
+
+    def rot(t):
+        e, o = t[..., 0], t[..., 1]
+        return _bf(e * c - o * s), _bf(o * c + e * s)
+
+    qe, qo = rot(x[:, :, 0])
+    ke, ko = rot(x[:, :, 1])
+    ve, vo = x[:, :, 2, ..., 0], x[:, :, 2, ..., 1]
+    # [B, heads, S, P]
+    qe, qo, ke, ko, ve, vo = (t.permute(0, 2, 1, 3) for t in (qe, qo, ke, ko, ve, vo))
+    sc = (qe @ ke.transpose(-1, -2) + qo @ ko.transpose(-1, -2)) * (1.0 / math.sqrt(HD))
+    p = torch.softmax(sc, dim=-1)
+    p = _bf(p)
+    oe, oo = p @ ve, p @ vo
+    out = torch.stack([oe, oo], dim=-1)  # [B, heads, S, P, 2]
+    return out.permute(0, 2, 1, 3, 4).reshape(B, S, D).to(BF16)
+
+
+def _rotate_half_fused(x, c, s):
+    """fast_talker.py:176-187: x'[d] = x[d] c[d] + sign(d) x[(d + HD/2) % HD] s[d], sign = -1 below HD/2."""
+    HD = x.shape[-1]
+    half = HD // 2
+    partner = (torch.arange(HD) + half) % HD
+    sign = torch.where(torch.arange(HD) < half, -1.0, 1.0)
+    return x * c + sign * x[..., partner] * s
+
+
+def qwen_decode_attn(qkv, k_cache, v_cache, pos, inv_freq, scale, nh, nkv, hd, block=64):
+    """fast_talker.py:165-212 for one token. qkv [(nh + 2 nkv) hd] bf16; k_cache, v_cache [nkv, max_len, hd]
+    bf16 (modified in place at row pos, :191-193); pos int; inv_freq [hd/2] fp32.
+    Angles f = pos * inv_freq[d % (hd/2)] with cos / sin rounded to bf16 (:178-180); q and k rotated and
+    rounded to bf16 (:184-187); online softmax in fp32 starting from the current position (m = q.k scale,
+    l = 1, acc = v, :195-197) and walking the cached prefix [0, pos) in blocks of `block` (:199-211).
+    Returns out [nh * hd] bf16."""
+    G = nh // nkv
+    half = hd // 2
+    d = torch.arange(hd)
+    f = torch.tensor(float(pos), dtype=torch.float32) * inv_freq.float()[d % half]
+    c = _bf(torch.cos(f))
+    s = _bf(torch.sin(f))
+    x = qkv.float()
+    q = _bf(_rotate_half_fused(x[: nh * hd].reshape(nh, hd), c, s))
+    k = _bf(_rotate_half_fused(x[nh * hd:(nh + nkv) * hd].reshape(nkv, hd), c, s))
+    v = x[(nh + nkv) * hd:(nh + 2 * nkv) * hd].reshape(nkv, hd)
+    k_cache[:, pos] = k.to(BF16)
+    v_cache[:, pos] = v.to(BF16)
+    kvh = torch.arange(nh) // G
+    kq, vq = k[kvh], v[kvh]  # [nh, hd]: each query head's own k / v
+    m = (q * kq).sum(-1) * scale
+    l = torch.ones(nh)
+    acc = vq.clone()
+    K = k_cache.float()[kvh]  # [nh, max_len, hd]
+    V = v_cache.float()[kvh]
+    for start in range(0, pos, block):
+        stop = min(start + block, pos)
+        sc = (K[:, start:stop] * q[:, None, :]).sum(-1) * scale  # [nh, n]
+        m_new = torch.maximum(m, sc.max(-1).values)
+        alpha = torch.exp(m - m_new)
+        p = torch.exp(sc - m_new[:, None])
+        acc = acc * alpha[:, None] + (p[:, :, None] * V[:, start:stop]).sum(1)
+        l = l * alpha + p.sum(-1)
+        m = m_new
+    return (acc / l[:, None]).reshape(-1).to(BF16)
+
+
+def silu_mul(gu, inter):
+    """fast_talker.py:215-222: g, u = gu[..., :I], gu[..., I:2I]; out = bf16(bf16(g / (1 + exp(-g))) * u)."""
+    g = gu[..., :inter].float()
+    u = gu[..., inter:2 * inter].float()
+    g = _bf(g / (1.0 + torch.exp(-g)))
+    return (g * u).to(BF16)

@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "mingmoe.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(mm_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t)\s+(mm_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_expected_entry_points():
@@ -76,6 +76,19 @@ def test_argument_validation_reports_messages():
                                                 32, None, 0, P, P, P, 2048, 0, None))
     assert "M=17" in _err(lib.mm_small_linear(P, 17, 64, 64, P, 64, 64, None, 0, None, 0, None, 0.0, None, P, 64, None))
     assert "scale dtype" in _err(lib.mm_quantize_rows_int8(P, mm.MM_BF16, 4, 64, 64, P, 64, P, mm.MM_INT8, None))
+    assert "seq=9" in _err(lib.mm_rope_attn(P, 2, 9, 1024, 16, P, P, P, None))
+    assert "head dim 65" in _err(lib.mm_rope_attn(P, 2, 3, 1040, 16, P, P, P, None))
+    assert "head dim 48" in _err(lib.mm_qwen_decode_attn(P, 8, 2, 48, P, P, 64, P, mm.MM_INT64, P, 0.1, P, P, 1 << 20,
+                                                         None))
+    assert "at most 16" in _err(lib.mm_qwen_decode_attn(P, 34, 2, 64, P, P, 64, P, mm.MM_INT64, P, 0.1, P, P, 1 << 20,
+                                                        None))
+    need = lib.mm_decode_attn_workspace(14, 64, 1024)
+    assert need == 14 * 16 * (64 + 2) * 4 and lib.mm_decode_attn_workspace(0, 64, 1024) == 0
+    assert "workspace needs" in _err(lib.mm_qwen_decode_attn(P, 14, 2, 64, P, P, 1024, P, mm.MM_INT64, P, 0.1, P, P,
+                                                             need - 4, None))
+    assert "int32 or int64" in _err(lib.mm_qwen_decode_attn(P, 14, 2, 64, P, P, 1024, P, mm.MM_FP32, P, 0.1, P, P,
+                                                            need, None))
+    assert "row stride" in _err(lib.mm_silu_mul(P, 1, 4864, 4864, P, 4864, None))
 
 
 def test_wrappers_refuse_cpu_tensors():
@@ -91,16 +104,23 @@ def test_wrappers_refuse_cpu_tensors():
         fastlinear.small_linear(x, torch.zeros(8, 64, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="no CPU path"):
         fused_moe._align_blocks(torch.zeros(7, dtype=torch.long), 65, 64)
+    import fast_talker
+    with pytest.raises(ValueError, match="no CPU path"):
+        fast_talker.silu_mul(torch.zeros(1, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="no CPU path"):
+        fast_talker.rope_attn(torch.zeros(1, 3, 192, dtype=torch.bfloat16), torch.ones(3, 16), torch.zeros(3, 16), 2)
 
 
 def test_reference_module_surface_is_kept():
+    import fast_talker
     import fused_moe
     import fused_ops
     import fastlinear
     for mod, names in ((fused_moe, ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "_align_blocks",
                                     "CFG", "GCFG", "_graph_us"]),
                        (fused_ops, ["rms_norm", "moe_route"]),
-                       (fastlinear, ["small_linear", "save_cache", "_graph_time", "CACHE_FILE", "_best"])):
+                       (fastlinear, ["small_linear", "save_cache", "_graph_time", "CACHE_FILE", "_best"]),
+                       (fast_talker, ["rope_attn", "_fuse", "FastQwen2Step"])):
         for n in names:
             assert hasattr(mod, n), f"{mod.__name__}.{n}"
     fastlinear.save_cache()  # nothing tuned: writes nothing

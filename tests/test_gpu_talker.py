@@ -1,0 +1,205 @@
+"""GPU parity of the Talker kernels (rope_attn, qwen_decode_attn, silu_mul) against the CPU oracle.
+
+bf16 outputs must match within rtol 2e-2 / atol 1e-2; cache rows written by the decode attention within
+one bf16 ulp (k: fp32 rotation rounded once on both sides) or bit-exact (v is copied); cache rows other
+than pos must be untouched. The Talker LLM shape is Qwen2-0.5B-like (14 query heads, 2 KV heads,
+head dim 64, a 1024-position cache); the DiT / aggregator attention is 16 heads of 64 over 3 / 2 tokens."""
+import math
+
+import pytest
+import torch
+
+import fast_talker as FT
+from oracle import talker_oracle as T
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+RTOL, ATOL = 2e-2, 1e-2
+
+
+def close(got, want, rtol=RTOL, atol=ATOL):
+    torch.testing.assert_close(got.float().cpu(), want.float().cpu(), rtol=rtol, atol=atol)
+
+
+# -------------------------------------------------------------------------------------------- rope_attn
+
+@pytest.mark.parametrize("B,S,D,heads", [(2, 3, 1024, 16), (1, 2, 1024, 16), (2, 1, 256, 4), (3, 5, 384, 3),
+                                         (2, 8, 512, 8), (1, 4, 1536, 6), (2, 3, 96, 3), (4, 6, 160, 2)])
+def test_rope_attn(B, S, D, heads):
+    print(f"rope_attn B={B} S={S} D={D} heads={heads}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + S)
+    qkv = torch.randn(B, S, 3 * D, generator=g).to(BF)
+    ang = torch.rand(S, D // heads // 2, generator=g) * 2 * math.pi
+    cos, sin = ang.cos(), ang.sin()
+    got = FT.rope_attn(qkv.to(DEV), cos.to(DEV), sin.to(DEV), heads)
+    torch.cuda.synchronize()
+    want = T.rope_attn(qkv, cos, sin, heads)
+    close(got, want)
+    if S == 1:
+        assert torch.equal(got.cpu(), qkv[:, :, 2 * D:])
+
+
+def test_rope_attn_rejects_long_sequences():
+    qkv = torch.zeros(1, 9, 3 * 64, device=DEV, dtype=BF)
+    cs = torch.zeros(9, 16, device=DEV)
+    with pytest.raises(ValueError, match="seq"):
+        FT.rope_attn(qkv, cs, cs, 2)
+
+
+# ------------------------------------------------------------------------------------- decode attention
+
+def _decode_inputs(nh, nkv, hd, max_len, seed, theta=1e6):
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn((nh + 2 * nkv) * hd, generator=g).to(BF)
+    kc = torch.randn(1, nkv, max_len, hd, generator=g).to(BF)
+    vc = torch.randn(1, nkv, max_len, hd, generator=g).to(BF)
+    inv_freq = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    return qkv, kc, vc, inv_freq
+
+
+def _run_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, pos_dtype=torch.int64):
+    max_len = kc.shape[2]
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    out = FT.qwen_decode_attn(qkv.to(DEV)[None], kd, vd, torch.tensor([pos], device=DEV, dtype=pos_dtype),
+                              inv_freq.to(DEV), None, max_len, 1.0 / math.sqrt(hd), nh, nkv, hd)
+    torch.cuda.synchronize()
+    return out.cpu().reshape(-1), kd.cpu(), vd.cpu()
+
+
+def _check_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, got, kd, vd):
+    kw, vw = kc[0].clone(), vc[0].clone()
+    want = T.qwen_decode_attn(qkv, kw, vw, pos, inv_freq, 1.0 / math.sqrt(hd), nh, nkv, hd)
+    close(got, want)
+    torch.testing.assert_close(kd[0, :, pos].float(), kw[:, pos].float(), rtol=2 ** -7, atol=0)
+    assert torch.equal(vd[0, :, pos], vw[:, pos])
+    others = torch.ones(kc.shape[2], dtype=torch.bool)
+    others[pos] = False
+    assert torch.equal(kd[0][:, others], kc[0][:, others]) and torch.equal(vd[0][:, others], vc[0][:, others])
+
+
+@pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 500, 1023])
+def test_decode_attn_talker_shape(pos):
+    nh, nkv, hd, max_len = 14, 2, 64, 1024
+    print(f"decode_attn nh={nh} nkv={nkv} hd={hd} max_len={max_len} pos={pos}", flush=True)
+    qkv, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 20 + pos)
+    got, kd, vd = _run_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd)
+    _check_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, got, kd, vd)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_len,pos", [(16, 16, 128, 200, 130), (16, 1, 32, 100, 99),
+                                                   (12, 2, 128, 4096, 4000), (8, 4, 256, 300, 257),
+                                                   (6, 2, 96, 129, 128), (7, 7, 64, 1, 0)])
+def test_decode_attn_shapes(nh, nkv, hd, max_len, pos):
+    print(f"decode_attn nh={nh} nkv={nkv} hd={hd} max_len={max_len} pos={pos}", flush=True)
+    qkv, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 40 + hd)
+    got, kd, vd = _run_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, pos_dtype=torch.int32)
+    _check_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, got, kd, vd)
+
+
+def test_decode_attn_consecutive_steps_fill_the_cache():
+    """Four decode steps at positions T..T+3 on one cache (the pattern of the reference's
+    dev/test_fast_llm.py): each step reads the rows the previous steps wrote."""
+    nh, nkv, hd, max_len, T0 = 14, 2, 64, 256, 97
+    _, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 60)
+    kw, vw = kc[0].clone(), vc[0].clone()
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    inv_d = inv_freq.to(DEV)
+    pos = torch.empty(1, device=DEV, dtype=torch.long)
+    ws = FT.decode_attn_workspace(nh, hd, max_len, DEV)
+    g = torch.Generator().manual_seed(61)
+    for j in range(4):
+        qkv = torch.randn((nh + 2 * nkv) * hd, generator=g).to(BF)
+        pos.fill_(T0 + j)
+        got = FT.qwen_decode_attn(qkv.to(DEV), kd, vd, pos, inv_d, None, max_len, 0.125, nh, nkv, hd, workspace=ws)
+        want = T.qwen_decode_attn(qkv, kw, vw, T0 + j, inv_freq, 0.125, nh, nkv, hd)
+        close(got.reshape(-1), want)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(kd[0].float().cpu(), kw.float(), rtol=2 ** -7, atol=0)
+    assert torch.equal(vd[0].cpu(), vw)
+
+
+def test_decode_attn_position_out_of_range_gives_nan_and_leaves_cache():
+    nh, nkv, hd, max_len = 14, 2, 64, 128
+    qkv, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 70)
+    for bad in (max_len, -1):
+        got, kd, vd = _run_decode(qkv, kc, vc, bad, inv_freq, nh, nkv, hd)
+        assert torch.isnan(got.float()).all()
+        assert torch.equal(kd, kc) and torch.equal(vd, vc)
+
+
+def test_decode_attn_graph_replays_follow_position():
+    """Captured once, replayed with a new pos and new qkv each time (the Talker replays its decode step in a
+    graph): every replay matches the oracle on the cache state it sees."""
+    nh, nkv, hd, max_len = 14, 2, 64, 512
+    _, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 80)
+    kw, vw = kc[0].clone(), vc[0].clone()
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    inv_d = inv_freq.to(DEV)
+    qkv = torch.zeros((nh + 2 * nkv) * hd, device=DEV, dtype=BF)
+    pos = torch.zeros(1, device=DEV, dtype=torch.long)
+    out = torch.empty(1, nh * hd, device=DEV, dtype=BF)
+    ws = FT.decode_attn_workspace(nh, hd, max_len, DEV)
+
+    def step():
+        FT.qwen_decode_attn(qkv, kd, vd, pos, inv_d, out, max_len, 0.125, nh, nkv, hd, workspace=ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # eager warm-up (writes row 0 of the cache; restored below)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step()
+    torch.cuda.synchronize()
+    kd.copy_(kc)
+    vd.copy_(vc)
+    g = torch.Generator().manual_seed(81)
+    for j, p in enumerate((5, 6, 64, 300, 301)):
+        x = torch.randn((nh + 2 * nkv) * hd, generator=g).to(BF)
+        qkv.copy_(x)
+        pos.fill_(p)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = T.qwen_decode_attn(x, kw, vw, p, inv_freq, 0.125, nh, nkv, hd)
+        close(out.reshape(-1), want)
+    torch.testing.assert_close(kd[0].float().cpu(), kw.float(), rtol=2 ** -7, atol=0)
+
+
+def test_decode_attn_rejects_bad_shapes():
+    z = torch.zeros(1024, device=DEV, dtype=BF)
+    cache = torch.zeros(1, 2, 8, 48, device=DEV, dtype=BF)
+    pos = torch.zeros(1, device=DEV, dtype=torch.long)
+    with pytest.raises(ValueError, match="head dim"):
+        FT.qwen_decode_attn(z[: (4 + 4) * 48], cache, cache, pos, torch.zeros(24, device=DEV), None, 8, 0.1, 4, 2, 48)
+    cache32 = torch.zeros(1, 2, 8, 32, device=DEV, dtype=BF)
+    with pytest.raises(ValueError, match="pos"):
+        FT.qwen_decode_attn(z[:512], cache32, cache32, pos.float(), torch.zeros(16, device=DEV), None, 8, 0.1, 12, 2,
+                            32)
+
+
+# --------------------------------------------------------------------------------------------- silu_mul
+
+@pytest.mark.parametrize("rows,I", [(1, 4864), (3, 4864), (1, 100), (2, 8), (1, 1), (4, 2816)])
+def test_silu_mul(rows, I):
+    g = torch.Generator().manual_seed(rows * 7 + I)
+    gu = (torch.randn(rows, 2 * I, generator=g) * 3).to(BF)
+    got = FT.silu_mul(gu.to(DEV)).cpu()
+    want = T.silu_mul(gu, I)
+    torch.testing.assert_close(got.float(), want.float(), rtol=2 ** -7, atol=0)
+    assert (got == want).float().mean() > 0.99
+
+
+def test_silu_mul_strided_rows_and_out():
+    g = torch.Generator().manual_seed(5)
+    big = (torch.randn(3, 2 * 4864 + 64, generator=g) * 3).to(BF).to(DEV)
+    gu = big[:, : 2 * 4864]
+    out = torch.empty(3, 4864 + 8, device=DEV, dtype=BF)
+    res = FT.silu_mul(gu, out[:, :4864])
+    torch.cuda.synchronize()
+    torch.testing.assert_close(res.float().cpu(), T.silu_mul(gu.cpu(), 4864).float(), rtol=2 ** -7, atol=0)
+    assert res.data_ptr() == out.data_ptr()
