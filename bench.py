@@ -9,7 +9,8 @@ combine + residual, replayed from one hipGraph. `value` is tokens/s over exactly
 
 Also measured and reported under "extra": decode of 1 token (bf16) as a hipGraph step and per kernel,
 int8 decode at batch 1/2/4/8, the 2048-token Zipf prefill, and the full 28-layer synthetic decode step
-(+ LM head) in one hipGraph. The roofline of the dominant kernel (prefill gate/up) is its algorithmic
+(+ LM head) in one hipGraph, and the Talker path (a 24-layer Qwen2-0.5B-shaped LLM decode step and its
+rotary / decode attention and silu_mul kernels). The roofline of the dominant kernel (prefill gate/up) is its algorithmic
 bytes over its average duration from HIP events on its own stream; the CPU baseline is the oracle's
 torch path on a bounded sample of the same workload on this host.
 """
@@ -41,7 +42,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra workloads to run (decode,int8,zipf,full)")
+    ap.add_argument("--only", default="", help="comma list of extra workloads to run (decode,int8,zipf,full,talker)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 counter passes (traffic = null)")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
@@ -337,6 +338,51 @@ def full_decode_metrics(stream, layers=28):
             "moe_TBs": moe_layer_bytes * layers / moe_ms / 1e9}
 
 
+# ------------------------------------------------------------------------------------------- Talker path
+
+def talker_metrics(stream, layers=24, max_len=1024, pos=512):
+    """The Talker's per-token work on the HIP kernels: one decode step of a Qwen2-0.5B-shaped Talker LLM
+    (FastQwen2Step: 24 layers, hidden 896, 14 query / 2 KV heads of 64, intermediate 4864) at position 512
+    of a 1024-position cache, replayed from one hipGraph; and per kernel (20 launches in one graph): the decode
+    attention at that position, the rotary attention of a DiT block (2 x 3 tokens) and of an aggregator
+    block (1 x 2 tokens), 16 heads of 64, and silu_mul over 4864."""
+    import fast_talker as FT
+    import workloads as W
+    dev = "cuda"
+    llm = W.TalkerLLM(layers=layers, max_len=max_len, seed=3000, device=dev)
+    llm.fill_cache(pos, seed=3001)
+    fs = FT.FastQwen2Step(llm)
+    x = W.normal((1, 1, W.TALKER_HIDDEN), 0.1, 3002, dev)
+    p = torch.tensor([pos], device=dev)
+    g = graph_of(lambda: fs(x, p), stream)  # every replay rewrites cache row pos with the same values
+    step_ms = time_graph(g, stream, 20)
+    nh, nkv, hd = llm.nh, llm.nkv, llm.hd
+    qkv = W.normal((1, (nh + 2 * nkv) * hd), 1.0, 3003, dev)
+    out = torch.empty(1, nh * hd, device=dev, dtype=torch.bfloat16)
+    ws = FT.decode_attn_workspace(nh, hd, max_len, dev)
+    kc, vc = llm.k[0], llm.v[0]
+    attn_ms = kernel_ms(lambda: FT.qwen_decode_attn(qkv, kc, vc, p, llm.inv_freq, out, max_len, hd ** -0.5, nh,
+                                                    nkv, hd, workspace=ws), stream)
+    rope = {}
+    for name, (B, S) in (("dit", (2, 3)), ("aggregator", (1, 2))):
+        q = W.normal((B, S, 3 * 1024), 1.0, 3004 + S, dev)
+        ang = torch.rand(S, 32, device=dev) * 6.283
+        c, s_ = ang.cos().contiguous(), ang.sin().contiguous()
+        rope[name] = kernel_ms(lambda: FT.rope_attn(q, c, s_, 16), stream) * 1e3
+    gu = W.normal((1, 2 * W.TALKER_INTER), 1.0, 3006, dev)
+    act = torch.empty(1, W.TALKER_INTER, device=dev, dtype=torch.bfloat16)
+    silu_ms = kernel_ms(lambda: FT.silu_mul(gu, act), stream)
+    H, I = W.TALKER_HIDDEN, W.TALKER_INTER
+    w_bytes = layers * ((nh + 2 * nkv) * hd * H + H * nh * hd + 2 * I * H + H * I) * 2
+    kv_bytes = 2 * nkv * (pos + 1) * hd * 2
+    del g, fs, llm
+    return {"layers": layers, "pos": pos, "max_len": max_len, "step_us": step_ms * 1e3,
+            "step_bytes": w_bytes + layers * kv_bytes, "step_TBs": (w_bytes + layers * kv_bytes) / step_ms / 1e9,
+            "decode_attn_us": attn_ms * 1e3, "decode_attn_kv_bytes": kv_bytes,
+            "rope_attn_dit_us": rope["dit"], "rope_attn_aggregator_us": rope["aggregator"],
+            "silu_mul_us": silu_ms * 1e3}
+
+
 # -------------------------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(b, bias, n_sample=64, reps=2):
@@ -411,6 +457,10 @@ def main():
         torch.cuda.empty_cache()
         extra["full_decode_28l"] = full_decode_metrics(stream)
         log(f"[bench] full decode: {extra['full_decode_28l']}")
+    if want("talker"):
+        torch.cuda.empty_cache()
+        extra["talker"] = talker_metrics(stream)
+        log(f"[bench] talker: {extra['talker']}")
     gu_s = head["gate_up_us"] * 1e-6
     achieved = head["gate_up_bytes"] / gu_s / 1e9
     traffic = None

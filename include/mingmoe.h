@@ -185,12 +185,22 @@ int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, 
  * points of its epilogue: bf16 before the activation and before the residual add.
  * x, w, b, residual, norm_g, y: bf16. norm_g (optional): RMSNorm prologue with norm_eps,
  * x -> bf16(bf16(x * rstd) * g). b, residual, norm_g may be NULL. act: MM_ACT_*.
- * xn_buf: bf16 scratch [M, K] used when a norm prologue is given (may be NULL otherwise). */
+ * xn_buf: bf16 scratch [M, K], used only when a norm prologue is given and K > 8192 (may be NULL otherwise);
+ * shorter rows get the norm fused into the GEMV. */
 int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride,
                     const void* w, int64_t N, int64_t w_row_stride,
                     const void* b, int act, const void* residual, int64_t res_row_stride,
                     const void* norm_g, float norm_eps, void* xn_buf,
                     void* y, int64_t y_row_stride, void* stream);
+
+/* act = silu_mul(small_linear(norm?(x), W)) in one kernel: W [2*inter, K] holds the gate rows then the up
+ * rows; y[:, p] = bf16(bf16(silu(g_p)) * u_p) with g_p, u_p the bf16-rounded projections of rows p and
+ * inter + p, so the result equals small_linear followed by silu_mul bit for bit. No counterpart in the
+ * reference: it fuses fast_talker.py:258-260 (gate|up small_linear, _silu_mul) for callers that own the
+ * layer loop. x, w, norm_g, y: bf16; M <= 16; K <= 8192, a multiple of 8; norm_g may be NULL. */
+int mm_small_linear_glu(const void* x, int64_t M, int64_t K, int64_t x_row_stride, const void* w, int64_t inter,
+                        int64_t w_row_stride, const void* norm_g, float norm_eps, void* y, int64_t y_row_stride,
+                        void* stream);
 
 /* Symmetric per-row int8: amax = max(max|w|, 1e-8); scale = amax / 127;
  * q = clamp(round_half_even(w / scale), -127, 127).

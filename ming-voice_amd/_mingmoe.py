@@ -53,6 +53,7 @@ SIGNATURES = {
                               _I64, _P], ctypes.c_int),
     "mm_small_linear": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _I64, _P, _F32, _P, _P, _I64, _P],
                         ctypes.c_int),
+    "mm_small_linear_glu": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _I64, _P], ctypes.c_int),
     "mm_quantize_rows_int8": ([_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P], ctypes.c_int),
     "mm_rope_attn": ([_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
     "mm_decode_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),

@@ -1,7 +1,10 @@
 // Small-M linear, M <= 16 (fastlinear.py:123-174): y = act(norm?(x) . W^T + b) [+ residual].
-// HBM-bound GEMV: each wave streams weight rows with 16-byte loads, the activation rows are re-read from
-// the L1/L2 caches. The optional RMSNorm prologue runs first as its own pass into a bf16 scratch buffer,
-// with the rounding points of the reference (x -> bf16(x * rstd) -> * g -> bf16, rstd = 1/sqrt(ss/K + eps)).
+// HBM-bound GEMV, latency-bound at decode sizes (a few MB per call). For rows of up to 1024 16-byte chunks
+// (K <= 8192) one pass covers the row: a wave shares each of its rows across its 64 lanes and issues all
+// weight loads of its rows at once, so it waits for memory once; the activation chunks come from the L1/L2
+// caches. The optional RMSNorm prologue is fused there: the lanes of a wave hold the whole activation row,
+// so they sum its squares themselves, with the rounding points of the reference (x -> bf16(x * rstd) -> * g
+// -> bf16, rstd = 1/sqrt(ss/K + eps)). Longer rows take several passes and run the norm as its own kernel.
 #include "mm_common.h"
 
 namespace {
@@ -61,7 +64,120 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
-// Each wave computes GPW = 64/LPR rows at a time, R times; LPR lanes share one row, NC chunks per lane.
+__device__ __forceinline__ void epilogue(const LinArgs& a, int m, int64_t n, float v) {
+  if (a.b) v += bf16_to_f32(a.b[n]);
+  v = apply_act(v, a.act);
+  if (a.res) v = round_bf16(v) + bf16_to_f32(a.res[m * a.rs + n]);
+  a.y[m * a.ys + n] = f32_to_bf16(v);
+}
+
+// Elementwise bf16(bf16(x * rstd) * g) of one 8-element chunk (the norm prologue's rounding points).
+__device__ __forceinline__ uint4 norm_chunk(uint4 xv, uint4 gv, float rstd) {
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  uint32_t r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float y0 = round_bf16(__uint_as_float(xw[i] << 16) * rstd) * __uint_as_float(gw[i] << 16);
+    const float y1 = round_bf16(__uint_as_float(xw[i] & 0xffff0000u) * rstd) * __uint_as_float(gw[i] & 0xffff0000u);
+    r[i] = static_cast<uint32_t>(f32_to_bf16(y0)) | (static_cast<uint32_t>(f32_to_bf16(y1)) << 16);
+  }
+  return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+__device__ __forceinline__ float sumsq8(uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a0 = __uint_as_float(w[i] << 16), a1 = __uint_as_float(w[i] & 0xffff0000u);
+    s = fmaf(a0, a0, s);
+    s = fmaf(a1, a1, s);
+  }
+  return s;
+}
+
+// One pass per row (64 * NC >= K / 8): the 64 lanes of a wave share a row, lane s holding chunks
+// s + 64 j (j < NC), and a wave computes R rows whose R * NC weight loads per lane are all issued at once,
+// so it waits for memory once. Chunk indices past the row are clamped to its last chunk (a valid address)
+// and their products dropped by a select. The activation chunks of a lane are loaded once per token row
+// and reused for the R weight rows; with NORM the wave sums their squares (the whole row passes through
+// its lanes) and normalises them in place, 8 * NC elements per lane.
+// GLU (R = 2): the wave's two rows are gate row p and up row p + N of a [2N, K] weight, and the output is
+// y[:, p] = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections: small_linear followed by
+// silu_mul (fast_talker.py:258-260), bit for bit, without the [M, 2N] intermediate.
+template <int NC, int R, bool NORM, bool GLU = false>
+__global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, const uint16_t* __restrict__ norm_g,
+                                                                 float norm_eps) {
+  static_assert(!GLU || R == 2, "GLU pairs a gate row with an up row");
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  const int64_t nch = a.K / 8;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GLU ? 1 : R);
+  // weight row of the wave's i-th row (clamped into the matrix) and whether that row exists
+  auto wrow = [&](int i) -> int64_t {
+    const int64_t n = GLU ? n0 + i * a.N : n0 + i;
+    return (GLU ? n0 < a.N : n < a.N) ? n : (GLU ? i * a.N + a.N - 1 : a.N - 1);
+  };
+  int64_t cc[NC];
+  bool cin[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int64_t c = lane + static_cast<int64_t>(kWave) * j;
+    cin[j] = c < nch;
+    cc[j] = cin[j] ? c : nch - 1;
+  }
+  uint4 w[R][NC];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t nl = wrow(i);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) w[i][j] = *reinterpret_cast<const uint4*>(a.w + nl * a.ws + cc[j] * 8);
+  }
+  uint4 gv[NC];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) gv[j] = *reinterpret_cast<const uint4*>(norm_g + cc[j] * 8);
+  }
+#pragma unroll
+  for (int m = 0; m < kMaxM; ++m) {
+    if (m < a.M) {
+      const uint16_t* xr = a.x + m * a.xs;
+      uint4 xv[NC];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) xv[j] = *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
+      if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) ss += cin[j] ? sumsq8(xv[j]) : 0.f;
+        ss = wave_sum(ss);
+        const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + norm_eps);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) xv[j] = norm_chunk(xv[j], gv[j], rstd);
+      }
+      float t[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        t[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const float d = dot8_bf16(w[i][j], xv[j], 0.f);
+          t[i] += cin[j] ? d : 0.f;
+        }
+        t[i] = wave_sum(t[i]);  // every lane holds the sum
+      }
+      if constexpr (GLU) {
+        if (lane == 0 && n0 < a.N)
+          a.y[m * a.ys + n0] = f32_to_bf16(round_bf16(silu(round_bf16(t[0]))) * round_bf16(t[1]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < R; ++i)  // lane i writes row n0 + i
+          if (lane == i && n0 + i < a.N) epilogue(a, m, n0 + i, t[i]);
+      }
+    }
+  }
+}
+
+// Rows longer than one pass: each wave computes GPW = 64/LPR rows at a time, R times; LPR lanes share one
+// row, NC chunks per lane per pass.
 template <int LPR, int NC, int R>
 __global__ __launch_bounds__(256) void small_linear_kernel(LinArgs a) {
   constexpr int GPW = kWave / LPR;
@@ -99,16 +215,24 @@ __global__ __launch_bounds__(256) void small_linear_kernel(LinArgs a) {
     for (int m = 0; m < kMaxM; ++m)
       if (m < a.M) acc[m] = group_sum<LPR>(acc[m]);
 #pragma unroll
-    for (int m = 0; m < kMaxM; ++m) {
-      if (m < a.M && s == 0 && nok) {
-        float v = acc[m];
-        if (a.b) v += bf16_to_f32(a.b[n]);
-        v = apply_act(v, a.act);
-        if (a.res) v = round_bf16(v) + bf16_to_f32(a.res[m * a.rs + n]);
-        a.y[m * a.ys + n] = f32_to_bf16(v);
-      }
-    }
+    for (int m = 0; m < kMaxM; ++m)
+      if (m < a.M && s == 0 && nok) epilogue(a, m, n, acc[m]);
   }
+}
+
+template <int NC, int R>
+int launch_1pass(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.N + 4 * R - 1) / (4 * R)));
+  if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, true>), grid, dim3(256), 0, st, a, g, eps);
+  else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, false>), grid, dim3(256), 0, st, a, g, eps);
+  return mm::check_launch("small_linear");
+}
+
+// R rows per wave when that still gives every CU a workgroup; one row per wave otherwise.
+template <int NC, int RMAX>
+int launch_1pass_r(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
+  if (RMAX > 1 && a.N >= static_cast<int64_t>(4) * RMAX * mm::cu_count()) return launch_1pass<NC, RMAX>(a, g, eps, st);
+  return launch_1pass<NC, 1>(a, g, eps, st);
 }
 
 template <int LPR, int NC>
@@ -138,6 +262,23 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
   hipStream_t st = MM_STREAM(stream);
   const uint16_t* xin = static_cast<const uint16_t*>(x);
   int64_t xs = x_row_stride;
+  const int64_t nch = K / 8;
+  if (nch <= 64 * 16) {  // one pass per row, norm fused
+    MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0, "small_linear: x rows must be 16-byte aligned");
+    MM_REQUIRE(!norm_g || mm::aligned16(norm_g), "small_linear: norm_g must be 16-byte aligned");
+    LinArgs a{xin, xs, static_cast<int>(M), K, static_cast<const uint16_t*>(w), N, w_row_stride,
+              static_cast<const uint16_t*>(b), act, static_cast<const uint16_t*>(residual), res_row_stride,
+              static_cast<uint16_t*>(y), y_row_stride};
+    auto g = static_cast<const uint16_t*>(norm_g);
+    // chunks per lane NC = ceil(nch / 64), rounded up to an instantiated size; at most 16 loads per lane
+    // (rows per wave measured on MI355X: 2 at K = 896, 1 at K = 2048)
+    if (nch <= 64) return launch_1pass_r<1, 4>(a, g, norm_eps, st);
+    if (nch <= 128) return launch_1pass_r<2, 2>(a, g, norm_eps, st);
+    if (nch <= 256) return launch_1pass_r<4, 1>(a, g, norm_eps, st);
+    if (nch <= 512) return launch_1pass_r<8, 2>(a, g, norm_eps, st);
+    if (nch <= 768) return launch_1pass_r<12, 1>(a, g, norm_eps, st);
+    return launch_1pass_r<16, 1>(a, g, norm_eps, st);
+  }
   if (norm_g) {
     MM_REQUIRE(xn_buf && mm::aligned16(xn_buf), "small_linear: norm prologue needs a 16-byte aligned xn_buf [M, K]");
     hipLaunchKernelGGL(small_norm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, xin, xs, K,
@@ -152,8 +293,42 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
   LinArgs a{xin, xs, static_cast<int>(M), K, static_cast<const uint16_t*>(w), N, w_row_stride,
             static_cast<const uint16_t*>(b), act, static_cast<const uint16_t*>(residual), res_row_stride,
             static_cast<uint16_t*>(y), y_row_stride};
-  // rows of nch 16-byte chunks; rows longer than LPR * NC chunks take several passes
+  return launch<64, 4>(a, st);  // several passes of 256 chunks per row
+}
+
+namespace {
+
+template <int NC>
+int launch_glu(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.N + 3) / 4));
+  if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, 2, true, true>), grid, dim3(256), 0, st, a, g, eps);
+  else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, 2, false, true>), grid, dim3(256), 0, st, a, g, eps);
+  return mm::check_launch("small_linear_glu");
+}
+
+}  // namespace
+
+extern "C" int mm_small_linear_glu(const void* x, int64_t M, int64_t K, int64_t x_row_stride, const void* w,
+                                   int64_t inter, int64_t w_row_stride, const void* norm_g, float norm_eps, void* y,
+                                   int64_t y_row_stride, void* stream) {
+  MM_REQUIRE(M >= 1 && M <= kMaxM, "small_linear_glu: M=%lld must be in [1, %d]", (long long)M, kMaxM);
+  MM_REQUIRE(K > 0 && inter > 0 && K % 8 == 0 && K <= 8192,
+             "small_linear_glu: K=%lld must be a positive multiple of 8 up to 8192, inter=%lld > 0", (long long)K,
+             (long long)inter);
+  MM_REQUIRE(x && w && y, "small_linear_glu: null pointer");
+  MM_REQUIRE(x_row_stride >= K && w_row_stride >= K && y_row_stride >= inter, "small_linear_glu: row stride too small");
+  MM_REQUIRE(mm::aligned16(w) && (w_row_stride * 2) % 16 == 0 && mm::aligned16(x) && (x_row_stride * 2) % 16 == 0,
+             "small_linear_glu: x and weight rows must be 16-byte aligned");
+  MM_REQUIRE(!norm_g || mm::aligned16(norm_g), "small_linear_glu: norm_g must be 16-byte aligned");
+  LinArgs a{static_cast<const uint16_t*>(x), x_row_stride, static_cast<int>(M), K, static_cast<const uint16_t*>(w),
+            inter, w_row_stride, nullptr, MM_ACT_NONE, nullptr, 0, static_cast<uint16_t*>(y), y_row_stride};
+  auto g = static_cast<const uint16_t*>(norm_g);
+  hipStream_t st = MM_STREAM(stream);
   const int64_t nch = K / 8;
-  if (nch >= 128) return launch<64, 4>(a, st);
-  return launch<16, 4>(a, st);
+  if (nch <= 64) return launch_glu<1>(a, g, norm_eps, st);
+  if (nch <= 128) return launch_glu<2>(a, g, norm_eps, st);
+  if (nch <= 256) return launch_glu<4>(a, g, norm_eps, st);
+  if (nch <= 512) return launch_glu<8>(a, g, norm_eps, st);
+  if (nch <= 768) return launch_glu<12>(a, g, norm_eps, st);
+  return launch_glu<16>(a, g, norm_eps, st);
 }

@@ -5,6 +5,7 @@
   qwen_decode_attn(qkv, k, v, pos, ...) single-token GQA decode attention over StaticQwen2's KV cache,
                                        writing this token's k / v at `pos` (fast_talker.py:165-212)
   silu_mul(gu, out=None)               bf16(bf16(silu(g)) * u) of the Qwen2 MLP (fast_talker.py:215-222)
+  gate_up_silu(x, wgu, norm=None)      silu_mul(small_linear(x, wgu, norm=norm)) in one kernel, bit for bit
   FastQwen2Step                        the Talker LLM decode step built from small_linear and the kernels
                                        above (fast_talker.py:225-262)
 
@@ -19,7 +20,7 @@ import torch.nn.functional as F
 import _mingmoe as _mm
 from fastlinear import small_linear
 
-__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "FastQwen2Step", "decode_attn_workspace"]
+__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "gate_up_silu", "FastQwen2Step", "decode_attn_workspace"]
 
 
 def rope_attn(qkv, cos, sin, heads):
@@ -116,6 +117,34 @@ def silu_mul(gu, out=None):
     return out
 
 
+def gate_up_silu(x, wgu, norm=None, out=None):
+    """x [..., K] bf16; wgu [2I, K] bf16 (gate rows, then up rows); norm: (gamma, eps) RMSNorm prologue.
+    Returns bf16(bf16(silu(g)) * u) [..., I], equal bit for bit to silu_mul(small_linear(x, wgu, norm=norm))
+    (fast_talker.py:258-260) without the [..., 2I] intermediate. At most 16 rows, K <= 8192."""
+    g = norm[0] if norm is not None else None
+    _mm.require_gpu(x, wgu, out, g)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    for name, t in (("x", x2), ("wgu", wgu), ("norm gamma", g)):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"gate_up_silu: {name} must be bf16 (got {t.dtype})")
+    if wgu.dim() != 2 or wgu.shape[1] != K or wgu.shape[0] % 2 or wgu.stride(1) != 1:
+        raise ValueError(f"gate_up_silu: wgu must be [2I, {K}] with a contiguous last dim (got {tuple(wgu.shape)})")
+    if g is not None and not g.is_contiguous():
+        g = g.contiguous()
+    I = wgu.shape[0] // 2
+    M = x2.shape[0]
+    y = torch.empty(M, I, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(M, I)
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_small_linear_glu(_mm.ptr(x2), M, K, x2.stride(0), _mm.ptr(wgu), I, wgu.stride(0), _mm.ptr(g),
+                                          float(norm[1]) if norm is not None else 0.0, _mm.ptr(y), y.stride(0),
+                                          _mm.stream_of(x)), "gate_up_silu")
+    return y.reshape(*x.shape[:-1], I)
+
+
 def _fuse(mods, attr="weight"):
     """One contiguous tensor holding the `attr` of each Linear in mods, stacked along dim 0; each module's
     parameter becomes a view into it, so the weights are held once (fast_talker.py:21-31)."""
@@ -132,8 +161,8 @@ class FastQwen2Step:
     """Single-token decode of the Talker's Qwen2 over StaticQwen2's static KV cache (fast_talker.py:225-262).
 
     Per layer: small_linear(RMSNorm -> fused q|k|v + bias), qwen_decode_attn (rotary, cache write at pos,
-    attention), small_linear(o_proj + residual), small_linear(RMSNorm -> fused gate|up), silu_mul,
-    small_linear(down_proj + residual); the final norm is torch's rms_norm as in the reference."""
+    attention), small_linear(o_proj + residual), gate_up_silu(RMSNorm -> fused gate|up -> silu_mul, one
+    kernel), small_linear(down_proj + residual); the final norm is torch's rms_norm as in the reference."""
 
     def __init__(self, static_llm):
         m = static_llm.m
@@ -174,6 +203,6 @@ class FastQwen2Step:
             a = qwen_decode_attn(qkv, sl.k[i], sl.v[i], pos, sl.inv_freq, None, sl.max_len, self.scale, self.nh,
                                  self.nkv, self.hd, workspace=ws)
             h = small_linear(a, L["wo"], None, residual=h)
-            act = silu_mul(small_linear(h, L["wgu"], None, norm=L["n2"]))
+            act = gate_up_silu(h, L["wgu"], norm=L["n2"])  # = silu_mul(small_linear(h, wgu, norm=n2))
             h = small_linear(act, L["wd"], None, residual=h)
         return F.rms_norm(h, (H,), self.norm[0], self.norm[1]).reshape(1, 1, H)

@@ -12,8 +12,10 @@ one device and copies.
   ragged_bias(...)      router bias ~ N(0, 0.5): ragged per-expert token counts (512-token prefill)
   zipf_bias(...)        router bias log p_e, p_e ~ rank^-1.2 under a fixed permutation (2048-token prefill)
   moe_block_forward     RMSNorm -> router -> MoE (+ residual) through the HIP kernels
+  TalkerLLM(...)        a synthetic Qwen2 Talker LLM with StaticQwen2's attributes and KV cache layout
 """
 import math
+from types import SimpleNamespace
 
 import torch
 
@@ -101,3 +103,63 @@ def flops_per_pair(hidden=HIDDEN, inter=INTER):
 
 def nb_blocks(P, E1, BM=64):
     return math.ceil((P + E1 * (BM - 1)) / BM)
+
+
+# ------------------------------------------------------------------------------------------- Talker LLM
+
+TALKER_HIDDEN, TALKER_HEADS, TALKER_KV_HEADS, TALKER_INTER, TALKER_LAYERS = 896, 14, 2, 4864, 24
+
+
+class _RMSNorm(torch.nn.Module):
+    """Holds what FastQwen2Step reads of a Qwen2RMSNorm: `weight` and `variance_epsilon`."""
+
+    def __init__(self, w, eps):
+        super().__init__()
+        self.weight = torch.nn.Parameter(w, requires_grad=False)
+        self.variance_epsilon = eps
+
+
+def _linear(w, b=None):
+    lin = torch.nn.Linear(w.shape[1], w.shape[0], bias=b is not None, device=w.device, dtype=w.dtype)
+    lin.requires_grad_(False)
+    lin.weight.copy_(w)
+    if b is not None:
+        lin.bias.copy_(b)
+    return lin
+
+
+class TalkerLLM:
+    """A Qwen2 decoder with random weights, exposing the attributes of engine.py's StaticQwen2
+    (engine.py:1250-1266): `m.layers[i].{self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj,
+    input_layernorm, post_attention_layernorm}`, `m.norm`, nh / nkv / hd, the static KV cache
+    k, v [layers, 1, nkv, max_len, hd] (bf16, zeros) and inv_freq [hd/2] fp32 (rope theta 1e6).
+    Defaults are Qwen2-0.5B-shaped (hidden 896, 14 query / 2 KV heads of 64, intermediate 4864, 24 layers).
+    Weights ~ N(0, 0.02) bf16 (q/k/v biases too), norm weights ~ 1 + N(0, 0.02); seeds seed + 16 i + j."""
+
+    def __init__(self, layers=TALKER_LAYERS, max_len=1024, seed=0, device="cpu", hidden=TALKER_HIDDEN,
+                 heads=TALKER_HEADS, kv_heads=TALKER_KV_HEADS, inter=TALKER_INTER, theta=1e6, eps=1e-6):
+        hd = hidden // heads
+        self.nh, self.nkv, self.hd, self.max_len = heads, kv_heads, hd, max_len
+        L = []
+        for i in range(layers):
+            s = seed + 16 * i
+            w = lambda shape, j, **kw: normal(shape, 0.02, s + j, device, **kw)  # noqa: E731
+            attn = SimpleNamespace(q_proj=_linear(w((heads * hd, hidden), 0), w((heads * hd,), 1)),
+                                   k_proj=_linear(w((kv_heads * hd, hidden), 2), w((kv_heads * hd,), 3)),
+                                   v_proj=_linear(w((kv_heads * hd, hidden), 4), w((kv_heads * hd,), 5)),
+                                   o_proj=_linear(w((hidden, heads * hd), 6)))
+            mlp = SimpleNamespace(gate_proj=_linear(w((inter, hidden), 7)), up_proj=_linear(w((inter, hidden), 8)),
+                                  down_proj=_linear(w((hidden, inter), 9)))
+            L.append(SimpleNamespace(self_attn=attn, mlp=mlp,
+                                     input_layernorm=_RMSNorm(w((hidden,), 10, mean=1.0), eps),
+                                     post_attention_layernorm=_RMSNorm(w((hidden,), 11, mean=1.0), eps)))
+        self.m = SimpleNamespace(layers=L, norm=_RMSNorm(normal((hidden,), 0.02, seed + 16 * layers, device,
+                                                                mean=1.0), eps))
+        self.k = torch.zeros(layers, 1, kv_heads, max_len, hd, dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.inv_freq = 1.0 / (theta ** (torch.arange(0, hd, 2, device=device, dtype=torch.float32) / hd))
+
+    def fill_cache(self, n, seed=1):
+        """Rows [0, n) of every layer's cache ~ N(0, 1): a stand-in for an already-prefilled context."""
+        self.k[:, :, :, :n] = normal(self.k[:, :, :, :n].shape, 1.0, seed, self.k.device)
+        self.v[:, :, :, :n] = normal(self.v[:, :, :, :n].shape, 1.0, seed + 1, self.v.device)

@@ -11,6 +11,7 @@ tests/test_talker_oracle.py.
 import math
 
 import torch
+import torch.nn.functional as F
 
 BF16 = torch.bfloat16
 
@@ -103,3 +104,67 @@ def silu_mul(gu, inter):
     u = gu[..., inter:2 * inter].float()
     g = _bf(g / (1.0 + torch.exp(-g)))
     return (g * u).to(BF16)
+
+
+def fast_qwen2_step(x, layers, k_cache, v_cache, pos, inv_freq, nh, nkv, hd, final_norm):
+    """fast_talker.py:247-262, one token through the Talker LLM: per layer
+    qkv = small_linear(x, wqkv, bqkv, norm=n1); a = decode attention (:255-256); h = small_linear(a, wo) + h;
+    gu = small_linear(h, wgu, norm=n2); h = small_linear(silu_mul(gu), wd) + h; then torch's rms_norm.
+    layers: dicts of CPU tensors wqkv, bqkv, wo, wgu, wd, n1 = (w, eps), n2; k_cache, v_cache
+    [layers, nkv, max_len, hd] are written at row pos. Returns [1, 1, H] bf16."""
+    from oracle.moe_oracle import small_linear
+    H = x.shape[-1]
+    h = x.reshape(1, H)
+    scale = 1.0 / math.sqrt(hd)
+    for i, L in enumerate(layers):
+        qkv = small_linear(h, L["wqkv"], L["bqkv"], norm=L["n1"])
+        a = qwen_decode_attn(qkv.reshape(-1), k_cache[i], v_cache[i], pos, inv_freq, scale, nh, nkv, hd)
+        h = small_linear(a.reshape(1, -1), L["wo"], residual=h)
+        gu = small_linear(h, L["wgu"], norm=L["n2"])
+        h = small_linear(silu_mul(gu, L["wgu"].shape[0] // 2), L["wd"], residual=h)
+    w, eps = final_norm
+    return F.rms_norm(h.float(), (H,), w.float(), eps).to(BF16).reshape(1, 1, H)
+
+
+def static_qwen2_step_fp32(x, layers, k_cache, v_cache, pos, inv_freq, nh, nkv, hd, final_norm):
+    """engine.py:1268-1293 (StaticQwen2.forward) for one token in fp32, with HF Qwen2 modules' math:
+    RMSNorm x * rsqrt(mean(x^2) + eps) * w; q/k/v = Linear (+ bias); rotate-half rotary with emb = [f, f];
+    cache write at pos; SDPA over the GQA-expanded cache with mask ar <= pos; o_proj + residual;
+    down(silu(gate(x)) * up(x)) + residual; final RMSNorm. layers: dicts as for fast_qwen2_step (the fused
+    q|k|v and gate|up weights are split back by rows). k_cache, v_cache fp32 [layers, nkv, max_len, hd]."""
+    H = x.shape[-1]
+    h = x.float().reshape(1, H)
+
+    def rms(t, n):
+        w, eps = n
+        return t * torch.rsqrt((t * t).mean(-1, keepdim=True) + eps) * w.float()
+
+    def rotate_half(t):
+        t1, t2 = t.chunk(2, dim=-1)
+        return torch.cat((-t2, t1), dim=-1)
+
+    f = float(pos) * inv_freq.float()
+    emb = torch.cat([f, f])
+    cos, sin = emb.cos(), emb.sin()
+    rep = nh // nkv
+    max_len = k_cache.shape[2]
+    mask = (torch.arange(max_len) <= pos)[None, None]
+    for i, L in enumerate(layers):
+        xn = rms(h, L["n1"])
+        qkv = xn @ L["wqkv"].float().t() + L["bqkv"].float()
+        q = qkv[0, : nh * hd].reshape(nh, hd)
+        k = qkv[0, nh * hd:(nh + nkv) * hd].reshape(nkv, hd)
+        v = qkv[0, (nh + nkv) * hd:].reshape(nkv, hd)
+        q = q * cos + rotate_half(q) * sin
+        k = k * cos + rotate_half(k) * sin
+        k_cache[i, :, pos] = k
+        v_cache[i, :, pos] = v
+        kk = k_cache[i][:, None].expand(nkv, rep, max_len, hd).reshape(nh, max_len, hd)
+        vv = v_cache[i][:, None].expand(nkv, rep, max_len, hd).reshape(nh, max_len, hd)
+        o = F.scaled_dot_product_attention(q[:, None], kk, vv, attn_mask=mask)
+        h = h + o.reshape(1, -1) @ L["wo"].float().t()
+        xn = rms(h, L["n2"])
+        inter = L["wgu"].shape[0] // 2
+        gu = xn @ L["wgu"].float().t()
+        h = h + (F.silu(gu[:, :inter]) * gu[:, inter:]) @ L["wd"].float().t()
+    return rms(h, final_norm).reshape(1, 1, H)

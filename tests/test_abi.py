@@ -89,6 +89,7 @@ def test_argument_validation_reports_messages():
     assert "int32 or int64" in _err(lib.mm_qwen_decode_attn(P, 14, 2, 64, P, P, 1024, P, mm.MM_FP32, P, 0.1, P, P,
                                                             need, None))
     assert "row stride" in _err(lib.mm_silu_mul(P, 1, 4864, 4864, P, 4864, None))
+    assert "up to 8192" in _err(lib.mm_small_linear_glu(P, 1, 9216, 9216, P, 64, 9216, None, 0.0, P, 64, None))
 
 
 def test_wrappers_refuse_cpu_tensors():
@@ -120,7 +121,7 @@ def test_reference_module_surface_is_kept():
                                     "CFG", "GCFG", "_graph_us"]),
                        (fused_ops, ["rms_norm", "moe_route"]),
                        (fastlinear, ["small_linear", "save_cache", "_graph_time", "CACHE_FILE", "_best"]),
-                       (fast_talker, ["rope_attn", "_fuse", "FastQwen2Step"])):
+                       (fast_talker, ["rope_attn", "_fuse", "FastQwen2Step", "qwen_decode_attn", "silu_mul"])):
         for n in names:
             assert hasattr(mod, n), f"{mod.__name__}.{n}"
     fastlinear.save_cache()  # nothing tuned: writes nothing

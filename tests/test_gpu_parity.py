@@ -359,8 +359,11 @@ def test_moe_block_forward(blk):
 # -------------------------------------------------------------------------------------------- small linear
 
 @pytest.mark.parametrize("M", [1, 2, 6, 16, 20])
-@pytest.mark.parametrize("KN", [(2048, 2048), (2048, 256), (896, 1152), (4864, 896)])
+@pytest.mark.parametrize("KN", [(2048, 2048), (2048, 256), (896, 1152), (4864, 896), (256, 77), (1024, 130),
+                                (6144, 64), (8192, 33), (9216, 40)])
 def test_small_linear(M, KN):
+    """Every launch shape: one pass per row with 16 / 32 / 64 lanes per row and 4..16 chunks per lane (K up to
+    8192, norm fused), and the multi-pass kernel with its separate norm kernel (K = 9216)."""
     K, N = KN
     x = W.normal((M, K), 1.0, 100 + M, DEV)
     w = W.normal((N, K), 0.02, 101, DEV)

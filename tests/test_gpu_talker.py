@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import fast_talker as FT
+import workloads as W
 from oracle import talker_oracle as T
 
 pytestmark = pytest.mark.gpu
@@ -194,6 +195,21 @@ def test_silu_mul(rows, I):
     assert (got == want).float().mean() > 0.99
 
 
+@pytest.mark.parametrize("M,K,I,norm", [(1, 896, 4864, True), (2, 896, 4864, False), (1, 2048, 1408, True),
+                                         (3, 64, 40, True), (1, 4864, 896, False), (16, 1024, 256, True)])
+def test_gate_up_silu_equals_small_linear_then_silu_mul(M, K, I, norm):
+    import fastlinear
+    x = W.normal((M, K), 0.5, 600 + K, DEV)
+    w = W.normal((2 * I, K), 0.05, 601, DEV)
+    nm = (W.normal((K,), 0.02, 602, DEV, mean=1.0), 1e-6) if norm else None
+    fused = FT.gate_up_silu(x, w, norm=nm)
+    unfused = FT.silu_mul(fastlinear.small_linear(x, w, norm=nm))
+    torch.cuda.synchronize()
+    assert torch.equal(fused, unfused)
+    gu_o = T.silu_mul(fastlinear.small_linear(x, w, norm=nm).cpu(), I)
+    assert torch.equal(fused.cpu(), gu_o) or (fused.cpu().float() - gu_o.float()).abs().max() < 2e-2
+
+
 def test_silu_mul_strided_rows_and_out():
     g = torch.Generator().manual_seed(5)
     big = (torch.randn(3, 2 * 4864 + 64, generator=g) * 3).to(BF).to(DEV)
@@ -203,3 +219,76 @@ def test_silu_mul_strided_rows_and_out():
     torch.cuda.synchronize()
     torch.testing.assert_close(res.float().cpu(), T.silu_mul(gu.cpu(), 4864).float(), rtol=2 ** -7, atol=0)
     assert res.data_ptr() == out.data_ptr()
+
+
+# ------------------------------------------------------------------------------------ Talker LLM step
+
+def _cpu_layers(fs):
+    """FastQwen2Step's fused per-layer weights as CPU tensors (the oracle's input)."""
+    out = []
+    for L in fs.layers:
+        out.append({k: (v[0].cpu(), v[1]) if isinstance(v, tuple) else v.cpu() for k, v in L.items()})
+    return out
+
+
+def test_fast_qwen2_step_matches_oracle_and_unfused_path():
+    """Three decode steps of a 4-layer Qwen2-0.5B-shaped Talker LLM after a 150-position context (the pattern
+    of the reference's dev/test_fast_llm.py): each output matches the oracle's restatement of the fast step,
+    and the unfused fp32 StaticQwen2 forward to bf16 accuracy; the caches match the oracle's."""
+    nh, nkv, hd, T0 = 14, 2, 64, 150
+    llm = W.TalkerLLM(layers=4, max_len=256, seed=200, device=DEV)
+    llm.fill_cache(T0, seed=300)
+    fs = FT.FastQwen2Step(llm)
+    layers = _cpu_layers(fs)
+    kc, vc = llm.k[:, 0].cpu(), llm.v[:, 0].cpu()
+    k32, v32 = kc.float(), vc.float()
+    inv = llm.inv_freq.cpu()
+    fn = (llm.m.norm.weight.detach().cpu(), llm.m.norm.variance_epsilon)
+    for j in range(3):
+        x = W.normal((1, 1, W.TALKER_HIDDEN), 0.1, 400 + j)
+        pos = T0 + j
+        print(f"talker step pos={pos}", flush=True)
+        out = fs(x.to(DEV), torch.tensor([pos], device=DEV)).float().cpu()
+        want = T.fast_qwen2_step(x, layers, kc, vc, pos, inv, nh, nkv, hd, fn)
+        ref = T.static_qwen2_step_fp32(x, layers, k32, v32, pos, inv, nh, nkv, hd, fn)
+        close(out, want, atol=2e-2)
+        rel = ((out - ref.float()).norm() / ref.float().norm()).item()
+        assert rel < 3e-2, rel
+    torch.cuda.synchronize()
+    close(llm.k[:, 0], kc)
+    close(llm.v[:, 0], vc)
+
+
+def test_fast_qwen2_step_graph_replays_match_eager():
+    """The step captured once and replayed with new inputs and positions equals eager calls bit for bit,
+    cache writes included."""
+    H, T0 = W.TALKER_HIDDEN, 60
+    llm = W.TalkerLLM(layers=3, max_len=128, seed=210, device=DEV)
+    llm.fill_cache(T0, seed=310)
+    fs = FT.FastQwen2Step(llm)
+    k0, v0 = llm.k.clone(), llm.v.clone()
+    xs = [W.normal((1, 1, H), 0.1, 500 + j, DEV) for j in range(3)]
+    eager = [fs(xs[j], torch.tensor([T0 + j], device=DEV)).clone() for j in range(3)]
+    k_e, v_e = llm.k.clone(), llm.v.clone()
+    x_s = xs[0].clone()
+    pos_s = torch.full((1,), T0, device=DEV, dtype=torch.long)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fs(x_s, pos_s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out_s = fs(x_s, pos_s)
+    torch.cuda.synchronize()
+    llm.k.copy_(k0)
+    llm.v.copy_(v0)
+    for j in range(3):
+        x_s.copy_(xs[j])
+        pos_s.fill_(T0 + j)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, eager[j]), f"replay {j}"
+    assert torch.equal(llm.k, k_e) and torch.equal(llm.v, v_e)

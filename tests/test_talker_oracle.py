@@ -168,3 +168,39 @@ def test_silu_mul_matches_torch_silu_and_closed_forms():
     special = torch.tensor([[0.0, 30.0, -100.0, 1.5, 2.0, 3.0]]).to(BF)  # g | u
     out = T.silu_mul(special, 3).float()
     assert out[0, 0] == 0 and out[0, 1] == 60.0 and out[0, 2] == 0
+
+
+def _layers_of(llm):
+    """The fused per-layer weights FastQwen2Step builds (q|k|v and gate|up stacked by rows), on the CPU."""
+    out = []
+    for layer in llm.m.layers:
+        a, mlp = layer.self_attn, layer.mlp
+        out.append({"wqkv": torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]),
+                    "bqkv": torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]),
+                    "wo": a.o_proj.weight, "wgu": torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]),
+                    "wd": mlp.down_proj.weight,
+                    "n1": (layer.input_layernorm.weight.detach(), layer.input_layernorm.variance_epsilon),
+                    "n2": (layer.post_attention_layernorm.weight.detach(),
+                           layer.post_attention_layernorm.variance_epsilon)})
+    return out
+
+
+@pytest.mark.parametrize("pos", [0, 40])
+def test_fast_step_oracle_matches_unfused_static_qwen2(pos):
+    import workloads as W
+    llm = W.TalkerLLM(layers=2, max_len=64, seed=30)
+    llm.fill_cache(pos, seed=31)
+    layers = _layers_of(llm)
+    x = W.normal((1, 1, W.TALKER_HIDDEN), 0.1, 32)  # small like embeddings, so the layers dominate the output
+    fn = (llm.m.norm.weight.detach(), llm.m.norm.variance_epsilon)
+    kc, vc = llm.k[:, 0].clone(), llm.v[:, 0].clone()
+    got = T.fast_qwen2_step(x, layers, kc, vc, pos, llm.inv_freq, 14, 2, 64, fn).float()
+    k32, v32 = llm.k[:, 0].float(), llm.v[:, 0].float()
+    ref = T.static_qwen2_step_fp32(x, layers, k32, v32, pos, llm.inv_freq, 14, 2, 64, fn)
+    assert ((got - ref).norm() / ref.norm()).item() < 2e-2
+    torch.testing.assert_close(kc.float(), k32, rtol=2e-2, atol=2e-2)
+    # planted mistake: k and v swapped in the fused projection
+    bad = [dict(L, wqkv=torch.cat([L["wqkv"][:896], L["wqkv"][1024:], L["wqkv"][896:1024]]),
+                bqkv=torch.cat([L["bqkv"][:896], L["bqkv"][1024:], L["bqkv"][896:1024]])) for L in layers]
+    wrong = T.fast_qwen2_step(x, bad, llm.k[:, 0].clone(), llm.v[:, 0].clone(), pos, llm.inv_freq, 14, 2, 64, fn)
+    assert ((wrong.float() - ref).norm() / ref.norm()).item() > 0.2
