@@ -8,6 +8,8 @@
   gate_up_silu(x, wgu, norm=None)      silu_mul(small_linear(x, wgu, norm=norm)) in one kernel, bit for bit
   FastQwen2Step                        the Talker LLM decode step built from small_linear and the kernels
                                        above (fast_talker.py:225-262)
+  FastTail                             the per-latent flow-matching DiT loop, aggregator and stop head on
+                                       small_linear and rope_attn (fast_talker.py:82-160)
 
 Every op runs on torch's current stream, allocates only with torch (so it can be captured in a graph),
 and raises if the HIP library is missing: there is no CPU or Triton path.
@@ -20,7 +22,8 @@ import torch.nn.functional as F
 import _mingmoe as _mm
 from fastlinear import small_linear
 
-__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "gate_up_silu", "FastQwen2Step", "decode_attn_workspace"]
+__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "gate_up_silu", "FastQwen2Step", "FastTail",
+           "decode_attn_workspace"]
 
 
 def rope_attn(qkv, cos, sin, heads):
@@ -155,6 +158,98 @@ def _fuse(mods, attr="weight"):
         p.data = fused[row:row + p.shape[0]]
         row += p.shape[0]
     return fused
+
+
+class _Block:
+    """One DiT / aggregator transformer block on the fused kernels (fast_talker.py:82-102):
+    h = h + to_out(rope_attn(q|k|v(RMSNorm1(h)))); h = h + W2(GELU_tanh(W1(RMSNorm2(h)))), every bias, norm,
+    activation and residual in a small_linear prologue or epilogue."""
+
+    def __init__(self, blk):
+        at = blk.attn
+        if at.q_norm is not None or at.pe_attn_head is not None:
+            raise ValueError("DiT block with q/k norms or a positional attention head is not supported")
+        ff = blk.mlp.ff
+        if ff[0][1].approximate != "tanh":
+            raise ValueError("DiT feed-forward must use GELU(approximate='tanh')")
+        self.heads = at.heads
+        self.wqkv = _fuse([at.to_q, at.to_k, at.to_v])
+        self.bqkv = _fuse([at.to_q, at.to_k, at.to_v], "bias")
+        self.wo, self.bo = at.to_out[0].weight, at.to_out[0].bias
+        self.n1 = (blk.norm1.weight, blk.norm1.eps)
+        self.n2 = (blk.norm2.weight, blk.norm2.eps)
+        self.w1, self.b1 = ff[0][0].weight, ff[0][0].bias
+        self.w2, self.b2 = ff[2].weight, ff[2].bias
+
+    def __call__(self, h, cos, sin):
+        att = rope_attn(small_linear(h, self.wqkv, self.bqkv, norm=self.n1), cos, sin, self.heads)
+        h = small_linear(att, self.wo, self.bo, residual=h)
+        f = small_linear(h, self.w1, self.b1, act=1, norm=self.n2)
+        return small_linear(f, self.w2, self.b2, residual=h)
+
+
+def _rope_tables(rotary, n):
+    """cos / sin [n, hd/2] fp32 of the block's rotary embedding: forward_from_seq_len gives each pair's angle
+    twice (interleaved), so every other column is taken (fast_talker.py:105-108)."""
+    freqs, _ = rotary.forward_from_seq_len(n)
+    ang = freqs[0, :, 0::2].float()
+    return ang.cos().contiguous(), ang.sin().contiguous()
+
+
+class FastTail:
+    """y_latent, next_input_embedding, stop_prob = tail(hidden, history, noise) (fast_talker.py:111-160).
+
+    Flow matching with classifier-free guidance at temperature 0: per step the DiT runs on a batch of two
+    3-token sequences [condition + timestep, history, current latent] (conditioned and null rows), and
+    y += (pred + (pred - null) * cfg) * dt. Then the aggregator maps [cls, latent] to the next LLM input and
+    the stop head gives P(stop). Everything constant over the steps (timestep and condition embeddings,
+    rotary tables, the cls token) is computed once here."""
+
+    def __init__(self, talker, ts, dts, cfg_strength):
+        t = talker.t
+        dit, agg = t.cfm.model, t.aggregator
+        if getattr(dit, "spk_embedder", None) is not None:
+            raise ValueError("DiT with a speaker embedder is not supported")
+        dev = t.stop_head.weight.device
+        self.cfg = cfg_strength
+        self.dts = [d.reshape(1) for d in dts]
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            self.t_emb = [dit.t_embedder(ts[i].reshape(1)).to(torch.bfloat16) for i in range(len(self.dts))]
+            self.cls = agg.word_embedder(torch.zeros(1, 1, dtype=torch.long, device=dev)).to(torch.bfloat16)
+        self.c_w, self.c_b = dit.c_embedder.cond_embedder.weight, dit.c_embedder.cond_embedder.bias
+        self.null_c = self.c_b.reshape(1, -1)  # the condition embedder of a zero condition is its bias
+        self.x_w, self.x_b = dit.x_embedder.weight, dit.x_embedder.bias
+        self.f_norm = (dit.final_layer.norm_final.weight, dit.final_layer.norm_final.eps)
+        self.f_w, self.f_b = dit.final_layer.linear.weight, dit.final_layer.linear.bias
+        self.blocks = [_Block(b) for b in dit.blocks]
+        self.cos3, self.sin3 = _rope_tables(dit.rotary_embed, 3)
+        self.a_x_w, self.a_x_b = agg.x_embedder.weight, agg.x_embedder.bias
+        self.a_blocks = [_Block(b) for b in agg.blocks]
+        self.cos2, self.sin2 = _rope_tables(agg.rotary_embed, 2)
+        self.a_norm = (agg.final_layer.norm_final.weight, agg.final_layer.norm_final.eps)
+        self.a_w, self.a_b = agg.final_layer.linear.weight, agg.final_layer.linear.bias
+        self.s_w, self.s_b = t.stop_head.weight, t.stop_head.bias
+
+    def __call__(self, hidden, hist, noise):
+        D = self.x_w.shape[0]
+        cond = torch.cat([small_linear(hidden.reshape(1, -1), self.c_w, self.c_b), self.null_c], 0)  # [2, D]
+        h_emb = small_linear(hist.reshape(1, -1), self.x_w, self.x_b).expand(2, D)
+        y = noise.reshape(1, -1)
+        for i, dt in enumerate(self.dts):
+            y_emb = small_linear(y, self.x_w, self.x_b).expand(2, D)
+            h = torch.stack([cond + self.t_emb[i], h_emb, y_emb], 1)  # [2, 3, D]
+            for blk in self.blocks:
+                h = blk(h, self.cos3, self.sin3)
+            out = small_linear(h[:, -1], self.f_w, self.f_b, norm=self.f_norm)  # [2, latent]
+            pred, null = out[0:1], out[1:2]
+            y = y + (pred + (pred - null) * self.cfg) * dt
+        Da = self.a_x_w.shape[0]
+        a = torch.stack([self.cls.reshape(1, Da), small_linear(y, self.a_x_w, self.a_x_b)], 1)  # [1, 2, Da]
+        for blk in self.a_blocks:
+            a = blk(a, self.cos2, self.sin2)
+        x_next = small_linear(a[:, 0], self.a_w, self.a_b, norm=self.a_norm).reshape(1, 1, -1)
+        stop = small_linear(hidden.reshape(1, -1), self.s_w, self.s_b).float().softmax(-1)[0, 1]
+        return y.reshape(1, 1, -1), x_next, stop
 
 
 class FastQwen2Step:

@@ -77,7 +77,7 @@ def small_linear(x, w, b=None, act=0, residual=None, out=None, norm=None):
     shape = x.shape
     K = shape[-1]
     x2 = x.reshape(-1, K)
-    if not x2.is_contiguous():
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:  # rows strided by a 16-byte multiple pass as is
         x2 = x2.contiguous()
     M, N = x2.shape[0], w.shape[0]
     for name, t in (("x", x2), ("w", w), ("b", b), ("residual", residual), ("norm gamma", g)):

@@ -13,6 +13,7 @@ one device and copies.
   zipf_bias(...)        router bias log p_e, p_e ~ rank^-1.2 under a fixed permutation (2048-token prefill)
   moe_block_forward     RMSNorm -> router -> MoE (+ residual) through the HIP kernels
   TalkerLLM(...)        a synthetic Qwen2 Talker LLM with StaticQwen2's attributes and KV cache layout
+  TalkerTail(...)       a synthetic Talker (DiT + aggregator + stop head) with the attributes FastTail reads
 """
 import math
 from types import SimpleNamespace
@@ -163,3 +164,73 @@ class TalkerLLM:
         """Rows [0, n) of every layer's cache ~ N(0, 1): a stand-in for an already-prefilled context."""
         self.k[:, :, :, :n] = normal(self.k[:, :, :, :n].shape, 1.0, seed, self.k.device)
         self.v[:, :, :, :n] = normal(self.v[:, :, :, :n].shape, 1.0, seed + 1, self.v.device)
+
+
+class _Rotary:
+    """forward_from_seq_len(n) -> (freqs [1, n, hd], 1.0) with each pair's angle t * inv_freq[p] twice,
+    interleaved, as x_transformers' RotaryEmbedding returns them."""
+
+    def __init__(self, hd, device, theta=10000.0):
+        self.inv_freq = 1.0 / (theta ** (torch.arange(0, hd, 2, device=device, dtype=torch.float32) / hd))
+
+    def forward_from_seq_len(self, n):
+        f = torch.arange(n, device=self.inv_freq.device, dtype=torch.float32)[:, None] * self.inv_freq[None]
+        return torch.stack([f, f], -1).reshape(1, n, -1), 1.0
+
+
+class _TimestepEmbedder:
+    """t [1] -> [1, D] bf16: sinusoidal features of t through a fixed random linear map."""
+
+    def __init__(self, D, seed, device, nf=32):
+        self.freqs = torch.exp(-math.log(1000.0) * torch.arange(nf // 2, device=device, dtype=torch.float32) / (nf // 2))
+        self.proj = normal((nf, D), 0.5, seed, device, dtype=torch.float32)
+
+    def __call__(self, t):
+        a = t.float().reshape(-1, 1) * 1000.0 * self.freqs[None]
+        return (torch.cat([a.sin(), a.cos()], -1) @ self.proj).to(torch.bfloat16)
+
+
+def _dit_block(D, heads, F, seed, device):
+    w = lambda shape, j, **kw: normal(shape, 0.02, seed + j, device, **kw)  # noqa: E731
+    attn = SimpleNamespace(heads=heads, to_q=_linear(w((D, D), 0), w((D,), 1)), to_k=_linear(w((D, D), 2), w((D,), 3)),
+                           to_v=_linear(w((D, D), 4), w((D,), 5)), to_out=[_linear(w((D, D), 6), w((D,), 7))],
+                           q_norm=None, pe_attn_head=None)
+    ff = [[_linear(w((F, D), 8), w((F,), 9)), SimpleNamespace(approximate="tanh")], None,
+          _linear(w((D, F), 10), w((D,), 11))]
+    return SimpleNamespace(attn=attn, mlp=SimpleNamespace(ff=ff),
+                           norm1=SimpleNamespace(weight=w((D,), 12, mean=1.0), eps=1e-6),
+                           norm2=SimpleNamespace(weight=w((D,), 13, mean=1.0), eps=1e-6))
+
+
+class TalkerTail:
+    """A Talker with random weights exposing what FastTail reads (fast_talker.py:114-137): t.cfm.model (the
+    DiT: t_embedder, c_embedder.cond_embedder, x_embedder, blocks, rotary_embed, final_layer), t.aggregator
+    (word_embedder, x_embedder, blocks, rotary_embed, final_layer) and t.stop_head; ts (steps + 1 bf16
+    timesteps in [0, 1]), dts and cfg_strength 2.0. Default shapes (an assumption: the reference loads its
+    Talker config from the model directory): DiT hidden 1024, 16 heads, MLP 4096, 4 blocks; aggregator 2
+    blocks; latent 64; LLM hidden 896; 10 steps."""
+
+    def __init__(self, seed=0, device="cpu", llm_hidden=TALKER_HIDDEN, dim=1024, heads=16, mlp=4096, depth=4,
+                 agg_depth=2, latent=64, steps=10):
+        w = lambda shape, j, **kw: normal(shape, 0.02, seed + j, device, **kw)  # noqa: E731
+        hd = dim // heads
+        final = lambda j, out: SimpleNamespace(norm_final=SimpleNamespace(weight=w((dim,), j, mean=1.0), eps=1e-6),  # noqa: E731
+                                               linear=_linear(w((out, dim), j + 1), w((out,), j + 2)))
+        dit = SimpleNamespace(
+            spk_embedder=None, t_embedder=_TimestepEmbedder(dim, seed + 1, device),
+            c_embedder=SimpleNamespace(cond_embedder=_linear(w((dim, llm_hidden), 2), w((dim,), 3))),
+            x_embedder=_linear(w((dim, latent), 4), w((dim,), 5)),
+            blocks=[_dit_block(dim, heads, mlp, seed + 100 + 20 * i, device) for i in range(depth)],
+            rotary_embed=_Rotary(hd, device), final_layer=final(10, latent))
+        emb = torch.nn.Embedding(1, dim, device=device, dtype=torch.bfloat16)
+        emb.requires_grad_(False)
+        emb.weight.copy_(normal((1, dim), 1.0, seed + 20, device))
+        agg = SimpleNamespace(
+            word_embedder=emb, x_embedder=_linear(w((dim, latent), 21), w((dim,), 22)),
+            blocks=[_dit_block(dim, heads, mlp, seed + 500 + 20 * i, device) for i in range(agg_depth)],
+            rotary_embed=_Rotary(hd, device), final_layer=final(30, llm_hidden))
+        self.t = SimpleNamespace(cfm=SimpleNamespace(model=dit), aggregator=agg,
+                                 stop_head=_linear(normal((2, llm_hidden), 0.05, seed + 40, device), w((2,), 41)))
+        self.ts = torch.linspace(0, 1, steps + 1, device=device).to(torch.bfloat16)
+        self.dts = [self.ts[s + 1] - self.ts[s] for s in range(steps)]
+        self.cfg_strength = 2.0

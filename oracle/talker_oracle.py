@@ -168,3 +168,60 @@ def static_qwen2_step_fp32(x, layers, k_cache, v_cache, pos, inv_freq, nh, nkv, 
         gu = xn @ L["wgu"].float().t()
         h = h + (F.silu(gu[:, :inter]) * gu[:, inter:]) @ L["wd"].float().t()
     return rms(h, final_norm).reshape(1, 1, H)
+
+
+def _dit_block(b, h, cos, sin):
+    """fast_talker.py:97-102 on the oracle's small_linear and rope_attn."""
+    from oracle.moe_oracle import small_linear
+    att = rope_attn(small_linear(h, b["wqkv"], b["bqkv"], norm=b["n1"]), cos, sin, b["heads"])
+    h = small_linear(att, b["wo"], b["bo"], residual=h)
+    f = small_linear(h, b["w1"], b["b1"], act=1, norm=b["n2"])
+    return small_linear(f, b["w2"], b["b2"], residual=h)
+
+
+def fast_tail(P, hidden, hist, noise):
+    """fast_talker.py:139-160 (FastTail.__call__) on the CPU: P holds FastTail's hoisted constants as CPU
+    tensors (c_w, c_b, x_w, x_b, t_emb list, dts list, cfg, blocks / a_blocks as dicts, cos3 / sin3,
+    cos2 / sin2, f_norm, f_w, f_b, cls, a_x_w, a_x_b, a_norm, a_w, a_b, s_w, s_b). The latent update
+    y + (pred + (pred - null) * cfg) * dt runs in bf16 torch ops in the same order as the reference.
+    Returns (latent [1, 1, L], next input [1, 1, H], stop probability)."""
+    from oracle.moe_oracle import small_linear
+    D = P["x_w"].shape[0]
+    c = small_linear(hidden.reshape(1, -1), P["c_w"], P["c_b"])
+    c2 = torch.cat([c, P["c_b"].reshape(1, -1)], 0)
+    he = small_linear(hist.reshape(1, -1), P["x_w"], P["x_b"])
+    y = noise.reshape(1, -1)
+    for s, dt in enumerate(P["dts"]):
+        ye = small_linear(y, P["x_w"], P["x_b"])
+        h = torch.stack([c2 + P["t_emb"][s], he.expand(2, D), ye.expand(2, D)], 1)
+        for b in P["blocks"]:
+            h = _dit_block(b, h, P["cos3"], P["sin3"])
+        out = small_linear(h[:, -1], P["f_w"], P["f_b"], norm=P["f_norm"])
+        pred, null = out[0:1], out[1:2]
+        y = y + (pred + (pred - null) * P["cfg"]) * dt
+    Da = P["a_x_w"].shape[0]
+    a = torch.stack([P["cls"].reshape(1, Da), small_linear(y, P["a_x_w"], P["a_x_b"])], 1)
+    for b in P["a_blocks"]:
+        a = _dit_block(b, a, P["cos2"], P["sin2"])
+    x_next = small_linear(a[:, 0], P["a_w"], P["a_b"], norm=P["a_norm"]).reshape(1, 1, -1)
+    stop = small_linear(hidden.reshape(1, -1), P["s_w"], P["s_b"]).float().softmax(-1)[0, 1]
+    return y.reshape(1, 1, -1), x_next, stop
+
+
+def _cpu(v):
+    if torch.is_tensor(v):
+        return v.detach().cpu()
+    if isinstance(v, (tuple, list)):
+        return type(v)(_cpu(x) for x in v)
+    return v
+
+
+def tail_constants(ft):
+    """FastTail's hoisted constants (attributes of a fast_talker.FastTail) as CPU tensors: fast_tail's P."""
+    keys = ("c_w", "c_b", "x_w", "x_b", "t_emb", "dts", "cfg", "cos3", "sin3", "cos2", "sin2", "f_norm", "f_w", "f_b",
+            "cls", "a_x_w", "a_x_b", "a_norm", "a_w", "a_b", "s_w", "s_b")
+    P = {k: _cpu(getattr(ft, k)) for k in keys}
+    bk = ("heads", "wqkv", "bqkv", "wo", "bo", "n1", "n2", "w1", "b1", "w2", "b2")
+    P["blocks"] = [{k: _cpu(getattr(b, k)) for k in bk} for b in ft.blocks]
+    P["a_blocks"] = [{k: _cpu(getattr(b, k)) for k in bk} for b in ft.a_blocks]
+    return P

@@ -121,7 +121,8 @@ def test_reference_module_surface_is_kept():
                                     "CFG", "GCFG", "_graph_us"]),
                        (fused_ops, ["rms_norm", "moe_route"]),
                        (fastlinear, ["small_linear", "save_cache", "_graph_time", "CACHE_FILE", "_best"]),
-                       (fast_talker, ["rope_attn", "_fuse", "FastQwen2Step", "qwen_decode_attn", "silu_mul"])):
+                       (fast_talker, ["rope_attn", "_fuse", "_Block", "_rope_tables", "FastTail", "FastQwen2Step",
+                                      "qwen_decode_attn", "silu_mul"])):
         for n in names:
             assert hasattr(mod, n), f"{mod.__name__}.{n}"
     fastlinear.save_cache()  # nothing tuned: writes nothing

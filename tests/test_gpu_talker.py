@@ -292,3 +292,56 @@ def test_fast_qwen2_step_graph_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out_s, eager[j]), f"replay {j}"
     assert torch.equal(llm.k, k_e) and torch.equal(llm.v, v_e)
+
+
+# ------------------------------------------------------------------------------------------ Talker tail
+
+def test_fast_tail_matches_oracle():
+    """Three flow-matching steps of a 2-block DiT (hidden 1024, 16 heads) and a 1-block aggregator: latent,
+    next LLM input and stop probability against the oracle's restatement of FastTail on the same constants."""
+    tk = W.TalkerTail(seed=700, device=DEV, depth=2, agg_depth=1, steps=3)
+    ft = FT.FastTail(tk, tk.ts, tk.dts, tk.cfg_strength)
+    P = T.tail_constants(ft)
+    for trial in range(2):
+        hidden = W.normal((1, 1, W.TALKER_HIDDEN), 1.0, 710 + trial)
+        hist = W.normal((1, 1, 64), 1.0, 720 + trial)
+        noise = W.normal((1, 1, 64), 1.0, 730 + trial)
+        print(f"fast_tail trial {trial}", flush=True)
+        lat, x_next, stop = ft(hidden.to(DEV), hist.to(DEV), noise.to(DEV))
+        w_lat, w_x, w_stop = T.fast_tail(P, hidden, hist, noise)
+        # the CFG update y += (3 pred - 2 null) dt amplifies one-ulp bf16 differences from step to step, so
+        # the composed tail is held to a norm-relative bar (as the reference's dev/test_fast_tail.py reports
+        # it); every kernel inside is held to the elementwise bar in its own tests
+        for got, want in ((lat, w_lat), (x_next, w_x)):
+            d = got.float().cpu() - want.float()
+            assert (d.norm() / want.float().norm()).item() < 2e-2 and d.abs().max().item() < 0.1
+        assert abs(stop.item() - w_stop.item()) < 1e-2
+
+
+def test_fast_tail_graph_replays_match_eager():
+    """The tail captured once and replayed on new inputs equals eager calls bit for bit (the engine replays
+    it from a graph, engine.py:1412-1414)."""
+    tk = W.TalkerTail(seed=740, device=DEV, depth=1, agg_depth=1, steps=2)
+    ft = FT.FastTail(tk, tk.ts, tk.dts, tk.cfg_strength)
+    ins = [[W.normal(shape, 1.0, 750 + 3 * j + k, DEV) for k, shape in enumerate(((1, 1, W.TALKER_HIDDEN),
+                                                                                     (1, 1, 64), (1, 1, 64)))]
+           for j in range(3)]
+    eager = [tuple(t.clone() for t in ft(*x)) for x in ins]
+    bufs = [t.clone() for t in ins[0]]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ft(*bufs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = ft(*bufs)
+    for j in range(3):
+        for b, x in zip(bufs, ins[j]):
+            b.copy_(x)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager[j]):
+            assert torch.equal(o, e), f"replay {j}"

@@ -204,3 +204,23 @@ def test_fast_step_oracle_matches_unfused_static_qwen2(pos):
                 bqkv=torch.cat([L["bqkv"][:896], L["bqkv"][1024:], L["bqkv"][896:1024]])) for L in layers]
     wrong = T.fast_qwen2_step(x, bad, llm.k[:, 0].clone(), llm.v[:, 0].clone(), pos, llm.inv_freq, 14, 2, 64, fn)
     assert ((wrong.float() - ref).norm() / ref.norm()).item() > 0.2
+
+
+def test_fast_tail_oracle_closed_forms():
+    """Zero step sizes leave the latent at the noise exactly; the stop probability is the 2-way softmax of
+    the stop head on the LLM hidden state (F.linear in float64); the aggregator output depends on the latent."""
+    import warnings
+    import fast_talker as FT
+    import workloads as W
+    tk = W.TalkerTail(seed=5, depth=1, agg_depth=1, steps=2, dim=128, heads=2, mlp=256, latent=16, llm_hidden=64)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")  # autocast("cuda") on a CPU-only torch only warns
+        ft = FT.FastTail(tk, tk.ts, tk.dts, tk.cfg_strength)
+    P = T.tail_constants(ft)
+    hidden, hist, noise = (W.normal(s, 1.0, 60 + i) for i, s in enumerate(((1, 1, 64), (1, 1, 16), (1, 1, 16))))
+    lat0, x0, stop = T.fast_tail(dict(P, dts=[torch.zeros(1, dtype=BF)] * 2), hidden, hist, noise)
+    assert torch.equal(lat0, noise)
+    want = F.softmax(F.linear(hidden.double().reshape(1, -1), P["s_w"].double(), P["s_b"].double()), -1)[0, 1]
+    assert abs(stop.item() - want.item()) < 1e-2
+    lat, x1, _ = T.fast_tail(P, hidden, hist, noise)
+    assert not torch.equal(lat, noise) and not torch.equal(x1, x0)
