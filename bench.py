@@ -343,7 +343,9 @@ def full_decode_metrics(stream, layers=28):
 def talker_metrics(stream, layers=24, max_len=1024, pos=512):
     """The Talker's per-token work on the HIP kernels: one decode step of a Qwen2-0.5B-shaped Talker LLM
     (FastQwen2Step: 24 layers, hidden 896, 14 query / 2 KV heads of 64, intermediate 4864) at position 512
-    of a 1024-position cache, replayed from one hipGraph; and per kernel (20 launches in one graph): the decode
+    of a 1024-position cache, replayed from one hipGraph; the per-latent tail (FastTail: 10 CFG steps of a
+    4-block DiT of hidden 1024, a 2-block aggregator, the stop head) from one hipGraph; and per kernel (20
+    launches in one graph): the decode
     attention at that position, the rotary attention of a DiT block (2 x 3 tokens) and of an aggregator
     block (1 x 2 tokens), 16 heads of 64, and silu_mul over 4864."""
     import fast_talker as FT
@@ -376,7 +378,14 @@ def talker_metrics(stream, layers=24, max_len=1024, pos=512):
     w_bytes = layers * ((nh + 2 * nkv) * hd * H + H * nh * hd + 2 * I * H + H * I) * 2
     kv_bytes = 2 * nkv * (pos + 1) * hd * 2
     del g, fs, llm
-    return {"layers": layers, "pos": pos, "max_len": max_len, "step_us": step_ms * 1e3,
+    # the per-latent tail: 10 CFG flow-matching steps of a 4-block DiT (hidden 1024) + 2-block aggregator
+    tk = W.TalkerTail(seed=3100, device=dev)
+    ft = FT.FastTail(tk, tk.ts, tk.dts, tk.cfg_strength)
+    ins = [W.normal(shape, 1.0, 3110 + i, dev) for i, shape in enumerate(((1, 1, H), (1, 1, 64), (1, 1, 64)))]
+    gt = graph_of(lambda: ft(*ins), stream)
+    tail_ms = time_graph(gt, stream, 20)
+    del gt, ft, tk
+    return {"layers": layers, "pos": pos, "max_len": max_len, "step_us": step_ms * 1e3, "tail_us": tail_ms * 1e3,
             "step_bytes": w_bytes + layers * kv_bytes, "step_TBs": (w_bytes + layers * kv_bytes) / step_ms / 1e9,
             "decode_attn_us": attn_ms * 1e3, "decode_attn_kv_bytes": kv_bytes,
             "rope_attn_dit_us": rope["dit"], "rope_attn_aggregator_us": rope["aggregator"],

@@ -96,23 +96,32 @@ __device__ __forceinline__ float sumsq8(uint4 v) {
   return s;
 }
 
+// Token rows whose activation chunks are held at once (1 when there is a single row).
+constexpr int row_group(int NC) { return NC <= 2 ? 8 : NC <= 4 ? 4 : NC <= 8 ? 2 : 1; }
+
 // One pass per row (64 * NC >= K / 8): the 64 lanes of a wave share a row, lane s holding chunks
 // s + 64 j (j < NC), and a wave computes R rows whose R * NC weight loads per lane are all issued at once,
 // so it waits for memory once. Chunk indices past the row are clamped to its last chunk (a valid address)
-// and their products dropped by a select. The activation chunks of a lane are loaded once per token row
-// and reused for the R weight rows; with NORM the wave sums their squares (the whole row passes through
-// its lanes) and normalises them in place, 8 * NC elements per lane.
+// and their products dropped by a select. Token rows go in groups of MG: the activation chunks of a whole
+// group are loaded before any of its math. NORM: the whole activation row passes through the wave's lanes,
+// so the wave sums its squares itself; with several rows the 4 waves of the workgroup split the group's
+// rows, normalise them into LDS, and all read them back. The bias, GELU / SiLU and residual run once per
+// group in parallel, lane = (token row, output row), with the bias and residuals read before any store.
 // GLU (R = 2): the wave's two rows are gate row p and up row p + N of a [2N, K] weight, and the output is
 // y[:, p] = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections: small_linear followed by
 // silu_mul (fast_talker.py:258-260), bit for bit, without the [M, 2N] intermediate.
-template <int NC, int R, bool NORM, bool GLU = false>
+template <int NC, int R, bool NORM, bool GLU, int MG>
 __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, const uint16_t* __restrict__ norm_g,
                                                                  float norm_eps) {
   static_assert(!GLU || R == 2, "GLU pairs a gate row with an up row");
+  static_assert(MG * R <= kWave, "one epilogue lane per (token row, output row)");
+  constexpr bool kShareNorm = NORM && MG > 1;
+  constexpr int OUTS = GLU ? 1 : R;  // output rows per wave
+  __shared__ uint4 lx[kShareNorm ? MG * NC * kWave : 1];
   const int lane = lane_id(), wave = threadIdx.x / kWave;
   const int64_t nch = a.K / 8;
-  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GLU ? 1 : R);
-  // weight row of the wave's i-th row (clamped into the matrix) and whether that row exists
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * OUTS;
+  // weight row of the wave's i-th row, clamped into the matrix
   auto wrow = [&](int i) -> int64_t {
     const int64_t n = GLU ? n0 + i * a.N : n0 + i;
     return (GLU ? n0 < a.N : n < a.N) ? n : (GLU ? i * a.N + a.N - 1 : a.N - 1);
@@ -137,40 +146,82 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
 #pragma unroll
     for (int j = 0; j < NC; ++j) gv[j] = *reinterpret_cast<const uint4*>(norm_g + cc[j] * 8);
   }
+  // this lane's epilogue slot: token row m0 + e_mm, output row e_n
+  const int e_mm = lane / OUTS, e_i = lane % OUTS;
+  const int64_t e_n = n0 + e_i;
+  const bool e_on = e_mm < MG && e_n < a.N;
+  const int64_t e_nc = e_n < a.N ? e_n : a.N - 1;
+  const float bias = (!GLU && a.b) ? bf16_to_f32(a.b[e_nc]) : 0.f;
+  for (int m0 = 0; m0 < kMaxM; m0 += MG) {
+    if (m0 >= a.M) break;  // uniform
+    const int e_m = min(m0 + e_mm, a.M - 1);
+    const float res = (!GLU && a.res) ? bf16_to_f32(a.res[e_m * a.rs + e_nc]) : 0.f;
+    uint4 xg[MG][NC];
+    if constexpr (kShareNorm) {
+      for (int mm = wave; mm < MG; mm += 4) {
+        const uint16_t* xr = a.x + min(m0 + mm, a.M - 1) * a.xs;  // rows past M re-read the last one, unused
+        uint4 xv[NC];
 #pragma unroll
-  for (int m = 0; m < kMaxM; ++m) {
-    if (m < a.M) {
-      const uint16_t* xr = a.x + m * a.xs;
-      uint4 xv[NC];
-#pragma unroll
-      for (int j = 0; j < NC; ++j) xv[j] = *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
-      if constexpr (NORM) {
+        for (int j = 0; j < NC; ++j) xv[j] = *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j) ss += cin[j] ? sumsq8(xv[j]) : 0.f;
-        ss = wave_sum(ss);
-        const float rstd = 1.0f / sqrtf(ss / static_cast<float>(a.K) + norm_eps);
+        const float rstd = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.K) + norm_eps);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) xv[j] = norm_chunk(xv[j], gv[j], rstd);
+        for (int j = 0; j < NC; ++j) lx[(mm * NC + j) * kWave + lane] = norm_chunk(xv[j], gv[j], rstd);
       }
-      float t[R];
+      __syncthreads();
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        t[i] = 0.f;
+      for (int mm = 0; mm < MG; ++mm)
 #pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const float d = dot8_bf16(w[i][j], xv[j], 0.f);
-          t[i] += cin[j] ? d : 0.f;
+        for (int j = 0; j < NC; ++j) xg[mm][j] = lx[(mm * NC + j) * kWave + lane];
+      __syncthreads();  // the next group overwrites lx
+    } else {
+#pragma unroll
+      for (int mm = 0; mm < MG; ++mm) {
+        const uint16_t* xr = a.x + min(m0 + mm, a.M - 1) * a.xs;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) xg[mm][j] = *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
+      }
+    }
+    float keep = 0.f, keep_up = 0.f;
+#pragma unroll
+    for (int mm = 0; mm < MG; ++mm) {
+      if (m0 + mm < a.M) {  // uniform
+        uint4* xv = xg[mm];
+        if constexpr (NORM && !kShareNorm) {
+          float ss = 0.f;
+#pragma unroll
+          for (int j = 0; j < NC; ++j) ss += cin[j] ? sumsq8(xv[j]) : 0.f;
+          const float rstd = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.K) + norm_eps);
+#pragma unroll
+          for (int j = 0; j < NC; ++j) xv[j] = norm_chunk(xv[j], gv[j], rstd);
         }
-        t[i] = wave_sum(t[i]);  // every lane holds the sum
-      }
-      if constexpr (GLU) {
-        if (lane == 0 && n0 < a.N)
-          a.y[m * a.ys + n0] = f32_to_bf16(round_bf16(silu(round_bf16(t[0]))) * round_bf16(t[1]));
-      } else {
 #pragma unroll
-        for (int i = 0; i < R; ++i)  // lane i writes row n0 + i
-          if (lane == i && n0 + i < a.N) epilogue(a, m, n0 + i, t[i]);
+        for (int i = 0; i < R; ++i) {
+          float t = 0.f;
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            const float d = dot8_bf16(w[i][j], xv[j], 0.f);
+            t += cin[j] ? d : 0.f;
+          }
+          t = wave_sum(t);  // every lane holds the sum; the lane of its epilogue slot keeps it
+          if constexpr (GLU) {
+            if (e_mm == mm) (i == 0 ? keep : keep_up) = t;
+          } else {
+            if (e_mm == mm && e_i == i) keep = t;
+          }
+        }
+      }
+    }
+    const int m = m0 + e_mm;
+    if (e_on && m < a.M) {
+      if constexpr (GLU) {
+        a.y[m * a.ys + n0] = f32_to_bf16(round_bf16(silu(round_bf16(keep))) * round_bf16(keep_up));
+      } else {
+        float v = apply_act(a.b ? keep + bias : keep, a.act);
+        if (a.res) v = round_bf16(v) + res;
+        a.y[m * a.ys + e_n] = f32_to_bf16(v);
       }
     }
   }
@@ -220,12 +271,18 @@ __global__ __launch_bounds__(256) void small_linear_kernel(LinArgs a) {
   }
 }
 
-template <int NC, int R>
+template <int NC, int R, bool GLU, int MG>
+void launch_1pass_mg(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(GLU ? (a.N + 3) / 4 : (a.N + 4 * R - 1) / (4 * R)));
+  if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, true, GLU, MG>), grid, dim3(256), 0, st, a, g, eps);
+  else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, false, GLU, MG>), grid, dim3(256), 0, st, a, g, eps);
+}
+
+template <int NC, int R, bool GLU = false>
 int launch_1pass(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((a.N + 4 * R - 1) / (4 * R)));
-  if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, true>), grid, dim3(256), 0, st, a, g, eps);
-  else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, false>), grid, dim3(256), 0, st, a, g, eps);
-  return mm::check_launch("small_linear");
+  if (a.M == 1) launch_1pass_mg<NC, R, GLU, 1>(a, g, eps, st);
+  else launch_1pass_mg<NC, R, GLU, row_group(NC)>(a, g, eps, st);
+  return mm::check_launch(GLU ? "small_linear_glu" : "small_linear");
 }
 
 // R rows per wave when that still gives every CU a workgroup; one row per wave otherwise.
@@ -300,10 +357,7 @@ namespace {
 
 template <int NC>
 int launch_glu(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((a.N + 3) / 4));
-  if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, 2, true, true>), grid, dim3(256), 0, st, a, g, eps);
-  else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, 2, false, true>), grid, dim3(256), 0, st, a, g, eps);
-  return mm::check_launch("small_linear_glu");
+  return launch_1pass<NC, 2, true>(a, g, eps, st);
 }
 
 }  // namespace
