@@ -10,7 +10,8 @@ combine + residual, replayed from one hipGraph. `value` is tokens/s over exactly
 Also measured and reported under "extra": decode of 1 token (bf16) as a hipGraph step and per kernel,
 int8 decode at batch 1/2/4/8, the 2048-token Zipf prefill, and the full 28-layer synthetic decode step
 (+ LM head) in one hipGraph, and the Talker path (a 24-layer Qwen2-0.5B-shaped LLM decode step and its
-rotary / decode attention and silu_mul kernels). The roofline of the dominant kernel (prefill gate/up) is its algorithmic
+rotary / decode attention and silu_mul kernels), and the ingestion of one MoE layer's experts from
+safetensors shards into the stacked bf16 / int8 layout. The roofline of the dominant kernel (prefill gate/up) is its algorithmic
 bytes over its average duration from HIP events on its own stream; the CPU baseline is the oracle's
 torch path on a bounded sample of the same workload on this host.
 """
@@ -42,7 +43,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default="", help="comma list of extra workloads to run (decode,int8,zipf,full,talker)")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra workloads to run (decode,int8,zipf,full,talker,ingest)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 counter passes (traffic = null)")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
@@ -392,6 +394,94 @@ def talker_metrics(stream, layers=24, max_len=1024, pos=512):
             "silu_mul_us": silu_ms * 1e3}
 
 
+# ------------------------------------------------------------------------------------- expert ingestion
+
+def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=8):
+    """One thinker MoE layer's experts (64 routed + shared, bf16, 1.125 GB over 4 safetensors shards in a
+    temporary directory, so the reads come from the page cache) ingested into a bf16 stack and an int8 stack
+    (bf16 scales) with expert_load.load_stacked_experts; next to them the reference's method on the same
+    files (direct_load.py:109-131 + engine.py:130-135: threads pread each tensor into a bytearray, copy it
+    to the GPU from pageable memory, and quantise it there), and a pinned host-to-device copy of 1 GiB (the
+    link's practical ceiling)."""
+    import fused_moe
+    import expert_load as EL
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from ckpt_util import expert_tensors, write_checkpoint
+    from concurrent.futures import ThreadPoolExecutor
+    dev = torch.device("cuda")
+    pfx = "model.layers.1.mlp"
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR")) as tmp:
+        t = expert_tensors(pfx, n_experts, hidden, inter, seed=4000)
+        root = write_checkpoint(os.path.join(tmp, "ck"), t, shards=4, extra=False)
+        nbytes = sum(v.numel() * v.element_size() for v in t.values())
+        del t
+        E1 = n_experts + 1
+        bf = {"w_gu": torch.empty(E1, 2 * inter, hidden, dtype=torch.bfloat16, device=dev),
+              "w_d": torch.empty(E1, hidden, inter, dtype=torch.bfloat16, device=dev)}
+        q8 = {"q_gu": torch.empty(E1, 2 * inter, hidden, dtype=torch.int8, device=dev),
+              "q_d": torch.empty(E1, hidden, inter, dtype=torch.int8, device=dev),
+              "s_gu": torch.empty(E1, 2 * inter, dtype=torch.bfloat16, device=dev),
+              "s_d": torch.empty(E1, hidden, dtype=torch.bfloat16, device=dev)}
+        idx = EL.checkpoint_index(root)
+
+        def timed(fn, reps=3):
+            fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+            return sorted(ts)[len(ts) // 2]
+
+        t_bf = timed(lambda: EL.load_stacked_experts(idx, pfx, n_experts, out=bf, threads=threads))
+        t_q8 = timed(lambda: EL.load_stacked_experts(idx, pfx, n_experts, int8=True, out=q8, threads=threads))
+
+        items = EL.expert_items(idx, pfx, n_experts)
+        hdr = {p_: EL.read_header(p_) for p_ in set(idx.values())}
+        jobs = sorted((idx[k], hdr[idx[k]][k][2], hdr[idx[k]][k][3] - hdr[idx[k]][k][2], part, slot, hdr[idx[k]][k][1])
+                      for k, part, slot in items)
+        groups = [jobs[i::threads] for i in range(threads)]
+
+        def ref_method(int8):
+            def work(group):
+                st = torch.cuda.Stream()
+                with torch.cuda.stream(st):
+                    for path, off, n, part, slot, shape in group:
+                        fd = os.open(path, os.O_RDONLY)
+                        buf = bytearray(n)
+                        mv, got = memoryview(buf), 0
+                        while got < n:
+                            got += os.preadv(fd, [mv[got:]], off + got)
+                        os.close(fd)
+                        src = torch.frombuffer(buf, dtype=torch.bfloat16).reshape(shape)
+                        r0 = inter if part == 1 else 0
+                        if int8:
+                            qq, ss = fused_moe.quantize_rows_int8(src.to(dev), scale_dtype=torch.bfloat16)
+                            qd, sd = (q8["q_d"], q8["s_d"]) if part == 2 else (q8["q_gu"], q8["s_gu"])
+                            qd[slot, r0:r0 + qq.shape[0]].copy_(qq)
+                            sd[slot, r0:r0 + qq.shape[0]].copy_(ss)
+                        else:
+                            (bf["w_d"][slot] if part == 2 else bf["w_gu"][slot, r0:r0 + shape[0]]).copy_(src)
+                    st.synchronize()
+            with ThreadPoolExecutor(threads) as ex:
+                list(ex.map(work, groups))
+
+        t_ref_bf = timed(lambda: ref_method(False))
+        t_ref_q8 = timed(lambda: ref_method(True))
+    pinned = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    t_h2d = timed(lambda: dst.copy_(pinned, non_blocking=True))
+    del pinned, dst, bf, q8
+    torch.cuda.empty_cache()
+    gbs = lambda sec: nbytes / sec / 1e9  # noqa: E731
+    return {"file_bytes": nbytes, "threads": threads, "bf16_s": t_bf, "bf16_GBs": gbs(t_bf), "int8_s": t_q8,
+            "int8_GBs": gbs(t_q8), "reference_method_bf16_GBs": gbs(t_ref_bf),
+            "reference_method_int8_GBs": gbs(t_ref_q8), "pinned_h2d_GBs": (1 << 30) / t_h2d / 1e9,
+            "source": "page cache (files just written)"}
+
+
 # -------------------------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(b, bias, n_sample=64, reps=2):
@@ -470,6 +560,9 @@ def main():
         torch.cuda.empty_cache()
         extra["talker"] = talker_metrics(stream)
         log(f"[bench] talker: {extra['talker']}")
+    if want("ingest"):
+        extra["ingest"] = ingest_metrics()
+        log(f"[bench] ingest: {extra['ingest']}")
     gu_s = head["gate_up_us"] * 1e-6
     achieved = head["gate_up_bytes"] / gu_s / 1e9
     traffic = None

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 3
+#define MM_ABI_VERSION 4
 
 /* status codes */
 #define MM_OK 0
@@ -244,6 +244,36 @@ int mm_qwen_decode_attn(const void* qkv, int nh, int nkv, int hd, void* k_cache,
  * rows <= 65535; row strides in elements. */
 int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stride, void* out,
                 int64_t out_row_stride, void* stream);
+
+/* ---- Expert ingestion from safetensors shards (engine.py:126-188, direct_load.py:81-131). */
+
+#define MM_PART_GATE 0 /* rows 0..I-1 of w_gu[slot] */
+#define MM_PART_UP 1   /* rows I..2I-1 of w_gu[slot] */
+#define MM_PART_DOWN 2 /* w_d[slot] */
+
+/* One expert matrix in a file: `nbytes` bytes at absolute `offset` of `path` hold a row-major
+ * [rows, cols] tensor of src_dtype (MM_BF16 / MM_FP16 / MM_FP32). */
+typedef struct mm_ingest_item {
+  const char* path;
+  int64_t offset;
+  int64_t nbytes;
+  int32_t src_dtype;
+  int32_t part;
+  int64_t slot;
+  int64_t rows;
+  int64_t cols;
+} mm_ingest_item;
+
+/* Reads every item and writes it into the stack `dst`: as bf16 (fp16 / fp32 file data rounded to nearest
+ * even), or, when dst->w_dtype is MM_INT8, quantised per row as mm_quantize_rows_int8 does (scales in
+ * dst->s_dtype). Replaces the per-tensor loader hooks of engine.py:126-147 (quantize-on-load) and the
+ * restacking of engine.py:150-188 / 343-361. n_threads workers read with pread in file order, each through
+ * two pinned host slots and one device slot of slot_bytes (host_staging: 2 * n_threads * slot_bytes of
+ * pinned host memory; dev_staging: n_threads * slot_bytes of device memory; slot_bytes >= every item's
+ * nbytes). Blocking: returns when every matrix is in place, on streams of its own; the caller finishes its
+ * own work on dst before the call. Shapes must match the stack: gate / up [inter, hidden], down [hidden, inter]. */
+int mm_ingest_experts(const mm_ingest_item* items, int64_t n_items, const mm_experts* dst, void* host_staging,
+                      void* dev_staging, int64_t slot_bytes, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -16,13 +16,22 @@ MM_OK, MM_ERR_ARG, MM_ERR_HIP = 0, 1, 2
 MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
 
 # exported entry points and their argument types (include/mingmoe.h)
 _P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+
+MM_PART_GATE, MM_PART_UP, MM_PART_DOWN = 0, 1, 2
+
+
+class IngestItem(ctypes.Structure):
+    """mm_ingest_item: one expert matrix in a file (path, absolute byte offset and size, dtype, where it goes)."""
+    _fields_ = [("path", ctypes.c_char_p), ("offset", _I64), ("nbytes", _I64), ("src_dtype", ctypes.c_int32),
+                ("part", ctypes.c_int32), ("slot", _I64), ("rows", _I64), ("cols", _I64)]
 
 
 class Experts(ctypes.Structure):
@@ -55,6 +64,7 @@ SIGNATURES = {
                         ctypes.c_int),
     "mm_small_linear_glu": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _I64, _P], ctypes.c_int),
     "mm_quantize_rows_int8": ([_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P], ctypes.c_int),
+    "mm_ingest_experts": ([ctypes.POINTER(IngestItem), _I64, ctypes.POINTER(Experts), _P, _P, _I64, _I32], ctypes.c_int),
     "mm_rope_attn": ([_P, _I64, _I64, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
     "mm_decode_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),
     "mm_qwen_decode_attn": ([_P, _I32, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F32, _P, _P, _I64, _P],

@@ -90,6 +90,18 @@ def test_argument_validation_reports_messages():
                                                             need, None))
     assert "row stride" in _err(lib.mm_silu_mul(P, 1, 4864, 4864, P, 4864, None))
     assert "up to 8192" in _err(lib.mm_small_linear_glu(P, 1, 9216, 9216, P, 64, 9216, None, 0.0, P, 64, None))
+    ex = mm.Experts()
+    ex.w_gu, ex.w_d, ex.w_dtype, ex.n_slots, ex.hidden, ex.inter = 16, 16, mm.MM_BF16, 5, 256, 128
+    ex.gu_stride_e, ex.gu_stride_n, ex.d_stride_e, ex.d_stride_n = 256 * 256, 256, 256 * 128, 128
+    items = (mm.IngestItem * 1)(mm.IngestItem(b"/nonexistent", 0, 128 * 256 * 2, mm.MM_BF16, mm.MM_PART_DOWN, 0,
+                                              128, 256))
+    assert "does not fit the stack" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
+    items[0] = mm.IngestItem(b"/nonexistent", 0, 1000, mm.MM_BF16, mm.MM_PART_GATE, 0, 128, 256)
+    assert "bytes for a" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
+    items[0] = mm.IngestItem(b"/nonexistent", 0, 128 * 256 * 2, mm.MM_BF16, mm.MM_PART_GATE, 5, 128, 256)
+    assert "slot 5" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
+    ex.w_dtype = mm.MM_INT8
+    assert "needs fp32 or bf16 scales" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
 
 
 def test_wrappers_refuse_cpu_tensors():
