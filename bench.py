@@ -396,7 +396,7 @@ def talker_metrics(stream, layers=24, max_len=1024, pos=512):
 
 # ------------------------------------------------------------------------------------- expert ingestion
 
-def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=8):
+def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=4, ref_threads=8):
     """One thinker MoE layer's experts (64 routed + shared, bf16, 1.125 GB over 4 safetensors shards in a
     temporary directory, so the reads come from the page cache) ingested into a bf16 stack and an int8 stack
     (bf16 scales) with expert_load.load_stacked_experts; next to them the reference's method on the same
@@ -442,7 +442,7 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=8):
         hdr = {p_: EL.read_header(p_) for p_ in set(idx.values())}
         jobs = sorted((idx[k], hdr[idx[k]][k][2], hdr[idx[k]][k][3] - hdr[idx[k]][k][2], part, slot, hdr[idx[k]][k][1])
                       for k, part, slot in items)
-        groups = [jobs[i::threads] for i in range(threads)]
+        groups = [jobs[i::ref_threads] for i in range(ref_threads)]  # direct_load.py's default of 8 workers
 
         def ref_method(int8):
             def work(group):
@@ -465,7 +465,7 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=8):
                         else:
                             (bf["w_d"][slot] if part == 2 else bf["w_gu"][slot, r0:r0 + shape[0]]).copy_(src)
                     st.synchronize()
-            with ThreadPoolExecutor(threads) as ex:
+            with ThreadPoolExecutor(ref_threads) as ex:
                 list(ex.map(work, groups))
 
         t_ref_bf = timed(lambda: ref_method(False))
@@ -476,7 +476,7 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=8):
     del pinned, dst, bf, q8
     torch.cuda.empty_cache()
     gbs = lambda sec: nbytes / sec / 1e9  # noqa: E731
-    return {"file_bytes": nbytes, "threads": threads, "bf16_s": t_bf, "bf16_GBs": gbs(t_bf), "int8_s": t_q8,
+    return {"file_bytes": nbytes, "threads": threads, "reference_threads": ref_threads, "bf16_s": t_bf, "bf16_GBs": gbs(t_bf), "int8_s": t_q8,
             "int8_GBs": gbs(t_q8), "reference_method_bf16_GBs": gbs(t_ref_bf),
             "reference_method_int8_GBs": gbs(t_ref_q8), "pinned_h2d_GBs": (1 << 30) / t_h2d / 1e9,
             "source": "page cache (files just written)"}

@@ -156,7 +156,9 @@ void worker(int dev, int t, const mm_ingest_item* items, const int64_t* order, i
     const Dest d = dest_of(ex, it);
     const bool direct = ex.w_dtype == MM_BF16 && it.src_dtype == MM_BF16;
     hipError_t e = hipSuccess;
-    if (direct) {
+    if (direct && d.row_stride == it.cols) {  // the matrix is one contiguous block of the stack
+      e = hipMemcpyAsync(d.base, hslot[b], it.nbytes, hipMemcpyHostToDevice, st);
+    } else if (direct) {
       e = hipMemcpy2DAsync(d.base, d.row_stride * 2, hslot[b], it.cols * 2, it.cols * 2, it.rows,
                            hipMemcpyHostToDevice, st);
     } else {

@@ -78,13 +78,14 @@ def expert_items(index, prefix, n_experts, shared=True):
 
 
 def load_stacked_experts(index, prefix, n_experts, *, shared=True, int8=False, scale_dtype=torch.bfloat16,
-                         device="cuda", out=None, threads=8):
+                         device="cuda", out=None, threads=4):
     """Reads the MoE block `prefix`'s experts from the checkpoint `index` ({key: file}, or a model directory)
     into stacked tensors on `device`: {"w_gu": [E1, 2I, H], "w_d": [E1, H, I]} in bf16, or with int8=True
     {"q_gu", "q_d" (int8), "s_gu": [E1, 2I], "s_d": [E1, H] (scale_dtype)}, E1 = n_experts + 1 with the shared
     expert. `out` may hold those tensors already (for example the views a model's MoE block owns); they are
     filled in place. int8 rows are quantised as quantize_rows_int8 does; fp16 / fp32 file data is rounded
-    to bf16. Blocks until the stack is complete."""
+    to bf16. Blocks until the stack is complete. `threads` readers (4 measured best on MI355X: 53-54 GB/s of
+    page-cached file data, 93 % of the pinned host-to-device copy rate)."""
     if isinstance(index, (str, os.PathLike)):
         index = checkpoint_index(index)
     items = expert_items(index, prefix, n_experts, shared)
@@ -112,11 +113,11 @@ def load_stacked_experts(index, prefix, n_experts, *, shared=True, int8=False, s
         else:
             out = {"w_gu": torch.empty(E1, 2 * I, H, dtype=torch.bfloat16, device=dev),
                    "w_d": torch.empty(E1, H, I, dtype=torch.bfloat16, device=dev)}
+    _mm.require_gpu(*out.values())
     if int8:
         ex = _mm.experts(out["q_gu"], out["q_d"], out["s_gu"], out["s_d"])
     else:
         ex = _mm.experts(out["w_gu"], out["w_d"])
-    _mm.require_gpu(*out.values())
     if ex.inter != I or ex.hidden != H:
         raise ValueError(f"the stack holds I={ex.inter}, H={ex.hidden}; the checkpoint has I={I}, H={H}")
     arr = (_mm.IngestItem * len(rows))()
