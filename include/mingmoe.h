@@ -186,7 +186,7 @@ int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, 
  * x, w, b, residual, norm_g, y: bf16. norm_g (optional): RMSNorm prologue with norm_eps,
  * x -> bf16(bf16(x * rstd) * g). b, residual, norm_g may be NULL. act: MM_ACT_*.
  * xn_buf: bf16 scratch [M, K], used only when a norm prologue is given and K > 8192 (may be NULL otherwise);
- * shorter rows get the norm fused into the GEMV. */
+ * shorter rows get the norm fused into the GEMV. x_row_stride 0 repeats one activation row M times. */
 int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride,
                     const void* w, int64_t N, int64_t w_row_stride,
                     const void* b, int act, const void* residual, int64_t res_row_stride,
@@ -238,6 +238,13 @@ int64_t mm_decode_attn_workspace(int nh, int hd, int64_t max_len);
 int mm_qwen_decode_attn(const void* qkv, int nh, int nkv, int hd, void* k_cache, void* v_cache, int64_t max_len,
                         const void* pos, int pos_dtype, const float* inv_freq, float scale, void* out,
                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The flow-matching update of the Talker tail in one kernel: y_out = y + (pred + (pred - null) * cfg) * dt
+ * with bf16 rounding after every operation, as the bf16 torch expression of fast_talker.py:151-152 rounds.
+ * y, y_out: bf16 [n] (may alias); pred_null: bf16, rows pred and null `pn_row_stride` elements apart;
+ * dt: device scalar (MM_BF16 or MM_FP32). No counterpart kernel in the reference (five torch launches). */
+int mm_cfg_update(const void* y, const void* pred_null, int64_t pn_row_stride, int64_t n, float cfg, const void* dt,
+                  int dt_dtype, void* y_out, void* stream);
 
 /* out = bf16(bf16(silu(g)) * u) for rows of gu = [g | u], each 2*inter wide.
  * Replaces fast_talker._silu_mul (fast_talker.py:215-222, launched at :259-260). gu, out bf16;

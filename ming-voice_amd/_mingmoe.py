@@ -70,6 +70,7 @@ SIGNATURES = {
     "mm_qwen_decode_attn": ([_P, _I32, _I32, _I32, _P, _P, _I64, _P, _I32, _P, _F32, _P, _P, _I64, _P],
                             ctypes.c_int),
     "mm_silu_mul": ([_P, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
+    "mm_cfg_update": ([_P, _P, _I64, _I64, _F32, _P, _I32, _P, _P], ctypes.c_int),
 }
 
 _lib = None

@@ -313,7 +313,8 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
   MM_REQUIRE(N <= 0x7fffffffLL * 8, "small_linear: N too large");
   MM_REQUIRE(x && w && y, "small_linear: null pointer");
   MM_REQUIRE(act == MM_ACT_NONE || act == MM_ACT_GELU_TANH || act == MM_ACT_SILU, "small_linear: unknown act %d", act);
-  MM_REQUIRE(x_row_stride >= K && w_row_stride >= K && y_row_stride >= N, "small_linear: row stride too small");
+  MM_REQUIRE((x_row_stride >= K || x_row_stride == 0) && w_row_stride >= K && y_row_stride >= N,
+             "small_linear: row stride too small (x rows may also repeat one row, stride 0)");
   MM_REQUIRE(!residual || res_row_stride >= N, "small_linear: residual row stride too small");
   MM_REQUIRE(mm::aligned16(w) && (w_row_stride * 2) % 16 == 0, "small_linear: weight rows must be 16-byte aligned");
   hipStream_t st = MM_STREAM(stream);

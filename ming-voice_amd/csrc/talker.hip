@@ -434,7 +434,34 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   out[blockIdx.y * os + i] = f32_to_bf16(g * bf16_to_f32(row[I + i]));
 }
 
+// ------------------------------------------------------------------------------------------ CFG update
+
+// y_out = bf16(y + bf16(bf16(pred + bf16(bf16(pred - null) * cfg)) * dt)): the bf16 torch expression
+// y + (pred + (pred - null) * cfg) * dt (fast_talker.py:151-152), one rounding per operation.
+__global__ __launch_bounds__(256) void cfg_update_kernel(const uint16_t* __restrict__ y, const uint16_t* __restrict__ pn,
+                                                         int64_t ps, int64_t n, float cfg, const void* __restrict__ dt,
+                                                         int dt_dtype, uint16_t* y_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float d = dt_dtype == MM_FP32 ? *static_cast<const float*>(dt) : bf16_to_f32(*static_cast<const uint16_t*>(dt));
+  const float pred = bf16_to_f32(pn[i]), null = bf16_to_f32(pn[ps + i]);
+  const float t = round_bf16(round_bf16(pred + round_bf16(round_bf16(pred - null) * cfg)) * d);
+  y_out[i] = f32_to_bf16(bf16_to_f32(y[i]) + t);
+}
+
 }  // namespace
+
+extern "C" int mm_cfg_update(const void* y, const void* pred_null, int64_t pn_row_stride, int64_t n, float cfg,
+                             const void* dt, int dt_dtype, void* y_out, void* stream) {
+  MM_REQUIRE(y && pred_null && dt && y_out, "cfg_update: null pointer");
+  MM_REQUIRE(n >= 1 && n <= (1LL << 31) && pn_row_stride >= n, "cfg_update: n=%lld, pred/null row stride %lld",
+             (long long)n, (long long)pn_row_stride);
+  MM_REQUIRE(dt_dtype == MM_BF16 || dt_dtype == MM_FP32, "cfg_update: dt must be bf16 or fp32");
+  hipLaunchKernelGGL(cfg_update_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, MM_STREAM(stream),
+                     static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(pred_null), pn_row_stride, n, cfg, dt,
+                     dt_dtype, static_cast<uint16_t*>(y_out));
+  return mm::check_launch("cfg_update");
+}
 
 extern "C" int mm_rope_attn(const void* qkv, int64_t batch, int64_t seq, int64_t dim, int heads, const float* cos_t,
                             const float* sin_t, void* out, void* stream) {

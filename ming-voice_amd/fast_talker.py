@@ -22,7 +22,7 @@ import torch.nn.functional as F
 import _mingmoe as _mm
 from fastlinear import small_linear
 
-__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "gate_up_silu", "FastQwen2Step", "FastTail",
+__all__ = ["rope_attn", "qwen_decode_attn", "silu_mul", "gate_up_silu", "cfg_update", "FastQwen2Step", "FastTail",
            "decode_attn_workspace"]
 
 
@@ -117,6 +117,28 @@ def silu_mul(gu, out=None):
     with _mm.on_device(gu):
         _mm.check(lib.mm_silu_mul(_mm.ptr(g2), g2.shape[0], I, g2.stride(0), _mm.ptr(o2), o2.stride(0),
                                   _mm.stream_of(gu)), "silu_mul")
+    return out
+
+
+def cfg_update(y, pred_null, cfg, dt, out=None):
+    """y + (pred + (pred - null) * cfg) * dt for bf16 y [1, L], pred_null [2, L] (rows pred, null) and a
+    one-element dt tensor, rounded to bf16 after every operation exactly as the torch expression of
+    fast_talker.py:151-152 is, in one kernel. Returns out (a new [1, L] tensor by default; may be y)."""
+    _mm.require_gpu(y, pred_null, dt, out)
+    L = y.shape[-1]
+    if y.dtype != torch.bfloat16 or pred_null.dtype != torch.bfloat16 or y.numel() != L or not y.is_contiguous():
+        raise ValueError("cfg_update: y must be a contiguous bf16 [1, L] row and pred_null bf16")
+    if pred_null.dim() != 2 or pred_null.shape[0] != 2 or pred_null.shape[1] != L or pred_null.stride(1) != 1:
+        raise ValueError(f"cfg_update: pred_null must be [2, {L}] with a contiguous last dim")
+    # a bf16 dt (any one-element shape) or a 0-dim fp32 dt keep the expression in bf16; a [1] fp32 dt would
+    # promote it to fp32 in torch, which this kernel does not reproduce
+    if dt.numel() != 1 or not (dt.dtype == torch.bfloat16 or (dt.dtype == torch.float32 and dt.dim() == 0)):
+        raise ValueError("cfg_update: dt must be a one-element bf16 tensor or a 0-dim fp32 tensor")
+    out = torch.empty_like(y) if out is None else out
+    lib = _mm.load()
+    with _mm.on_device(y):
+        _mm.check(lib.mm_cfg_update(_mm.ptr(y), _mm.ptr(pred_null), pred_null.stride(0), L, float(cfg), _mm.ptr(dt),
+                                    _mm.dtype_code(dt), _mm.ptr(out), _mm.stream_of(y)), "cfg_update")
     return out
 
 
@@ -215,6 +237,7 @@ class FastTail:
         self.dts = [d.reshape(1) for d in dts]
         with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
             self.t_emb = [dit.t_embedder(ts[i].reshape(1)).to(torch.bfloat16) for i in range(len(self.dts))]
+            self.t_emb_all = torch.cat(self.t_emb, 0)  # [steps, D]
             self.cls = agg.word_embedder(torch.zeros(1, 1, dtype=torch.long, device=dev)).to(torch.bfloat16)
         self.c_w, self.c_b = dit.c_embedder.cond_embedder.weight, dit.c_embedder.cond_embedder.bias
         self.null_c = self.c_b.reshape(1, -1)  # the condition embedder of a zero condition is its bias
@@ -232,17 +255,21 @@ class FastTail:
 
     def __call__(self, hidden, hist, noise):
         D = self.x_w.shape[0]
+        steps = len(self.dts)
         cond = torch.cat([small_linear(hidden.reshape(1, -1), self.c_w, self.c_b), self.null_c], 0)  # [2, D]
-        h_emb = small_linear(hist.reshape(1, -1), self.x_w, self.x_b).expand(2, D)
+        # the DiT input of every step, [steps, 2, 3, D]: condition + timestep, history, current latent; the
+        # first two are known now, the latent slot is written by the x_embedder at each step
+        hs = torch.empty(steps, 2, 3, D, device=cond.device, dtype=cond.dtype)
+        torch.add(cond[None], self.t_emb_all[:, None], out=hs[:, :, 0])
+        hs[:, :, 1] = small_linear(hist.reshape(1, -1), self.x_w, self.x_b)
         y = noise.reshape(1, -1)
         for i, dt in enumerate(self.dts):
-            y_emb = small_linear(y, self.x_w, self.x_b).expand(2, D)
-            h = torch.stack([cond + self.t_emb[i], h_emb, y_emb], 1)  # [2, 3, D]
+            small_linear(y.expand(2, -1), self.x_w, self.x_b, out=hs[i, :, 2])  # both rows at once
+            h = hs[i]
             for blk in self.blocks:
                 h = blk(h, self.cos3, self.sin3)
-            out = small_linear(h[:, -1], self.f_w, self.f_b, norm=self.f_norm)  # [2, latent]
-            pred, null = out[0:1], out[1:2]
-            y = y + (pred + (pred - null) * self.cfg) * dt
+            out = small_linear(h[:, -1], self.f_w, self.f_b, norm=self.f_norm)  # [2, latent]: pred, null
+            y = cfg_update(y, out, self.cfg, dt)  # y + (pred + (pred - null) * cfg) * dt
         Da = self.a_x_w.shape[0]
         a = torch.stack([self.cls.reshape(1, Da), small_linear(y, self.a_x_w, self.a_x_b)], 1)  # [1, 2, Da]
         for blk in self.a_blocks:

@@ -318,6 +318,19 @@ def test_fast_tail_matches_oracle():
         assert abs(stop.item() - w_stop.item()) < 1e-2
 
 
+@pytest.mark.parametrize("L,dt_dtype", [(64, torch.bfloat16), (1000, torch.float32), (1, torch.bfloat16)])
+def test_cfg_update_equals_the_torch_expression(L, dt_dtype):
+    g = torch.Generator().manual_seed(L)
+    y = torch.randn(1, L, generator=g).to(BF).to(DEV)
+    out = torch.randn(2, L, generator=g).to(BF).to(DEV)
+    dt = torch.tensor([0.1015625] if dt_dtype == BF else 0.1015625, dtype=dt_dtype, device=DEV)
+    got = FT.cfg_update(y, out, 2.0, dt)
+    pred, null = out[0:1], out[1:2]
+    want = y + (pred + (pred - null) * 2.0) * dt
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_fast_tail_graph_replays_match_eager():
     """The tail captured once and replayed on new inputs equals eager calls bit for bit (the engine replays
     it from a graph, engine.py:1412-1414)."""
