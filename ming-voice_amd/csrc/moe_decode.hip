@@ -1,13 +1,17 @@
 // Decode MoE for 1..8 tokens (fused_moe.py:13-83): expert-gathered GEMV pair, HBM-bound.
 //
-// Kernel A (gate/up): grid (row tiles of I, distinct experts). Each workgroup finds the distinct experts of
-// the batch from the ids (in first-appearance order), takes the one given by blockIdx.y, and streams its
-// gate and up rows once with 16-byte loads, dotting them with every token routed to that expert.
+// Kernel A (gate/up): grid (row tiles of I, slots of the batch). The workgroup of slot u reads the slot's
+// expert with one scalar load and streams its gate and up rows once with 16-byte buffer loads, dotting them
+// with the token (one token: per slot; a batch: the first slot of each distinct expert takes every token
+// routed there, staged in LDS).
 //   a[p, r] = bf16(bf16(silu(bf16(g))) * bf16(u)),  g/u = x_t . row (* row scale for int8)
-// Kernel B (down + combine): grid (row tiles of H). Each wave streams the down rows of one distinct
-// expert for the tile, dots them with a[p] of every pair routed there, rounds to bf16 (after the row
-// scale for int8) and parks the result in LDS; the workgroup then sums over slots in order per token:
+// Kernel B (down + combine): grid (row tiles of H). Each wave streams the tile's down rows of one slot's
+// expert, dots them with a[p] of the pairs routed there, rounds to bf16 (after the row scale for int8)
+// and parks the result in LDS; the workgroup then sums over slots in order per token:
 //   y[t, h] = bf16(sum_k wts[t,k] * part[t*nk+k, h]) (+ residual, rounded again)
+// Both kernels keep each lane's loads back to back: buffer loads return zero past a row's end (no branch
+// or mask per load), the combine's operands are fetched at kernel start without a wait, and the one-token
+// instances fit 64 VGPRs, so a whole grid is resident at once (8 waves per SIMD).
 #include "mm_common.h"
 #include "mm_select.h"
 
@@ -16,6 +20,7 @@ namespace {
 using namespace mmd;
 
 constexpr int kMaxPairs = 64;
+
 
 struct DecodeArgs {
   const uint16_t* x;
@@ -41,32 +46,24 @@ struct DecodeArgs {
   int64_t ys;
 };
 
-// Distinct experts of the batch. Lane p < P holds pair p's expert; returns the expert of distinct slot u
-// (or -1 when the batch has fewer distinct experts) and the mask of pairs routed to it. Distinct experts
-// are enumerated in first-appearance order: the lowest remaining lane leads, and one ballot takes every
-// pair of its expert (one readlane + one ballot per distinct expert, no per-pair shuffles).
-__device__ __forceinline__ int distinct_expert(const DecodeArgs& a, int u, unsigned long long& pairs) {
+// ------------------------------------------------------------------------------------------- pairs
+//
+// Slot u = t * nk + k is pair u of the batch. With one token every slot is computed on its own (a
+// repeated expert is streamed once per slot: exact, and free of any cross-lane bookkeeping before the
+// weight loads). With several tokens a slot is handled only when it is the first of its expert, together
+// with every later pair routed there, so each distinct expert is streamed once.
+
+// Slot u's expert, read at a wave-uniform address (a scalar load), or -1 for an id outside [0, E1).
+__device__ __forceinline__ int slot_expert(const DecodeArgs& a, int u) {
+  const int t = u / a.nk, k = u - t * a.nk;
+  const int64_t id = load_id(a.ids, a.ids_dtype, t * a.ids_rs + k);
+  return (id < 0 || id >= a.E1) ? -1 : static_cast<int>(id);
+}
+
+// Lane p < P holds pair p's expert; other lanes hold -1.
+__device__ __forceinline__ int lane_pair_expert(const DecodeArgs& a) {
   const int lane = lane_id();
-  int64_t id = -1;
-  if (lane < a.P) {
-    const int t = lane / a.nk, k = lane - t * a.nk;
-    id = load_id(a.ids, a.ids_dtype, t * a.ids_rs + k);
-    if (id < 0 || id >= a.E1) id = -1;
-  }
-  const int my = static_cast<int>(id);
-  unsigned long long remaining = __ballot(my >= 0);
-  for (int i = 0; remaining; ++i) {
-    const int leader = __ffsll(static_cast<long long>(remaining)) - 1;
-    const int e = __builtin_amdgcn_readlane(my, leader);
-    const unsigned long long same = __ballot(my == e);
-    if (i == u) {
-      pairs = same;
-      return e;
-    }
-    remaining &= ~same;
-  }
-  pairs = 0ull;
-  return -1;
+  return lane < a.P ? slot_expert(a, lane) : -1;
 }
 
 // 16-byte chunk c of a weight row holds CE elements; the matching activation chunk is CE bf16 values.
@@ -75,16 +72,39 @@ struct Act {
   uint4 v[Q ? 2 : 1];
 };
 
+__device__ __forceinline__ uint4 and_mask(const uint4& v, uint32_t m) {
+  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
+
+// Chunk c of an LDS row; a lane past the row (ok false) reads the row's first chunk and zeroes it.
 template <bool Q>
-__device__ __forceinline__ void load_act(Act<Q>& o, const uint16_t* row, int64_t c, bool ok) {
-  if (!ok) {
-    o.v[0] = make_uint4(0, 0, 0, 0);
-    if (Q) o.v[Q ? 1 : 0] = make_uint4(0, 0, 0, 0);
-    return;
-  }
-  const uint4* p = reinterpret_cast<const uint4*>(row + c * (Q ? 16 : 8));
-  o.v[0] = p[0];
-  if (Q) o.v[Q ? 1 : 0] = p[1];
+__device__ __forceinline__ void lds_act(Act<Q>& o, const uint16_t* row, int64_t c, bool ok) {
+  const uint4* p = reinterpret_cast<const uint4*>(row) + (ok ? c : 0) * (Q ? 2 : 1);
+  const uint32_t m = ok ? ~0u : 0u;
+  o.v[0] = and_mask(p[0], m);
+  if (Q) o.v[Q ? 1 : 0] = and_mask(p[1], m);
+}
+
+// Global operands are read through buffer resources (a wave-uniform base and byte size): a load at an
+// offset past the end returns zero, so a lane past a row's end is given kPast as its offset instead of a
+// branch or a mask, and all of a lane's loads issue back to back.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kPast = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
+// Activation chunk c (CE bf16 values) of the row starting at byte `row` of resource r; kPast when !ok.
+template <bool Q>
+__device__ __forceinline__ void buf_act(Act<Q>& o, rsrc_t r, uint32_t row, int64_t c, bool ok) {
+  const uint32_t off = ok ? row + static_cast<uint32_t>(c) * (Q ? 32u : 16u) : kPast;
+  o.v[0] = buf16(r, off);
+  if (Q) o.v[Q ? 1 : 0] = buf16(r, off + 16u);
 }
 
 template <bool Q>
@@ -93,27 +113,34 @@ __device__ __forceinline__ float dot_chunk(const uint4& w, const Act<Q>& x, floa
   else return dot8_bf16(w, x.v[0], acc);
 }
 
-__device__ __forceinline__ uint4 load_w(const void* base, int64_t byte_off, bool ok) {
-  if (!ok) return make_uint4(0, 0, 0, 0);
-  return *reinterpret_cast<const uint4*>(static_cast<const char*>(base) + byte_off);
-}
-
 // ------------------------------------------------------------------------------------------- kernel A
 
-// Epilogue of one gate/up row pair for one pair p: scales (int8), bf16 rounding points, SiLU, product.
+// Epilogue of one gate/up row pair for one pair p: scales (int8, fetched with the weights), bf16 rounding
+// points, SiLU, product.
 template <bool Q>
-__device__ __forceinline__ void gate_up_store(const DecodeArgs& a, int e, int64_t r, int p, float ag, float au) {
+__device__ __forceinline__ void gate_up_store(const DecodeArgs& a, int64_t r, int p, float ag, float au, float sg,
+                                              float su) {
   if (Q) {
-    ag *= load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + r);
-    au *= load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + a.I + r);
+    ag *= sg;
+    au *= su;
   }
   const float gg = round_bf16(ag), uu = round_bf16(au);
   const float act = round_bf16(silu(gg));
   a.a_buf[static_cast<int64_t>(p) * a.I + r] = f32_to_bf16(act * uu);
 }
 
-// One token per expert (batch 1, or a batch whose tokens chose distinct experts): the token's activation
-// chunks stay in registers for all rows of the wave.
+// The int8 row scales of gate row r and up row r + I of expert e (1 for bf16 weights).
+template <bool Q>
+__device__ __forceinline__ void gate_up_scales(const DecodeArgs& a, int e, int64_t r, bool rok, float& sg, float& su) {
+  sg = su = 1.f;
+  if (Q) {
+    const int64_t base = static_cast<int64_t>(e) * a.sgu_se + (rok ? r : 0);
+    sg = load_scale(a.s_gu, a.s_dtype, base);
+    su = load_scale(a.s_gu, a.s_dtype, base + a.I);
+  }
+}
+
+// One token for one expert: the token's activation chunks stay in registers for all rows of the wave.
 template <bool Q, int LPR, int NC, int R>
 __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, const char* wbase, int64_t row0) {
   constexpr int ES = Q ? 1 : 2;
@@ -122,28 +149,34 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
   const int g = lane / LPR, s = lane % LPR;
   const int64_t nch = a.H * ES / 16;
   const int tok = p / a.nk;
-  float accg[R], accu[R];
+  float accg[R], accu[R], sg[R], su[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) accg[i] = accu[i] = 0.f;
+  const uint32_t rowb = static_cast<uint32_t>(a.gu_sn * ES);
+  const rsrc_t wr = make_rsrc(wbase, 2 * a.I * a.gu_sn * ES);
+  const rsrc_t xr = make_rsrc(a.x, static_cast<int64_t>(a.n_tokens) * a.xs * 2);
+  const uint32_t xrow = static_cast<uint32_t>(tok * a.xs * 2);
   for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {  // one pass unless H is long
-    Act<Q> xa[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
-      load_act<Q>(xa[j], a.x + tok * a.xs, c, c < nch);
-    }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
       const bool rok = r < a.I;
+      const uint32_t goff = static_cast<uint32_t>(r) * rowb, uoff = static_cast<uint32_t>(r + a.I) * rowb;
       uint4 wg[NC], wu[NC];
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
         const bool ok = rok && c < nch;
-        wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
-        wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
+        wg[j] = buf16(wr, ok ? goff + static_cast<uint32_t>(c) * 16u : kPast);
+        wu[j] = buf16(wr, ok ? uoff + static_cast<uint32_t>(c) * 16u : kPast);
       }
+      Act<Q> xa[NC];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
+        buf_act<Q>(xa[j], xr, xrow, c, c < nch);
+      }
+      if (c0 == 0) gate_up_scales<Q>(a, e, r, rok, sg[i], su[i]);  // issued behind the weights
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         accg[i] = dot_chunk<Q>(wg[j], xa[j], accg[i]);
@@ -155,7 +188,7 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
   for (int i = 0; i < R; ++i) {
     const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
     const float ag = group_sum<LPR>(accg[i]), au = group_sum<LPR>(accu[i]);
-    if (s == 0 && r < a.I) gate_up_store<Q>(a, e, r, p, ag, au);
+    if (s == 0 && r < a.I) gate_up_store<Q>(a, r, p, ag, au, sg[i], su[i]);
   }
 }
 
@@ -183,13 +216,18 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
   for (int i = 0; i < R; ++i) {
     const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
     const bool rok = r < a.I;
+    float sg, su;
+    gate_up_scales<Q>(a, e, r, rok, sg, su);
+    const uint32_t rowb = static_cast<uint32_t>(a.gu_sn * ES);
+    const rsrc_t wr = make_rsrc(wbase, 2 * a.I * a.gu_sn * ES);
+    const uint32_t goff = static_cast<uint32_t>(r) * rowb, uoff = static_cast<uint32_t>(r + a.I) * rowb;
     uint4 wg[NC], wu[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int64_t c = s + static_cast<int64_t>(LPR) * j;
       const bool ok = rok && c < nch;
-      wg[j] = load_w(wbase, r * a.gu_sn * ES + c * 16, ok);
-      wu[j] = load_w(wbase, (r + a.I) * a.gu_sn * ES + c * 16, ok);
+      wg[j] = buf16(wr, ok ? goff + static_cast<uint32_t>(c) * 16u : kPast);
+      wu[j] = buf16(wr, ok ? uoff + static_cast<uint32_t>(c) * 16u : kPast);
     }
     for (int t = 0; t < cntp; ++t) {
       float ag = 0.f, au = 0.f;
@@ -197,13 +235,13 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
       for (int j = 0; j < NC; ++j) {
         const int64_t c = s + static_cast<int64_t>(LPR) * j;
         Act<Q> xv;
-        load_act<Q>(xv, xs + t * a.H, c, c < nch);
+        lds_act<Q>(xv, xs + t * a.H, c, c < nch);
         ag = dot_chunk<Q>(wg[j], xv, ag);
         au = dot_chunk<Q>(wu[j], xv, au);
       }
       ag = group_sum<LPR>(ag);
       au = group_sum<LPR>(au);
-      if (s == 0 && rok) gate_up_store<Q>(a, e, r, spid[t], ag, au);
+      if (s == 0 && rok) gate_up_store<Q>(a, r, spid[t], ag, au, sg, su);
     }
   }
   __syncthreads();  // the staging buffer is reused by the next group
@@ -211,42 +249,50 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
 
 constexpr int kMaxTokens = 8;
 
-template <bool Q, int LPR, int NC, int R, int MAXT>
+// Grid (row tiles of I, slots). ONE (one token): the workgroup computes its slot's pair. Otherwise the
+// workgroup of the first slot of each distinct expert takes every pair routed there.
+template <bool Q, int LPR, int NC, int R, int MAXT, bool ONE>
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
   extern __shared__ uint4 xs_raw[];  // MAXT bf16 rows of the hidden dim (MAXT > 1 only)
   __shared__ int spid[MAXT];
-  unsigned long long pairs;
-  const int e = distinct_expert(a, blockIdx.y, pairs);
+  const int u = blockIdx.y;
+  const int e = slot_expert(a, u);
   if (e < 0) return;
   constexpr int ES = Q ? 1 : 2;
   constexpr int GPW = kWave / LPR;  // row pairs per wave per step
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * (GPW * R);
   const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
-  if constexpr (MAXT == 1) {
-    while (pairs) {
-      const int p = __ffsll(static_cast<long long>(pairs)) - 1;
-      pairs &= pairs - 1ull;
-      gate_up_one<Q, LPR, NC, R>(a, e, p, wbase, row0);
-    }
+  if constexpr (ONE) {
+    gate_up_one<Q, LPR, NC, R>(a, e, u, wbase, row0);
   } else {
-    const bool one_pass = a.H * ES / 16 <= static_cast<int64_t>(LPR) * NC;
-    while (pairs) {
-      if (!one_pass || __popcll(pairs) == 1) {
+    unsigned long long pairs = __ballot(lane_pair_expert(a) == e);
+    if (__ffsll(static_cast<long long>(pairs)) - 1 != u) return;  // an earlier slot streams this expert
+    if constexpr (MAXT == 1) {
+      while (pairs) {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
         pairs &= pairs - 1ull;
         gate_up_one<Q, LPR, NC, R>(a, e, p, wbase, row0);
-        continue;
       }
-      int cntp = 0;
-      while (pairs && cntp < MAXT) {  // the next MAXT pairs of this expert, in pair order
-        const int p = __ffsll(static_cast<long long>(pairs)) - 1;
-        pairs &= pairs - 1ull;
-        if (threadIdx.x == 0) spid[cntp] = p;
-        ++cntp;
+    } else {
+      const bool one_pass = a.H * ES / 16 <= static_cast<int64_t>(LPR) * NC;
+      while (pairs) {
+        if (!one_pass || __popcll(pairs) == 1) {
+          const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+          pairs &= pairs - 1ull;
+          gate_up_one<Q, LPR, NC, R>(a, e, p, wbase, row0);
+          continue;
+        }
+        int cntp = 0;
+        while (pairs && cntp < MAXT) {  // the next MAXT pairs of this expert, in pair order
+          const int p = __ffsll(static_cast<long long>(pairs)) - 1;
+          pairs &= pairs - 1ull;
+          if (threadIdx.x == 0) spid[cntp] = p;
+          ++cntp;
+        }
+        __syncthreads();
+        gate_up_many<Q, LPR, NC, R, MAXT>(a, e, cntp, spid, wbase, row0, reinterpret_cast<uint16_t*>(xs_raw));
       }
-      __syncthreads();
-      gate_up_many<Q, LPR, NC, R, MAXT>(a, e, cntp, spid, wbase, row0, reinterpret_cast<uint16_t*>(xs_raw));
     }
   }
 }
@@ -255,64 +301,94 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
 
 constexpr int kDownWaves = 8;
 
-template <bool Q, int LPR, int NC>
+// Grid: row tiles of H (RW = 64 / LPR rows). Wave w takes slots w, w + 8, ... (ONE: each; otherwise the
+// first slot of each distinct expert, with all its pairs), streams the tile's rows of the slot's expert
+// (LPR lanes per row) once, dots them with a[p] of the pairs, rounds to bf16 (after the row scale for int8)
+// into LDS; the workgroup then sums over slots in order per token and adds the residual.
+template <bool Q, int LPR, int NC, bool ONEPASS, bool ONE>
 __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs a) {
-  constexpr int ES = Q ? 1 : 2;
   constexpr int RW = kWave / LPR;  // output rows per workgroup
+  constexpr int CE = Q ? 16 : 8;   // weights per 16-byte chunk
   __shared__ float part[kMaxPairs][RW];
-  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  __shared__ float swts[kMaxPairs];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / LPR, s = lane % LPR;
-  const int64_t h = static_cast<int64_t>(blockIdx.x) * RW + g;
+  const int h = static_cast<int>(blockIdx.x) * RW + g;
   const bool hok = h < a.H;
-  const int64_t nch = a.I * ES / 16;
+  const int64_t nch = a.I / CE;
 
-  for (int i = threadIdx.x; i < kMaxPairs * RW; i += blockDim.x) (&part[0][0])[i] = 0.f;
-  __syncthreads();
+  // The combine's operands are fetched now, into registers, so their loads overlap the weight stream: the
+  // slot weight of pair tid and the residual of this thread's (token, row) output. Nothing waits here.
+  const int tid = threadIdx.x;
+  const int ct = tid / RW, cr = tid % RW;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * RW + cr;
+  const bool combiner = tid < a.n_tokens * RW && ch < a.H;
+  const uint16_t res_raw = (combiner && a.res) ? a.res[ct * a.res_rs + ch] : 0;
+  float wt = 0.f;
+  if (tid < a.P) {
+    const int t = tid / a.nk, k = tid - t * a.nk;
+    wt = a.wts[t * a.wts_rs + k];
+  }
 
-  for (int u = wave;; u += kDownWaves) {
-    unsigned long long pairs;
-    const int e = distinct_expert(a, u, pairs);
-    if (e < 0) break;
-    const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
+  const int myid = ONE ? -1 : lane_pair_expert(a);
+  const rsrc_t ar = make_rsrc(a.a_buf, static_cast<int64_t>(a.P) * a.I * 2);
+  for (int u = wave; u < a.P; u += kDownWaves) {
+    const int e = slot_expert(a, u);
+    if (e < 0) {  // a dropped pair contributes nothing
+      if (s == 0) part[u][g] = 0.f;
+      continue;
+    }
+    unsigned long long pairs = 1ull << u;
+    if (!ONE) {
+      pairs = __ballot(myid == e);
+      if (__ffsll(static_cast<long long>(pairs)) - 1 != u) continue;  // an earlier slot has this expert
+    }
+    // the expert's down matrix as one resource; this lane group's row starts at byte wrow
+    const rsrc_t wr = make_rsrc(static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * (Q ? 1 : 2),
+                                a.H * a.d_sn * (Q ? 1 : 2));
+    const uint32_t wrow = static_cast<uint32_t>((hok ? h : 0) * a.d_sn * (Q ? 1 : 2));
     float sc = 1.f;
-    if (Q && hok) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + h);
-    if (nch <= static_cast<int64_t>(LPR) * NC) {
-      // the whole row fits one pass: load the weights once for every pair of the expert
+    if constexpr (ONEPASS) {
+      // the whole row in registers, loaded once for every pair of the expert
       uint4 w[NC];
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         const int64_t c = s + static_cast<int64_t>(LPR) * j;
-        w[j] = load_w(wbase, h * a.d_sn * ES + c * 16, hok && c < nch);
+        w[j] = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
       }
-      while (pairs) {
+      if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + (hok ? h : 0));
+      do {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
         pairs &= pairs - 1ull;
-        const uint16_t* ar = a.a_buf + static_cast<int64_t>(p) * a.I;
-        float acc = 0.f;
+        const uint32_t arow = static_cast<uint32_t>(p * a.I * 2);
+        Act<Q> av[NC];  // every load issued before the first dot
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
           const int64_t c = s + static_cast<int64_t>(LPR) * j;
-          Act<Q> av;
-          load_act<Q>(av, ar, c, c < nch);
-          acc = dot_chunk<Q>(w[j], av, acc);
+          buf_act<Q>(av[j], ar, arow, c, c < nch);
         }
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) acc = dot_chunk<Q>(w[j], av[j], acc);
         acc = group_sum<LPR>(acc);
         if (s == 0 && hok) part[p][g] = round_bf16(Q ? acc * sc : acc);
-      }
+      } while (!ONE && pairs);
     } else {
       // long rows: passes of LPR * NC chunks per pair (weights re-read from cache for later pairs)
+      if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + (hok ? h : 0));
       while (pairs) {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
         pairs &= pairs - 1ull;
-        const uint16_t* ar = a.a_buf + static_cast<int64_t>(p) * a.I;
+        const uint32_t arow = static_cast<uint32_t>(p * a.I * 2);
         float acc = 0.f;
         for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(LPR) * NC) {
 #pragma unroll
           for (int j = 0; j < NC; ++j) {
             const int64_t c = c0 + s + static_cast<int64_t>(LPR) * j;
-            const uint4 w = load_w(wbase, h * a.d_sn * ES + c * 16, hok && c < nch);
+            const uint4 w = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
             Act<Q> av;
-            load_act<Q>(av, ar, c, c < nch);
+            buf_act<Q>(av, ar, arow, c, c < nch);
             acc = dot_chunk<Q>(w, av, acc);
           }
         }
@@ -321,20 +397,16 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
       }
     }
   }
+  if (tid < a.P) swts[tid] = wt;
   __syncthreads();
 
   // combine: one thread per (token, row), slots summed in order
-  const int tid = threadIdx.x;
-  if (tid < a.n_tokens * RW) {
-    const int t = tid / RW, r = tid % RW;
-    const int64_t hh = static_cast<int64_t>(blockIdx.x) * RW + r;
-    if (hh < a.H) {
-      float acc = 0.f;
-      for (int k = 0; k < a.nk; ++k) acc = fmaf(a.wts[t * a.wts_rs + k], part[t * a.nk + k][r], acc);
-      float out = round_bf16(acc);
-      if (a.res) out = out + bf16_to_f32(a.res[t * a.res_rs + hh]);
-      a.y[t * a.ys + hh] = f32_to_bf16(out);
-    }
+  if (combiner) {
+    float acc = 0.f;
+    for (int k = 0; k < a.nk; ++k) acc = fmaf(swts[ct * a.nk + k], part[ct * a.nk + k][cr], acc);
+    float out = round_bf16(acc);
+    if (a.res) out = out + bf16_to_f32(res_raw);
+    a.y[ct * a.ys + ch] = f32_to_bf16(out);
   }
 }
 
@@ -343,9 +415,12 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
 template <bool Q, int LPR, int NC, int R, int MAXT>
 int launch_a(const DecodeArgs& a, hipStream_t st) {
   constexpr int rows_per_wg = 4 * (kWave / LPR) * R;
-  dim3 grid(static_cast<unsigned>((a.I + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(min(a.P, a.E1)));
+  dim3 grid(static_cast<unsigned>((a.I + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(a.P));
   const size_t lds = MAXT > 1 ? static_cast<size_t>(MAXT) * a.H * 2 : 0;
-  hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT>), grid, dim3(256), lds, st, a);
+  if (a.n_tokens == 1)
+    hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT, true>), grid, dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT, false>), grid, dim3(256), lds, st, a);
   return mm::check_launch("moe_decode gate_up");
 }
 
@@ -353,7 +428,13 @@ template <bool Q, int LPR, int NC>
 int launch_b(const DecodeArgs& a, hipStream_t st) {
   constexpr int RW = kWave / LPR;
   dim3 grid(static_cast<unsigned>((a.H + RW - 1) / RW));
-  hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC>), grid, dim3(kDownWaves * 64), 0, st, a);
+  const bool onepass = a.I * (Q ? 1 : 2) / 16 <= static_cast<int64_t>(LPR) * NC;
+  if (onepass && a.n_tokens == 1)
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+  else if (onepass)
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false>), grid, dim3(kDownWaves * 64), 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
   return mm::check_launch("moe_decode down");
 }
 
