@@ -277,22 +277,23 @@ def decode_metrics(b, n, stream, int8=False, seed=40):
 # ------------------------------------------------------------------------------------- full decode step
 
 def full_decode_metrics(stream, layers=28):
-    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1; and the
+    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1 (the first
+    RMSNorm runs inside the q|k|v GEMV, whose rows are the q, k and v weights stacked); and the
     28 MoE blocks alone (median of 5 timings): the decode MoE layer with every layer's experts read from
     HBM, as in a real forward pass (the single-layer decode figures can hit the 256 MB last-level cache)."""
     import fastlinear
     import fused_moe
-    import fused_ops
     import workloads as W
     H, dev = W.HIDDEN, "cuda"
     L = []
     for li in range(layers):
         s = 1000 + 16 * li
+        q, k, v = W.normal((H, H), 0.02, s + 1, dev), W.normal((256, H), 0.02, s + 2, dev), W.normal((256, H), 0.02, s + 3, dev)
         L.append({
-            "ln1": W.normal((H,), 0.02, s, dev, mean=1.0), "q": W.normal((H, H), 0.02, s + 1, dev),
-            "k": W.normal((256, H), 0.02, s + 2, dev), "v": W.normal((256, H), 0.02, s + 3, dev),
+            "ln1": W.normal((H,), 0.02, s, dev, mean=1.0), "qkv": torch.cat([q, k, v]),  # q|k|v rows, one GEMV
             "o": W.normal((H, H), 0.02, s + 4, dev), "blk": W.block(seed=s + 5, device=dev),
         })
+        del q, k, v
     fn = W.normal((H,), 0.02, 999, dev, mean=1.0)
     head = W.normal((W.VOCAB, H), 0.02, 998, dev)
     x0 = W.tokens(1, seed=997, device=dev)
@@ -305,11 +306,8 @@ def full_decode_metrics(stream, layers=28):
     def step():
         h = x0
         for p in L:
-            xn = fused_ops.rms_norm(h, p["ln1"], W.EPS)
-            q = fastlinear.small_linear(xn, p["q"])
-            fastlinear.small_linear(xn, p["k"])
-            fastlinear.small_linear(xn, p["v"])
-            h = fastlinear.small_linear(q, p["o"], residual=h)  # attention itself is outside the MoE path
+            qkv = fastlinear.small_linear(h, p["qkv"], norm=(p["ln1"], W.EPS))  # RMSNorm fused into q|k|v
+            h = fastlinear.small_linear(qkv[:, :H], p["o"], residual=h)  # attention itself is outside the MoE path
             b = p["blk"]
             h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
                                            logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
@@ -510,6 +508,22 @@ def cpu_baseline(b, bias, n_sample=64, reps=2):
                       f"{platform.processor() or platform.machine()}"}
 
 
+def box_info():
+    """The GPU this run measured (decode timings of one build differ by up to ~35% between boxes)."""
+    p = torch.cuda.get_device_properties(0)
+    info = {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
+            "host": platform.node()}
+    smi = shutil.which("rocm-smi")
+    if smi:
+        try:
+            r = subprocess.run([smi, "--showclocks", "--json"], capture_output=True, text=True, timeout=20)
+            card = next(iter(json.loads(r.stdout).values()))
+            info["clocks"] = {k: v for k, v in card.items() if "clock" in k.lower() and ("sclk" in k.lower() or "mclk" in k.lower())}
+        except Exception as e:  # clocks are informational only
+            info["clocks"] = f"unavailable: {type(e).__name__}"
+    return info
+
+
 def main():
     args = parse()
     if args.pmc_probe:
@@ -581,6 +595,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "prefill_gate_up_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
         "cpu_baseline": cpu,
+        "box": box_info(),
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

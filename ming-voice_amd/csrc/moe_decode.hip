@@ -85,20 +85,6 @@ __device__ __forceinline__ void lds_act(Act<Q>& o, const uint16_t* row, int64_t 
   if (Q) o.v[Q ? 1 : 0] = and_mask(p[1], m);
 }
 
-// Global operands are read through buffer resources (a wave-uniform base and byte size): a load at an
-// offset past the end returns zero, so a lane past a row's end is given kPast as its offset instead of a
-// branch or a mask, and all of a lane's loads issue back to back.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr uint32_t kPast = 0x80000000u;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-
-__device__ __forceinline__ uint4 buf16(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
-}
-
 // Activation chunk c (CE bf16 values) of the row starting at byte `row` of resource r; kPast when !ok.
 template <bool Q>
 __device__ __forceinline__ void buf_act(Act<Q>& o, rsrc_t r, uint32_t row, int64_t c, bool ok) {

@@ -120,6 +120,98 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
         ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
 }
 
+// The same for bf16 rows of at most 2048 * J elements (H a multiple of 8, 16-byte aligned rows), in one
+// memory round trip: thread i owns the 8-element chunks i + 256 j, and every load of the workgroup (its
+// router row, the RMSNorm weight, the token rows) is issued at kernel start through buffer resources.
+// The sum of squares runs over the chunks exactly as row_rstd256 does, so xn matches mm_rms_norm bit for
+// bit; a chunk's logit terms are added in element order, chunks in j order, then the waves in order.
+template <int J>
+__global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* __restrict__ x, int n_tokens, int64_t H,
+                                                               int64_t xs, const float* __restrict__ w32, int E,
+                                                               float* __restrict__ logits,
+                                                               const uint16_t* __restrict__ norm_w, float eps,
+                                                               uint16_t* __restrict__ xn_out) {
+  __shared__ float red_ss[8][4];
+  __shared__ float red[4][8];
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const int nch = static_cast<int>(H / 8);
+  const rsrc_t wr = make_rsrc(w32 + static_cast<int64_t>(e) * H, H * 4);
+  const rsrc_t xr = make_rsrc(x, static_cast<int64_t>(n_tokens) * xs * 2);
+  const rsrc_t nr = make_rsrc(norm_w, norm_w ? H * 2 : 0);
+  uint4 wv[J][2], nv[J], xv[J][8];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = tid + 256 * j;
+    const bool ok = c < nch;
+    wv[j][0] = buf16(wr, ok ? static_cast<uint32_t>(c) * 32u : kPast);
+    wv[j][1] = buf16(wr, ok ? static_cast<uint32_t>(c) * 32u + 16u : kPast);
+    nv[j] = buf16(nr, ok ? static_cast<uint32_t>(c) * 16u : kPast);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      if (t < n_tokens) xv[j][t] = buf16(xr, ok ? static_cast<uint32_t>(t * xs * 2 + c * 16) : kPast);
+  }
+  float rstd[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) rstd[t] = 1.f;
+  if (norm_w) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t < n_tokens) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) ss = chunk_ss_bf16x8(xv[j][t], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) red_ss[t][wave] = ss;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      if (t < n_tokens)
+        rstd[t] = rsqrtf((((red_ss[t][0] + red_ss[t][1]) + red_ss[t][2]) + red_ss[t][3]) / static_cast<float>(H) + eps);
+  }
+  const bool store_xn = xn_out && e == 0;
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = tid + 256 * j;
+    const uint32_t wq[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w, wv[j][1].x, wv[j][1].y, wv[j][1].z, wv[j][1].w};
+    const uint32_t nq[4] = {nv[j].x, nv[j].y, nv[j].z, nv[j].w};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t < n_tokens) {
+        const uint32_t xq[4] = {xv[j][t].x, xv[j][t].y, xv[j][t].z, xv[j][t].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float lo = __uint_as_float(xq[i] << 16), hi = __uint_as_float(xq[i] & 0xffff0000u);
+          if (norm_w) {
+            lo = round_bf16(__uint_as_float(nq[i] << 16) * round_bf16(lo * rstd[t]));
+            hi = round_bf16(__uint_as_float(nq[i] & 0xffff0000u) * round_bf16(hi * rstd[t]));
+          }
+          o[i] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+          acc[t] = fmaf(lo, __uint_as_float(wq[2 * i]), acc[t]);
+          acc[t] = fmaf(hi, __uint_as_float(wq[2 * i + 1]), acc[t]);
+        }
+        if (store_xn && c < nch) reinterpret_cast<uint4*>(xn_out + t * H)[c] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    if (t < n_tokens) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) red[wave][t] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < n_tokens)
+    logits[static_cast<int64_t>(tid) * E + e] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+}
+
 // logits for many tokens on fp32 MFMA (v_mfma_f32_16x16x4_f32): a workgroup of 16 waves computes 16
 // tokens x 16 experts, each wave a contiguous run of the hidden dim. In a wave the lane (row r = lane % 16,
 // quarter q = lane / 16) takes k = run + 16j + 4q + i of token row r and router row r, so the 4 quarters
@@ -273,7 +365,18 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
   const auto* xp = static_cast<const typename TX::T*>(x);
   const auto* nw = static_cast<const uint16_t*>(norm_w);
   auto* xo = static_cast<uint16_t*>(xn_out);
-  if (n_tokens <= 8) {  // the RMSNorm is fused only here; larger batches take normalised rows
+  const bool fast = TX::kBf16 && (H & 7) == 0 && H <= 4096 && (xs & 7) == 0 && mm::aligned16(x) && mm::aligned16(w32) &&
+                    (!norm_w || mm::aligned16(norm_w)) && (!xn_out || mm::aligned16(xn_out)) &&
+                    n_tokens * xs * 2 < (1LL << 31);
+  if (n_tokens <= 8 && fast) {  // the RMSNorm is fused only for up to 8 tokens; larger batches take normalised rows
+    const auto* xb = static_cast<const uint16_t*>(x);
+    if (H <= 2048)
+      hipLaunchKernelGGL(router_gemv_bf16_kernel<1>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xb,
+                         static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
+    else
+      hipLaunchKernelGGL(router_gemv_bf16_kernel<2>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xb,
+                         static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
+  } else if (n_tokens <= 8) {
     hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xp,
                        static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
   } else {
