@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 4
+#define MM_ABI_VERSION 5
 
 /* status codes */
 #define MM_OK 0
@@ -154,9 +154,16 @@ int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, c
  * Replaces fused_moe.fused_moe_prefill / _moe_gu_grouped / _moe_down_grouped (fused_moe.py:92-196).
  * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs
  * p = t*nk + k whose id lies outside [0, n_slots) contribute nothing); wts fp32 [n_tokens*nk];
- * sorted_ids / bexp / expert_offsets / nb / block_m (64) from mm_align_blocks; a_buf bf16
+ * sorted_ids / bexp / expert_offsets / nb / block_m from mm_align_blocks, block_m = 64 or, for bf16 experts,
+ * 128 (mm_prefill_block_m gives the faster one for a shape); a_buf bf16
  * [n_tokens*nk, inter] and part_buf bf16 [n_tokens*nk, hidden] (per-pair expert outputs bf16(a . Wd^T),
  * before the slot weight) are scratch; y bf16 [n_tokens, hidden]. */
+/* Rows per expert block the prefill kernels take for a shape (the align padding): 128 for bf16 experts
+ * (w_dtype MM_BF16) averaging at least 128 pairs (n_tokens * nk >= 128 * n_slots: each weight slab then
+ * feeds twice the MFMA rows), else 64. No counterpart in the reference (its grouped kernels take BM = 64,
+ * fused_moe.py:176-196). */
+int32_t mm_prefill_block_m(int64_t n_tokens, int64_t nk, int64_t n_slots, int w_dtype);
+
 int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
                    int64_t nk, const void* ids, int ids_dtype, const float* wts,
                    const int32_t* sorted_ids, const int32_t* bexp, const int32_t* expert_offsets,
@@ -171,7 +178,8 @@ int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const 
  * sequence of engine.py:229, 284-309.
  * ex->n_slots must be n_experts + 1. logits fp32 [n_tokens, n_experts]; ids [n_tokens, top_k+1]
  * (MM_INT32 / MM_INT64); wts fp32 [n_tokens, top_k+1]; xn bf16 [n_tokens, hidden] (16-byte aligned);
- * sorted_ids / bexp / expert_offsets / nb sized as for mm_align_blocks with block_m 64; a_buf / part_buf
+ * sorted_ids / bexp / expert_offsets / nb sized as for mm_align_blocks with block_m =
+ * mm_prefill_block_m(n_tokens, top_k + 1, n_experts + 1, ex->w_dtype); a_buf / part_buf
  * as for mm_moe_prefill; y bf16 [n_tokens, hidden] (must not alias x when add_residual). */
 int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
                          const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,

@@ -16,7 +16,7 @@ MM_OK, MM_ERR_ARG, MM_ERR_HIP = 0, 1, 2
 MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -57,6 +57,7 @@ SIGNATURES = {
                         ctypes.c_int32, _P, _I64, _P, _P, _P, _I64, _I32, _P], ctypes.c_int),
     "mm_moe_block_decode": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
                              ctypes.POINTER(Experts), _P, _P, _I32, _P, _P, _P, _I32, _P, _I64, _P], ctypes.c_int),
+    "mm_prefill_block_m": ([_I64, _I64, _I64, _I32], ctypes.c_int32),
     "mm_moe_block_prefill": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
                               ctypes.POINTER(Experts), _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _P,
                               _I64, _P], ctypes.c_int),

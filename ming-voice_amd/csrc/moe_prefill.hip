@@ -21,7 +21,11 @@ namespace {
 
 using namespace mmd;
 
-constexpr int kBM = 64;          // rows (pairs) per block, = align block_m
+// Rows (pairs) per expert block, = align block_m: 64, or 128 for bf16 weights when experts average at least
+// 128 pairs (then every weight slab feeds twice the MFMA rows: the 2048-token Zipf block runs 18% faster,
+// while a 512-token block, about 55 pairs per expert, runs 8% slower). kBM is the largest.
+constexpr int kBM = 128;
+constexpr int kBMSmall = 64;
 constexpr int kXcds = 8;
 // Tile shape per weight type and GEMM: output columns per tile (BN) and waves per workgroup. The k-slab is
 // 64 elements; 128-column bf16 tiles keep 3 slabs in flight, int8 and 256-column tiles 2 (LDS = slabs x
@@ -72,9 +76,10 @@ struct PrefillArgs {
   int64_t ys;
 };
 
-// Tile of this workgroup: expert e, block blk (rows blk*64 ..), column tile nt. False: no tile.
+// Tile of this workgroup: expert e, block blk (rows blk*BM ..), column tile nt. False: no tile.
+template <int BM>
 __device__ __forceinline__ bool map_tile(const PrefillArgs& a, int NT, int& e, int& blk, int& nt) {
-  const int used_blocks = a.offsets[a.E1] / kBM;
+  const int used_blocks = a.offsets[a.E1] / BM;
   const int G = used_blocks * NT;
   const int per = (G + kXcds - 1) / kXcds;
   const int w = blockIdx.x;
@@ -83,7 +88,7 @@ __device__ __forceinline__ bool map_tile(const PrefillArgs& a, int NT, int& e, i
   const int L = xcd * per + idx;
   if (L >= G) return false;
   e = a.bexp[L / NT];
-  const int b0 = a.offsets[e] / kBM, nblk = a.offsets[e + 1] / kBM - b0;
+  const int b0 = a.offsets[e] / BM, nblk = a.offsets[e + 1] / BM - b0;
   const int local = L - b0 * NT;
   nt = local / nblk;
   blk = b0 + local % nblk;
@@ -118,20 +123,21 @@ __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
 
 __device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes for masked lanes
 
-template <bool Quant, int TileN, int Waves = 4>
+template <bool Quant, int TileN, int Waves = 4, int BlockM = kBMSmall>
 struct Geo {
   static constexpr bool Q = Quant;
+  static constexpr int BM = BlockM;                   // rows (pairs) per tile
   static constexpr int BN = TileN;                    // output columns per tile
   static constexpr int NW = Waves;                    // waves per workgroup
   static constexpr int BK = 64;                       // k elements per slab
-  static constexpr int NS = Q || BN >= 256 ? 2 : 3;   // slabs in flight
+  static constexpr int NS = Q || BN >= 256 || BM > 64 ? 2 : 3;  // slabs in flight
   static constexpr int WM = (BN <= 64 || NW == 8) ? 2 : 1;  // wave rows
   static constexpr int WN = NW / WM;                  // wave columns
-  static constexpr int FM = kBM / WM / 16;            // 16-row fragments per wave
+  static constexpr int FM = BM / WM / 16;             // 16-row fragments per wave
   static constexpr int FN = BN / WN / 16;             // 16-column fragments per wave
   static constexpr int AROW = BK * 2;                 // activation (bf16) bytes per row per slab
   static constexpr int ROWB = Q ? BK : BK * 2;        // weight bytes per row per slab
-  static constexpr int A_BYTES = kBM * AROW;
+  static constexpr int A_BYTES = BM * AROW;
   static constexpr int B_BYTES = BN * ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr size_t LDS = static_cast<size_t>(NS) * STAGE;
@@ -306,18 +312,18 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
 
 // ------------------------------------------------------------------------------------------- gate / up
 
-template <bool Q, int BN, int NW>
+template <bool Q, int BN, int NW, int BM>
 __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a) {
-  using G = Geo<Q, BN, NW>;
+  using G = Geo<Q, BN, NW, BM>;
   constexpr int HALF = G::BN / 2;  // gate columns per tile (and as many up columns)
   extern __shared__ uint4 lds_raw[];
-  __shared__ int spair[kBM];
+  __shared__ int spair[BM];
   const int NT = static_cast<int>((a.I + HALF - 1) / HALF);
   int e, blk, nt;
-  if (!map_tile(a, NT, e, blk, nt)) return;
+  if (!map_tile<BM>(a, NT, e, blk, nt)) return;
   constexpr int ES = Q ? 1 : 2;
   const int64_t I = a.I, n0 = static_cast<int64_t>(nt) * HALF;
-  if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
+  if (threadIdx.x < BM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * BM + threadIdx.x];
   __syncthreads();
   // activation row of tile row r (token of pair spair[r]); weight row of tile column r (gate columns
   // first, then the matching up rows); null = masked
@@ -332,7 +338,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
-  const int r0 = wm * (kBM / G::WM);
+  const int r0 = wm * (BM / G::WM);
   constexpr int FG = G::FN / 2;      // gate fragments of the wave; the next FG are the matching up ones
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
@@ -363,17 +369,17 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
 
 // ----------------------------------------------------------------------------------------------- down
 
-template <bool Q, int BN, int NW>
+template <bool Q, int BN, int NW, int BM>
 __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
-  using G = Geo<Q, BN, NW>;
+  using G = Geo<Q, BN, NW, BM>;
   extern __shared__ uint4 lds_raw[];
-  __shared__ int spair[kBM];
+  __shared__ int spair[BM];
   const int NT = static_cast<int>((a.H + G::BN - 1) / G::BN);
   int e, blk, nt;
-  if (!map_tile(a, NT, e, blk, nt)) return;
+  if (!map_tile<BM>(a, NT, e, blk, nt)) return;
   constexpr int ES = Q ? 1 : 2;
   const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * G::BN;
-  if (threadIdx.x < kBM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * kBM + threadIdx.x];
+  if (threadIdx.x < BM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * BM + threadIdx.x];
   __syncthreads();
   auto xrow = [&](int r) -> const uint16_t* {
     const int p = spair[r];
@@ -386,7 +392,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
-  const int r0 = wm * (kBM / G::WM);
+  const int r0 = wm * (BM / G::WM);
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
   tile_gemm<G>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
@@ -471,37 +477,37 @@ int allow_lds(K kernel, size_t bytes, const char* what) {
   return MM_OK;
 }
 
-template <bool Q, int BN, int NW>
+template <bool Q, int BN, int NW, int BM>
 int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
-  using G = Geo<Q, BN, NW>;
+  using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.I + G::BN / 2 - 1) / (G::BN / 2);
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = allow_lds(prefill_gate_up_kernel<Q, BN, NW>, G::LDS, "prefill_gate_up");
+  int rc = allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM>, G::LDS, "prefill_gate_up");
   if (rc) return rc;
-  hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
   return mm::check_launch("moe_prefill gate_up");
 }
 
-template <bool Q, int BN, int NW>
+template <bool Q, int BN, int NW, int BM>
 int launch_down(const PrefillArgs& a, int64_t nb, hipStream_t st) {
-  using G = Geo<Q, BN, NW>;
+  using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.H + G::BN - 1) / G::BN;
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = allow_lds(prefill_down_kernel<Q, BN, NW>, G::LDS, "prefill_down");
+  int rc = allow_lds(prefill_down_kernel<Q, BN, NW, BM>, G::LDS, "prefill_down");
   if (rc) return rc;
-  hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
   return mm::check_launch("moe_prefill down");
 }
 
-template <bool Q>
+template <bool Q, int BM>
 int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
   constexpr int GU_BN = Q ? MM_PREFILL_GU_BN_INT8 : MM_PREFILL_GU_BN_BF16;
   constexpr int DOWN_BN = Q ? MM_PREFILL_DOWN_BN_INT8 : MM_PREFILL_DOWN_BN_BF16;
   constexpr int GU_NW = Q ? 4 : MM_PREFILL_GU_WAVES_BF16;
   constexpr int DOWN_NW = Q ? 4 : MM_PREFILL_DOWN_WAVES_BF16;
   int rc;
-  if ((phases & MM_PHASE_GATE_UP) && (rc = launch_gate_up<Q, GU_BN, GU_NW>(a, nb, st))) return rc;
-  if ((phases & MM_PHASE_DOWN) && (rc = launch_down<Q, DOWN_BN, DOWN_NW>(a, nb, st))) return rc;
+  if ((phases & MM_PHASE_GATE_UP) && (rc = launch_gate_up<Q, GU_BN, GU_NW, BM>(a, nb, st))) return rc;
+  if ((phases & MM_PHASE_DOWN) && (rc = launch_down<Q, DOWN_BN, DOWN_NW, BM>(a, nb, st))) return rc;
   return MM_OK;
 }
 
@@ -511,6 +517,11 @@ namespace mm {
 int check_experts(const char* who, const mm_experts* ex);
 }
 
+extern "C" int32_t mm_prefill_block_m(int64_t n_tokens, int64_t nk, int64_t n_slots, int w_dtype) {
+  // bf16 experts averaging at least 128 pairs take 128-row blocks; everything else 64
+  return w_dtype == MM_BF16 && n_slots > 0 && n_tokens * nk >= static_cast<int64_t>(kBM) * n_slots ? kBM : kBMSmall;
+}
+
 extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex, int64_t nk,
                               const void* ids, int ids_dtype, const float* wts, const int32_t* sorted_ids,
                               const int32_t* bexp, const int32_t* expert_offsets, int64_t nb, int32_t block_m,
@@ -518,7 +529,8 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
                               int64_t y_row_stride, int phases, void* stream) {
   int rc = mm::check_experts("moe_prefill", ex);
   if (rc) return rc;
-  MM_REQUIRE(block_m == kBM, "moe_prefill: block_m must be %d (got %d)", kBM, block_m);
+  MM_REQUIRE(block_m == kBMSmall || (block_m == kBM && ex->w_dtype == MM_BF16),
+             "moe_prefill: block_m must be %d (or %d for bf16 experts; got %d)", kBMSmall, kBM, block_m);
   MM_REQUIRE(n_tokens >= 0 && nk >= 1 && n_tokens * nk <= (1LL << 30), "moe_prefill: bad token/slot counts");
   MM_REQUIRE(nb >= 0 && nb * 16 <= 0x7fffffffLL, "moe_prefill: bad block count");
   MM_REQUIRE(ex->n_slots <= 0x7fffffff && ex->hidden % 8 == 0, "moe_prefill: hidden must be a multiple of 8");
@@ -565,7 +577,9 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   hipStream_t st = MM_STREAM(stream);
   if (phases == MM_PHASE_ALL) phases = MM_PHASE_GATE_UP | MM_PHASE_DOWN | MM_PHASE_COMBINE;
   if (nb > 0) {
-    rc = ex->w_dtype == MM_INT8 ? launch_gemms<true>(a, nb, phases, st) : launch_gemms<false>(a, nb, phases, st);
+    if (ex->w_dtype == MM_INT8) rc = launch_gemms<true, kBMSmall>(a, nb, phases, st);
+    else if (block_m == kBM) rc = launch_gemms<false, kBM>(a, nb, phases, st);
+    else rc = launch_gemms<false, kBMSmall>(a, nb, phases, st);
     if (rc) return rc;
   }
   if (!(phases & MM_PHASE_COMBINE)) return MM_OK;
@@ -605,10 +619,11 @@ extern "C" int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_r
   rc = mm::router_front(x, n_tokens, ex->hidden, x_row_stride, norm_w, eps, w32, sp, logits, ids, ids_dtype, wts, nk, xn,
                         st);
   if (rc) return rc;
-  rc = mm_align_blocks(ids, ids_dtype, n_tokens * nk, static_cast<int32_t>(ex->n_slots), kBM, sorted_ids, bexp, nb,
+  const int32_t bm = mm_prefill_block_m(n_tokens, nk, ex->n_slots, ex->w_dtype);
+  rc = mm_align_blocks(ids, ids_dtype, n_tokens * nk, static_cast<int32_t>(ex->n_slots), bm, sorted_ids, bexp, nb,
                        expert_offsets, stream);
   if (rc) return rc;
-  return mm_moe_prefill(xn, n_tokens, ex->hidden, ex, nk, ids, ids_dtype, wts, sorted_ids, bexp, expert_offsets, nb, kBM,
+  return mm_moe_prefill(xn, n_tokens, ex->hidden, ex, nk, ids, ids_dtype, wts, sorted_ids, bexp, expert_offsets, nb, bm,
                         add_residual ? x : nullptr, x_row_stride, a_buf, part_buf, y, y_row_stride, MM_PHASE_ALL,
                         stream);
 }

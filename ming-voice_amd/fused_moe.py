@@ -24,7 +24,7 @@ __all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "CFG",
 CFG = dict(A=dict(BN=16, BK=256, num_warps=4), B=dict(BN=16, BK=256, num_warps=4))
 GCFG = dict(A=dict(BM=64, BN=64, BK=64, num_warps=4), B=dict(BM=64, BN=128, BK=64, num_warps=4))
 
-BLOCK_M = 64        # rows per expert block in prefill (align padding)
+BLOCK_M = 64        # rows per expert block of the reference's grouped kernels (_align_blocks default)
 MAX_DECODE_TOKENS = 8
 _MAX_PAIRS = 64
 
@@ -164,14 +164,22 @@ def _align_blocks(flat, E1, BM, expert_offsets=None, out=None):
     return sorted_ids, bexp, nb
 
 
+def prefill_block_m(n_tokens, kp1, n_slots, w_dtype=torch.bfloat16):
+    """Rows per expert block the prefill kernels take for this shape (the align padding): 128 for bf16 experts
+    averaging at least 128 pairs, else 64."""
+    code = _mm.MM_INT8 if w_dtype == torch.int8 else _mm.MM_BF16
+    return int(_mm.load().mm_prefill_block_m(int(n_tokens), int(kp1), int(n_slots), code))
+
+
 class PrefillScratch:
     """Device buffers of one prefill call (align output and intermediates), reusable across calls of the
-    same shape so that a caller can keep them outside the timed or captured region."""
+    same shape and expert dtype so that a caller can keep them outside the timed or captured region."""
 
-    def __init__(self, N, KP1, E1, H, I, device, block=False):
+    def __init__(self, N, KP1, E1, H, I, device, block=False, w_dtype=torch.bfloat16):
         P = N * KP1
-        self.nb = _num_blocks(P, E1, BLOCK_M)
-        self.sorted_ids = torch.empty(self.nb * BLOCK_M, dtype=torch.int32, device=device)
+        self.block_m = prefill_block_m(N, KP1, E1, w_dtype)
+        self.nb = _num_blocks(P, E1, self.block_m)
+        self.sorted_ids = torch.empty(self.nb * self.block_m, dtype=torch.int32, device=device)
         self.bexp = torch.empty(self.nb, dtype=torch.int32, device=device)
         self.offsets = torch.empty(E1 + 1, dtype=torch.int32, device=device)
         self.a = torch.empty(P, I, device=device, dtype=torch.bfloat16)
@@ -208,12 +216,14 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
     if P != N * KP1:
         raise ValueError("fused_moe_prefill: ids must be [N, K+1]")
     wts = weights.reshape(-1).float().contiguous()
-    sc = scratch if scratch is not None else PrefillScratch(N, KP1, E1, H, I, x.device)
+    sc = scratch if scratch is not None else PrefillScratch(N, KP1, E1, H, I, x.device, w_dtype=w_gu.dtype)
     if sc.a.shape != (P, I) or sc.y.shape != (N, H) or sc.offsets.numel() != E1 + 1:
         raise ValueError("fused_moe_prefill: scratch was made for another shape")
+    if sc.block_m != prefill_block_m(N, KP1, E1, w_gu.dtype):
+        raise ValueError("fused_moe_prefill: scratch was made for another expert dtype (PrefillScratch w_dtype)")
     nb = sc.nb
     if align:
-        _align_blocks(flat, E1, BLOCK_M, expert_offsets=sc.offsets, out=(sc.sorted_ids, sc.bexp))
+        _align_blocks(flat, E1, sc.block_m, expert_offsets=sc.offsets, out=(sc.sorted_ids, sc.bexp))
     sorted_ids, bexp, a, part, y = sc.sorted_ids, sc.bexp, sc.a, sc.part, sc.y
     r2 = None
     if residual is not None:
@@ -226,7 +236,7 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
     with _mm.on_device(x):
         _mm.check(lib.mm_moe_prefill(_mm.ptr(x2), N, x2.stride(0), ex, KP1, _mm.ptr(flat), _mm.dtype_code(flat),
                                      _mm.ptr(wts), _mm.ptr(sorted_ids), _mm.ptr(bexp), _mm.ptr(sc.offsets), nb,
-                                     BLOCK_M, _mm.ptr(r2), r2.stride(0) if r2 is not None else 0, _mm.ptr(a),
+                                     sc.block_m, _mm.ptr(r2), r2.stride(0) if r2 is not None else 0, _mm.ptr(a),
                                      _mm.ptr(part), _mm.ptr(y), H,
                                      phases, _mm.stream_of(x)), "fused_moe_prefill")
     return y
@@ -253,7 +263,10 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
     if scoring not in _SCORING:
         raise ValueError(f"moe_block_prefill: scoring must be one of {sorted(_SCORING)}")
     ex = _mm.experts(w_gu, w_d, s_gu, s_d)
-    sc = scratch if scratch is not None else PrefillScratch(N, NK, ex.n_slots, H, ex.inter, x.device, block=True)
+    sc = scratch if scratch is not None else PrefillScratch(N, NK, ex.n_slots, H, ex.inter, x.device, block=True,
+                                                             w_dtype=w_gu.dtype)
+    if sc.block_m != prefill_block_m(N, NK, ex.n_slots, w_gu.dtype):
+        raise ValueError("moe_block_prefill: scratch was made for another expert dtype (PrefillScratch w_dtype)")
     if not hasattr(sc, "xn") or sc.xn.shape != (N, H) or sc.ids.shape != (N, NK) or sc.logits.shape != (N, E) \
             or sc.a.shape != (N * NK, ex.inter) or sc.offsets.numel() != ex.n_slots + 1:
         raise ValueError("moe_block_prefill: scratch was made for another shape (or without block=True)")

@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "mingmoe.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t)\s+(mm_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int32_t|int64_t|size_t)\s+(mm_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_expected_entry_points():
@@ -82,6 +82,9 @@ def test_argument_validation_reports_messages():
                                                          None))
     assert "at most 16" in _err(lib.mm_qwen_decode_attn(P, 34, 2, 64, P, P, 64, P, mm.MM_INT64, P, 0.1, P, P, 1 << 20,
                                                         None))
+    assert lib.mm_prefill_block_m(2048, 7, 65, mm.MM_BF16) == 128 and lib.mm_prefill_block_m(512, 7, 65, mm.MM_BF16) == 64
+    assert lib.mm_prefill_block_m(2048, 7, 65, mm.MM_INT8) == 64 and lib.mm_prefill_block_m(1189, 7, 65, mm.MM_BF16) == 128
+    assert lib.mm_prefill_block_m(1188, 7, 65, mm.MM_BF16) == 64
     need = lib.mm_decode_attn_workspace(14, 64, 1024)
     assert need == 14 * 16 * (64 + 2) * 4 and lib.mm_decode_attn_workspace(0, 64, 1024) == 0
     assert "workspace needs" in _err(lib.mm_qwen_decode_attn(P, 14, 2, 64, P, P, 1024, P, mm.MM_INT64, P, 0.1, P, P,

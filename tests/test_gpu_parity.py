@@ -277,7 +277,7 @@ def test_moe_block_prefill_matches_unfused_and_oracle(blk, n, int8):
     x = W.tokens(n, seed=160 + n, device=DEV)
     wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
     sg, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
-    sc = fused_moe.PrefillScratch(n, 7, 65, W.HIDDEN, W.INTER, DEV, block=True)
+    sc = fused_moe.PrefillScratch(n, 7, 65, W.HIDDEN, W.INTER, DEV, block=True, w_dtype=wg.dtype)
     y, ids, wts, logits = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=6, bias=bias,
                                                       s_gu=sg, s_d=sd, scratch=sc)
     xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
@@ -290,8 +290,26 @@ def test_moe_block_prefill_matches_unfused_and_oracle(blk, n, int8):
     close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
 
 
+def test_moe_block_prefill_zipf_2048_128_row_blocks(blk):
+    """2048 Zipf-routed tokens average 220 pairs per expert, so bf16 experts take 128-row blocks: the block
+    equals the unfused chain bit for bit, and a seeded subset matches the oracle."""
+    b, cpu = blk
+    bias = W.zipf_bias(device=DEV)
+    x = W.tokens(2048, seed=92, device=DEV)
+    assert fused_moe.prefill_block_m(2048, 7, 65) == 128 and fused_moe.prefill_block_m(512, 7, 65) == 64
+    assert fused_moe.prefill_block_m(2048, 7, 65, torch.int8) == 64
+    y, ids, wts, _ = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=6,
+                                                 bias=bias)
+    xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+    y2 = fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x)
+    assert torch.equal(y, y2)
+    sub = torch.randperm(2048, generator=torch.Generator().manual_seed(2))[:128]
+    close(y.cpu()[sub], _oracle_moe(cpu, xn[sub.to(DEV)], ids[sub.to(DEV)], wts[sub.to(DEV)],
+                                    residual=x.cpu()[sub]))
+
+
 def test_prefill_zipf_2048_int8_subset(blk):
-    """Hot experts of the Zipf batch on the int8 path: block pairs as 128-row tiles, odd last blocks alone."""
+    """Hot experts of the Zipf batch on the int8 path (64-row blocks, many per hot expert)."""
     b, cpu = blk
     x = W.tokens(2048, seed=91, device=DEV)
     xn, ids, wts = _route_tokens(b, x, W.zipf_bias(device=DEV))
