@@ -290,6 +290,34 @@ def test_moe_block_prefill_matches_unfused_and_oracle(blk, n, int8):
     close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
 
 
+@pytest.mark.parametrize("H,E,n,scoring,groups,top_k", [(1536, 48, 37, "softmax", (1, 1), 6),
+                                                         (2048, 64, 40, "sigmoid", (8, 4), 6),
+                                                         (1024, 64, 9, "softmax", (1, 1), 8),
+                                                         (2560, 64, 20, "softmax", (1, 1), 6)])
+def test_block_prefill_router_front_shapes(H, E, n, scoring, groups, top_k):
+    """The router front of the prefill block at other shapes: normalised rows, logits, ids and weights equal
+    rms_norm -> route bit for bit with a partial 16-token group, an expert count that is not a multiple of
+    16, rows wider than 2048 and the sigmoid group router; the block output equals fused_moe_prefill."""
+    I = 128
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 170, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 171, DEV)
+    w32 = W.normal((E, H), 0.02, 172, DEV, dtype=torch.float32)
+    bias = W.normal((E,), 0.05, 173, DEV, dtype=torch.float32)
+    nw = W.normal((H,), 0.02, 174, DEV, mean=1.0)
+    x = W.tokens(n, seed=175, device=DEV, hidden=H)
+    ng, tg = groups
+    y, ids, wts, logits = fused_moe.moe_block_prefill(x, nw, 1e-6, w32, w_gu, w_d, top_k=top_k, bias=bias,
+                                                      scoring=scoring, n_group=ng, topk_group=tg, scale=1.5)
+    xn = fused_ops.rms_norm(x, nw, 1e-6)
+    i2, w2, l2 = fused_ops.route(xn, w32, bias, top_k=top_k, scoring=scoring, n_group=ng, topk_group=tg, scale=1.5)
+    assert torch.equal(logits, l2) and torch.equal(ids, i2.long()) and torch.equal(wts, w2)
+    y2 = fused_moe.fused_moe_prefill(xn, w_gu, w_d, i2, w2, residual=x)
+    assert torch.equal(y, y2)
+    ref_ids, _ = O.router_select(logits.cpu(), bias.cpu(), scoring=scoring, n_group=ng, topk_group=tg, top_k=top_k,
+                                 scale=1.5)
+    assert torch.equal(ids.cpu(), ref_ids)
+
+
 def test_moe_block_prefill_zipf_2048_128_row_blocks(blk):
     """2048 Zipf-routed tokens average 220 pairs per expert, so bf16 experts take 128-row blocks: the block
     equals the unfused chain bit for bit, and a seeded subset matches the oracle."""
