@@ -513,14 +513,19 @@ def box_info():
     p = torch.cuda.get_device_properties(0)
     info = {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
             "host": platform.node()}
-    smi = shutil.which("rocm-smi")
-    if smi:
-        try:
-            r = subprocess.run([smi, "--showclocks", "--json"], capture_output=True, text=True, timeout=20)
-            card = next(iter(json.loads(r.stdout).values()))
-            info["clocks"] = {k: v for k, v in card.items() if "clock" in k.lower() and ("sclk" in k.lower() or "mclk" in k.lower())}
-        except Exception as e:  # clocks are informational only
-            info["clocks"] = f"unavailable: {type(e).__name__}"
+    # clocks from the amdgpu sysfs tables (the current level is marked '*'); read as files, no child
+    # process, so the run stays safe under a profiler that initialises the GPU in every process it starts
+    clocks = {}
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        for table in ("pp_dpm_sclk", "pp_dpm_mclk"):
+            try:
+                with open(os.path.join(dev, table)) as f:
+                    cur = [ln.split(":", 1)[-1].strip(" *\n") for ln in f if ln.rstrip().endswith("*")]
+            except OSError:
+                continue
+            if cur:
+                clocks[f"{os.path.basename(os.path.dirname(dev))}.{table[7:]}"] = cur[0]
+    info["clocks"] = clocks or "unavailable"
     return info
 
 
