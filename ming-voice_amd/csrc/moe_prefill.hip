@@ -225,11 +225,23 @@ __device__ __forceinline__ bf16x8_t lds_frag16(const char* base, int pos) {
   return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(base + pos));
 }
 
+// Rows of the expert block in spair that hold pairs (< P). align pads each expert's rows at the end of
+// its run, so they are a prefix of the block. Wave-uniform.
+template <int BM>
+__device__ __forceinline__ int valid_rows(const int* spair, int P) {
+  int n = 0;
+#pragma unroll
+  for (int r = 0; r < BM; r += kWave) n += __popcll(__ballot(spair[r + lane_id()] < P));
+  return __builtin_amdgcn_readfirstlane(n);
+}
+
 // The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
-// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j.
+// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j. Row fragments at or
+// past fm_live (wave-uniform) hold only padding rows: their LDS reads and MFMAs are skipped and their
+// accumulators stay zero (the epilogues store no padding row).
 template <class G, class XRowFn, class WRowFn, class BColFn>
 __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t K, XRowFn xrow,
-                                          WRowFn wrow, char* lds, int r0, BColFn bcol) {
+                                          WRowFn wrow, char* lds, int r0, BColFn bcol, int fm_live) {
   constexpr int NS = G::NS, LOADS = G::LOADS, FM = G::FM, FN = G::FN;
   const int lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
@@ -283,12 +295,13 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
           bf16x8_t fa[FM];
 #pragma unroll
           for (int i = 0; i < FM; ++i)
-            fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, 8 * g + 2 * lq + ks));
+            if (i < fm_live) fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, 8 * g + 2 * lq + ks));
 #pragma unroll
           for (int i = 0; i < FM; ++i)
+            if (i < fm_live)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
+              for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[ks][j], acc[i][j], 0, 0, 0);
         }
       }
     } else {
@@ -297,14 +310,16 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
         const int ch = ks * 4 + lq;
         bf16x8_t fa[FM], fb[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, ch));
+        for (int i = 0; i < FM; ++i)
+          if (i < fm_live) fa[i] = lds_frag16(sa, pos_row<G::AROW>(r0 + 16 * i + lr, ch));
 #pragma unroll
         for (int j = 0; j < FN; ++j) fb[j] = lds_frag16(sb, pos_row<G::ROWB>(bcol(j) + lr, ch));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
+          if (i < fm_live)
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
       }
     }
   }
@@ -342,8 +357,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   constexpr int FG = G::FN / 2;      // gate fragments of the wave; the next FG are the matching up ones
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
+  const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
   tile_gemm<G>(acc, a.H, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0,
-               [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); });
+               [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); }, fm_live);
 #pragma unroll
   for (int j = 0; j < FG; ++j) {
     const int64_t col = n0 + g0 + 16 * j + (lane & 15);
@@ -395,7 +411,9 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int r0 = wm * (BM / G::WM);
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
-  tile_gemm<G>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; });
+  const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
+  tile_gemm<G>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; },
+               fm_live);
 #pragma unroll
   for (int j = 0; j < G::FN; ++j) {
     const int64_t h = h0 + c0 + 16 * j + (lane & 15);
