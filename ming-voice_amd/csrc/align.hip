@@ -11,7 +11,13 @@ using namespace mmd;
 constexpr int kWaves = 16;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxSlots = 256;
+constexpr int kIdBatch = 8;            // id loads in flight per lane
+constexpr int kMaxStaged = 48 * 1024;  // pairs whose expert ids stay in LDS (2 bytes each) between the passes
+constexpr uint16_t kNoExpert = 0xffff;
 
+// STAGED: the counting pass keeps each pair's expert id in LDS (dynamic, P x 2 bytes), so the scatter pass
+// reads ids from LDS instead of a second, latency-bound pass over global memory.
+template <bool STAGED>
 __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict__ flat, int flat_dtype, int P, int E1,
                                                          int BM, int32_t* __restrict__ sorted_ids,
                                                          int32_t* __restrict__ bexp, int nb,
@@ -19,6 +25,7 @@ __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict_
   __shared__ int cnt[kWaves][kMaxSlots];                 // per-wave counts, then per-wave write cursors
   __shared__ unsigned long long lanes[kWaves][kMaxSlots]; // per-wave lane masks of one 64-pair chunk
   __shared__ int pend[kMaxSlots];                         // padded end row of each expert
+  extern __shared__ uint16_t staged[];                    // STAGED: expert id of pair p (kNoExpert: dropped)
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = lane_id();
 
@@ -33,9 +40,20 @@ __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict_
   // each wave owns a contiguous, 64-aligned segment of pairs
   const int seg = ((P + kWaves - 1) / kWaves + kWave - 1) / kWave * kWave;
   const int beg = min(P, wave * seg), end = min(P, beg + seg);
-  for (int p = beg + lane; p < end; p += kWave) {
-    const int64_t e = load_id(flat, flat_dtype, p);
-    if (e >= 0 && e < E1) atomicAdd(&cnt[wave][e], 1);
+  // ids in batches of kIdBatch loads per lane, all issued before the first is used (a lane past the end
+  // re-reads the segment's last id and discards it)
+  for (int c0 = beg; c0 < end; c0 += kWave * kIdBatch) {
+    int64_t ev[kIdBatch];
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) ev[u] = load_id(flat, flat_dtype, min(c0 + u * kWave + lane, end - 1));
+#pragma unroll
+    for (int u = 0; u < kIdBatch; ++u) {
+      const int p = c0 + u * kWave + lane;
+      if (p >= end) continue;
+      const bool valid = ev[u] >= 0 && ev[u] < E1;
+      if (STAGED) staged[p] = valid ? static_cast<uint16_t>(ev[u]) : kNoExpert;
+      if (valid) atomicAdd(&cnt[wave][ev[u]], 1);
+    }
   }
   __syncthreads();
 
@@ -73,7 +91,11 @@ __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict_
   for (int c0 = beg; c0 < end; c0 += kWave) {
     const int p = c0 + lane;
     int64_t e = -1;
-    if (p < end) e = load_id(flat, flat_dtype, p);
+    if (STAGED) {
+      if (p < end && staged[p] != kNoExpert) e = staged[p];
+    } else if (p < end) {
+      e = load_id(flat, flat_dtype, p);
+    }
     const bool valid = e >= 0 && e < E1;
     if (valid) atomicOr(&lanes[wave][e], 1ull << lane);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -128,8 +150,17 @@ extern "C" int mm_align_blocks(const void* flat, int flat_dtype, int64_t P, int3
              (long long)want);
   MM_REQUIRE(nb * block_m <= (1LL << 31) - 1, "align_blocks: too many rows");
   MM_REQUIRE(sorted_ids && bexp && (P == 0 || flat), "align_blocks: null pointer");
-  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(kThreads), 0, MM_STREAM(stream), flat, flat_dtype,
-                     static_cast<int>(P), static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp,
-                     static_cast<int>(nb), expert_offsets);
+  if (P <= kMaxStaged) {
+    const size_t lds = (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
+    int rc = mm::allow_lds(align_kernel<true>, static_cast<size_t>(kMaxStaged) * 2, "align_blocks");
+    if (rc) return rc;
+    hipLaunchKernelGGL(align_kernel<true>, dim3(1), dim3(kThreads), lds, MM_STREAM(stream), flat, flat_dtype,
+                       static_cast<int>(P), static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp,
+                       static_cast<int>(nb), expert_offsets);
+  } else {
+    hipLaunchKernelGGL(align_kernel<false>, dim3(1), dim3(kThreads), 0, MM_STREAM(stream), flat, flat_dtype,
+                       static_cast<int>(P), static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp,
+                       static_cast<int>(nb), expert_offsets);
+  }
   return mm::check_launch("align_blocks");
 }

@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <mutex>
+
 #include "mingmoe.h"
 
 // ------------------------------------------------------------------------------------------ host side
@@ -24,6 +26,24 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Number of compute units of the current device (queried once per device, thread-safe).
 int cu_count();
+
+// Dynamic LDS above the default limit needs an opt-in per kernel and device (done once each; the static
+// state is per kernel instantiation).
+template <class K>
+int allow_lds(K kernel, size_t bytes, const char* what) {
+  static std::mutex mu;
+  static bool done[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!done[dev]) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(bytes));
+    if (e != hipSuccess) return set_error(MM_ERR_HIP, "HIP error setting LDS size of %s: %s", what, hipGetErrorString(e));
+    done[dev] = true;
+  }
+  return MM_OK;
+}
 
 }  // namespace mm
 

@@ -12,8 +12,6 @@
 // 64-wide slabs of the activation rows and of the weight rows straight into LDS (global_load_lds, several
 // slabs in flight) and feeds v_mfma_f32_16x16x32_bf16 from there. int8 weights stay int8 in LDS and are
 // widened to bf16 (exact for |q| <= 127) as fragments are read.
-#include <mutex>
-
 #include "mm_common.h"
 #include "mm_select.h"
 
@@ -478,29 +476,13 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   }
 }
 
-// Dynamic LDS above the default limit needs an opt-in per kernel and device (done once each).
-template <class K>
-int allow_lds(K kernel, size_t bytes, const char* what) {
-  static std::mutex mu;
-  static bool done[64] = {false};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!done[dev]) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(bytes));
-    if (e != hipSuccess) return mm::set_error(MM_ERR_HIP, "HIP error setting LDS size of %s: %s", what, hipGetErrorString(e));
-    done[dev] = true;
-  }
-  return MM_OK;
-}
 
 template <bool Q, int BN, int NW, int BM>
 int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
   using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.I + G::BN / 2 - 1) / (G::BN / 2);
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM>, G::LDS, "prefill_gate_up");
+  int rc = mm::allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM>, G::LDS, "prefill_gate_up");
   if (rc) return rc;
   hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
   return mm::check_launch("moe_prefill gate_up");
@@ -511,7 +493,7 @@ int launch_down(const PrefillArgs& a, int64_t nb, hipStream_t st) {
   using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.H + G::BN - 1) / G::BN;
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = allow_lds(prefill_down_kernel<Q, BN, NW, BM>, G::LDS, "prefill_down");
+  int rc = mm::allow_lds(prefill_down_kernel<Q, BN, NW, BM>, G::LDS, "prefill_down");
   if (rc) return rc;
   hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
   return mm::check_launch("moe_prefill down");

@@ -122,8 +122,11 @@ def test_router_ties_pick_lowest_index():
 # ------------------------------------------------------------------------------------------------ align
 
 @pytest.mark.parametrize("P,E1,dtype", [(0, 65, torch.int64), (7, 65, torch.int64), (3584, 65, torch.int32),
-                                        (14336, 65, torch.int64), (5000, 256, torch.int64), (33, 1, torch.int32)])
+                                        (14336, 65, torch.int64), (5000, 256, torch.int64), (33, 1, torch.int32),
+                                        (49152, 256, torch.int32), (50001, 65, torch.int64)])
 def test_align_bit_exact(P, E1, dtype):
+    """Pairs up to 48 K keep their expert ids in LDS between the counting and scatter passes; above that the
+    scatter re-reads them (P = 49152 and 50001 straddle the switch)."""
     g = torch.Generator().manual_seed(P + E1)
     flat = torch.randint(0, E1, (P,), generator=g).to(dtype)
     if P > 100:
