@@ -535,8 +535,8 @@ def main():
         pmc_probe()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the MoE block path has no multi-GPU code in this build "
-              "(use --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: the MoE block path has no multi-GPU code (use --gpus 1)",
+              file=sys.stderr)
         sys.exit(2)
     import _mingmoe
     import workloads as W

@@ -1,7 +1,7 @@
 """CPU oracle of the Ming thinker MoE block — TEST INFRASTRUCTURE ONLY.
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as
-the checker (or the timed CPU baseline); the product path (ming-voice_amd/) never calls it.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only to
+check results against (or as the timed CPU baseline); the product path (ming-voice_amd/) never calls it.
 
 It restates, in plain torch (fp32 math on the CPU) and numpy (integer work), the algorithm of the reference
 kernels and torch paths, with the same rounding points. Each function cites the reference file:line it

@@ -1,7 +1,7 @@
 """CPU oracle of the Talker's three small kernels — TEST INFRASTRUCTURE ONLY.
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as
-the checker (or the timed CPU baseline); the product path (ming-voice_amd/) never calls it.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only to
+check results against (or as the timed CPU baseline); the product path (ming-voice_amd/) never calls it.
 
 It restates in plain torch (fp32 on the CPU) the algorithm of fast_talker.py's Triton kernels, with their
 rounding points. How each function is pinned (closed forms, the unfused torch path of engine.py's
