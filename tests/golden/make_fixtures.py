@@ -17,6 +17,9 @@ What the expectations restate, and from where (paths relative to the Ming Voice 
             a = bf16(bf16(silu(g)) * u), part = bf16(a . Wd), y = bf16(sum_k w_k * part_k) + x rounded
             to bf16; dot products in float64 (the kernels' fp32 sums differ from these by far less than
             one bf16 ulp at these sizes, so the tests compare with the bf16 tolerance).
+  moe int8  the same block with the experts quantised per row with bf16 scales (engine.py:126-147 with
+            quantize_rows_int8, scale rounded to bf16 and q = round(w / scale)); fused_moe.py:34-38,
+            60-61: the row scale multiplies the float64 accumulator before each bf16 rounding.
 bf16 rounding is done on the float32 bit pattern (round to nearest, ties to even) with numpy integers.
 """
 import math
@@ -77,6 +80,21 @@ def quantize(w):
     return q, s
 
 
+def quantize_bf16_scales(w):
+    """Rows of w (last dim) -> (q int8, scale as bf16 values): scale = bf16(max(|w|, 1e-8) / 127) and
+    q = round-half-even(w / scale) clamped to [-127, 127], the division in fp32."""
+    flat = w.reshape(-1, w.shape[-1])
+    q = np.zeros(flat.shape, np.int8)
+    sc = np.zeros(flat.shape[0], np.float32)
+    for r in range(flat.shape[0]):
+        amax = max(max(abs(float(v)) for v in flat[r]), 1e-8)
+        scale = bf16(f32(f32(amax) / 127.0))
+        sc[r] = scale
+        for c in range(flat.shape[1]):
+            q[r, c] = max(-127, min(127, round(f32(float(flat[r, c]) / scale))))
+    return q.reshape(w.shape), sc.reshape(w.shape[:-1])
+
+
 def select(logits, bias, top_k, E):
     N = logits.shape[0]
     ids = np.zeros((N, top_k + 1), np.int64)
@@ -97,20 +115,24 @@ def select(logits, bias, top_k, E):
     return ids, wts
 
 
-def moe(x, w_gu, w_d, ids, wts):
+def moe(x, w_gu, w_d, ids, wts, s_gu=None, s_d=None):
     N, H = x.shape
     I = w_d.shape[-1]
     y = np.zeros((N, H), np.float32)
     a_rows = np.zeros((N * ids.shape[1], I), np.float32)
+    one = lambda *_: 1.0  # noqa: E731
+    sg = (lambda e, r: float(s_gu[e, r])) if s_gu is not None else one
+    sd = (lambda e, h: float(s_d[e, h])) if s_d is not None else one
     for t in range(N):
         acc = np.zeros(H, np.float64)
         for k in range(ids.shape[1]):
             e = int(ids[t, k])
-            g = [bf16(sum(float(x[t, h]) * float(w_gu[e, r, h]) for h in range(H))) for r in range(I)]
-            u = [bf16(sum(float(x[t, h]) * float(w_gu[e, I + r, h]) for h in range(H))) for r in range(I)]
+            g = [bf16(sum(float(x[t, h]) * float(w_gu[e, r, h]) for h in range(H)) * sg(e, r)) for r in range(I)]
+            u = [bf16(sum(float(x[t, h]) * float(w_gu[e, I + r, h]) for h in range(H)) * sg(e, I + r))
+                 for r in range(I)]
             a = [bf16(bf16(gg / (1.0 + math.exp(-gg))) * uu) for gg, uu in zip(g, u)]
             a_rows[t * ids.shape[1] + k] = a
-            part = [bf16(sum(a[r] * float(w_d[e, h, r]) for r in range(I))) for h in range(H)]
+            part = [bf16(sum(a[r] * float(w_d[e, h, r]) for r in range(I)) * sd(e, h)) for h in range(H)]
             acc += float(wts[t, k]) * np.array(part, np.float64)
         y[t] = [bf16(bf16(v) + float(x[t, h])) for h, v in enumerate(acc)]
     return y, a_rows
@@ -148,6 +170,11 @@ def main():
     wts = np.array([[0.6, 0.4, 1.0], [0.7, 0.3, 1.0], [0.5, 0.5, 1.0]], np.float32)
     fx["moe_x"], fx["moe_w_gu"], fx["moe_w_d"], fx["moe_ids"], fx["moe_wts"] = x, w_gu, w_d, ids, wts
     fx["moe_y"], fx["moe_a"] = moe(x, w_gu, w_d, ids, wts)
+    # the same block on int8 experts with bf16 row scales
+    q_gu, s_gu = quantize_bf16_scales(w_gu)
+    q_d, s_d = quantize_bf16_scales(w_d)
+    fx["moe_q_gu"], fx["moe_s_gu"], fx["moe_q_d"], fx["moe_s_d"] = q_gu, s_gu, q_d, s_d
+    fx["moe_y_i8"], fx["moe_a_i8"] = moe(x, q_gu, q_d, ids, wts, s_gu, s_d)
     np.savez_compressed(OUT, **fx)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes)")
 

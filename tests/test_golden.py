@@ -59,3 +59,21 @@ def test_moe_matches_golden(fx):
     # most outputs agree to the bit: a dropped rounding point would move far more than a few of them
     assert (a.float() == torch.from_numpy(fx["moe_a"])).float().mean() > 0.9
     assert (y.float() == torch.from_numpy(fx["moe_y"])).float().mean() > 0.9
+
+
+def test_int8_block_matches_golden(fx):
+    """The same block on int8 experts with bf16 row scales: the quantiser and the int8 MoE restated by the
+    oracle reproduce the brute force's codes, scales and outputs."""
+    w_gu = torch.from_numpy(fx["moe_w_gu"]).to(BF)
+    w_d = torch.from_numpy(fx["moe_w_d"]).to(BF)
+    q_gu, s_gu = O.quantize_rows_int8(w_gu, scale_dtype=BF)
+    q_d, s_d = O.quantize_rows_int8(w_d, scale_dtype=BF)
+    assert torch.equal(q_gu, torch.from_numpy(fx["moe_q_gu"])) and torch.equal(q_d, torch.from_numpy(fx["moe_q_d"]))
+    assert torch.equal(s_gu.float(), torch.from_numpy(fx["moe_s_gu"]))
+    assert torch.equal(s_d.float(), torch.from_numpy(fx["moe_s_d"]))
+    x = torch.from_numpy(fx["moe_x"]).to(BF)
+    y, a = O.moe(x, q_gu, q_d, torch.from_numpy(fx["moe_ids"]), torch.from_numpy(fx["moe_wts"]), s_gu, s_d,
+                 residual=x, return_a=True)
+    torch.testing.assert_close(a.float(), torch.from_numpy(fx["moe_a_i8"]), rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(y.float(), torch.from_numpy(fx["moe_y_i8"]), rtol=2e-2, atol=1e-2)
+    assert (y.float() == torch.from_numpy(fx["moe_y_i8"])).float().mean() > 0.9

@@ -76,3 +76,32 @@ def test_prefill_golden(fx, reps):
     ids, wts = fx["moe_ids"].repeat(reps, 1).to(DEV), fx["moe_wts"].repeat(reps, 1).to(DEV)
     y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts, residual=x)
     _close(y, fx["moe_y"].repeat(reps, 1))
+
+
+def _int8_block(fx):
+    return (fx["moe_q_gu"].to(DEV), fx["moe_s_gu"].to(BF).to(DEV), fx["moe_q_d"].to(DEV),
+            fx["moe_s_d"].to(BF).to(DEV))
+
+
+def test_quantize_bf16_scales_golden(fx):
+    q, s = fused_moe.quantize_rows_int8(fx["moe_w_gu"].to(BF).to(DEV), scale_dtype=BF)
+    assert torch.equal(q.cpu(), fx["moe_q_gu"]) and torch.equal(s.float().cpu(), fx["moe_s_gu"])
+
+
+def test_decode_int8_golden(fx):
+    x = fx["moe_x"].to(BF).to(DEV)
+    q_gu, s_gu, q_d, s_d = _int8_block(fx)
+    ids, wts = fx["moe_ids"].to(DEV), fx["moe_wts"].to(DEV)
+    a_buf = torch.empty(ids.numel(), q_d.shape[-1], device=DEV, dtype=BF)
+    y = fused_moe.fused_moe_decode(x, q_gu, q_d, ids, wts, a_buf=a_buf, s_gu=s_gu, s_d=s_d, residual=x)
+    _close(a_buf, fx["moe_a_i8"])
+    _close(y, fx["moe_y_i8"])
+
+
+@pytest.mark.parametrize("reps", [1, 4])
+def test_prefill_int8_golden(fx, reps):
+    x = fx["moe_x"].to(BF).repeat(reps, 1).to(DEV)
+    q_gu, s_gu, q_d, s_d = _int8_block(fx)
+    ids, wts = fx["moe_ids"].repeat(reps, 1).to(DEV), fx["moe_wts"].repeat(reps, 1).to(DEV)
+    y = fused_moe.fused_moe_prefill(x, q_gu, q_d, ids, wts, s_gu=s_gu, s_d=s_d, residual=x)
+    _close(y, fx["moe_y_i8"].repeat(reps, 1))
