@@ -1,7 +1,8 @@
 // Grouped prefill MoE on bf16 MFMA (fused_moe.py:92-196).
 //
-// mm_align_blocks groups the (token, slot) pairs by expert into blocks of 64 rows and reports each expert's
-// padded row range. A tile is (expert block of 64 pairs) x (BN = 128 or 256 output columns):
+// mm_align_blocks groups the (token, slot) pairs by expert into blocks of BM rows (64, or 128 for bf16
+// experts averaging at least 128 pairs) and reports each expert's padded row range. A tile is (expert block
+// of BM pairs) x (BN = 128 or 256 output columns):
 //   GATE_UP: columns are BN/2 gate + the matching BN/2 up rows of W_gu[e]; the epilogue writes
 //            a[pair] = bf16(bf16(silu(bf16(g))) * bf16(u)) (int8: row scale on the fp32 accumulator first).
 //   DOWN:    columns are BN rows of W_d[e]; the epilogue writes part[pair] = bf16(a . Wd^T [* s]).
@@ -26,10 +27,12 @@ constexpr int kBM = 128;
 constexpr int kBMSmall = 64;
 constexpr int kXcds = 8;
 // Tile shape per weight type and GEMM: output columns per tile (BN) and waves per workgroup. The k-slab is
-// 64 elements; 128-column bf16 tiles keep 3 slabs in flight, int8 and 256-column tiles 2 (LDS = slabs x
-// (8 KB + BN x 64 x weight bytes), two workgroups per CU). Waves split the 64 x BN tile as 1 x 4 (4 waves,
-// each 64 rows x BN/4) or 2 x NW/2 (8 waves, or 64-column tiles). Measured on the 512-token block: 8-wave
-// 128-column bf16 tiles are the fastest of 64/128/256 columns x 4/8 waves x 2/3 slabs.
+// 64 elements; 128-column bf16 tiles of 64-pair blocks keep 3 slabs in flight, int8, 256-column and
+// 128-pair tiles 2 (LDS = slabs x (BM x 128 B + BN x 64 x weight bytes), two workgroups per CU). Waves
+// split the BM x BN tile as 1 x 4 (4 waves, each BM rows x BN/4) or 2 x NW/2 (8 waves, or 64-column
+// tiles). Measured on the 512-token block: 8-wave 128-column bf16 tiles are the fastest of 64/128/256
+// columns x 4/8 waves x 2/3 slabs; on the 2048-token Zipf block the same shape with 128-pair blocks beats
+// 16 waves, 4 waves of 64 x 64, 3-4 slabs, 32-k slabs and 256-column tiles.
 #ifndef MM_PREFILL_GU_BN_BF16
 #define MM_PREFILL_GU_BN_BF16 128
 #endif
