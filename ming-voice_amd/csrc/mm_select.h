@@ -288,4 +288,32 @@ __device__ __forceinline__ float row_rstd256(const typename TX::T* xr, int64_t n
   return rsqrtf(t / static_cast<float>(n) + eps);
 }
 
+// The same normalisation by one wave holding a whole bf16 row: lane l holds chunks l + 64 j (j < NC; zero
+// past the row). Chunk l + 64 j is chunk (l + 64 j) % 256 of row_rstd256's thread of that index, in its
+// wave j % 4, and a thread adds its chunks in j order, so summing per j % 4, reducing each by wave_sum and
+// adding the four in order gives row_rstd256's bits. The chunks become bf16(w * bf16(x * rstd)) in place,
+// as mm_rms_norm writes them (nv: the norm weight's chunks, bf16).
+template <int NC>
+__device__ __forceinline__ void norm_row_chunks64(uint4 (&xv)[NC], const uint4 (&nv)[NC], int64_t n, float eps) {
+  float ssw[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < NC; ++j) ssw[j % 4] = chunk_ss_bf16x8(xv[j], ssw[j % 4]);
+  const float tot = ((wave_sum(ssw[0]) + wave_sum(ssw[1])) + wave_sum(ssw[2])) + wave_sum(ssw[3]);
+  const float rstd = rsqrtf(tot / static_cast<float>(n) + eps);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const uint32_t xq[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+    const uint32_t nq[4] = {nv[j].x, nv[j].y, nv[j].z, nv[j].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = round_bf16(__uint_as_float(nq[i] << 16) * round_bf16(__uint_as_float(xq[i] << 16) * rstd));
+      const float hi =
+          round_bf16(__uint_as_float(nq[i] & 0xffff0000u) * round_bf16(__uint_as_float(xq[i] & 0xffff0000u) * rstd));
+      o[i] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+    }
+    xv[j] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 }  // namespace mmd

@@ -289,6 +289,87 @@ __global__ __launch_bounds__(kRouterWaves * 64) void router_mfma_kernel(const ty
   }
 }
 
+// router_mfma_kernel with the RMSNorm fused, for the prefill block (bf16 rows of at most 512 * NC
+// elements, H a multiple of 8, 16-byte aligned): wave w first normalises token row t0 + w in one pass
+// (norm_row_chunks64: the bits of mm_rms_norm) into LDS, and the workgroups of the first expert group store
+// those rows to xn_out; the MFMA loop is router_mfma_kernel's, with the token operand read from LDS, so
+// the logits are those of mm_rms_norm + router_mfma_kernel bit for bit. Saves the norm's launch.
+template <int NC>
+__global__ __launch_bounds__(kRouterWaves * 64) void router_norm_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                             int n_tokens, int64_t H, int64_t xs,
+                                                                             const uint16_t* __restrict__ norm_w,
+                                                                             float eps, const float* __restrict__ w32,
+                                                                             int E, float* __restrict__ logits,
+                                                                             uint16_t* __restrict__ xn_out) {
+  constexpr int U = 8;  // 16-k groups in flight per lane
+  extern __shared__ uint4 rows_lds[];
+  __shared__ float red[kRouterWaves][16][17];
+  uint16_t* xl = reinterpret_cast<uint16_t*>(rows_lds);
+  const int64_t P = H + 16;  // LDS row pitch (elements): the 16 rows an operand load reads hit distinct banks
+  const int lane = lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+  {
+    const int t = t0 + wave;
+    const int64_t nch = H / 8;
+    const rsrc_t xr = make_rsrc(x, static_cast<int64_t>(n_tokens) * xs * 2);
+    const rsrc_t nr = make_rsrc(norm_w, H * 2);
+    uint4 xv[NC], nv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t c = lane + 64 * j;
+      xv[j] = buf16(xr, c < nch && t < n_tokens ? static_cast<uint32_t>(t * xs * 2 + c * 16) : kPast);
+      nv[j] = buf16(nr, c < nch ? static_cast<uint32_t>(c * 16) : kPast);
+    }
+    norm_row_chunks64<NC>(xv, nv, H, eps);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t c = lane + 64 * j;
+      if (c < nch) {
+        *reinterpret_cast<uint4*>(xl + wave * P + c * 8) = xv[j];
+        if (blockIdx.x == 0 && t < n_tokens) *reinterpret_cast<uint4*>(xn_out + static_cast<int64_t>(t) * H + c * 8) = xv[j];
+      }
+    }
+  }
+  __syncthreads();
+  const int row = lane % 16, q = lane / 16;
+  const int e = e0 + row;
+  const bool exp_ok = e < E;
+  const int64_t KW = (H + kRouterWaves * 16 - 1) / (kRouterWaves * 16) * 16;
+  const int64_t kw0 = static_cast<int64_t>(wave) * KW;
+  const float* wr = w32 + static_cast<int64_t>(exp_ok ? e : 0) * H;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t j0 = 0; j0 < KW; j0 += 16 * U) {
+    float4 bv[U];
+    uint2 araw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = kw0 + j0 + 16 * u + 4 * q;
+      const bool in = j0 + 16 * u < KW && k < H;
+      bv[u] = *reinterpret_cast<const float4*>(in && exp_ok ? wr + k : g_zero4);
+      araw[u] = in ? *reinterpret_cast<const uint2*>(xl + row * P + k) : make_uint2(0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(araw[u].x << 16), bv[u].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(araw[u].x & 0xffff0000u), bv[u].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(araw[u].y << 16), bv[u].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(araw[u].y & 0xffff0000u), bv[u].w, acc, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) red[wave][4 * q + v][row] = acc[v];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int i = threadIdx.x / 16, jj = threadIdx.x % 16;
+    if (t0 + i < n_tokens && e0 + jj < E) {
+      float sum = red[0][i][jj];
+#pragma unroll
+      for (int w = 1; w < kRouterWaves; ++w) sum += red[w][i][jj];
+      logits[static_cast<int64_t>(t0 + i) * E + e0 + jj] = sum;
+    }
+  }
+}
+
 struct SelectArgs {
   const float* logits;
   int n_tokens, E;
@@ -392,16 +473,35 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
 namespace mm {
 
 // Router of the MoE block front for bf16 tokens: RMSNorm (norm_w bf16, eps) into xn_out ([n_tokens, H]
-// bf16), logits of the normalised rows, then the selection with the shared expert appended. Up to 8 tokens
-// the norm runs inside the logits kernel; larger batches normalise first (mm_rms_norm), which is faster
-// than repeating the row reduction in every router workgroup. Either way xn is bit-identical.
+// bf16), logits of the normalised rows, then the selection with the shared expert appended. The norm runs
+// inside the logits kernel (router_gemv_bf16_kernel up to 8 tokens, router_norm_mfma_kernel above, each
+// workgroup normalising its 16 token rows); rows too long or misaligned for those normalise first
+// (mm_rms_norm). Either way xn is bit-identical.
 int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
                  const float* w32, const SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
                  int64_t out_row_stride, void* xn_out, hipStream_t s) {
   MM_REQUIRE(n_tokens >= 1 && n_tokens <= 0x7fffffffLL, "router: bad token count");
   int rc;
+  const bool fused = n_tokens > 8 && H % 8 == 0 && H <= 4096 && xs % 8 == 0 && xn_out && aligned16(x) &&
+                     aligned16(norm_w) && aligned16(xn_out) && aligned16(w32) && n_tokens * xs * 2 < (1LL << 31);
   if (n_tokens <= 8) {
     rc = launch_logits<BF16>(x, n_tokens, H, xs, w32, sp.E, logits, s, norm_w, eps, xn_out);
+  } else if (fused) {  // the norm inside the logits kernel: one launch fewer
+    dim3 grid(static_cast<unsigned>((sp.E + 15) / 16), static_cast<unsigned>((n_tokens + 15) / 16));
+    const size_t lds = static_cast<size_t>(16) * (H + 16) * 2;
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* nw = static_cast<const uint16_t*>(norm_w);
+    auto* xo = static_cast<uint16_t*>(xn_out);
+    if (H <= 2048) {
+      if ((rc = allow_lds(router_norm_mfma_kernel<4>, lds, "router_norm"))) return rc;
+      hipLaunchKernelGGL(router_norm_mfma_kernel<4>, grid, dim3(kRouterWaves * 64), lds, s, xp,
+                         static_cast<int>(n_tokens), H, xs, nw, eps, w32, static_cast<int>(sp.E), logits, xo);
+    } else {
+      if ((rc = allow_lds(router_norm_mfma_kernel<8>, lds, "router_norm"))) return rc;
+      hipLaunchKernelGGL(router_norm_mfma_kernel<8>, grid, dim3(kRouterWaves * 64), lds, s, xp,
+                         static_cast<int>(n_tokens), H, xs, nw, eps, w32, static_cast<int>(sp.E), logits, xo);
+    }
+    if ((rc = check_launch("router_norm"))) return rc;
   } else {
     rc = mm_rms_norm(x, MM_BF16, n_tokens, H, xs, norm_w, MM_BF16, eps, xn_out, MM_BF16, H, s);
     if (rc) return rc;
