@@ -151,11 +151,26 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
   const int64_t e_n = n0 + e_i;
   const bool e_on = e_mm < MG && e_n < a.N;
   const int64_t e_nc = e_n < a.N ? e_n : a.N - 1;
-  const float bias = (!GLU && a.b) ? bf16_to_f32(a.b[e_nc]) : 0.f;
+  // A single token row (decode): bias and residual through buffer resources (empty when absent: the load
+  // returns 0, no branch) and the row's activation chunks, all issued with the weights, so the wave waits
+  // for memory once instead of once per conditional load. Several rows keep the plain loads (prefetching
+  // them costs more registers than it saves).
+  constexpr bool kPrefetch = MG == 1;
+  const rsrc_t brs = make_rsrc(a.b, (kPrefetch && !GLU && a.b) ? a.N * 2 : 0);
+  const rsrc_t rrs = make_rsrc(a.res, (kPrefetch && !GLU && a.res) ? static_cast<int64_t>(a.M) * a.rs * 2 : 0);
+  const float bias = kPrefetch ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(brs, static_cast<int>(e_nc * 2), 0, 0))
+                               : ((!GLU && a.b) ? bf16_to_f32(a.b[e_nc]) : 0.f);
+  uint4 xfirst[NC];
+  if constexpr (kPrefetch) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) xfirst[j] = *reinterpret_cast<const uint4*>(a.x + cc[j] * 8);
+  }
   for (int m0 = 0; m0 < kMaxM; m0 += MG) {
     if (m0 >= a.M) break;  // uniform
     const int e_m = min(m0 + e_mm, a.M - 1);
-    const float res = (!GLU && a.res) ? bf16_to_f32(a.res[e_m * a.rs + e_nc]) : 0.f;
+    const float res =
+        kPrefetch ? bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rrs, static_cast<int>((e_m * a.rs + e_nc) * 2), 0, 0))
+                  : ((!GLU && a.res) ? bf16_to_f32(a.res[e_m * a.rs + e_nc]) : 0.f);
     uint4 xg[MG][NC];
     if constexpr (kShareNorm) {
       for (int mm = wave; mm < MG; mm += 4) {
@@ -181,7 +196,8 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
       for (int mm = 0; mm < MG; ++mm) {
         const uint16_t* xr = a.x + min(m0 + mm, a.M - 1) * a.xs;
 #pragma unroll
-        for (int j = 0; j < NC; ++j) xg[mm][j] = *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
+        for (int j = 0; j < NC; ++j)
+          xg[mm][j] = (kPrefetch && m0 == 0) ? xfirst[j] : *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
       }
     }
     float keep = 0.f, keep_up = 0.f;
