@@ -150,6 +150,25 @@ int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, c
                         void* ids, int ids_dtype, float* wts, void* a_buf, void* workspace, int add_residual,
                         void* y, int64_t y_row_stride, void* stream);
 
+/* mm_moe_block_decode with its scratch (the normalised rows and the gated activations, the `workspace` and
+ * `a_buf` of mm_moe_block_decode) held in a static device array of MM_NOALLOC_SCRATCH_BYTES per GPU instead of
+ * caller buffers: the call allocates nothing and takes no scratch argument; the caller passes the inputs and
+ * the outputs (logits, ids, wts, y). Same kernels and bit-identical results as mm_moe_block_decode.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Limit: mm_moe_block_decode_noalloc_bytes()
+ * of the shape must not exceed MM_NOALLOC_SCRATCH_BYTES (larger shapes return MM_ERR_ARG). Each GPU holds its
+ * own array from the first call on it until the process ends; calls that overlap on one GPU (two streams or
+ * threads at once) share that array and race. */
+#define MM_NOALLOC_SCRATCH_BYTES (2 * 1024 * 1024)
+/* Bytes of that scratch a shape needs: the normalised rows (n_tokens * hidden bf16, rounded up to 256 bytes)
+ * then the activations (n_tokens * (top_k + 1) * inter bf16); -1 for an invalid shape. */
+int64_t mm_moe_block_decode_noalloc_bytes(int64_t n_tokens, int64_t top_k, int64_t hidden, int64_t inter);
+int mm_moe_block_decode_noalloc(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                                const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                                int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                                void* ids, int ids_dtype, float* wts, int add_residual, void* y,
+                                int64_t y_row_stride, void* stream);
+
 /* Grouped prefill MoE over the blocks produced by mm_align_blocks (same math as mm_moe_decode).
  * Replaces fused_moe.fused_moe_prefill / _moe_gu_grouped / _moe_down_grouped (fused_moe.py:92-196).
  * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs

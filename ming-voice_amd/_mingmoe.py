@@ -57,6 +57,9 @@ SIGNATURES = {
                         ctypes.c_int32, _P, _I64, _P, _P, _P, _I64, _I32, _P], ctypes.c_int),
     "mm_moe_block_decode": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
                              ctypes.POINTER(Experts), _P, _P, _I32, _P, _P, _P, _I32, _P, _I64, _P], ctypes.c_int),
+    "mm_moe_block_decode_noalloc_bytes": ([_I64, _I64, _I64, _I64], ctypes.c_int64),
+    "mm_moe_block_decode_noalloc": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
+                                     ctypes.POINTER(Experts), _P, _P, _I32, _P, _I32, _P, _I64, _P], ctypes.c_int),
     "mm_prefill_block_m": ([_I64, _I64, _I64, _I32], ctypes.c_int32),
     "mm_moe_block_prefill": ([_P, _I64, _I64, _P, _F32, _P, _I64, _P, _I32, _I32, _I32, _I32, _F32,
                               ctypes.POINTER(Experts), _P, _P, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _I32, _P,

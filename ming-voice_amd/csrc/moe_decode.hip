@@ -604,25 +604,25 @@ int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const v
 // to the workspace), selection, gate/up on the normalised rows, down + combine with the raw rows as
 // residual. (Selecting in the router's last-finishing workgroup instead costs more in device-wide fences
 // than the launch it saves.) The ids / weights it writes are the ones the unfused chain produces.
-extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
-                                   const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
-                                   int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
-                                   void* ids, int ids_dtype, float* wts, void* a_buf, void* workspace,
-                                   int add_residual, void* y, int64_t y_row_stride, void* stream) {
-  int rc = mm::check_experts("moe_block_decode", ex);
+static int block_decode(const char* who, const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w,
+                        float eps, const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                        int topk_group, int top_k, float scale, const mm_experts* ex, float* logits, void* ids,
+                        int ids_dtype, float* wts, void* a_buf, void* workspace, int add_residual, void* y,
+                        int64_t y_row_stride, void* stream) {
+  int rc = mm::check_experts(who, ex);
   if (rc) return rc;
   const int64_t nk = static_cast<int64_t>(top_k) + 1;
   rc = mm::check_router_args(n_tokens, n_experts, scoring, n_group, topk_group, top_k, 1, ids, ids_dtype, wts, nk);
   if (rc) return rc;
   MM_REQUIRE(n_tokens >= 1 && n_tokens <= kMaxTokens && n_tokens * nk <= kMaxPairs,
-             "moe_block_decode: 1..%d tokens with (top_k + 1) * tokens <= %d", kMaxTokens, kMaxPairs);
-  MM_REQUIRE(ex->n_slots == n_experts + 1, "moe_block_decode: expert slots (%lld) must be n_experts + 1 (shared last)",
+             "%s: 1..%d tokens with (top_k + 1) * tokens <= %d", who, kMaxTokens, kMaxPairs);
+  MM_REQUIRE(ex->n_slots == n_experts + 1, "%s: expert slots (%lld) must be n_experts + 1 (shared last)", who,
              (long long)ex->n_slots);
-  MM_REQUIRE(x && norm_w && w32 && logits && a_buf && workspace && y, "moe_block_decode: null pointer");
-  MM_REQUIRE(x_row_stride >= ex->hidden && y_row_stride >= ex->hidden, "moe_block_decode: row stride smaller than hidden");
+  MM_REQUIRE(x && norm_w && w32 && logits && a_buf && workspace && y, "%s: null pointer", who);
+  MM_REQUIRE(x_row_stride >= ex->hidden && y_row_stride >= ex->hidden, "%s: row stride smaller than hidden", who);
   MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0 && mm::aligned16(a_buf) && mm::aligned16(workspace),
-             "moe_block_decode: x, a_buf and workspace must be 16-byte aligned");
-  MM_REQUIRE(ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "moe_block_decode: shape too large");
+             "%s: x, a_buf and workspace must be 16-byte aligned", who);
+  MM_REQUIRE(ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "%s: shape too large", who);
   hipStream_t st = MM_STREAM(stream);
   const mmd::SelectParams sp{bias, static_cast<int>(n_experts), scoring, n_group, topk_group, top_k, scale, 1};
   void* xn = workspace;
@@ -663,4 +663,83 @@ extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_ro
   rc = q ? dispatch_a<true>(a, st) : dispatch_a<false>(a, st);
   if (rc) return rc;
   return q ? dispatch_b<true>(a, st) : dispatch_b<false>(a, st);
+}
+
+extern "C" int mm_moe_block_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w, float eps,
+                                   const float* w32, int64_t n_experts, const float* bias, int scoring, int n_group,
+                                   int topk_group, int top_k, float scale, const mm_experts* ex, float* logits,
+                                   void* ids, int ids_dtype, float* wts, void* a_buf, void* workspace,
+                                   int add_residual, void* y, int64_t y_row_stride, void* stream) {
+  return block_decode("moe_block_decode", x, n_tokens, x_row_stride, norm_w, eps, w32, n_experts, bias, scoring,
+                      n_group, topk_group, top_k, scale, ex, logits, ids, ids_dtype, wts, a_buf, workspace,
+                      add_residual, y, y_row_stride, stream);
+}
+
+// ------------------------------------------------------------------------------- allocation-free variant
+//
+// The scratch of mm_moe_block_decode (the normalised rows and the gated activations) in a file-scope device
+// array instead of caller buffers. Each device holds its own copy at its own address, found once per device
+// with hipGetSymbolAddress; the host never passes the array's name itself (a host-side stand-in) to a kernel.
+// Every byte the kernels read from it is written earlier in the same call (the router writes all normalised
+// rows, gate/up every activation row of a kept pair, and down never reads the row of a dropped pair), so
+// nothing needs clearing between calls. Calls that overlap on one device share the array and race.
+
+static __device__ __align__(256) unsigned char scratch[MM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The current device's address of `scratch` (looked up on the first call on each device).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return mm::set_error(MM_ERR_HIP, "HIP error in hipGetDevice: %s", hipGetErrorString(e));
+  MM_REQUIRE(dev >= 0 && dev < kMaxDevices, "moe_block_decode_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return mm::set_error(MM_ERR_HIP, "HIP error in hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MM_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t mm_moe_block_decode_noalloc_bytes(int64_t n_tokens, int64_t top_k, int64_t hidden, int64_t inter) {
+  if (n_tokens < 1 || top_k < 0 || hidden < 1 || inter < 1 || n_tokens > kMaxTokens || hidden > (1 << 20) ||
+      inter > (1 << 20))
+    return -1;
+  const int64_t xn = (n_tokens * hidden * 2 + 255) / 256 * 256;
+  return xn + n_tokens * (top_k + 1) * inter * 2;
+}
+
+extern "C" int mm_moe_block_decode_noalloc(const void* x, int64_t n_tokens, int64_t x_row_stride, const void* norm_w,
+                                           float eps, const float* w32, int64_t n_experts, const float* bias,
+                                           int scoring, int n_group, int topk_group, int top_k, float scale,
+                                           const mm_experts* ex, float* logits, void* ids, int ids_dtype, float* wts,
+                                           int add_residual, void* y, int64_t y_row_stride, void* stream) {
+  MM_REQUIRE(ex, "moe_block_decode_noalloc: null expert descriptor");
+  const int64_t need = mm_moe_block_decode_noalloc_bytes(n_tokens, top_k, ex->hidden, ex->inter);
+  MM_REQUIRE(need > 0, "moe_block_decode_noalloc: bad shape (%lld tokens, top_k %d, hidden %lld, inter %lld)",
+             (long long)n_tokens, top_k, (long long)ex->hidden, (long long)ex->inter);
+  MM_REQUIRE(need <= MM_NOALLOC_SCRATCH_BYTES,
+             "moe_block_decode_noalloc: %lld tokens x %d slots at hidden %lld / inter %lld need %lld bytes of "
+             "scratch, above the %d-byte maximum",
+             (long long)n_tokens, top_k + 1, (long long)ex->hidden, (long long)ex->inter, (long long)need,
+             MM_NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  int rc = scratch_on_current_device(&base);
+  if (rc) return rc;
+  char* xn = static_cast<char*>(base);
+  char* a_buf = xn + (n_tokens * ex->hidden * 2 + 255) / 256 * 256;
+  return block_decode("moe_block_decode_noalloc", x, n_tokens, x_row_stride, norm_w, eps, w32, n_experts, bias,
+                      scoring, n_group, topk_group, top_k, scale, ex, logits, ids, ids_dtype, wts, a_buf, xn,
+                      add_residual, y, y_row_stride, stream);
 }
