@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 5
+#define MM_ABI_VERSION 6
 
 /* status codes */
 #define MM_OK 0
@@ -52,6 +52,9 @@ extern "C" {
 #define MM_ACT_NONE 0
 #define MM_ACT_GELU_TANH 1
 #define MM_ACT_SILU 2
+/* ORed into small_linear's act: the norm prologue rounds once, bf16(x * rstd * g), as torch's F.rms_norm does on
+ * the reference's path for more than 16 rows (fastlinear.py:151-160), instead of bf16(bf16(x * rstd) * g). */
+#define MM_NORM_ROUND_ONCE 0x100
 
 /* Stacked expert weights, as the thinker lays them out (engine.py:150-188, 313-391):
  *   w_gu [n_slots, 2*inter, hidden]  rows 0..inter-1 = gate, inter..2*inter-1 = up
@@ -211,7 +214,9 @@ int mm_moe_block_prefill(const void* x, int64_t n_tokens, int64_t x_row_stride, 
  * Replaces fastlinear.small_linear / _small_m_linear (fastlinear.py:123-174) including the rounding
  * points of its epilogue: bf16 before the activation and before the residual add.
  * x, w, b, residual, norm_g, y: bf16. norm_g (optional): RMSNorm prologue with norm_eps,
- * x -> bf16(bf16(x * rstd) * g). b, residual, norm_g may be NULL. act: MM_ACT_*.
+ * x -> bf16(bf16(x * rstd) * g), or bf16(x * rstd * g) with MM_NORM_ROUND_ONCE in act (the rounding of the
+ * reference's torch path for M > 16, which callers run as 16-row pieces). b, residual, norm_g may be NULL.
+ * act: MM_ACT_* (| MM_NORM_ROUND_ONCE).
  * xn_buf: bf16 scratch [M, K], used only when a norm prologue is given and K > 8192 (may be NULL otherwise);
  * shorter rows get the norm fused into the GEMV. x_row_stride 0 repeats one activation row M times. */
 int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_row_stride,

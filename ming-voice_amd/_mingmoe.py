@@ -16,7 +16,8 @@ MM_OK, MM_ERR_ARG, MM_ERR_HIP = 0, 1, 2
 MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
-ABI_VERSION = 5
+MM_NORM_ROUND_ONCE = 0x100
+ABI_VERSION = 6
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}

@@ -22,6 +22,7 @@ struct LinArgs {
   int64_t N, ws;
   const uint16_t* b;
   int act;
+  bool norm_once;  // the norm prologue rounds once, bf16(x * rstd * g) (F.rms_norm), instead of twice
   const uint16_t* res;
   int64_t rs;
   uint16_t* y;
@@ -29,7 +30,7 @@ struct LinArgs {
 };
 
 __global__ __launch_bounds__(256) void small_norm_kernel(const uint16_t* __restrict__ x, int64_t xs, int64_t K,
-                                                         const uint16_t* __restrict__ g, float eps,
+                                                         const uint16_t* __restrict__ g, float eps, bool once,
                                                          uint16_t* __restrict__ xn) {
   __shared__ float red[4];
   const int m = blockIdx.x;
@@ -45,8 +46,8 @@ __global__ __launch_bounds__(256) void small_norm_kernel(const uint16_t* __restr
   const float tot = red[0] + red[1] + red[2] + red[3];
   const float rstd = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
   for (int64_t k = threadIdx.x; k < K; k += 256) {
-    const float v = round_bf16(bf16_to_f32(xr[k]) * rstd);
-    xn[m * K + k] = f32_to_bf16(v * bf16_to_f32(g[k]));
+    const float v = bf16_to_f32(xr[k]) * rstd;
+    xn[m * K + k] = f32_to_bf16((once ? v : round_bf16(v)) * bf16_to_f32(g[k]));
   }
 }
 
@@ -71,14 +72,16 @@ __device__ __forceinline__ void epilogue(const LinArgs& a, int m, int64_t n, flo
   a.y[m * a.ys + n] = f32_to_bf16(v);
 }
 
-// Elementwise bf16(bf16(x * rstd) * g) of one 8-element chunk (the norm prologue's rounding points).
-__device__ __forceinline__ uint4 norm_chunk(uint4 xv, uint4 gv, float rstd) {
+// Elementwise bf16(bf16(x * rstd) * g) of one 8-element chunk (the norm prologue's rounding points), or with
+// `once` bf16(x * rstd * g) (F.rms_norm's single rounding, the reference's path for more than 16 rows).
+__device__ __forceinline__ uint4 norm_chunk(uint4 xv, uint4 gv, float rstd, bool once) {
   const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
   uint32_t r[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float y0 = round_bf16(__uint_as_float(xw[i] << 16) * rstd) * __uint_as_float(gw[i] << 16);
-    const float y1 = round_bf16(__uint_as_float(xw[i] & 0xffff0000u) * rstd) * __uint_as_float(gw[i] & 0xffff0000u);
+    const float x0 = __uint_as_float(xw[i] << 16) * rstd, x1 = __uint_as_float(xw[i] & 0xffff0000u) * rstd;
+    const float y0 = (once ? x0 : round_bf16(x0)) * __uint_as_float(gw[i] << 16);
+    const float y1 = (once ? x1 : round_bf16(x1)) * __uint_as_float(gw[i] & 0xffff0000u);
     r[i] = static_cast<uint32_t>(f32_to_bf16(y0)) | (static_cast<uint32_t>(f32_to_bf16(y1)) << 16);
   }
   return make_uint4(r[0], r[1], r[2], r[3]);
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
         for (int j = 0; j < NC; ++j) ss += cin[j] ? sumsq8(xv[j]) : 0.f;
         const float rstd = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.K) + norm_eps);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) lx[(mm * NC + j) * kWave + lane] = norm_chunk(xv[j], gv[j], rstd);
+        for (int j = 0; j < NC; ++j) lx[(mm * NC + j) * kWave + lane] = norm_chunk(xv[j], gv[j], rstd, a.norm_once);
       }
       __syncthreads();
 #pragma unroll
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
           for (int j = 0; j < NC; ++j) ss += cin[j] ? sumsq8(xv[j]) : 0.f;
           const float rstd = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(a.K) + norm_eps);
 #pragma unroll
-          for (int j = 0; j < NC; ++j) xv[j] = norm_chunk(xv[j], gv[j], rstd);
+          for (int j = 0; j < NC; ++j) xv[j] = norm_chunk(xv[j], gv[j], rstd, a.norm_once);
         }
 #pragma unroll
         for (int i = 0; i < R; ++i) {
@@ -328,6 +331,8 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
              (long long)K, (long long)N);
   MM_REQUIRE(N <= 0x7fffffffLL * 8, "small_linear: N too large");
   MM_REQUIRE(x && w && y, "small_linear: null pointer");
+  const bool once = (act & MM_NORM_ROUND_ONCE) != 0;
+  act &= ~MM_NORM_ROUND_ONCE;
   MM_REQUIRE(act == MM_ACT_NONE || act == MM_ACT_GELU_TANH || act == MM_ACT_SILU, "small_linear: unknown act %d", act);
   MM_REQUIRE((x_row_stride >= K || x_row_stride == 0) && w_row_stride >= K && y_row_stride >= N,
              "small_linear: row stride too small (x rows may also repeat one row, stride 0)");
@@ -341,7 +346,7 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
     MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0, "small_linear: x rows must be 16-byte aligned");
     MM_REQUIRE(!norm_g || mm::aligned16(norm_g), "small_linear: norm_g must be 16-byte aligned");
     LinArgs a{xin, xs, static_cast<int>(M), K, static_cast<const uint16_t*>(w), N, w_row_stride,
-              static_cast<const uint16_t*>(b), act, static_cast<const uint16_t*>(residual), res_row_stride,
+              static_cast<const uint16_t*>(b), act, once, static_cast<const uint16_t*>(residual), res_row_stride,
               static_cast<uint16_t*>(y), y_row_stride};
     auto g = static_cast<const uint16_t*>(norm_g);
     // chunks per lane NC = ceil(nch / 64), rounded up to an instantiated size; at most 16 loads per lane
@@ -356,7 +361,7 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
   if (norm_g) {
     MM_REQUIRE(xn_buf && mm::aligned16(xn_buf), "small_linear: norm prologue needs a 16-byte aligned xn_buf [M, K]");
     hipLaunchKernelGGL(small_norm_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, st, xin, xs, K,
-                       static_cast<const uint16_t*>(norm_g), norm_eps, static_cast<uint16_t*>(xn_buf));
+                       static_cast<const uint16_t*>(norm_g), norm_eps, once, static_cast<uint16_t*>(xn_buf));
     int rc = mm::check_launch("small_linear norm");
     if (rc) return rc;
     xin = static_cast<const uint16_t*>(xn_buf);
@@ -365,7 +370,7 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
     MM_REQUIRE(mm::aligned16(x) && (x_row_stride * 2) % 16 == 0, "small_linear: x rows must be 16-byte aligned");
   }
   LinArgs a{xin, xs, static_cast<int>(M), K, static_cast<const uint16_t*>(w), N, w_row_stride,
-            static_cast<const uint16_t*>(b), act, static_cast<const uint16_t*>(residual), res_row_stride,
+            static_cast<const uint16_t*>(b), act, false, static_cast<const uint16_t*>(residual), res_row_stride,
             static_cast<uint16_t*>(y), y_row_stride};
   return launch<64, 4>(a, st);  // several passes of 256 chunks per row
 }
@@ -392,7 +397,7 @@ extern "C" int mm_small_linear_glu(const void* x, int64_t M, int64_t K, int64_t 
              "small_linear_glu: x and weight rows must be 16-byte aligned");
   MM_REQUIRE(!norm_g || mm::aligned16(norm_g), "small_linear_glu: norm_g must be 16-byte aligned");
   LinArgs a{static_cast<const uint16_t*>(x), x_row_stride, static_cast<int>(M), K, static_cast<const uint16_t*>(w),
-            inter, w_row_stride, nullptr, MM_ACT_NONE, nullptr, 0, static_cast<uint16_t*>(y), y_row_stride};
+            inter, w_row_stride, nullptr, MM_ACT_NONE, false, nullptr, 0, static_cast<uint16_t*>(y), y_row_stride};
   auto g = static_cast<const uint16_t*>(norm_g);
   hipStream_t st = MM_STREAM(stream);
   const int64_t nch = K / 8;

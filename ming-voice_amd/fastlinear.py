@@ -3,8 +3,10 @@ y = act(norm?(x) @ W^T + b) + residual, bandwidth-bound GEMV for decode-sized ac
 
 The reference tunes Triton block configs per shape and caches them in CACHE_FILE; the HIP kernel picks
 its launch shape from (M, K) alone, so nothing is tuned: `_best` stays empty, `save_cache()` has nothing
-to write, and shapes never need tuning before graph capture. Rows beyond 16 run as 16-row pieces of the
-same kernel, so every M has the same rounding points.
+to write, and shapes never need tuning before graph capture. More than 16 rows run as 16-row pieces of the
+same kernel with the rounding points of the reference's torch path for that case (fastlinear.py:151-160):
+the same as the kernel's except the RMSNorm prologue, which F.rms_norm rounds once, bf16(x * rstd * g),
+where the Triton kernel rounds twice, bf16(bf16(x * rstd) * g).
 """
 import json
 import os
@@ -100,6 +102,8 @@ def small_linear(x, w, b=None, act=0, residual=None, out=None, norm=None):
     y = torch.empty(M, N, device=x.device, dtype=x.dtype) if out is None else out.reshape(M, N)
     # the library fuses the norm into the GEMV for K <= 8192 and needs the scratch row only beyond that
     xn = torch.empty(min(M, MAX_M), K, device=x.device, dtype=torch.bfloat16) if norm is not None and K > 8192 else None
+    if M > MAX_M and norm is not None:
+        act = int(act) | _mm.MM_NORM_ROUND_ONCE  # F.rms_norm's single rounding (fastlinear.py:151-153)
     lib = _mm.load()
     with _mm.on_device(x):
         for m0 in range(0, M, MAX_M):

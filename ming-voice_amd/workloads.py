@@ -12,6 +12,8 @@ one device and copies.
   ragged_bias(...)      router bias ~ N(0, 0.5): ragged per-expert token counts (512-token prefill)
   zipf_bias(...)        router bias log p_e, p_e ~ rank^-1.2 under a fixed permutation (2048-token prefill)
   moe_block_forward     RMSNorm -> router -> MoE (+ residual) through the HIP kernels
+  thinker_layer(...)    one synthetic thinker layer (q|k|v and o projections + MoE block)
+  ThinkerDecodeStep     the synthetic 28-layer thinker decode step + LM head (one token)
   TalkerLLM(...)        a synthetic Qwen2 Talker LLM with StaticQwen2's attributes and KV cache layout
   TalkerTail(...)       a synthetic Talker (DiT + aggregator + stop head) with the attributes FastTail reads
 """
@@ -104,6 +106,96 @@ def flops_per_pair(hidden=HIDDEN, inter=INTER):
 
 def nb_blocks(P, E1, BM=64):
     return math.ceil((P + E1 * (BM - 1)) / BM)
+
+
+# ------------------------------------------------------------------------------ thinker decode step
+
+ATTN_Q, ATTN_KV = 2048, 256  # q and o are 2048 x 2048; k and v 256 x 2048
+
+
+def thinker_layer(li, device="cpu", seed=1000, proj=True, int8=False, scale_dtype=torch.bfloat16):
+    """Weights of thinker layer li: RMSNorm ln1 (seed s = seed + 16 li), the q | k | v rows stacked into one
+    [2048 + 256 + 256, 2048] matrix (seeds s+1..s+3, one GEMV), o (s+4) and one MoE block (seeds s+5..s+8).
+    proj False leaves the projections out; int8 replaces the block's experts by int8 + row scales."""
+    s = seed + 16 * li
+    p = {"blk": block(seed=s + 5, device=device)}
+    if int8:
+        quantize_block(p["blk"], scale_dtype)
+        del p["blk"]["w_gu"], p["blk"]["w_d"]
+    if proj:
+        q = normal((ATTN_Q, HIDDEN), 0.02, s + 1, device)
+        k = normal((ATTN_KV, HIDDEN), 0.02, s + 2, device)
+        v = normal((ATTN_KV, HIDDEN), 0.02, s + 3, device)
+        p["ln1"] = normal((HIDDEN,), 0.02, s, device, mean=1.0)
+        p["qkv"] = torch.cat([q, k, v])
+        p["o"] = normal((HIDDEN, ATTN_Q), 0.02, s + 4, device)
+    return p
+
+
+class ThinkerDecodeStep:
+    """The synthetic thinker decode step of one token on the HIP kernels:
+    `layers` x (RMSNorm fused into the q | k | v GEMV -> o projection + residual -> MoE block with its RMSNorm,
+    softmax top-6 + shared expert, + residual) -> final RMSNorm fused into the LM head [vocab, 2048].
+    The attention itself (the KDA / MLA mixers of the real thinker) is not part of this step: the o projection
+    reads the q rows of the projection output. Weights ~ N(0, 0.02) bf16 (norm weights 1 + N(0, 0.02)), seeds
+    as thinker_layer; final norm seed 999, head 998, input token x0 ~ N(0, 1) seed 997. The router outputs
+    and the gated activations share one set of buffers across layers. Calling the object runs the step and
+    returns the logits [1, vocab]; x0 may be overwritten in place between calls (a captured graph reads it)."""
+
+    def __init__(self, layers=28, device="cuda", vocab=VOCAB, seed=1000):
+        self.L = [thinker_layer(li, device, seed) for li in range(layers)]
+        self.final_norm = normal((HIDDEN,), 0.02, 999, device, mean=1.0)
+        self.head = normal((vocab, HIDDEN), 0.02, 998, device)
+        self.x0 = tokens(1, seed=997, device=device)
+        self.logits = torch.empty(1, EXPERTS, device=device)
+        self.ids = torch.empty(1, TOP_K + 1, device=device, dtype=torch.long)
+        self.wts = torch.empty(1, TOP_K + 1, device=device)
+        self.a_buf = torch.empty(TOP_K + 1, INTER, device=device, dtype=torch.bfloat16)
+
+    def layer(self, p, h):
+        from fastlinear import small_linear
+        from fused_moe import moe_block_decode
+        qkv = small_linear(h, p["qkv"], norm=(p["ln1"], EPS))
+        h = small_linear(qkv[:, :HIDDEN], p["o"], residual=h)
+        b = p["blk"]
+        return moe_block_decode(h, b["norm_w"], EPS, b["w32"], b["w_gu"], b["w_d"], top_k=TOP_K, logits=self.logits,
+                                ids=self.ids, wts=self.wts, a_buf=self.a_buf)[0]
+
+    def __call__(self):
+        from fastlinear import small_linear
+        h = self.x0
+        for p in self.L:
+            h = self.layer(p, h)
+        return small_linear(h, self.head, norm=(self.final_norm, EPS))
+
+    def trace(self):
+        """The same step run eagerly, keeping each layer's input and router picks:
+        ([(h_in, ids, wts)] per layer, the last layer's output, logits)."""
+        from fastlinear import small_linear
+        h, out = self.x0, []
+        for p in self.L:
+            h_in = h.clone()
+            h = self.layer(p, h)
+            out.append((h_in, self.ids.clone(), self.wts.clone()))
+        return out, h, small_linear(h, self.head, norm=(self.final_norm, EPS))
+
+    def moe_only(self):
+        """The MoE blocks alone, chained, every layer's experts distinct memory."""
+        from fused_moe import moe_block_decode
+        h = self.x0
+        for p in self.L:
+            b = p["blk"]
+            h = moe_block_decode(h, b["norm_w"], EPS, b["w32"], b["w_gu"], b["w_d"], top_k=TOP_K, logits=self.logits,
+                                 ids=self.ids, wts=self.wts, a_buf=self.a_buf)[0]
+        return h
+
+    def bytes_per_step(self):
+        """HBM bytes one step must read: projections, 7 experts and the router of every layer, the LM head."""
+        n = len(self.L)
+        proj = n * ((ATTN_Q + 2 * ATTN_KV) * HIDDEN + HIDDEN * ATTN_Q) * 2
+        moe = n * (TOP_K + 1) * expert_bytes()
+        router = n * EXPERTS * HIDDEN * 4
+        return proj + moe + router + self.head.numel() * 2
 
 
 # ------------------------------------------------------------------------------------------- Talker LLM

@@ -203,10 +203,13 @@ def moe_int8_fallback(x, q_gu, q_d, s_gu, s_d, ids, weights):
 # -------------------------------------------------------------------------------------------- small linear
 
 def small_linear(x, w, b=None, act=0, residual=None, norm=None):
-    """fastlinear.py:123-165 for M <= 16: optional RMSNorm prologue (rstd = 1/sqrt(ss/K + eps);
+    """fastlinear.py:123-165 for M <= 16 rows: optional RMSNorm prologue (rstd = 1/sqrt(ss/K + eps);
     x -> bf16(bf16(x * rstd) * g)), acc = x . W^T (fp32), + b, act with a bf16 rounding first
-    (1 = GELU tanh, 2 = SiLU), residual after a bf16 rounding, cast to x.dtype."""
+    (1 = GELU tanh, 2 = SiLU), residual after a bf16 rounding, cast to x.dtype.
+    More than 16 rows take the reference's torch path instead (small_linear_torch)."""
     K = x.shape[-1]
+    if x.reshape(-1, K).shape[0] > 16:
+        return small_linear_torch(x, w, b, act, residual, norm)
     xf = x.float().reshape(-1, K)
     if norm is not None:
         g, eps = norm
@@ -226,3 +229,30 @@ def small_linear(x, w, b=None, act=0, residual=None, norm=None):
     if residual is not None:
         acc = _bf(acc) + residual.float().reshape(acc.shape)
     return acc.to(x.dtype).reshape(*x.shape[:-1], w.shape[0])
+
+
+def small_linear_torch(x, w, b=None, act=0, residual=None, norm=None):
+    """fastlinear.py:151-160, the reference's path for M > 16 rows, as torch computes it on x.dtype tensors:
+    F.rms_norm (x * rsqrt(mean(x^2) + eps) * w in fp32, rounded once), F.linear (fp32 accumulation, + b, one
+    rounding), F.gelu(approximate="tanh") / F.silu on the rounded output (fp32 inside, rounded), then
+    + residual (rounded). Each rounding is to x.dtype. Only the norm differs from the M <= 16 formula, which
+    rounds x * rstd before the weight."""
+    F = torch.nn.functional
+    dt = x.dtype
+    K = x.shape[-1]
+    xf = x.float().reshape(-1, K)
+    if norm is not None:
+        g, eps = norm
+        xf = (xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps) * g.float()).to(dt).float()
+    acc = xf @ w.float().t()
+    if b is not None:
+        acc = acc + b.float()
+    y = acc.to(dt).float()
+    if act == 1:
+        y = F.gelu(y, approximate="tanh").to(dt).float()
+    elif act == 2:
+        y = F.silu(y).to(dt).float()
+    y = y.reshape(*x.shape[:-1], w.shape[0])
+    if residual is not None:
+        y = y + residual.float()
+    return y.to(dt)

@@ -405,14 +405,46 @@ def test_moe_block_forward(blk):
         close(y, _oracle_moe(cpu, xn, ids, wts, residual=x.cpu()))
 
 
+# ------------------------------------------------------------- the reference's torch int8 path (engine.py)
+
+@pytest.fixture(scope="module")
+def fallback_weights(blk):
+    """The int8 experts dequantised as the reference's unfused int8 prefill does it (engine.py:478-479:
+    (q.half() * s.half()).to(bf16)), once, on the CPU."""
+    _, cpu = blk
+    d_gu = (cpu["q_gu"].half() * cpu["s_gu"][:, :, None].half()).to(BF)
+    d_d = (cpu["q_d"].half() * cpu["s_d"][:, :, None].half()).to(BF)
+    return d_gu, d_d
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 100, 512])
+def test_int8_matches_the_reference_torch_int8_path(blk, fallback_weights, n):
+    """int8 decode (1..8 tokens: the decode kernels) and int8 prefill (100, 512 tokens: align + grouped MFMA)
+    against the reference's own torch int8 path (engine.py:455-486, restated by O.moe_int8_fallback): experts
+    dequantised with fp16 rounding, per-expert bf16 products, fp32 sum over slots. The HIP kernels apply the
+    row scale to the fp32 accumulator instead, so the two differ by weight rounding only (bf16 tolerance)."""
+    b, cpu = blk
+    x = W.tokens(n, seed=160 + n, device=DEV)
+    xn, ids, wts = _route_tokens(b, x, W.ragged_bias(device=DEV) if n == 512 else None)
+    y = fused_moe.fused_moe_prefill(xn, b["q_gu"], b["q_d"], ids, wts, s_gu=b["s_gu"], s_d=b["s_d"])
+    d_gu, d_d = fallback_weights
+    ref = O.moe(xn.cpu(), d_gu, d_d, ids.cpu(), wts.cpu())  # = O.moe_int8_fallback, dequantised once
+    close(y, ref)
+    if n == 100:
+        torch.testing.assert_close(ref, O.moe_int8_fallback(xn.cpu(), cpu["q_gu"], cpu["q_d"], cpu["s_gu"], cpu["s_d"],
+                                                            ids.cpu(), wts.cpu()), rtol=0, atol=0)
+
+
 # -------------------------------------------------------------------------------------------- small linear
 
-@pytest.mark.parametrize("M", [1, 2, 6, 16, 20])
+@pytest.mark.parametrize("M", [1, 2, 6, 16, 20, 64])
 @pytest.mark.parametrize("KN", [(2048, 2048), (2048, 256), (896, 1152), (4864, 896), (256, 77), (1024, 130),
                                 (6144, 64), (8192, 33), (9216, 40)])
 def test_small_linear(M, KN):
     """Every launch shape: one pass per row with 16 / 32 / 64 lanes per row and 4..16 chunks per lane (K up to
-    8192, norm fused), and the multi-pass kernel with its separate norm kernel (K = 9216)."""
+    8192, norm fused), and the multi-pass kernel with its separate norm kernel (K = 9216). More than 16 rows
+    (20, 64) are checked against the reference's torch path for that case (fastlinear.py:151-160: the norm
+    rounded once), the others against its Triton kernel's rounding."""
     K, N = KN
     x = W.normal((M, K), 1.0, 100 + M, DEV)
     w = W.normal((N, K), 0.02, 101, DEV)

@@ -319,3 +319,51 @@ def test_small_linear_norm_prologue_matches_library():
     got = O.small_linear(x, w, norm=(gam, 1e-6))
     ref = F.linear(F.rms_norm(x.float(), (512,), gam.float(), 1e-6), w.float())
     _close(got, ref)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_small_linear_torch_branch_equals_bf16_library_ops(act):
+    """More than 16 rows follow the reference's torch path (fastlinear.py:151-160). Torch's own bf16 CPU ops
+    (F.rms_norm, F.linear, F.gelu / F.silu and the residual add on bf16 tensors) round where the branch says;
+    they may differ in the GEMM's summation order, i.e. by an output ulp here and there."""
+    g = torch.Generator().manual_seed(10)
+    M, K, N = 40, 512, 96
+    x = (torch.randn(M, K, generator=g) * 2).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(BF)
+    b = torch.randn(N, generator=g).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF)
+    gam = (1 + 0.1 * torch.randn(K, generator=g)).to(BF)
+    got = O.small_linear(x, w, b, act, r, norm=(gam, 1e-6))
+    y = F.linear(F.rms_norm(x, (K,), gam, 1e-6), w, b)
+    y = {0: y, 1: F.gelu(y, approximate="tanh"), 2: F.silu(y)}[act] + r
+    assert got.dtype == BF and got.shape == (M, N)
+    diff = (got.float() - y.float()).abs()
+    ulp = y.float().abs().clamp_min(2 ** -6) * 2 ** -7  # one or two bf16 ulps
+    assert (diff <= ulp).float().mean() > 0.97 and (diff <= 4 * ulp).all()
+
+
+def test_small_linear_torch_branch_agrees_with_the_kernel_formula():
+    """Both branches round at the same points after the GEMM (bf16 before the activation and before the
+    residual); the norm rounds once on the torch branch and twice in the kernel formula, an ulp of the
+    normalised row at most. So 20 rows through the torch branch equal 16 + 4 rows through the M <= 16 formula
+    within the bf16 tolerance, most outputs within an ulp; a planted mistake (the residual added before the activation) is caught, and the
+    branch's norm is the single-rounded one (bit-equal to F.rms_norm on bf16, unlike the two-step form)."""
+    g = torch.Generator().manual_seed(11)
+    M, K, N = 20, 256, 64
+    x = torch.randn(M, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(BF)
+    b = torch.randn(N, generator=g).to(BF)
+    r = torch.randn(M, N, generator=g).to(BF)
+    gam = (1 + 0.1 * torch.randn(K, generator=g)).to(BF)
+    for act in (0, 1, 2):  # no residual here: one that cancels the output would magnify a one-ulp difference
+        whole = O.small_linear(x, w, b, act, norm=(gam, 1e-6))
+        parts = torch.cat([O.small_linear(x[:16], w, b, act, norm=(gam, 1e-6)),
+                           O.small_linear(x[16:], w, b, act, norm=(gam, 1e-6))])
+        _close(whole, parts, rtol=2e-2, atol=1e-2)
+        d = (whole.float() - parts.float()).abs()
+        assert (d <= parts.float().abs().clamp_min(2 ** -6) * 2 ** -7).float().mean() > 0.8
+    planted = F.gelu(O.small_linear(x, w, b, 0, r, norm=(gam, 1e-6)).float(), approximate="tanh")
+    assert not torch.allclose(planted, O.small_linear(x, w, b, 1, r, norm=(gam, 1e-6)).float(), rtol=2e-2, atol=1e-2)
+    xn1 = O.small_linear(x, torch.eye(K).to(BF), norm=(gam, 1e-6))  # 20 rows: the torch branch's norm, exactly
+    assert torch.equal(xn1, F.rms_norm(x, (K,), gam, 1e-6))
+    assert not torch.equal(O.small_linear(x[:16], torch.eye(K).to(BF), norm=(gam, 1e-6)), xn1[:16])
