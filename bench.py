@@ -7,13 +7,14 @@ shared expert, softmax top-6, router bias ~ N(0, 0.5) for ragged expert loads). 
 block on inputs already resident in HBM: RMSNorm -> router -> align -> grouped gate/up -> down ->
 combine + residual, replayed from one hipGraph. `value` is tokens/s over exactly K timed steps.
 
-Also measured and reported under "extra": decode of 1 token (bf16) as a hipGraph step and per kernel,
-int8 decode at batch 1/2/4/8, the 2048-token Zipf prefill, and the full 28-layer synthetic decode step
-(+ LM head) in one hipGraph, and the Talker path (a 24-layer Qwen2-0.5B-shaped LLM decode step and its
-rotary / decode attention and silu_mul kernels), and the ingestion of one MoE layer's experts from
-safetensors shards into the stacked bf16 / int8 layout. The roofline of the dominant kernel (prefill gate/up) is its algorithmic
-bytes over its average duration from HIP events on its own stream; the CPU baseline is the oracle's
-torch path on a bounded sample of the same workload on this host.
+Also measured and reported under "extra": the 2048-token Zipf prefill; the full 28-layer synthetic decode
+step (+ LM head) in one hipGraph; decode of 1 token (bf16) and int8 decode at batch 1/2/4/8 through 28
+distinct layers (cold: every layer's experts read from HBM), per layer and per kernel; the Talker path (a
+24-layer Qwen2-0.5B-shaped LLM decode step and its rotary / decode attention and silu_mul kernels); and the
+ingestion of one MoE layer's experts from safetensors shards into the stacked bf16 / int8 layout. The
+roofline of the dominant kernel (prefill gate/up) is its algorithmic bytes over its average duration from HIP
+events on its own stream; the CPU baseline is the reference's torch path (the per-expert bf16 loop) on all
+512 tokens of the headline workload on this host.
 """
 import argparse
 import csv
@@ -221,117 +222,102 @@ def pmc_traffic(timeout=90):
 
 # ------------------------------------------------------------------------------------------------ decode
 
-def decode_metrics(b, n, stream, int8=False, seed=40):
+def median_graph_ms(g, stream, reps=20, runs=5):
+    return sorted(time_graph(g, stream, reps) for _ in range(runs))[runs // 2]
+
+
+def decode_metrics(blocks, n, stream, int8=False, seed=40):
+    """Decode of n tokens through len(blocks) distinct MoE blocks chained (layer l's output is layer l+1's
+    input), every block's experts in memory of their own: the 28 layers' active experts (28 x 121 MB in bf16,
+    28 x 61 MB in int8 for one token) far exceed the 256 MB last-level cache, so every expert byte of a layer
+    comes from HBM, as in a real forward pass. Per layer (graph replays, median of 5 timings): the fused
+    block (moe_block_decode: router + norm, selection, gate/up, down + combine), the unfused chain
+    (rms_norm -> moe_route -> fused_moe_decode), and each MoE kernel alone (its launches over the 28 layers
+    in one graph, on the inputs the chain gave each layer). Bytes: each layer's realised distinct experts."""
     import fused_moe
     import fused_ops
     import _mingmoe
     import workloads as W
-    x = W.tokens(n, seed=seed + n, device="cuda")
-    w_gu, w_d = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
-    sgu, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
-    E = b["w32"].shape[0]
-    logits = torch.empty(n, E, device="cuda")
-    ids = torch.empty(n, W.TOP_K + 1, device="cuda", dtype=torch.long)
-    wts = torch.empty(n, W.TOP_K + 1, device="cuda")
-    a_buf = torch.empty(n * (W.TOP_K + 1), W.INTER, device="cuda", dtype=torch.bfloat16)
-    out = torch.empty(n, W.HIDDEN, device="cuda", dtype=torch.bfloat16)
-    st = {}
+    L, dev = len(blocks), "cuda"
+    H, I, E, NK = W.HIDDEN, W.INTER, W.EXPERTS, W.TOP_K + 1
+    x0 = W.tokens(n, seed=seed + n, device=dev)
 
-    def step():
-        xn = st["xn"] = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
-        fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, ids, wts, scoring="softmax")
-        fused_moe.fused_moe_decode(xn, w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu, s_d=sd, residual=x)
+    def experts(b):
+        return (b["q_gu"], b["q_d"], b["s_gu"], b["s_d"]) if int8 else (b["w_gu"], b["w_d"], None, None)
 
-    g = graph_of(step, stream)
-    ms_unfused = time_graph(g, stream, 200)
+    logits = torch.empty(n, E, device=dev)
+    ids = torch.empty(n, NK, device=dev, dtype=torch.long)
+    wts = torch.empty(n, NK, device=dev)
+    a_buf = torch.empty(n * NK, I, device=dev, dtype=torch.bfloat16)
 
-    def fused_step():
-        fused_moe.moe_block_decode(x, b["norm_w"], W.EPS, b["w32"], w_gu, w_d, top_k=W.TOP_K, s_gu=sgu, s_d=sd,
-                                   logits=logits, ids=ids, wts=wts, a_buf=a_buf, out=out)
+    def fused():
+        h = x0
+        for b in blocks:
+            wg, wd, sg, sd = experts(b)
+            h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=W.TOP_K, s_gu=sg, s_d=sd,
+                                           logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
+        return h
 
-    gf = graph_of(fused_step, stream)
-    ms = time_graph(gf, stream, 200)
+    def unfused():
+        h = x0
+        for b in blocks:
+            wg, wd, sg, sd = experts(b)
+            xn = fused_ops.rms_norm(h, b["norm_w"], W.EPS)
+            fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, ids, wts, scoring="softmax")
+            h = fused_moe.fused_moe_decode(xn, wg, wd, ids, wts, a_buf=a_buf, s_gu=sg, s_d=sd, residual=h)
+        return h
+
+    ms = median_graph_ms(graph_of(fused, stream), stream) / L
+    ms_unfused = median_graph_ms(graph_of(unfused, stream), stream) / L
+    # each layer's kernel inputs, from one eager pass of the unfused chain
+    per = []
+    h = x0
+    for b in blocks:
+        xn = fused_ops.rms_norm(h, b["norm_w"], W.EPS)
+        li, lw = torch.empty_like(ids), torch.empty_like(wts)
+        fused_ops.moe_route(xn, b["w32"], None, 1, 1, W.TOP_K, 1.0, logits, li, lw, scoring="softmax")
+        per.append({"xn": xn, "ids": li, "wts": lw, "res": h, "a": torch.empty_like(a_buf),
+                    "out": torch.empty(n, H, device=dev, dtype=torch.bfloat16)})
+        wg, wd, sg, sd = experts(b)
+        h = fused_moe.fused_moe_decode(xn, wg, wd, li, lw, s_gu=sg, s_d=sd, residual=h)
 
     def phase(p):
-        return lambda: fused_moe.fused_moe_decode(st["xn"], w_gu, w_d, ids, wts, a_buf=a_buf, out=out, s_gu=sgu,
-                                                  s_d=sd, residual=x, phases=p)
-    gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream, 50)
-    dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream, 50)
-    uniq = int(torch.unique(ids).numel())
-    H, I = W.HIDDEN, W.INTER
-    es = 1 if int8 else 2
-    sb = 2 if int8 else 0
+        def run():
+            for b, q in zip(blocks, per):
+                wg, wd, sg, sd = experts(b)
+                fused_moe.fused_moe_decode(q["xn"], wg, wd, q["ids"], q["wts"], a_buf=q["a"], out=q["out"], s_gu=sg,
+                                           s_d=sd, residual=q["res"], phases=p)
+        return run
+    gu_ms = median_graph_ms(graph_of(phase(_mingmoe.MM_PHASE_GATE_UP), stream), stream) / L
+    dn_ms = median_graph_ms(graph_of(phase(_mingmoe.MM_PHASE_DOWN), stream), stream) / L
+    uniq = sum(int(torch.unique(q["ids"]).numel()) for q in per) / L  # distinct experts per layer
+    es, sb = (1, 2) if int8 else (2, 0)
     gu_bytes = uniq * (2 * I * H * es + 2 * I * sb)
     dn_bytes = uniq * (H * I * es + H * sb)
+    moe_bytes = gu_bytes + dn_bytes
     return {
-        "tokens": n, "int8": int8, "unique_experts": uniq, "us_per_step": ms * 1e3, "us_per_token": ms * 1e3 / n,
-        "us_per_step_unfused": ms_unfused * 1e3,
-        "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3,
+        "tokens": n, "int8": int8, "layers": L, "cold": True, "unique_experts_per_layer": uniq,
+        "us_per_layer": ms * 1e3, "us_per_token_per_layer": ms * 1e3 / n, "us_per_layer_unfused": ms_unfused * 1e3,
+        "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3, "moe_bytes_per_layer": moe_bytes,
         "gate_up_TBs": gu_bytes / gu_ms / 1e9, "down_TBs": dn_bytes / dn_ms / 1e9,
-        "moe_TBs": (gu_bytes + dn_bytes) / (gu_ms + dn_ms) / 1e9,
-        "layer_TBs": (gu_bytes + dn_bytes) / ms / 1e9,
-        "moe_hbm_pct": (gu_bytes + dn_bytes) / ((gu_ms + dn_ms) * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+        "moe_TBs": moe_bytes / (gu_ms + dn_ms) / 1e9, "layer_TBs": moe_bytes / ms / 1e9,
+        "moe_hbm_pct": moe_bytes / ((gu_ms + dn_ms) * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+        "layer_hbm_pct": moe_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
     }
 
 
 # ------------------------------------------------------------------------------------- full decode step
 
-def full_decode_metrics(stream, layers=28):
-    """28 x (RMSNorm -> q/k/v/o projections -> RMSNorm -> MoE block) -> RMSNorm -> LM head, batch 1 (the first
-    RMSNorm runs inside the q|k|v GEMV, whose rows are the q, k and v weights stacked); and the
-    28 MoE blocks alone (median of 5 timings): the decode MoE layer with every layer's experts read from
-    HBM, as in a real forward pass (the single-layer decode figures can hit the 256 MB last-level cache)."""
-    import fastlinear
-    import fused_moe
+def full_decode_metrics(step, stream):
+    """The synthetic thinker decode step (workloads.ThinkerDecodeStep: 28 x (RMSNorm fused into the q|k|v GEMV
+    -> o projection + residual -> MoE block) -> final RMSNorm + LM head 2048 -> 126464, batch 1) in one
+    hipGraph, and its 28 MoE blocks alone (median of 5 timings), every layer's experts distinct memory."""
     import workloads as W
-    H, dev = W.HIDDEN, "cuda"
-    L = []
-    for li in range(layers):
-        s = 1000 + 16 * li
-        q, k, v = W.normal((H, H), 0.02, s + 1, dev), W.normal((256, H), 0.02, s + 2, dev), W.normal((256, H), 0.02, s + 3, dev)
-        L.append({
-            "ln1": W.normal((H,), 0.02, s, dev, mean=1.0), "qkv": torch.cat([q, k, v]),  # q|k|v rows, one GEMV
-            "o": W.normal((H, H), 0.02, s + 4, dev), "blk": W.block(seed=s + 5, device=dev),
-        })
-        del q, k, v
-    fn = W.normal((H,), 0.02, 999, dev, mean=1.0)
-    head = W.normal((W.VOCAB, H), 0.02, 998, dev)
-    x0 = W.tokens(1, seed=997, device=dev)
-    E = W.EXPERTS
-    logits = torch.empty(1, E, device=dev)
-    ids = torch.empty(1, W.TOP_K + 1, device=dev, dtype=torch.long)
-    wts = torch.empty(1, W.TOP_K + 1, device=dev)
-    a_buf = torch.empty(W.TOP_K + 1, W.INTER, device=dev, dtype=torch.bfloat16)
-
-    def step():
-        h = x0
-        for p in L:
-            qkv = fastlinear.small_linear(h, p["qkv"], norm=(p["ln1"], W.EPS))  # RMSNorm fused into q|k|v
-            h = fastlinear.small_linear(qkv[:, :H], p["o"], residual=h)  # attention itself is outside the MoE path
-            b = p["blk"]
-            h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
-                                           logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
-        return fastlinear.small_linear(h, head, norm=(fn, W.EPS))
-
-    g = graph_of(step, stream)
-    ms = time_graph(g, stream, 20)
-
-    def moe_only():  # the 28 MoE blocks alone, distinct weights per layer (no reuse from the last-level cache)
-        h = x0
-        for p in L:
-            b = p["blk"]
-            h = fused_moe.moe_block_decode(h, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
-                                           logits=logits, ids=ids, wts=wts, a_buf=a_buf)[0]
-        return h
-
-    gm = graph_of(moe_only, stream)
-    moe_ms = sorted(time_graph(gm, stream, 20) for _ in range(5))[2]
-    proj = 28 * (2 * H * H + 2 * 256 * H) * 2
-    moe = 28 * 7 * W.expert_bytes()
-    router = 28 * E * H * 4
-    total = proj + moe + router + W.VOCAB * H * 2
-    moe_layer_bytes = 7 * W.expert_bytes() + E * H * 4
-    del L, head
+    layers = len(step.L)
+    ms = median_graph_ms(graph_of(step, stream), stream)
+    moe_ms = median_graph_ms(graph_of(step.moe_only, stream), stream)
+    total = step.bytes_per_step()
+    moe_layer_bytes = (W.TOP_K + 1) * W.expert_bytes() + W.EXPERTS * W.HIDDEN * 4
     return {"layers": layers, "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
             "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
             "moe_us_per_layer": moe_ms * 1e3 / layers, "moe_layer_bytes": moe_layer_bytes,
@@ -403,8 +389,7 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=4, ref_threads
     link's practical ceiling)."""
     import fused_moe
     import expert_load as EL
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from ckpt_util import expert_tensors, write_checkpoint
+    from workloads import expert_tensors, write_checkpoint
     from concurrent.futures import ThreadPoolExecutor
     dev = torch.device("cuda")
     pfx = "model.layers.1.mlp"
@@ -482,30 +467,48 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=4, ref_threads
 
 # -------------------------------------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(b, bias, n_sample=64, reps=2):
-    """The oracle's torch CPU path (RMSNorm, router, per-expert MoE loop, combine) on the first n_sample
-    tokens of the 512-token workload; returns tokens/s and the threads used."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(b, bias, n=512, warmup=2, reps=7):
+    """The reference's CPU torch path for the headline block on all n tokens of the same seeded input: RMSNorm
+    and the fp32 router (O.rms_norm, O.router_logits, O.router_select), the per-expert bf16 loop of
+    dev/test_moe_prefill.py:24-38 (O.moe_reference_loop: one GEMM pair per active expert, index_add in fp32),
+    the residual add. torch's intra-op threads (the box's CPU share); median of `reps` runs after `warmup`."""
     from oracle import moe_oracle as O
     import workloads as W
     cpu = {k: b[k].cpu() for k in ("norm_w", "w32", "w_gu", "w_d")}
-    x = W.tokens(512, seed=70, device="cuda")[:n_sample].cpu()
+    x = W.tokens(n, seed=70, device="cuda").cpu()
     bias_c = bias.cpu()
 
     def run():
         xn = O.rms_norm(x, cpu["norm_w"], W.EPS)
         ids, wts = O.router_select(O.router_logits(xn, cpu["w32"]), bias_c, scoring="softmax", top_k=W.TOP_K)
-        return O.moe(xn, cpu["w_gu"], cpu["w_d"], ids, wts, residual=x)
+        y = O.moe_reference_loop(xn, cpu["w_gu"], cpu["w_d"], ids, wts)
+        return (y.to(torch.bfloat16).float() + x.float()).to(torch.bfloat16)
 
-    run()
+    for _ in range(warmup):
+        run()
     ts = []
     for _ in range(reps):
         t = time.perf_counter()
         run()
         ts.append(time.perf_counter() - t)
     t = sorted(ts)[len(ts) // 2]
-    return {"value": n_sample / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"first {n_sample} of the 512 tokens, median of {reps} runs after 1 warmup, "
-                      f"{platform.processor() or platform.machine()}"}
+    return {"value": n / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"all {n} tokens of the headline workload: RMSNorm, fp32 router, the reference's per-expert "
+                      f"bf16 loop (dev/test_moe_prefill.py:24-38), residual; median of {reps} runs after {warmup} "
+                      "warmups",
+            "ms_per_step": t * 1e3, "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads(), "torch": torch.__version__}
 
 
 def box_info():
@@ -553,16 +556,6 @@ def main():
     extra = {"prefill_512": head}
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: not args.quick and (not only or k in only))
-    if want("decode"):
-        extra["decode_bf16_b1"] = decode_metrics(b, 1, stream)
-        log(f"[bench] decode bf16: {extra['decode_bf16_b1']}")
-    if want("int8"):
-        W.quantize_block(b, torch.bfloat16)
-        for n in (1, 2, 4, 8):
-            extra[f"decode_int8_b{n}"] = decode_metrics(b, n, stream, int8=True)
-            log(f"[bench] decode int8 b{n}: {extra[f'decode_int8_b{n}']}")
-        for k in ("q_gu", "q_d", "s_gu", "s_d"):
-            b.pop(k)
     if want("zipf"):
         extra["prefill_2048_zipf"] = prefill_metrics(b, 2048, W.zipf_bias(device="cuda"), 10, 2, stream, seed=90)
         log(f"[bench] zipf: {extra['prefill_2048_zipf']}")
@@ -570,11 +563,27 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(b, bias)
         log(f"[bench] cpu baseline: {cpu}")
-    if want("full"):
-        del b
+    del b
+    torch.cuda.empty_cache()
+    if want("full") or want("decode") or want("int8"):
+        # 28 distinct layers: the full step, and its MoE blocks for the (cold) decode figures
+        step = W.ThinkerDecodeStep(28, "cuda")
+        torch.cuda.synchronize()
+        blocks = [p["blk"] for p in step.L]
+        if want("full"):
+            extra["full_decode_28l"] = full_decode_metrics(step, stream)
+            log(f"[bench] full decode: {extra['full_decode_28l']}")
+        if want("decode"):
+            extra["decode_bf16_b1"] = decode_metrics(blocks, 1, stream)
+            log(f"[bench] decode bf16 b1: {extra['decode_bf16_b1']}")
+        if want("int8"):
+            for blk in blocks:  # int8 experts with bf16 row scales from the same bf16 masters
+                W.quantize_block(blk, torch.bfloat16)
+            for n in (1, 2, 4, 8):
+                extra[f"decode_int8_b{n}"] = decode_metrics(blocks, n, stream, int8=True)
+                log(f"[bench] decode int8 b{n}: {extra[f'decode_int8_b{n}']}")
+        del step, blocks
         torch.cuda.empty_cache()
-        extra["full_decode_28l"] = full_decode_metrics(stream)
-        log(f"[bench] full decode: {extra['full_decode_28l']}")
     if want("talker"):
         torch.cuda.empty_cache()
         extra["talker"] = talker_metrics(stream)

@@ -77,7 +77,7 @@ def expert_items(index, prefix, n_experts, shared=True):
     return out
 
 
-def load_stacked_experts(index, prefix, n_experts, *, shared=True, int8=False, scale_dtype=torch.bfloat16,
+def load_stacked_experts(index, prefix, n_experts, *, shared=True, int8=False, scale_dtype=torch.float32,
                          device="cuda", out=None, threads=4):
     """Reads the MoE block `prefix`'s experts from the checkpoint `index` ({key: file}, or a model directory)
     into stacked tensors on `device`: {"w_gu": [E1, 2I, H], "w_d": [E1, H, I]} in bf16, or with int8=True

@@ -12,6 +12,7 @@ one device and copies.
   ragged_bias(...)      router bias ~ N(0, 0.5): ragged per-expert token counts (512-token prefill)
   zipf_bias(...)        router bias log p_e, p_e ~ rank^-1.2 under a fixed permutation (2048-token prefill)
   moe_block_forward     RMSNorm -> router -> MoE (+ residual) through the HIP kernels
+  expert_tensors, write_checkpoint   a layer's experts in the checkpoint key layout, as safetensors shards
   thinker_layer(...)    one synthetic thinker layer (q|k|v and o projections + MoE block)
   ThinkerDecodeStep     the synthetic 28-layer thinker decode step + LM head (one token)
   TalkerLLM(...)        a synthetic Qwen2 Talker LLM with StaticQwen2's attributes and KV cache layout
@@ -106,6 +107,47 @@ def flops_per_pair(hidden=HIDDEN, inter=INTER):
 
 def nb_blocks(P, E1, BM=64):
     return math.ceil((P + E1 * (BM - 1)) / BM)
+
+
+# ------------------------------------------------------------------------------ synthetic checkpoints
+
+def expert_tensors(prefix, n_experts, hidden, inter, seed, dtype=torch.bfloat16):
+    """One MoE layer's experts in the thinker's checkpoint key layout: `{prefix}.experts.{e}.{gate,up,down}_proj
+    .weight` for e < n_experts and `{prefix}.shared_experts.*`, ~ N(0, 0.05^2), drawn on the CPU from `seed`."""
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for e in list(range(n_experts)) + ["shared"]:
+        p = f"{prefix}.shared_experts." if e == "shared" else f"{prefix}.experts.{e}."
+        out[p + "gate_proj.weight"] = (torch.randn(inter, hidden, generator=g) * 0.05).to(dtype)
+        out[p + "up_proj.weight"] = (torch.randn(inter, hidden, generator=g) * 0.05).to(dtype)
+        out[p + "down_proj.weight"] = (torch.randn(hidden, inter, generator=g) * 0.05).to(dtype)
+    return out
+
+
+def write_checkpoint(root, tensors, shards=2, extra=True):
+    """Writes `tensors` as a sharded safetensors checkpoint under `root` (round robin over `shards` files, with
+    two unrelated tensors per shard when `extra`) and its model.safetensors.index.json. Returns `root`."""
+    import json
+    import os
+
+    from safetensors.torch import save_file
+    os.makedirs(root, exist_ok=True)
+    keys = sorted(tensors)
+    files = [{} for _ in range(shards)]
+    for i, k in enumerate(keys):
+        files[i % shards][k] = tensors[k].contiguous()
+    if extra:
+        for s in range(shards):
+            files[s][f"model.layers.{s}.input_layernorm.weight"] = torch.ones(64, dtype=torch.bfloat16)
+            files[s][f"model.layers.{s}.self_attn.q_proj.weight"] = torch.zeros(8, 64, dtype=torch.float32)
+    weight_map = {}
+    for s, f in enumerate(files):
+        name = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
+        save_file(f, os.path.join(root, name), metadata={"format": "pt"})
+        weight_map.update({k: name for k in f})
+    with open(os.path.join(root, "model.safetensors.index.json"), "w") as fh:
+        json.dump({"metadata": {}, "weight_map": weight_map}, fh)
+    return root
 
 
 # ------------------------------------------------------------------------------ thinker decode step

@@ -256,3 +256,32 @@ def small_linear_torch(x, w, b=None, act=0, residual=None, norm=None):
     if residual is not None:
         y = y + residual.float()
     return y.to(dt)
+
+
+# ------------------------------------------------------------------------------- reference torch loop
+
+def moe_reference_loop(x, w_gu, w_d, ids, weights):
+    """dev/test_moe_prefill.py:24-38, the reference's per-expert torch loop ("what the HF path does: one small
+    GEMM pair per active expert"), on x.dtype tensors: pairs sorted by expert (argsort of the flat ids), then
+    for each expert with pairs: gu = x[tok] @ W_gu[e]^T, a = silu(gu[:, :I]) * gu[:, I:], and
+    index_add of (a @ W_d[e]^T).float() * w into an fp32 [N, H] sum. Returns the fp32 sum. The CPU baseline
+    times this loop; torch's own bf16 ops round where the reference's do on the GPU."""
+    F = torch.nn.functional
+    N, H = x.shape
+    NK = ids.shape[1]
+    E1, I = w_d.shape[0], w_d.shape[-1]
+    y = torch.zeros(N, H, dtype=torch.float32)
+    flat = ids.reshape(-1)
+    order = flat.argsort()
+    counts = torch.bincount(flat, minlength=E1).tolist()
+    tok = order // NK
+    wf = weights.reshape(-1).float()
+    s = 0
+    for e, c in enumerate(counts):
+        if c:
+            t = tok[s:s + c]
+            gu = x[t] @ w_gu[e].T
+            a = F.silu(gu[:, :I]) * gu[:, I:]
+            y.index_add_(0, t, (a @ w_d[e].T).float() * wf[order[s:s + c]][:, None])
+        s += c
+    return y

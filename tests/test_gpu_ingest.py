@@ -4,7 +4,8 @@ import pytest
 import torch
 
 import expert_load as EL
-from ckpt_util import expert_tensors, stacked, write_checkpoint
+from ckpt_util import stacked
+from workloads import expert_tensors, write_checkpoint
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu

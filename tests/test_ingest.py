@@ -7,7 +7,7 @@ import torch
 from safetensors import safe_open
 
 import expert_load as EL
-from ckpt_util import expert_tensors, write_checkpoint
+from workloads import expert_tensors, write_checkpoint
 
 
 def test_read_header_matches_safetensors_library(tmp_path):

@@ -367,3 +367,17 @@ def test_small_linear_torch_branch_agrees_with_the_kernel_formula():
     xn1 = O.small_linear(x, torch.eye(K).to(BF), norm=(gam, 1e-6))  # 20 rows: the torch branch's norm, exactly
     assert torch.equal(xn1, F.rms_norm(x, (K,), gam, 1e-6))
     assert not torch.equal(O.small_linear(x[:16], torch.eye(K).to(BF), norm=(gam, 1e-6)), xn1[:16])
+
+
+def test_reference_loop_equals_the_kernel_formula():
+    """O.moe_reference_loop (dev/test_moe_prefill.py:24-38, the CPU baseline) rounds where the kernels do (bf16 g
+    and u from the bf16 GEMM, bf16 silu, bf16 a, bf16 part) and sums the slots in fp32 in expert order: equal to
+    O.moe up to the order of that sum and an ulp of bf16 GEMM output. A planted mistake in the pair -> token
+    map (order % NK instead of order // NK) is caught."""
+    x, w_gu, w_d, ids, wts = _tiny(7)
+    y = O.moe_reference_loop(x, w_gu, w_d, ids, wts)
+    assert y.dtype == torch.float32
+    _close(y.to(BF), O.moe(x, w_gu, w_d, ids, wts), rtol=1e-2, atol=4e-3)
+    perm = torch.arange(x.shape[0]).flip(0)
+    bad = O.moe_reference_loop(x[perm], w_gu, w_d, ids, wts)  # tokens no longer match their ids
+    assert not torch.allclose(bad.to(BF).float(), O.moe(x, w_gu, w_d, ids, wts).float(), rtol=1e-2, atol=4e-3)
