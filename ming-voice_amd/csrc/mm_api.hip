@@ -2,7 +2,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "mm_common.h"
 
@@ -46,6 +48,21 @@ int cu_count() {
     counts[dev] = n;
   }
   return counts[dev];
+}
+
+int allow_lds_ptr(const void* kernel, size_t bytes, const char* what) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> set;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = set[{kernel, dev}];
+  if (bytes > have) {
+    hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return set_error(MM_ERR_HIP, "HIP error setting LDS size of %s: %s", what, hipGetErrorString(e));
+    have = bytes;
+  }
+  return MM_OK;
 }
 
 }  // namespace mm

@@ -24,25 +24,22 @@ size_t dtype_size(int dtype);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Largest byte span a buffer resource (mmd::make_rsrc) may describe: the kernels address it with 32-bit
+// offsets and use 2^31 (mmd::kPast) as the offset that reads zero, so every valid offset must stay below it.
+constexpr int64_t kMaxRsrcBytes = 0x7fffffffLL;
+inline bool rsrc_fits(int64_t bytes) { return bytes >= 0 && bytes <= kMaxRsrcBytes; }
+
 // Number of compute units of the current device (queried once per device, thread-safe).
 int cu_count();
 
-// Dynamic LDS above the default limit needs an opt-in per kernel and device (done once each; the static
-// state is per kernel instantiation).
+// Dynamic LDS above the default limit needs an opt-in per kernel and device: the attribute is set the first
+// time a kernel is launched on a device with a given size, and again whenever a launch needs more than the
+// size set so far (state keyed by the kernel's address and the device, thread-safe).
+int allow_lds_ptr(const void* kernel, size_t bytes, const char* what);
+
 template <class K>
 int allow_lds(K kernel, size_t bytes, const char* what) {
-  static std::mutex mu;
-  static bool done[64] = {false};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!done[dev]) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(bytes));
-    if (e != hipSuccess) return set_error(MM_ERR_HIP, "HIP error setting LDS size of %s: %s", what, hipGetErrorString(e));
-    done[dev] = true;
-  }
-  return MM_OK;
+  return allow_lds_ptr(reinterpret_cast<const void*>(kernel), bytes, what);
 }
 
 }  // namespace mm

@@ -532,6 +532,16 @@ int check_experts(const char* who, const mm_experts* ex) {
   return MM_OK;
 }
 
+// The decode kernels address one expert's gate/up rows and its down rows through one buffer resource each.
+int check_decode_spans(const char* who, const mm_experts* ex) {
+  const int64_t es = ex->w_dtype == MM_INT8 ? 1 : 2;
+  const int64_t gu = 2 * ex->inter * ex->gu_stride_n * es, d = ex->hidden * ex->d_stride_n * es;
+  MM_REQUIRE(rsrc_fits(gu) && rsrc_fits(d),
+             "%s: one expert's weights span %lld (gate/up) and %lld (down) bytes; each must stay below 2^31", who,
+             (long long)gu, (long long)d);
+  return MM_OK;
+}
+
 }  // namespace mm
 
 extern "C" int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stride, const mm_experts* ex,
@@ -539,6 +549,7 @@ extern "C" int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stri
                              int64_t wts_row_stride, const void* residual, int64_t res_row_stride, void* a_buf, void* y,
                              int64_t y_row_stride, int phases, void* stream) {
   int rc = mm::check_experts("moe_decode", ex);
+  if (!rc) rc = mm::check_decode_spans("moe_decode", ex);
   if (rc) return rc;
   MM_REQUIRE(n_tokens >= 1 && nk >= 1 && n_tokens * nk <= kMaxPairs,
              "moe_decode: n_tokens * nk must be in [1, %d] (got %lld x %lld)", kMaxPairs, (long long)n_tokens,
@@ -551,6 +562,8 @@ extern "C" int mm_moe_decode(const void* x, int64_t n_tokens, int64_t x_row_stri
   MM_REQUIRE(ids_row_stride >= nk && wts_row_stride >= nk, "moe_decode: ids/wts row stride smaller than nk");
   MM_REQUIRE(!residual || res_row_stride >= ex->hidden, "moe_decode: residual row stride smaller than hidden");
   MM_REQUIRE(ex->n_slots <= 0x7fffffff && ex->hidden <= 0x7fffffff && ex->inter <= 0x7fffffff, "moe_decode: shape too large");
+  MM_REQUIRE(mm::rsrc_fits(n_tokens * x_row_stride * 2) && mm::rsrc_fits(n_tokens * nk * ex->inter * 2),
+             "moe_decode: x rows or a_buf span 2^31 bytes or more");
   DecodeArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.xs = x_row_stride;
@@ -610,6 +623,7 @@ static int block_decode(const char* who, const void* x, int64_t n_tokens, int64_
                         int ids_dtype, float* wts, void* a_buf, void* workspace, int add_residual, void* y,
                         int64_t y_row_stride, void* stream) {
   int rc = mm::check_experts(who, ex);
+  if (!rc) rc = mm::check_decode_spans(who, ex);
   if (rc) return rc;
   const int64_t nk = static_cast<int64_t>(top_k) + 1;
   rc = mm::check_router_args(n_tokens, n_experts, scoring, n_group, topk_group, top_k, 1, ids, ids_dtype, wts, nk);

@@ -337,6 +337,8 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
   MM_REQUIRE((x_row_stride >= K || x_row_stride == 0) && w_row_stride >= K && y_row_stride >= N,
              "small_linear: row stride too small (x rows may also repeat one row, stride 0)");
   MM_REQUIRE(!residual || res_row_stride >= N, "small_linear: residual row stride too small");
+  MM_REQUIRE(mm::rsrc_fits(N * 2) && (!residual || mm::rsrc_fits(M * res_row_stride * 2)),
+             "small_linear: bias or residual spans 2^31 bytes or more");
   MM_REQUIRE(mm::aligned16(w) && (w_row_stride * 2) % 16 == 0, "small_linear: weight rows must be 16-byte aligned");
   hipStream_t st = MM_STREAM(stream);
   const uint16_t* xin = static_cast<const uint16_t*>(x);

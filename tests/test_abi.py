@@ -141,3 +141,24 @@ def test_reference_module_surface_is_kept():
         for n in names:
             assert hasattr(mod, n), f"{mod.__name__}.{n}"
     fastlinear.save_cache()  # nothing tuned: writes nothing
+
+
+def test_decode_refuses_expert_spans_beyond_32_bit_offsets():
+    """The decode kernels read one expert's rows through a buffer resource addressed by 32-bit offsets, with
+    2^31 as the offset that reads zero; a descriptor whose expert spans 2^31 bytes or more is refused before any
+    launch (an int8 expert with 2 x 32768 gate/up rows of 32768 bytes spans exactly 2^31)."""
+    lib = mm.load()
+    P = ctypes.c_void_p(16)
+    ex = mm.Experts()
+    ex.w_gu, ex.w_d, ex.s_gu, ex.s_d, ex.w_dtype, ex.s_dtype = 16, 16, 16, 16, mm.MM_INT8, mm.MM_FP32
+    ex.n_slots, ex.hidden, ex.inter = 2, 32768, 32768
+    ex.gu_stride_n, ex.d_stride_n = 32768, 32768
+    ex.gu_stride_e, ex.d_stride_e = 2 * 32768 * 32768, 32768 * 32768
+    ex.sgu_stride_e, ex.sd_stride_e = 2 * 32768, 32768
+    assert "2^31" in _err(lib.mm_moe_decode(P, 1, 32768, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None, 0, P, P,
+                                            32768, 0, None))
+    ex.inter = 16384  # 2 x 16384 rows of 32768 bytes = 2^30: passes this check and stops at the next (10 x 7 pairs)
+    ex.gu_stride_e, ex.d_stride_e, ex.sgu_stride_e = 2 * 16384 * 32768, 32768 * 16384, 2 * 16384
+    ex.d_stride_n = 16384
+    assert "n_tokens * nk" in _err(lib.mm_moe_decode(P, 10, 32768, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None,
+                                                     0, P, P, 32768, 0, None))

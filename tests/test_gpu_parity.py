@@ -365,7 +365,7 @@ def test_prefill_zipf_2048_subset_and_histogram(blk):
 def test_prefill_and_decode_ragged_shapes(int8):
     """Tails on every tiled dim: hidden 1536 (6 column tiles of 256), inter 208 (partial 128-column tile and a
     partial 64-wide k slab), 129 expert slots (the Ming thinker's 128 + shared), top-8. 1100 tokens put
-    about 69 pairs on each expert: the 128-row tiles (block pairs) and the odd last blocks."""
+    about 69 pairs on each routed expert (64-pair blocks, several per expert, odd last blocks)."""
     H, I, E, K = 1536, 208, 128, 8
     w_gu = W.normal((E + 1, 2 * I, H), 0.02, 130, DEV)
     w_d = W.normal((E + 1, H, I), 0.02, 131, DEV)
@@ -384,6 +384,25 @@ def test_prefill_and_decode_ragged_shapes(int8):
             y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
             ref = O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu())
         close(y, ref)
+
+
+def test_prefill_ragged_shapes_128_pair_blocks():
+    """The 128-pair blocks (bf16 experts averaging at least 128 pairs: 700 tokens x 7 slots over 33 slots) on
+    ragged dims: hidden 1536, inter 208 (a partial 128-column tile and a partial 64-wide k slab), so the
+    two-row-wave layout of those tiles meets padding rows, partial column tiles and the k tail."""
+    H, I, E, K = 1536, 208, 32, 6
+    n = 700
+    assert fused_moe.prefill_block_m(n, K + 1, E + 1) == 128
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 135, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 136, DEV)
+    g = torch.Generator().manual_seed(137)
+    sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
+    sel[: n // 3, 0] = 5  # one hot expert: several full 128-pair blocks
+    ids = torch.cat([sel, torch.full((n, 1), E)], 1).to(DEV)
+    wts = torch.cat([torch.rand(n, K, generator=g), torch.ones(n, 1)], 1).to(DEV)
+    x = W.normal((n, H), 1.0, 138, DEV)
+    y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
+    close(y, O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu()))
 
 
 def test_prefill_equals_per_token_decode(blk):
