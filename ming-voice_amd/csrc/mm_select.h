@@ -14,24 +14,33 @@ struct SelectParams {
   int append_shared;
 };
 
-// Arg-max over the lane-held slots then across the wave; lowest expert index wins ties. Slot 0 seeds the
-// search so that an all -inf input still yields the lowest index, as an arg-max with first-index ties
-// does; slots past the valid range hold -inf and larger indices.
+// Arg-max over the lane-held slots then across the wave; lowest expert index wins ties. The maximum comes from
+// DPP row reductions (wave_max), the index from one ballot per slot: expert e = lane + 64 j, so the lowest index
+// holding the maximum lies in the lowest slot j whose ballot is non-empty, at that ballot's lowest set lane. A
+// maximum that no lane matches (NaN keys) falls back to the lowest valid slot. Slots past the valid range hold
+// -inf and larger indices, so an all -inf input yields the lowest index.
 template <int NS>
 __device__ __forceinline__ void slots_argmax(const float (&v)[NS], int nslots, float& best, int& bidx) {
-  const int lane = lane_id();
-  best = v[0];
-  bidx = lane;
+  float m = v[0];
 #pragma unroll
-  for (int j = 1; j < NS; ++j) {
-    if (j < nslots && v[j] > best) { best = v[j]; bidx = lane + kWave * j; }
+  for (int j = 1; j < NS; ++j)
+    if (j < nslots) m = fmaxf(m, v[j]);
+  best = wave_max(m);
+  bidx = -1;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (bidx < 0 && j < nslots) {
+      const unsigned long long hit = __ballot(v[j] == best);
+      if (hit) bidx = __ffsll(static_cast<long long>(hit)) - 1 + kWave * j;
+    }
   }
-  wave_argmax(best, bidx);
+  if (bidx < 0) bidx = 0;
 }
 
-// Fast path of select_token for at most 64 experts without group limits: one expert per lane, every lane
-// ranks its key against all others (value descending, index ascending, through scalar lane reads), so the
-// picks need no chain of cross-lane reductions. Same picks, order and arithmetic as the general path.
+// Fast path of select_token for at most 64 experts without group limits: one expert per lane. Each of the top_k
+// rounds takes the maximum key of the lanes not yet picked (DPP reductions), then the lowest such lane with a
+// ballot, so the picks come in the order of a stable descending sort (value descending, index ascending). Same
+// picks, order and arithmetic as the general path.
 __device__ __forceinline__ void select_token64(const SelectParams& a, const float* lg, int& id, float& w, bool& has) {
   const int lane = lane_id();
   const int E = a.E;
@@ -53,22 +62,20 @@ __device__ __forceinline__ void select_token64(const SelectParams& a, const floa
     const float den = wave_sum(valid ? score : 0.f);
     score = score / den;
   }
-  // rank = lanes ahead of this one: larger key, or equal key and lower index
-  int rank = 0;
-  const int kb = __float_as_int(key);
-  for (int j = 0; j < kWave; ++j) {
-    const float kj = __int_as_float(__builtin_amdgcn_readlane(kb, j));
-    rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
-  }
   // lane k gathers the k-th pick; the weights' sum runs over the picks in order
+  bool taken = !valid;
   float total = 0.f, sel_w = 0.f;
   int sel_e = 0;
   const int sb = __float_as_int(score);
   for (int k = 0; k < a.top_k; ++k) {
-    const int src = __ffsll(static_cast<long long>(__ballot(rank == k))) - 1;
+    const float m = wave_max(taken ? -INFINITY : key);
+    unsigned long long hit = __ballot(!taken && key == m);
+    if (!hit) hit = __ballot(!taken);  // NaN keys: the lowest lane not yet picked
+    const int src = __ffsll(static_cast<long long>(hit)) - 1;
     const float s = __int_as_float(__builtin_amdgcn_readlane(sb, src));
     total += s;
     if (lane == k) { sel_w = s; sel_e = src; }
+    if (lane == src) taken = true;
   }
   has = false;
   w = 0.f;
