@@ -596,7 +596,7 @@ int check_router_args(int64_t n_tokens, int64_t E, int scoring, int n_group, int
                       int append_shared, const void* ids, int ids_dtype, const float* wts, int64_t out_row_stride);
 int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
                  const float* w32, const mmd::SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
-                 int64_t out_row_stride, void* xn_out, hipStream_t s);
+                 int64_t out_row_stride, void* xn_out, hipStream_t s, bool with_select = true);
 }  // namespace mm
 
 // Whole MoE block for a prefill batch: RMSNorm into xn, router logits, selection, align, gate/up and down

@@ -476,10 +476,11 @@ namespace mm {
 // bf16), logits of the normalised rows, then the selection with the shared expert appended. The norm runs
 // inside the logits kernel (router_gemv_bf16_kernel up to 8 tokens, router_norm_mfma_kernel above, each
 // workgroup normalising its 16 token rows); rows too long or misaligned for those normalise first
-// (mm_rms_norm). Either way xn is bit-identical.
+// (mm_rms_norm). Either way xn is bit-identical. with_select false stops after the logits (a caller that
+// selects inside its next kernel).
 int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const void* norm_w, float eps,
                  const float* w32, const SelectParams& sp, float* logits, void* ids, int ids_dtype, float* wts,
-                 int64_t out_row_stride, void* xn_out, hipStream_t s) {
+                 int64_t out_row_stride, void* xn_out, hipStream_t s, bool with_select) {
   MM_REQUIRE(n_tokens >= 1 && n_tokens <= 0x7fffffffLL, "router: bad token count");
   int rc;
   const bool fused = n_tokens > 8 && H % 8 == 0 && H <= 4096 && xs % 8 == 0 && xn_out && aligned16(x) &&
@@ -507,7 +508,7 @@ int router_front(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const v
     if (rc) return rc;
     rc = launch_logits<BF16>(xn_out, n_tokens, H, H, w32, sp.E, logits, s);
   }
-  if (rc) return rc;
+  if (rc || !with_select) return rc;
   return launch_select(logits, n_tokens, sp.E, sp.bias, sp.scoring, sp.n_group, sp.topk_group, sp.top_k, sp.scale,
                        sp.append_shared, ids, ids_dtype, wts, out_row_stride, s);
 }
