@@ -1,0 +1,181 @@
+"""The thinker's attention mixers on hand-written gfx950 HIP kernels: the KDA (Kimi delta attention) layers'
+recurrent core, short convolutions and gated output norm, and the MLA layers' single-token attention over the
+static cache.
+
+  fused_recurrent_kda   drop-in for fla.ops.kda.fused_recurrent_kda (fla-core 0.5.2; engine.py:242-262): same
+                        keywords, B = 1; the state is fp32 [1, H, K, V], updated in place with inplace=True
+  short_conv            the step form of fla's ShortConvolution (a [1, C, W] cache of the last inputs, SiLU)
+  rms_norm_gated        fla's FusedRMSNormGated with a sigmoid gate (a KDA layer's o_norm)
+  mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
+                        masked softmax attention over positions 0..pos
+Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
+passed in); there is no CPU path.
+"""
+import torch
+
+import _mingmoe as _mm
+
+__all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "mla_decode_attn", "mla_attn_workspace"]
+
+
+def _f32_or_bf16(t, name):
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"{name} must be fp32 or bf16 (got {t.dtype})")
+    return _mm.MM_FP32 if t.dtype == torch.float32 else _mm.MM_BF16
+
+
+def _tokens(t, name, H, D):
+    """[1, T, H, D] or [T, H, D] with contiguous heads -> (tensor, T, token stride in elements)."""
+    if t.dim() == 4:
+        if t.shape[0] != 1:
+            raise ValueError(f"{name}: batch {t.shape[0]} (B = 1 only)")
+        t = t[0]
+    if t.dim() != 3 or t.shape[1] != H or t.shape[2] != D:
+        raise ValueError(f"{name}: expected [1, T, {H}, {D}], got {tuple(t.shape)}")
+    if t.stride(2) != 1 or t.stride(1) != D:
+        t = t.contiguous()
+    return t, t.shape[0], t.stride(0)
+
+
+def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
+                        output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
+                        lower_bound=None, inplace=False, out=None, **unused):
+    """q, k [1, T, H, K] bf16; v [1, T, H, V] bf16; g [1, T, H, K] (bf16 / fp32; the raw gate projection when
+    use_gate_in_kernel, else a log decay); beta [1, T, H] (fp32 / bf16); A_log [H], dt_bias [H * K] (or [H, K]);
+    initial_state [1, H, K, V] fp32 (zeros when None). Returns (o [1, T, H, V] bf16, final_state or None).
+    scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor)."""
+    _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out)
+    if q.dim() != 4 or q.shape[0] != 1:
+        raise ValueError(f"fused_recurrent_kda: q must be [1, T, H, K] (got {tuple(q.shape)})")
+    _, T, H, K = q.shape
+    V = v.shape[-1]
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"fused_recurrent_kda: {name} must be bf16 (got {t.dtype})")
+    q2, _, qts = _tokens(q, "q", H, K)
+    k2, _, kts = _tokens(k, "k", H, K)
+    v2, _, vts = _tokens(v, "v", H, V)
+    g2, _, gts = _tokens(g, "g", H, K)
+    gdt = _f32_or_bf16(g2, "g")
+    b2 = beta[0] if beta.dim() == 3 else beta
+    if tuple(b2.shape) != (T, H):
+        raise ValueError(f"fused_recurrent_kda: beta must be [1, T, H] (got {tuple(beta.shape)})")
+    if b2.stride(1) != 1:
+        b2 = b2.contiguous()
+    bdt = _f32_or_bf16(b2, "beta")
+    use_gate = bool(use_gate_in_kernel)
+    if use_gate:
+        if A_log is None or dt_bias is None:
+            raise ValueError("fused_recurrent_kda: use_gate_in_kernel needs A_log and dt_bias")
+        A_log = A_log.float().reshape(H).contiguous()
+        dt_bias = dt_bias.float().reshape(H * K).contiguous()
+    if initial_state is None:
+        state = torch.zeros(H, K, V, device=q.device, dtype=torch.float32)
+    else:
+        if initial_state.dtype != torch.float32 or tuple(initial_state.shape[-3:]) != (H, K, V):
+            raise ValueError(f"fused_recurrent_kda: initial_state must be fp32 [1, {H}, {K}, {V}]")
+        if inplace:
+            if not initial_state.is_contiguous():
+                raise ValueError("fused_recurrent_kda: inplace needs a contiguous initial_state")
+            state = initial_state
+        else:
+            state = initial_state.reshape(H, K, V).clone()
+    o = torch.empty(T, H, V, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(T, H, V)
+    if o.dtype != torch.bfloat16 or o.stride(2) != 1 or o.stride(1) != V:
+        raise ValueError("fused_recurrent_kda: out must be bf16 [1, T, H, V] with contiguous heads")
+    sc = float(scale) if scale is not None else K ** -0.5
+    lb = float("nan") if lower_bound is None else float(lower_bound)
+    lib = _mm.load()
+    with _mm.on_device(q):
+        _mm.check(lib.mm_kda_recurrent(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts,
+                                       _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,
+                                       1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0, sc, T, H, K, V,
+                                       _mm.ptr(state), _mm.ptr(o), o.stride(0), _mm.stream_of(q)), "fused_recurrent_kda")
+    final = None
+    if output_final_state or inplace:
+        final = state if (inplace and initial_state is not None) else state.reshape(1, H, K, V)
+    return o.reshape(1, T, H, V), final
+
+
+def short_conv(x, cache, weight, bias=None, activation="silu", out=None):
+    """x [1, T, C] or [T, C] bf16; cache [1, C, W] bf16 (the last W inputs per channel, updated in place); weight
+    [C, 1, W] or [C, W] bf16; bias [C] or None. Returns y with x's shape: act(conv over the window) per token."""
+    _mm.require_gpu(x, cache, weight, bias, out)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    T, C = x2.shape
+    W = cache.shape[-1]
+    if cache.numel() != C * W or not cache.is_contiguous() or cache.dtype != torch.bfloat16:
+        raise ValueError(f"short_conv: cache must be a contiguous bf16 [1, {C}, W] tensor")
+    w2 = weight.reshape(C, -1)
+    if w2.shape[1] != W or w2.dtype != torch.bfloat16:
+        raise ValueError(f"short_conv: weight must be bf16 [{C}, 1, {W}]")
+    w2 = w2.contiguous()
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    if activation not in ("silu", "swish", None):
+        raise ValueError(f"short_conv: activation {activation!r} (silu or None)")
+    y = torch.empty(T, C, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(T, C)
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_short_conv(_mm.ptr(x2), x2.stride(0), T, C, _mm.ptr(cache), W, _mm.ptr(w2), _mm.ptr(bias),
+                                    0 if activation is None else 1, _mm.ptr(y), y.stride(0), _mm.stream_of(x)),
+                  "short_conv")
+    return y.reshape(x.shape)
+
+
+def rms_norm_gated(x, g, weight, eps=1e-5, out=None):
+    """bf16(x * rsqrt(mean(x^2) + eps) * weight * sigmoid(g)) over the last dim (<= 512); x, g bf16 of one shape."""
+    _mm.require_gpu(x, g, weight, out)
+    n = x.shape[-1]
+    x2 = x.reshape(-1, n)
+    g2 = g.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if g2.stride(-1) != 1:
+        g2 = g2.contiguous()
+    if x2.shape != g2.shape:
+        raise ValueError("rms_norm_gated: x and g must have one shape")
+    y = torch.empty(x2.shape, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(x2.shape)
+    w = weight.to(torch.bfloat16).contiguous()
+    lib = _mm.load()
+    with _mm.on_device(x):
+        _mm.check(lib.mm_rms_norm_gated(_mm.ptr(x2), x2.stride(0), _mm.ptr(g2), g2.stride(0), _mm.ptr(w), x2.shape[0], n,
+                                        float(eps), _mm.ptr(y), y.stride(0), _mm.stream_of(x)), "rms_norm_gated")
+    return y.reshape(x.shape)
+
+
+def mla_attn_workspace(nh, dv, max_len, device):
+    n = int(_mm.load().mm_mla_attn_workspace(int(nh), int(dv), int(max_len)))
+    return torch.empty(max(n // 4, 1), device=device, dtype=torch.float32)
+
+
+def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None, workspace=None):
+    """One token of an MLA layer. q, k_new [nh, dqk] (any leading shape with nh * dqk elements), v_new [nh, dv];
+    k_cache [1, nh, max_len, dqk], v_cache [1, nh, max_len, dv] (bf16, the layer's StaticHybridCache buffers);
+    pos: a device tensor holding the position (int64 / int32). Writes the new rows at pos and returns
+    out [nh, dv] = softmax(scale * q . K[0..pos]^T) . V[0..pos] (scale defaults to dqk ** -0.5)."""
+    _mm.require_gpu(q, k_new, v_new, k_cache, v_cache, pos, out, workspace)
+    nh, max_len, dqk = k_cache.shape[-3:]
+    dv = v_cache.shape[-1]
+    if tuple(v_cache.shape[-3:-1]) != (nh, max_len) or not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("mla_decode_attn: caches must be contiguous [1, nh, max_len, d]")
+    qf = q.reshape(nh, dqk).contiguous()
+    kf = k_new.reshape(nh, dqk).contiguous()
+    vf = v_new.reshape(nh, dv).contiguous()
+    for name, t in (("q", qf), ("k_new", kf), ("v_new", vf), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"mla_decode_attn: {name} must be bf16")
+    if pos.dtype not in (torch.int64, torch.int32) or pos.numel() != 1:
+        raise ValueError("mla_decode_attn: pos must be a one-element int64 / int32 device tensor")
+    y = torch.empty(nh, dv, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(nh, dv)
+    ws = mla_attn_workspace(nh, dv, max_len, q.device) if workspace is None else workspace
+    sc = float(scale) if scale is not None else dqk ** -0.5
+    lib = _mm.load()
+    with _mm.on_device(q):
+        _mm.check(lib.mm_mla_decode_attn(_mm.ptr(qf), _mm.ptr(kf), _mm.ptr(vf), nh, dqk, dv, _mm.ptr(k_cache),
+                                         _mm.ptr(v_cache), max_len, _mm.ptr(pos), _mm.dtype_code(pos), sc, _mm.ptr(y),
+                                         _mm.ptr(ws), ws.numel() * ws.element_size(), _mm.stream_of(q)),
+                  "mla_decode_attn")
+    return y

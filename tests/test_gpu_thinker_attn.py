@@ -1,0 +1,162 @@
+"""GPU parity of the thinker's attention mixers (KDA recurrent core, short convolution, gated norm, MLA decode
+attention) against oracle/thinker_attn_oracle.py on seeded inputs. bf16 outputs within rtol 2e-2 / atol 1e-2; the fp32
+KDA state within rtol 1e-3 / atol 1e-4 of the float64 oracle; cache rows bit-exact."""
+import pytest
+import torch
+
+import thinker_attn as TA
+import workloads as W
+from oracle import thinker_attn_oracle as A
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+def close(got, want, rtol=2e-2, atol=1e-2):
+    torch.testing.assert_close(got.float().cpu(), want.float().cpu(), rtol=rtol, atol=atol)
+
+
+def _kda_inputs(T, H, K, V, seed, gdt=torch.float32):
+    q = W.normal((1, T, H, K), 1.0, seed, DEV)
+    k = W.normal((1, T, H, K), 1.0, seed + 1, DEV)
+    v = W.normal((1, T, H, V), 1.0, seed + 2, DEV)
+    g = W.normal((1, T, H, K), 1.0, seed + 3, DEV, dtype=gdt)
+    beta = torch.sigmoid(W.normal((1, T, H), 1.0, seed + 4, DEV, dtype=torch.float32))
+    A_log = W.normal((H,), 0.5, seed + 5, DEV, dtype=torch.float32)
+    dt = W.normal((H * K,), 0.5, seed + 6, DEV, dtype=torch.float32)
+    S0 = W.normal((1, H, K, V), 0.3, seed + 7, DEV, dtype=torch.float32)
+    return q, k, v, g, beta, A_log, dt, S0
+
+
+@pytest.mark.parametrize("T,H,K,V", [(1, 16, 128, 128), (7, 4, 128, 128), (64, 2, 128, 128), (3, 5, 64, 64),
+                                     (9, 3, 128, 64), (4, 2, 64, 128)])
+@pytest.mark.parametrize("gate", ["softplus", "lower_bound", "none"])
+def test_kda_recurrent_matches_oracle(T, H, K, V, gate):
+    print(f"[kda] T={T} H={H} K={K} V={V} gate={gate}", flush=True)
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 200 + T + K, torch.bfloat16 if gate == "none" else torch.float32)
+    if gate == "none":  # g is already a log decay: keep it small and negative
+        g = (-0.1 * g.float().abs()).to(BF)
+    lb = -5.0 if gate == "lower_bound" else None
+    state = S0.clone()
+    o, fin = TA.fused_recurrent_kda(q, k, v, g, beta, A_log=A_log, dt_bias=dt, initial_state=state,
+                                    output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                    use_gate_in_kernel=gate != "none", lower_bound=lb)
+    assert torch.equal(state, S0)  # not in place by default
+    ro, rS = A.kda_recurrent(q[0].cpu(), k[0].cpu(), v[0].cpu(), g[0].cpu(), beta[0].cpu(), S0[0].cpu(),
+                             A_log=A_log.cpu(), dt_bias=dt.cpu(), use_gate=gate != "none", lower_bound=lb)
+    close(o[0], ro)
+    torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
+
+
+def test_kda_inplace_decode_steps_and_graph_replays():
+    """A decode step (T = 1) updates the state in place; a captured step replayed with new tokens advances it
+    exactly as eager steps do."""
+    H, K, V = 8, 128, 128
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(1, H, K, V, 300)
+    st_e, st_g = S0.clone(), S0.clone()
+    out_g = torch.empty(1, 1, H, V, device=DEV, dtype=BF)
+
+    def step(state, out=None):
+        return TA.fused_recurrent_kda(q, k, v, g, beta, A_log=A_log, dt_bias=dt, initial_state=state, inplace=True,
+                                      use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, out=out)[0]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        step(st_g, out_g)
+    torch.cuda.synchronize()
+    assert torch.equal(st_g, S0)  # capture does not run the kernel
+    for i in range(3):
+        for t, seed in ((q, 310), (k, 311), (v, 312)):
+            t.copy_(W.normal(t.shape, 1.0, seed + 10 * i, DEV))
+        want = step(st_e).clone()
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, want) and torch.equal(st_g, st_e), i
+    assert not torch.equal(st_e, S0)
+
+
+def test_kda_zero_write_strength_keeps_the_state():
+    """beta = 0 with gate inputs of -1e30 (the padded-prompt trick, engine.py:252-253): the state is unchanged."""
+    H, K, V = 4, 128, 128
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(3, H, K, V, 320)
+    g = torch.full_like(g, -1e30)
+    _, fin = TA.fused_recurrent_kda(q, k, v, g, torch.zeros_like(beta), A_log=A_log, dt_bias=dt, initial_state=S0,
+                                    output_final_state=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True)
+    assert torch.equal(fin, S0)
+
+
+@pytest.mark.parametrize("T,C,Wd", [(1, 6144, 4), (5, 6144, 4), (3, 1000, 2), (2, 77, 8)])
+def test_short_conv_matches_oracle(T, C, Wd):
+    x = W.normal((1, T, C), 1.0, 400 + T, DEV)
+    cache = W.normal((1, C, Wd), 1.0, 401, DEV)
+    w = W.normal((C, 1, Wd), 0.5, 402, DEV)
+    b = W.normal((C,), 0.5, 403, DEV)
+    c0 = cache.clone()
+    y = TA.short_conv(x, cache, w, b)
+    ry, rc = A.short_conv(x[0].cpu(), c0[0].cpu(), w[:, 0].cpu(), b.cpu())
+    close(y[0], ry)
+    assert torch.equal(cache[0].cpu(), rc.to(BF))  # the window holds bf16 inputs exactly
+
+
+def test_rms_norm_gated_matches_oracle():
+    x = W.normal((7, 16, 128), 2.0, 410, DEV)
+    g = W.normal((7, 16, 128), 1.0, 411, DEV)
+    w = W.normal((128,), 0.1, 412, DEV, mean=1.0)
+    close(TA.rms_norm_gated(x, g, w, 1e-5), A.rms_norm_gated(x.cpu(), g.cpu(), w.cpu(), 1e-5))
+
+
+@pytest.mark.parametrize("nh,dq,dv,L", [(16, 192, 128, 1024), (4, 64, 64, 300), (2, 96, 32, 70)])
+def test_mla_decode_attn_matches_oracle(nh, dq, dv, L):
+    kc = W.normal((1, nh, L, dq), 1.0, 420, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 421, DEV)
+    for pos in sorted({0, 1, 63, 64, 65, L // 2, L - 1}):
+        print(f"[mla] nh={nh} dq={dq} dv={dv} L={L} pos={pos}", flush=True)
+        q = W.normal((nh, dq), 1.0, 430 + pos, DEV)
+        kn = W.normal((nh, dq), 1.0, 431 + pos, DEV)
+        vn = W.normal((nh, dv), 1.0, 432 + pos, DEV)
+        k0, v0 = kc.clone(), vc.clone()
+        out = TA.mla_decode_attn(q, kn, vn, kc, vc, torch.tensor([pos], device=DEV))
+        ro, rk, rv = A.mla_decode_attn(q.cpu(), kn.cpu(), vn.cpu(), k0[0].cpu(), v0[0].cpu(), pos)
+        close(out, ro)
+        assert torch.equal(kc[0].cpu(), rk) and torch.equal(vc[0].cpu(), rv)
+
+
+def test_mla_out_of_range_position_writes_nothing():
+    nh, dq, dv, L = 4, 64, 64, 128
+    kc = W.normal((1, nh, L, dq), 1.0, 440, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 441, DEV)
+    k0, v0 = kc.clone(), vc.clone()
+    q = W.normal((nh, dq), 1.0, 442, DEV)
+    out = TA.mla_decode_attn(q, q, q, kc, vc, torch.tensor([L], device=DEV))
+    assert torch.isnan(out.float()).all() and torch.equal(kc, k0) and torch.equal(vc, v0)
+
+
+def test_mla_graph_replays_follow_the_position():
+    """The attention captured once and replayed at positions 5, 6, 7 equals eager calls on a copy of the cache."""
+    nh, dq, dv, L = 16, 192, 128, 256
+    kc = W.normal((1, nh, L, dq), 1.0, 450, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 451, DEV)
+    ke, ve = kc.clone(), vc.clone()
+    q = W.normal((nh, dq), 1.0, 452, DEV)
+    kn, vn = W.normal((nh, dq), 1.0, 453, DEV), W.normal((nh, dv), 1.0, 454, DEV)
+    pos = torch.tensor([5], device=DEV)
+    out = torch.empty(nh, dv, device=DEV, dtype=BF)
+    ws = TA.mla_attn_workspace(nh, dv, L, DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        TA.mla_decode_attn(q, kn, vn, kc, vc, pos, out=out, workspace=ws)
+    for p in (5, 6, 7):
+        pos.fill_(p)
+        q.copy_(W.normal((nh, dq), 1.0, 460 + p, DEV))
+        want = TA.mla_decode_attn(q, kn, vn, ke, ve, torch.tensor([p], device=DEV)).clone()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want) and torch.equal(kc, ke) and torch.equal(vc, ve), p
