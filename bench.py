@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run (decode,int8,zipf,full,talker,ingest)")
+                    help="comma list of extra workloads to run (decode,int8,zipf,full,hybrid,talker,ingest)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 counter passes (traffic = null)")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
@@ -324,6 +324,25 @@ def full_decode_metrics(step, stream):
             "moe_TBs": moe_layer_bytes * layers / moe_ms / 1e9}
 
 
+def hybrid_decode_metrics(stream, layers=28, pos=456):
+    """One decode token of the synthetic hybrid thinker (workloads.HybridThinkerStep: 21 KDA + 7 MLA layers, each
+    with its MoE block, final norm + LM head) replayed from one hipGraph. Every replay advances the position on
+    the device: one eager call at pos, then replays at pos + 1, pos + 2, ...; the timed ones (5 x 20 after 2
+    warm-up replays each) lie in pos + 3 .. pos + 110 of a 1024-row cache, mean pos + 56.5 (512.5 by default)."""
+    import workloads as W
+    step = W.HybridThinkerStep(layers, "cuda", pos=pos)
+    torch.cuda.synchronize()
+    ms = median_graph_ms(graph_of(step, stream), stream)
+    total = step.bytes_per_step(pos + 56)
+    kda = sum(p["kind"] == "kda" for p in step.L)
+    out = {"layers": layers, "kda_layers": kda, "mla_layers": layers - kda, "positions": [pos + 3, pos + 110],
+           "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
+           "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100}
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------------------------------------- Talker path
 
 def talker_metrics(stream, layers=24, max_len=1024, pos=512):
@@ -584,6 +603,9 @@ def main():
                 log(f"[bench] decode int8 b{n}: {extra[f'decode_int8_b{n}']}")
         del step, blocks
         torch.cuda.empty_cache()
+    if want("hybrid"):
+        extra["hybrid_decode_28l"] = hybrid_decode_metrics(stream)
+        log(f"[bench] hybrid decode: {extra['hybrid_decode_28l']}")
     if want("talker"):
         torch.cuda.empty_cache()
         extra["talker"] = talker_metrics(stream)

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 7
+#define MM_ABI_VERSION 8
 
 /* status codes */
 #define MM_OK 0
@@ -293,15 +293,15 @@ int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stri
  *   g' = -exp(A_log[h]) * softplus(g + dt_bias[h]) (lower_bound NaN) or lower_bound * sigmoid(exp(A_log[h]) * (g + dt_bias))
  *        when use_gate, else g' = g (already a log decay)
  *   S = S * exp(g')[:, None]; u = beta * (v - S^T k); S = S + k u^T; o = S^T q   (S [K, V])
- * q, k [T, H, K] bf16, v [T, H, V] bf16, g [T, H, K] (MM_BF16 / MM_FP32), beta [T, H] (MM_BF16 / MM_FP32; already the
- * sigmoid of the projection), each with its token stride in elements; A_log [H], dt_bias [H * K] fp32 (used when
+ * q, k [T, H, K] bf16, v [T, H, V] bf16, g [T, H, K] (MM_BF16 / MM_FP32), beta [T, H] (MM_BF16 / MM_FP32; the write
+ * strength, or with beta_logits the projection whose sigmoid it is), each with its token stride in elements; A_log [H], dt_bias [H * K] fp32 (used when
  * use_gate); state [H, K, V] fp32, read and updated in place; o [T, H, V] bf16 (token stride o_ts).
- * K and V: 64 or 128. */
+ * K: 64 or 128; V: a multiple of 16 up to 4096. */
 int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                      const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
                      const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm, int use_gate,
-                     float scale, int64_t T, int64_t H, int64_t K, int64_t V, float* state, void* o, int64_t o_ts,
-                     void* stream);
+                     int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V, float* state, void* o,
+                     int64_t o_ts, void* stream);
 
 /* Depthwise causal convolution over time, the step form of fla's ShortConvolution (the q / k / v convolutions of a
  * KDA layer, engine.py:247-249, caches engine.py:645-647): per channel, for each of T tokens in order, the window
@@ -317,15 +317,16 @@ int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache
 int mm_rms_norm_gated(const void* x, int64_t x_rs, const void* g, int64_t g_rs, const void* w, int64_t rows, int64_t n,
                       float eps, void* y, int64_t y_rs, void* stream);
 
-/* Bytes of fp32 workspace mm_mla_decode_attn needs: nh * ceil(max_len / 64) * (dv + 2) * 4 (0 if invalid). */
+/* Bytes of fp32 workspace mm_mla_decode_attn needs: nh * ceil(max_len / 32) * (dv + 2) * 4 (0 if invalid). */
 int64_t mm_mla_attn_workspace(int nh, int dv, int64_t max_len);
 
 /* Single-token attention of an MLA layer over its static cache (the StaticHybridCache update and the masked
  * attention of engine.py:537-548, 679-686): k_new / v_new are written at row pos of k_cache [nh, max_len, dqk] and
  * v_cache [nh, max_len, dv] (bf16), then out[h] = softmax(scale * q[h] . K[h, 0..pos]^T) . V[h, 0..pos] in fp32,
  * rounded to bf16. q, k_new [nh, dqk], v_new [nh, dv], out [nh, dv] bf16; pos a device scalar (MM_INT64 /
- * MM_INT32). A pos outside [0, max_len) writes nothing to the caches and sets out to NaN. dqk a multiple of 32 up
- * to 512, dv up to 256. workspace: at least mm_mla_attn_workspace(nh, dv, max_len) bytes, 16-byte aligned. */
+ * MM_INT32). A pos outside [0, max_len) writes nothing to the caches and sets out to NaN. dqk a multiple of 8 up
+ * to 512, dv a multiple of 8 up to 256; rows past pos are never read. q, k_new, v_new, the caches and the
+ * workspace (at least mm_mla_attn_workspace(nh, dv, max_len) bytes) 16-byte aligned. */
 int mm_mla_decode_attn(const void* q, const void* k_new, const void* v_new, int nh, int dqk, int dv, void* k_cache,
                        void* v_cache, int64_t max_len, const void* pos, int pos_dtype, float scale, void* out,
                        void* workspace, int64_t workspace_bytes, void* stream);

@@ -3,9 +3,9 @@
 //   kda_recurrent_kernel   Kimi delta attention, the recurrent form fla's fused_recurrent_kda computes (called at
 //                          engine.py:258 and inside the model's KDA layers): per head a [K, V] fp32 state, per token
 //                          q, k l2-normalised (q scaled), a per-key-channel decay exp(g) from the gate, the delta
-//                          rule update and the readout. One workgroup per head holds the state in registers for
-//                          all T tokens: thread (kg, c) keeps rows kg*K/4 .. of column c; the sums over k go
-//                          through LDS in a fixed order.
+//                          rule update and the readout. A workgroup holds 16 value columns of one head's state in
+//                          registers for all T tokens (the columns are independent); the sums over k go through
+//                          lanes, then LDS, in a fixed order.
 //   short_conv_kernel      the depthwise causal convolution of ShortConvolution's step form (a cache of the last W
 //                          inputs per channel), SiLU, T tokens in order.
 //   rms_norm_gated_kernel  FusedRMSNormGated with a sigmoid gate: bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)).
@@ -13,7 +13,7 @@
 //                          single-token attention of an MLA layer over its static cache (engine.py:523-548: k, v
 //                          [heads, max_len, d], rows written at the position with index_copy_): the new k, v rows
 //                          are stored at pos, then softmax(scale q . K[0..pos]^T) . V[0..pos] in two passes
-//                          (64-position chunks, then a merge of the chunks' softmax states), all in fp32.
+//                          (32-position chunks, then a merge of the chunks' softmax states), all in fp32.
 #include "mm_common.h"
 
 namespace {
@@ -33,12 +33,12 @@ struct KdaArgs {
   const float* A_log;                      // [H]
   const float* dt_bias;                    // [H * K]
   float lower_bound;                       // NaN: the softplus gate
-  int use_l2norm, use_gate;
+  int use_l2norm, use_gate, beta_logits;
   float scale;
   float* state;                            // [H, K, V] fp32, updated in place
   uint16_t* o;                             // [T, H, V] bf16
   int64_t o_ts;
-  int T, H;
+  int T, H, V;
 };
 
 __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
@@ -48,91 +48,105 @@ __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
 // softplus with the usual threshold: x above 20 returns x
 __device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-// One workgroup of 4 * V threads per head; thread (kg = tid / V, c = tid % V) holds state rows kg * RK .. + RK - 1
-// of column c, RK = K / 4.
-template <int K, int V>
-__global__ __launch_bounds__(4 * V) void kda_recurrent_kernel(KdaArgs a) {
-  constexpr int RK = K / 4;
-  constexpr int NT = 4 * V;
-  __shared__ float red_q[4], red_k[4];
-  __shared__ float part_u[4][V], part_o[4][V];
-  const int h = blockIdx.x;
-  const int tid = threadIdx.x, c = tid % V, kg = tid / V;
-  const int r0 = kg * RK;
-  float* st = a.state + static_cast<int64_t>(h) * K * V;
-  float S[RK];
+constexpr int kKdaCols = 16;  // value columns per workgroup: 16 lanes read a 64-byte segment of a state row
+
+// Grid (V / 16, H) x 256 threads: each value column of the recurrence is independent (u and o of column v read
+// only column v of S), so a head's columns spread over V / 16 workgroups. Wave w, lane (rg = lane / 16,
+// c = lane % 16) holds state rows r = 16 i + 4 w + rg (i < K / 16) of column 16 * blockIdx.x + c: one load of a
+// wave reads 4 rows x 64 bytes. Per token the first K threads (whole waves) put each key channel's q, k and decay
+// into LDS, once for the workgroup, with the sums of q^2 and k^2. Sums over rows: lane-internal, then over the
+// 4 row groups of a wave (xor 16, then 32), then over the 4 waves through LDS, in a fixed order.
+template <int K>
+__global__ __launch_bounds__(256) void kda_recurrent_kernel(KdaArgs a) {
+  constexpr int CB = kKdaCols, RPT = K / 16;
+  static_assert(K % kWave == 0 && K <= 256, "kda key dim");
+  __shared__ float s_q[K], s_k[K], s_dec[K];
+  __shared__ float s_red[K / kWave][2];
+  __shared__ float part_u[4][CB], part_o[4][CB];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
+  const int c = lane % CB, rg = lane / CB;
+  const int64_t V = a.V;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col;
+  float S[RPT];
 #pragma unroll
-  for (int i = 0; i < RK; ++i) S[i] = st[static_cast<int64_t>(r0 + i) * V + c];
-  float nA = 0.f, dtb[RK];
+  for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
+  const bool chan = tid < K;  // whole waves
+  float nA = 0.f, dtb = 0.f;
   if (a.use_gate) {
     nA = __expf(a.A_log[h]);
-#pragma unroll
-    for (int i = 0; i < RK; ++i) dtb[i] = a.dt_bias[static_cast<int64_t>(h) * K + r0 + i];
+    if (chan) dtb = a.dt_bias[static_cast<int64_t>(h) * K + tid];
   }
   for (int t = 0; t < a.T; ++t) {
-    float qv[RK], kv[RK], gv[RK];
-    const uint16_t* qp = a.q + t * a.q_ts + static_cast<int64_t>(h) * K + r0;
-    const uint16_t* kp = a.k + t * a.k_ts + static_cast<int64_t>(h) * K + r0;
-#pragma unroll
-    for (int i = 0; i < RK; ++i) {
-      qv[i] = bf16_to_f32(qp[i]);
-      kv[i] = bf16_to_f32(kp[i]);
-      gv[i] = ld_any(a.g, a.g_dtype, t * a.g_ts + static_cast<int64_t>(h) * K + r0 + i);
-    }
-    const float vc = bf16_to_f32(a.v[t * a.v_ts + static_cast<int64_t>(h) * V + c]);
-    const float beta = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
-    float sq = 0.f, sk = 0.f;
-    if (a.use_l2norm) {
-#pragma unroll
-      for (int i = 0; i < RK; ++i) {
-        sq = fmaf(qv[i], qv[i], sq);
-        sk = fmaf(kv[i], kv[i], sk);
+    if (chan) {
+      const int64_t i = static_cast<int64_t>(h) * K + tid;
+      const float qv = bf16_to_f32(a.q[t * a.q_ts + i]);
+      const float kv = bf16_to_f32(a.k[t * a.k_ts + i]);
+      float gl = ld_any(a.g, a.g_dtype, t * a.g_ts + i);
+      if (a.use_gate) {
+        const float x = gl + dtb;
+        gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
       }
-      if (c == 0) {
-        red_q[kg] = sq;
-        red_k[kg] = sk;
+      s_q[tid] = qv;
+      s_k[tid] = kv;
+      s_dec[tid] = __expf(gl);
+      if (a.use_l2norm) {
+        const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+        if (lane == 0) {
+          s_red[w][0] = sq;
+          s_red[w][1] = sk;
+        }
       }
     }
+    const float vc = bf16_to_f32(a.v[t * a.v_ts + static_cast<int64_t>(h) * V + col]);
+    float beta = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
+    if (a.beta_logits) beta = 1.f / (1.f + __expf(-beta));
     __syncthreads();
     float qs = a.scale, ks = 1.f;
     if (a.use_l2norm) {
-      qs = a.scale / sqrtf(((red_q[0] + red_q[1]) + red_q[2]) + red_q[3] + 1e-6f);
-      ks = 1.f / sqrtf(((red_k[0] + red_k[1]) + red_k[2]) + red_k[3] + 1e-6f);
+      float sq = s_red[0][0], sk = s_red[0][1];
+#pragma unroll
+      for (int j = 1; j < K / kWave; ++j) {
+        sq += s_red[j][0];
+        sk += s_red[j][1];
+      }
+      qs = a.scale / sqrtf(sq + 1e-6f);
+      ks = 1.f / sqrtf(sk + 1e-6f);
     }
     // decay, then the part of v the state already predicts from k
     float pu = 0.f;
 #pragma unroll
-    for (int i = 0; i < RK; ++i) {
-      float gl = gv[i];
-      if (a.use_gate) {
-        const float x = gl + dtb[i];
-        gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
-      }
-      S[i] *= __expf(gl);
-      kv[i] *= ks;
-      pu = fmaf(kv[i], S[i], pu);
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w + rg;
+      S[i] *= s_dec[r];
+      pu = fmaf(s_k[r] * ks, S[i], pu);
     }
-    part_u[kg][c] = pu;
+    pu += __shfl_xor(pu, 16, kWave);
+    pu += __shfl_xor(pu, 32, kWave);
+    if (rg == 0) part_u[w][c] = pu;
     __syncthreads();
     const float u = (vc - (((part_u[0][c] + part_u[1][c]) + part_u[2][c]) + part_u[3][c])) * beta;
     float po = 0.f;
 #pragma unroll
-    for (int i = 0; i < RK; ++i) {
-      S[i] = fmaf(kv[i], u, S[i]);
-      po = fmaf(qv[i] * qs, S[i], po);
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w + rg;
+      S[i] = fmaf(s_k[r] * ks, u, S[i]);
+      po = fmaf(s_q[r] * qs, S[i], po);
     }
-    part_o[kg][c] = po;
+    po += __shfl_xor(po, 16, kWave);
+    po += __shfl_xor(po, 32, kWave);
+    if (rg == 0) part_o[w][c] = po;
+    // the next token rewrites s_* after this barrier, when every thread has read them; part_u / part_o are
+    // rewritten after the next token's first and second barriers, when wave 0 has read them
     __syncthreads();
-    if (kg == 0) {
+    if (w == 0 && rg == 0) {
       const float o = ((part_o[0][c] + part_o[1][c]) + part_o[2][c]) + part_o[3][c];
-      a.o[t * a.o_ts + static_cast<int64_t>(h) * V + c] = f32_to_bf16(o);
+      a.o[t * a.o_ts + static_cast<int64_t>(h) * V + col] = f32_to_bf16(o);
     }
-    // the next token's partials reuse red_* / part_*: every thread has read them before this barrier's end
-    __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < RK; ++i) st[static_cast<int64_t>(r0 + i) * V + c] = S[i];
-  static_assert(NT <= 1024 && K % 4 == 0, "kda shape");
+  for (int i = 0; i < RPT; ++i) st[static_cast<int64_t>(16 * i + 4 * w + rg) * V] = S[i];
 }
 
 // ----------------------------------------------------------------------------------------- short conv
@@ -197,7 +211,7 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
 
 // ------------------------------------------------------------------------------------ MLA decode attention
 
-constexpr int kMlaChunk = 64;  // positions per workgroup: 4 waves of 16
+constexpr int kMlaChunk = 32;  // positions per workgroup: 4 waves of 8
 
 struct MlaArgs {
   const uint16_t* q;      // [nh, dqk]
@@ -219,124 +233,160 @@ __device__ __forceinline__ int64_t load_pos64(const void* p, int dt) {
   return dt == MM_INT64 ? *static_cast<const int64_t*>(p) : static_cast<int64_t>(*static_cast<const int32_t*>(p));
 }
 
-// Grid (chunks, heads) x 4 waves. Wave w scores positions t0 .. t0+15 (t0 = chunk * 64 + 16 w): 4 lanes per
-// position, each a quarter of the q . k dot (dqk / 4 elements, 16-byte loads), reduced over the 4 lanes; the new
-// row stands in for row pos (it is also stored there, by the wave that holds pos). Softmax over the chunk, then
-// lane = value dimension for p . V.
-template <int DQ4, int NDV>
+__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// Grid (chunks, heads) x 4 waves; wave w owns positions t0 .. t0 + 7 (t0 = 32 chunk + 8 w), the new row standing
+// in for row pos (and stored there by the wave that holds pos). First every lane issues its loads of the wave's
+// value rows (LPR lanes x 8 dims per row, 64 / LPR rows per load), then the scores: 8 lanes per position, lane
+// part taking the 16-byte pieces part, part + 8, ... of the q . k dot (KP of them at most), summed over the
+// 8 lanes. Softmax over the chunk (a max over the 4 waves through LDS), p . V in the lanes' 8 dims, summed over
+// a wave's row groups, then over the 4 waves in LDS; wave 0 writes the chunk's [dv] sums, max and sum of p.
+template <int KP, int LPR>
 __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
-  __shared__ float sp[4][16];
-  __shared__ float sm[4], sl[4];
-  __shared__ float sacc[4][64 * NDV];
+  constexpr int RPL = kWave / LPR;  // value rows per load
+  constexpr int VI = 8 / RPL;       // loads covering a wave's 8 positions
+  __shared__ float s_sc[kMlaChunk], s_max[4], s_l[4];
+  __shared__ float s_acc[4][8 * LPR];
   const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int h = blockIdx.y, chunk = blockIdx.x;
   const int64_t pos = load_pos64(a.pos, a.pos_dtype);
   const int64_t c0 = static_cast<int64_t>(chunk) * kMlaChunk;
   if (pos < 0 || pos >= a.max_len || c0 > pos) return;  // uniform over the workgroup
-  const int64_t t0 = c0 + wave * 16;
-  const int tl = lane / 4, qd = lane % 4;  // position t0 + tl, quarter qd of the dims
-  const int64_t t = t0 + tl;
-  const int dq4 = a.dqk / 4;               // elements per quarter (a multiple of 8)
-  const uint16_t* qrow = a.q + static_cast<int64_t>(h) * a.dqk + qd * dq4;
-  const bool is_new = t == pos;
-  const uint16_t* krow = is_new ? a.k_new + static_cast<int64_t>(h) * a.dqk + qd * dq4
-                                : a.kc + (static_cast<int64_t>(h) * a.max_len + min(t, a.max_len - 1)) * a.dqk + qd * dq4;
+  const int64_t t0 = c0 + wave * 8;
+  const int64_t hk = static_cast<int64_t>(h) * a.max_len;
+  // value rows t0 + vr + RPL i, dims 8 vd .. 8 vd + 7; rows past pos are not read (zeros: the cache there may
+  // hold anything, and 0 * NaN would poison the sums)
+  const int vr = lane / LPR, vd = lane % LPR;
+  const bool vdim = vd * 8 < a.dv;
+  uint4 vv[VI];
+#pragma unroll
+  for (int i = 0; i < VI; ++i) {
+    const int64_t tt = t0 + vr + RPL * i;
+    const uint16_t* row = tt == pos ? a.v_new + static_cast<int64_t>(h) * a.dv : a.vc + (hk + tt) * a.dv;
+    vv[i] = vdim && tt <= pos ? *reinterpret_cast<const uint4*>(row + vd * 8) : make_uint4(0, 0, 0, 0);
+  }
+  // scores: position t0 + sp, pieces part + 8 j (rows past pos are not read)
+  const int sp = lane / 8, part = lane % 8;
+  const int64_t t = t0 + sp;
+  const int np = t <= pos ? a.dqk / 8 : 0;
+  const uint16_t* krow = t == pos ? a.k_new + static_cast<int64_t>(h) * a.dqk : a.kc + (hk + t) * a.dqk;
+  const uint16_t* qrow = a.q + static_cast<int64_t>(h) * a.dqk;
+  uint4 kb[KP], qa[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    const int pc = part + 8 * j;
+    if (pc < np) {
+      kb[j] = *reinterpret_cast<const uint4*>(krow + pc * 8);
+      qa[j] = *reinterpret_cast<const uint4*>(qrow + pc * 8);
+    }
+  }
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < DQ4; ++j) {
-    if (j * 8 < dq4) {
-      const uint4 qa = *reinterpret_cast<const uint4*>(qrow + j * 8);
-      const uint4 kb = *reinterpret_cast<const uint4*>(krow + j * 8);
-      s = dot8_bf16(kb, qa, s);
-    }
-  }
-  s += __shfl_xor(s, 1, kWave);
-  s += __shfl_xor(s, 2, kWave);
-  const bool valid = t <= pos;
-  const float sc = valid ? s * a.scale : -INFINITY;
-  if (qd == 0) sp[wave][tl] = sc;
+  for (int j = 0; j < KP; ++j)
+    if (part + 8 * j < np) s = dot8_bf16(kb[j], qa[j], s);
+  s += dpp_f32<kDppXor1>(s);
+  s += dpp_f32<kDppXor2>(s);
+  s += dpp_f32<kDppHalfMirror>(s);
+  const float sc = t <= pos ? s * a.scale : -INFINITY;
+  const float wm = wave_max(sc);
+  if (part == 0) s_sc[wave * 8 + sp] = sc;
+  if (lane == 0) s_max[wave] = wm;
   // the wave holding pos stores the new rows into the cache
-  if (pos >= t0 && pos < t0 + 16) {
-    uint16_t* kd = a.kc + (static_cast<int64_t>(h) * a.max_len + pos) * a.dqk;
-    uint16_t* vd = a.vc + (static_cast<int64_t>(h) * a.max_len + pos) * a.dv;
+  if (pos >= t0 && pos < t0 + 8) {
+    uint16_t* kd = a.kc + (hk + pos) * a.dqk;
+    uint16_t* vd_ = a.vc + (hk + pos) * a.dv;
     for (int i = lane; i < a.dqk; i += kWave) kd[i] = a.k_new[static_cast<int64_t>(h) * a.dqk + i];
-    for (int i = lane; i < a.dv; i += kWave) vd[i] = a.v_new[static_cast<int64_t>(h) * a.dv + i];
+    for (int i = lane; i < a.dv; i += kWave) vd_[i] = a.v_new[static_cast<int64_t>(h) * a.dv + i];
   }
   __syncthreads();
-  // chunk softmax state (every wave computes the same max and sum from LDS)
-  float m = -INFINITY;
-  for (int i = 0; i < 64; ++i) m = fmaxf(m, sp[i / 16][i % 16]);  // finite: position c0 <= pos is valid
-  // p . V over the wave's 16 positions, lane = value dimension
-  float acc[NDV], lsum = 0.f;
+  const float m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));  // finite: c0 <= pos is valid
+  float acc[8];
 #pragma unroll
-  for (int j = 0; j < NDV; ++j) acc[j] = 0.f;
-  for (int i = 0; i < 16; ++i) {
-    const int64_t tt = t0 + i;
-    const float p = tt <= pos ? __expf(sp[wave][i] - m) : 0.f;
-    lsum += p;
-    const uint16_t* vrow = tt == pos ? a.v_new + static_cast<int64_t>(h) * a.dv
-                                     : a.vc + (static_cast<int64_t>(h) * a.max_len + min(tt, a.max_len - 1)) * a.dv;
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NDV; ++j) {
-      const int d = lane + kWave * j;
-      if (d < a.dv && p != 0.f) acc[j] = fmaf(p, bf16_to_f32(vrow[d]), acc[j]);
+  for (int i = 0; i < VI; ++i) {
+    const int r = vr + RPL * i;
+    const float p = t0 + r <= pos ? __expf(s_sc[wave * 8 + r] - m) : 0.f;
+    const uint32_t x[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] = fmaf(p, bf_lo(x[e]), acc[2 * e]);
+      acc[2 * e + 1] = fmaf(p, bf_hi(x[e]), acc[2 * e + 1]);
     }
   }
 #pragma unroll
-  for (int j = 0; j < NDV; ++j) sacc[wave][lane + kWave * j] = acc[j];
-  if (lane == 0) sl[wave] = lsum;
-  if (lane == 0) sm[wave] = m;
+  for (int off = LPR; off < kWave; off *= 2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], off, kWave);
+  if (lane < LPR && vdim) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_acc[wave][vd * 8 + e] = acc[e];
+  }
+  // the wave's sum of p: lane i < 8 for position t0 + i
+  const float pl = lane < 8 && t0 + lane <= pos ? __expf(s_sc[wave * 8 + lane] - m) : 0.f;
+  const float lsum = wave_sum(pl);
+  if (lane == 0) s_l[wave] = lsum;
   __syncthreads();
   if (wave != 0) return;
   float* dst = a.ws + (static_cast<int64_t>(h) * a.nc + chunk) * (a.dv + 2);
-#pragma unroll
-  for (int j = 0; j < NDV; ++j) {
-    const int d = lane + kWave * j;
-    if (d < a.dv) dst[d] = ((sacc[0][d] + sacc[1][d]) + sacc[2][d]) + sacc[3][d];
-  }
+  for (int d = lane; d < a.dv; d += kWave) dst[d] = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
   if (lane == 0) {
     dst[a.dv] = m;
-    dst[a.dv + 1] = ((sl[0] + sl[1]) + sl[2]) + sl[3];
+    dst[a.dv + 1] = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
   }
 }
 
-// One wave per head: merges the chunks 0 .. pos / 64 (max of the maxima, rescaled sums) and writes bf16.
+// One workgroup of 4 waves per head merges the chunks 0 .. pos / 32: the max of the maxima (lanes over chunks),
+// then wave w rescales and sums chunks w, w + 4, ... (lane = value dimension), the 4 waves' sums added in LDS.
 // A position outside [0, max_len) writes NaN (and the split kernel wrote nothing).
 template <int NDV>
-__global__ __launch_bounds__(64) void mla_merge_kernel(MlaArgs a) {
-  const int h = blockIdx.x, lane = lane_id();
+__global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
+  __shared__ float s_acc[4][kWave * NDV], s_l[4], s_m[4];
+  const int h = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int64_t pos = load_pos64(a.pos, a.pos_dtype);
   if (pos < 0 || pos >= a.max_len) {
-    for (int d = lane; d < a.dv; d += kWave) a.out[static_cast<int64_t>(h) * a.dv + d] = 0x7fc0;  // NaN
+    for (int d = tid; d < a.dv; d += 256) a.out[static_cast<int64_t>(h) * a.dv + d] = 0x7fc0;  // NaN
     return;
   }
   const int n = static_cast<int>(pos / kMlaChunk) + 1;
-  const float* base = a.ws + static_cast<int64_t>(h) * a.nc * (a.dv + 2);
-  float m = -INFINITY;
-  for (int c = 0; c < n; ++c) m = fmaxf(m, base[static_cast<int64_t>(c) * (a.dv + 2) + a.dv]);
+  const int64_t cs = a.dv + 2;
+  const float* base = a.ws + static_cast<int64_t>(h) * a.nc * cs;
+  float mx = -INFINITY;
+  for (int c = tid; c < n; c += 256) mx = fmaxf(mx, base[c * cs + a.dv]);
+  mx = wave_max(mx);
+  if (lane == 0) s_m[wave] = mx;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
   float acc[NDV], l = 0.f;
 #pragma unroll
   for (int j = 0; j < NDV; ++j) acc[j] = 0.f;
-  for (int c = 0; c < n; ++c) {
-    const float* p = base + static_cast<int64_t>(c) * (a.dv + 2);
-    const float w = __expf(p[a.dv] - m);
-    l = fmaf(p[a.dv + 1], w, l);
+#pragma unroll 4
+  for (int c = wave; c < n; c += 4) {
+    const float* p = base + c * cs;
+    const float wgt = __expf(p[a.dv] - m);
+    l = fmaf(p[a.dv + 1], wgt, l);
 #pragma unroll
     for (int j = 0; j < NDV; ++j) {
       const int d = lane + kWave * j;
-      if (d < a.dv) acc[j] = fmaf(p[d], w, acc[j]);
+      if (d < a.dv) acc[j] = fmaf(p[d], wgt, acc[j]);
     }
   }
 #pragma unroll
-  for (int j = 0; j < NDV; ++j) {
-    const int d = lane + kWave * j;
-    if (d < a.dv) a.out[static_cast<int64_t>(h) * a.dv + d] = f32_to_bf16(acc[j] / l);
+  for (int j = 0; j < NDV; ++j) s_acc[wave][lane + kWave * j] = acc[j];
+  if (lane == 0) s_l[wave] = l;
+  __syncthreads();
+  const float lt = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
+  for (int d = tid; d < a.dv; d += 256) {
+    const float o = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
+    a.out[static_cast<int64_t>(h) * a.dv + d] = f32_to_bf16(o / lt);
   }
 }
 
-template <int K, int V>
+template <int K>
 int launch_kda(const KdaArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((kda_recurrent_kernel<K, V>), dim3(static_cast<unsigned>(a.H)), dim3(4 * V), 0, st, a);
+  hipLaunchKernelGGL((kda_recurrent_kernel<K>), dim3(static_cast<unsigned>(a.V / kKdaCols), static_cast<unsigned>(a.H)),
+                     dim3(256), 0, st, a);
   return mm::check_launch("kda_recurrent");
 }
 
@@ -345,13 +395,14 @@ int launch_kda(const KdaArgs& a, hipStream_t st) {
 extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                                 const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
                                 int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound,
-                                int use_qk_l2norm, int use_gate, float scale, int64_t T, int64_t H, int64_t K,
-                                int64_t V, float* state, void* o, int64_t o_ts, void* stream) {
+                                int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
+                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, void* stream) {
   MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535, "kda_recurrent: bad T=%lld or H=%lld", (long long)T,
              (long long)H);
-  // a thread holds K / 4 floats each of state, q, k, g and dt_bias; 4 V threads per workgroup
-  MM_REQUIRE((K == 64 || K == 128) && (V == 64 || V == 128), "kda_recurrent: head dims K=%lld, V=%lld must be 64 or 128",
-             (long long)K, (long long)V);
+  // a thread holds K / 16 state values; workgroups of 16 value columns
+  MM_REQUIRE((K == 64 || K == 128) && V % kKdaCols == 0 && V >= kKdaCols && V <= 4096,
+             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 16 up to 4096)", (long long)K,
+             (long long)V);
   MM_REQUIRE(g_dtype == MM_BF16 || g_dtype == MM_FP32, "kda_recurrent: g must be bf16 or fp32");
   MM_REQUIRE(beta_dtype == MM_BF16 || beta_dtype == MM_FP32, "kda_recurrent: beta must be bf16 or fp32");
   MM_REQUIRE(q && k && v && g && beta && state && o, "kda_recurrent: null pointer");
@@ -377,18 +428,16 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
   a.lower_bound = lower_bound;
   a.use_l2norm = use_qk_l2norm;
   a.use_gate = use_gate;
+  a.beta_logits = beta_logits;
   a.scale = scale;
   a.state = state;
   a.o = static_cast<uint16_t*>(o);
   a.o_ts = o_ts;
   a.T = static_cast<int>(T);
   a.H = static_cast<int>(H);
+  a.V = static_cast<int>(V);
   hipStream_t st = MM_STREAM(stream);
-  if (K == 64 && V == 64) return launch_kda<64, 64>(a, st);
-  if (K == 64 && V == 128) return launch_kda<64, 128>(a, st);
-  if (K == 128 && V == 64) return launch_kda<128, 64>(a, st);
-  if (K == 128 && V == 128) return launch_kda<128, 128>(a, st);
-  return mm::set_error(MM_ERR_ARG, "kda_recurrent: K=%lld, V=%lld not instantiated", (long long)K, (long long)V);
+  return K == 64 ? launch_kda<64>(a, st) : launch_kda<128>(a, st);
 }
 
 extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
@@ -438,13 +487,14 @@ extern "C" int mm_mla_decode_attn(const void* q, const void* k_new, const void* 
                                   void* k_cache, void* v_cache, int64_t max_len, const void* pos, int pos_dtype,
                                   float scale, void* out, void* workspace, int64_t workspace_bytes, void* stream) {
   MM_REQUIRE(nh >= 1 && nh <= 65535 && max_len >= 1 && max_len <= (1LL << 24), "mla_decode_attn: bad nh or max_len");
-  MM_REQUIRE(dqk % 32 == 0 && dqk >= 32 && dqk <= 512, "mla_decode_attn: dqk=%d must be a multiple of 32 in [32, 512]",
+  MM_REQUIRE(dqk % 8 == 0 && dqk >= 8 && dqk <= 512, "mla_decode_attn: dqk=%d must be a multiple of 8 in [8, 512]",
              dqk);
-  MM_REQUIRE(dv >= 1 && dv <= 256, "mla_decode_attn: dv=%d must be in [1, 256]", dv);
+  MM_REQUIRE(dv % 8 == 0 && dv >= 8 && dv <= 256, "mla_decode_attn: dv=%d must be a multiple of 8 in [8, 256]", dv);
   MM_REQUIRE(pos_dtype == MM_INT64 || pos_dtype == MM_INT32, "mla_decode_attn: pos must be int64 or int32");
   MM_REQUIRE(q && k_new && v_new && k_cache && v_cache && pos && out && workspace, "mla_decode_attn: null pointer");
-  MM_REQUIRE(mm::aligned16(q) && mm::aligned16(k_new) && mm::aligned16(k_cache) && mm::aligned16(workspace),
-             "mla_decode_attn: q, k_new, k_cache and the workspace must be 16-byte aligned");
+  MM_REQUIRE(mm::aligned16(q) && mm::aligned16(k_new) && mm::aligned16(v_new) && mm::aligned16(k_cache) &&
+                 mm::aligned16(v_cache) && mm::aligned16(workspace),
+             "mla_decode_attn: q, k_new, v_new, the caches and the workspace must be 16-byte aligned");
   MM_REQUIRE(workspace_bytes >= mm_mla_attn_workspace(nh, dv, max_len), "mla_decode_attn: workspace too small");
   MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -464,15 +514,21 @@ extern "C" int mm_mla_decode_attn(const void* q, const void* k_new, const void* 
   a.out = static_cast<uint16_t*>(out);
   hipStream_t st = MM_STREAM(stream);
   dim3 grid(static_cast<unsigned>(a.nc), static_cast<unsigned>(nh));
-  const int dq4 = dqk / 4;  // 16-byte pieces per quarter: dq4 / 8
-  if (dq4 <= 8 * 2 && dv <= 64) hipLaunchKernelGGL((mla_split_kernel<2, 1>), grid, dim3(256), 0, st, a);
-  else if (dq4 <= 8 * 2) hipLaunchKernelGGL((mla_split_kernel<2, 4>), grid, dim3(256), 0, st, a);
-  else if (dv <= 128) hipLaunchKernelGGL((mla_split_kernel<16, 2>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((mla_split_kernel<16, 4>), grid, dim3(256), 0, st, a);
+  const int kp = (dqk / 8 + 7) / 8;  // 16-byte pieces of a k row per lane, 8 lanes per position
+  if (dv <= 128) {
+    if (kp <= 1) hipLaunchKernelGGL((mla_split_kernel<1, 16>), grid, dim3(256), 0, st, a);
+    else if (kp <= 2) hipLaunchKernelGGL((mla_split_kernel<2, 16>), grid, dim3(256), 0, st, a);
+    else if (kp <= 4) hipLaunchKernelGGL((mla_split_kernel<4, 16>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((mla_split_kernel<8, 16>), grid, dim3(256), 0, st, a);
+  } else {
+    if (kp <= 2) hipLaunchKernelGGL((mla_split_kernel<2, 32>), grid, dim3(256), 0, st, a);
+    else if (kp <= 4) hipLaunchKernelGGL((mla_split_kernel<4, 32>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((mla_split_kernel<8, 32>), grid, dim3(256), 0, st, a);
+  }
   int rc = mm::check_launch("mla_decode_attn split");
   if (rc) return rc;
-  if (dv <= 64) hipLaunchKernelGGL(mla_merge_kernel<1>, dim3(static_cast<unsigned>(nh)), dim3(64), 0, st, a);
-  else if (dv <= 128) hipLaunchKernelGGL(mla_merge_kernel<2>, dim3(static_cast<unsigned>(nh)), dim3(64), 0, st, a);
-  else hipLaunchKernelGGL(mla_merge_kernel<4>, dim3(static_cast<unsigned>(nh)), dim3(64), 0, st, a);
+  if (dv <= 64) hipLaunchKernelGGL(mla_merge_kernel<1>, dim3(static_cast<unsigned>(nh)), dim3(256), 0, st, a);
+  else if (dv <= 128) hipLaunchKernelGGL(mla_merge_kernel<2>, dim3(static_cast<unsigned>(nh)), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(mla_merge_kernel<4>, dim3(static_cast<unsigned>(nh)), dim3(256), 0, st, a);
   return mm::check_launch("mla_decode_attn merge");
 }

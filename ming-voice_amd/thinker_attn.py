@@ -39,11 +39,12 @@ def _tokens(t, name, H, D):
 
 def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
                         output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
-                        lower_bound=None, inplace=False, out=None, **unused):
+                        lower_bound=None, inplace=False, out=None, beta_is_logits=False, **unused):
     """q, k [1, T, H, K] bf16; v [1, T, H, V] bf16; g [1, T, H, K] (bf16 / fp32; the raw gate projection when
     use_gate_in_kernel, else a log decay); beta [1, T, H] (fp32 / bf16); A_log [H], dt_bias [H * K] (or [H, K]);
     initial_state [1, H, K, V] fp32 (zeros when None). Returns (o [1, T, H, V] bf16, final_state or None).
-    scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor)."""
+    scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor);
+    beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel."""
     _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out)
     if q.dim() != 4 or q.shape[0] != 1:
         raise ValueError(f"fused_recurrent_kda: q must be [1, T, H, K] (got {tuple(q.shape)})")
@@ -89,7 +90,8 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     with _mm.on_device(q):
         _mm.check(lib.mm_kda_recurrent(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts,
                                        _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,
-                                       1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0, sc, T, H, K, V,
+                                       1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0,
+                                       1 if beta_is_logits else 0, sc, T, H, K, V,
                                        _mm.ptr(state), _mm.ptr(o), o.stride(0), _mm.stream_of(q)), "fused_recurrent_kda")
     final = None
     if output_final_state or inplace:
@@ -146,6 +148,12 @@ def rms_norm_gated(x, g, weight, eps=1e-5, out=None):
     return y.reshape(x.shape)
 
 
+def _aligned16(t):
+    """t contiguous at a 16-byte aligned address (a copy when a view is not)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def mla_attn_workspace(nh, dv, max_len, device):
     n = int(_mm.load().mm_mla_attn_workspace(int(nh), int(dv), int(max_len)))
     return torch.empty(max(n // 4, 1), device=device, dtype=torch.float32)
@@ -161,9 +169,7 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None
     dv = v_cache.shape[-1]
     if tuple(v_cache.shape[-3:-1]) != (nh, max_len) or not k_cache.is_contiguous() or not v_cache.is_contiguous():
         raise ValueError("mla_decode_attn: caches must be contiguous [1, nh, max_len, d]")
-    qf = q.reshape(nh, dqk).contiguous()
-    kf = k_new.reshape(nh, dqk).contiguous()
-    vf = v_new.reshape(nh, dv).contiguous()
+    qf, kf, vf = (_aligned16(t.reshape(nh, d)) for t, d in ((q, dqk), (k_new, dqk), (v_new, dv)))
     for name, t in (("q", qf), ("k_new", kf), ("v_new", vf), ("k_cache", k_cache), ("v_cache", v_cache)):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"mla_decode_attn: {name} must be bf16")

@@ -15,6 +15,7 @@ one device and copies.
   expert_tensors, write_checkpoint   a layer's experts in the checkpoint key layout, as safetensors shards
   thinker_layer(...)    one synthetic thinker layer (q|k|v and o projections + MoE block)
   ThinkerDecodeStep     the synthetic 28-layer thinker decode step + LM head (one token)
+  HybridThinkerStep     the same with the thinker's KDA / MLA attention mixers between the projections
   TalkerLLM(...)        a synthetic Qwen2 Talker LLM with StaticQwen2's attributes and KV cache layout
   TalkerTail(...)       a synthetic Talker (DiT + aggregator + stop head) with the attributes FastTail reads
 """
@@ -194,14 +195,17 @@ class ThinkerDecodeStep:
         self.wts = torch.empty(1, TOP_K + 1, device=device)
         self.a_buf = torch.empty(TOP_K + 1, INTER, device=device, dtype=torch.bfloat16)
 
-    def layer(self, p, h):
-        from fastlinear import small_linear
+    def layer_moe(self, b, h):
+        """The MoE block of a layer on h (its norm, router, experts and the residual add), router buffers shared."""
         from fused_moe import moe_block_decode
-        qkv = small_linear(h, p["qkv"], norm=(p["ln1"], EPS))
-        h = small_linear(qkv[:, :HIDDEN], p["o"], residual=h)
-        b = p["blk"]
         return moe_block_decode(h, b["norm_w"], EPS, b["w32"], b["w_gu"], b["w_d"], top_k=TOP_K, logits=self.logits,
                                 ids=self.ids, wts=self.wts, a_buf=self.a_buf)[0]
+
+    def layer(self, p, h):
+        from fastlinear import small_linear
+        qkv = small_linear(h, p["qkv"], norm=(p["ln1"], EPS))
+        h = small_linear(qkv[:, :HIDDEN], p["o"], residual=h)
+        return self.layer_moe(p["blk"], h)
 
     def __call__(self):
         from fastlinear import small_linear
@@ -238,6 +242,136 @@ class ThinkerDecodeStep:
         moe = n * (TOP_K + 1) * expert_bytes()
         router = n * EXPERTS * HIDDEN * 4
         return proj + moe + router + self.head.numel() * 2
+
+
+# ----------------------------------------------------------------------- hybrid thinker decode step
+
+KDA_HEADS, KDA_DIM, KDA_CONV, KDA_LORA = 16, 128, 4, 128
+MLA_HEADS, MLA_QK, MLA_V = 16, 192, 128
+
+
+class HybridThinkerStep:
+    """One decode token of a synthetic hybrid thinker on the HIP kernels (the layer kinds engine.py:636-648 caches):
+    `layers` layers, every `mla_every`-th an MLA layer and the others KDA layers, each followed by the MoE block of
+    ThinkerDecodeStep; final RMSNorm fused into the LM head; the position advances on the device (engine.py:681-686).
+      KDA layer: RMSNorm fused into one GEMV of [q | k | v (16 x 128 each) | f_a | g_a (rank 128) | b (16)];
+        f = f_b(f_a), gg = g_b(g_a); short convolutions of q | k | v (window 4, SiLU, caches [1, 6144, 4]);
+        fused_recurrent_kda (l2-normalised q, k, in-kernel gate with A_log, dt_bias; beta = sigmoid(b) in the kernel; state
+        [1, 16, 128, 128] fp32 in place); gated RMSNorm with gg; o projection + residual.
+      MLA layer: RMSNorm fused into one GEMV of [q | k (16 x 192) | v (16 x 128)]; attention over the static cache
+        (k [1, 16, max_len, 192], v [1, 16, max_len, 128], rows written at pos); o projection + residual.
+    The real model's projection internals (the rotary part of q / k, the latent kv compression) are not modelled:
+    q, k and v come straight from one GEMV. Shapes beyond the configs' hidden 2048 (head counts, dims, the 3:1 mix)
+    are an assumption. Weights ~ N(0, 0.02) (norm weights 1 + N(0, 0.02), A_log, dt_bias ~ N(0, 0.5), conv ~
+    N(0, 0.5)); the caches hold a context of `pos` tokens (random rows, states ~ N(0, 0.1)). Calling the object
+    runs one step and returns the logits [1, vocab]."""
+
+    def __init__(self, layers=28, device="cuda", vocab=VOCAB, max_len=1024, pos=512, mla_every=4, seed=5000):
+        import thinker_attn as TA
+        self.TA = TA
+        self.moe = ThinkerDecodeStep(0, device, vocab=vocab, seed=seed)  # the shared router buffers, head, final norm
+        H, dev = HIDDEN, device
+        kd = KDA_HEADS * KDA_DIM
+        self.max_len = max_len
+        self.L = []
+        for li in range(layers):
+            s = seed + 64 * li
+            w = lambda shape, j, std=0.02, **kw: normal(shape, std, s + j, dev, **kw)  # noqa: E731
+            p = {"blk": block(seed=s + 1, device=dev), "ln1": w((H,), 6, mean=1.0)}
+            if (li + 1) % mla_every == 0:
+                p["kind"] = "mla"
+                p["qkv"] = torch.cat([w((MLA_HEADS * MLA_QK, H), 10), w((MLA_HEADS * MLA_QK, H), 11),
+                                      w((MLA_HEADS * MLA_V, H), 12)])
+                p["o"] = w((H, MLA_HEADS * MLA_V), 13)
+                p["kc"] = normal((1, MLA_HEADS, max_len, MLA_QK), 1.0, s + 14, dev)
+                p["vc"] = normal((1, MLA_HEADS, max_len, MLA_V), 1.0, s + 15, dev)
+            else:
+                p["kind"] = "kda"
+                p["proj"] = torch.cat([w((3 * kd, H), 20), w((KDA_LORA, H), 21), w((KDA_LORA, H), 22),
+                                       w((KDA_HEADS, H), 23)])
+                p["f_b"] = w((kd, KDA_LORA), 24)
+                p["g_b"] = w((kd, KDA_LORA), 25)
+                p["conv_w"] = w((3 * kd, 1, KDA_CONV), 26, std=0.5)
+                p["conv"] = w((1, 3 * kd, KDA_CONV), 27, std=1.0)
+                p["A_log"] = w((KDA_HEADS,), 28, std=0.5, dtype=torch.float32)
+                p["dt_bias"] = w((kd,), 29, std=0.5, dtype=torch.float32)
+                p["o_norm"] = w((KDA_DIM,), 30, mean=1.0)
+                p["o"] = w((H, kd), 31)
+                p["state"] = w((1, KDA_HEADS, KDA_DIM, KDA_DIM), 32, std=0.1, dtype=torch.float32)
+            self.L.append(p)
+        self.x0 = tokens(1, seed=seed + 1, device=dev)
+        self.pos = torch.tensor([pos], device=dev, dtype=torch.long)
+        self.ws = TA.mla_attn_workspace(MLA_HEADS, MLA_V, max_len, dev)
+
+    def mixer(self, p, h):
+        """The attention half of a layer: h -> h + o(mixer(norm(h)))."""
+        from fastlinear import small_linear
+        TA = self.TA
+        kd = KDA_HEADS * KDA_DIM
+        if p["kind"] == "mla":
+            qkv = small_linear(h, p["qkv"], norm=(p["ln1"], EPS))
+            nq = MLA_HEADS * MLA_QK
+            o = TA.mla_decode_attn(qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:], p["kc"], p["vc"], self.pos,
+                                   workspace=self.ws)
+            return small_linear(o.reshape(1, -1), p["o"], residual=h)
+        pr = small_linear(h, p["proj"], norm=(p["ln1"], EPS))
+        f = small_linear(pr[:, 3 * kd:3 * kd + KDA_LORA], p["f_b"])
+        gg = small_linear(pr[:, 3 * kd + KDA_LORA:3 * kd + 2 * KDA_LORA], p["g_b"])
+        qkv = TA.short_conv(pr[:, :3 * kd], p["conv"], p["conv_w"])
+        b = pr[:, 3 * kd + 2 * KDA_LORA:]  # the beta projection: the kernel applies its sigmoid
+        shp = (1, 1, KDA_HEADS, KDA_DIM)
+        o, _ = TA.fused_recurrent_kda(qkv[:, :kd].reshape(shp), qkv[:, kd:2 * kd].reshape(shp),
+                                      qkv[:, 2 * kd:].reshape(shp), f.reshape(shp), b.reshape(1, 1, KDA_HEADS),
+                                      A_log=p["A_log"], dt_bias=p["dt_bias"], initial_state=p["state"], inplace=True,
+                                      use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True)
+        on = TA.rms_norm_gated(o.reshape(KDA_HEADS, KDA_DIM), gg.reshape(KDA_HEADS, KDA_DIM), p["o_norm"], 1e-5)
+        return small_linear(on.reshape(1, kd), p["o"], residual=h)
+
+    def __call__(self):
+        from fastlinear import small_linear
+        m = self.moe
+        h = self.x0
+        for p in self.L:
+            h = m.layer_moe(p["blk"], self.mixer(p, h))
+        logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
+        self.pos.add_(1)
+        return logits
+
+    def bytes_per_step(self, pos=None):
+        """HBM bytes one step must read or write at position pos (default: the current one): every weight of the
+        mixers, the KDA states (read + written) and conv caches, the MLA cache rows 0..pos, the 7 experts and
+        router of every MoE block, the LM head."""
+        pos = int(self.pos) if pos is None else pos
+        H, kd, total = HIDDEN, KDA_HEADS * KDA_DIM, 0
+        for p in self.L:
+            if p["kind"] == "mla":
+                total += (p["qkv"].numel() + p["o"].numel()) * 2
+                total += (pos + 1) * MLA_HEADS * (MLA_QK + MLA_V) * 2
+            else:
+                total += (p["proj"].numel() + p["f_b"].numel() + p["g_b"].numel() + p["o"].numel()) * 2
+                total += p["conv_w"].numel() * 2 + 2 * p["conv"].numel() * 2 + 2 * p["state"].numel() * 4
+            total += H * 2 + (TOP_K + 1) * expert_bytes() + EXPERTS * H * 4
+        return total + self.moe.head.numel() * 2
+
+    def state_copy(self):
+        """A copy of the step's mutable state: KDA states and conv caches, MLA caches, the position."""
+        keys = ("state", "conv", "kc", "vc")
+        return {"pos": self.pos.clone(), "L": [{k: p[k].clone() for k in keys if k in p} for p in self.L]}
+
+    def trace(self):
+        """The step run eagerly, keeping per layer (input, mixer output, router ids, weights); returns that list
+        and the logits. The state advances as in a call."""
+        from fastlinear import small_linear
+        m = self.moe
+        h, out = self.x0, []
+        for p in self.L:
+            h_in = h.clone()
+            hm = self.mixer(p, h)
+            h = m.layer_moe(p["blk"], hm)
+            out.append((h_in, hm.clone(), m.ids.clone(), m.wts.clone()))
+        logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
+        self.pos.add_(1)
+        return out, h, logits
 
 
 # ------------------------------------------------------------------------------------------- Talker LLM

@@ -30,7 +30,7 @@ def _kda_inputs(T, H, K, V, seed, gdt=torch.float32):
 
 
 @pytest.mark.parametrize("T,H,K,V", [(1, 16, 128, 128), (7, 4, 128, 128), (64, 2, 128, 128), (3, 5, 64, 64),
-                                     (9, 3, 128, 64), (4, 2, 64, 128)])
+                                     (9, 3, 128, 64), (4, 2, 64, 128), (3, 2, 64, 48), (2, 3, 128, 32)])
 @pytest.mark.parametrize("gate", ["softplus", "lower_bound", "none"])
 def test_kda_recurrent_matches_oracle(T, H, K, V, gate):
     print(f"[kda] T={T} H={H} K={K} V={V} gate={gate}", flush=True)
@@ -109,11 +109,12 @@ def test_rms_norm_gated_matches_oracle():
     close(TA.rms_norm_gated(x, g, w, 1e-5), A.rms_norm_gated(x.cpu(), g.cpu(), w.cpu(), 1e-5))
 
 
-@pytest.mark.parametrize("nh,dq,dv,L", [(16, 192, 128, 1024), (4, 64, 64, 300), (2, 96, 32, 70)])
+@pytest.mark.parametrize("nh,dq,dv,L", [(16, 192, 128, 1024), (4, 64, 64, 300), (2, 96, 32, 70), (3, 72, 40, 100),
+                                        (2, 512, 256, 90), (1, 8, 8, 33)])
 def test_mla_decode_attn_matches_oracle(nh, dq, dv, L):
     kc = W.normal((1, nh, L, dq), 1.0, 420, DEV)
     vc = W.normal((1, nh, L, dv), 1.0, 421, DEV)
-    for pos in sorted({0, 1, 63, 64, 65, L // 2, L - 1}):
+    for pos in sorted({p for p in (0, 1, 31, 32, 33, 63, 64, 65, L // 2, L - 1) if p < L}):
         print(f"[mla] nh={nh} dq={dq} dv={dv} L={L} pos={pos}", flush=True)
         q = W.normal((nh, dq), 1.0, 430 + pos, DEV)
         kn = W.normal((nh, dq), 1.0, 431 + pos, DEV)
@@ -123,6 +124,23 @@ def test_mla_decode_attn_matches_oracle(nh, dq, dv, L):
         ro, rk, rv = A.mla_decode_attn(q.cpu(), kn.cpu(), vn.cpu(), k0[0].cpu(), v0[0].cpu(), pos)
         close(out, ro)
         assert torch.equal(kc[0].cpu(), rk) and torch.equal(vc[0].cpu(), rv)
+
+
+def test_mla_rows_past_the_position_are_never_read():
+    """Cache rows past pos filled with NaN (an uninitialised cache) leave the output finite and equal to the
+    oracle's; the last position of a partial chunk and of the cache included."""
+    nh, dq, dv, L = 4, 192, 128, 100
+    for pos in (0, 31, 37, 99):
+        kc = W.normal((1, nh, L, dq), 1.0, 470, DEV)
+        vc = W.normal((1, nh, L, dv), 1.0, 471, DEV)
+        kc[:, :, pos + 1:] = float("nan")
+        vc[:, :, pos + 1:] = float("nan")
+        k0, v0 = kc.clone(), vc.clone()
+        q, kn, vn = W.normal((nh, dq), 1.0, 472, DEV), W.normal((nh, dq), 1.0, 473, DEV), W.normal((nh, dv), 1.0, 474, DEV)
+        out = TA.mla_decode_attn(q, kn, vn, kc, vc, torch.tensor([pos], device=DEV, dtype=torch.int32))
+        ro, _, _ = A.mla_decode_attn(q.cpu(), kn.cpu(), vn.cpu(), k0[0].cpu(), v0[0].cpu(), pos)
+        assert torch.isfinite(out.float()).all(), pos
+        close(out, ro)
 
 
 def test_mla_out_of_range_position_writes_nothing():
@@ -160,3 +178,99 @@ def test_mla_graph_replays_follow_the_position():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want) and torch.equal(kc, ke) and torch.equal(vc, ve), p
+
+
+def test_kda_beta_logits_apply_the_sigmoid():
+    """beta_is_logits=True (the kernel applies the sigmoid of the beta projection) against the oracle given the
+    sigmoid's values."""
+    T, H, K, V = 2, 4, 128, 128
+    q, k, v, g, _, A_log, dt, S0 = _kda_inputs(T, H, K, V, 330)
+    b = W.normal((1, T, H), 2.0, 335, DEV)
+    o, fin = TA.fused_recurrent_kda(q, k, v, g, b, A_log=A_log, dt_bias=dt, initial_state=S0, output_final_state=True,
+                                    use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True)
+    ro, rS = A.kda_recurrent(q[0].cpu(), k[0].cpu(), v[0].cpu(), g[0].cpu(), torch.sigmoid(b[0].cpu().double()),
+                             S0[0].cpu(), A_log=A_log.cpu(), dt_bias=dt.cpu())
+    close(o[0], ro)
+    torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
+
+
+# ------------------------------------------------------------------------------ the hybrid decode step
+
+def test_hybrid_step_graph_replays_equal_eager_steps():
+    """The hybrid thinker decode step (KDA and MLA layers + MoE blocks + LM head, the position advancing on the
+    device) captured once: three replays equal three eager steps of an identical copy, logits, every KDA state
+    and conv cache, the MLA caches and the position bit for bit."""
+    print("[hybrid] graph vs eager, 8 layers", flush=True)
+    eager = W.HybridThinkerStep(8, DEV, pos=100, seed=7000)
+    graphed = W.HybridThinkerStep(8, DEV, pos=100, seed=7000)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = graphed()
+    torch.cuda.synchronize()
+    for i in range(3):
+        want = eager().clone()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        a, b = eager.state_copy(), graphed.state_copy()
+        assert torch.equal(a["pos"], b["pos"]) and int(b["pos"]) == 101 + i
+        for la, lb in zip(a["L"], b["L"]):
+            for key in la:
+                assert torch.equal(la[key], lb[key]), (i, key)
+    del eager, graphed, g, out
+    torch.cuda.empty_cache()
+
+
+def _oracle_mixer(p, st, h, pos):
+    """One hybrid layer's mixer on the oracle (state st: the layer's KDA state / conv cache or MLA caches before)."""
+    from oracle import moe_oracle as O
+    H = W.HIDDEN
+    kd = W.KDA_HEADS * W.KDA_DIM
+    if p["kind"] == "mla":
+        qkv = O.small_linear(h, p["qkv"].cpu(), norm=(p["ln1"].cpu(), W.EPS))
+        nq = W.MLA_HEADS * W.MLA_QK
+        o, _, _ = A.mla_decode_attn(qkv[0, :nq].reshape(W.MLA_HEADS, -1), qkv[0, nq:2 * nq].reshape(W.MLA_HEADS, -1),
+                                    qkv[0, 2 * nq:].reshape(W.MLA_HEADS, -1), st["kc"][0].cpu(), st["vc"][0].cpu(),
+                                    pos)
+        return O.small_linear(o.reshape(1, -1).to(BF), p["o"].cpu(), residual=h)
+    pr = O.small_linear(h, p["proj"].cpu(), norm=(p["ln1"].cpu(), W.EPS))
+    f = O.small_linear(pr[:, 3 * kd:3 * kd + W.KDA_LORA], p["f_b"].cpu())
+    gg = O.small_linear(pr[:, 3 * kd + W.KDA_LORA:3 * kd + 2 * W.KDA_LORA], p["g_b"].cpu())
+    qkv, _ = A.short_conv(pr[:, :3 * kd], st["conv"][0].cpu(), p["conv_w"][:, 0].cpu())
+    qkv = qkv.to(BF)
+    beta = torch.sigmoid(pr[:, 3 * kd + 2 * W.KDA_LORA:].double())
+    shp = (1, W.KDA_HEADS, W.KDA_DIM)
+    o, _ = A.kda_recurrent(qkv[:, :kd].reshape(shp), qkv[:, kd:2 * kd].reshape(shp), qkv[:, 2 * kd:].reshape(shp),
+                           f.reshape(shp), beta.reshape(1, -1), st["state"][0].cpu(), A_log=p["A_log"].cpu(),
+                           dt_bias=p["dt_bias"].cpu())
+    on = A.rms_norm_gated(o[0].to(BF), gg.reshape(W.KDA_HEADS, W.KDA_DIM), p["o_norm"].cpu(), 1e-5)
+    return O.small_linear(on.reshape(1, kd).to(BF), p["o"].cpu(), residual=h)
+
+
+def test_hybrid_step_layers_match_the_oracle():
+    """4 layers (3 KDA, 1 MLA) at full width, each half checked on the GPU's own input: the mixer (projections,
+    convolutions, KDA recurrence or MLA attention, output norm / projection) and the MoE block, within the bf16
+    tolerance on at least 99.5 % of elements (an element can be the small difference of two large bf16 values)."""
+    from oracle import moe_oracle as O
+    print("[hybrid] 4 layers vs oracle", flush=True)
+    step = W.HybridThinkerStep(4, DEV, pos=200, seed=7100)
+    before = step.state_copy()
+    trace, _, _ = step.trace()
+    for li, (p, st, (h_in, hm, ids, wts)) in enumerate(zip(step.L, before["L"], trace)):
+        want = _oracle_mixer(p, st, h_in.cpu(), 200)
+        d = (hm.float().cpu() - want.float()).abs()
+        ok = float((d <= 1e-2 + 2e-2 * want.float().abs()).float().mean())
+        print(f"[hybrid] layer {li} ({p['kind']}) mixer: max |d| {float(d.max()):.4f} within-tol {ok:.4f}", flush=True)
+        assert ok >= 0.995, (li, p["kind"], ok)
+        assert float((hm.float() - h_in.float()).abs().mean()) > 0.05 * float(h_in.float().abs().mean())  # it mixes
+        b = {k: v.cpu() for k, v in p["blk"].items()}
+        xn = O.rms_norm(hm.cpu(), b["norm_w"], W.EPS)
+        moe = O.moe(xn, b["w_gu"], b["w_d"], ids.cpu(), wts.cpu(), residual=hm.cpu())
+        nxt = trace[li + 1][0] if li + 1 < len(trace) else None
+        if nxt is not None:
+            d = (nxt.float().cpu() - moe.float()).abs()
+            assert float((d <= 1e-2 + 2e-2 * moe.float().abs()).float().mean()) >= 0.995, li
