@@ -209,6 +209,229 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
   }
 }
 
+// ------------------------------------------------------------------------- one KDA decode token, two kernels
+//
+// The per-token core of a KDA layer (engine.py:242-263: the q/k/v short convolutions, the gate's LoRA up-projection
+// f = f_b . fa, beta, fused_recurrent_kda, then g = g_b . ga and the gated output norm) in two launches instead of
+// five, on the layer's projection row pr = [q | k (H K each) | v (H V) | fa | ga (R each) | beta logits (H)]:
+//   kda_step_kernel  grid (V / 16, H): the head's K key channels and the block's 16 value columns are convolved
+//                    over their cached windows (SiLU, rounded to bf16 as short_conv_kernel stores them), each key
+//                    channel's gate f = bf16(sum_r f_b[ch, r] fa[r]), beta = sigmoid(logit); then one
+//                    token of kda_recurrent_kernel's recurrence. The output goes to y.
+//   kda_out_kernel   one workgroup per head row: g = bf16(sum_r g_b[ch, r] ga[r]), y = rms_norm_gated(y, g) in
+//                    place (each lane reads its elements before writing them); then every conv window shifts in the
+//                    row's inputs. The shift waits for this second kernel because all V / 16 workgroups of a head
+//                    read the head's q and k windows in the first.
+// Same arithmetic as the five kernels except the order of the f and g dots (two lanes per row here, each over
+// its half in order; small_linear reduces over more lanes), so f and g can differ in the last bf16 place.
+
+struct KdaStepArgs {
+  const uint16_t* pr;      // projection row
+  const uint16_t* conv_w;  // [2 H K + H V, W]
+  uint16_t* cache;         // [2 H K + H V, W], shifted by kda_out_kernel
+  const uint16_t* f_b;     // [H K, R]
+  const uint16_t* g_b;     // [H V, R]
+  const float* A_log;      // [H]
+  const float* dt_bias;    // [H K]
+  float lower_bound;       // NaN: the softplus gate
+  float scale;
+  float* state;            // [H, K, V] fp32, updated in place
+  const uint16_t* o_norm;  // [V]
+  float eps;
+  uint16_t* y;             // [H, V]: the recurrence output, then the normed output
+  int H, V, R;
+};
+
+template <int W>
+__device__ __forceinline__ float conv_step(const KdaStepArgs& a, int64_t ch) {
+  const uint2 cw = *reinterpret_cast<const uint2*>(a.cache + ch * W);
+  const uint2 ww = *reinterpret_cast<const uint2*>(a.conv_w + ch * W);
+  static_assert(W == 4, "window of 4");
+  // the window after the shift: cache[1..3], then the new input
+  const float win[4] = {__uint_as_float(cw.x & 0xffff0000u), __uint_as_float(cw.y << 16),
+                        __uint_as_float(cw.y & 0xffff0000u), bf16_to_f32(a.pr[ch])};
+  const float wt[4] = {__uint_as_float(ww.x << 16), __uint_as_float(ww.x & 0xffff0000u), __uint_as_float(ww.y << 16),
+                       __uint_as_float(ww.y & 0xffff0000u)};
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = fmaf(wt[j], win[j], acc);
+  return round_bf16(silu(acc));
+}
+
+constexpr int kKdaMaxR = 256;
+
+// LoRA up-projection of `rows` rows (row i at m + i * R, bf16, 16-byte aligned) with vec (fp32 in LDS, R
+// entries): out[i] = bf16(sum_r m[i, r] vec[r]), into LDS. Two neighbouring lanes share a row, each taking its
+// half in r order (one wave load covers 32 rows x 256 bytes at R = 128), and one shuffle adds the halves.
+// Whole workgroup (256 threads); ends with a barrier.
+__device__ __forceinline__ void lora_rows(const uint16_t* m, int rows, int R, const float* vec, float* out) {
+  const int half = threadIdx.x & 1, h2 = R / 2;
+  for (int i0 = 0; i0 < rows; i0 += 128) {
+    const int i = i0 + static_cast<int>(threadIdx.x >> 1);
+    const bool ok = i < rows;
+    const uint16_t* row = m + static_cast<int64_t>(ok ? i : 0) * R + half * h2;
+    float acc = 0.f;
+    int r0 = 0;
+    for (; r0 + 64 <= h2; r0 += 64) {
+      uint4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const uint4*>(row + r0 + 8 * j);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t u[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const float* vv = vec + half * h2 + r0 + 8 * j;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc = fmaf(__uint_as_float(u[q] << 16), vv[2 * q], acc);
+          acc = fmaf(__uint_as_float(u[q] & 0xffff0000u), vv[2 * q + 1], acc);
+        }
+      }
+    }
+    for (; r0 < h2; r0 += 4) {  // R / 2 is a multiple of 4: 8-byte pieces
+      const uint2 v = *reinterpret_cast<const uint2*>(row + r0);
+      const float* vv = vec + half * h2 + r0;
+      acc = fmaf(__uint_as_float(v.x << 16), vv[0], acc);
+      acc = fmaf(__uint_as_float(v.x & 0xffff0000u), vv[1], acc);
+      acc = fmaf(__uint_as_float(v.y << 16), vv[2], acc);
+      acc = fmaf(__uint_as_float(v.y & 0xffff0000u), vv[3], acc);
+    }
+    acc += __shfl_xor(acc, 1, kWave);
+    if (ok && half == 0) out[i] = round_bf16(acc);
+  }
+  __syncthreads();
+}
+
+template <int K, int W>
+__global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
+  constexpr int CB = kKdaCols, RPT = K / 16;
+  static_assert(K % kWave == 0 && K <= 256, "kda key dim");
+  __shared__ float s_q[K], s_k[K], s_dec[K], s_fa[kKdaMaxR], s_f[K];
+  __shared__ float s_red[K / kWave][2];
+  __shared__ float part_u[4][CB], part_o[4][CB];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
+  const int c = lane % CB, rg = lane / CB;
+  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col;
+  float S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
+  const int64_t fa0 = 2 * HK + a.H * V;  // fa, then ga, then the beta logits
+  for (int r = tid; r < a.R; r += 256) s_fa[r] = bf16_to_f32(a.pr[fa0 + r]);
+  const float vc = conv_step<W>(a, 2 * HK + static_cast<int64_t>(h) * V + col);
+  float beta = bf16_to_f32(a.pr[fa0 + 2 * a.R + h]);
+  beta = 1.f / (1.f + __expf(-beta));
+  const bool chan = tid < K;  // whole waves
+  const int64_t i = static_cast<int64_t>(h) * K + (chan ? tid : 0);
+  // the key channels' inputs are fetched with the rest, before the gate projections
+  const float qv = conv_step<W>(a, i), kv = conv_step<W>(a, HK + i), dtb = a.dt_bias[i];
+  __syncthreads();
+  lora_rows(a.f_b + static_cast<int64_t>(h) * K * a.R, K, a.R, s_fa, s_f);  // the head's gate projections
+  if (chan) {
+    const float x = s_f[tid] + dtb;
+    const float nA = __expf(a.A_log[h]);
+    const float gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
+    s_q[tid] = qv;
+    s_k[tid] = kv;
+    s_dec[tid] = __expf(gl);
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+    if (lane == 0) {
+      s_red[w][0] = sq;
+      s_red[w][1] = sk;
+    }
+  }
+  __syncthreads();
+  float sq = s_red[0][0], sk = s_red[0][1];
+#pragma unroll
+  for (int j = 1; j < K / kWave; ++j) {
+    sq += s_red[j][0];
+    sk += s_red[j][1];
+  }
+  const float qs = a.scale / sqrtf(sq + 1e-6f), ks = 1.f / sqrtf(sk + 1e-6f);
+  float pu = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = 16 * i + 4 * w + rg;
+    S[i] *= s_dec[r];
+    pu = fmaf(s_k[r] * ks, S[i], pu);
+  }
+  pu += __shfl_xor(pu, 16, kWave);
+  pu += __shfl_xor(pu, 32, kWave);
+  if (rg == 0) part_u[w][c] = pu;
+  __syncthreads();
+  const float u = (vc - (((part_u[0][c] + part_u[1][c]) + part_u[2][c]) + part_u[3][c])) * beta;
+  float po = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = 16 * i + 4 * w + rg;
+    S[i] = fmaf(s_k[r] * ks, u, S[i]);
+    po = fmaf(s_q[r] * qs, S[i], po);
+  }
+  po += __shfl_xor(po, 16, kWave);
+  po += __shfl_xor(po, 32, kWave);
+  if (rg == 0) part_o[w][c] = po;
+  __syncthreads();
+  if (w == 0 && rg == 0) {
+    const float o = ((part_o[0][c] + part_o[1][c]) + part_o[2][c]) + part_o[3][c];
+    a.y[static_cast<int64_t>(h) * V + col] = f32_to_bf16(o);
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) st[static_cast<int64_t>(16 * i + 4 * w + rg) * V] = S[i];
+}
+
+// Grid H x 256: workgroup = head row (V <= 512 elements); its g projections go through LDS, then wave 0 norms the
+// row (8 elements per lane); the threads of the whole grid then shift the conv windows of all 2 H K + H V channels.
+template <int W>
+__global__ __launch_bounds__(256) void kda_out_kernel(KdaStepArgs a, int K) {
+  __shared__ float s_ga[kKdaMaxR], s_g[512];
+  static_assert(W == 4, "window of 4");
+  constexpr int kShift = 4;  // conv channels a thread shifts at most (grids of H workgroups, H >= ceil(C / 1024))
+  const int tid = threadIdx.x, lane = lane_id();
+  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K;
+  const int64_t ga0 = 2 * HK + a.H * V + a.R;
+  const int64_t C = 2 * HK + a.H * V;
+  const int64_t row = blockIdx.x;
+  // every load up front: this thread's conv windows and new inputs, the row to norm (wave 0), ga
+  const int64_t nthr = static_cast<int64_t>(gridDim.x) * 256, c0 = row * 256 + tid;
+  uint2 cw[kShift];
+  uint32_t xin[kShift];
+#pragma unroll
+  for (int j = 0; j < kShift; ++j) {
+    const int64_t ch = c0 + j * nthr;
+    cw[j] = ch < C ? *reinterpret_cast<const uint2*>(a.cache + ch * W) : make_uint2(0u, 0u);
+    xin[j] = ch < C ? a.pr[ch] : 0u;
+  }
+  float xv[8], ss = 0.f;
+  if (tid < kWave) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + kWave * j;
+      xv[j] = i < V ? bf16_to_f32(a.y[row * V + i]) : 0.f;
+      ss = fmaf(xv[j], xv[j], ss);
+    }
+  }
+  for (int r = tid; r < a.R; r += 256) s_ga[r] = bf16_to_f32(a.pr[ga0 + r]);
+  __syncthreads();
+  lora_rows(a.g_b + row * V * a.R, static_cast<int>(V), a.R, s_ga, s_g);
+  if (tid < kWave) {
+    const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + kWave * j;
+      if (i < V) a.y[row * V + i] = f32_to_bf16(xv[j] * rstd * bf16_to_f32(a.o_norm[i]) / (1.f + __expf(-s_g[i])));
+    }
+  }
+  // conv windows: drop the oldest input, append this token's
+#pragma unroll
+  for (int j = 0; j < kShift; ++j) {
+    const int64_t ch = c0 + j * nthr;
+    if (ch < C)
+      *reinterpret_cast<uint2*>(a.cache + ch * W) =
+          make_uint2((cw[j].x >> 16) | (cw[j].y << 16), (cw[j].y >> 16) | (xin[j] << 16));
+  }
+}
+
 // ------------------------------------------------------------------------------------ MLA decode attention
 
 constexpr int kMlaChunk = 32;  // positions per workgroup: 4 waves of 8
@@ -476,6 +699,52 @@ extern "C" int mm_rms_norm_gated(const void* x, int64_t x_rs, const void* g, int
                      static_cast<const uint16_t*>(x), x_rs, static_cast<const uint16_t*>(g), g_rs,
                      static_cast<const uint16_t*>(w), rows, static_cast<int>(n), eps, static_cast<uint16_t*>(y), y_rs);
   return mm::check_launch("rms_norm_gated");
+}
+
+extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* conv_w, void* conv_cache, int64_t W,
+                                  const void* f_b, const void* g_b, int64_t R, const float* A_log, const float* dt_bias,
+                                  float lower_bound, float scale, float* state, int64_t H, int64_t K, int64_t V,
+                                  const void* o_norm, float eps, void* y, void* stream) {
+  MM_REQUIRE(H >= 1 && H <= 65535, "kda_decode_step: bad H=%lld", (long long)H);
+  MM_REQUIRE(K == 128 && V % kKdaCols == 0 && V >= kKdaCols && V <= 512,
+             "kda_decode_step: head dims K=%lld (128), V=%lld (a multiple of 16 up to 512)", (long long)K, (long long)V);
+  MM_REQUIRE(W == 4, "kda_decode_step: conv window %lld (4)", (long long)W);
+  MM_REQUIRE(2 * K + V <= 4 * 256, "kda_decode_step: 2 K + V = %lld conv channels per head, at most 1024",
+             (long long)(2 * K + V));
+  MM_REQUIRE(R >= 16 && R <= kKdaMaxR && R % 16 == 0, "kda_decode_step: LoRA rank %lld (a multiple of 16 up to %d)",
+             (long long)R, kKdaMaxR);
+  MM_REQUIRE(pr_len == 2 * H * K + H * V + 2 * R + H,
+             "kda_decode_step: projection row of %lld elements, expected 2 H K + H V + 2 R + H = %lld", (long long)pr_len,
+             (long long)(2 * H * K + H * V + 2 * R + H));
+  MM_REQUIRE(pr && conv_w && conv_cache && f_b && g_b && A_log && dt_bias && state && o_norm && y,
+             "kda_decode_step: null pointer");
+  MM_REQUIRE(mm::aligned16(f_b) && mm::aligned16(g_b) && (reinterpret_cast<uintptr_t>(conv_w) & 7) == 0 &&
+                 (reinterpret_cast<uintptr_t>(conv_cache) & 7) == 0,
+             "kda_decode_step: f_b, g_b 16-byte and the conv weight / cache 8-byte aligned");
+  KdaStepArgs a;
+  a.pr = static_cast<const uint16_t*>(pr);
+  a.conv_w = static_cast<const uint16_t*>(conv_w);
+  a.cache = static_cast<uint16_t*>(conv_cache);
+  a.f_b = static_cast<const uint16_t*>(f_b);
+  a.g_b = static_cast<const uint16_t*>(g_b);
+  a.A_log = A_log;
+  a.dt_bias = dt_bias;
+  a.lower_bound = lower_bound;
+  a.scale = scale;
+  a.state = state;
+  a.o_norm = static_cast<const uint16_t*>(o_norm);
+  a.eps = eps;
+  a.y = static_cast<uint16_t*>(y);
+  a.H = static_cast<int>(H);
+  a.V = static_cast<int>(V);
+  a.R = static_cast<int>(R);
+  hipStream_t st = MM_STREAM(stream);
+  hipLaunchKernelGGL((kda_step_kernel<128, 4>), dim3(static_cast<unsigned>(V / kKdaCols), static_cast<unsigned>(H)),
+                     dim3(256), 0, st, a);
+  int rc = mm::check_launch("kda_decode_step");
+  if (rc) return rc;
+  hipLaunchKernelGGL(kda_out_kernel<4>, dim3(static_cast<unsigned>(H)), dim3(256), 0, st, a, static_cast<int>(K));
+  return mm::check_launch("kda_decode_step out");
 }
 
 extern "C" int64_t mm_mla_attn_workspace(int nh, int dv, int64_t max_len) {

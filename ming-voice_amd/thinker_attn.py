@@ -6,6 +6,8 @@ static cache.
                         keywords, B = 1; the state is fp32 [1, H, K, V], updated in place with inplace=True
   short_conv            the step form of fla's ShortConvolution (a [1, C, W] cache of the last inputs, SiLU)
   rms_norm_gated        fla's FusedRMSNormGated with a sigmoid gate (a KDA layer's o_norm)
+  kda_decode_step       one decode token of a KDA layer's core (convolutions, the f / g LoRA up-projections, the
+                        recurrence, the gated norm) in two kernels instead of the five calls above
   mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
                         masked softmax attention over positions 0..pos
 Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
@@ -15,7 +17,8 @@ import torch
 
 import _mingmoe as _mm
 
-__all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "mla_decode_attn", "mla_attn_workspace"]
+__all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
+           "mla_attn_workspace"]
 
 
 def _f32_or_bf16(t, name):
@@ -146,6 +149,49 @@ def rms_norm_gated(x, g, weight, eps=1e-5, out=None):
         _mm.check(lib.mm_rms_norm_gated(_mm.ptr(x2), x2.stride(0), _mm.ptr(g2), g2.stride(0), _mm.ptr(w), x2.shape[0], n,
                                         float(eps), _mm.ptr(y), y.stride(0), _mm.stream_of(x)), "rms_norm_gated")
     return y.reshape(x.shape)
+
+
+def kda_decode_step(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_norm, *, heads, eps=1e-5,
+                    lower_bound=None, scale=None, out=None):
+    """One decode token of a KDA layer's core in two kernels, on the layer's projection row
+    pr = [q | k (heads * K each) | v (heads * V) | fa | ga (rank R each) | beta logits (heads)] ([1, len] or [len]
+    bf16): the short convolutions of q, k, v over conv_cache ([1, C, 4] bf16, C = 2 heads K + heads V, shifted in
+    place; conv_w [C, 1, 4]), f = f_b(fa), the recurrence of fused_recurrent_kda (l2-normed q and k, the in-kernel
+    gate with A_log / dt_bias, beta = sigmoid of its logit; state [1, heads, K, V] fp32 in place), g = g_b(ga) and
+    the gated RMSNorm with o_norm. Returns y [heads, V] bf16, the input of the layer's o projection. Same results
+    as short_conv -> small_linear -> fused_recurrent_kda -> small_linear -> rms_norm_gated (engine.py:242-265) up to
+    the last bf16 place of f and g. K = 128."""
+    _mm.require_gpu(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_norm, out)
+    H = int(heads)
+    if state.dtype != torch.float32 or not state.is_contiguous() or state.dim() < 3:
+        raise ValueError("kda_decode_step: state must be a contiguous fp32 [1, H, K, V] tensor")
+    K, V = state.shape[-2:]
+    R = f_b.shape[-1]
+    if tuple(state.shape[-3:]) != (H, K, V):
+        raise ValueError(f"kda_decode_step: state must be [1, {H}, K, V] (got {tuple(state.shape)})")
+    p = pr.reshape(-1)
+    C = 2 * H * K + H * V
+    for name, t, shape in (("conv_cache", conv_cache, (C, 4)), ("conv_w", conv_w, (C, 4)), ("f_b", f_b, (H * K, R)),
+                           ("g_b", g_b, (H * V, R))):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != shape[0] * shape[1]:
+            raise ValueError(f"kda_decode_step: {name} must be a contiguous bf16 tensor of {shape[0]} x {shape[1]}")
+    if p.dtype != torch.bfloat16 or p.stride(0) != 1:
+        raise ValueError("kda_decode_step: pr must be a contiguous bf16 row")
+    y = torch.empty(H, V, device=pr.device, dtype=torch.bfloat16) if out is None else out
+    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() != H * V:
+        raise ValueError(f"kda_decode_step: out must be a contiguous bf16 [{H}, {V}] tensor")
+    A = A_log.float().reshape(H).contiguous()
+    dtb = dt_bias.float().reshape(H * K).contiguous()
+    w = o_norm.to(torch.bfloat16).contiguous()
+    fb, gb = _aligned16(f_b), _aligned16(g_b)
+    sc = float(scale) if scale is not None else K ** -0.5
+    lb = float("nan") if lower_bound is None else float(lower_bound)
+    lib = _mm.load()
+    with _mm.on_device(pr):
+        _mm.check(lib.mm_kda_decode_step(_mm.ptr(p), p.numel(), _mm.ptr(conv_w), _mm.ptr(conv_cache), 4, _mm.ptr(fb),
+                                         _mm.ptr(gb), R, _mm.ptr(A), _mm.ptr(dtb), lb, sc, _mm.ptr(state), H, K, V,
+                                         _mm.ptr(w), float(eps), _mm.ptr(y), _mm.stream_of(pr)), "kda_decode_step")
+    return y.reshape(H, V)
 
 
 def _aligned16(t):

@@ -257,7 +257,8 @@ class HybridThinkerStep:
       KDA layer: RMSNorm fused into one GEMV of [q | k | v (16 x 128 each) | f_a | g_a (rank 128) | b (16)];
         f = f_b(f_a), gg = g_b(g_a); short convolutions of q | k | v (window 4, SiLU, caches [1, 6144, 4]);
         fused_recurrent_kda (l2-normalised q, k, in-kernel gate with A_log, dt_bias; beta = sigmoid(b) in the kernel; state
-        [1, 16, 128, 128] fp32 in place); gated RMSNorm with gg; o projection + residual.
+        [1, 16, 128, 128] fp32 in place); gated RMSNorm with gg; o projection + residual. With fused_kda (the default)
+        the part between the two projections runs as kda_decode_step's two kernels.
       MLA layer: RMSNorm fused into one GEMV of [q | k (16 x 192) | v (16 x 128)]; attention over the static cache
         (k [1, 16, max_len, 192], v [1, 16, max_len, 128], rows written at pos); o projection + residual.
     The real model's projection internals (the rotary part of q / k, the latent kv compression) are not modelled:
@@ -266,9 +267,11 @@ class HybridThinkerStep:
     N(0, 0.5)); the caches hold a context of `pos` tokens (random rows, states ~ N(0, 0.1)). Calling the object
     runs one step and returns the logits [1, vocab]."""
 
-    def __init__(self, layers=28, device="cuda", vocab=VOCAB, max_len=1024, pos=512, mla_every=4, seed=5000):
+    def __init__(self, layers=28, device="cuda", vocab=VOCAB, max_len=1024, pos=512, mla_every=4, seed=5000,
+                 fused_kda=True):
         import thinker_attn as TA
         self.TA = TA
+        self.fused_kda = fused_kda  # the KDA core as kda_decode_step's two kernels, else the five-call chain
         self.moe = ThinkerDecodeStep(0, device, vocab=vocab, seed=seed)  # the shared router buffers, head, final norm
         H, dev = HIDDEN, device
         kd = KDA_HEADS * KDA_DIM
@@ -315,6 +318,10 @@ class HybridThinkerStep:
                                    workspace=self.ws)
             return small_linear(o.reshape(1, -1), p["o"], residual=h)
         pr = small_linear(h, p["proj"], norm=(p["ln1"], EPS))
+        if self.fused_kda:
+            on = TA.kda_decode_step(pr, p["conv_w"], p["conv"], p["f_b"], p["g_b"], p["A_log"], p["dt_bias"], p["state"],
+                                    p["o_norm"], heads=KDA_HEADS, eps=1e-5)
+            return small_linear(on.reshape(1, kd), p["o"], residual=h)
         f = small_linear(pr[:, 3 * kd:3 * kd + KDA_LORA], p["f_b"])
         gg = small_linear(pr[:, 3 * kd + KDA_LORA:3 * kd + 2 * KDA_LORA], p["g_b"])
         qkv = TA.short_conv(pr[:, :3 * kd], p["conv"], p["conv_w"])

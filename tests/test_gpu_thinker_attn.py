@@ -274,3 +274,60 @@ def test_hybrid_step_layers_match_the_oracle():
         if nxt is not None:
             d = (nxt.float().cpu() - moe.float()).abs()
             assert float((d <= 1e-2 + 2e-2 * moe.float().abs()).float().mean()) >= 0.995, li
+
+
+@pytest.mark.parametrize("H,V,R,lower_bound", [(16, 128, 128, None), (3, 64, 64, None), (5, 128, 32, -5.0)])
+def test_kda_decode_step_equals_the_five_call_chain(H, V, R, lower_bound):
+    """kda_decode_step (two kernels) against short_conv -> small_linear(f) -> fused_recurrent_kda ->
+    small_linear(g) -> rms_norm_gated on identical copies of the layer state, three tokens in a row: the conv caches
+    bit for bit, the KDA state and the normed output within tolerance (the f / g dots round in another order)."""
+    from fastlinear import small_linear
+    K, Wd = 128, 4
+    C = 2 * H * K + H * V
+    s = 300 + H + R
+    conv_w = W.normal((C, 1, Wd), 0.5, s, DEV)
+    f_b = W.normal((H * K, R), 0.02 * 8, s + 1, DEV)
+    g_b = W.normal((H * V, R), 0.02 * 8, s + 2, DEV)
+    A_log = W.normal((H,), 0.5, s + 3, DEV, dtype=torch.float32)
+    dt = W.normal((H * K,), 0.5, s + 4, DEV, dtype=torch.float32)
+    o_norm = W.normal((V,), 0.02, s + 5, DEV, mean=1.0)
+    st_a = W.normal((1, H, K, V), 0.1, s + 6, DEV, dtype=torch.float32)
+    cache_a = W.normal((1, C, Wd), 1.0, s + 7, DEV)
+    st_b, cache_b = st_a.clone(), cache_a.clone()
+    for t in range(3):
+        print(f"[kda_step] H={H} V={V} R={R} token {t}", flush=True)
+        pr = W.normal((1, C + 2 * R + H), 1.0, s + 10 + t, DEV)
+        got = TA.kda_decode_step(pr, conv_w, cache_a, f_b, g_b, A_log, dt, st_a, o_norm, heads=H,
+                                 lower_bound=lower_bound)
+        qkv = TA.short_conv(pr[:, :C], cache_b, conv_w)
+        f = small_linear(pr[:, C:C + R], f_b)
+        gg = small_linear(pr[:, C + R:C + 2 * R], g_b)
+        b = pr[:, C + 2 * R:]
+        o, _ = TA.fused_recurrent_kda(qkv[:, :H * K].reshape(1, 1, H, K), qkv[:, H * K:2 * H * K].reshape(1, 1, H, K),
+                                      qkv[:, 2 * H * K:].reshape(1, 1, H, V), f.reshape(1, 1, H, K), b.reshape(1, 1, H),
+                                      A_log=A_log, dt_bias=dt, initial_state=st_b, inplace=True,
+                                      use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True,
+                                      lower_bound=lower_bound)
+        want = TA.rms_norm_gated(o.reshape(H, V), gg.reshape(H, V), o_norm, 1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(cache_a, cache_b), t
+        close(got, want)
+        torch.testing.assert_close(st_a.cpu(), st_b.cpu(), rtol=2e-2, atol=2e-3)
+
+
+def test_kda_decode_step_rejects_bad_shapes():
+    K = 128
+    st = torch.zeros(1, 2, K, 64, device=DEV)
+    C = 2 * 2 * K + 2 * 64
+    pr = torch.zeros(1, C + 2 * 32 + 2, device=DEV, dtype=BF)
+    conv_w = torch.zeros(C, 1, 4, device=DEV, dtype=BF)
+    cache = torch.zeros(1, C, 4, device=DEV, dtype=BF)
+    f_b = torch.zeros(2 * K, 32, device=DEV, dtype=BF)
+    g_b = torch.zeros(2 * 64, 32, device=DEV, dtype=BF)
+    a = torch.zeros(2, device=DEV)
+    dt = torch.zeros(2 * K, device=DEV)
+    on = torch.ones(64, device=DEV, dtype=BF)
+    with pytest.raises((ValueError, RuntimeError)):
+        TA.kda_decode_step(pr[:, :-1], conv_w, cache, f_b, g_b, a, dt, st, on, heads=2)  # row one element short
+    with pytest.raises((ValueError, RuntimeError)):
+        TA.kda_decode_step(pr, conv_w, cache, f_b, g_b, a, dt, torch.zeros(1, 2, 64, 64, device=DEV), on, heads=2)
