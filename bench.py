@@ -326,7 +326,8 @@ def full_decode_metrics(step, stream):
 
 def hybrid_decode_metrics(stream, layers=28, pos=456):
     """One decode token of the synthetic hybrid thinker (workloads.HybridThinkerStep: 21 KDA + 7 MLA layers, each
-    with its MoE block, final norm + LM head) replayed from one hipGraph. Every replay advances the position on
+    with its MoE block, final norm + LM head) replayed from one hipGraph, and the same with the KDA cores as the
+    five-call chain (`us_per_token_kda_chain`). Every replay advances the position on
     the device: one eager call at pos, then replays at pos + 1, pos + 2, ...; the timed ones (5 x 20 after 2
     warm-up replays each) lie in pos + 3 .. pos + 110 of a 1024-row cache, mean pos + 56.5 (512.5 by default)."""
     import workloads as W
@@ -335,9 +336,13 @@ def hybrid_decode_metrics(stream, layers=28, pos=456):
     ms = median_graph_ms(graph_of(step, stream), stream)
     total = step.bytes_per_step(pos + 56)
     kda = sum(p["kind"] == "kda" for p in step.L)
+    # the same step with each KDA core as the five-call chain (short_conv, the f / g projections,
+    # fused_recurrent_kda, rms_norm_gated) instead of kda_decode_step's two kernels, same process and box
+    step.fused_kda = False
+    ms_chain = median_graph_ms(graph_of(step, stream), stream)
     out = {"layers": layers, "kda_layers": kda, "mla_layers": layers - kda, "positions": [pos + 3, pos + 110],
            "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
-           "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100}
+           "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100, "us_per_token_kda_chain": ms_chain * 1e3}
     del step
     torch.cuda.empty_cache()
     return out

@@ -81,8 +81,8 @@ SIGNATURES = {
     "mm_short_conv": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _P], ctypes.c_int),
     "mm_rms_norm_gated": ([_P, _I64, _P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P], ctypes.c_int),
     "mm_mla_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),
-    "mm_kda_decode_step": ([_P, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P, _F32, _F32, _P, _I64, _I64, _I64, _P, _F32,
-                            _P, _P], ctypes.c_int),
+    "mm_kda_decode_step": ([_P, _I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), _I64, _P, _P,
+                            _I64, _P, _P, _F32, _F32, _P, _I64, _I64, _I64, _P, _F32, _P, _P], ctypes.c_int),
     "mm_mla_decode_attn": ([_P, _P, _P, _I32, _I32, _I32, _P, _P, _I64, _P, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
 }
 

@@ -226,9 +226,9 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
 // its half in order; small_linear reduces over more lanes), so f and g can differ in the last bf16 place.
 
 struct KdaStepArgs {
-  const uint16_t* pr;      // projection row
-  const uint16_t* conv_w;  // [2 H K + H V, W]
-  uint16_t* cache;         // [2 H K + H V, W], shifted by kda_out_kernel
+  const uint16_t* pr;         // projection row
+  const uint16_t* conv_w[3];  // q, k [H K, W] and v [H V, W] conv weights
+  uint16_t* cache[3];         // the q, k and v conv caches of the same shapes, shifted by kda_out_kernel
   const uint16_t* f_b;     // [H K, R]
   const uint16_t* g_b;     // [H V, R]
   const float* A_log;      // [H]
@@ -242,10 +242,19 @@ struct KdaStepArgs {
   int H, V, R;
 };
 
+// Conv channel ch of the projection row (q channels, then k, then v): its section and index there.
+__device__ __forceinline__ int conv_section(int64_t ch, int64_t HK, int64_t& idx) {
+  const int sec = ch < HK ? 0 : (ch < 2 * HK ? 1 : 2);
+  idx = ch - (sec == 0 ? 0 : (sec == 1 ? HK : 2 * HK));
+  return sec;
+}
+
 template <int W>
-__device__ __forceinline__ float conv_step(const KdaStepArgs& a, int64_t ch) {
-  const uint2 cw = *reinterpret_cast<const uint2*>(a.cache + ch * W);
-  const uint2 ww = *reinterpret_cast<const uint2*>(a.conv_w + ch * W);
+__device__ __forceinline__ float conv_step(const KdaStepArgs& a, int64_t ch, int64_t HK) {
+  int64_t idx;
+  const int sec = conv_section(ch, HK, idx);
+  const uint2 cw = *reinterpret_cast<const uint2*>(a.cache[sec] + idx * W);
+  const uint2 ww = *reinterpret_cast<const uint2*>(a.conv_w[sec] + idx * W);
   static_assert(W == 4, "window of 4");
   // the window after the shift: cache[1..3], then the new input
   const float win[4] = {__uint_as_float(cw.x & 0xffff0000u), __uint_as_float(cw.y << 16),
@@ -319,13 +328,13 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
   for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
   const int64_t fa0 = 2 * HK + a.H * V;  // fa, then ga, then the beta logits
   for (int r = tid; r < a.R; r += 256) s_fa[r] = bf16_to_f32(a.pr[fa0 + r]);
-  const float vc = conv_step<W>(a, 2 * HK + static_cast<int64_t>(h) * V + col);
+  const float vc = conv_step<W>(a, 2 * HK + static_cast<int64_t>(h) * V + col, HK);
   float beta = bf16_to_f32(a.pr[fa0 + 2 * a.R + h]);
   beta = 1.f / (1.f + __expf(-beta));
   const bool chan = tid < K;  // whole waves
   const int64_t i = static_cast<int64_t>(h) * K + (chan ? tid : 0);
   // the key channels' inputs are fetched with the rest, before the gate projections
-  const float qv = conv_step<W>(a, i), kv = conv_step<W>(a, HK + i), dtb = a.dt_bias[i];
+  const float qv = conv_step<W>(a, i, HK), kv = conv_step<W>(a, HK + i, HK), dtb = a.dt_bias[i];
   __syncthreads();
   lora_rows(a.f_b + static_cast<int64_t>(h) * K * a.R, K, a.R, s_fa, s_f);  // the head's gate projections
   if (chan) {
@@ -399,7 +408,9 @@ __global__ __launch_bounds__(256) void kda_out_kernel(KdaStepArgs a, int K) {
 #pragma unroll
   for (int j = 0; j < kShift; ++j) {
     const int64_t ch = c0 + j * nthr;
-    cw[j] = ch < C ? *reinterpret_cast<const uint2*>(a.cache + ch * W) : make_uint2(0u, 0u);
+    int64_t idx;
+    const int sec = conv_section(ch < C ? ch : 0, HK, idx);
+    cw[j] = ch < C ? *reinterpret_cast<const uint2*>(a.cache[sec] + idx * W) : make_uint2(0u, 0u);
     xin[j] = ch < C ? a.pr[ch] : 0u;
   }
   float xv[8], ss = 0.f;
@@ -426,9 +437,12 @@ __global__ __launch_bounds__(256) void kda_out_kernel(KdaStepArgs a, int K) {
 #pragma unroll
   for (int j = 0; j < kShift; ++j) {
     const int64_t ch = c0 + j * nthr;
-    if (ch < C)
-      *reinterpret_cast<uint2*>(a.cache + ch * W) =
+    if (ch < C) {
+      int64_t idx;
+      const int sec = conv_section(ch, HK, idx);
+      *reinterpret_cast<uint2*>(a.cache[sec] + idx * W) =
           make_uint2((cw[j].x >> 16) | (cw[j].y << 16), (cw[j].y >> 16) | (xin[j] << 16));
+    }
   }
 }
 
@@ -701,10 +715,10 @@ extern "C" int mm_rms_norm_gated(const void* x, int64_t x_rs, const void* g, int
   return mm::check_launch("rms_norm_gated");
 }
 
-extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* conv_w, void* conv_cache, int64_t W,
-                                  const void* f_b, const void* g_b, int64_t R, const float* A_log, const float* dt_bias,
-                                  float lower_bound, float scale, float* state, int64_t H, int64_t K, int64_t V,
-                                  const void* o_norm, float eps, void* y, void* stream) {
+extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* const* conv_w, void* const* conv_cache,
+                                  int64_t W, const void* f_b, const void* g_b, int64_t R, const float* A_log,
+                                  const float* dt_bias, float lower_bound, float scale, float* state, int64_t H,
+                                  int64_t K, int64_t V, const void* o_norm, float eps, void* y, void* stream) {
   MM_REQUIRE(H >= 1 && H <= 65535, "kda_decode_step: bad H=%lld", (long long)H);
   MM_REQUIRE(K == 128 && V % kKdaCols == 0 && V >= kKdaCols && V <= 512,
              "kda_decode_step: head dims K=%lld (128), V=%lld (a multiple of 16 up to 512)", (long long)K, (long long)V);
@@ -718,13 +732,16 @@ extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* co
              (long long)(2 * H * K + H * V + 2 * R + H));
   MM_REQUIRE(pr && conv_w && conv_cache && f_b && g_b && A_log && dt_bias && state && o_norm && y,
              "kda_decode_step: null pointer");
-  MM_REQUIRE(mm::aligned16(f_b) && mm::aligned16(g_b) && (reinterpret_cast<uintptr_t>(conv_w) & 7) == 0 &&
-                 (reinterpret_cast<uintptr_t>(conv_cache) & 7) == 0,
-             "kda_decode_step: f_b, g_b 16-byte and the conv weight / cache 8-byte aligned");
+  MM_REQUIRE(mm::aligned16(f_b) && mm::aligned16(g_b), "kda_decode_step: f_b and g_b must be 16-byte aligned");
   KdaStepArgs a;
+  for (int i = 0; i < 3; ++i) {
+    MM_REQUIRE(conv_w[i] && conv_cache[i] && (reinterpret_cast<uintptr_t>(conv_w[i]) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(conv_cache[i]) & 7) == 0,
+               "kda_decode_step: conv weight / cache %d null or not 8-byte aligned", i);
+    a.conv_w[i] = static_cast<const uint16_t*>(conv_w[i]);
+    a.cache[i] = static_cast<uint16_t*>(conv_cache[i]);
+  }
   a.pr = static_cast<const uint16_t*>(pr);
-  a.conv_w = static_cast<const uint16_t*>(conv_w);
-  a.cache = static_cast<uint16_t*>(conv_cache);
   a.f_b = static_cast<const uint16_t*>(f_b);
   a.g_b = static_cast<const uint16_t*>(g_b);
   a.A_log = A_log;

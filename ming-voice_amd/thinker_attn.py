@@ -13,6 +13,8 @@ static cache.
 Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
 passed in); there is no CPU path.
 """
+import ctypes
+
 import torch
 
 import _mingmoe as _mm
@@ -151,17 +153,32 @@ def rms_norm_gated(x, g, weight, eps=1e-5, out=None):
     return y.reshape(x.shape)
 
 
+def _three(t, sizes, name):
+    """A (q, k, v) triple of tensors, or one tensor holding the three along dim -2 (split into views)."""
+    if isinstance(t, (tuple, list)):
+        if len(t) != 3:
+            raise ValueError(f"kda_decode_step: {name} must hold q, k and v")
+        return list(t)
+    x = t.reshape(-1, t.shape[-1])
+    if x.shape[0] != sum(sizes):
+        raise ValueError(f"kda_decode_step: {name} must have {sum(sizes)} channels (got {x.shape[0]})")
+    return list(torch.split(x, sizes, dim=0))
+
+
 def kda_decode_step(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_norm, *, heads, eps=1e-5,
                     lower_bound=None, scale=None, out=None):
     """One decode token of a KDA layer's core in two kernels, on the layer's projection row
     pr = [q | k (heads * K each) | v (heads * V) | fa | ga (rank R each) | beta logits (heads)] ([1, len] or [len]
-    bf16): the short convolutions of q, k, v over conv_cache ([1, C, 4] bf16, C = 2 heads K + heads V, shifted in
-    place; conv_w [C, 1, 4]), f = f_b(fa), the recurrence of fused_recurrent_kda (l2-normed q and k, the in-kernel
-    gate with A_log / dt_bias, beta = sigmoid of its logit; state [1, heads, K, V] fp32 in place), g = g_b(ga) and
-    the gated RMSNorm with o_norm. Returns y [heads, V] bf16, the input of the layer's o projection. Same results
-    as short_conv -> small_linear -> fused_recurrent_kda -> small_linear -> rms_norm_gated (engine.py:242-265) up to
-    the last bf16 place of f and g. K = 128."""
-    _mm.require_gpu(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_norm, out)
+    bf16). conv_w and conv_cache: the q, k and v conv1d weights ([C, 1, 4]) and the layer's three conv caches
+    ([1, C, 4], shifted in place), each a (q, k, v) tuple as the model and its cache hold them (engine.py:645-647),
+    or one tensor of all 2 heads K + heads V channels in that order. Then f = f_b(fa), the recurrence of
+    fused_recurrent_kda (l2-normed q and k, the in-kernel gate with A_log / dt_bias, beta = sigmoid of its logit;
+    state [1, heads, K, V] fp32 in place), g = g_b(ga) and the gated RMSNorm with o_norm. Returns y [heads, V] bf16,
+    the input of the layer's o projection. Same results as short_conv -> small_linear -> fused_recurrent_kda ->
+    small_linear -> rms_norm_gated (engine.py:242-265) up to the last bf16 place of f and g. K = 128."""
+    ws = conv_w if isinstance(conv_w, (tuple, list)) else [conv_w]
+    cs = conv_cache if isinstance(conv_cache, (tuple, list)) else [conv_cache]
+    _mm.require_gpu(pr, *ws, *cs, f_b, g_b, A_log, dt_bias, state, o_norm, out)
     H = int(heads)
     if state.dtype != torch.float32 or not state.is_contiguous() or state.dim() < 3:
         raise ValueError("kda_decode_step: state must be a contiguous fp32 [1, H, K, V] tensor")
@@ -169,12 +186,17 @@ def kda_decode_step(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_n
     R = f_b.shape[-1]
     if tuple(state.shape[-3:]) != (H, K, V):
         raise ValueError(f"kda_decode_step: state must be [1, {H}, K, V] (got {tuple(state.shape)})")
+    sizes = [H * K, H * K, H * V]
+    wq = _three(conv_w, sizes, "conv_w")
+    cq = _three(conv_cache, sizes, "conv_cache")
+    for name, group in (("conv_w", wq), ("conv_cache", cq)):
+        for t, n in zip(group, sizes):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != n * 4:
+                raise ValueError(f"kda_decode_step: each {name} part must be a contiguous bf16 [{n}, 4] tensor")
+    for name, t, rows in (("f_b", f_b, H * K), ("g_b", g_b, H * V)):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != rows * R:
+            raise ValueError(f"kda_decode_step: {name} must be a contiguous bf16 [{rows}, {R}] tensor")
     p = pr.reshape(-1)
-    C = 2 * H * K + H * V
-    for name, t, shape in (("conv_cache", conv_cache, (C, 4)), ("conv_w", conv_w, (C, 4)), ("f_b", f_b, (H * K, R)),
-                           ("g_b", g_b, (H * V, R))):
-        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != shape[0] * shape[1]:
-            raise ValueError(f"kda_decode_step: {name} must be a contiguous bf16 tensor of {shape[0]} x {shape[1]}")
     if p.dtype != torch.bfloat16 or p.stride(0) != 1:
         raise ValueError("kda_decode_step: pr must be a contiguous bf16 row")
     y = torch.empty(H, V, device=pr.device, dtype=torch.bfloat16) if out is None else out
@@ -186,11 +208,13 @@ def kda_decode_step(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_n
     fb, gb = _aligned16(f_b), _aligned16(g_b)
     sc = float(scale) if scale is not None else K ** -0.5
     lb = float("nan") if lower_bound is None else float(lower_bound)
+    wp = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in wq])
+    cp = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in cq])
     lib = _mm.load()
     with _mm.on_device(pr):
-        _mm.check(lib.mm_kda_decode_step(_mm.ptr(p), p.numel(), _mm.ptr(conv_w), _mm.ptr(conv_cache), 4, _mm.ptr(fb),
-                                         _mm.ptr(gb), R, _mm.ptr(A), _mm.ptr(dtb), lb, sc, _mm.ptr(state), H, K, V,
-                                         _mm.ptr(w), float(eps), _mm.ptr(y), _mm.stream_of(pr)), "kda_decode_step")
+        _mm.check(lib.mm_kda_decode_step(_mm.ptr(p), p.numel(), wp, cp, 4, _mm.ptr(fb), _mm.ptr(gb), R, _mm.ptr(A),
+                                         _mm.ptr(dtb), lb, sc, _mm.ptr(state), H, K, V, _mm.ptr(w), float(eps),
+                                         _mm.ptr(y), _mm.stream_of(pr)), "kda_decode_step")
     return y.reshape(H, V)
 
 

@@ -331,3 +331,28 @@ def test_kda_decode_step_rejects_bad_shapes():
         TA.kda_decode_step(pr[:, :-1], conv_w, cache, f_b, g_b, a, dt, st, on, heads=2)  # row one element short
     with pytest.raises((ValueError, RuntimeError)):
         TA.kda_decode_step(pr, conv_w, cache, f_b, g_b, a, dt, torch.zeros(1, 2, 64, 64, device=DEV), on, heads=2)
+
+
+def test_kda_decode_step_takes_the_three_caches_of_the_reference_layout():
+    """The q, k and v conv weights and caches as three separate tensors (the model's conv1d modules and
+    _KDAState's tuple, engine.py:645-647) give exactly what one combined tensor gives."""
+    H, K, V, R = 4, 128, 128, 128
+    C = 2 * H * K + H * V
+    w_all = W.normal((C, 1, 4), 0.5, 410, DEV)
+    c_all = W.normal((1, C, 4), 1.0, 411, DEV)
+    f_b, g_b = W.normal((H * K, R), 0.1, 412, DEV), W.normal((H * V, R), 0.1, 413, DEV)
+    A_log = W.normal((H,), 0.5, 414, DEV, dtype=torch.float32)
+    dt = W.normal((H * K,), 0.5, 415, DEV, dtype=torch.float32)
+    o_norm = W.normal((V,), 0.02, 416, DEV, mean=1.0)
+    st1 = W.normal((1, H, K, V), 0.1, 417, DEV, dtype=torch.float32)
+    st2 = st1.clone()
+    sizes = (H * K, H * K, H * V)
+    ws = tuple(t.clone() for t in torch.split(w_all, sizes, dim=0))
+    cs = tuple(t.clone() for t in torch.split(c_all, sizes, dim=1))
+    for t in range(2):
+        pr = W.normal((1, C + 2 * R + H), 1.0, 420 + t, DEV)
+        a = TA.kda_decode_step(pr, w_all, c_all, f_b, g_b, A_log, dt, st1, o_norm, heads=H)
+        b = TA.kda_decode_step(pr, ws, cs, f_b, g_b, A_log, dt, st2, o_norm, heads=H)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(st1, st2), t
+        assert torch.equal(c_all, torch.cat(cs, dim=1)), t
