@@ -242,23 +242,16 @@ struct KdaStepArgs {
   int H, V, R;
 };
 
-// Conv channel ch of the projection row (q channels, then k, then v): its section and index there.
-__device__ __forceinline__ int conv_section(int64_t ch, int64_t HK, int64_t& idx) {
-  const int sec = ch < HK ? 0 : (ch < 2 * HK ? 1 : 2);
-  idx = ch - (sec == 0 ? 0 : (sec == 1 ? HK : 2 * HK));
-  return sec;
-}
-
+// One step of a conv channel (index idx of its section, new input x): SiLU of the window after the shift,
+// rounded to bf16 as short_conv_kernel stores it.
 template <int W>
-__device__ __forceinline__ float conv_step(const KdaStepArgs& a, int64_t ch, int64_t HK) {
-  int64_t idx;
-  const int sec = conv_section(ch, HK, idx);
-  const uint2 cw = *reinterpret_cast<const uint2*>(a.cache[sec] + idx * W);
-  const uint2 ww = *reinterpret_cast<const uint2*>(a.conv_w[sec] + idx * W);
+__device__ __forceinline__ float conv_step(const uint16_t* cache, const uint16_t* weight, int64_t idx, uint16_t x) {
+  const uint2 cw = *reinterpret_cast<const uint2*>(cache + idx * W);
+  const uint2 ww = *reinterpret_cast<const uint2*>(weight + idx * W);
   static_assert(W == 4, "window of 4");
   // the window after the shift: cache[1..3], then the new input
   const float win[4] = {__uint_as_float(cw.x & 0xffff0000u), __uint_as_float(cw.y << 16),
-                        __uint_as_float(cw.y & 0xffff0000u), bf16_to_f32(a.pr[ch])};
+                        __uint_as_float(cw.y & 0xffff0000u), bf16_to_f32(x)};
   const float wt[4] = {__uint_as_float(ww.x << 16), __uint_as_float(ww.x & 0xffff0000u), __uint_as_float(ww.y << 16),
                        __uint_as_float(ww.y & 0xffff0000u)};
   float acc = 0.f;
@@ -267,47 +260,54 @@ __device__ __forceinline__ float conv_step(const KdaStepArgs& a, int64_t ch, int
   return round_bf16(silu(acc));
 }
 
-constexpr int kKdaMaxR = 256;
+constexpr int kKdaMaxR = 256;  // LoRA rank limit: one fa / ga element per thread of 256
 
-// LoRA up-projection of `rows` rows (row i at m + i * R, bf16, 16-byte aligned) with vec (fp32 in LDS, R
-// entries): out[i] = bf16(sum_r m[i, r] vec[r]), into LDS. Two neighbouring lanes share a row, each taking its
-// half in r order (one wave load covers 32 rows x 256 bytes at R = 128), and one shuffle adds the halves.
-// Whole workgroup (256 threads); ends with a barrier.
-__device__ __forceinline__ void lora_rows(const uint16_t* m, int rows, int R, const float* vec, float* out) {
-  const int half = threadIdx.x & 1, h2 = R / 2;
-  for (int i0 = 0; i0 < rows; i0 += 128) {
-    const int i = i0 + static_cast<int>(threadIdx.x >> 1);
-    const bool ok = i < rows;
-    const uint16_t* row = m + static_cast<int64_t>(ok ? i : 0) * R + half * h2;
-    float acc = 0.f;
-    int r0 = 0;
-    for (; r0 + 64 <= h2; r0 += 64) {
-      uint4 v[8];
+// LoRA up-projection rows (row i at m + i * R, bf16, 16-byte aligned) times vec (fp32 in LDS, R entries):
+// out[i] = bf16(sum_r m[i, r] vec[r]). R is taken in pieces of kLoraPiece; two neighbouring lanes share a row and
+// a piece, each taking its half of it in r order (one wave load covers 32 rows x 256 bytes), and one shuffle adds
+// the halves. lora_fetch issues a lane's loads for one piece, so that a kernel can issue its first piece with its
+// other loads at the start; lora_piece does the arithmetic once vec is in LDS.
+constexpr int kLoraPiece = 128;
+
+struct LoraPart {
+  uint4 v[kLoraPiece / 16];
+};
+
+__device__ __forceinline__ void lora_fetch(const uint16_t* m, int64_t i, bool ok, int R, int r0, LoraPart& lp) {
+  const int rh = r0 + (threadIdx.x & 1) * (kLoraPiece / 2);
+  const uint16_t* p = m + (ok ? i : 0) * R + rh;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const uint4*>(row + r0 + 8 * j);
+  for (int j = 0; j < kLoraPiece / 16; ++j)
+    lp.v[j] = ok && rh + 8 * j < R ? *reinterpret_cast<const uint4*>(p + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
+}
+
+__device__ __forceinline__ float lora_piece(const LoraPart& lp, const float* vec, int R, int r0, float acc) {
+  const int rh = r0 + (threadIdx.x & 1) * (kLoraPiece / 2);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t u[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-        const float* vv = vec + half * h2 + r0 + 8 * j;
+  for (int j = 0; j < kLoraPiece / 16; ++j) {
+    if (rh + 8 * j >= R) break;  // R is a multiple of 16: whole 8-element pieces
+    const uint32_t u[4] = {lp.v[j].x, lp.v[j].y, lp.v[j].z, lp.v[j].w};
+    const float* vv = vec + rh + 8 * j;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc = fmaf(__uint_as_float(u[q] << 16), vv[2 * q], acc);
-          acc = fmaf(__uint_as_float(u[q] & 0xffff0000u), vv[2 * q + 1], acc);
-        }
-      }
+    for (int q = 0; q < 4; ++q) {
+      acc = fmaf(__uint_as_float(u[q] << 16), vv[2 * q], acc);
+      acc = fmaf(__uint_as_float(u[q] & 0xffff0000u), vv[2 * q + 1], acc);
     }
-    for (; r0 < h2; r0 += 4) {  // R / 2 is a multiple of 4: 8-byte pieces
-      const uint2 v = *reinterpret_cast<const uint2*>(row + r0);
-      const float* vv = vec + half * h2 + r0;
-      acc = fmaf(__uint_as_float(v.x << 16), vv[0], acc);
-      acc = fmaf(__uint_as_float(v.x & 0xffff0000u), vv[1], acc);
-      acc = fmaf(__uint_as_float(v.y << 16), vv[2], acc);
-      acc = fmaf(__uint_as_float(v.y & 0xffff0000u), vv[3], acc);
-    }
-    acc += __shfl_xor(acc, 1, kWave);
-    if (ok && half == 0) out[i] = round_bf16(acc);
   }
-  __syncthreads();
+  return acc;
+}
+
+// One pass of 128 rows (i = i0 + threadIdx.x / 2) with its first piece already fetched into lp: the remaining
+// pieces are fetched here. Lanes of a row pair both hold the bf16-rounded result.
+__device__ __forceinline__ float lora_row(const uint16_t* m, int64_t i, bool ok, int R, const float* vec,
+                                          const LoraPart& first) {
+  float acc = lora_piece(first, vec, R, 0, 0.f);
+  for (int r0 = kLoraPiece; r0 < R; r0 += kLoraPiece) {
+    LoraPart lp;
+    lora_fetch(m, i, ok, R, r0, lp);
+    acc = lora_piece(lp, vec, R, r0, acc);
+  }
+  return round_bf16(acc + __shfl_xor(acc, 1, kWave));
 }
 
 template <int K, int W>
@@ -322,24 +322,34 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
   const int c = lane % CB, rg = lane / CB;
   const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
+  // every load is issued before the first barrier: fa, the first piece of the head's gate projections (row
+  // tid / 2 of K = 128), the state block, the conv windows and inputs, beta, dt_bias and A_log
+  const int64_t fa0 = 2 * HK + a.H * V;  // fa, then ga, then the beta logits
+  const uint16_t fa = a.pr[fa0 + min(tid, a.R - 1)];  // R <= 256: one element per thread
+  const uint16_t* fb = a.f_b + static_cast<int64_t>(h) * K * a.R;
+  LoraPart lp;
+  lora_fetch(fb, tid >> 1, true, a.R, 0, lp);
   float* st = a.state + static_cast<int64_t>(h) * K * V + col;
   float S[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
-  const int64_t fa0 = 2 * HK + a.H * V;  // fa, then ga, then the beta logits
-  for (int r = tid; r < a.R; r += 256) s_fa[r] = bf16_to_f32(a.pr[fa0 + r]);
-  const float vc = conv_step<W>(a, 2 * HK + static_cast<int64_t>(h) * V + col, HK);
+  const int64_t vi = static_cast<int64_t>(h) * V + col;
+  const float vc = conv_step<W>(a.cache[2], a.conv_w[2], vi, a.pr[2 * HK + vi]);
   float beta = bf16_to_f32(a.pr[fa0 + 2 * a.R + h]);
   beta = 1.f / (1.f + __expf(-beta));
   const bool chan = tid < K;  // whole waves
   const int64_t i = static_cast<int64_t>(h) * K + (chan ? tid : 0);
-  // the key channels' inputs are fetched with the rest, before the gate projections
-  const float qv = conv_step<W>(a, i, HK), kv = conv_step<W>(a, HK + i, HK), dtb = a.dt_bias[i];
+  const float qv = conv_step<W>(a.cache[0], a.conv_w[0], i, a.pr[i]);
+  const float kv = conv_step<W>(a.cache[1], a.conv_w[1], i, a.pr[HK + i]);
+  const float dtb = a.dt_bias[i], nA = __expf(a.A_log[h]);
+  if (tid < a.R) s_fa[tid] = bf16_to_f32(fa);
   __syncthreads();
-  lora_rows(a.f_b + static_cast<int64_t>(h) * K * a.R, K, a.R, s_fa, s_f);  // the head's gate projections
+  static_assert(K == 128, "one pass of 128 gate rows over 256 threads");
+  const float fv = lora_row(fb, tid >> 1, true, a.R, s_fa, lp);
+  if ((tid & 1) == 0) s_f[tid >> 1] = fv;
+  __syncthreads();
   if (chan) {
     const float x = s_f[tid] + dtb;
-    const float nA = __expf(a.A_log[h]);
     const float gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
     s_q[tid] = qv;
     s_k[tid] = kv;
@@ -391,58 +401,74 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
 
 // Grid H x 256: workgroup = head row (V <= 512 elements); its g projections go through LDS, then wave 0 norms the
 // row (8 elements per lane); the threads of the whole grid then shift the conv windows of all 2 H K + H V channels.
+// Every global load is issued before the first barrier, unconditionally (indices clamped into range, the values
+// past the end unused), so the kernel waits on memory once before its LDS work.
 template <int W>
 __global__ __launch_bounds__(256) void kda_out_kernel(KdaStepArgs a, int K) {
   __shared__ float s_ga[kKdaMaxR], s_g[512];
   static_assert(W == 4, "window of 4");
-  constexpr int kShift = 4;  // conv channels a thread shifts at most (grids of H workgroups, H >= ceil(C / 1024))
   const int tid = threadIdx.x, lane = lane_id();
-  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K;
-  const int64_t ga0 = 2 * HK + a.H * V + a.R;
-  const int64_t C = 2 * HK + a.H * V;
+  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K, HV = static_cast<int64_t>(a.H) * V;
+  const int64_t ga0 = 2 * HK + HV + a.R;
   const int64_t row = blockIdx.x;
-  // every load up front: this thread's conv windows and new inputs, the row to norm (wave 0), ga
-  const int64_t nthr = static_cast<int64_t>(gridDim.x) * 256, c0 = row * 256 + tid;
-  uint2 cw[kShift];
-  uint32_t xin[kShift];
+  // this thread's conv channels, section by section (the section's cache pointer stays uniform): with H x 256
+  // threads, K = 128 and V <= 512, one q channel, one k channel and up to two v channels
+  const int64_t nthr = static_cast<int64_t>(gridDim.x) * 256, t0 = row * 256 + tid;
+  constexpr int kItems = 4;
+  uint2 cw[kItems];
+  uint32_t xin[kItems];
 #pragma unroll
-  for (int j = 0; j < kShift; ++j) {
-    const int64_t ch = c0 + j * nthr;
-    int64_t idx;
-    const int sec = conv_section(ch < C ? ch : 0, HK, idx);
-    cw[j] = ch < C ? *reinterpret_cast<const uint2*>(a.cache[sec] + idx * W) : make_uint2(0u, 0u);
-    xin[j] = ch < C ? a.pr[ch] : 0u;
+  for (int j = 0; j < kItems; ++j) {
+    const int sec = j < 2 ? j : 2;
+    const int64_t idx = t0 + (j == 3 ? nthr : 0), n = sec == 2 ? HV : HK;
+    const int64_t ic = idx < n ? idx : n - 1;
+    cw[j] = *reinterpret_cast<const uint2*>(a.cache[sec] + ic * W);
+    xin[j] = a.pr[sec * HK + ic];
   }
-  float xv[8], ss = 0.f;
+  // the row to norm and the norm weights (every wave loads them; wave 0 uses them), ga, the g projections' first
+  // piece for rows tid / 2
+  uint16_t yr[8], nr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t ic = min(static_cast<int64_t>(lane + kWave * j), V - 1);
+    yr[j] = a.y[row * V + ic];
+    nr[j] = a.o_norm[ic];
+  }
+  const uint16_t ga = a.pr[ga0 + min(tid, a.R - 1)];  // R <= 256: one element per thread
+  const uint16_t* gb = a.g_b + row * V * a.R;
+  LoraPart lp;
+  lora_fetch(gb, tid >> 1, tid >> 1 < V, a.R, 0, lp);
+  if (tid < a.R) s_ga[tid] = bf16_to_f32(ga);
+  __syncthreads();
+  for (int i0 = 0; i0 < V; i0 += 128) {
+    const int i = i0 + (tid >> 1);
+    if (i0 > 0) lora_fetch(gb, i, i < V, a.R, 0, lp);
+    const float gv = lora_row(gb, i, i < V, a.R, s_ga, lp);
+    if ((tid & 1) == 0 && i < V) s_g[i] = gv;
+  }
+  __syncthreads();
   if (tid < kWave) {
+    float xv[8], ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int i = lane + kWave * j;
-      xv[j] = i < V ? bf16_to_f32(a.y[row * V + i]) : 0.f;
+      xv[j] = lane + kWave * j < V ? bf16_to_f32(yr[j]) : 0.f;
       ss = fmaf(xv[j], xv[j], ss);
     }
-  }
-  for (int r = tid; r < a.R; r += 256) s_ga[r] = bf16_to_f32(a.pr[ga0 + r]);
-  __syncthreads();
-  lora_rows(a.g_b + row * V * a.R, static_cast<int>(V), a.R, s_ga, s_g);
-  if (tid < kWave) {
     const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = lane + kWave * j;
-      if (i < V) a.y[row * V + i] = f32_to_bf16(xv[j] * rstd * bf16_to_f32(a.o_norm[i]) / (1.f + __expf(-s_g[i])));
+      if (i < V) a.y[row * V + i] = f32_to_bf16(xv[j] * rstd * bf16_to_f32(nr[j]) / (1.f + __expf(-s_g[i])));
     }
   }
   // conv windows: drop the oldest input, append this token's
 #pragma unroll
-  for (int j = 0; j < kShift; ++j) {
-    const int64_t ch = c0 + j * nthr;
-    if (ch < C) {
-      int64_t idx;
-      const int sec = conv_section(ch, HK, idx);
+  for (int j = 0; j < kItems; ++j) {
+    const int sec = j < 2 ? j : 2;
+    const int64_t idx = t0 + (j == 3 ? nthr : 0), n = sec == 2 ? HV : HK;
+    if (idx < n)
       *reinterpret_cast<uint2*>(a.cache[sec] + idx * W) =
           make_uint2((cw[j].x >> 16) | (cw[j].y << 16), (cw[j].y >> 16) | (xin[j] << 16));
-    }
   }
 }
 
@@ -723,8 +749,6 @@ extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* co
   MM_REQUIRE(K == 128 && V % kKdaCols == 0 && V >= kKdaCols && V <= 512,
              "kda_decode_step: head dims K=%lld (128), V=%lld (a multiple of 16 up to 512)", (long long)K, (long long)V);
   MM_REQUIRE(W == 4, "kda_decode_step: conv window %lld (4)", (long long)W);
-  MM_REQUIRE(2 * K + V <= 4 * 256, "kda_decode_step: 2 K + V = %lld conv channels per head, at most 1024",
-             (long long)(2 * K + V));
   MM_REQUIRE(R >= 16 && R <= kKdaMaxR && R % 16 == 0, "kda_decode_step: LoRA rank %lld (a multiple of 16 up to %d)",
              (long long)R, kKdaMaxR);
   MM_REQUIRE(pr_len == 2 * H * K + H * V + 2 * R + H,
