@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 8
+#define MM_ABI_VERSION 9
 
 /* status codes */
 #define MM_OK 0
@@ -345,6 +345,20 @@ int64_t mm_mla_attn_workspace(int nh, int dv, int64_t max_len);
 int mm_mla_decode_attn(const void* q, const void* k_new, const void* v_new, int nh, int dqk, int dv, void* k_cache,
                        void* v_cache, int64_t max_len, const void* pos, int pos_dtype, float scale, void* out,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- The two ends of a greedy decode step (engine.py:685-689). */
+
+/* out[i, :] = table[ids[i], :] for i < n: word_embeddings(tok_buf) (engine.py:686). table [V, H] and out rows of
+ * bf16 / fp16 / fp32 (dtype), 16-byte aligned rows, H * element size a multiple of 16; ids MM_INT32 / MM_INT64 [n]
+ * on the device. An id outside [0, V) gives a row of zeros (torch's embedding stops on a device-side assert). */
+int mm_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t table_row_stride, const void* ids,
+                  int ids_dtype, int64_t n, void* out, int64_t out_row_stride, void* stream);
+
+/* out[r] = logits[r].argmax() (engine.py:688, logits.argmax(-1)) for each of `rows` rows of n elements (bf16 or
+ * fp32, x_row_stride elements apart): torch's order, the largest value, NaN above every number, the lowest index
+ * among equals. out: int64 [rows] on the device. */
+int mm_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t x_row_stride, int64_t* out,
+                   void* stream);
 
 /* ---- Expert ingestion from safetensors shards (engine.py:126-188, direct_load.py:81-131). */
 

@@ -1,0 +1,155 @@
+// The two ends of a greedy decode step (engine.py:685-689): the embedding lookup of the previous token
+// (word_embeddings(tok_buf)) and the greedy pick logits.argmax(-1) written back for the next step.
+//
+//   embed_rows_kernel   out[i] = table[ids[i]] (a row copy in 16-byte pieces; an id outside [0, V) gives a row
+//                       of zeros, where torch's embedding would stop on a device-side assert).
+//   argmax_rows_kernel  one workgroup of 1024 threads per row: every 16-byte load of the row is issued before
+//                       the first comparison (one trip to memory), then the (value, index) pairs are reduced
+//                       lane -> wave -> workgroup. torch.argmax's order: the largest value, NaN above every
+//                       number, the lowest index among equals; so the result does not depend on the
+//                       reduction's shape.
+#include "mm_common.h"
+
+namespace {
+
+using namespace mmd;
+
+// (v, i) beats (bv, bi) in torch.argmax's order
+__device__ __forceinline__ bool beats(float v, int64_t i, float bv, int64_t bi) {
+  const bool vn = isnan(v), bn = isnan(bv);
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void take(float& bv, int64_t& bi, float v, int64_t i) {
+  if (beats(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+constexpr int kArgThreads = 1024;
+constexpr int kArgLoads = 16;  // 16-byte loads in flight per thread
+
+// VEC: rows 16-byte aligned and n a multiple of the elements per 16 bytes; otherwise one element per load.
+template <bool F32, bool VEC>
+__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const void* __restrict__ x, int64_t n, int64_t rs,
+                                                                  int64_t* __restrict__ out) {
+  __shared__ float s_v[kArgThreads / kWave];
+  __shared__ int64_t s_i[kArgThreads / kWave];
+  constexpr int EPC = F32 ? 4 : 8;  // elements per 16-byte chunk
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  float bv = -INFINITY;
+  int64_t bi = n;  // no index yet: any element at index < n with the same value wins
+  if constexpr (VEC) {
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * rs * (F32 ? 4 : 2));
+    const int64_t nch = n / EPC;
+    for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(kArgThreads) * kArgLoads) {
+      uint4 v[kArgLoads];
+#pragma unroll
+      for (int j = 0; j < kArgLoads; ++j) {
+        const int64_t c = c0 + tid + static_cast<int64_t>(kArgThreads) * j;
+        v[j] = xr[c < nch ? c : nch - 1];  // clamped: the value is not used past the end
+      }
+#pragma unroll
+      for (int j = 0; j < kArgLoads; ++j) {
+        const int64_t c = c0 + tid + static_cast<int64_t>(kArgThreads) * j;
+        if (c >= nch) break;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if constexpr (F32) {
+            take(bv, bi, __uint_as_float(w[q]), c * EPC + q);
+          } else {
+            take(bv, bi, __uint_as_float(w[q] << 16), c * EPC + 2 * q);
+            take(bv, bi, __uint_as_float(w[q] & 0xffff0000u), c * EPC + 2 * q + 1);
+          }
+        }
+      }
+    }
+  } else {
+    const char* xr = static_cast<const char*>(x) + row * rs * (F32 ? 4 : 2);
+    for (int64_t i = tid; i < n; i += kArgThreads) {
+      const float v = F32 ? reinterpret_cast<const float*>(xr)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(xr)[i]);
+      take(bv, bi, v, i);
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const float ov = __shfl_xor(bv, m, kWave);
+    const int64_t oi = __shfl_xor(bi, m, kWave);
+    take(bv, bi, ov, oi);
+  }
+  if (lane == 0) {
+    s_v[wave] = bv;
+    s_i[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgThreads / kWave; ++w) take(bv, bi, s_v[w], s_i[w]);
+    out[row] = bi;
+  }
+}
+
+// Grid (pieces of a row / 256, rows): thread = one 16-byte piece of the output row.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint4* __restrict__ table, int64_t V, int64_t pieces,
+                                                         int64_t trs, const void* ids, int ids_dtype,
+                                                         uint4* __restrict__ out, int64_t ors) {
+  const int64_t i = blockIdx.y;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= pieces) return;
+  const int64_t id = load_id(ids, ids_dtype, i);
+  const bool ok = id >= 0 && id < V;
+  out[i * ors + c] = ok ? table[id * trs + c] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+int dtype_bytes(int dt) { return dt == MM_FP32 ? 4 : (dt == MM_BF16 || dt == MM_FP16 ? 2 : 0); }
+
+}  // namespace
+
+extern "C" int mm_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t x_row_stride, int64_t* out,
+                              void* stream) {
+  MM_REQUIRE(x_dtype == MM_BF16 || x_dtype == MM_FP32, "argmax_rows: x must be bf16 or fp32");
+  MM_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && n >= 1 && n < (1LL << 40),
+             "argmax_rows: rows=%lld, n=%lld (n >= 1)", (long long)rows, (long long)n);
+  MM_REQUIRE(x_row_stride >= n || rows <= 1, "argmax_rows: row stride %lld smaller than n=%lld", (long long)x_row_stride,
+             (long long)n);
+  MM_REQUIRE(x && out, "argmax_rows: null pointer");
+  if (rows == 0) return MM_OK;
+  hipStream_t st = MM_STREAM(stream);
+  const bool f32 = x_dtype == MM_FP32;
+  const int es = f32 ? 4 : 2, epc = 16 / es;
+  const bool vec = mm::aligned16(x) && (x_row_stride * es) % 16 == 0 && n % epc == 0;
+  const dim3 grid(static_cast<unsigned>(rows)), block(kArgThreads);
+  if (f32) {
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<true, true>), grid, block, 0, st, x, n, x_row_stride, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<true, false>), grid, block, 0, st, x, n, x_row_stride, out);
+  } else {
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<false, true>), grid, block, 0, st, x, n, x_row_stride, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<false, false>), grid, block, 0, st, x, n, x_row_stride, out);
+  }
+  return mm::check_launch("argmax_rows");
+}
+
+extern "C" int mm_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t table_row_stride,
+                             const void* ids, int ids_dtype, int64_t n, void* out, int64_t out_row_stride,
+                             void* stream) {
+  const int es = dtype_bytes(dtype);
+  MM_REQUIRE(es > 0, "embed_rows: table must be bf16, fp16 or fp32");
+  MM_REQUIRE(ids_dtype == MM_INT32 || ids_dtype == MM_INT64, "embed_rows: ids must be int32 or int64");
+  MM_REQUIRE(V >= 1 && H >= 1 && n >= 0 && n <= 65535, "embed_rows: V=%lld, H=%lld, n=%lld (n <= 65535)",
+             (long long)V, (long long)H, (long long)n);
+  MM_REQUIRE(table_row_stride >= H && out_row_stride >= H, "embed_rows: row stride smaller than H");
+  MM_REQUIRE(table && ids && out, "embed_rows: null pointer");
+  MM_REQUIRE(mm::aligned16(table) && mm::aligned16(out) && (H * es) % 16 == 0 && (table_row_stride * es) % 16 == 0 &&
+                 (out_row_stride * es) % 16 == 0,
+             "embed_rows: table and out rows must be 16-byte aligned and H * element size a multiple of 16");
+  if (n == 0) return MM_OK;
+  const int64_t pieces = H * es / 16;
+  hipStream_t st = MM_STREAM(stream);
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256), static_cast<unsigned>(n)),
+                     dim3(256), 0, st, static_cast<const uint4*>(table), V, pieces, table_row_stride * es / 16, ids,
+                     ids_dtype, static_cast<uint4*>(out), out_row_stride * es / 16);
+  return mm::check_launch("embed_rows");
+}

@@ -10,6 +10,8 @@ static cache.
                         recurrence, the gated norm) in two kernels instead of the five calls above
   mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
                         masked softmax attention over positions 0..pos
+  embed_rows            word_embeddings(tok_buf), the input row of a decode step (engine.py:686)
+  argmax_rows           logits.argmax(-1), the greedy pick a decode step writes back (engine.py:688)
 Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
 passed in); there is no CPU path.
 """
@@ -20,7 +22,7 @@ import torch
 import _mingmoe as _mm
 
 __all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
-           "mla_attn_workspace"]
+           "mla_attn_workspace", "embed_rows", "argmax_rows"]
 
 
 def _f32_or_bf16(t, name):
@@ -254,4 +256,53 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None
                                          _mm.ptr(v_cache), max_len, _mm.ptr(pos), _mm.dtype_code(pos), sc, _mm.ptr(y),
                                          _mm.ptr(ws), ws.numel() * ws.element_size(), _mm.stream_of(q)),
                   "mla_decode_attn")
+    return y
+
+
+def embed_rows(table, ids, *, out=None):
+    """word_embeddings(ids) (engine.py:686) for a bf16 / fp16 / fp32 table [V, H] with 16-byte aligned rows and
+    device ids (int64 / int32, any shape of n elements): returns out [*ids.shape, H], out[i] = table[ids[i]]. An id
+    outside [0, V) gives a row of zeros, where torch's embedding stops on a device-side assert."""
+    _mm.require_gpu(table, ids, out)
+    if table.dim() != 2 or table.stride(1) != 1:
+        raise ValueError("embed_rows: table must be [V, H] with contiguous rows")
+    if table.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise ValueError("embed_rows: table must be bf16, fp16 or fp32")
+    if ids.dtype not in (torch.int64, torch.int32):
+        raise ValueError("embed_rows: ids must be int64 or int32")
+    V, H = table.shape
+    idf = ids.reshape(-1)
+    if not idf.is_contiguous():
+        idf = idf.contiguous()
+    n = idf.numel()
+    shape = (*ids.shape, H)
+    y = torch.empty(shape, device=table.device, dtype=table.dtype) if out is None else out
+    if tuple(y.shape) != shape or y.dtype != table.dtype or not y.is_contiguous():
+        raise ValueError(f"embed_rows: out must be a contiguous {table.dtype} tensor of shape {shape}")
+    lib = _mm.load()
+    with _mm.on_device(table):
+        _mm.check(lib.mm_embed_rows(_mm.ptr(table), _mm.dtype_code(table), V, H, table.stride(0), _mm.ptr(idf),
+                                    _mm.dtype_code(idf), n, _mm.ptr(y), H, _mm.stream_of(table)), "embed_rows")
+    return y
+
+
+def argmax_rows(logits, *, out=None):
+    """logits.argmax(-1) (engine.py:688) over the last dim of bf16 / fp32 logits [..., n] (last dim contiguous):
+    torch's order, the largest value, NaN above every number, the lowest index among equals. Returns int64
+    [...]; out: an int64 device tensor with one element per row (e.g. the [1, 1] token buffer), written in place."""
+    _mm.require_gpu(logits, out)
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("argmax_rows: logits must be bf16 or fp32")
+    n = logits.shape[-1]
+    x2 = logits.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    y = torch.empty(logits.shape[:-1], device=logits.device, dtype=torch.int64) if out is None else out
+    if y.dtype != torch.int64 or y.numel() != rows or not y.is_contiguous():
+        raise ValueError(f"argmax_rows: out must be a contiguous int64 tensor of {rows} elements")
+    lib = _mm.load()
+    with _mm.on_device(logits):
+        _mm.check(lib.mm_argmax_rows(_mm.ptr(x2), _mm.dtype_code(x2), rows, n, x2.stride(0) if rows > 1 else n,
+                                     _mm.ptr(y), _mm.stream_of(logits)), "argmax_rows")
     return y

@@ -264,8 +264,10 @@ class HybridThinkerStep:
     The real model's projection internals (the rotary part of q / k, the latent kv compression) are not modelled:
     q, k and v come straight from one GEMV. Shapes beyond the configs' hidden 2048 (head counts, dims, the 3:1 mix)
     are an assumption. Weights ~ N(0, 0.02) (norm weights 1 + N(0, 0.02), A_log, dt_bias ~ N(0, 0.5), conv ~
-    N(0, 0.5)); the caches hold a context of `pos` tokens (random rows, states ~ N(0, 0.1)). Calling the object
-    runs one step and returns the logits [1, vocab]."""
+    N(0, 0.5)); the caches hold a context of `pos` tokens (random rows, states ~ N(0, 0.1)).
+    A step is greedy decoding's (engine.py:685-689): the input row is the word embedding [vocab, 2048] (~ N(0, 1))
+    of the token in `tok` [1, 1] (int64, on the device), and the step writes the argmax of its logits back there.
+    Calling the object runs one step and returns the logits [1, vocab]."""
 
     def __init__(self, layers=28, device="cuda", vocab=VOCAB, max_len=1024, pos=512, mla_every=4, seed=5000,
                  fused_kda=True):
@@ -302,7 +304,9 @@ class HybridThinkerStep:
                 p["o"] = w((H, kd), 31)
                 p["state"] = w((1, KDA_HEADS, KDA_DIM, KDA_DIM), 32, std=0.1, dtype=torch.float32)
             self.L.append(p)
-        self.x0 = tokens(1, seed=seed + 1, device=dev)
+        self.embed = normal((vocab, H), 1.0, seed + 1, dev)
+        self.tok = torch.tensor([[(seed * 7919) % vocab]], device=dev, dtype=torch.long)
+        self.h_in = torch.empty(1, 1, H, device=dev, dtype=torch.bfloat16)
         self.pos = torch.tensor([pos], device=dev, dtype=torch.long)
         self.ws = TA.mla_attn_workspace(MLA_HEADS, MLA_V, max_len, dev)
 
@@ -334,20 +338,26 @@ class HybridThinkerStep:
         on = TA.rms_norm_gated(o.reshape(KDA_HEADS, KDA_DIM), gg.reshape(KDA_HEADS, KDA_DIM), p["o_norm"], 1e-5)
         return small_linear(on.reshape(1, kd), p["o"], residual=h)
 
+    def embed_token(self):
+        """word_embeddings(tok) -> the step's input row [1, 2048] (a view of a buffer the step owns)."""
+        return self.TA.embed_rows(self.embed, self.tok, out=self.h_in)[0]
+
     def __call__(self):
         from fastlinear import small_linear
         m = self.moe
-        h = self.x0
+        h = self.embed_token()
         for p in self.L:
             h = m.layer_moe(p["blk"], self.mixer(p, h))
         logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
+        self.TA.argmax_rows(logits, out=self.tok)
         self.pos.add_(1)
         return logits
 
     def bytes_per_step(self, pos=None):
         """HBM bytes one step must read or write at position pos (default: the current one): every weight of the
         mixers, the KDA states (read + written) and conv caches, the MLA cache rows 0..pos, the 7 experts and
-        router of every MoE block, the LM head."""
+        router of every MoE block, the embedding row, the LM head and its logits (written, then read by the
+        argmax)."""
         pos = int(self.pos) if pos is None else pos
         H, kd, total = HIDDEN, KDA_HEADS * KDA_DIM, 0
         for p in self.L:
@@ -358,25 +368,28 @@ class HybridThinkerStep:
                 total += (p["proj"].numel() + p["f_b"].numel() + p["g_b"].numel() + p["o"].numel()) * 2
                 total += p["conv_w"].numel() * 2 + 2 * p["conv"].numel() * 2 + 2 * p["state"].numel() * 4
             total += H * 2 + (TOP_K + 1) * expert_bytes() + EXPERTS * H * 4
-        return total + self.moe.head.numel() * 2
+        vocab = self.moe.head.shape[0]
+        return total + H * 2 + self.moe.head.numel() * 2 + 2 * vocab * 2
 
     def state_copy(self):
-        """A copy of the step's mutable state: KDA states and conv caches, MLA caches, the position."""
+        """A copy of the step's mutable state: KDA states and conv caches, MLA caches, the position, the token."""
         keys = ("state", "conv", "kc", "vc")
-        return {"pos": self.pos.clone(), "L": [{k: p[k].clone() for k in keys if k in p} for p in self.L]}
+        return {"pos": self.pos.clone(), "tok": self.tok.clone(),
+                "L": [{k: p[k].clone() for k in keys if k in p} for p in self.L]}
 
     def trace(self):
         """The step run eagerly, keeping per layer (input, mixer output, router ids, weights); returns that list
         and the logits. The state advances as in a call."""
         from fastlinear import small_linear
         m = self.moe
-        h, out = self.x0, []
+        h, out = self.embed_token(), []
         for p in self.L:
             h_in = h.clone()
             hm = self.mixer(p, h)
             h = m.layer_moe(p["blk"], hm)
             out.append((h_in, hm.clone(), m.ids.clone(), m.wts.clone()))
         logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
+        self.TA.argmax_rows(logits, out=self.tok)
         self.pos.add_(1)
         return out, h, logits
 

@@ -105,6 +105,12 @@ def test_argument_validation_reports_messages():
     assert "slot 5" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
     ex.w_dtype = mm.MM_INT8
     assert "needs fp32 or bf16 scales" in _err(lib.mm_ingest_experts(items, 1, ctypes.byref(ex), P, P, 1 << 20, 2))
+    assert "bf16 or fp32" in _err(lib.mm_argmax_rows(P, mm.MM_INT8, 1, 64, 64, P, None))
+    assert "n=0" in _err(lib.mm_argmax_rows(P, mm.MM_BF16, 1, 0, 64, P, None))
+    assert "row stride" in _err(lib.mm_argmax_rows(P, mm.MM_FP32, 2, 64, 32, P, None))
+    assert "int32 or int64" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 64, 64, P, mm.MM_FP32, 1, P, 64, None))
+    assert "16-byte aligned" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 12, 12, P, mm.MM_INT64, 1, P, 12, None))
+    assert "bf16, fp16 or fp32" in _err(lib.mm_embed_rows(P, mm.MM_INT8, 100, 64, 64, P, mm.MM_INT64, 1, P, 64, None))
 
 
 def test_wrappers_refuse_cpu_tensors():

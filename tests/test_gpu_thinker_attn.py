@@ -218,6 +218,7 @@ def test_hybrid_step_graph_replays_equal_eager_steps():
         assert torch.equal(out, want), i
         a, b = eager.state_copy(), graphed.state_copy()
         assert torch.equal(a["pos"], b["pos"]) and int(b["pos"]) == 101 + i
+        assert torch.equal(a["tok"], b["tok"]) and int(b["tok"]) == int(out.float().cpu().argmax()), i
         for la, lb in zip(a["L"], b["L"]):
             for key in la:
                 assert torch.equal(la[key], lb[key]), (i, key)
@@ -259,7 +260,10 @@ def test_hybrid_step_layers_match_the_oracle():
     print("[hybrid] 4 layers vs oracle", flush=True)
     step = W.HybridThinkerStep(4, DEV, pos=200, seed=7100)
     before = step.state_copy()
-    trace, _, _ = step.trace()
+    trace, _, logits = step.trace()
+    # the step's two ends: its input is the embedding row of the token, the argmax of its logits the next token
+    assert torch.equal(trace[0][0].cpu(), step.embed[int(before["tok"])].cpu()[None])
+    assert int(step.tok) == int(logits.float().cpu().argmax())
     for li, (p, st, (h_in, hm, ids, wts)) in enumerate(zip(step.L, before["L"], trace)):
         want = _oracle_mixer(p, st, h_in.cpu(), 200)
         d = (hm.float().cpu() - want.float()).abs()
@@ -356,3 +360,48 @@ def test_kda_decode_step_takes_the_three_caches_of_the_reference_layout():
         torch.cuda.synchronize()
         assert torch.equal(a, b) and torch.equal(st1, st2), t
         assert torch.equal(c_all, torch.cat(cs, dim=1)), t
+
+
+# ------------------------------------------------------------------------ the two ends of a decode step
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_argmax_rows_matches_torch_argmax(dtype):
+    """argmax_rows against torch.argmax on the CPU (the reference's logits.argmax(-1)): random rows of lengths that
+    take the vector and the scalar paths (the LM head's 126464 among them), planted ties (the first index wins),
+    NaN (above every number, the first one wins), rows of -inf, all-equal rows and a row offset by one element."""
+    print(f"[argmax] {dtype}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    for n in (1, 7, 8, 64, 1000, 1003, 126464):
+        x = torch.randn(5, n, generator=g).to(dtype)
+        if n > 1:
+            x[1, n // 3] = x[1, n - 1] = x[1].max() + 1  # a tie: the first wins
+            x[2, n // 2] = float("nan")
+            x[2, n - 1] = float("nan")
+        x[3] = float("-inf")
+        x[4] = 0.5
+        got = TA.argmax_rows(x.to(DEV)).cpu()
+        assert torch.equal(got, x.argmax(-1)), (n, got, x.argmax(-1))
+        if n > 8:  # rows not 16-byte aligned: the scalar path
+            xv = x.to(DEV)[:, 1:]
+            assert torch.equal(TA.argmax_rows(xv).cpu(), x[:, 1:].argmax(-1)), n
+    tok = torch.zeros(1, 1, dtype=torch.long, device=DEV)
+    x = torch.randn(1, 126464, generator=g).to(dtype)
+    TA.argmax_rows(x.to(DEV), out=tok)
+    assert int(tok) == int(x.argmax())
+
+
+@pytest.mark.parametrize("dtype,id_dtype", [(torch.bfloat16, torch.int64), (torch.float32, torch.int32)])
+def test_embed_rows_matches_index_select(dtype, id_dtype):
+    """embed_rows against index_select (word_embeddings of engine.py:686), bit for bit, with an id outside the
+    table giving a row of zeros."""
+    print(f"[embed] {dtype} {id_dtype}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    V, H = 1000, 2048
+    table = torch.randn(V, H, generator=g).to(dtype)
+    ids = torch.tensor([[3], [999], [0], [3]], dtype=id_dtype)
+    got = TA.embed_rows(table.to(DEV), ids.to(DEV)).cpu()
+    assert got.shape == (4, 1, H) and torch.equal(got, table[ids.long()])
+    bad = TA.embed_rows(table.to(DEV), torch.tensor([V, -1], dtype=id_dtype, device=DEV)).cpu()
+    assert torch.equal(bad, torch.zeros(2, H, dtype=dtype))
+    with pytest.raises(ValueError, match="int64 or int32"):
+        TA.embed_rows(table.to(DEV), torch.zeros(1, device=DEV))
