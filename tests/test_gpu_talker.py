@@ -90,8 +90,12 @@ def test_decode_attn_talker_shape(pos):
 
 @pytest.mark.parametrize("nh,nkv,hd,max_len,pos", [(16, 16, 128, 200, 130), (16, 1, 32, 100, 99),
                                                    (12, 2, 128, 4096, 4000), (8, 4, 256, 300, 257),
-                                                   (6, 2, 96, 129, 128), (7, 7, 64, 1, 0)])
+                                                   (6, 2, 96, 129, 128), (7, 7, 64, 1, 0),
+                                                   (14, 2, 64, 2048, 1500), (14, 2, 64, 1025, 1024),
+                                                   (4, 2, 32, 1024, 1023)])
 def test_decode_attn_shapes(nh, nkv, hd, max_len, pos):
+    """Head dims 32-256, GQA groups 1-16, caches of 1 to 4096 positions (a partial last chunk, pos at a chunk
+    edge and at the cache end)."""
     print(f"decode_attn nh={nh} nkv={nkv} hd={hd} max_len={max_len} pos={pos}", flush=True)
     qkv, kc, vc, inv_freq = _decode_inputs(nh, nkv, hd, max_len, 40 + hd)
     got, kd, vd = _run_decode(qkv, kc, vc, pos, inv_freq, nh, nkv, hd, pos_dtype=torch.int32)
