@@ -14,18 +14,27 @@ namespace {
 
 using namespace mmd;
 
-// (v, i) beats (bv, bi) in torch.argmax's order
-__device__ __forceinline__ bool beats(float v, int64_t i, float bv, int64_t bi) {
-  const bool vn = isnan(v), bn = isnan(bv);
-  if (vn || bn) return vn && (!bn || i < bi);
-  return v > bv || (v == bv && i < bi);
+// (v, i) beats (bv, bi) in torch.argmax's order: the larger value, NaN above every number, the lower index
+// among equals (and among NaNs). Branch-free.
+__device__ __forceinline__ bool beats(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  const bool num = !vn && !bn && (v > bv || (v == bv && i < bi));
+  return num || (vn && (!bn || i < bi));
 }
 
-__device__ __forceinline__ void take(float& bv, int64_t& bi, float v, int64_t i) {
-  if (beats(v, i, bv, bi)) {
-    bv = v;
-    bi = i;
-  }
+// A thread's scan visits indices in increasing order, so a later element wins only when strictly larger or the
+// first NaN; bi < 0 marks "nothing yet".
+__device__ __forceinline__ void scan(float& bv, int& bi, float v, int i) {
+  const bool vn = v != v, bn = bv != bv;
+  const bool b = bi < 0 || (vn ? !bn : (!bn && v > bv));
+  bv = b ? v : bv;
+  bi = b ? i : bi;
+}
+
+__device__ __forceinline__ void merge(float& bv, int& bi, float v, int i) {
+  const bool b = i >= 0 && (bi < 0 || beats(v, i, bv, bi));
+  bv = b ? v : bv;
+  bi = b ? i : bi;
 }
 
 constexpr int kArgThreads = 1024;
@@ -33,53 +42,53 @@ constexpr int kArgLoads = 16;  // 16-byte loads in flight per thread
 
 // VEC: rows 16-byte aligned and n a multiple of the elements per 16 bytes; otherwise one element per load.
 template <bool F32, bool VEC>
-__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const void* __restrict__ x, int64_t n, int64_t rs,
+__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const void* __restrict__ x, int n, int64_t rs,
                                                                   int64_t* __restrict__ out) {
   __shared__ float s_v[kArgThreads / kWave];
-  __shared__ int64_t s_i[kArgThreads / kWave];
+  __shared__ int s_i[kArgThreads / kWave];
   constexpr int EPC = F32 ? 4 : 8;  // elements per 16-byte chunk
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-  float bv = -INFINITY;
-  int64_t bi = n;  // no index yet: any element at index < n with the same value wins
+  float bv = 0.f;
+  int bi = -1;
   if constexpr (VEC) {
     const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * rs * (F32 ? 4 : 2));
-    const int64_t nch = n / EPC;
-    for (int64_t c0 = 0; c0 < nch; c0 += static_cast<int64_t>(kArgThreads) * kArgLoads) {
+    const int nch = n / EPC;
+    for (int c0 = 0; c0 < nch; c0 += kArgThreads * kArgLoads) {
       uint4 v[kArgLoads];
 #pragma unroll
       for (int j = 0; j < kArgLoads; ++j) {
-        const int64_t c = c0 + tid + static_cast<int64_t>(kArgThreads) * j;
+        const int c = c0 + tid + kArgThreads * j;
         v[j] = xr[c < nch ? c : nch - 1];  // clamped: the value is not used past the end
       }
 #pragma unroll
       for (int j = 0; j < kArgLoads; ++j) {
-        const int64_t c = c0 + tid + static_cast<int64_t>(kArgThreads) * j;
-        if (c >= nch) break;
-        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const int c = c0 + tid + kArgThreads * j;
+        if (c < nch) {  // uniform for all but the last chunks
+          const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if constexpr (F32) {
-            take(bv, bi, __uint_as_float(w[q]), c * EPC + q);
-          } else {
-            take(bv, bi, __uint_as_float(w[q] << 16), c * EPC + 2 * q);
-            take(bv, bi, __uint_as_float(w[q] & 0xffff0000u), c * EPC + 2 * q + 1);
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (F32) {
+              scan(bv, bi, __uint_as_float(w[q]), c * EPC + q);
+            } else {
+              scan(bv, bi, __uint_as_float(w[q] << 16), c * EPC + 2 * q);
+              scan(bv, bi, __uint_as_float(w[q] & 0xffff0000u), c * EPC + 2 * q + 1);
+            }
           }
         }
       }
     }
   } else {
     const char* xr = static_cast<const char*>(x) + row * rs * (F32 ? 4 : 2);
-    for (int64_t i = tid; i < n; i += kArgThreads) {
-      const float v = F32 ? reinterpret_cast<const float*>(xr)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(xr)[i]);
-      take(bv, bi, v, i);
-    }
+    for (int i = tid; i < n; i += kArgThreads)
+      scan(bv, bi, F32 ? reinterpret_cast<const float*>(xr)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(xr)[i]),
+           i);
   }
 #pragma unroll
   for (int m = 1; m < kWave; m <<= 1) {
     const float ov = __shfl_xor(bv, m, kWave);
-    const int64_t oi = __shfl_xor(bi, m, kWave);
-    take(bv, bi, ov, oi);
+    const int oi = __shfl_xor(bi, m, kWave);
+    merge(bv, bi, ov, oi);
   }
   if (lane == 0) {
     s_v[wave] = bv;
@@ -87,7 +96,7 @@ __global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const void* __
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < kArgThreads / kWave; ++w) take(bv, bi, s_v[w], s_i[w]);
+    for (int w = 1; w < kArgThreads / kWave; ++w) merge(bv, bi, s_v[w], s_i[w]);
     out[row] = bi;
   }
 }
@@ -111,8 +120,8 @@ int dtype_bytes(int dt) { return dt == MM_FP32 ? 4 : (dt == MM_BF16 || dt == MM_
 extern "C" int mm_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t x_row_stride, int64_t* out,
                               void* stream) {
   MM_REQUIRE(x_dtype == MM_BF16 || x_dtype == MM_FP32, "argmax_rows: x must be bf16 or fp32");
-  MM_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && n >= 1 && n < (1LL << 40),
-             "argmax_rows: rows=%lld, n=%lld (n >= 1)", (long long)rows, (long long)n);
+  MM_REQUIRE(rows >= 0 && rows <= 0x7fffffffLL && n >= 1 && n <= 0x7fffffffLL,
+             "argmax_rows: rows=%lld, n=%lld (1 <= n < 2^31)", (long long)rows, (long long)n);
   MM_REQUIRE(x_row_stride >= n || rows <= 1, "argmax_rows: row stride %lld smaller than n=%lld", (long long)x_row_stride,
              (long long)n);
   MM_REQUIRE(x && out, "argmax_rows: null pointer");
@@ -123,11 +132,11 @@ extern "C" int mm_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t 
   const bool vec = mm::aligned16(x) && (x_row_stride * es) % 16 == 0 && n % epc == 0;
   const dim3 grid(static_cast<unsigned>(rows)), block(kArgThreads);
   if (f32) {
-    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<true, true>), grid, block, 0, st, x, n, x_row_stride, out);
-    else hipLaunchKernelGGL((argmax_rows_kernel<true, false>), grid, block, 0, st, x, n, x_row_stride, out);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<true, true>), grid, block, 0, st, x, static_cast<int>(n), x_row_stride, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<true, false>), grid, block, 0, st, x, static_cast<int>(n), x_row_stride, out);
   } else {
-    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<false, true>), grid, block, 0, st, x, n, x_row_stride, out);
-    else hipLaunchKernelGGL((argmax_rows_kernel<false, false>), grid, block, 0, st, x, n, x_row_stride, out);
+    if (vec) hipLaunchKernelGGL((argmax_rows_kernel<false, true>), grid, block, 0, st, x, static_cast<int>(n), x_row_stride, out);
+    else hipLaunchKernelGGL((argmax_rows_kernel<false, false>), grid, block, 0, st, x, static_cast<int>(n), x_row_stride, out);
   }
   return mm::check_launch("argmax_rows");
 }
