@@ -113,7 +113,9 @@ constexpr int row_group(int NC) { return NC <= 2 ? 8 : NC <= 4 ? 4 : NC <= 8 ? 2
 // GLU (R = 2): the wave's two rows are gate row p and up row p + N of a [2N, K] weight, and the output is
 // y[:, p] = bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections: small_linear followed by
 // silu_mul (fast_talker.py:258-260), bit for bit, without the [M, 2N] intermediate.
-template <int NC, int R, bool NORM, bool GLU, int MG>
+// SPLIT: each workgroup takes the one token group blockIdx.y of a grid with a y row per group; otherwise it
+// takes every group in turn.
+template <int NC, int R, bool NORM, bool GLU, int MG, bool SPLIT = false>
 __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, const uint16_t* __restrict__ norm_g,
                                                                  float norm_eps) {
   static_assert(!GLU || R == 2, "GLU pairs a gate row with an up row");
@@ -166,9 +168,12 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
   uint4 xfirst[NC];
   if constexpr (kPrefetch) {
 #pragma unroll
-    for (int j = 0; j < NC; ++j) xfirst[j] = *reinterpret_cast<const uint4*>(a.x + cc[j] * 8);
+    for (int j = 0; j < NC; ++j)
+      xfirst[j] = *reinterpret_cast<const uint4*>(a.x + (SPLIT ? static_cast<int64_t>(blockIdx.y) * MG * a.xs : 0) +
+                                                  cc[j] * 8);
   }
-  for (int m0 = 0; m0 < kMaxM; m0 += MG) {
+  const int mfirst = SPLIT ? static_cast<int>(blockIdx.y) * MG : 0;
+  for (int m0 = mfirst; m0 < kMaxM; m0 += MG) {
     if (m0 >= a.M) break;  // uniform
     const int e_m = min(m0 + e_mm, a.M - 1);
     const float res =
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
         const uint16_t* xr = a.x + min(m0 + mm, a.M - 1) * a.xs;
 #pragma unroll
         for (int j = 0; j < NC; ++j)
-          xg[mm][j] = (kPrefetch && m0 == 0) ? xfirst[j] : *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
+          xg[mm][j] = (kPrefetch && m0 == mfirst) ? xfirst[j] : *reinterpret_cast<const uint4*>(xr + cc[j] * 8);
       }
     }
     float keep = 0.f, keep_up = 0.f;
@@ -243,6 +248,7 @@ __global__ __launch_bounds__(256) void small_linear_1pass_kernel(LinArgs a, cons
         a.y[m * a.ys + e_n] = f32_to_bf16(v);
       }
     }
+    if constexpr (SPLIT) break;  // this workgroup's one group
   }
 }
 
@@ -292,7 +298,20 @@ __global__ __launch_bounds__(256) void small_linear_kernel(LinArgs a) {
 
 template <int NC, int R, bool GLU, int MG>
 void launch_1pass_mg(const LinArgs& a, const uint16_t* g, float eps, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(GLU ? (a.N + 3) / 4 : (a.N + 4 * R - 1) / (4 * R)));
+  // Several token groups run in parallel workgroups (grid y) when the whole grid fits on the GPU at once: the
+  // workgroups of one row block then read its weights together (one HBM read), where one workgroup taking the
+  // groups in turn leaves a single wave per SIMD working through them serially. Larger grids keep one y row,
+  // since workgroups of the same rows that are not resident together would each stream the weights.
+  const unsigned gx = static_cast<unsigned>(GLU ? (a.N + 3) / 4 : (a.N + 4 * R - 1) / (4 * R));
+  const unsigned ng = static_cast<unsigned>((a.M + MG - 1) / MG);
+  const bool split = ng > 1 && static_cast<int64_t>(gx) * ng <= static_cast<int64_t>(4) * mm::cu_count();
+  if (split) {
+    const dim3 grid(gx, ng);
+    if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, true, GLU, MG, true>), grid, dim3(256), 0, st, a, g, eps);
+    else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, false, GLU, MG, true>), grid, dim3(256), 0, st, a, g, eps);
+    return;
+  }
+  const dim3 grid(gx);
   if (g) hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, true, GLU, MG>), grid, dim3(256), 0, st, a, g, eps);
   else hipLaunchKernelGGL((small_linear_1pass_kernel<NC, R, false, GLU, MG>), grid, dim3(256), 0, st, a, g, eps);
 }
