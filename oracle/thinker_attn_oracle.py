@@ -1,7 +1,7 @@
 """CPU oracle of the thinker's attention mixers (KDA and MLA layers) — TEST INFRASTRUCTURE ONLY.
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, as the checker; the
-product path (ming-voice_amd/) never calls it.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only to check
+results against; the product path (ming-voice_amd/) never calls it.
 
 The KDA functions restate the published algorithm of fla-core 0.5.2 (requirements.txt:11), which the reference calls
 (engine.py:242-262) and which is not in the reference tree: the recurrent form of Kimi delta attention
