@@ -601,22 +601,39 @@ __global__ __launch_bounds__(256) void mla_split_kernel(MlaArgs a) {
 }
 
 // One workgroup of 4 waves per head merges the chunks 0 .. pos / 32: the max of the maxima (lanes over chunks),
-// then wave w rescales and sums chunks w, w + 4, ... (lane = value dimension), the 4 waves' sums added in LDS.
+// then wave w rescales and sums chunks w, w + 4, ... in that order (lane = value dimension), the 4 waves' sums
+// added in LDS. The chunk states a wave needs for the first kMergeBatch of its chunks and the maxima of the first
+// 256 chunks are loaded before pos arrives (chunks clamped into the workspace, the ones past pos dropped by
+// selects), so the kernel waits for memory about once; longer prefixes load the rest afterwards.
 // A position outside [0, max_len) writes NaN (and the split kernel wrote nothing).
+constexpr int kMergeBatch = 8;  // chunks per wave loaded ahead: 4 waves x 8 x 32 positions = 1024 positions
+
 template <int NDV>
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
   __shared__ float s_acc[4][kWave * NDV], s_l[4], s_m[4];
   const int h = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
+  const int64_t cs = a.dv + 2;
+  const float* base = a.ws + static_cast<int64_t>(h) * a.nc * cs;
+  // loads that do not depend on pos
+  const float m_first = base[static_cast<int64_t>(min(tid, a.nc - 1)) * cs + a.dv];
+  float pm[kMergeBatch], pl[kMergeBatch], pv[kMergeBatch][NDV];
+#pragma unroll
+  for (int b = 0; b < kMergeBatch; ++b) {
+    const float* p = base + static_cast<int64_t>(min(wave + 4 * b, a.nc - 1)) * cs;
+    pm[b] = p[a.dv];
+    pl[b] = p[a.dv + 1];
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) pv[b][j] = p[min(lane + kWave * j, a.dv - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // pos (a scalar load) after the vector loads
   const int64_t pos = load_pos64(a.pos, a.pos_dtype);
   if (pos < 0 || pos >= a.max_len) {
     for (int d = tid; d < a.dv; d += 256) a.out[static_cast<int64_t>(h) * a.dv + d] = 0x7fc0;  // NaN
     return;
   }
   const int n = static_cast<int>(pos / kMlaChunk) + 1;
-  const int64_t cs = a.dv + 2;
-  const float* base = a.ws + static_cast<int64_t>(h) * a.nc * cs;
-  float mx = -INFINITY;
-  for (int c = tid; c < n; c += 256) mx = fmaxf(mx, base[c * cs + a.dv]);
+  float mx = tid < n ? m_first : -INFINITY;
+  for (int c = tid + 256; c < n; c += 256) mx = fmaxf(mx, base[c * cs + a.dv]);
   mx = wave_max(mx);
   if (lane == 0) s_m[wave] = mx;
   __syncthreads();
@@ -624,8 +641,19 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
   float acc[NDV], l = 0.f;
 #pragma unroll
   for (int j = 0; j < NDV; ++j) acc[j] = 0.f;
-#pragma unroll 4
-  for (int c = wave; c < n; c += 4) {
+#pragma unroll
+  for (int b = 0; b < kMergeBatch; ++b) {
+    if (wave + 4 * b < n) {  // uniform
+      const float wgt = __expf(pm[b] - m);
+      l = fmaf(pl[b], wgt, l);
+#pragma unroll
+      for (int j = 0; j < NDV; ++j) {
+        const int d = lane + kWave * j;
+        if (d < a.dv) acc[j] = fmaf(pv[b][j], wgt, acc[j]);
+      }
+    }
+  }
+  for (int c = wave + 4 * kMergeBatch; c < n; c += 4) {
     const float* p = base + c * cs;
     const float wgt = __expf(p[a.dv] - m);
     l = fmaf(p[a.dv + 1], wgt, l);

@@ -110,8 +110,10 @@ def test_rms_norm_gated_matches_oracle():
 
 
 @pytest.mark.parametrize("nh,dq,dv,L", [(16, 192, 128, 1024), (4, 64, 64, 300), (2, 96, 32, 70), (3, 72, 40, 100),
-                                        (2, 512, 256, 90), (1, 8, 8, 33)])
+                                        (2, 512, 256, 90), (1, 8, 8, 33), (2, 64, 64, 2048), (1, 32, 32, 9000)])
 def test_mla_decode_attn_matches_oracle(nh, dq, dv, L):
+    """Positions at chunk edges and the cache end; caches past 1024 positions take the merge's chunks beyond its
+    loaded-ahead batch, past 8192 its maxima beyond the first 256 chunks."""
     kc = W.normal((1, nh, L, dq), 1.0, 420, DEV)
     vc = W.normal((1, nh, L, dv), 1.0, 421, DEV)
     for pos in sorted({p for p in (0, 1, 31, 32, 33, 63, 64, 65, L // 2, L - 1) if p < L}):
