@@ -337,7 +337,7 @@ def hybrid_decode_metrics(stream, layers=28, pos=456):
     total = step.bytes_per_step(pos + 56)
     kda = sum(p["kind"] == "kda" for p in step.L)
     # the same step with each KDA core as the five-call chain (short_conv, the f / g projections,
-    # fused_recurrent_kda, rms_norm_gated) instead of kda_decode_step's two kernels, same process and box
+    # fused_recurrent_kda, rms_norm_gated) instead of kda_decode_step's one kernel, same process and box
     step.fused_kda = False
     ms_chain = median_graph_ms(graph_of(step, stream), stream)
     out = {"layers": layers, "kda_layers": kda, "mla_layers": layers - kda, "positions": [pos + 3, pos + 110],

@@ -317,14 +317,14 @@ int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache
 int mm_rms_norm_gated(const void* x, int64_t x_rs, const void* g, int64_t g_rs, const void* w, int64_t rows, int64_t n,
                       float eps, void* y, int64_t y_rs, void* stream);
 
-/* One decode token of a KDA layer's core in two kernels: the chain mm_short_conv (q, k, v; SiLU) ->
+/* One decode token of a KDA layer's core in one kernel: the chain mm_short_conv (q, k, v; SiLU) ->
  * f = bf16(f_b . fa) -> mm_kda_recurrent (l2-normed q / k, the in-kernel gate, beta as logits) -> g = bf16(g_b . ga)
  * -> mm_rms_norm_gated of engine.py:242-265 for one token, on the layer's projection row
  * pr = [q | k (H K each) | v (H V) | fa | ga (R each) | beta logits (H)] (bf16, pr_len elements). conv_w[3] and
  * conv_cache[3]: the q, k and v conv weights ([C, 1, W] as the conv1d modules hold them) and the layer's three conv
  * caches ([1, C, W], shifted in place), C = H K, H K, H V, bf16, 8-byte aligned; f_b [H K, R], g_b [H V, R] bf16 (LoRA
- * up-projections); A_log [H], dt_bias [H K] fp32; state [H, K, V] fp32, updated in place; o_norm [V] bf16;
- * y [H, V] bf16 out. K = 128, V a multiple of 16 up to 512, W = 4, R a multiple of 16 up to 256. No single call of
+ * up-projections); A_log [H], dt_bias [H K] fp32; state [H, K, V] fp32 (16-byte aligned), updated in place;
+ * o_norm [V] bf16; y [H, V] bf16 out. K = 128, V a multiple of 16 up to 512, W = 4, R a multiple of 16 up to 256. No single call of
  * the reference does this: it fuses the five launches of one KDA layer step; results equal the chain's except
  * where the f / g dots round differently in the last bf16 place. */
 int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* const* conv_w, void* const* conv_cache, int64_t W,

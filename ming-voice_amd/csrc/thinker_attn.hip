@@ -9,6 +9,8 @@
 //   short_conv_kernel      the depthwise causal convolution of ShortConvolution's step form (a cache of the last W
 //                          inputs per channel), SiLU, T tokens in order.
 //   rms_norm_gated_kernel  FusedRMSNormGated with a sigmoid gate: bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)).
+//   kda_token_kernel       one decode token of a KDA layer's core (the three above plus the gate's LoRA
+//                          up-projections) in one launch, one workgroup per head.
 //   mla_split_kernel / mla_merge_kernel
 //                          single-token attention of an MLA layer over its static cache (engine.py:523-548: k, v
 //                          [heads, max_len, d], rows written at the position with index_copy_): the new k, v rows
@@ -209,26 +211,28 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
   }
 }
 
-// ------------------------------------------------------------------------- one KDA decode token, two kernels
+// ------------------------------------------------------------------------------ one KDA decode token, one kernel
 //
 // The per-token core of a KDA layer (engine.py:242-263: the q/k/v short convolutions, the gate's LoRA up-projection
-// f = f_b . fa, beta, fused_recurrent_kda, then g = g_b . ga and the gated output norm) in two launches instead of
-// five, on the layer's projection row pr = [q | k (H K each) | v (H V) | fa | ga (R each) | beta logits (H)]:
-//   kda_step_kernel  grid (V / 16, H): the head's K key channels and the block's 16 value columns are convolved
-//                    over their cached windows (SiLU, rounded to bf16 as short_conv_kernel stores them), each key
-//                    channel's gate f = bf16(sum_r f_b[ch, r] fa[r]), beta = sigmoid(logit); then one
-//                    token of kda_recurrent_kernel's recurrence. The output goes to y.
-//   kda_out_kernel   one workgroup per head row: g = bf16(sum_r g_b[ch, r] ga[r]), y = rms_norm_gated(y, g) in
-//                    place (each lane reads its elements before writing them); then every conv window shifts in the
-//                    row's inputs. The shift waits for this second kernel because all V / 16 workgroups of a head
-//                    read the head's q and k windows in the first.
-// Same arithmetic as the five kernels except the order of the f and g dots (two lanes per row here, each over
-// its half in order; small_linear reduces over more lanes), so f and g can differ in the last bf16 place.
+// f = f_b . fa, beta, fused_recurrent_kda, then g = g_b . ga and the gated output norm) in one launch instead of
+// five, on the layer's projection row pr = [q | k (H K each) | v (H V) | fa | ga (R each) | beta logits (H)].
+// kda_token_kernel: one workgroup of 16 waves per head, so every step that needs the whole head (the l2 norms over
+// the key channels, the output norm over the value columns, the conv windows of the head's channels) stays inside
+// the workgroup:
+//   - the head's K key channels and V value channels are convolved over their cached windows (SiLU, rounded to
+//     bf16 as short_conv_kernel stores them) and the windows shift in this token's inputs;
+//   - f = bf16(sum_r f_b[ch, r] fa[r]) per key channel and g = bf16(sum_r g_b[ch, r] ga[r]) per value column
+//     (two lanes per LoRA row, each over its half of R in order, one shuffle);
+//   - one token of kda_recurrent_kernel's recurrence, column block by column block (four waves per block of 16
+//     value columns, the sums over key rows in kda_recurrent_kernel's order);
+//   - y = rms_norm_gated(bf16(o), g).
+// Same arithmetic as the five kernels except the order of the f and g dots (small_linear reduces over more
+// lanes), so f and g can differ in the last bf16 place.
 
 struct KdaStepArgs {
   const uint16_t* pr;         // projection row
   const uint16_t* conv_w[3];  // q, k [H K, W] and v [H V, W] conv weights
-  uint16_t* cache[3];         // the q, k and v conv caches of the same shapes, shifted by kda_out_kernel
+  uint16_t* cache[3];         // the q, k and v conv caches of the same shapes, shifted in place
   const uint16_t* f_b;     // [H K, R]
   const uint16_t* g_b;     // [H V, R]
   const float* A_log;      // [H]
@@ -238,18 +242,13 @@ struct KdaStepArgs {
   float* state;            // [H, K, V] fp32, updated in place
   const uint16_t* o_norm;  // [V]
   float eps;
-  uint16_t* y;             // [H, V]: the recurrence output, then the normed output
+  uint16_t* y;             // [H, V]: the normed output
   int H, V, R;
 };
 
-// One step of a conv channel (index idx of its section, new input x): SiLU of the window after the shift,
-// rounded to bf16 as short_conv_kernel stores it.
-template <int W>
-__device__ __forceinline__ float conv_step(const uint16_t* cache, const uint16_t* weight, int64_t idx, uint16_t x) {
-  const uint2 cw = *reinterpret_cast<const uint2*>(cache + idx * W);
-  const uint2 ww = *reinterpret_cast<const uint2*>(weight + idx * W);
-  static_assert(W == 4, "window of 4");
-  // the window after the shift: cache[1..3], then the new input
+// SiLU of a conv channel's window after the shift (cache cw[1..3], then the new input x), rounded to bf16 as
+// short_conv_kernel stores it; ww the channel's 4 weights.
+__device__ __forceinline__ float conv4(uint2 cw, uint2 ww, uint16_t x) {
   const float win[4] = {__uint_as_float(cw.x & 0xffff0000u), __uint_as_float(cw.y << 16),
                         __uint_as_float(cw.y & 0xffff0000u), bf16_to_f32(x)};
   const float wt[4] = {__uint_as_float(ww.x << 16), __uint_as_float(ww.x & 0xffff0000u), __uint_as_float(ww.y << 16),
@@ -258,6 +257,11 @@ __device__ __forceinline__ float conv_step(const uint16_t* cache, const uint16_t
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc = fmaf(wt[j], win[j], acc);
   return round_bf16(silu(acc));
+}
+
+// The window after this token: the oldest input dropped, x appended.
+__device__ __forceinline__ uint2 conv4_shift(uint2 cw, uint16_t x) {
+  return make_uint2((cw.x >> 16) | (cw.y << 16), (cw.y >> 16) | (static_cast<uint32_t>(x) << 16));
 }
 
 constexpr int kKdaMaxR = 256;  // LoRA rank limit: one fa / ga element per thread of 256
@@ -297,8 +301,8 @@ __device__ __forceinline__ float lora_piece(const LoraPart& lp, const float* vec
   return acc;
 }
 
-// One pass of 128 rows (i = i0 + threadIdx.x / 2) with its first piece already fetched into lp: the remaining
-// pieces are fetched here. Lanes of a row pair both hold the bf16-rounded result.
+// One row (i, shared by the lane pair threadIdx.x / 2) with its first piece already fetched into lp: the
+// remaining pieces are fetched here. Both lanes of the pair hold the bf16-rounded result.
 __device__ __forceinline__ float lora_row(const uint16_t* m, int64_t i, bool ok, int R, const float* vec,
                                           const LoraPart& first) {
   float acc = lora_piece(first, vec, R, 0, 0.f);
@@ -310,43 +314,93 @@ __device__ __forceinline__ float lora_row(const uint16_t* m, int64_t i, bool ok,
   return round_bf16(acc + __shfl_xor(acc, 1, kWave));
 }
 
-template <int K, int W>
-__global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
-  constexpr int CB = kKdaCols, RPT = K / 16;
-  static_assert(K % kWave == 0 && K <= 256, "kda key dim");
-  __shared__ float s_q[K], s_k[K], s_dec[K], s_fa[kKdaMaxR], s_f[K];
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// v + v of lane ^ m, element by element
+__device__ __forceinline__ float4 xor_add4(float4 v, int m) {
+  return make_float4(v.x + __shfl_xor(v.x, m, kWave), v.y + __shfl_xor(v.y, m, kWave), v.z + __shfl_xor(v.z, m, kWave),
+                     v.w + __shfl_xor(v.w, m, kWave));
+}
+
+constexpr int kKdaThreads = 512;
+
+// Grid H x 512 threads, K = 128, V <= 128 NP. Wave w, lane (rg = lane / 16, c4 = lane % 16): row group w4 = w % 4
+// and column half hf = w / 4; in pass p the lane holds state rows r = 16 i + 4 w4 + rg (i < 8) of the four columns
+// 128 p + 64 hf + 4 c4 .. + 3 (one 16-byte load per row). Each column's sums over rows keep kda_recurrent_kernel's
+// order: lane-internal over i, then over the 4 row groups of a wave (xor 16, then 32), then over the 4 waves of
+// its half through LDS. Threads 0..255 take the f rows (K of them, a lane pair each), threads 256..511 the g rows,
+// 128 per pass; threads < K the q and k channels, threads < V the v channels. Every global load is issued before
+// the first barrier; column groups past V read zeros and write nothing (buffer bounds).
+template <int NP>
+__global__ __launch_bounds__(kKdaThreads) void kda_token_kernel(KdaStepArgs a) {
+  constexpr int K = 128, RPT = K / 16, NV = 128 * NP;
+  __shared__ float s_fga[2 * kKdaMaxR], s_f[K], s_q[K], s_k[K], s_dec[K], s_g[NV], s_vc[NV], s_nr[NV];
   __shared__ float s_red[K / kWave][2];
-  __shared__ float part_u[4][CB], part_o[4][CB];
-  const int h = blockIdx.y;
+  __shared__ float4 part_u[NP][2][4][16], part_o[NP][2][4][16];
+  __shared__ uint16_t s_o[NV];
+  const int h = blockIdx.x;
   const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
-  const int c = lane % CB, rg = lane / CB;
-  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
-  // every load is issued before the first barrier: fa, the first piece of the head's gate projections (row
-  // tid / 2 of K = 128), the state block, the conv windows and inputs, beta, dt_bias and A_log
-  const int64_t fa0 = 2 * HK + a.H * V;  // fa, then ga, then the beta logits
-  const uint16_t fa = a.pr[fa0 + min(tid, a.R - 1)];  // R <= 256: one element per thread
-  const uint16_t* fb = a.f_b + static_cast<int64_t>(h) * K * a.R;
+  const int rg = lane / 16, c4 = lane % 16, w4 = w % 4, hf = w / 4;
+  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K, HV = static_cast<int64_t>(a.H) * V;
+  const int64_t fa0 = 2 * HK + HV;  // fa, then ga, then the beta logits
+  // fa (threads 0..255) and ga (256..511): R <= 256, one element per thread
+  const int sec = tid >> 8, j8 = tid & 255;
+  const uint16_t fga = a.pr[fa0 + sec * a.R + min(j8, a.R - 1)];
+  // the first piece of this lane pair's f row (threads < 256) or g row
+  const bool frow = tid < 256;
+  const int gi0 = (tid - 256) >> 1;
+  const uint16_t* lm = frow ? a.f_b + static_cast<int64_t>(h) * K * a.R : a.g_b + static_cast<int64_t>(h) * V * a.R;
   LoraPart lp;
-  lora_fetch(fb, tid >> 1, true, a.R, 0, lp);
-  float* st = a.state + static_cast<int64_t>(h) * K * V + col;
-  float S[RPT];
+  lora_fetch(lm, frow ? tid >> 1 : gi0, frow || gi0 < V, a.R, 0, lp);
+  // the state rows of this lane's columns, through a resource over the head's [K, V] block (32-bit offsets)
+  const rsrc_t srs = make_rsrc(a.state + static_cast<int64_t>(h) * K * V, static_cast<int64_t>(K) * V * 4);
+  const uint32_t rstep = 16u * static_cast<uint32_t>(V) * 4u;
+  uint32_t soff[NP];
+  float4 S[NP][RPT];
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
-  const int64_t vi = static_cast<int64_t>(h) * V + col;
-  const float vc = conv_step<W>(a.cache[2], a.conv_w[2], vi, a.pr[2 * HK + vi]);
+  for (int p = 0; p < NP; ++p) {
+    const int col = 128 * p + 64 * hf + 4 * c4;
+    soff[p] = col < V ? (static_cast<uint32_t>(4 * w4 + rg) * static_cast<uint32_t>(V) + col) * 4u : kPast;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) S[p][i] = __builtin_bit_cast(float4, buf16(srs, soff[p] + i * rstep));
+  }
+  // conv channels: q and k channel tid (tid < K), v channel tid (tid < V); indices clamped, results unused past
+  // the end
+  const int64_t iq = static_cast<int64_t>(h) * K + min(tid, K - 1), iv = static_cast<int64_t>(h) * V + min<int64_t>(tid, V - 1);
+  const uint2 cwq = *reinterpret_cast<const uint2*>(a.cache[0] + iq * 4), wq = *reinterpret_cast<const uint2*>(a.conv_w[0] + iq * 4);
+  const uint2 cwk = *reinterpret_cast<const uint2*>(a.cache[1] + iq * 4), wk = *reinterpret_cast<const uint2*>(a.conv_w[1] + iq * 4);
+  const uint2 cwv = *reinterpret_cast<const uint2*>(a.cache[2] + iv * 4), wv = *reinterpret_cast<const uint2*>(a.conv_w[2] + iv * 4);
+  const uint16_t xq = a.pr[iq], xk = a.pr[HK + iq], xv = a.pr[2 * HK + iv];
+  const float dtb = a.dt_bias[iq], nA = __expf(a.A_log[h]);
+  const uint16_t nrm = a.o_norm[min<int64_t>(tid, V - 1)];  // the output norm's weight of column tid
   float beta = bf16_to_f32(a.pr[fa0 + 2 * a.R + h]);
+
+  const bool chan = tid < K, vchan = tid < V;
+  const float qv = conv4(cwq, wq, xq), kv = conv4(cwk, wk, xk);
+  if (chan) {
+    *reinterpret_cast<uint2*>(a.cache[0] + iq * 4) = conv4_shift(cwq, xq);
+    *reinterpret_cast<uint2*>(a.cache[1] + iq * 4) = conv4_shift(cwk, xk);
+  }
+  if (vchan) {
+    s_vc[tid] = conv4(cwv, wv, xv);
+    s_nr[tid] = bf16_to_f32(nrm);
+    *reinterpret_cast<uint2*>(a.cache[2] + iv * 4) = conv4_shift(cwv, xv);
+  }
+  if (j8 < a.R) s_fga[sec * kKdaMaxR + j8] = bf16_to_f32(fga);
   beta = 1.f / (1.f + __expf(-beta));
-  const bool chan = tid < K;  // whole waves
-  const int64_t i = static_cast<int64_t>(h) * K + (chan ? tid : 0);
-  const float qv = conv_step<W>(a.cache[0], a.conv_w[0], i, a.pr[i]);
-  const float kv = conv_step<W>(a.cache[1], a.conv_w[1], i, a.pr[HK + i]);
-  const float dtb = a.dt_bias[i], nA = __expf(a.A_log[h]);
-  if (tid < a.R) s_fa[tid] = bf16_to_f32(fa);
   __syncthreads();
-  static_assert(K == 128, "one pass of 128 gate rows over 256 threads");
-  const float fv = lora_row(fb, tid >> 1, true, a.R, s_fa, lp);
-  if ((tid & 1) == 0) s_f[tid >> 1] = fv;
+  if (frow) {
+    static_assert(K == 128, "one pass of 128 f rows over 256 threads");
+    const float fv = lora_row(lm, tid >> 1, true, a.R, s_fga, lp);
+    if ((tid & 1) == 0) s_f[tid >> 1] = fv;
+  } else {
+    for (int i0 = 0; i0 < V; i0 += 128) {  // wave-uniform trip count
+      const int i = i0 + gi0;
+      if (i0 > 0) lora_fetch(lm, i, i < V, a.R, 0, lp);
+      const float gv = lora_row(lm, i, i < V, a.R, s_fga + kKdaMaxR, lp);
+      if ((tid & 1) == 0 && i < V) s_g[i] = gv;
+    }
+  }
   __syncthreads();
   if (chan) {
     const float x = s_f[tid] + dtb;
@@ -368,107 +422,84 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepArgs a) {
     sk += s_red[j][1];
   }
   const float qs = a.scale / sqrtf(sq + 1e-6f), ks = 1.f / sqrtf(sk + 1e-6f);
-  float pu = 0.f;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = 16 * i + 4 * w + rg;
-    S[i] *= s_dec[r];
-    pu = fmaf(s_k[r] * ks, S[i], pu);
-  }
-  pu += __shfl_xor(pu, 16, kWave);
-  pu += __shfl_xor(pu, 32, kWave);
-  if (rg == 0) part_u[w][c] = pu;
-  __syncthreads();
-  const float u = (vc - (((part_u[0][c] + part_u[1][c]) + part_u[2][c]) + part_u[3][c])) * beta;
-  float po = 0.f;
+  for (int p = 0; p < NP; ++p) {
+    float4 pu = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = 16 * i + 4 * w + rg;
-    S[i] = fmaf(s_k[r] * ks, u, S[i]);
-    po = fmaf(s_q[r] * qs, S[i], po);
-  }
-  po += __shfl_xor(po, 16, kWave);
-  po += __shfl_xor(po, 32, kWave);
-  if (rg == 0) part_o[w][c] = po;
-  __syncthreads();
-  if (w == 0 && rg == 0) {
-    const float o = ((part_o[0][c] + part_o[1][c]) + part_o[2][c]) + part_o[3][c];
-    a.y[static_cast<int64_t>(h) * V + col] = f32_to_bf16(o);
-  }
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) st[static_cast<int64_t>(16 * i + 4 * w + rg) * V] = S[i];
-}
-
-// Grid H x 256: workgroup = head row (V <= 512 elements); its g projections go through LDS, then wave 0 norms the
-// row (8 elements per lane); the threads of the whole grid then shift the conv windows of all 2 H K + H V channels.
-// Every global load is issued before the first barrier, unconditionally (indices clamped into range, the values
-// past the end unused), so the kernel waits on memory once before its LDS work.
-template <int W>
-__global__ __launch_bounds__(256) void kda_out_kernel(KdaStepArgs a, int K) {
-  __shared__ float s_ga[kKdaMaxR], s_g[512];
-  static_assert(W == 4, "window of 4");
-  const int tid = threadIdx.x, lane = lane_id();
-  const int64_t V = a.V, HK = static_cast<int64_t>(a.H) * K, HV = static_cast<int64_t>(a.H) * V;
-  const int64_t ga0 = 2 * HK + HV + a.R;
-  const int64_t row = blockIdx.x;
-  // this thread's conv channels, section by section (the section's cache pointer stays uniform): with H x 256
-  // threads, K = 128 and V <= 512, one q channel, one k channel and up to two v channels
-  const int64_t nthr = static_cast<int64_t>(gridDim.x) * 256, t0 = row * 256 + tid;
-  constexpr int kItems = 4;
-  uint2 cw[kItems];
-  uint32_t xin[kItems];
-#pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const int sec = j < 2 ? j : 2;
-    const int64_t idx = t0 + (j == 3 ? nthr : 0), n = sec == 2 ? HV : HK;
-    const int64_t ic = idx < n ? idx : n - 1;
-    cw[j] = *reinterpret_cast<const uint2*>(a.cache[sec] + ic * W);
-    xin[j] = a.pr[sec * HK + ic];
-  }
-  // the row to norm and the norm weights (every wave loads them; wave 0 uses them), ga, the g projections' first
-  // piece for rows tid / 2
-  uint16_t yr[8], nr[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int64_t ic = min(static_cast<int64_t>(lane + kWave * j), V - 1);
-    yr[j] = a.y[row * V + ic];
-    nr[j] = a.o_norm[ic];
-  }
-  const uint16_t ga = a.pr[ga0 + min(tid, a.R - 1)];  // R <= 256: one element per thread
-  const uint16_t* gb = a.g_b + row * V * a.R;
-  LoraPart lp;
-  lora_fetch(gb, tid >> 1, tid >> 1 < V, a.R, 0, lp);
-  if (tid < a.R) s_ga[tid] = bf16_to_f32(ga);
-  __syncthreads();
-  for (int i0 = 0; i0 < V; i0 += 128) {
-    const int i = i0 + (tid >> 1);
-    if (i0 > 0) lora_fetch(gb, i, i < V, a.R, 0, lp);
-    const float gv = lora_row(gb, i, i < V, a.R, s_ga, lp);
-    if ((tid & 1) == 0 && i < V) s_g[i] = gv;
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w4 + rg;
+      const float d = s_dec[r], kk = s_k[r] * ks;
+      S[p][i].x *= d;
+      S[p][i].y *= d;
+      S[p][i].z *= d;
+      S[p][i].w *= d;
+      pu.x = fmaf(kk, S[p][i].x, pu.x);
+      pu.y = fmaf(kk, S[p][i].y, pu.y);
+      pu.z = fmaf(kk, S[p][i].z, pu.z);
+      pu.w = fmaf(kk, S[p][i].w, pu.w);
+    }
+    pu = xor_add4(pu, 16);
+    pu = xor_add4(pu, 32);
+    if (rg == 0) part_u[p][hf][w4][c4] = pu;
   }
   __syncthreads();
-  if (tid < kWave) {
-    float xv[8], ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int col = 128 * p + 64 * hf + 4 * c4;
+    const float4 u0 = part_u[p][hf][0][c4], u1 = part_u[p][hf][1][c4], u2 = part_u[p][hf][2][c4], u3 = part_u[p][hf][3][c4];
+    const float4 u = make_float4((s_vc[col] - (((u0.x + u1.x) + u2.x) + u3.x)) * beta,
+                                 (s_vc[col + 1] - (((u0.y + u1.y) + u2.y) + u3.y)) * beta,
+                                 (s_vc[col + 2] - (((u0.z + u1.z) + u2.z) + u3.z)) * beta,
+                                 (s_vc[col + 3] - (((u0.w + u1.w) + u2.w) + u3.w)) * beta);
+    float4 po = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w4 + rg;
+      const float kk = s_k[r] * ks, qq = s_q[r] * qs;
+      S[p][i].x = fmaf(kk, u.x, S[p][i].x);
+      S[p][i].y = fmaf(kk, u.y, S[p][i].y);
+      S[p][i].z = fmaf(kk, u.z, S[p][i].z);
+      S[p][i].w = fmaf(kk, u.w, S[p][i].w);
+      po.x = fmaf(qq, S[p][i].x, po.x);
+      po.y = fmaf(qq, S[p][i].y, po.y);
+      po.z = fmaf(qq, S[p][i].z, po.z);
+      po.w = fmaf(qq, S[p][i].w, po.w);
+    }
+    po = xor_add4(po, 16);
+    po = xor_add4(po, 32);
+    if (rg == 0) part_o[p][hf][w4][c4] = po;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, S[p][i]), srs, static_cast<int>(soff[p] + i * rstep), 0, 0);
+  }
+  __syncthreads();
+  if (w4 == 0 && rg == 0) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int col = 128 * p + 64 * hf + 4 * c4;
+      const float4 o0 = part_o[p][hf][0][c4], o1 = part_o[p][hf][1][c4], o2 = part_o[p][hf][2][c4], o3 = part_o[p][hf][3][c4];
+      s_o[col] = f32_to_bf16(((o0.x + o1.x) + o2.x) + o3.x);
+      s_o[col + 1] = f32_to_bf16(((o0.y + o1.y) + o2.y) + o3.y);
+      s_o[col + 2] = f32_to_bf16(((o0.z + o1.z) + o2.z) + o3.z);
+      s_o[col + 3] = f32_to_bf16(((o0.w + o1.w) + o2.w) + o3.w);
+    }
+  }
+  __syncthreads();
+  // y = rms_norm_gated(bf16(o), g): wave 0, 8 elements per lane (V <= 512)
+  if (w == 0) {
+    float xo[8], ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      xv[j] = lane + kWave * j < V ? bf16_to_f32(yr[j]) : 0.f;
-      ss = fmaf(xv[j], xv[j], ss);
+      const int i = lane + kWave * j;
+      xo[j] = i < V ? bf16_to_f32(s_o[min(i, NV - 1)]) : 0.f;
+      ss = fmaf(xo[j], xo[j], ss);
     }
     const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(V) + a.eps);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = lane + kWave * j;
-      if (i < V) a.y[row * V + i] = f32_to_bf16(xv[j] * rstd * bf16_to_f32(nr[j]) / (1.f + __expf(-s_g[i])));
+      if (i < V) a.y[static_cast<int64_t>(h) * V + i] = f32_to_bf16(xo[j] * rstd * s_nr[i] / (1.f + __expf(-s_g[i])));
     }
-  }
-  // conv windows: drop the oldest input, append this token's
-#pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const int sec = j < 2 ? j : 2;
-    const int64_t idx = t0 + (j == 3 ? nthr : 0), n = sec == 2 ? HV : HK;
-    if (idx < n)
-      *reinterpret_cast<uint2*>(a.cache[sec] + idx * W) =
-          make_uint2((cw[j].x >> 16) | (cw[j].y << 16), (cw[j].y >> 16) | (xin[j] << 16));
   }
 }
 
@@ -784,7 +815,8 @@ extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* co
              (long long)(2 * H * K + H * V + 2 * R + H));
   MM_REQUIRE(pr && conv_w && conv_cache && f_b && g_b && A_log && dt_bias && state && o_norm && y,
              "kda_decode_step: null pointer");
-  MM_REQUIRE(mm::aligned16(f_b) && mm::aligned16(g_b), "kda_decode_step: f_b and g_b must be 16-byte aligned");
+  MM_REQUIRE(mm::aligned16(f_b) && mm::aligned16(g_b) && mm::aligned16(state),
+             "kda_decode_step: f_b, g_b and state must be 16-byte aligned");
   KdaStepArgs a;
   for (int i = 0; i < 3; ++i) {
     MM_REQUIRE(conv_w[i] && conv_cache[i] && (reinterpret_cast<uintptr_t>(conv_w[i]) & 7) == 0 &&
@@ -808,12 +840,11 @@ extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* co
   a.V = static_cast<int>(V);
   a.R = static_cast<int>(R);
   hipStream_t st = MM_STREAM(stream);
-  hipLaunchKernelGGL((kda_step_kernel<128, 4>), dim3(static_cast<unsigned>(V / kKdaCols), static_cast<unsigned>(H)),
-                     dim3(256), 0, st, a);
-  int rc = mm::check_launch("kda_decode_step");
-  if (rc) return rc;
-  hipLaunchKernelGGL(kda_out_kernel<4>, dim3(static_cast<unsigned>(H)), dim3(256), 0, st, a, static_cast<int>(K));
-  return mm::check_launch("kda_decode_step out");
+  const dim3 grid(static_cast<unsigned>(H)), block(kKdaThreads);
+  if (V <= 128) hipLaunchKernelGGL(kda_token_kernel<1>, grid, block, 0, st, a);
+  else if (V <= 256) hipLaunchKernelGGL(kda_token_kernel<2>, grid, block, 0, st, a);
+  else hipLaunchKernelGGL(kda_token_kernel<4>, grid, block, 0, st, a);
+  return mm::check_launch("kda_decode_step");
 }
 
 extern "C" int64_t mm_mla_attn_workspace(int nh, int dv, int64_t max_len) {

@@ -7,7 +7,7 @@ static cache.
   short_conv            the step form of fla's ShortConvolution (a [1, C, W] cache of the last inputs, SiLU)
   rms_norm_gated        fla's FusedRMSNormGated with a sigmoid gate (a KDA layer's o_norm)
   kda_decode_step       one decode token of a KDA layer's core (convolutions, the f / g LoRA up-projections, the
-                        recurrence, the gated norm) in two kernels instead of the five calls above
+                        recurrence, the gated norm) in one kernel instead of the five calls above
   mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
                         masked softmax attention over positions 0..pos
   embed_rows            word_embeddings(tok_buf), the input row of a decode step (engine.py:686)
@@ -169,7 +169,7 @@ def _three(t, sizes, name):
 
 def kda_decode_step(pr, conv_w, conv_cache, f_b, g_b, A_log, dt_bias, state, o_norm, *, heads, eps=1e-5,
                     lower_bound=None, scale=None, out=None):
-    """One decode token of a KDA layer's core in two kernels, on the layer's projection row
+    """One decode token of a KDA layer's core in one kernel, on the layer's projection row
     pr = [q | k (heads * K each) | v (heads * V) | fa | ga (rank R each) | beta logits (heads)] ([1, len] or [len]
     bf16). conv_w and conv_cache: the q, k and v conv1d weights ([C, 1, 4]) and the layer's three conv caches
     ([1, C, 4], shifted in place), each a (q, k, v) tuple as the model and its cache hold them (engine.py:645-647),

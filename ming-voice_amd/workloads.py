@@ -258,7 +258,7 @@ class HybridThinkerStep:
         f = f_b(f_a), gg = g_b(g_a); short convolutions of q | k | v (window 4, SiLU, caches [1, 6144, 4]);
         fused_recurrent_kda (l2-normalised q, k, in-kernel gate with A_log, dt_bias; beta = sigmoid(b) in the kernel; state
         [1, 16, 128, 128] fp32 in place); gated RMSNorm with gg; o projection + residual. With fused_kda (the default)
-        the part between the two projections runs as kda_decode_step's two kernels.
+        the part between the two projections runs as kda_decode_step's one kernel.
       MLA layer: RMSNorm fused into one GEMV of [q | k (16 x 192) | v (16 x 128)]; attention over the static cache
         (k [1, 16, max_len, 192], v [1, 16, max_len, 128], rows written at pos); o projection + residual.
     The real model's projection internals (the rotary part of q / k, the latent kv compression) are not modelled:
@@ -273,7 +273,7 @@ class HybridThinkerStep:
                  fused_kda=True):
         import thinker_attn as TA
         self.TA = TA
-        self.fused_kda = fused_kda  # the KDA core as kda_decode_step's two kernels, else the five-call chain
+        self.fused_kda = fused_kda  # the KDA core as kda_decode_step's one kernel, else the five-call chain
         self.moe = ThinkerDecodeStep(0, device, vocab=vocab, seed=seed)  # the shared router buffers, head, final norm
         H, dev = HIDDEN, device
         kd = KDA_HEADS * KDA_DIM
