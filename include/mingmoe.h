@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 9
+#define MM_ABI_VERSION 10
 
 /* status codes */
 #define MM_OK 0
@@ -61,7 +61,11 @@ extern "C" {
  *   w_d  [n_slots, hidden, inter]
  * with the shared expert in the last slot. The last dim must be contiguous and every row 16-byte
  * aligned. For int8 weights (w_dtype = MM_INT8) s_gu [n_slots, 2*inter] and s_d [n_slots, hidden]
- * hold one scale per output row (s_dtype MM_FP32 or MM_BF16); for bf16 weights they are NULL. */
+ * hold one scale per output row (s_dtype MM_FP32 or MM_BF16); for bf16 weights they are NULL.
+ * w_gu_slabs (optional, bf16 only; NULL for none) is a second copy of w_gu in the prefill layout that
+ * mm_gate_up_slabs writes: [n_slots][2*inter/8][hidden/64][8][64], contiguous, so that each 64-wide k-slab
+ * of 8 consecutive rows is one 1 KB piece. When it is set the prefill gate/up GEMM reads it instead of
+ * w_gu (same results, bit for bit); decode always reads w_gu. */
 typedef struct mm_experts {
   const void* w_gu;
   const void* w_d;
@@ -75,6 +79,7 @@ typedef struct mm_experts {
   int64_t gu_stride_e, gu_stride_n; /* element strides of w_gu dims 0 and 1 */
   int64_t d_stride_e, d_stride_n;   /* element strides of w_d dims 0 and 1 */
   int64_t sgu_stride_e, sd_stride_e; /* element strides of s_gu / s_d dim 0 */
+  const void* w_gu_slabs;             /* optional prefill copy of w_gu (see above) */
 } mm_experts;
 
 /* ABI version (MM_ABI_VERSION) and the last error message of this thread (returns its length). */
@@ -389,6 +394,18 @@ typedef struct mm_ingest_item {
  * own work on dst before the call. Shapes must match the stack: gate / up [inter, hidden], down [hidden, inter]. */
 int mm_ingest_experts(const mm_ingest_item* items, int64_t n_items, const mm_experts* dst, void* host_staging,
                       void* dev_staging, int64_t slot_bytes, int n_threads);
+
+/* Bytes of the prefill copy of ex->w_gu (n_slots * 2 * inter * hidden * 2), or 0 when the experts cannot have
+ * one (int8 weights, hidden not a multiple of 64 or inter not a multiple of 4). */
+int64_t mm_gate_up_slabs_bytes(const mm_experts* ex);
+
+/* Writes the prefill copy of ex->w_gu (any row strides) into `out` (mm_gate_up_slabs_bytes bytes, 16-byte
+ * aligned): out[e][q][t][j][c] = w_gu[e][8 q + j][64 t + c]. A load-time step like the quantise-on-load
+ * hooks (engine.py:126-147); no call of the reference does this: its Triton GEMM reads the row layout. The
+ * copy costs a second gate/up stack (750 MB per 64+1-expert layer of hidden 2048, inter 1408) and lets the
+ * prefill gate/up GEMM read each k-slab of a weight tile as 16 pieces of 1 KB, one per direct-load
+ * instruction, instead of 128 pieces of 128 bytes. */
+int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream);
 
 #ifdef __cplusplus
 }

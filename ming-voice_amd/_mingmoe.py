@@ -17,7 +17,7 @@ MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
 MM_NORM_ROUND_ONCE = 0x100
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -40,7 +40,7 @@ class Experts(ctypes.Structure):
     _fields_ = [("w_gu", _P), ("w_d", _P), ("s_gu", _P), ("s_d", _P), ("w_dtype", ctypes.c_int32),
                 ("s_dtype", ctypes.c_int32), ("n_slots", _I64), ("hidden", _I64), ("inter", _I64),
                 ("gu_stride_e", _I64), ("gu_stride_n", _I64), ("d_stride_e", _I64), ("d_stride_n", _I64),
-                ("sgu_stride_e", _I64), ("sd_stride_e", _I64)]
+                ("sgu_stride_e", _I64), ("sd_stride_e", _I64), ("w_gu_slabs", _P)]
 
 
 SIGNATURES = {
@@ -86,6 +86,8 @@ SIGNATURES = {
     "mm_mla_decode_attn": ([_P, _P, _P, _I32, _I32, _I32, _P, _P, _I64, _P, _I32, _F32, _P, _P, _I64, _P], ctypes.c_int),
     "mm_embed_rows": ([_P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _I64, _P], ctypes.c_int),
     "mm_argmax_rows": ([_P, _I32, _I64, _I64, _I64, _P, _P], ctypes.c_int),
+    "mm_gate_up_slabs_bytes": ([ctypes.POINTER(Experts)], _I64),
+    "mm_gate_up_slabs": ([ctypes.POINTER(Experts), _P, _P], ctypes.c_int),
 }
 
 _lib = None
@@ -171,8 +173,9 @@ class on_device:
         return False
 
 
-def experts(w_gu, w_d, s_gu=None, s_d=None):
-    """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales)."""
+def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None):
+    """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales); w_gu_slabs: the
+    prefill copy of w_gu that fused_moe.gate_up_slabs makes (bf16 only), or None."""
     if w_gu.dim() != 3 or w_d.dim() != 3:
         raise ValueError("w_gu and w_d must be 3-D stacked expert tensors")
     E1, two_i, H = w_gu.shape
@@ -202,4 +205,9 @@ def experts(w_gu, w_d, s_gu=None, s_d=None):
         ex.sgu_stride_e, ex.sd_stride_e = s_gu.stride(0), s_d.stride(0)
     else:
         ex.s_dtype = MM_FP32
+    if w_gu_slabs is not None:
+        if q or w_gu_slabs.dtype != torch.bfloat16 or not w_gu_slabs.is_contiguous() or \
+                w_gu_slabs.numel() != w_gu.shape[0] * w_gu.shape[1] * w_gu.shape[2] or w_gu_slabs.device != w_gu.device:
+            raise ValueError("w_gu_slabs must be the contiguous bf16 prefill copy of w_gu (fused_moe.gate_up_slabs)")
+        ex.w_gu_slabs = w_gu_slabs.data_ptr()
     return ex

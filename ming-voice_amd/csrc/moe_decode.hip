@@ -562,6 +562,11 @@ int check_experts(const char* who, const mm_experts* ex) {
     MM_REQUIRE(ex->s_dtype == MM_FP32 || ex->s_dtype == MM_BF16, "%s: scales must be fp32 or bf16", who);
     MM_REQUIRE(ex->sgu_stride_e >= 2 * ex->inter && ex->sd_stride_e >= ex->hidden, "%s: bad scale strides", who);
   }
+  if (ex->w_gu_slabs) {
+    MM_REQUIRE(mm_gate_up_slabs_bytes(ex) > 0,
+               "%s: a prefill copy of w_gu needs bf16 experts, hidden a multiple of 64 and inter a multiple of 4", who);
+    MM_REQUIRE(aligned16(ex->w_gu_slabs), "%s: the prefill copy of w_gu must be 16-byte aligned", who);
+  }
   return MM_OK;
 }
 

@@ -52,6 +52,15 @@ constexpr int kXcds = 8;
 #define MM_PREFILL_DOWN_WAVES_BF16 8
 #endif
 
+// Rows per piece of the prefill copy of w_gu: [E1][2I/R][H/64][R][64], so a 64-k slab of R consecutive rows is
+// one piece of R * 128 bytes. R = 8 makes a piece the 1 KB that one direct-load instruction of a wave fills (8
+// rows x 128 bytes): measured on the 512-token block, gate/up 163.5 us with the row layout, 156-157 / 146-149 /
+// 140-143 / 142-145 us with R = 2 / 4 / 8 / 16.
+#ifndef MM_SLAB_ROWS
+#define MM_SLAB_ROWS 8
+#endif
+constexpr int kSlabRows = MM_SLAB_ROWS;
+
 struct PrefillArgs {
   const uint16_t* x;
   int64_t xs;
@@ -69,6 +78,7 @@ struct PrefillArgs {
   int s_dtype;
   int64_t H, I;
   int64_t gu_se, gu_sn, d_se, d_sn, sgu_se, sd_se;
+  int gu_slabs;  // w_gu is the prefill copy: [E1][2I/R][H/64][R][64], R = kSlabRows
   const uint16_t* res;
   int64_t res_rs;
   uint16_t* a_buf;
@@ -199,10 +209,10 @@ struct LoadMap {
 };
 
 // Issues the direct loads of slab kt into LDS stage `st` (arow/brow: this thread's source row starts,
-// null for masked rows; k counted in elements).
+// null for masked rows; k counted in elements; slab kt of a weight row starts kt * bslab elements in).
 template <class G>
 __device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K, const LoadMap<G>& m,
-                                           const uint16_t* const* arow, const char* const* brow) {
+                                           const uint16_t* const* arow, const char* const* brow, int64_t bslab) {
   constexpr int ES = G::Q ? 1 : 2;
   char* sa = lds + st * G::STAGE;
   char* sb = sa + G::A_BYTES;
@@ -216,8 +226,8 @@ __device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K,
   }
 #pragma unroll
   for (int j = 0; j < G::B_INSTR; ++j) {
-    const int64_t k = k0 + m.cb[j] * (16 / ES);
-    const void* src = (brow[j] && k < K) ? static_cast<const void*>(brow[j] + k * ES) : static_cast<const void*>(g_zero_chunk);
+    const int64_t k = k0 + m.cb[j] * (16 / ES), kb = kt * bslab + m.cb[j] * (16 / ES);
+    const void* src = (brow[j] && k < K) ? static_cast<const void*>(brow[j] + kb * ES) : static_cast<const void*>(g_zero_chunk);
     load_lds16(src, sb + (w * G::B_INSTR + j) * 1024);
   }
 }
@@ -237,12 +247,13 @@ __device__ __forceinline__ int valid_rows(const int* spair, int P) {
 }
 
 // The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
-// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j. Row fragments at or
+// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j; wrow(r) is where weight
+// row r's first slab starts and bslab the elements between its slabs. Row fragments at or
 // past fm_live (wave-uniform) hold only padding rows: their LDS reads and MFMAs are skipped and their
 // accumulators stay zero (the epilogues store no padding row).
 template <class G, class XRowFn, class WRowFn, class BColFn>
 __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t K, XRowFn xrow,
-                                          WRowFn wrow, char* lds, int r0, BColFn bcol, int fm_live) {
+                                          WRowFn wrow, int64_t bslab, char* lds, int r0, BColFn bcol, int fm_live) {
   constexpr int NS = G::NS, LOADS = G::LOADS, FM = G::FM, FN = G::FN;
   const int lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
@@ -260,7 +271,7 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
   const int nk = static_cast<int>((K + G::BK - 1) / G::BK);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue_slab<G>(lds, s, s, K, m, arow, brow);
+    if (s < nk) issue_slab<G>(lds, s, s, K, m, arow, brow, bslab);
   for (int kt = 0; kt < nk; ++kt) {
     // slabs issued after kt so far: min(nk - 1 - kt, NS - 2); wait for kt's own loads
     const int pending = min(nk - 1 - kt, NS - 2);
@@ -275,7 +286,7 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
     // slab kt visible to all waves; every wave is done with slab kt-1. A plain barrier: the loads of
     // slab kt were waited for above, and a memory fence would also wait for the later slabs' loads.
     __builtin_amdgcn_s_barrier();
-    if (kt + NS - 1 < nk) issue_slab<G>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow);
+    if (kt + NS - 1 < nk) issue_slab<G>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow, bslab);
     const char* sa = lds + (kt % NS) * G::STAGE;
     const char* sb = sa + G::A_BYTES;
     if constexpr (G::Q) {
@@ -328,7 +339,8 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
 
 // ------------------------------------------------------------------------------------------- gate / up
 
-template <bool Q, int BN, int NW, int BM>
+// SL: the weights are the prefill copy of w_gu (kSlabRows-row pieces), else the row layout.
+template <bool Q, int BN, int NW, int BM, bool SL = false>
 __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a) {
   using G = Geo<Q, BN, NW, BM>;
   constexpr int HALF = G::BN / 2;  // gate columns per tile (and as many up columns)
@@ -349,8 +361,10 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   };
   const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
   auto wrow = [&](int r) -> const char* {
-    const int64_t col = n0 + (r % HALF);
-    return col < I ? wbase + ((r < HALF ? col : I + col) * a.gu_sn) * ES : nullptr;
+    const int64_t col = n0 + (r % HALF), rr = r < HALF ? col : I + col;
+    // the prefill copy: row rr is row rr % R of piece group rr / R, whose 64-k slabs are R * 64 elements apart
+    const int64_t off = SL ? (rr / kSlabRows) * kSlabRows * a.H + (rr % kSlabRows) * 64 : rr * a.gu_sn;
+    return col < I ? wbase + off * ES : nullptr;
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
@@ -359,7 +373,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, a.H, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<G>(acc, a.H, xrow, wrow, SL ? kSlabRows * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); }, fm_live);
 #pragma unroll
   for (int j = 0; j < FG; ++j) {
@@ -413,7 +427,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, I, xrow, wrow, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; },
+  tile_gemm<G>(acc, I, xrow, wrow, G::BK, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; },
                fm_live);
 #pragma unroll
   for (int j = 0; j < G::FN; ++j) {
@@ -480,14 +494,15 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
 }
 
 
-template <bool Q, int BN, int NW, int BM>
+template <bool Q, int BN, int NW, int BM, bool SL>
 int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
   using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.I + G::BN / 2 - 1) / (G::BN / 2);
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = mm::allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM>, G::LDS, "prefill_gate_up");
+  int rc = mm::allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM, SL>, G::LDS, "prefill_gate_up");
   if (rc) return rc;
-  hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_gate_up_kernel<Q, BN, NW, BM, SL>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS,
+                     st, a);
   return mm::check_launch("moe_prefill gate_up");
 }
 
@@ -509,15 +524,59 @@ int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
   constexpr int GU_NW = Q ? 4 : MM_PREFILL_GU_WAVES_BF16;
   constexpr int DOWN_NW = Q ? 4 : MM_PREFILL_DOWN_WAVES_BF16;
   int rc;
-  if ((phases & MM_PHASE_GATE_UP) && (rc = launch_gate_up<Q, GU_BN, GU_NW, BM>(a, nb, st))) return rc;
+  if (phases & MM_PHASE_GATE_UP) {
+    if constexpr (Q) rc = launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
+    else rc = a.gu_slabs ? launch_gate_up<Q, GU_BN, GU_NW, BM, true>(a, nb, st) : launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
+    if (rc) return rc;
+  }
   if ((phases & MM_PHASE_DOWN) && (rc = launch_down<Q, DOWN_BN, DOWN_NW, BM>(a, nb, st))) return rc;
   return MM_OK;
+}
+
+// The prefill copy of w_gu, one 16-byte chunk per thread in output order (grid-stride): chunk c of expert e is
+// 8-element piece c % 8 of row j = (c / 8) % R of k-slab t = (c / 8R) % KT of row group q = c / (8R KT),
+// KT = H / 64, R = kSlabRows.
+__global__ __launch_bounds__(256) void gate_up_slabs_kernel(const uint16_t* __restrict__ w, int64_t se, int64_t sn,
+                                                           int64_t rows, int64_t H, int64_t total,
+                                                           uint4* __restrict__ out) {
+  const int64_t per = rows * H / 8, KT = H / 64;
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < total;
+       c += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t e = c / per, ce = c - e * per;
+    const int64_t piece = ce & 7, j = (ce >> 3) % kSlabRows, t = (ce / (8 * kSlabRows)) % KT, q = (ce / (8 * kSlabRows)) / KT;
+    out[c] = *reinterpret_cast<const uint4*>(w + e * se + (kSlabRows * q + j) * sn + 64 * t + 8 * piece);
+  }
 }
 
 }  // namespace
 
 namespace mm {
 int check_experts(const char* who, const mm_experts* ex);
+}
+
+extern "C" int64_t mm_gate_up_slabs_bytes(const mm_experts* ex) {
+  if (!ex || ex->w_dtype != MM_BF16 || ex->hidden <= 0 || ex->hidden % 64 != 0 || ex->inter <= 0 ||
+      (2 * ex->inter) % kSlabRows != 0 || ex->n_slots <= 0)
+    return 0;
+  return ex->n_slots * 2 * ex->inter * ex->hidden * 2;
+}
+
+extern "C" int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream) {
+  // only w_gu is read: w_d, the scales and w_gu_slabs may be unset
+  MM_REQUIRE(ex && ex->w_gu, "gate_up_slabs: null expert descriptor or w_gu");
+  const int64_t bytes = mm_gate_up_slabs_bytes(ex);
+  MM_REQUIRE(bytes > 0, "gate_up_slabs: needs bf16 experts, hidden a multiple of 64 and 2 inter of %d", kSlabRows);
+  MM_REQUIRE(ex->gu_stride_n >= ex->hidden && ex->gu_stride_e >= 2 * ex->inter * ex->gu_stride_n,
+             "gate_up_slabs: w_gu strides do not describe [E, 2I, H] with a contiguous last dim");
+  MM_REQUIRE(mm::aligned16(ex->w_gu) && (ex->gu_stride_n * 2) % 16 == 0 && (ex->gu_stride_e * 2) % 16 == 0,
+             "gate_up_slabs: w_gu rows must be 16-byte aligned");
+  MM_REQUIRE(out && mm::aligned16(out), "gate_up_slabs: out must be a 16-byte aligned buffer");
+  const int64_t total = bytes / 16;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(gate_up_slabs_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
+                     static_cast<const uint16_t*>(ex->w_gu), ex->gu_stride_e, ex->gu_stride_n, 2 * ex->inter,
+                     ex->hidden, total, static_cast<uint4*>(out));
+  return mm::check_launch("gate_up_slabs");
 }
 
 extern "C" int32_t mm_prefill_block_m(int64_t n_tokens, int64_t nk, int64_t n_slots, int w_dtype) {
@@ -558,15 +617,17 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   a.sorted_ids = sorted_ids;
   a.bexp = bexp;
   a.offsets = expert_offsets;
-  a.w_gu = ex->w_gu;
+  // bf16 experts with a prefill copy of w_gu: the gate/up GEMM reads that copy (64-k slabs 64 R elements apart)
+  a.gu_slabs = ex->w_gu_slabs && ex->w_dtype == MM_BF16 ? 1 : 0;
+  a.w_gu = a.gu_slabs ? ex->w_gu_slabs : ex->w_gu;
   a.w_d = ex->w_d;
   a.s_gu = ex->s_gu;
   a.s_d = ex->s_d;
   a.s_dtype = ex->s_dtype;
   a.H = ex->hidden;
   a.I = ex->inter;
-  a.gu_se = ex->gu_stride_e;
-  a.gu_sn = ex->gu_stride_n;
+  a.gu_se = a.gu_slabs ? 2 * ex->inter * ex->hidden : ex->gu_stride_e;
+  a.gu_sn = a.gu_slabs ? 0 : ex->gu_stride_n;
   a.d_se = ex->d_stride_e;
   a.d_sn = ex->d_stride_n;
   a.sgu_se = ex->sgu_stride_e;

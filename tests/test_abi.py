@@ -111,6 +111,23 @@ def test_argument_validation_reports_messages():
     assert "int32 or int64" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 64, 64, P, mm.MM_FP32, 1, P, 64, None))
     assert "16-byte aligned" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 12, 12, P, mm.MM_INT64, 1, P, 12, None))
     assert "bf16, fp16 or fp32" in _err(lib.mm_embed_rows(P, mm.MM_INT8, 100, 64, 64, P, mm.MM_INT64, 1, P, 64, None))
+    ex = mm.Experts()
+    ex.w_gu, ex.w_d, ex.w_dtype, ex.n_slots, ex.hidden, ex.inter = 16, 16, mm.MM_BF16, 65, 2048, 1408
+    ex.gu_stride_e, ex.gu_stride_n, ex.d_stride_e, ex.d_stride_n = 2816 * 2048, 2048, 2048 * 1408, 1408
+    assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 65 * 2816 * 2048 * 2
+    ex.w_gu_slabs = 24  # misaligned copy
+    assert "must be 16-byte aligned" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P,
+                                                                P, P, 10, 64, None, 0, P, P, P, 2048, 0, None))
+    assert "out must be" in _err(lib.mm_gate_up_slabs(ctypes.byref(ex), ctypes.c_void_p(8), None))
+    ex.hidden, ex.gu_stride_n, ex.gu_stride_e, ex.d_stride_e = 2040, 2040, 2816 * 2040, 2040 * 1408
+    assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 0
+    assert "hidden a multiple of 64" in _err(lib.mm_gate_up_slabs(ctypes.byref(ex), P, None))
+    ex.hidden, ex.gu_stride_n, ex.gu_stride_e, ex.d_stride_e = 2048, 2048, 2816 * 2048, 2048 * 1408
+    ex.w_dtype, ex.s_gu, ex.s_d, ex.s_dtype, ex.sgu_stride_e, ex.sd_stride_e = mm.MM_INT8, 16, 16, mm.MM_FP32, 2816, 2048
+    ex.w_gu_slabs = 32
+    assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 0
+    assert "needs bf16 experts" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P,
+                                                          10, 64, None, 0, P, P, P, 2048, 0, None))
 
 
 def test_wrappers_refuse_cpu_tensors():
@@ -126,6 +143,8 @@ def test_wrappers_refuse_cpu_tensors():
         fastlinear.small_linear(x, torch.zeros(8, 64, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="no CPU path"):
         fused_moe._align_blocks(torch.zeros(7, dtype=torch.long), 65, 64)
+    with pytest.raises(ValueError, match="no CPU path"):
+        fused_moe.gate_up_slabs(torch.zeros(1, 8, 64, dtype=torch.bfloat16))
     import fast_talker
     with pytest.raises(ValueError, match="no CPU path"):
         fast_talker.silu_mul(torch.zeros(1, 64, dtype=torch.bfloat16))
