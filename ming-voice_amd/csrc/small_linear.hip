@@ -371,10 +371,15 @@ extern "C" int mm_small_linear(const void* x, int64_t M, int64_t K, int64_t x_ro
               static_cast<uint16_t*>(y), y_row_stride};
     auto g = static_cast<const uint16_t*>(norm_g);
     // chunks per lane NC = ceil(nch / 64), rounded up to an instantiated size; at most 16 loads per lane
-    // (rows per wave measured on MI355X: 2 at K = 896, 1 at K = 2048)
+    // (rows per wave measured on MI355X: 2 at K = 896; at K = 2048 1 up to N = 2048, 2 from N = 16 per CU on,
+    // where each wave's activation row (and norm weights) from L2 then serves two weight rows: one token,
+    // 6416 / 8192 / 126464 rows with the norm fused 9.3 / 10.8 / 120.5 -> 8.6 / 9.5 / 88.5 us)
     if (nch <= 64) return launch_1pass_r<1, 4>(a, g, norm_eps, st);
     if (nch <= 128) return launch_1pass_r<2, 2>(a, g, norm_eps, st);
-    if (nch <= 256) return launch_1pass_r<4, 1>(a, g, norm_eps, st);
+    if (nch <= 256) {
+      if (N >= static_cast<int64_t>(16) * mm::cu_count()) return launch_1pass<4, 2>(a, g, norm_eps, st);
+      return launch_1pass<4, 1>(a, g, norm_eps, st);
+    }
     if (nch <= 512) return launch_1pass_r<8, 2>(a, g, norm_eps, st);
     if (nch <= 768) return launch_1pass_r<12, 1>(a, g, norm_eps, st);
     return launch_1pass_r<16, 1>(a, g, norm_eps, st);
