@@ -156,22 +156,28 @@ def blk():
     return b
 
 
-@pytest.mark.parametrize("n,int8", [(32, False), (64, False), (128, False), (512, False), (100, True)])
-def test_moe_block_prefill_graph_replays_follow_new_inputs(blk, n, int8):
+@pytest.mark.parametrize("n,int8,slabs", [(32, False, False), (64, False, False), (128, False, False),
+                                          (512, False, False), (100, True, False), (512, False, True),
+                                          (2048, False, True)])
+def test_moe_block_prefill_graph_replays_follow_new_inputs(blk, n, int8, slabs):
     """moe_block_prefill captured once for a bucket of n token rows and replayed on new rows (new routing,
-    new per-expert counts and block layout): outputs, ids and weights equal an eager call every time."""
-    print(f"[prefill graph] n={n} int8={int8}", flush=True)
+    new per-expert counts and block layout): outputs, ids and weights equal an eager call every time. With
+    slabs the captured block reads the prefill copy of the gate/up stack and the eager call the row layout
+    (2048 tokens: 128-pair blocks)."""
+    print(f"[prefill graph] n={n} int8={int8} slabs={slabs}", flush=True)
     wg, wd = (blk["q_gu"], blk["q_d"]) if int8 else (blk["w_gu"], blk["w_d"])
     sg, sd = (blk["s_gu"], blk["s_d"]) if int8 else (None, None)
     bias = W.ragged_bias(device=DEV)
     x = W.tokens(n, seed=170 + n, device=DEV)
     sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, W.EXPERTS + 1, W.HIDDEN, W.INTER, DEV, block=True, w_dtype=wg.dtype)
 
-    def run(inp, scratch):
-        return fused_moe.moe_block_prefill(inp, blk["norm_w"], W.EPS, blk["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
-                                           s_gu=sg, s_d=sd, scratch=scratch)
+    wq = fused_moe.gate_up_slabs(wg) if slabs else None
 
-    g, (y, ids, wts, logits) = _capture(lambda: run(x, sc))
+    def run(inp, scratch, w_gu_slabs=None):
+        return fused_moe.moe_block_prefill(inp, blk["norm_w"], W.EPS, blk["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
+                                           s_gu=sg, s_d=sd, scratch=scratch, w_gu_slabs=w_gu_slabs)
+
+    g, (y, ids, wts, logits) = _capture(lambda: run(x, sc, wq))
     sc2 = fused_moe.PrefillScratch(n, W.TOP_K + 1, W.EXPERTS + 1, W.HIDDEN, W.INTER, DEV, block=True,
                                    w_dtype=wg.dtype)
     seen = set()
