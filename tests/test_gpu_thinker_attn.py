@@ -283,13 +283,15 @@ def test_hybrid_step_layers_match_the_oracle():
 
 
 @pytest.mark.parametrize("H,V,R,lower_bound", [(16, 128, 128, None), (3, 64, 64, None), (5, 128, 32, -5.0),
-                                                (2, 256, 128, None), (1, 512, 256, None), (4, 144, 160, None)])
+                                                (2, 256, 128, None), (1, 512, 256, None), (4, 144, 160, None),
+                                                (2, 16, 16, None), (1, 496, 32, -2.0)])
 def test_kda_decode_step_equals_the_five_call_chain(H, V, R, lower_bound):
     """kda_decode_step (one kernel) against short_conv -> small_linear(f) -> fused_recurrent_kda ->
     small_linear(g) -> rms_norm_gated on identical copies of the layer state, three tokens in a row: the conv caches
     bit for bit, the KDA state and the normed output within tolerance (the f / g dots round in another order).
-    V above 128 takes several passes of 128 value columns and 128 g rows (144: a partial second pass; 512: four),
-    R above 128 a second LoRA piece (160: a partial one)."""
+    V above 128 takes several passes of 128 value columns and 128 g rows (144: a partial second pass; 512: four;
+    496: a partial last block), R above 128 a second LoRA piece (160: a partial one); V = 16 leaves most of a
+    wave's columns past V, R = 16 one lane of each pair without a piece."""
     from fastlinear import small_linear
     K, Wd = 128, 4
     C = 2 * H * K + H * V
