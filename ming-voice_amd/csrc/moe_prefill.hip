@@ -600,7 +600,7 @@ extern "C" int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream) {
   // only w_gu is read: w_d, the scales and w_gu_slabs may be unset
   MM_REQUIRE(ex && ex->w_gu, "gate_up_slabs: null expert descriptor or w_gu");
   const int64_t bytes = mm_gate_up_slabs_bytes(ex);
-  MM_REQUIRE(bytes > 0, "gate_up_slabs: needs bf16 experts, hidden a multiple of 64 and 2 inter of %d", kSlabRows);
+  MM_REQUIRE(bytes > 0, "gate_up_slabs: needs bf16 experts, hidden a multiple of 64 and 2 * inter a multiple of %d", kSlabRows);
   MM_REQUIRE(ex->gu_stride_n >= ex->hidden && ex->gu_stride_e >= 2 * ex->inter * ex->gu_stride_n,
              "gate_up_slabs: w_gu strides do not describe [E, 2I, H] with a contiguous last dim");
   MM_REQUIRE(mm::aligned16(ex->w_gu) && (ex->gu_stride_n * 2) % 16 == 0 && (ex->gu_stride_e * 2) % 16 == 0,

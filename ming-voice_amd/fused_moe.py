@@ -299,7 +299,7 @@ def gate_up_slabs(w_gu, out=None):
         raise ValueError("gate_up_slabs: w_gu must be a bf16 [E1, 2I, H] stack with a contiguous last dim")
     E1, two_i, H = w_gu.shape
     if H % 64 or two_i % 8:
-        raise ValueError(f"gate_up_slabs: hidden ({H}) must be a multiple of 64 and 2I ({two_i}) of 8")
+        raise ValueError(f"gate_up_slabs: hidden ({H}) must be a multiple of 64 and 2I ({two_i}) a multiple of 8")
     ex = _mm.Experts()  # only w_gu is read
     ex.w_gu, ex.w_dtype, ex.s_dtype = w_gu.data_ptr(), _mm.MM_BF16, _mm.MM_FP32
     ex.n_slots, ex.hidden, ex.inter = E1, H, two_i // 2
