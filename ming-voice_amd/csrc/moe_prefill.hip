@@ -27,8 +27,9 @@ constexpr int kBM = 128;
 constexpr int kBMSmall = 64;
 constexpr int kXcds = 8;
 // Tile shape per weight type and GEMM: output columns per tile (BN) and waves per workgroup. The k-slab is
-// 64 elements; 128-column bf16 tiles of 64-pair blocks keep 3 slabs in flight, int8, 256-column and
-// 128-pair tiles 2 (LDS = slabs x (BM x 128 B + BN x 64 x weight bytes), two workgroups per CU). Waves
+// 64 elements, with 2 slabs in flight (LDS = slabs x (BM x 128 B + BN x 64 x weight bytes): three 64-pair
+// bf16 workgroups share a CU, two of 128-pair tiles), except the gate/up GEMM on the row layout, whose
+// 64-pair bf16 tiles keep 3 in flight (two workgroups per CU; slabs_in_flight). Waves
 // split the BM x BN tile as 1 x 4 (4 waves, each BM rows x BN/4) or 2 x NW/2 (8 waves, or 64-column
 // tiles). Measured on the 512-token block: 8-wave 128-column bf16 tiles are the fastest of 64/128/256
 // columns x 4/8 waves x 2/3 slabs; on the 2048-token Zipf block the same shape with 128-pair blocks beats
@@ -134,14 +135,21 @@ __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
 
 __device__ __attribute__((aligned(16))) uint4 g_zero_chunk[1];  // 16 zero bytes for masked lanes
 
-template <bool Quant, int TileN, int Waves = 4, int BlockM = kBMSmall>
+// Slabs in flight. Measured on the 512-token block (µs): the gate/up GEMM on the row layout 163.3-166.0 with 3
+// (two workgroups per CU) against 168.3-169.2 with 2 (three per CU); on the prefill copy 141.6-144.8 with 3
+// against 137.7-139.1 with 2; the down GEMM 80.6-81.3 with 3 against 77.1-78.1 with 2.
+constexpr int slabs_in_flight(bool q, int bn, int bm, bool row_gate_up) {
+  return row_gate_up && !q && bn < 256 && bm <= kBMSmall ? 3 : 2;
+}
+
+template <bool Quant, int TileN, int Waves = 4, int BlockM = kBMSmall, bool RowGateUp = false>
 struct Geo {
   static constexpr bool Q = Quant;
   static constexpr int BM = BlockM;                   // rows (pairs) per tile
   static constexpr int BN = TileN;                    // output columns per tile
   static constexpr int NW = Waves;                    // waves per workgroup
   static constexpr int BK = 64;                       // k elements per slab
-  static constexpr int NS = Q || BN >= 256 || BM > 64 ? 2 : 3;  // slabs in flight
+  static constexpr int NS = slabs_in_flight(Q, BN, BM, RowGateUp);
   static constexpr int WM = (BN <= 64 || NW == 8) ? 2 : 1;  // wave rows
   static constexpr int WN = NW / WM;                  // wave columns
   static constexpr int FM = BM / WM / 16;             // 16-row fragments per wave
@@ -369,7 +377,7 @@ __device__ __forceinline__ void store_rows(const uint16_t* ot, int os, const int
 // SL: the weights are the prefill copy of w_gu (kSlabRows-row pieces), else the row layout.
 template <bool Q, int BN, int NW, int BM, bool SL = false>
 __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a) {
-  using G = Geo<Q, BN, NW, BM>;
+  using G = Geo<Q, BN, NW, BM, !SL>;
   constexpr int HALF = G::BN / 2;  // gate columns per tile (and as many up columns)
   extern __shared__ uint4 lds_raw[];
   __shared__ int spair[BM];
@@ -531,7 +539,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
 
 template <bool Q, int BN, int NW, int BM, bool SL>
 int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
-  using G = Geo<Q, BN, NW, BM>;
+  using G = Geo<Q, BN, NW, BM, !SL>;
   const int64_t nt = (a.I + G::BN / 2 - 1) / (G::BN / 2);
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
   int rc = mm::allow_lds(prefill_gate_up_kernel<Q, BN, NW, BM, SL>, G::LDS, "prefill_gate_up");
