@@ -90,11 +90,13 @@ def kernel_ms(fn, stream, reps=20):
 # ----------------------------------------------------------------------------------------------- prefill
 
 def prefill_setup(b, n, bias, seed, slabs=True):
-    """The prefill block on n tokens; slabs: the gate/up GEMM reads b["w_gu_slabs"] (fused_moe.gate_up_slabs of
-    b["w_gu"], made once like a load-time layout step) when the block holds one."""
+    """The prefill block on n tokens; slabs: the GEMMs read b["w_gu_slabs"] and b["w_d_slabs"]
+    (fused_moe.gate_up_slabs / down_slabs of b["w_gu"] / b["w_d"], made once like a load-time layout step) when the
+    block holds them."""
     import fused_moe
     import workloads as W
     wq = b.get("w_gu_slabs") if slabs else None
+    wdq = b.get("w_d_slabs") if slabs else None
     x = W.tokens(n, seed=seed, device="cuda")
     E1, I, H = b["w_gu"].shape[0], b["w_d"].shape[-1], b["w_d"].shape[1]
     sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True)
@@ -102,11 +104,12 @@ def prefill_setup(b, n, bias, seed, slabs=True):
 
     def step():  # the whole block: RMSNorm + router + select + align + gate/up + down + combine (+ x)
         return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
-                                           bias=bias, scoring="softmax", scratch=sc, w_gu_slabs=wq)[0]
+                                           bias=bias, scoring="softmax", scratch=sc, w_gu_slabs=wq,
+                                           w_d_slabs=wdq)[0]
 
     step()
     torch.cuda.synchronize()
-    st["w_gu_slabs"] = wq
+    st["w_gu_slabs"], st["w_d_slabs"] = wq, wdq
     return x, sc, st, step
 
 
@@ -136,7 +139,8 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True):
 
     def phase(p):
         return lambda: fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], ids, st["wts"], residual=x,
-                                                   scratch=sc, phases=p, align=False, w_gu_slabs=st["w_gu_slabs"])
+                                                   scratch=sc, phases=p, align=False, w_gu_slabs=st["w_gu_slabs"],
+                                                   w_d_slabs=st["w_d_slabs"])
     gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream)
     dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream)
     cb_ms = kernel_ms(phase(_mingmoe.MM_PHASE_COMBINE), stream)
@@ -153,6 +157,7 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True):
         "mfma_pct": flops / (moe_ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 100,
         "hbm_pct_weights": used * W.expert_bytes() / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
         "gate_up_weights": "slab copy" if st["w_gu_slabs"] is not None else "rows",
+        "down_weights": "slab copy" if st["w_d_slabs"] is not None else "rows",
     }
 
 
@@ -579,12 +584,14 @@ def main():
     t0 = time.time()
     import fused_moe
     b = W.block(seed=0, device="cuda")
-    # the prefill layout copy of the gate/up stack (load-time, outside the timed region; decode reads w_gu)
+    # the prefill layout copies of the gate/up and down stacks (load-time, outside the timed region; decode reads
+    # w_gu and w_d)
     b["w_gu_slabs"] = fused_moe.gate_up_slabs(b["w_gu"])
+    b["w_d_slabs"] = fused_moe.down_slabs(b["w_d"])
     bias = W.ragged_bias(device="cuda")
     torch.cuda.synchronize()
     log(f"[bench] block ready {time.time() - t0:.1f}s")
-    # The same block with the gate/up GEMM on the row layout the engine stacks (no prefill copy), for comparison.
+    # The same block with both GEMMs on the row layouts the engine stacks (no prefill copies), for comparison.
     # It runs first: the first timed work of a fresh process runs about 5 % slower while the GPU clocks ramp up.
     rows = prefill_metrics(b, 512, bias, args.steps, args.warmup, stream, slabs=False)
     log(f"[bench] prefill 512, row layout: {rows['tokens_per_s']:.0f} tok/s, gate/up {rows['gate_up_us']:.1f} us")
@@ -646,7 +653,8 @@ def main():
         "config": {"workload": "thinker MoE block prefill, 512 tokens, hidden 2048, 64+1 experts x 1408, "
                                "softmax top-6, ragged router bias", "tokens": 512, "hidden": 2048, "experts": 64,
                    "inter": 1408, "top_k": 6, "graph": True,
-                   "gate_up_weights": "prefill copy of the gate/up stack (gate_up_slabs, made at load)"},
+                   "gate_up_weights": "prefill copy of the gate/up stack (gate_up_slabs, made at load)",
+                   "down_weights": "prefill copy of the down stack (down_slabs, made at load)"},
         "roofline": {"bound": "hbm", "kernel": "prefill_gate_up_kernel<false, 128, 8, 64, true>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
         "cpu_baseline": cpu,

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 10
+#define MM_ABI_VERSION 11
 
 /* status codes */
 #define MM_OK 0
@@ -65,7 +65,8 @@ extern "C" {
  * w_gu_slabs (optional, bf16 only; NULL for none) is a second copy of w_gu in the prefill layout that
  * mm_gate_up_slabs writes: [n_slots][2*inter/8][hidden/64][8][64], contiguous, so that each 64-wide k-slab
  * of 8 consecutive rows is one 1 KB piece. When it is set the prefill gate/up GEMM reads it instead of
- * w_gu (same results, bit for bit); decode always reads w_gu. */
+ * w_gu (same results, bit for bit); decode always reads w_gu. w_d_slabs (optional, bf16 only) is the same
+ * for w_d, written by mm_down_slabs: [n_slots][hidden/8][inter/64][8][64], read by the prefill down GEMM. */
 typedef struct mm_experts {
   const void* w_gu;
   const void* w_d;
@@ -80,6 +81,7 @@ typedef struct mm_experts {
   int64_t d_stride_e, d_stride_n;   /* element strides of w_d dims 0 and 1 */
   int64_t sgu_stride_e, sd_stride_e; /* element strides of s_gu / s_d dim 0 */
   const void* w_gu_slabs;             /* optional prefill copy of w_gu (see above) */
+  const void* w_d_slabs;              /* optional prefill copy of w_d (see above) */
 } mm_experts;
 
 /* ABI version (MM_ABI_VERSION) and the last error message of this thread (returns its length). */
@@ -406,6 +408,16 @@ int64_t mm_gate_up_slabs_bytes(const mm_experts* ex);
  * prefill gate/up GEMM read each k-slab of a weight tile as 16 pieces of 1 KB, one per direct-load
  * instruction, instead of 128 pieces of 128 bytes. */
 int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream);
+
+/* Bytes of the prefill copy of ex->w_d (n_slots * hidden * inter * 2), or 0 when the experts cannot have one
+ * (int8 weights, inter not a multiple of 64 or hidden not a multiple of 8). */
+int64_t mm_down_slabs_bytes(const mm_experts* ex);
+
+/* Writes the prefill copy of ex->w_d (any row strides) into `out` (mm_down_slabs_bytes bytes, 16-byte
+ * aligned): out[e][q][t][j][c] = w_d[e][8 q + j][64 t + c]. The same load-time step as mm_gate_up_slabs, for
+ * the down GEMM's weights (375 MB more per 64+1-expert layer of hidden 2048, inter 1408); no counterpart in
+ * the reference. */
+int mm_down_slabs(const mm_experts* ex, void* out, void* stream);
 
 #ifdef __cplusplus
 }

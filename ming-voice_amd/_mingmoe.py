@@ -17,7 +17,7 @@ MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
 MM_NORM_ROUND_ONCE = 0x100
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -40,7 +40,7 @@ class Experts(ctypes.Structure):
     _fields_ = [("w_gu", _P), ("w_d", _P), ("s_gu", _P), ("s_d", _P), ("w_dtype", ctypes.c_int32),
                 ("s_dtype", ctypes.c_int32), ("n_slots", _I64), ("hidden", _I64), ("inter", _I64),
                 ("gu_stride_e", _I64), ("gu_stride_n", _I64), ("d_stride_e", _I64), ("d_stride_n", _I64),
-                ("sgu_stride_e", _I64), ("sd_stride_e", _I64), ("w_gu_slabs", _P)]
+                ("sgu_stride_e", _I64), ("sd_stride_e", _I64), ("w_gu_slabs", _P), ("w_d_slabs", _P)]
 
 
 SIGNATURES = {
@@ -88,6 +88,8 @@ SIGNATURES = {
     "mm_argmax_rows": ([_P, _I32, _I64, _I64, _I64, _P, _P], ctypes.c_int),
     "mm_gate_up_slabs_bytes": ([ctypes.POINTER(Experts)], _I64),
     "mm_gate_up_slabs": ([ctypes.POINTER(Experts), _P, _P], ctypes.c_int),
+    "mm_down_slabs_bytes": ([ctypes.POINTER(Experts)], _I64),
+    "mm_down_slabs": ([ctypes.POINTER(Experts), _P, _P], ctypes.c_int),
 }
 
 _lib = None
@@ -173,9 +175,10 @@ class on_device:
         return False
 
 
-def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None):
-    """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales); w_gu_slabs: the
-    prefill copy of w_gu that fused_moe.gate_up_slabs makes (bf16 only), or None."""
+def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None, w_d_slabs=None):
+    """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales); w_gu_slabs /
+    w_d_slabs: the prefill copies of w_gu / w_d that fused_moe.gate_up_slabs / down_slabs make (bf16 only), or
+    None."""
     if w_gu.dim() != 3 or w_d.dim() != 3:
         raise ValueError("w_gu and w_d must be 3-D stacked expert tensors")
     E1, two_i, H = w_gu.shape
@@ -210,4 +213,9 @@ def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None):
                 w_gu_slabs.numel() != w_gu.shape[0] * w_gu.shape[1] * w_gu.shape[2] or w_gu_slabs.device != w_gu.device:
             raise ValueError("w_gu_slabs must be the contiguous bf16 prefill copy of w_gu (fused_moe.gate_up_slabs)")
         ex.w_gu_slabs = w_gu_slabs.data_ptr()
+    if w_d_slabs is not None:
+        if q or w_d_slabs.dtype != torch.bfloat16 or not w_d_slabs.is_contiguous() or \
+                w_d_slabs.numel() != w_d.shape[0] * w_d.shape[1] * w_d.shape[2] or w_d_slabs.device != w_d.device:
+            raise ValueError("w_d_slabs must be the contiguous bf16 prefill copy of w_d (fused_moe.down_slabs)")
+        ex.w_d_slabs = w_d_slabs.data_ptr()
     return ex

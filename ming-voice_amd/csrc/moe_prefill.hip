@@ -80,6 +80,7 @@ struct PrefillArgs {
   int64_t H, I;
   int64_t gu_se, gu_sn, d_se, d_sn, sgu_se, sd_se;
   int gu_slabs;  // w_gu is the prefill copy: [E1][2I/R][H/64][R][64], R = kSlabRows
+  int d_slabs;   // w_d is the prefill copy: [E1][H/R][I/64][R][64]
   const uint16_t* res;
   int64_t res_rs;
   uint16_t* a_buf;
@@ -440,7 +441,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
 
 // ----------------------------------------------------------------------------------------------- down
 
-template <bool Q, int BN, int NW, int BM>
+// SL: the weights are the prefill copy of w_d (kSlabRows-row pieces), else the row layout.
+template <bool Q, int BN, int NW, int BM, bool SL = false>
 __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   using G = Geo<Q, BN, NW, BM>;
   extern __shared__ uint4 lds_raw[];
@@ -459,7 +461,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
   auto wrow = [&](int r) -> const char* {
     const int64_t h = h0 + r;
-    return h < H ? wbase + (h * a.d_sn) * ES : nullptr;
+    const int64_t off = SL ? (h / kSlabRows) * kSlabRows * I + (h % kSlabRows) * 64 : h * a.d_sn;
+    return h < H ? wbase + off * ES : nullptr;
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int wm = wave / G::WN, wn = wave % G::WN;
@@ -467,8 +470,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, I, xrow, wrow, G::BK, reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; },
-               fm_live);
+  tile_gemm<G>(acc, I, xrow, wrow, SL ? kSlabRows * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
+               [&](int j) { return c0 + 16 * j; }, fm_live);
   // the output tile [BM][BN] goes through LDS, then out in rows (as in gate/up)
   constexpr int OS = G::BN + 8;
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds_raw);
@@ -549,14 +552,15 @@ int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
   return mm::check_launch("moe_prefill gate_up");
 }
 
-template <bool Q, int BN, int NW, int BM>
+template <bool Q, int BN, int NW, int BM, bool SL>
 int launch_down(const PrefillArgs& a, int64_t nb, hipStream_t st) {
   using G = Geo<Q, BN, NW, BM>;
   const int64_t nt = (a.H + G::BN - 1) / G::BN;
   const int64_t g = (nb * nt + kXcds - 1) / kXcds * kXcds;
-  int rc = mm::allow_lds(prefill_down_kernel<Q, BN, NW, BM>, G::LDS, "prefill_down");
+  int rc = mm::allow_lds(prefill_down_kernel<Q, BN, NW, BM, SL>, G::LDS, "prefill_down");
   if (rc) return rc;
-  hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW, BM>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st, a);
+  hipLaunchKernelGGL((prefill_down_kernel<Q, BN, NW, BM, SL>), dim3(static_cast<unsigned>(g)), dim3(NW * 64), G::LDS, st,
+                     a);
   return mm::check_launch("moe_prefill down");
 }
 
@@ -572,16 +576,19 @@ int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
     else rc = a.gu_slabs ? launch_gate_up<Q, GU_BN, GU_NW, BM, true>(a, nb, st) : launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
     if (rc) return rc;
   }
-  if ((phases & MM_PHASE_DOWN) && (rc = launch_down<Q, DOWN_BN, DOWN_NW, BM>(a, nb, st))) return rc;
+  if (phases & MM_PHASE_DOWN) {
+    if constexpr (Q) rc = launch_down<Q, DOWN_BN, DOWN_NW, BM, false>(a, nb, st);
+    else rc = a.d_slabs ? launch_down<Q, DOWN_BN, DOWN_NW, BM, true>(a, nb, st) : launch_down<Q, DOWN_BN, DOWN_NW, BM, false>(a, nb, st);
+    if (rc) return rc;
+  }
   return MM_OK;
 }
 
-// The prefill copy of w_gu, one 16-byte chunk per thread in output order (grid-stride): chunk c of expert e is
-// 8-element piece c % 8 of row j = (c / 8) % R of k-slab t = (c / 8R) % KT of row group q = c / (8R KT),
-// KT = H / 64, R = kSlabRows.
-__global__ __launch_bounds__(256) void gate_up_slabs_kernel(const uint16_t* __restrict__ w, int64_t se, int64_t sn,
-                                                           int64_t rows, int64_t H, int64_t total,
-                                                           uint4* __restrict__ out) {
+// The prefill copy of a weight stack w [E1, rows, K] (w_gu: rows 2I, K = H; w_d: rows H, K = I), one 16-byte
+// chunk per thread in output order (grid-stride): chunk c of expert e is 8-element piece c % 8 of row
+// j = (c / 8) % R of k-slab t = (c / 8R) % KT of row group q = c / (8R KT), KT = K / 64, R = kSlabRows.
+__global__ __launch_bounds__(256) void slab_copy_kernel(const uint16_t* __restrict__ w, int64_t se, int64_t sn,
+                                                       int64_t rows, int64_t H, int64_t total, uint4* __restrict__ out) {
   const int64_t per = rows * H / 8, KT = H / 64;
   for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < total;
        c += static_cast<int64_t>(gridDim.x) * 256) {
@@ -616,10 +623,35 @@ extern "C" int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream) {
   MM_REQUIRE(out && mm::aligned16(out), "gate_up_slabs: out must be a 16-byte aligned buffer");
   const int64_t total = bytes / 16;
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(gate_up_slabs_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
+  hipLaunchKernelGGL(slab_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
                      static_cast<const uint16_t*>(ex->w_gu), ex->gu_stride_e, ex->gu_stride_n, 2 * ex->inter,
                      ex->hidden, total, static_cast<uint4*>(out));
   return mm::check_launch("gate_up_slabs");
+}
+
+extern "C" int64_t mm_down_slabs_bytes(const mm_experts* ex) {
+  if (!ex || ex->w_dtype != MM_BF16 || ex->inter <= 0 || ex->inter % 64 != 0 || ex->hidden <= 0 ||
+      ex->hidden % kSlabRows != 0 || ex->n_slots <= 0)
+    return 0;
+  return ex->n_slots * ex->hidden * ex->inter * 2;
+}
+
+extern "C" int mm_down_slabs(const mm_experts* ex, void* out, void* stream) {
+  // only w_d is read: w_gu, the scales and the copies may be unset
+  MM_REQUIRE(ex && ex->w_d, "down_slabs: null expert descriptor or w_d");
+  const int64_t bytes = mm_down_slabs_bytes(ex);
+  MM_REQUIRE(bytes > 0, "down_slabs: needs bf16 experts, inter a multiple of 64 and hidden a multiple of %d", kSlabRows);
+  MM_REQUIRE(ex->d_stride_n >= ex->inter && ex->d_stride_e >= ex->hidden * ex->d_stride_n,
+             "down_slabs: w_d strides do not describe [E, H, I] with a contiguous last dim");
+  MM_REQUIRE(mm::aligned16(ex->w_d) && (ex->d_stride_n * 2) % 16 == 0 && (ex->d_stride_e * 2) % 16 == 0,
+             "down_slabs: w_d rows must be 16-byte aligned");
+  MM_REQUIRE(out && mm::aligned16(out), "down_slabs: out must be a 16-byte aligned buffer");
+  const int64_t total = bytes / 16;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(slab_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
+                     static_cast<const uint16_t*>(ex->w_d), ex->d_stride_e, ex->d_stride_n, ex->hidden, ex->inter, total,
+                     static_cast<uint4*>(out));
+  return mm::check_launch("down_slabs");
 }
 
 extern "C" int32_t mm_prefill_block_m(int64_t n_tokens, int64_t nk, int64_t n_slots, int w_dtype) {
@@ -663,7 +695,9 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   // bf16 experts with a prefill copy of w_gu: the gate/up GEMM reads that copy (64-k slabs 64 R elements apart)
   a.gu_slabs = ex->w_gu_slabs && ex->w_dtype == MM_BF16 ? 1 : 0;
   a.w_gu = a.gu_slabs ? ex->w_gu_slabs : ex->w_gu;
-  a.w_d = ex->w_d;
+  // the same for w_d and the down GEMM
+  a.d_slabs = ex->w_d_slabs && ex->w_dtype == MM_BF16 ? 1 : 0;
+  a.w_d = a.d_slabs ? ex->w_d_slabs : ex->w_d;
   a.s_gu = ex->s_gu;
   a.s_d = ex->s_d;
   a.s_dtype = ex->s_dtype;
@@ -671,8 +705,8 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   a.I = ex->inter;
   a.gu_se = a.gu_slabs ? 2 * ex->inter * ex->hidden : ex->gu_stride_e;
   a.gu_sn = a.gu_slabs ? 0 : ex->gu_stride_n;
-  a.d_se = ex->d_stride_e;
-  a.d_sn = ex->d_stride_n;
+  a.d_se = a.d_slabs ? ex->hidden * ex->inter : ex->d_stride_e;
+  a.d_sn = a.d_slabs ? 0 : ex->d_stride_n;
   a.sgu_se = ex->sgu_stride_e;
   a.sd_se = ex->sd_stride_e;
   a.res = static_cast<const uint16_t*>(residual);

@@ -11,6 +11,7 @@ Experts (plus the shared expert, stored as expert index E) live in stacked tenso
   quantize_rows_int8 symmetric per-row int8 (fused_moe.py:199-204)
   gate_up_slabs      the prefill copy of a bf16 w_gu (each 64-k slab of 8 rows one 1 KB piece), made once at
                      load; passed as w_gu_slabs, the prefill gate/up GEMM reads it instead of w_gu (same results)
+  down_slabs         the same for w_d, passed as w_d_slabs and read by the prefill down GEMM
 
 CFG and GCFG are kept for callers that read or tune them; the HIP kernels choose their own tiles, so the
 values are advisory.
@@ -21,7 +22,7 @@ import torch
 
 import _mingmoe as _mm
 
-__all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "gate_up_slabs", "CFG", "GCFG"]
+__all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "gate_up_slabs", "down_slabs", "CFG", "GCFG"]
 
 CFG = dict(A=dict(BN=16, BK=256, num_warps=4), B=dict(BN=16, BK=256, num_warps=4))
 GCFG = dict(A=dict(BM=64, BN=64, BK=64, num_warps=4), B=dict(BM=64, BN=128, BK=64, num_warps=4))
@@ -195,10 +196,11 @@ class PrefillScratch:
 
 
 def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residual=None, scratch=None,
-                      phases=_mm.MM_PHASE_ALL, align=True, w_gu_slabs=None):
+                      phases=_mm.MM_PHASE_ALL, align=True, w_gu_slabs=None, w_d_slabs=None):
     """x: [N, H] bf16; ids: [N, K+1] expert ids per token (shared expert included); weights: [N, K+1] fp32.
     Returns [N, H] bf16 = sum_k weights[:, k] * expert_k(x) (+ residual). w_gu_slabs: gate_up_slabs(w_gu), read by
-    the gate/up GEMM instead of w_gu (same results).
+    the gate/up GEMM instead of w_gu; w_d_slabs: down_slabs(w_d), read by the down GEMM instead of w_d (same
+    results).
     scratch (a PrefillScratch) supplies the buffers; phases / align=False run part of the pipeline on
     scratch left by an earlier call, for timing one kernel."""
     _mm.require_gpu(x, w_gu, w_d, ids, weights, s_gu, s_d, residual)
@@ -211,7 +213,7 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
                                 phases=phases & (_mm.MM_PHASE_GATE_UP | _mm.MM_PHASE_DOWN))
     if x.dtype != torch.bfloat16:
         raise ValueError(f"fused_moe_prefill: x must be bf16 (got {x.dtype})")
-    ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs)
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs, w_d_slabs)
     E1, I = ex.n_slots, ex.inter
     x2 = x if x.is_contiguous() else x.contiguous()
     flat = _flat_ids(ids).reshape(-1)
@@ -246,12 +248,13 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
 
 
 def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scoring="softmax", n_group=1,
-                      topk_group=1, scale=1.0, s_gu=None, s_d=None, residual=True, scratch=None, w_gu_slabs=None):
+                      topk_group=1, scale=1.0, s_gu=None, s_d=None, residual=True, scratch=None, w_gu_slabs=None,
+                      w_d_slabs=None):
     """One prefill MoE block: RMSNorm (norm_w, eps; normalised rows kept in the scratch), router, expert
     selection (shared expert appended), align, gate/up, down, combine (+ x).
     Same results as rms_norm -> route -> fused_moe_prefill(residual=x). Returns (y [N, H], ids, wts,
-    logits), views of `scratch` (a PrefillScratch made with block=True; allocated when None). w_gu_slabs: as in
-    fused_moe_prefill."""
+    logits), views of `scratch` (a PrefillScratch made with block=True; allocated when None). w_gu_slabs,
+    w_d_slabs: as in fused_moe_prefill."""
     _mm.require_gpu(x, norm_w, w32, w_gu, w_d, bias, s_gu, s_d)
     H = x.shape[-1]
     x2 = x.reshape(-1, H)
@@ -266,7 +269,7 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
         raise ValueError("moe_block_prefill: bias must be a contiguous fp32 [E] tensor")
     if scoring not in _SCORING:
         raise ValueError(f"moe_block_prefill: scoring must be one of {sorted(_SCORING)}")
-    ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs)
+    ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs, w_d_slabs)
     sc = scratch if scratch is not None else PrefillScratch(N, NK, ex.n_slots, H, ex.inter, x.device, block=True,
                                                              w_dtype=w_gu.dtype)
     if sc.block_m != prefill_block_m(N, NK, ex.n_slots, w_gu.dtype):
@@ -311,6 +314,31 @@ def gate_up_slabs(w_gu, out=None):
     lib = _mm.load()
     with _mm.on_device(w_gu):
         _mm.check(lib.mm_gate_up_slabs(ex, _mm.ptr(q), _mm.stream_of(w_gu)), "gate_up_slabs")
+    return q
+
+
+def down_slabs(w_d, out=None):
+    """The prefill copy of a bf16 down stack w_d [E1, H, I] (I a multiple of 64, H of 8):
+    out[e, q, t, j, c] = w_d[e, 8 q + j, 64 t + c], a contiguous [E1, H / 8, I / 64, 8, 64] bf16 tensor, laid out
+    as gate_up_slabs lays out w_gu. A load-time step: it costs a second down stack and lets the prefill down GEMM
+    read each k-slab of a weight tile as 1 KB pieces. Pass the result as w_d_slabs."""
+    _mm.require_gpu(w_d, out)
+    if w_d.dim() != 3 or w_d.dtype != torch.bfloat16 or w_d.stride(2) != 1:
+        raise ValueError("down_slabs: w_d must be a bf16 [E1, H, I] stack with a contiguous last dim")
+    E1, H, I = w_d.shape
+    if I % 64 or H % 8:
+        raise ValueError(f"down_slabs: inter ({I}) must be a multiple of 64 and hidden ({H}) a multiple of 8")
+    ex = _mm.Experts()  # only w_d is read
+    ex.w_d, ex.w_dtype, ex.s_dtype = w_d.data_ptr(), _mm.MM_BF16, _mm.MM_FP32
+    ex.n_slots, ex.hidden, ex.inter = E1, H, I
+    ex.d_stride_e, ex.d_stride_n = w_d.stride(0), w_d.stride(1)
+    shape = (E1, H // 8, I // 64, 8, 64)
+    q = torch.empty(shape, device=w_d.device, dtype=torch.bfloat16) if out is None else out
+    if q.dtype != torch.bfloat16 or not q.is_contiguous() or tuple(q.shape) != shape:
+        raise ValueError(f"down_slabs: out must be a contiguous bf16 {shape} tensor")
+    lib = _mm.load()
+    with _mm.on_device(w_d):
+        _mm.check(lib.mm_down_slabs(ex, _mm.ptr(q), _mm.stream_of(w_d)), "down_slabs")
     return q
 
 

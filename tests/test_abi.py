@@ -128,6 +128,21 @@ def test_argument_validation_reports_messages():
     assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 0
     assert "needs bf16 experts" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P,
                                                           10, 64, None, 0, P, P, P, 2048, 0, None))
+    # the prefill copy of w_d
+    ex = mm.Experts()
+    ex.w_gu, ex.w_d, ex.w_dtype, ex.n_slots, ex.hidden, ex.inter = 16, 16, mm.MM_BF16, 65, 2048, 1408
+    ex.gu_stride_e, ex.gu_stride_n, ex.d_stride_e, ex.d_stride_n = 2816 * 2048, 2048, 2048 * 1408, 1408
+    assert lib.mm_down_slabs_bytes(ctypes.byref(ex)) == 65 * 2048 * 1408 * 2
+    ex.w_d_slabs = 24  # misaligned copy
+    assert "prefill copy of w_d must be 16-byte aligned" in _err(lib.mm_moe_prefill(
+        P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10, 64, None, 0, P, P, P, 2048, 0, None))
+    assert "out must be" in _err(lib.mm_down_slabs(ctypes.byref(ex), ctypes.c_void_p(8), None))
+    ex.inter, ex.gu_stride_e, ex.d_stride_e, ex.d_stride_n = 1400, 2800 * 2048, 2048 * 1400, 1400
+    assert lib.mm_down_slabs_bytes(ctypes.byref(ex)) == 0
+    assert "inter a multiple of 64" in _err(lib.mm_down_slabs(ctypes.byref(ex), P, None))
+    ex.w_d_slabs = 32
+    assert "a prefill copy of w_d needs bf16 experts" in _err(lib.mm_moe_prefill(
+        P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10, 64, None, 0, P, P, P, 2048, 0, None))
 
 
 def test_wrappers_refuse_cpu_tensors():
@@ -145,6 +160,8 @@ def test_wrappers_refuse_cpu_tensors():
         fused_moe._align_blocks(torch.zeros(7, dtype=torch.long), 65, 64)
     with pytest.raises(ValueError, match="no CPU path"):
         fused_moe.gate_up_slabs(torch.zeros(1, 8, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="no CPU path"):
+        fused_moe.down_slabs(torch.zeros(1, 8, 64, dtype=torch.bfloat16))
     import fast_talker
     with pytest.raises(ValueError, match="no CPU path"):
         fast_talker.silu_mul(torch.zeros(1, 64, dtype=torch.bfloat16))

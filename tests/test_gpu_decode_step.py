@@ -162,8 +162,8 @@ def blk():
 def test_moe_block_prefill_graph_replays_follow_new_inputs(blk, n, int8, slabs):
     """moe_block_prefill captured once for a bucket of n token rows and replayed on new rows (new routing,
     new per-expert counts and block layout): outputs, ids and weights equal an eager call every time. With
-    slabs the captured block reads the prefill copy of the gate/up stack and the eager call the row layout
-    (2048 tokens: 128-pair blocks)."""
+    slabs the captured block reads the prefill copies of the gate/up and down stacks and the eager call the row
+    layout (2048 tokens: 128-pair blocks)."""
     print(f"[prefill graph] n={n} int8={int8} slabs={slabs}", flush=True)
     wg, wd = (blk["q_gu"], blk["q_d"]) if int8 else (blk["w_gu"], blk["w_d"])
     sg, sd = (blk["s_gu"], blk["s_d"]) if int8 else (None, None)
@@ -172,12 +172,14 @@ def test_moe_block_prefill_graph_replays_follow_new_inputs(blk, n, int8, slabs):
     sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, W.EXPERTS + 1, W.HIDDEN, W.INTER, DEV, block=True, w_dtype=wg.dtype)
 
     wq = fused_moe.gate_up_slabs(wg) if slabs else None
+    wdq = fused_moe.down_slabs(wd) if slabs else None
 
-    def run(inp, scratch, w_gu_slabs=None):
+    def run(inp, scratch, w_gu_slabs=None, w_d_slabs=None):
         return fused_moe.moe_block_prefill(inp, blk["norm_w"], W.EPS, blk["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
-                                           s_gu=sg, s_d=sd, scratch=scratch, w_gu_slabs=w_gu_slabs)
+                                           s_gu=sg, s_d=sd, scratch=scratch, w_gu_slabs=w_gu_slabs,
+                                           w_d_slabs=w_d_slabs)
 
-    g, (y, ids, wts, logits) = _capture(lambda: run(x, sc, wq))
+    g, (y, ids, wts, logits) = _capture(lambda: run(x, sc, wq, wdq))
     sc2 = fused_moe.PrefillScratch(n, W.TOP_K + 1, W.EXPERTS + 1, W.HIDDEN, W.INTER, DEV, block=True,
                                    w_dtype=wg.dtype)
     seen = set()

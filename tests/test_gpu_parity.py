@@ -420,23 +420,41 @@ def test_gate_up_slabs_copy_layout():
         fused_moe.gate_up_slabs(W.normal((2, 8, 96), 1.0, 142, DEV))
 
 
+def test_down_slabs_copy_layout():
+    """down_slabs writes out[e, q, t, j, c] = w_d[e, 8 q + j, 64 t + c], from a contiguous stack and from a strided
+    view (rows 384 apart, 8 spare rows per expert)."""
+    w = W.normal((5, 24, 320), 1.0, 147, DEV)
+    q = fused_moe.down_slabs(w)
+    assert torch.equal(q, w.reshape(5, 3, 8, 5, 64).permute(0, 1, 3, 2, 4).contiguous())
+    big = W.normal((5, 32, 384), 1.0, 148, DEV)
+    view = big[:, :24, :320]
+    assert view.stride(1) == 384 and view.stride(0) == 32 * 384
+    q2 = fused_moe.down_slabs(view)
+    assert torch.equal(q2, view.contiguous().reshape(5, 3, 8, 5, 64).permute(0, 1, 3, 2, 4).contiguous())
+    with pytest.raises(ValueError, match="multiple of 64"):
+        fused_moe.down_slabs(W.normal((2, 8, 96), 1.0, 149, DEV))
+
+
 @pytest.mark.parametrize("n,kind", [(100, "ragged"), (512, "ragged"), (2048, "zipf")])
 def test_prefill_reads_the_slab_copy_bit_for_bit(blk, n, kind):
-    """With the slab copy of w_gu the prefill block and fused_moe_prefill give the row layout's outputs bit for bit:
-    64-pair blocks at 100 and 512 tokens, 128-pair blocks for the 2048 Zipf tokens (the gate/up GEMM only reads
-    the weights at other addresses)."""
+    """With the slab copies of w_gu and w_d (each alone and both) the prefill block and fused_moe_prefill give the
+    row layout's outputs bit for bit: 64-pair blocks at 100 and 512 tokens, 128-pair blocks for the 2048 Zipf
+    tokens (the GEMMs only read the weights at other addresses)."""
     b, _ = blk
     wq = fused_moe.gate_up_slabs(b["w_gu"])
+    wd = fused_moe.down_slabs(b["w_d"])
     bias = W.zipf_bias(device=DEV) if kind == "zipf" else W.ragged_bias(device=DEV)
     x = W.tokens(n, seed=170 + n, device=DEV)
     y, ids, wts, _ = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=6,
                                                  bias=bias)
-    yq, idq, _, _ = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=6,
-                                                bias=bias, w_gu_slabs=wq)
-    assert torch.equal(idq, ids) and torch.equal(yq, y)
+    for gq, dq in ((wq, None), (wq, wd)):
+        yq, idq, _, _ = fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=6,
+                                                    bias=bias, w_gu_slabs=gq, w_d_slabs=dq)
+        assert torch.equal(idq, ids) and torch.equal(yq, y)
     xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
-    y2 = fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x, w_gu_slabs=wq)
-    assert torch.equal(y2, y)
+    for gq, dq in ((wq, None), (None, wd), (wq, wd)):
+        y2 = fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x, w_gu_slabs=gq, w_d_slabs=dq)
+        assert torch.equal(y2, y)
 
 
 def test_prefill_slab_copy_on_ragged_shapes():
@@ -453,6 +471,24 @@ def test_prefill_slab_copy_on_ragged_shapes():
         x = W.normal((n, H), 1.0, 146 + n, DEV)
         y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
         assert torch.equal(fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts, w_gu_slabs=wq), y), n
+
+
+def test_prefill_down_slab_copy_on_ragged_shapes():
+    """The down slab copy with a partial row tile of W_d (hidden 1544 = 12 x 128 + 8; hidden is not a multiple
+    of 64, so w_gu has no copy) at inter 192, 64- and 128-pair blocks."""
+    H, I, E, K = 1544, 192, 32, 6
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 150, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 151, DEV)
+    wd = fused_moe.down_slabs(w_d)
+    g = torch.Generator().manual_seed(152)
+    for n in (60, 700):
+        sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
+        ids = torch.cat([sel, torch.full((n, 1), E)], 1).to(DEV)
+        wts = torch.cat([torch.rand(n, K, generator=g), torch.ones(n, 1)], 1).to(DEV)
+        x = W.normal((n, H), 1.0, 153 + n, DEV)
+        y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
+        assert torch.equal(fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts, w_d_slabs=wd), y), n
+    close(y, O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu()))
 
 
 def test_prefill_equals_per_token_decode(blk):
