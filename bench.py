@@ -7,7 +7,8 @@ shared expert, softmax top-6, router bias ~ N(0, 0.5) for ragged expert loads). 
 block on inputs already resident in HBM: RMSNorm -> router -> align -> grouped gate/up -> down ->
 combine + residual, replayed from one hipGraph. `value` is tokens/s over exactly K timed steps.
 
-Also measured and reported under "extra": the 2048-token Zipf prefill; the full 28-layer synthetic decode
+Also measured and reported under "extra": the 2048-token Zipf prefill; the headline block with int8 experts
+(fp32 row scales); the block on the row layouts (no prefill copies); the full 28-layer synthetic decode
 step (+ LM head) in one hipGraph; decode of 1 token (bf16) and int8 decode at batch 1/2/4/8 through 28
 distinct layers (cold: every layer's experts read from HBM), per layer and per kernel; the Talker path (a
 24-layer Qwen2-0.5B-shaped LLM decode step and its rotary / decode attention and silu_mul kernels); and the
@@ -89,35 +90,39 @@ def kernel_ms(fn, stream, reps=20):
 
 # ----------------------------------------------------------------------------------------------- prefill
 
-def prefill_setup(b, n, bias, seed, slabs=True):
+def prefill_setup(b, n, bias, seed, slabs=True, int8=False):
     """The prefill block on n tokens; slabs: the GEMMs read b["w_gu_slabs"] and b["w_d_slabs"]
     (fused_moe.gate_up_slabs / down_slabs of b["w_gu"] / b["w_d"], made once like a load-time layout step) when the
-    block holds them."""
+    block holds them. int8: the experts are b["q_gu"] / b["q_d"] with row scales b["s_gu"] / b["s_d"] (no copies)."""
     import fused_moe
     import workloads as W
-    wq = b.get("w_gu_slabs") if slabs else None
-    wdq = b.get("w_d_slabs") if slabs else None
+    wq = b.get("w_gu_slabs") if slabs and not int8 else None
+    wdq = b.get("w_d_slabs") if slabs and not int8 else None
+    wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
+    sg, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
     x = W.tokens(n, seed=seed, device="cuda")
     E1, I, H = b["w_gu"].shape[0], b["w_d"].shape[-1], b["w_d"].shape[1]
-    sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True)
+    sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True, w_dtype=wg.dtype)
     st = {"xn": sc.xn, "ids": sc.ids, "wts": sc.wts}
 
     def step():  # the whole block: RMSNorm + router + select + align + gate/up + down + combine (+ x)
-        return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], b["w_gu"], b["w_d"], top_k=W.TOP_K,
-                                           bias=bias, scoring="softmax", scratch=sc, w_gu_slabs=wq,
+        return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
+                                           scoring="softmax", s_gu=sg, s_d=sd, scratch=sc, w_gu_slabs=wq,
                                            w_d_slabs=wdq)[0]
 
     step()
     torch.cuda.synchronize()
     st["w_gu_slabs"], st["w_d_slabs"] = wq, wdq
+    st["experts"] = (wg, wd, sg, sd)
     return x, sc, st, step
 
 
-def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True):
+def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8=False):
     import fused_moe
     import _mingmoe
     import workloads as W
-    x, sc, st, step = prefill_setup(b, n, bias, seed, slabs)
+    x, sc, st, step = prefill_setup(b, n, bias, seed, slabs, int8)
+    wg, wd, sg, sd = st["experts"]
     g = graph_of(step, stream)
     with torch.cuda.stream(stream):
         for _ in range(warmup):
@@ -138,15 +143,16 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True):
     P = ids.numel()
 
     def phase(p):
-        return lambda: fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], ids, st["wts"], residual=x,
+        return lambda: fused_moe.fused_moe_prefill(st["xn"], wg, wd, ids, st["wts"], s_gu=sg, s_d=sd, residual=x,
                                                    scratch=sc, phases=p, align=False, w_gu_slabs=st["w_gu_slabs"],
                                                    w_d_slabs=st["w_d_slabs"])
     gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream)
     dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream)
     cb_ms = kernel_ms(phase(_mingmoe.MM_PHASE_COMBINE), stream)
     H, I = W.HIDDEN, W.INTER
-    gu_bytes = used * 2 * I * H * 2 + n * H * 2 + P * I * 2
-    dn_bytes = used * H * I * 2 + P * I * 2 + P * H * 2
+    es, sb = (1, sg.element_size()) if int8 else (2, 0)  # weight bytes per element, scale bytes per row
+    gu_bytes = used * 2 * I * (H * es + sb) + n * H * 2 + P * I * 2
+    dn_bytes = used * H * (I * es + sb) + P * I * 2 + P * H * 2
     flops = P * W.flops_per_pair()
     moe_ms = gu_ms + dn_ms
     return {
@@ -155,7 +161,9 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True):
         "gate_up_us": gu_ms * 1e3, "down_us": dn_ms * 1e3, "combine_us": cb_ms * 1e3,
         "gate_up_GBs": gu_bytes / gu_ms / 1e6, "down_GBs": dn_bytes / dn_ms / 1e6, "gate_up_bytes": gu_bytes,
         "mfma_pct": flops / (moe_ms * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 100,
-        "hbm_pct_weights": used * W.expert_bytes() / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100,
+        "hbm_pct_weights": used * W.expert_bytes(int8=int8, scale_bytes=sb) / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9)
+        * 100,
+        "weights": f"int8 + {'fp32' if sb == 4 else 'bf16'} row scales" if int8 else "bf16",
         "gate_up_weights": "slab copy" if st["w_gu_slabs"] is not None else "rows",
         "down_weights": "slab copy" if st["w_d_slabs"] is not None else "rows",
     }
@@ -603,6 +611,11 @@ def main():
     if want("zipf"):
         extra["prefill_2048_zipf"] = prefill_metrics(b, 2048, W.zipf_bias(device="cuda"), 10, 2, stream, seed=90)
         log(f"[bench] zipf: {extra['prefill_2048_zipf']}")
+    if want("int8"):
+        # the headline block with int8 experts and fp32 row scales (the reference's int8 stacks), same masters
+        W.quantize_block(b, torch.float32)
+        extra["prefill_512_int8"] = prefill_metrics(b, 512, bias, 20, 3, stream, int8=True)
+        log(f"[bench] prefill 512 int8: {extra['prefill_512_int8']}")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(b, bias)
