@@ -90,14 +90,29 @@ def kernel_ms(fn, stream, reps=20):
 
 # ----------------------------------------------------------------------------------------------- prefill
 
+class copies:
+    """Sets fused_moe.PREFILL_COPIES for a block of calls: "registered" (the prefill GEMMs read the copies that
+    fused_moe.prefill_copies registered for the stacks, found by the calls themselves) or "off" (the stacks)."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        import fused_moe
+        self.prev, fused_moe.PREFILL_COPIES = fused_moe.PREFILL_COPIES, self.mode
+
+    def __exit__(self, *exc):
+        import fused_moe
+        fused_moe.PREFILL_COPIES = self.prev
+        return False
+
+
 def prefill_setup(b, n, bias, seed, slabs=True, int8=False):
-    """The prefill block on n tokens; slabs: the GEMMs read b["w_gu_slabs"] and b["w_d_slabs"]
-    (fused_moe.gate_up_slabs / down_slabs of b["w_gu"] / b["w_d"], made once like a load-time layout step) when the
-    block holds them. int8: the experts are b["q_gu"] / b["q_d"] with row scales b["s_gu"] / b["s_d"] (no copies)."""
+    """The prefill block on n tokens; slabs: the GEMMs read the prefill copies of b["w_gu"] / b["w_d"] registered
+    with fused_moe.prefill_copies (a load-time layout step), found by the calls themselves; else the stacks. int8:
+    the experts are b["q_gu"] / b["q_d"] with row scales b["s_gu"] / b["s_d"] (no copies)."""
     import fused_moe
     import workloads as W
-    wq = b.get("w_gu_slabs") if slabs and not int8 else None
-    wdq = b.get("w_d_slabs") if slabs and not int8 else None
     wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
     sg, sd = (b["s_gu"], b["s_d"]) if int8 else (None, None)
     x = W.tokens(n, seed=seed, device="cuda")
@@ -105,14 +120,18 @@ def prefill_setup(b, n, bias, seed, slabs=True, int8=False):
     sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True, w_dtype=wg.dtype)
     st = {"xn": sc.xn, "ids": sc.ids, "wts": sc.wts}
 
+    mode = "registered" if slabs and not int8 else "off"
+
     def step():  # the whole block: RMSNorm + router + select + align + gate/up + down + combine (+ x)
-        return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
-                                           scoring="softmax", s_gu=sg, s_d=sd, scratch=sc, w_gu_slabs=wq,
-                                           w_d_slabs=wdq)[0]
+        with copies(mode):
+            return fused_moe.moe_block_prefill(x, b["norm_w"], W.EPS, b["w32"], wg, wd, top_k=W.TOP_K, bias=bias,
+                                               scoring="softmax", s_gu=sg, s_d=sd, scratch=sc)[0]
 
     step()
     torch.cuda.synchronize()
-    st["w_gu_slabs"], st["w_d_slabs"] = wq, wdq
+    with copies(mode):
+        st["w_gu_slabs"], st["w_d_slabs"] = fused_moe._copies_for(wg, wd)
+    st["mode"] = mode
     st["experts"] = (wg, wd, sg, sd)
     return x, sc, st, step
 
@@ -134,6 +153,7 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8
         for _ in range(steps):
             g.replay()
         e1.record(stream)
+        busy = read_clocks()  # the replays are still running: the clocks of the timed region
         e1.synchronize()
         wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
@@ -143,9 +163,11 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8
     P = ids.numel()
 
     def phase(p):
-        return lambda: fused_moe.fused_moe_prefill(st["xn"], wg, wd, ids, st["wts"], s_gu=sg, s_d=sd, residual=x,
-                                                   scratch=sc, phases=p, align=False, w_gu_slabs=st["w_gu_slabs"],
-                                                   w_d_slabs=st["w_d_slabs"])
+        def run():
+            with copies(st["mode"]):
+                fused_moe.fused_moe_prefill(st["xn"], wg, wd, ids, st["wts"], s_gu=sg, s_d=sd, residual=x, scratch=sc,
+                                            phases=p, align=False)
+        return run
     gu_ms = kernel_ms(phase(_mingmoe.MM_PHASE_GATE_UP), stream)
     dn_ms = kernel_ms(phase(_mingmoe.MM_PHASE_DOWN), stream)
     cb_ms = kernel_ms(phase(_mingmoe.MM_PHASE_COMBINE), stream)
@@ -166,7 +188,28 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8
         "weights": f"int8 + {'fp32' if sb == 4 else 'bf16'} row scales" if int8 else "bf16",
         "gate_up_weights": "slab copy" if st["w_gu_slabs"] is not None else "rows",
         "down_weights": "slab copy" if st["w_d_slabs"] is not None else "rows",
+        "clocks_under_load": busy,
     }
+
+
+def engine_call_metrics(b, n, bias, stream, seed=70, reps=20):
+    """The reference engine's own prefill call, unchanged (engine.py:300-310): fused_moe_prefill(x, w_gu, w_d, ids,
+    wts) on the block's stacks, with no layout argument and no scratch, on the normalised rows and routing of the
+    headline workload. The call finds the prefill copies registered for the stacks; `reps` calls in one graph."""
+    import fused_moe
+    import fused_ops
+    import workloads as W
+    x = W.tokens(n, seed=seed, device="cuda")
+    xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+    ids, wts, _ = fused_ops.route(xn, b["w32"], bias, top_k=W.TOP_K, scoring="softmax")
+    out = {}
+    for mode in ("registered", "off"):
+        with copies(mode):
+            ms = kernel_ms(lambda: fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts), stream, reps)
+            found = fused_moe._copies_for(b["w_gu"], b["w_d"])
+        out[mode] = {"us": ms * 1e3, "tokens_per_s": n / ms * 1e3, "copies_found": [c is not None for c in found]}
+    return {"tokens": n, "call": "fused_moe_prefill(x, w_gu, w_d, ids, wts)", "with_copies": out["registered"],
+            "rows": out["off"]}
 
 
 # ------------------------------------------------------------------------------- HBM traffic (counters)
@@ -183,11 +226,12 @@ def pmc_probe():
     import workloads as W
     _mingmoe.load()
     b = W.block(seed=0, device="cuda")
-    b["w_gu_slabs"] = fused_moe.gate_up_slabs(b["w_gu"])
+    fused_moe.prefill_copies(b["w_gu"], b["w_d"])
     x, sc, st, step = prefill_setup(b, 512, W.ragged_bias(device="cuda"), 70)
-    for _ in range(PROBE_LAUNCHES):
-        fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], st["ids"], st["wts"], residual=x, scratch=sc,
-                                    phases=_mingmoe.MM_PHASE_GATE_UP, align=False, w_gu_slabs=st["w_gu_slabs"])
+    with copies("registered"):
+        for _ in range(PROBE_LAUNCHES):
+            fused_moe.fused_moe_prefill(st["xn"], b["w_gu"], b["w_d"], st["ids"], st["wts"], residual=x, scratch=sc,
+                                        phases=_mingmoe.MM_PHASE_GATE_UP, align=False)
     torch.cuda.synchronize()
     del b
     src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda")
@@ -511,14 +555,20 @@ def ingest_metrics(n_experts=64, hidden=2048, inter=1408, threads=4, ref_threads
 # -------------------------------------------------------------------------------------------- CPU baseline
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it: the model name, then family / model / stepping (some hosts report only
+    the brand in the name)."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
+                if not ln.strip():
+                    break  # the first processor's block
+                k, _, v = ln.partition(":")
+                fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return platform.processor() or platform.machine()
+        return platform.processor() or platform.machine()
+    ident = " ".join(f"{k.split()[-1]} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{fields.get('model name', platform.machine())} ({ident})" if ident else fields.get("model name", "")
 
 
 def cpu_baseline(b, bias, n=512, warmup=2, reps=7):
@@ -554,13 +604,10 @@ def cpu_baseline(b, bias, n=512, warmup=2, reps=7):
             "torch_threads": torch.get_num_threads(), "torch": torch.__version__}
 
 
-def box_info():
-    """The GPU this run measured (decode timings of one build differ by up to ~35% between boxes)."""
-    p = torch.cuda.get_device_properties(0)
-    info = {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
-            "host": platform.node()}
-    # clocks from the amdgpu sysfs tables (the current level is marked '*'); read as files, no child
-    # process, so the run stays safe under a profiler that initialises the GPU in every process it starts
+def read_clocks():
+    """Current shader and memory clock levels from the amdgpu sysfs tables (the current level is marked '*'); read
+    as files, no child process, so the run stays safe under a profiler that initialises the GPU in every process it
+    starts."""
     clocks = {}
     for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
         for table in ("pp_dpm_sclk", "pp_dpm_mclk"):
@@ -571,8 +618,15 @@ def box_info():
                 continue
             if cur:
                 clocks[f"{os.path.basename(os.path.dirname(dev))}.{table[7:]}"] = cur[0]
-    info["clocks"] = clocks or "unavailable"
-    return info
+    return clocks or "unavailable"
+
+
+def box_info():
+    """The GPU this run measured (decode timings of one build differ by up to ~35% between boxes). `clocks_idle` is
+    read after the work; the headline's `clocks_under_load` is read while its timed replays run."""
+    p = torch.cuda.get_device_properties(0)
+    return {"name": p.name, "arch": getattr(p, "gcnArchName", ""), "cus": p.multi_processor_count,
+            "host": platform.node(), "clocks_idle": read_clocks()}
 
 
 def main():
@@ -592,20 +646,22 @@ def main():
     t0 = time.time()
     import fused_moe
     b = W.block(seed=0, device="cuda")
-    # the prefill layout copies of the gate/up and down stacks (load-time, outside the timed region; decode reads
-    # w_gu and w_d)
-    b["w_gu_slabs"] = fused_moe.gate_up_slabs(b["w_gu"])
-    b["w_d_slabs"] = fused_moe.down_slabs(b["w_d"])
+    # the prefill layout copies of the gate/up and down stacks, registered for them (load-time, outside the timed
+    # region; decode reads w_gu and w_d): every prefill call on these stacks finds them
+    fused_moe.prefill_copies(b["w_gu"], b["w_d"])
     bias = W.ragged_bias(device="cuda")
     torch.cuda.synchronize()
     log(f"[bench] block ready {time.time() - t0:.1f}s")
-    # The same block with both GEMMs on the row layouts the engine stacks (no prefill copies), for comparison.
-    # It runs first: the first timed work of a fresh process runs about 5 % slower while the GPU clocks ramp up.
+    # A fresh process's first timed work runs about 5 % slower while the GPU clocks ramp up: one untimed pass of the
+    # headline first, then the same block on the row layouts the engine stacks (no copies), then the headline.
+    prefill_metrics(b, 512, bias, args.steps, args.warmup, stream)
     rows = prefill_metrics(b, 512, bias, args.steps, args.warmup, stream, slabs=False)
     log(f"[bench] prefill 512, row layout: {rows['tokens_per_s']:.0f} tok/s, gate/up {rows['gate_up_us']:.1f} us")
     head = prefill_metrics(b, 512, bias, args.steps, args.warmup, stream)
     log(f"[bench] prefill 512: {head['tokens_per_s']:.0f} tok/s, gate/up {head['gate_up_us']:.1f} us")
-    extra = {"prefill_512": head, "prefill_512_row_layout": rows}
+    extra = {"prefill_512": head, "prefill_512_row_layout": rows,
+             "prefill_512_engine_call": engine_call_metrics(b, 512, bias, stream)}
+    log(f"[bench] engine call: {extra['prefill_512_engine_call']}")
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: not args.quick and (not only or k in only))
     if want("zipf"):
@@ -651,6 +707,7 @@ def main():
     if want("ingest"):
         extra["ingest"] = ingest_metrics()
         log(f"[bench] ingest: {extra['ingest']}")
+    b_copy_bytes = (W.EXPERTS + 1) * W.expert_bytes()  # both copies: a second gate/up and down stack
     gu_s = head["gate_up_us"] * 1e-6
     achieved = head["gate_up_bytes"] / gu_s / 1e9
     traffic = None
@@ -666,8 +723,10 @@ def main():
         "config": {"workload": "thinker MoE block prefill, 512 tokens, hidden 2048, 64+1 experts x 1408, "
                                "softmax top-6, ragged router bias", "tokens": 512, "hidden": 2048, "experts": 64,
                    "inter": 1408, "top_k": 6, "graph": True,
-                   "gate_up_weights": "prefill copy of the gate/up stack (gate_up_slabs, made at load)",
-                   "down_weights": "prefill copy of the down stack (down_slabs, made at load)"},
+                   "gate_up_weights": "prefill copy of the gate/up stack (fused_moe.prefill_copies at load, found by "
+                                      "the call)",
+                   "down_weights": "prefill copy of the down stack (the same)",
+                   "copy_bytes_per_layer": b_copy_bytes},
         "roofline": {"bound": "hbm", "kernel": "prefill_gate_up_kernel<false, 128, 8, 64, true>", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
         "cpu_baseline": cpu,

@@ -175,10 +175,39 @@ class on_device:
         return False
 
 
+def version_of(t):
+    """torch's in-place write counter of t (shared by every view of one base tensor), or None for tensors that keep
+    none (made under torch.inference_mode)."""
+    try:
+        return t._version
+    except RuntimeError:
+        return None
+
+
+def source_stamp(w):
+    """What a prefill copy records of the stack it was made from: device, address, shape, strides and the write
+    counter at the time of the copy. A copy is current for a stack while the stamps agree."""
+    return (w.device.index, w.data_ptr(), tuple(w.shape), tuple(w.stride()), version_of(w))
+
+
+def check_copy(copy, w, what):
+    """Refuses (ValueError) a prefill copy that was not made from w by fused_moe.gate_up_slabs / down_slabs, or that
+    w was written to since (torch's write counter moved: the loader's copy_ into the stack, an in-place op)."""
+    stamp = getattr(copy, "_mm_source", None)
+    if stamp is None:
+        raise ValueError(f"{what} must be made by fused_moe.{'gate_up' if what == 'w_gu_slabs' else 'down'}_slabs "
+                         "(it carries the stamp of its source stack)")
+    now = source_stamp(w)
+    if stamp[:4] != now[:4]:
+        raise ValueError(f"{what} was made from another stack than the one passed")
+    if stamp[4] is None or stamp[4] != now[4]:
+        raise ValueError(f"{what} is stale: its stack was written to after the copy was made (make it again)")
+
+
 def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None, w_d_slabs=None):
     """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales); w_gu_slabs /
     w_d_slabs: the prefill copies of w_gu / w_d that fused_moe.gate_up_slabs / down_slabs make (bf16 only), or
-    None."""
+    None. A copy that does not carry the current stamp of its stack is refused (check_copy)."""
     if w_gu.dim() != 3 or w_d.dim() != 3:
         raise ValueError("w_gu and w_d must be 3-D stacked expert tensors")
     E1, two_i, H = w_gu.shape
@@ -212,10 +241,12 @@ def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None, w_d_slabs=None):
         if q or w_gu_slabs.dtype != torch.bfloat16 or not w_gu_slabs.is_contiguous() or \
                 w_gu_slabs.numel() != w_gu.shape[0] * w_gu.shape[1] * w_gu.shape[2] or w_gu_slabs.device != w_gu.device:
             raise ValueError("w_gu_slabs must be the contiguous bf16 prefill copy of w_gu (fused_moe.gate_up_slabs)")
+        check_copy(w_gu_slabs, w_gu, "w_gu_slabs")
         ex.w_gu_slabs = w_gu_slabs.data_ptr()
     if w_d_slabs is not None:
         if q or w_d_slabs.dtype != torch.bfloat16 or not w_d_slabs.is_contiguous() or \
                 w_d_slabs.numel() != w_d.shape[0] * w_d.shape[1] * w_d.shape[2] or w_d_slabs.device != w_d.device:
             raise ValueError("w_d_slabs must be the contiguous bf16 prefill copy of w_d (fused_moe.down_slabs)")
+        check_copy(w_d_slabs, w_d, "w_d_slabs")
         ex.w_d_slabs = w_d_slabs.data_ptr()
     return ex

@@ -108,15 +108,22 @@ __device__ __forceinline__ bool map_tile(const PrefillArgs& a, int NT, int& e, i
   return true;
 }
 
-// 16 int8 -> 16 bf16 (exact), as two uint4 of packed bf16 pairs.
+// Two fp32 values whose low 16 bits are zero -> packed bf16 pair (lo in bits 0-15): the high halves, one v_perm_b32.
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 16 int8 -> 16 bf16 (exact), as two uint4 of packed bf16 pairs. |q| <= 127 has at most 7 significant bits, so
+// fp32(q) has a zero low half and its high half is bf16(q): a byte convert per element and one permute per pair
+// (1.5 VALU ops per element, against 3 for a rounding convert of each value and a shift-or to pack).
 __device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
   const uint32_t in[4] = {q.x, q.y, q.z, q.w};
   uint32_t out[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t v = in[i];
-    out[2 * i] = static_cast<uint32_t>(f32_to_bf16(sbyte(v, 0))) | (static_cast<uint32_t>(f32_to_bf16(sbyte(v, 1))) << 16);
-    out[2 * i + 1] = static_cast<uint32_t>(f32_to_bf16(sbyte(v, 2))) | (static_cast<uint32_t>(f32_to_bf16(sbyte(v, 3))) << 16);
+    out[2 * i] = pack_hi16(sbyte(v, 0), sbyte(v, 1));
+    out[2 * i + 1] = pack_hi16(sbyte(v, 2), sbyte(v, 3));
   }
   lo = make_uint4(out[0], out[1], out[2], out[3]);
   hi = make_uint4(out[4], out[5], out[6], out[7]);
@@ -413,6 +420,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); }, fm_live);
   // the output tile [BM][HALF] goes through LDS (free once every wave is past the last slab), then out in rows
   constexpr int OS = HALF + 8;  // row stride (elements): rows 4 apart start 64 bytes apart on the banks
+  static_assert(static_cast<size_t>(BM) * OS * 2 <= G::LDS, "gate/up output tile must fit in the k-slab LDS");
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds_raw);
   __syncthreads();
 #pragma unroll
@@ -474,6 +482,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
                [&](int j) { return c0 + 16 * j; }, fm_live);
   // the output tile [BM][BN] goes through LDS, then out in rows (as in gate/up)
   constexpr int OS = G::BN + 8;
+  static_assert(static_cast<size_t>(BM) * OS * 2 <= G::LDS, "down output tile must fit in the k-slab LDS");
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds_raw);
   __syncthreads();
 #pragma unroll

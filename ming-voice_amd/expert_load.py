@@ -17,6 +17,7 @@ import os
 import struct
 
 import torch
+from torch.autograd.graph import increment_version
 
 import _mingmoe as _mm
 
@@ -135,4 +136,9 @@ def load_stacked_experts(index, prefix, n_experts, *, shared=True, int8=False, s
         torch.cuda.current_stream(dev).synchronize()  # allocation and any earlier writes to the stack are done
         _mm.check(lib.mm_ingest_experts(arr, len(rows), ex, _mm.ptr(host), _mm.ptr(stage), slot_bytes, threads),
                   "load_stacked_experts")
+    # the library wrote the stacks through raw pointers, which torch's write counters do not see: move them, so
+    # that a prefill copy made before this load counts as stale (fused_moe.prefill_copies)
+    for t in out.values():
+        if _mm.version_of(t) is not None:
+            increment_version(t)
     return out

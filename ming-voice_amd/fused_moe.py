@@ -12,17 +12,25 @@ Experts (plus the shared expert, stored as expert index E) live in stacked tenso
   gate_up_slabs      the prefill copy of a bf16 w_gu (each 64-k slab of 8 rows one 1 KB piece), made once at
                      load; passed as w_gu_slabs, the prefill gate/up GEMM reads it instead of w_gu (same results)
   down_slabs         the same for w_d, passed as w_d_slabs and read by the prefill down GEMM
+  prefill_copies     makes and registers both copies of a stack pair; fused_moe_prefill and moe_block_prefill then
+                     find them by themselves (PREFILL_COPIES = "auto" also makes them on the first eager call)
+
+A copy is bound to the stack it was made from: it records the stack's address, shape, strides and torch's
+write counter, and a copy whose stack was written to since (the loader's copy_ into it, any in-place op) is
+refused when passed explicitly and remade when found in the registry.
 
 CFG and GCFG are kept for callers that read or tune them; the HIP kernels choose their own tiles, so the
 values are advisory.
 """
 import time
+import weakref
 
 import torch
 
 import _mingmoe as _mm
 
-__all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "gate_up_slabs", "down_slabs", "CFG", "GCFG"]
+__all__ = ["fused_moe_decode", "fused_moe_prefill", "quantize_rows_int8", "gate_up_slabs", "down_slabs",
+           "prefill_copies", "release_prefill_copies", "CFG", "GCFG"]
 
 CFG = dict(A=dict(BN=16, BK=256, num_warps=4), B=dict(BN=16, BK=256, num_warps=4))
 GCFG = dict(A=dict(BM=64, BN=64, BK=64, num_warps=4), B=dict(BM=64, BN=128, BK=64, num_warps=4))
@@ -200,7 +208,9 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
     """x: [N, H] bf16; ids: [N, K+1] expert ids per token (shared expert included); weights: [N, K+1] fp32.
     Returns [N, H] bf16 = sum_k weights[:, k] * expert_k(x) (+ residual). w_gu_slabs: gate_up_slabs(w_gu), read by
     the gate/up GEMM instead of w_gu; w_d_slabs: down_slabs(w_d), read by the down GEMM instead of w_d (same
-    results).
+    results). When neither is passed, the copies registered for w_gu / w_d are used (prefill_copies; with
+    PREFILL_COPIES = "auto" an eager call makes them when the device has room), so the reference's call
+    fused_moe_prefill(x, w_gu, w_d, ids, wts) reads the prefill layout without a change.
     scratch (a PrefillScratch) supplies the buffers; phases / align=False run part of the pipeline on
     scratch left by an earlier call, for timing one kernel."""
     _mm.require_gpu(x, w_gu, w_d, ids, weights, s_gu, s_d, residual)
@@ -213,6 +223,8 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
                                 phases=phases & (_mm.MM_PHASE_GATE_UP | _mm.MM_PHASE_DOWN))
     if x.dtype != torch.bfloat16:
         raise ValueError(f"fused_moe_prefill: x must be bf16 (got {x.dtype})")
+    if w_gu_slabs is None and w_d_slabs is None:
+        w_gu_slabs, w_d_slabs = _copies_for(w_gu, w_d)
     ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs, w_d_slabs)
     E1, I = ex.n_slots, ex.inter
     x2 = x if x.is_contiguous() else x.contiguous()
@@ -254,7 +266,7 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
     selection (shared expert appended), align, gate/up, down, combine (+ x).
     Same results as rms_norm -> route -> fused_moe_prefill(residual=x). Returns (y [N, H], ids, wts,
     logits), views of `scratch` (a PrefillScratch made with block=True; allocated when None). w_gu_slabs,
-    w_d_slabs: as in fused_moe_prefill."""
+    w_d_slabs: as in fused_moe_prefill (registered copies are found the same way)."""
     _mm.require_gpu(x, norm_w, w32, w_gu, w_d, bias, s_gu, s_d)
     H = x.shape[-1]
     x2 = x.reshape(-1, H)
@@ -269,6 +281,8 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
         raise ValueError("moe_block_prefill: bias must be a contiguous fp32 [E] tensor")
     if scoring not in _SCORING:
         raise ValueError(f"moe_block_prefill: scoring must be one of {sorted(_SCORING)}")
+    if w_gu_slabs is None and w_d_slabs is None:
+        w_gu_slabs, w_d_slabs = _copies_for(w_gu, w_d)
     ex = _mm.experts(w_gu, w_d, s_gu, s_d, w_gu_slabs, w_d_slabs)
     sc = scratch if scratch is not None else PrefillScratch(N, NK, ex.n_slots, H, ex.inter, x.device, block=True,
                                                              w_dtype=w_gu.dtype)
@@ -296,7 +310,8 @@ def gate_up_slabs(w_gu, out=None):
     out[e, q, t, j, c] = w_gu[e, 8 q + j, 64 t + c], a contiguous [E1, 2I / 8, H / 64, 8, 64] bf16 tensor, so that
     each 64-wide k-slab of 8 consecutive rows is one 1 KB piece. A load-time step: it costs a second gate/up stack
     and lets the prefill gate/up GEMM read a tile's k-slab as 16 pieces of 1 KB (one per direct-load instruction)
-    instead of 128 pieces of 128 bytes. Pass the result as w_gu_slabs."""
+    instead of 128 pieces of 128 bytes. Pass the result as w_gu_slabs, or register it with prefill_copies. The result
+    records w_gu's stamp (_mingmoe.source_stamp); once w_gu is written to, the copy is refused until made again."""
     _mm.require_gpu(w_gu, out)
     if w_gu.dim() != 3 or w_gu.dtype != torch.bfloat16 or w_gu.stride(2) != 1:
         raise ValueError("gate_up_slabs: w_gu must be a bf16 [E1, 2I, H] stack with a contiguous last dim")
@@ -314,6 +329,7 @@ def gate_up_slabs(w_gu, out=None):
     lib = _mm.load()
     with _mm.on_device(w_gu):
         _mm.check(lib.mm_gate_up_slabs(ex, _mm.ptr(q), _mm.stream_of(w_gu)), "gate_up_slabs")
+    q._mm_source = _mm.source_stamp(w_gu)  # what the copy is current for (checked by _mingmoe.experts)
     return q
 
 
@@ -339,7 +355,113 @@ def down_slabs(w_d, out=None):
     lib = _mm.load()
     with _mm.on_device(w_d):
         _mm.check(lib.mm_down_slabs(ex, _mm.ptr(q), _mm.stream_of(w_d)), "down_slabs")
+    q._mm_source = _mm.source_stamp(w_d)
     return q
+
+
+# ------------------------------------------------------------------------- prefill copies bound to their stacks
+
+# "auto": an eager bf16 prefill call on a stack without a registered copy makes one (if the device keeps at
+# least COPY_FREE_FRACTION of its memory free afterwards) and registers it; "registered": only the copies made by
+# prefill_copies are used; "off": the prefill GEMMs read the stacks themselves (the row layout).
+PREFILL_COPIES = "auto"
+COPY_FREE_FRACTION = 0.10
+
+
+class _Entry:
+    """A registered prefill copy: the copy, a weak reference to its stack's base tensor (the entry goes when the
+    stack goes) and whether it was registered explicitly (trusted for stacks that keep no write counter)."""
+    __slots__ = ("copy", "ref", "explicit", "__weakref__")
+
+
+_registry = {}  # stack key (device, address, shape, strides) -> _Entry
+
+
+def _base(w):
+    return w._base if w._base is not None else w
+
+
+def _slab_shape_ok(w):
+    # gate/up copy [E1, 2I, H]: H a multiple of 64, 2I of 8; down copy [E1, H, I]: I a multiple of 64, H of 8
+    return w.dtype == torch.bfloat16 and w.dim() == 3 and w.stride(2) == 1 and \
+        w.shape[2] % 64 == 0 and w.shape[1] % 8 == 0
+
+
+def _register(w, copy, explicit):
+    key = _mm.source_stamp(w)[:4]
+    e = _Entry()
+    e.copy, e.explicit = copy, explicit
+
+    def gone(_ref, key=key, e=e):
+        if _registry.get(key) is e:
+            del _registry[key]
+    e.ref = weakref.ref(_base(w), gone)
+    _registry[key] = e
+
+
+def _registered(w, make):
+    """The current registered copy of stack w, made or remade here when allowed; None for the stack itself."""
+    if PREFILL_COPIES == "off" or not _slab_shape_ok(w):
+        return None
+    key = _mm.source_stamp(w)[:4]
+    e = _registry.get(key)
+    if e is not None and e.ref() is not _base(w):  # another tensor now lives at that address
+        del _registry[key]
+        e = None
+    ver = _mm.version_of(w)
+    if e is not None and ((ver is not None and e.copy._mm_source[4] == ver) or (ver is None and e.explicit)):
+        return e.copy
+    capturing = torch.cuda.is_current_stream_capturing()
+    if e is not None:  # the stack was written to after its copy was made
+        if capturing:
+            raise RuntimeError("fused_moe: an expert stack changed after its prefill copy was made; call "
+                               "fused_moe.prefill_copies(w_gu, w_d) again before capturing")
+        make(w, out=e.copy)
+        return e.copy
+    if capturing or PREFILL_COPIES != "auto" or ver is None:
+        return None
+    free, total = torch.cuda.mem_get_info(w.device)
+    if free - w.numel() * 2 < COPY_FREE_FRACTION * total:
+        return None
+    copy = make(w)
+    _register(w, copy, False)
+    return copy
+
+
+def _copies_for(w_gu, w_d):
+    if w_gu.dtype != torch.bfloat16:
+        return None, None
+    return _registered(w_gu, gate_up_slabs), _registered(w_d, down_slabs)
+
+
+def prefill_copies(w_gu, w_d):
+    """Makes (or remakes) the prefill copies of a bf16 stack pair and registers them: every later
+    fused_moe_prefill / moe_block_prefill on these stacks reads them, with no argument passed. A copy follows its
+    stack: once the stack is written to (torch's write counter moves), the next eager call remakes the copy in
+    place and a call under graph capture raises. Stacks made under torch.inference_mode keep no write counter:
+    their copies are trusted until prefill_copies is called again. Returns (w_gu copy, w_d copy), either None for a
+    shape the layout does not take. Costs a second copy of both stacks (1.125 GB per layer of hidden 2048,
+    64 + 1 experts of 1408)."""
+    _mm.require_gpu(w_gu, w_d)
+    out = []
+    for w, make in ((w_gu, gate_up_slabs), (w_d, down_slabs)):
+        if not _slab_shape_ok(w):
+            out.append(None)
+            continue
+        e = _registry.get(_mm.source_stamp(w)[:4])
+        copy = make(w, out=e.copy if e is not None and e.ref() is _base(w) else None)
+        _register(w, copy, True)
+        out.append(copy)
+    return tuple(out)
+
+
+def release_prefill_copies(*stacks):
+    """Drops the registered copies of the given stacks (of every stack when none is given)."""
+    if not stacks:
+        _registry.clear()
+        return
+    for w in stacks:
+        _registry.pop(_mm.source_stamp(w)[:4], None)
 
 
 def quantize_rows_int8(w, *, scale_dtype=torch.float32):

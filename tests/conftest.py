@@ -14,3 +14,16 @@ for p in (PKG, ROOT):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD Instinct GPU (MI355X / gfx950) and the built HIP library")
+
+
+import pytest  # noqa: E402
+
+
+@pytest.fixture(autouse=True)
+def _prefill_on_the_row_layout(monkeypatch):
+    """Prefill calls read the expert stacks themselves unless a test passes copies or turns the registry on: the row
+    layout stays covered, and tests of the copy registry set fused_moe.PREFILL_COPIES themselves."""
+    import fused_moe
+    monkeypatch.setattr(fused_moe, "PREFILL_COPIES", "off")
+    yield
+    fused_moe.release_prefill_copies()

@@ -243,6 +243,35 @@ def test_moe_block_decode_sigmoid_group_thinker_router():
     close(y, O.moe(xn, w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu(), residual=x.cpu()))
 
 
+@pytest.mark.parametrize("E", [48, 64])
+@pytest.mark.parametrize("scoring", ["sigmoid", "softmax"])
+def test_moe_block_decode_selecting_gate_up(E, scoring):
+    """One bf16 token with at most 64 experts and no groups: the gate/up kernel ranks the logits itself (lanes past E
+    masked). With a bias, sigmoid or softmax scoring and E below and at 64, every output equals the unfused chain
+    rms_norm -> moe_route -> fused_moe_decode bit for bit, and the ids the oracle's selection."""
+    H, I = 1024, 384
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 160 + E, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 161 + E, DEV)
+    w32 = W.normal((E, H), 0.02, 162 + E, DEV, dtype=torch.float32)
+    bias = W.normal((E,), 0.5, 163 + E, DEV, dtype=torch.float32)
+    nw = W.normal((H,), 0.02, 164 + E, DEV, mean=1.0)
+    x = W.tokens(1, seed=165 + E, device=DEV, hidden=H)
+    scale = 2.5 if scoring == "sigmoid" else 1.0
+    y, ids, wts, logits = fused_moe.moe_block_decode(x, nw, 1e-6, w32, w_gu, w_d, top_k=6, bias=bias, scoring=scoring,
+                                                     scale=scale)
+    xn = fused_ops.rms_norm(x, nw, 1e-6)
+    l2 = torch.empty(1, E, device=DEV)
+    i2 = torch.empty(1, 7, device=DEV, dtype=torch.long)
+    w2 = torch.empty(1, 7, device=DEV)
+    fused_ops.moe_route(xn, w32, bias, 1, 1, 6, scale, l2, i2, w2, scoring=scoring)
+    y2 = fused_moe.fused_moe_decode(xn, w_gu, w_d, i2, w2, residual=x)
+    assert torch.equal(logits, l2) and torch.equal(ids, i2) and torch.equal(wts, w2)
+    assert torch.equal(y, y2)
+    ref_ids, _ = O.router_select(logits.cpu(), bias.cpu(), scoring=scoring, top_k=6, scale=scale)
+    assert torch.equal(ids.cpu(), ref_ids)
+    assert int(ids[0, -1]) == E and float(wts[0, -1]) == 1.0
+
+
 @pytest.mark.parametrize("n", [2, 5, 8])
 def test_decode_bf16_batches_and_repeated_experts(blk, n):
     b, cpu = blk

@@ -64,6 +64,62 @@ def test_noalloc_matches_caller_scratch_twice(blk, int8):
         assert torch.isfinite(got[3].float()).all()
 
 
+_CAPTURE_FIRST = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import torch
+import _mingmoe as mm
+import workloads as W
+lib = mm.load()
+dev = "cuda"
+H, I, E, K = 512, 256, 16, 4
+b = W.block(seed=5, device=dev, hidden=H, inter=I, experts=E)
+ex = mm.experts(b["w_gu"], b["w_d"])
+x = W.tokens(2, seed=6, device=dev, hidden=H)
+def bufs():
+    return (torch.empty(2, E, device=dev), torch.empty(2, K + 1, device=dev, dtype=torch.int64),
+            torch.empty(2, K + 1, device=dev), torch.zeros(2, H, device=dev, dtype=torch.bfloat16))
+def common(o):
+    return (mm.ptr(x), 2, H, mm.ptr(b["norm_w"]), W.EPS, mm.ptr(b["w32"]), E, None, mm.MM_SCORE_SOFTMAX, 1, 1, K, 1.0,
+            ctypes.byref(ex), mm.ptr(o[0]), mm.ptr(o[1]), mm.MM_INT64, mm.ptr(o[2]))
+got, want = bufs(), bufs()
+s = torch.cuda.Stream()
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+print("[capture-first] capturing the first noalloc call of this process", flush=True)
+with torch.cuda.graph(g, stream=s):
+    mm.check(lib.mm_moe_block_decode_noalloc(*common(got), 1, mm.ptr(got[3]), H, mm.stream_of(x)), "noalloc")
+a_buf = torch.empty(2 * (K + 1), I, device=dev, dtype=torch.bfloat16)
+ws = torch.empty(2, H, device=dev, dtype=torch.bfloat16)
+mm.check(lib.mm_moe_block_decode(*common(want), mm.ptr(a_buf), mm.ptr(ws), 1, mm.ptr(want[3]), H, mm.stream_of(x)),
+         "caller scratch")
+torch.cuda.synchronize()
+for rep in range(3):
+    for t in got:
+        t.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    for name, a, w in zip(("logits", "ids", "wts", "y"), got, want):
+        assert torch.equal(a, w), (rep, name)
+    z = (x.float() * 2).sum()  # eager work between the replays
+    torch.cuda.synchronize()
+print("[capture-first] ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """A process whose first call of the entry point is made under hipGraph capture (the scratch address is looked up
+    on that call): the graph's replays equal the caller-scratch entry point's eager result, every replay."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_FIRST, os.path.join(root, "ming-voice_amd"), root],
+                       capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "[capture-first] ok" in r.stdout
+
+
 def test_noalloc_rejects_oversize_shape(blk):
     lib = mm.load()
     ex = mm.experts(blk["w_gu"], blk["w_d"])
