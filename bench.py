@@ -108,9 +108,9 @@ class copies:
 
 
 def prefill_setup(b, n, bias, seed, slabs=True, int8=False):
-    """The prefill block on n tokens; slabs: the GEMMs read the prefill copies of b["w_gu"] / b["w_d"] registered
-    with fused_moe.prefill_copies (a load-time layout step), found by the calls themselves; else the stacks. int8:
-    the experts are b["q_gu"] / b["q_d"] with row scales b["s_gu"] / b["s_d"] (no copies)."""
+    """The prefill block on n tokens; slabs: the GEMMs read the prefill copies of the stacks registered with
+    fused_moe.prefill_copies (a load-time layout step), found by the calls themselves; else the stacks. int8: the
+    experts are b["q_gu"] / b["q_d"] with row scales b["s_gu"] / b["s_d"]."""
     import fused_moe
     import workloads as W
     wg, wd = (b["q_gu"], b["q_d"]) if int8 else (b["w_gu"], b["w_d"])
@@ -120,7 +120,7 @@ def prefill_setup(b, n, bias, seed, slabs=True, int8=False):
     sc = fused_moe.PrefillScratch(n, W.TOP_K + 1, E1, H, I, x.device, block=True, w_dtype=wg.dtype)
     st = {"xn": sc.xn, "ids": sc.ids, "wts": sc.wts}
 
-    mode = "registered" if slabs and not int8 else "off"
+    mode = "registered" if slabs else "off"
 
     def step():  # the whole block: RMSNorm + router + select + align + gate/up + down + combine (+ x)
         with copies(mode):
@@ -186,6 +186,7 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8
         "hbm_pct_weights": used * W.expert_bytes(int8=int8, scale_bytes=sb) / (moe_ms * 1e-3) / (HBM_PEAK_GBS * 1e9)
         * 100,
         "weights": f"int8 + {'fp32' if sb == 4 else 'bf16'} row scales" if int8 else "bf16",
+        "mode": st["mode"],
         "gate_up_weights": "slab copy" if st["w_gu_slabs"] is not None else "rows",
         "down_weights": "slab copy" if st["w_d_slabs"] is not None else "rows",
         "clocks_under_load": busy,
@@ -670,6 +671,8 @@ def main():
     if want("int8"):
         # the headline block with int8 experts and fp32 row scales (the reference's int8 stacks), same masters
         W.quantize_block(b, torch.float32)
+        fused_moe.prefill_copies(b["q_gu"], b["q_d"])
+        extra["prefill_512_int8_row_layout"] = prefill_metrics(b, 512, bias, 20, 3, stream, int8=True, slabs=False)
         extra["prefill_512_int8"] = prefill_metrics(b, 512, bias, 20, 3, stream, int8=True)
         log(f"[bench] prefill 512 int8: {extra['prefill_512_int8']}")
     cpu = None

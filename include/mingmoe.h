@@ -62,11 +62,11 @@ extern "C" {
  * with the shared expert in the last slot. The last dim must be contiguous and every row 16-byte
  * aligned. For int8 weights (w_dtype = MM_INT8) s_gu [n_slots, 2*inter] and s_d [n_slots, hidden]
  * hold one scale per output row (s_dtype MM_FP32 or MM_BF16); for bf16 weights they are NULL.
- * w_gu_slabs (optional, bf16 only; NULL for none) is a second copy of w_gu in the prefill layout that
- * mm_gate_up_slabs writes: [n_slots][2*inter/8][hidden/64][8][64], contiguous, so that each 64-wide k-slab
- * of 8 consecutive rows is one 1 KB piece. When it is set the prefill gate/up GEMM reads it instead of
- * w_gu (same results, bit for bit); decode always reads w_gu. w_d_slabs (optional, bf16 only) is the same
- * for w_d, written by mm_down_slabs: [n_slots][hidden/8][inter/64][8][64], read by the prefill down GEMM. */
+ * w_gu_slabs (optional; NULL for none) is a second copy of w_gu in the prefill layout that mm_gate_up_slabs
+ * writes: [n_slots][2*inter/R][hidden/64][R][64] of w_gu's type, contiguous, R = 8 for bf16 and 16 for int8, so
+ * that each 64-wide k-slab of R consecutive rows is one 1 KB piece. When it is set the prefill gate/up GEMM reads
+ * it instead of w_gu (same results, bit for bit); decode always reads w_gu. w_d_slabs (optional) is the same for
+ * w_d, written by mm_down_slabs: [n_slots][hidden/R][inter/64][R][64], read by the prefill down GEMM. */
 typedef struct mm_experts {
   const void* w_gu;
   const void* w_d;
@@ -397,26 +397,26 @@ typedef struct mm_ingest_item {
 int mm_ingest_experts(const mm_ingest_item* items, int64_t n_items, const mm_experts* dst, void* host_staging,
                       void* dev_staging, int64_t slot_bytes, int n_threads);
 
-/* Bytes of the prefill copy of ex->w_gu (n_slots * 2 * inter * hidden * 2), or 0 when the experts cannot have
- * one (int8 weights, hidden not a multiple of 64 or inter not a multiple of 4). */
+/* Bytes of the prefill copy of ex->w_gu (n_slots * 2 * inter * hidden * weight bytes), or 0 when the experts
+ * cannot have one (hidden not a multiple of 64, or 2 * inter not a multiple of R: 8 for bf16, 16 for int8). */
 int64_t mm_gate_up_slabs_bytes(const mm_experts* ex);
 
 /* Writes the prefill copy of ex->w_gu (any row strides) into `out` (mm_gate_up_slabs_bytes bytes, 16-byte
- * aligned): out[e][q][t][j][c] = w_gu[e][8 q + j][64 t + c]. A load-time step like the quantise-on-load
+ * aligned): out[e][q][t][j][c] = w_gu[e][R q + j][64 t + c]. A load-time step like the quantise-on-load
  * hooks (engine.py:126-147); no call of the reference does this: its Triton GEMM reads the row layout. The
- * copy costs a second gate/up stack (750 MB per 64+1-expert layer of hidden 2048, inter 1408) and lets the
- * prefill gate/up GEMM read each k-slab of a weight tile as 16 pieces of 1 KB, one per direct-load
- * instruction, instead of 128 pieces of 128 bytes. */
+ * copy costs a second gate/up stack (750 MB in bf16, 375 MB in int8 per 64+1-expert layer of hidden 2048, inter
+ * 1408) and lets the prefill gate/up GEMM read each k-slab of a weight tile as 1 KB pieces, one per direct-load
+ * instruction, instead of 128-byte (bf16) or 64-byte (int8) row slices. */
 int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream);
 
-/* Bytes of the prefill copy of ex->w_d (n_slots * hidden * inter * 2), or 0 when the experts cannot have one
- * (int8 weights, inter not a multiple of 64 or hidden not a multiple of 8). */
+/* Bytes of the prefill copy of ex->w_d (n_slots * hidden * inter * weight bytes), or 0 when the experts cannot
+ * have one (inter not a multiple of 64, or hidden not a multiple of R: 8 for bf16, 16 for int8). */
 int64_t mm_down_slabs_bytes(const mm_experts* ex);
 
 /* Writes the prefill copy of ex->w_d (any row strides) into `out` (mm_down_slabs_bytes bytes, 16-byte
- * aligned): out[e][q][t][j][c] = w_d[e][8 q + j][64 t + c]. The same load-time step as mm_gate_up_slabs, for
- * the down GEMM's weights (375 MB more per 64+1-expert layer of hidden 2048, inter 1408); no counterpart in
- * the reference. */
+ * aligned): out[e][q][t][j][c] = w_d[e][R q + j][64 t + c]. The same load-time step as mm_gate_up_slabs, for
+ * the down GEMM's weights (375 MB in bf16, 188 MB in int8 more per 64+1-expert layer of hidden 2048, inter 1408);
+ * no counterpart in the reference. */
 int mm_down_slabs(const mm_experts* ex, void* out, void* stream);
 
 #ifdef __cplusplus

@@ -206,8 +206,7 @@ def check_copy(copy, w, what):
 
 def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None, w_d_slabs=None):
     """mm_experts for stacked weights w_gu [E1, 2I, H], w_d [E1, H, I] (bf16 or int8 + scales); w_gu_slabs /
-    w_d_slabs: the prefill copies of w_gu / w_d that fused_moe.gate_up_slabs / down_slabs make (bf16 only), or
-    None. A copy that does not carry the current stamp of its stack is refused (check_copy)."""
+    w_d_slabs: the prefill copies of w_gu / w_d that fused_moe.gate_up_slabs / down_slabs make, or None. A copy that does not carry the current stamp of its stack is refused (check_copy)."""
     if w_gu.dim() != 3 or w_d.dim() != 3:
         raise ValueError("w_gu and w_d must be 3-D stacked expert tensors")
     E1, two_i, H = w_gu.shape
@@ -238,15 +237,15 @@ def experts(w_gu, w_d, s_gu=None, s_d=None, w_gu_slabs=None, w_d_slabs=None):
     else:
         ex.s_dtype = MM_FP32
     if w_gu_slabs is not None:
-        if q or w_gu_slabs.dtype != torch.bfloat16 or not w_gu_slabs.is_contiguous() or \
+        if w_gu_slabs.dtype != w_gu.dtype or not w_gu_slabs.is_contiguous() or \
                 w_gu_slabs.numel() != w_gu.shape[0] * w_gu.shape[1] * w_gu.shape[2] or w_gu_slabs.device != w_gu.device:
-            raise ValueError("w_gu_slabs must be the contiguous bf16 prefill copy of w_gu (fused_moe.gate_up_slabs)")
+            raise ValueError("w_gu_slabs must be the contiguous prefill copy of w_gu (fused_moe.gate_up_slabs)")
         check_copy(w_gu_slabs, w_gu, "w_gu_slabs")
         ex.w_gu_slabs = w_gu_slabs.data_ptr()
     if w_d_slabs is not None:
-        if q or w_d_slabs.dtype != torch.bfloat16 or not w_d_slabs.is_contiguous() or \
+        if w_d_slabs.dtype != w_d.dtype or not w_d_slabs.is_contiguous() or \
                 w_d_slabs.numel() != w_d.shape[0] * w_d.shape[1] * w_d.shape[2] or w_d_slabs.device != w_d.device:
-            raise ValueError("w_d_slabs must be the contiguous bf16 prefill copy of w_d (fused_moe.down_slabs)")
+            raise ValueError("w_d_slabs must be the contiguous prefill copy of w_d (fused_moe.down_slabs)")
         check_copy(w_d_slabs, w_d, "w_d_slabs")
         ex.w_d_slabs = w_d_slabs.data_ptr()
     return ex

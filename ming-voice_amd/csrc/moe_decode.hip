@@ -564,12 +564,14 @@ int check_experts(const char* who, const mm_experts* ex) {
   }
   if (ex->w_gu_slabs) {
     MM_REQUIRE(mm_gate_up_slabs_bytes(ex) > 0,
-               "%s: a prefill copy of w_gu needs bf16 experts, hidden a multiple of 64 and inter a multiple of 4", who);
+               "%s: a prefill copy of w_gu needs hidden a multiple of 64 and inter a multiple of 4 (bf16) or 8 (int8)",
+               who);
     MM_REQUIRE(aligned16(ex->w_gu_slabs), "%s: the prefill copy of w_gu must be 16-byte aligned", who);
   }
   if (ex->w_d_slabs) {
     MM_REQUIRE(mm_down_slabs_bytes(ex) > 0,
-               "%s: a prefill copy of w_d needs bf16 experts, inter a multiple of 64 and hidden a multiple of 8", who);
+               "%s: a prefill copy of w_d needs inter a multiple of 64 and hidden a multiple of 8 (bf16) or 16 (int8)",
+               who);
     MM_REQUIRE(aligned16(ex->w_d_slabs), "%s: the prefill copy of w_d must be 16-byte aligned", who);
   }
   return MM_OK;

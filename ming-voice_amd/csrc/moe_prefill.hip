@@ -54,13 +54,15 @@ constexpr int kXcds = 8;
 #endif
 
 // Rows per piece of the prefill copy of w_gu: [E1][2I/R][H/64][R][64], so a 64-k slab of R consecutive rows is
-// one piece of R * 128 bytes. R = 8 makes a piece the 1 KB that one direct-load instruction of a wave fills (8
-// rows x 128 bytes): measured on the 512-token block, gate/up 163.5 us with the row layout, 156-157 / 146-149 /
-// 140-143 / 142-145 us with R = 2 / 4 / 8 / 16.
+// one piece of R * 64 weights. bf16: R = 8 makes a piece the 1 KB that one direct-load instruction of a wave fills
+// (8 rows x 128 bytes): measured on the 512-token block, gate/up 163.5 us with the row layout, 156-157 / 146-149 /
+// 140-143 / 142-145 us with R = 2 / 4 / 8 / 16. int8: R = 16, the same 1 KB (16 rows x 64 bytes).
 #ifndef MM_SLAB_ROWS
 #define MM_SLAB_ROWS 8
 #endif
 constexpr int kSlabRows = MM_SLAB_ROWS;
+constexpr int kSlabRowsI8 = 2 * kSlabRows;
+constexpr int slab_rows(bool q) { return q ? kSlabRowsI8 : kSlabRows; }
 
 struct PrefillArgs {
   const uint16_t* x;
@@ -79,7 +81,7 @@ struct PrefillArgs {
   int s_dtype;
   int64_t H, I;
   int64_t gu_se, gu_sn, d_se, d_sn, sgu_se, sd_se;
-  int gu_slabs;  // w_gu is the prefill copy: [E1][2I/R][H/64][R][64], R = kSlabRows
+  int gu_slabs;  // w_gu is the prefill copy: [E1][2I/R][H/64][R][64], R = slab_rows(int8)
   int d_slabs;   // w_d is the prefill copy: [E1][H/R][I/64][R][64]
   const uint16_t* res;
   int64_t res_rs;
@@ -402,11 +404,12 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
     const int p = spair[r];
     return p < a.P ? a.x + static_cast<int64_t>(p / a.nk) * a.xs : nullptr;
   };
+  constexpr int R = slab_rows(Q);
   const char* wbase = static_cast<const char*>(a.w_gu) + static_cast<int64_t>(e) * a.gu_se * ES;
   auto wrow = [&](int r) -> const char* {
     const int64_t col = n0 + (r % HALF), rr = r < HALF ? col : I + col;
     // the prefill copy: row rr is row rr % R of piece group rr / R, whose 64-k slabs are R * 64 elements apart
-    const int64_t off = SL ? (rr / kSlabRows) * kSlabRows * a.H + (rr % kSlabRows) * 64 : rr * a.gu_sn;
+    const int64_t off = SL ? (rr / R) * R * a.H + (rr % R) * 64 : rr * a.gu_sn;
     return col < I ? wbase + off * ES : nullptr;
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -416,7 +419,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, a.H, xrow, wrow, SL ? kSlabRows * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<G>(acc, a.H, xrow, wrow, SL ? R * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); }, fm_live);
   // the output tile [BM][HALF] goes through LDS (free once every wave is past the last slab), then out in rows
   constexpr int OS = HALF + 8;  // row stride (elements): rows 4 apart start 64 bytes apart on the banks
@@ -466,10 +469,11 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
     const int p = spair[r];
     return p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
   };
+  constexpr int R = slab_rows(Q);
   const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
   auto wrow = [&](int r) -> const char* {
     const int64_t h = h0 + r;
-    const int64_t off = SL ? (h / kSlabRows) * kSlabRows * I + (h % kSlabRows) * 64 : h * a.d_sn;
+    const int64_t off = SL ? (h / R) * R * I + (h % R) * 64 : h * a.d_sn;
     return h < H ? wbase + off * ES : nullptr;
   };
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -478,7 +482,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, I, xrow, wrow, SL ? kSlabRows * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<G>(acc, I, xrow, wrow, SL ? R * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return c0 + 16 * j; }, fm_live);
   // the output tile [BM][BN] goes through LDS, then out in rows (as in gate/up)
   constexpr int OS = G::BN + 8;
@@ -581,30 +585,46 @@ int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
   constexpr int DOWN_NW = Q ? 4 : MM_PREFILL_DOWN_WAVES_BF16;
   int rc;
   if (phases & MM_PHASE_GATE_UP) {
-    if constexpr (Q) rc = launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
-    else rc = a.gu_slabs ? launch_gate_up<Q, GU_BN, GU_NW, BM, true>(a, nb, st) : launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
+    rc = a.gu_slabs ? launch_gate_up<Q, GU_BN, GU_NW, BM, true>(a, nb, st) : launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
     if (rc) return rc;
   }
   if (phases & MM_PHASE_DOWN) {
-    if constexpr (Q) rc = launch_down<Q, DOWN_BN, DOWN_NW, BM, false>(a, nb, st);
-    else rc = a.d_slabs ? launch_down<Q, DOWN_BN, DOWN_NW, BM, true>(a, nb, st) : launch_down<Q, DOWN_BN, DOWN_NW, BM, false>(a, nb, st);
+    rc = a.d_slabs ? launch_down<Q, DOWN_BN, DOWN_NW, BM, true>(a, nb, st) : launch_down<Q, DOWN_BN, DOWN_NW, BM, false>(a, nb, st);
     if (rc) return rc;
   }
   return MM_OK;
 }
 
-// The prefill copy of a weight stack w [E1, rows, K] (w_gu: rows 2I, K = H; w_d: rows H, K = I), one 16-byte
-// chunk per thread in output order (grid-stride): chunk c of expert e is 8-element piece c % 8 of row
-// j = (c / 8) % R of k-slab t = (c / 8R) % KT of row group q = c / (8R KT), KT = K / 64, R = kSlabRows.
-__global__ __launch_bounds__(256) void slab_copy_kernel(const uint16_t* __restrict__ w, int64_t se, int64_t sn,
-                                                       int64_t rows, int64_t H, int64_t total, uint4* __restrict__ out) {
-  const int64_t per = rows * H / 8, KT = H / 64;
+// The prefill copy of a weight stack w [E1, rows, K] of ES-byte weights (w_gu: rows 2I, K = H; w_d: rows H, K = I),
+// one 16-byte chunk per thread in output order (grid-stride). A piece (64 chunks, 1 KB) holds the 64-k slab of R
+// rows, C = 64 * ES / 16 chunks per row: chunk c of expert e is chunk c % C of row j = (c / C) % R of k-slab
+// t = (c / 64) % KT of row group q = c / (64 KT), KT = K / 64, R = 64 / C.
+template <int ES>
+__global__ __launch_bounds__(256) void slab_copy_kernel(const char* __restrict__ w, int64_t se, int64_t sn,
+                                                       int64_t rows, int64_t K, int64_t total, uint4* __restrict__ out) {
+  constexpr int C = 64 * ES / 16, R = 64 / C;
+  static_assert(R == slab_rows(ES == 1), "piece rows");
+  const int64_t per = rows * K * ES / 16, KT = K / 64;
   for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < total;
        c += static_cast<int64_t>(gridDim.x) * 256) {
     const int64_t e = c / per, ce = c - e * per;
-    const int64_t piece = ce & 7, j = (ce >> 3) % kSlabRows, t = (ce / (8 * kSlabRows)) % KT, q = (ce / (8 * kSlabRows)) / KT;
-    out[c] = *reinterpret_cast<const uint4*>(w + e * se + (kSlabRows * q + j) * sn + 64 * t + 8 * piece);
+    const int64_t ch = ce % C, j = (ce / C) % R, t = (ce / 64) % KT, q = ce / (64 * KT);
+    out[c] = *reinterpret_cast<const uint4*>(w + (e * se + (R * q + j) * sn + 64 * t) * ES + ch * 16);
   }
+}
+
+// Launches the copy of one stack (ES from the descriptor's weight type).
+int launch_slab_copy(const void* w, int w_dtype, int64_t se, int64_t sn, int64_t rows, int64_t K, int64_t bytes,
+                     void* out, void* stream, const char* what) {
+  const int64_t total = bytes / 16;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+  if (w_dtype == MM_INT8)
+    hipLaunchKernelGGL(slab_copy_kernel<1>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
+                       static_cast<const char*>(w), se, sn, rows, K, total, static_cast<uint4*>(out));
+  else
+    hipLaunchKernelGGL(slab_copy_kernel<2>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
+                       static_cast<const char*>(w), se, sn, rows, K, total, static_cast<uint4*>(out));
+  return mm::check_launch(what);
 }
 
 }  // namespace
@@ -613,54 +633,56 @@ namespace mm {
 int check_experts(const char* who, const mm_experts* ex);
 }
 
+static int64_t weight_bytes(const mm_experts* ex) {
+  return ex->w_dtype == MM_INT8 ? 1 : ex->w_dtype == MM_BF16 ? 2 : 0;
+}
+
 extern "C" int64_t mm_gate_up_slabs_bytes(const mm_experts* ex) {
-  if (!ex || ex->w_dtype != MM_BF16 || ex->hidden <= 0 || ex->hidden % 64 != 0 || ex->inter <= 0 ||
-      (2 * ex->inter) % kSlabRows != 0 || ex->n_slots <= 0)
+  if (!ex || weight_bytes(ex) == 0 || ex->hidden <= 0 || ex->hidden % 64 != 0 || ex->inter <= 0 ||
+      (2 * ex->inter) % slab_rows(ex->w_dtype == MM_INT8) != 0 || ex->n_slots <= 0)
     return 0;
-  return ex->n_slots * 2 * ex->inter * ex->hidden * 2;
+  return ex->n_slots * 2 * ex->inter * ex->hidden * weight_bytes(ex);
 }
 
 extern "C" int mm_gate_up_slabs(const mm_experts* ex, void* out, void* stream) {
   // only w_gu is read: w_d, the scales and w_gu_slabs may be unset
   MM_REQUIRE(ex && ex->w_gu, "gate_up_slabs: null expert descriptor or w_gu");
   const int64_t bytes = mm_gate_up_slabs_bytes(ex);
-  MM_REQUIRE(bytes > 0, "gate_up_slabs: needs bf16 experts, hidden a multiple of 64 and 2 * inter a multiple of %d", kSlabRows);
+  MM_REQUIRE(bytes > 0,
+             "gate_up_slabs: needs bf16 or int8 experts, hidden a multiple of 64 and 2 * inter a multiple of %d (bf16) "
+             "or %d (int8)", kSlabRows, kSlabRowsI8);
+  const int64_t es = weight_bytes(ex);
   MM_REQUIRE(ex->gu_stride_n >= ex->hidden && ex->gu_stride_e >= 2 * ex->inter * ex->gu_stride_n,
              "gate_up_slabs: w_gu strides do not describe [E, 2I, H] with a contiguous last dim");
-  MM_REQUIRE(mm::aligned16(ex->w_gu) && (ex->gu_stride_n * 2) % 16 == 0 && (ex->gu_stride_e * 2) % 16 == 0,
+  MM_REQUIRE(mm::aligned16(ex->w_gu) && (ex->gu_stride_n * es) % 16 == 0 && (ex->gu_stride_e * es) % 16 == 0,
              "gate_up_slabs: w_gu rows must be 16-byte aligned");
   MM_REQUIRE(out && mm::aligned16(out), "gate_up_slabs: out must be a 16-byte aligned buffer");
-  const int64_t total = bytes / 16;
-  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(slab_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
-                     static_cast<const uint16_t*>(ex->w_gu), ex->gu_stride_e, ex->gu_stride_n, 2 * ex->inter,
-                     ex->hidden, total, static_cast<uint4*>(out));
-  return mm::check_launch("gate_up_slabs");
+  return launch_slab_copy(ex->w_gu, ex->w_dtype, ex->gu_stride_e, ex->gu_stride_n, 2 * ex->inter, ex->hidden, bytes, out,
+                          stream, "gate_up_slabs");
 }
 
 extern "C" int64_t mm_down_slabs_bytes(const mm_experts* ex) {
-  if (!ex || ex->w_dtype != MM_BF16 || ex->inter <= 0 || ex->inter % 64 != 0 || ex->hidden <= 0 ||
-      ex->hidden % kSlabRows != 0 || ex->n_slots <= 0)
+  if (!ex || weight_bytes(ex) == 0 || ex->inter <= 0 || ex->inter % 64 != 0 || ex->hidden <= 0 ||
+      ex->hidden % slab_rows(ex->w_dtype == MM_INT8) != 0 || ex->n_slots <= 0)
     return 0;
-  return ex->n_slots * ex->hidden * ex->inter * 2;
+  return ex->n_slots * ex->hidden * ex->inter * weight_bytes(ex);
 }
 
 extern "C" int mm_down_slabs(const mm_experts* ex, void* out, void* stream) {
   // only w_d is read: w_gu, the scales and the copies may be unset
   MM_REQUIRE(ex && ex->w_d, "down_slabs: null expert descriptor or w_d");
   const int64_t bytes = mm_down_slabs_bytes(ex);
-  MM_REQUIRE(bytes > 0, "down_slabs: needs bf16 experts, inter a multiple of 64 and hidden a multiple of %d", kSlabRows);
+  MM_REQUIRE(bytes > 0,
+             "down_slabs: needs bf16 or int8 experts, inter a multiple of 64 and hidden a multiple of %d (bf16) or %d "
+             "(int8)", kSlabRows, kSlabRowsI8);
+  const int64_t es = weight_bytes(ex);
   MM_REQUIRE(ex->d_stride_n >= ex->inter && ex->d_stride_e >= ex->hidden * ex->d_stride_n,
              "down_slabs: w_d strides do not describe [E, H, I] with a contiguous last dim");
-  MM_REQUIRE(mm::aligned16(ex->w_d) && (ex->d_stride_n * 2) % 16 == 0 && (ex->d_stride_e * 2) % 16 == 0,
+  MM_REQUIRE(mm::aligned16(ex->w_d) && (ex->d_stride_n * es) % 16 == 0 && (ex->d_stride_e * es) % 16 == 0,
              "down_slabs: w_d rows must be 16-byte aligned");
   MM_REQUIRE(out && mm::aligned16(out), "down_slabs: out must be a 16-byte aligned buffer");
-  const int64_t total = bytes / 16;
-  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-  hipLaunchKernelGGL(slab_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, MM_STREAM(stream),
-                     static_cast<const uint16_t*>(ex->w_d), ex->d_stride_e, ex->d_stride_n, ex->hidden, ex->inter, total,
-                     static_cast<uint4*>(out));
-  return mm::check_launch("down_slabs");
+  return launch_slab_copy(ex->w_d, ex->w_dtype, ex->d_stride_e, ex->d_stride_n, ex->hidden, ex->inter, bytes, out, stream,
+                          "down_slabs");
 }
 
 extern "C" int32_t mm_prefill_block_m(int64_t n_tokens, int64_t nk, int64_t n_slots, int w_dtype) {
@@ -701,11 +723,11 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   a.sorted_ids = sorted_ids;
   a.bexp = bexp;
   a.offsets = expert_offsets;
-  // bf16 experts with a prefill copy of w_gu: the gate/up GEMM reads that copy (64-k slabs 64 R elements apart)
-  a.gu_slabs = ex->w_gu_slabs && ex->w_dtype == MM_BF16 ? 1 : 0;
+  // experts with a prefill copy of w_gu: the gate/up GEMM reads that copy (64-k slabs 64 R elements apart)
+  a.gu_slabs = ex->w_gu_slabs ? 1 : 0;
   a.w_gu = a.gu_slabs ? ex->w_gu_slabs : ex->w_gu;
   // the same for w_d and the down GEMM
-  a.d_slabs = ex->w_d_slabs && ex->w_dtype == MM_BF16 ? 1 : 0;
+  a.d_slabs = ex->w_d_slabs ? 1 : 0;
   a.w_d = a.d_slabs ? ex->w_d_slabs : ex->w_d;
   a.s_gu = ex->s_gu;
   a.s_d = ex->s_d;

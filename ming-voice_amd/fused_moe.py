@@ -305,27 +305,33 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
     return sc.y, sc.ids, sc.wts, sc.logits
 
 
+def _piece_rows(w):
+    """Rows per 1 KB piece of the prefill layout: 8 for bf16 weights (128 bytes of a 64-k slab each), 16 for int8."""
+    return 8 if w.dtype == torch.bfloat16 else 16
+
+
 def gate_up_slabs(w_gu, out=None):
-    """The prefill copy of a bf16 gate/up stack w_gu [E1, 2I, H] (H a multiple of 64, I of 4):
-    out[e, q, t, j, c] = w_gu[e, 8 q + j, 64 t + c], a contiguous [E1, 2I / 8, H / 64, 8, 64] bf16 tensor, so that
-    each 64-wide k-slab of 8 consecutive rows is one 1 KB piece. A load-time step: it costs a second gate/up stack
-    and lets the prefill gate/up GEMM read a tile's k-slab as 16 pieces of 1 KB (one per direct-load instruction)
-    instead of 128 pieces of 128 bytes. Pass the result as w_gu_slabs, or register it with prefill_copies. The result
+    """The prefill copy of a gate/up stack w_gu [E1, 2I, H], bf16 or int8 (H a multiple of 64; 2I of R, R = 8 for
+    bf16 and 16 for int8): out[e, q, t, j, c] = w_gu[e, R q + j, 64 t + c], a contiguous [E1, 2I / R, H / 64, R, 64]
+    tensor of w_gu's dtype, so that each 64-wide k-slab of R consecutive rows is one 1 KB piece. A load-time step: it
+    costs a second gate/up stack and lets the prefill gate/up GEMM read a tile's k-slab as 1 KB pieces (one per
+    direct-load instruction) instead of 128- (bf16) or 64-byte (int8) row slices. Pass the result as w_gu_slabs, or register it with prefill_copies. The result
     records w_gu's stamp (_mingmoe.source_stamp); once w_gu is written to, the copy is refused until made again."""
     _mm.require_gpu(w_gu, out)
-    if w_gu.dim() != 3 or w_gu.dtype != torch.bfloat16 or w_gu.stride(2) != 1:
-        raise ValueError("gate_up_slabs: w_gu must be a bf16 [E1, 2I, H] stack with a contiguous last dim")
+    if w_gu.dim() != 3 or w_gu.dtype not in (torch.bfloat16, torch.int8) or w_gu.stride(2) != 1:
+        raise ValueError("gate_up_slabs: w_gu must be a bf16 or int8 [E1, 2I, H] stack with a contiguous last dim")
     E1, two_i, H = w_gu.shape
-    if H % 64 or two_i % 8:
-        raise ValueError(f"gate_up_slabs: hidden ({H}) must be a multiple of 64 and 2I ({two_i}) a multiple of 8")
+    R = _piece_rows(w_gu)
+    if H % 64 or two_i % R:
+        raise ValueError(f"gate_up_slabs: hidden ({H}) must be a multiple of 64 and 2I ({two_i}) a multiple of {R}")
     ex = _mm.Experts()  # only w_gu is read
-    ex.w_gu, ex.w_dtype, ex.s_dtype = w_gu.data_ptr(), _mm.MM_BF16, _mm.MM_FP32
+    ex.w_gu, ex.w_dtype, ex.s_dtype = w_gu.data_ptr(), _mm.dtype_code(w_gu), _mm.MM_FP32
     ex.n_slots, ex.hidden, ex.inter = E1, H, two_i // 2
     ex.gu_stride_e, ex.gu_stride_n = w_gu.stride(0), w_gu.stride(1)
-    shape = (E1, two_i // 8, H // 64, 8, 64)
-    q = torch.empty(shape, device=w_gu.device, dtype=torch.bfloat16) if out is None else out
-    if q.dtype != torch.bfloat16 or not q.is_contiguous() or tuple(q.shape) != shape:
-        raise ValueError(f"gate_up_slabs: out must be a contiguous bf16 {shape} tensor")
+    shape = (E1, two_i // R, H // 64, R, 64)
+    q = torch.empty(shape, device=w_gu.device, dtype=w_gu.dtype) if out is None else out
+    if q.dtype != w_gu.dtype or not q.is_contiguous() or tuple(q.shape) != shape:
+        raise ValueError(f"gate_up_slabs: out must be a contiguous {w_gu.dtype} {shape} tensor")
     lib = _mm.load()
     with _mm.on_device(w_gu):
         _mm.check(lib.mm_gate_up_slabs(ex, _mm.ptr(q), _mm.stream_of(w_gu)), "gate_up_slabs")
@@ -334,24 +340,25 @@ def gate_up_slabs(w_gu, out=None):
 
 
 def down_slabs(w_d, out=None):
-    """The prefill copy of a bf16 down stack w_d [E1, H, I] (I a multiple of 64, H of 8):
-    out[e, q, t, j, c] = w_d[e, 8 q + j, 64 t + c], a contiguous [E1, H / 8, I / 64, 8, 64] bf16 tensor, laid out
-    as gate_up_slabs lays out w_gu. A load-time step: it costs a second down stack and lets the prefill down GEMM
+    """The prefill copy of a down stack w_d [E1, H, I], bf16 or int8 (I a multiple of 64, H of R):
+    out[e, q, t, j, c] = w_d[e, R q + j, 64 t + c], a contiguous [E1, H / R, I / 64, R, 64] tensor, laid out as
+    gate_up_slabs lays out w_gu. A load-time step: it costs a second down stack and lets the prefill down GEMM
     read each k-slab of a weight tile as 1 KB pieces. Pass the result as w_d_slabs."""
     _mm.require_gpu(w_d, out)
-    if w_d.dim() != 3 or w_d.dtype != torch.bfloat16 or w_d.stride(2) != 1:
-        raise ValueError("down_slabs: w_d must be a bf16 [E1, H, I] stack with a contiguous last dim")
+    if w_d.dim() != 3 or w_d.dtype not in (torch.bfloat16, torch.int8) or w_d.stride(2) != 1:
+        raise ValueError("down_slabs: w_d must be a bf16 or int8 [E1, H, I] stack with a contiguous last dim")
     E1, H, I = w_d.shape
-    if I % 64 or H % 8:
-        raise ValueError(f"down_slabs: inter ({I}) must be a multiple of 64 and hidden ({H}) a multiple of 8")
+    R = _piece_rows(w_d)
+    if I % 64 or H % R:
+        raise ValueError(f"down_slabs: inter ({I}) must be a multiple of 64 and hidden ({H}) a multiple of {R}")
     ex = _mm.Experts()  # only w_d is read
-    ex.w_d, ex.w_dtype, ex.s_dtype = w_d.data_ptr(), _mm.MM_BF16, _mm.MM_FP32
+    ex.w_d, ex.w_dtype, ex.s_dtype = w_d.data_ptr(), _mm.dtype_code(w_d), _mm.MM_FP32
     ex.n_slots, ex.hidden, ex.inter = E1, H, I
     ex.d_stride_e, ex.d_stride_n = w_d.stride(0), w_d.stride(1)
-    shape = (E1, H // 8, I // 64, 8, 64)
-    q = torch.empty(shape, device=w_d.device, dtype=torch.bfloat16) if out is None else out
-    if q.dtype != torch.bfloat16 or not q.is_contiguous() or tuple(q.shape) != shape:
-        raise ValueError(f"down_slabs: out must be a contiguous bf16 {shape} tensor")
+    shape = (E1, H // R, I // 64, R, 64)
+    q = torch.empty(shape, device=w_d.device, dtype=w_d.dtype) if out is None else out
+    if q.dtype != w_d.dtype or not q.is_contiguous() or tuple(q.shape) != shape:
+        raise ValueError(f"down_slabs: out must be a contiguous {w_d.dtype} {shape} tensor")
     lib = _mm.load()
     with _mm.on_device(w_d):
         _mm.check(lib.mm_down_slabs(ex, _mm.ptr(q), _mm.stream_of(w_d)), "down_slabs")
@@ -361,7 +368,7 @@ def down_slabs(w_d, out=None):
 
 # ------------------------------------------------------------------------- prefill copies bound to their stacks
 
-# "auto": an eager bf16 prefill call on a stack without a registered copy makes one (if the device keeps at
+# "auto": an eager prefill call on a stack without a registered copy makes one (if the device keeps at
 # least COPY_FREE_FRACTION of its memory free afterwards) and registers it; "registered": only the copies made by
 # prefill_copies are used; "off": the prefill GEMMs read the stacks themselves (the row layout).
 PREFILL_COPIES = "auto"
@@ -382,9 +389,9 @@ def _base(w):
 
 
 def _slab_shape_ok(w):
-    # gate/up copy [E1, 2I, H]: H a multiple of 64, 2I of 8; down copy [E1, H, I]: I a multiple of 64, H of 8
-    return w.dtype == torch.bfloat16 and w.dim() == 3 and w.stride(2) == 1 and \
-        w.shape[2] % 64 == 0 and w.shape[1] % 8 == 0
+    # gate/up copy [E1, 2I, H]: H a multiple of 64, 2I of R; down copy [E1, H, I]: I a multiple of 64, H of R
+    return w.dtype in (torch.bfloat16, torch.int8) and w.dim() == 3 and w.stride(2) == 1 and \
+        w.shape[2] % 64 == 0 and w.shape[1] % _piece_rows(w) == 0
 
 
 def _register(w, copy, explicit):
@@ -392,9 +399,9 @@ def _register(w, copy, explicit):
     e = _Entry()
     e.copy, e.explicit = copy, explicit
 
-    def gone(_ref, key=key, e=e):
-        if _registry.get(key) is e:
-            del _registry[key]
+    def gone(_ref, key=key, e=e, reg=_registry):  # reg bound now: module globals are gone at interpreter exit
+        if reg.get(key) is e:
+            del reg[key]
     e.ref = weakref.ref(_base(w), gone)
     _registry[key] = e
 
@@ -421,7 +428,7 @@ def _registered(w, make):
     if capturing or PREFILL_COPIES != "auto" or ver is None:
         return None
     free, total = torch.cuda.mem_get_info(w.device)
-    if free - w.numel() * 2 < COPY_FREE_FRACTION * total:
+    if free - w.numel() * w.element_size() < COPY_FREE_FRACTION * total:
         return None
     copy = make(w)
     _register(w, copy, False)
@@ -429,19 +436,17 @@ def _registered(w, make):
 
 
 def _copies_for(w_gu, w_d):
-    if w_gu.dtype != torch.bfloat16:
-        return None, None
     return _registered(w_gu, gate_up_slabs), _registered(w_d, down_slabs)
 
 
 def prefill_copies(w_gu, w_d):
-    """Makes (or remakes) the prefill copies of a bf16 stack pair and registers them: every later
+    """Makes (or remakes) the prefill copies of a stack pair (bf16, or int8 without their scales) and registers them: every later
     fused_moe_prefill / moe_block_prefill on these stacks reads them, with no argument passed. A copy follows its
     stack: once the stack is written to (torch's write counter moves), the next eager call remakes the copy in
     place and a call under graph capture raises. Stacks made under torch.inference_mode keep no write counter:
     their copies are trusted until prefill_copies is called again. Returns (w_gu copy, w_d copy), either None for a
-    shape the layout does not take. Costs a second copy of both stacks (1.125 GB per layer of hidden 2048,
-    64 + 1 experts of 1408)."""
+    shape the layout does not take. Costs a second copy of both stacks (per layer of hidden 2048, 64 + 1 experts of
+    1408: 1.125 GB in bf16, 563 MB in int8)."""
     _mm.require_gpu(w_gu, w_d)
     out = []
     for w, make in ((w_gu, gate_up_slabs), (w_d, down_slabs)):

@@ -125,9 +125,13 @@ def test_argument_validation_reports_messages():
     ex.hidden, ex.gu_stride_n, ex.gu_stride_e, ex.d_stride_e = 2048, 2048, 2816 * 2048, 2048 * 1408
     ex.w_dtype, ex.s_gu, ex.s_d, ex.s_dtype, ex.sgu_stride_e, ex.sd_stride_e = mm.MM_INT8, 16, 16, mm.MM_FP32, 2816, 2048
     ex.w_gu_slabs = 32
+    assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 65 * 2816 * 2048  # int8 copies: 16-row pieces, 1 byte each
+    ex.hidden, ex.gu_stride_n, ex.gu_stride_e, ex.d_stride_e = 2064, 2064, 2816 * 2064, 2064 * 1408  # 16 x 129
+    ex.sd_stride_e = 2064
     assert lib.mm_gate_up_slabs_bytes(ctypes.byref(ex)) == 0
-    assert "needs bf16 experts" in _err(lib.mm_moe_prefill(P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P,
-                                                          10, 64, None, 0, P, P, P, 2048, 0, None))
+    assert "needs hidden a multiple of 64" in _err(lib.mm_moe_prefill(
+        P, 4, 2064, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10, 64, None, 0, P, P, P, 2064, 0, None))
+    assert "or 16 (int8)" in _err(lib.mm_gate_up_slabs(ctypes.byref(ex), P, None))
     # the prefill copy of w_d
     ex = mm.Experts()
     ex.w_gu, ex.w_d, ex.w_dtype, ex.n_slots, ex.hidden, ex.inter = 16, 16, mm.MM_BF16, 65, 2048, 1408
@@ -141,8 +145,13 @@ def test_argument_validation_reports_messages():
     assert lib.mm_down_slabs_bytes(ctypes.byref(ex)) == 0
     assert "inter a multiple of 64" in _err(lib.mm_down_slabs(ctypes.byref(ex), P, None))
     ex.w_d_slabs = 32
-    assert "a prefill copy of w_d needs bf16 experts" in _err(lib.mm_moe_prefill(
+    assert "a prefill copy of w_d needs inter a multiple of 64" in _err(lib.mm_moe_prefill(
         P, 4, 2048, ctypes.byref(ex), 7, P, mm.MM_INT64, P, P, P, P, 10, 64, None, 0, P, P, P, 2048, 0, None))
+    ex.inter, ex.gu_stride_e, ex.d_stride_e, ex.d_stride_n = 1408, 2816 * 2048, 2048 * 1408, 1408
+    ex.w_dtype, ex.s_gu, ex.s_d, ex.s_dtype, ex.sgu_stride_e, ex.sd_stride_e = mm.MM_INT8, 16, 16, mm.MM_FP32, 2816, 2048
+    assert lib.mm_down_slabs_bytes(ctypes.byref(ex)) == 65 * 2048 * 1408
+    ex.hidden, ex.sd_stride_e, ex.d_stride_e, ex.gu_stride_n, ex.gu_stride_e = 2056, 2056, 2056 * 1408, 2056, 2816 * 2056
+    assert lib.mm_down_slabs_bytes(ctypes.byref(ex)) == 0  # hidden 2056: a multiple of 8, not of 16
 
 
 def test_wrappers_refuse_cpu_tensors():

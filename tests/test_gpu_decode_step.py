@@ -158,7 +158,7 @@ def blk():
 
 @pytest.mark.parametrize("n,int8,slabs", [(32, False, False), (64, False, False), (128, False, False),
                                           (512, False, False), (100, True, False), (512, False, True),
-                                          (2048, False, True)])
+                                          (2048, False, True), (512, True, True)])
 def test_moe_block_prefill_graph_replays_follow_new_inputs(blk, n, int8, slabs):
     """moe_block_prefill captured once for a bucket of n token rows and replayed on new rows (new routing,
     new per-expert counts and block layout): outputs, ids and weights equal an eager call every time. With

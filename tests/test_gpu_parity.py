@@ -464,6 +464,48 @@ def test_down_slabs_copy_layout():
         fused_moe.down_slabs(W.normal((2, 8, 96), 1.0, 149, DEV))
 
 
+def test_int8_slab_copies_layout():
+    """int8 stacks take 16-row pieces: out[e, q, t, j, c] = w[e, 16 q + j, 64 t + c] (gate/up and down copies, from a
+    contiguous stack and from a strided view)."""
+    g = torch.Generator().manual_seed(155)
+    w = torch.randint(-127, 128, (3, 64, 320), generator=g, dtype=torch.int8).to(DEV)
+    want = w.reshape(3, 4, 16, 5, 64).permute(0, 1, 3, 2, 4).contiguous()
+    assert torch.equal(fused_moe.gate_up_slabs(w), want) and torch.equal(fused_moe.down_slabs(w), want)
+    big = torch.randint(-127, 128, (3, 80, 384), generator=g, dtype=torch.int8).to(DEV)
+    view = big[:, :64, :320]
+    assert torch.equal(fused_moe.gate_up_slabs(view),
+                       view.contiguous().reshape(3, 4, 16, 5, 64).permute(0, 1, 3, 2, 4).contiguous())
+    with pytest.raises(ValueError, match="multiple of 16"):
+        fused_moe.down_slabs(torch.zeros(2, 24, 64, dtype=torch.int8, device=DEV))
+
+
+@pytest.mark.parametrize("n,sdt", [(100, torch.bfloat16), (512, torch.float32)])
+def test_int8_prefill_reads_the_slab_copy_bit_for_bit(blk, n, sdt):
+    """int8 experts (bf16 or fp32 row scales) with prefill copies of q_gu and q_d: the block and fused_moe_prefill give
+    the row layout's outputs bit for bit, and the oracle's within tolerance."""
+    b, cpu = blk
+    if sdt == torch.float32:
+        q_gu, s_gu = fused_moe.quantize_rows_int8(b["w_gu"], scale_dtype=sdt)
+        q_d, s_d = fused_moe.quantize_rows_int8(b["w_d"], scale_dtype=sdt)
+    else:
+        q_gu, s_gu, q_d, s_d = b["q_gu"], b["s_gu"], b["q_d"], b["s_d"]
+    gq, dq = fused_moe.gate_up_slabs(q_gu), fused_moe.down_slabs(q_d)
+    bias = W.ragged_bias(device=DEV)
+    x = W.tokens(n, seed=190 + n, device=DEV)
+    args = (x, b["norm_w"], W.EPS, b["w32"], q_gu, q_d)
+    y, ids, wts, _ = fused_moe.moe_block_prefill(*args, top_k=6, bias=bias, s_gu=s_gu, s_d=s_d)
+    for g_, d_ in ((gq, None), (None, dq), (gq, dq)):
+        yq, idq, _, _ = fused_moe.moe_block_prefill(*args, top_k=6, bias=bias, s_gu=s_gu, s_d=s_d, w_gu_slabs=g_,
+                                                    w_d_slabs=d_)
+        assert torch.equal(idq, ids) and torch.equal(yq, y)
+    xn = fused_ops.rms_norm(x, b["norm_w"], W.EPS)
+    y2 = fused_moe.fused_moe_prefill(xn, q_gu, q_d, ids, wts, s_gu=s_gu, s_d=s_d, residual=x, w_gu_slabs=gq,
+                                     w_d_slabs=dq)
+    assert torch.equal(y2, y)
+    c = {"q_gu": q_gu.cpu(), "q_d": q_d.cpu(), "s_gu": s_gu.cpu(), "s_d": s_d.cpu()}
+    close(y, _oracle_moe(c, xn, ids, wts, int8=True, residual=x.cpu()))
+
+
 @pytest.mark.parametrize("n,kind", [(100, "ragged"), (512, "ragged"), (2048, "zipf")])
 def test_prefill_reads_the_slab_copy_bit_for_bit(blk, n, kind):
     """With the slab copies of w_gu and w_d (each alone and both) the prefill block and fused_moe_prefill give the
