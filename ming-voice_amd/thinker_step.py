@@ -1,0 +1,252 @@
+"""The hybrid thinker's greedy decode step (engine.py:665-689) on this build's kernels, built from the engine's objects.
+
+FastThinkerStep(model, cache_layers, tok_buf, pos_buf) takes what engine.Thinker holds once it is loaded and patched
+(engine.py:570-660): `model` is Thinker.model, `cache_layers` Thinker._layers, `tok_buf` / `pos_buf` its [1, 1] token
+and [1] position buffers. It reads, by the attribute paths the engine and its dev scripts use:
+
+  model.model.word_embeddings.weight     the input row of a step (engine.py:686)
+  model.model.layers[i]                  .attention, .attention_layer_type ("attention" = an MLA layer,
+                                         engine.py:640), .input_layernorm, .post_attention_layernorm, .mlp
+                                         (engine.py:1277, 1291; dev/profile_decode_layers.py:12-13)
+  model.model.norm, model.lm_head        the final norm and the head (engine.py:678-679)
+  RMSNorm modules                        .weight, .variance_epsilon (engine.py:229)
+  KDA attention (engine.py:234-267)      q_proj, k_proj, v_proj, f_a_proj, g_a_proj, b_proj (fused here into one GEMV
+                                         with the input norm), q_conv1d / k_conv1d / v_conv1d, f_b_proj, g_b_proj,
+                                         A_log, dt_bias, lower_bound, o_norm (.weight, .eps), o_proj, num_heads,
+                                         head_k_dim, head_dim; the LoRA gate form (no_kda_lora false)
+  MoE block, as _patch_moe leaves it     w_gu / w_d (or q_gu, q_d, s_gu, s_d for int8 experts) with the shared expert
+  (engine.py:313-391)                    in the last slot; gate.w32, gate.expert_bias, gate.top_k, gate.n_group,
+                                         gate.topk_group, gate.routed_scaling_factor (engine.py:284-297, 326-333)
+  cache_layers[i]                        engine._KDAState (.keys: the fp32 state [1, H, K, V]; .values: the q, k, v
+                                         conv caches [1, C, W]) or engine._MLAState (.k [1, nh, max_ctx, dqk],
+                                         .v [1, nh, max_ctx, dv]) (engine.py:495-526, 636-648)
+
+A step: h = word_embeddings(tok_buf); per layer h += mixer(input_layernorm(h)), then the MoE block with
+post_attention_layernorm and the residual (moe_block_decode: router, experts, combine); logits = lm_head(norm(h));
+tok_buf = argmax(logits); pos_buf += 1. KDA layers run the norm-fused projection GEMV, kda_decode_step (convolutions,
+gate LoRA up-projections, recurrence, gated norm) and the o projection with the residual: 3 launches. MLA layers run
+mla_qkv, mla_decode_attn (cache rows written at pos, attention over 0..pos) and the o projection.
+
+The MLA layers' projections are the model's remote code, which is not in the reference tree: pass
+mla_qkv(li, attention, h) -> (q [nh, dqk], k [nh, dqk], v [nh, dv]) computing a layer's new query, key and value rows
+from its input row h [1, H] (norm included). Without it, a layer whose attention has q_proj, k_proj and v_proj runs
+them fused with the input norm, with no rotary part (the synthetic thinker of this build's benchmark).
+
+Every call enqueues on torch's current stream and can be captured in one hipGraph (engine.py:694-713); the state
+lives in the engine's own buffers, so replays advance it as the engine's decode graphs do.
+"""
+import torch
+
+import fastlinear
+import fused_moe
+import thinker_attn as TA
+
+__all__ = ["FastThinkerStep"]
+
+_SCORING = ("sigmoid", "softmax")
+
+
+def _norm(mod, what):
+    w = getattr(mod, "weight", None)
+    eps = getattr(mod, "variance_epsilon", getattr(mod, "eps", None))
+    if w is None or eps is None:
+        raise ValueError(f"FastThinkerStep: {what} needs .weight and .variance_epsilon (or .eps)")
+    return w, float(eps)
+
+
+def _fuse(mods, what):
+    """One GEMV matrix (and bias, or None) from linear modules applied to the same input, rows stacked in order."""
+    ws = [m.weight for m in mods]
+    bs = [getattr(m, "bias", None) for m in mods]
+    if any(w.dim() != 2 or w.shape[1] != ws[0].shape[1] or w.dtype != torch.bfloat16 for w in ws):
+        raise ValueError(f"FastThinkerStep: {what} projections must be bf16 [out, hidden] matrices")
+    w = torch.cat(ws).contiguous()
+    if all(b is None for b in bs):
+        return w, None
+    b = torch.cat([bb if bb is not None else torch.zeros(ww.shape[0], device=w.device, dtype=w.dtype)
+                   for ww, bb in zip(ws, bs)]).to(torch.bfloat16).contiguous()
+    return w, b
+
+
+def _bias(mod):
+    b = getattr(mod, "bias", None)
+    return None if b is None else b.to(torch.bfloat16).contiguous()
+
+
+class FastThinkerStep:
+    """See the module docstring. scoring: the MoE router's form, "sigmoid" (the thinker's gate: sigmoid + expert
+    bias, group-limited top-k, engine.py:326-333) or "softmax" (softmax top-k, renormalised). n_layers: the first
+    n layers (Thinker.n_layers). fused_kda False runs each KDA core as its five calls (short_conv, the f and g
+    projections, fused_recurrent_kda, rms_norm_gated) instead of kda_decode_step's one kernel. Calling the object
+    runs one step and returns the logits [1, vocab]."""
+
+    def __init__(self, model, cache_layers, tok_buf, pos_buf, *, n_layers=None, scoring="sigmoid", mla_qkv=None,
+                 fused_kda=True):
+        if scoring not in _SCORING:
+            raise ValueError(f"FastThinkerStep: scoring must be one of {_SCORING}")
+        m = model.model
+        layers = list(m.layers)[: n_layers if n_layers is not None else len(m.layers)]
+        if len(cache_layers) < len(layers):
+            raise ValueError(f"FastThinkerStep: {len(layers)} layers but {len(cache_layers)} cache layers")
+        if tok_buf.dtype != torch.int64 or tok_buf.numel() != 1 or pos_buf.dtype != torch.int64 or pos_buf.numel() != 1:
+            raise ValueError("FastThinkerStep: tok_buf and pos_buf must be one-element int64 device tensors")
+        self.embed = m.word_embeddings.weight
+        self.final_norm = _norm(m.norm, "model.model.norm")
+        self.head = model.lm_head.weight
+        self.tok, self.pos = tok_buf, pos_buf
+        self.scoring, self.mla_qkv, self.fused_kda = scoring, mla_qkv, fused_kda
+        dev = self.embed.device
+        self.H = self.embed.shape[1]
+        self.h_in = torch.empty(1, 1, self.H, device=dev, dtype=self.embed.dtype)
+        self.L = [self._layer(li, layer, cache_layers[li]) for li, layer in enumerate(layers)]
+        # router outputs and gated activations, shared by the layers (a layer reads them before the next writes)
+        nk = max(p["blk"]["top_k"] for p in self.L) + 1 if self.L else 1
+        ne = max(p["blk"]["w32"].shape[0] for p in self.L) if self.L else 1
+        inter = max(p["blk"]["inter"] for p in self.L) if self.L else 1
+        self.logits = torch.empty(1, ne, device=dev)
+        self.ids = torch.empty(1, nk, device=dev, dtype=torch.int64)
+        self.wts = torch.empty(1, nk, device=dev)
+        self.a_buf = torch.empty(nk, inter, device=dev, dtype=torch.bfloat16)
+        mla = [p for p in self.L if p["kind"] == "mla"]
+        self.ws = None
+        if mla:
+            nh = max(p["kc"].shape[1] for p in mla)
+            dv = max(p["vc"].shape[-1] for p in mla)
+            max_len = max(p["kc"].shape[2] for p in mla)
+            self.ws = TA.mla_attn_workspace(nh, dv, max_len, dev)
+
+    # ------------------------------------------------------------------------------------------- set-up
+
+    def _layer(self, li, layer, cache):
+        a = layer.attention
+        p = {"ln1": _norm(layer.input_layernorm, f"layer {li} input_layernorm"), "blk": self._moe(li, layer)}
+        if getattr(layer, "attention_layer_type", None) == "attention":  # engine.py:640
+            p["kind"] = "mla"
+            p["kc"], p["vc"] = cache.k, cache.v
+            p["nh"], p["dqk"], p["dv"] = int(a.num_heads), int(a.qk_head_dim), int(a.v_head_dim)
+            if tuple(cache.k.shape[1:2]) != (p["nh"],) or cache.k.shape[-1] != p["dqk"] or cache.v.shape[-1] != p["dv"]:
+                raise ValueError(f"FastThinkerStep: layer {li}: the MLA cache does not match num_heads / head dims")
+            if self.mla_qkv is None:
+                if not all(hasattr(a, n) for n in ("q_proj", "k_proj", "v_proj")):
+                    raise ValueError(f"FastThinkerStep: layer {li} is an MLA layer without q_proj / k_proj / v_proj: "
+                                     "pass mla_qkv(li, attention, h) -> (q, k, v) for the model's projections")
+                p["qkv"], p["qkv_b"] = _fuse([a.q_proj, a.k_proj, a.v_proj], f"layer {li} MLA q | k | v")
+            p["o"], p["o_b"] = a.o_proj.weight, _bias(a.o_proj)
+            return p
+        p["kind"] = "kda"
+        if getattr(a, "no_kda_lora", False):
+            raise ValueError(f"FastThinkerStep: layer {li}: KDA without the gate LoRA (no_kda_lora) is not supported")
+        H, K, V = int(a.num_heads), int(a.head_k_dim), int(a.head_dim)
+        p["heads"], p["K"], p["V"] = H, K, V
+        p["proj"], p["proj_b"] = _fuse([a.q_proj, a.k_proj, a.v_proj, a.f_a_proj, a.g_a_proj, a.b_proj],
+                                       f"layer {li} KDA q | k | v | f_a | g_a | b")
+        p["rank"] = a.f_a_proj.weight.shape[0]
+        if a.g_a_proj.weight.shape[0] != p["rank"] or a.b_proj.weight.shape[0] != H:
+            raise ValueError(f"FastThinkerStep: layer {li}: f_a / g_a ranks differ or b_proj is not [heads, hidden]")
+        convs = (a.q_conv1d, a.k_conv1d, a.v_conv1d)
+        if any(getattr(c, "bias", None) is not None for c in convs):
+            raise ValueError(f"FastThinkerStep: layer {li}: short convolutions with a bias are not supported")
+        p["conv_w"] = tuple(c.weight for c in convs)
+        p["conv"] = tuple(cache.values)
+        p["state"] = cache.keys
+        p["f_b"], p["g_b"] = a.f_b_proj.weight, a.g_b_proj.weight
+        if _bias(a.f_b_proj) is not None or _bias(a.g_b_proj) is not None:
+            raise ValueError(f"FastThinkerStep: layer {li}: f_b_proj / g_b_proj with a bias are not supported")
+        p["A_log"], p["dt_bias"] = a.A_log, a.dt_bias
+        lb = getattr(a, "lower_bound", None)
+        p["lower_bound"] = None if lb is None else float(lb)
+        p["o_norm"] = _norm(a.o_norm, f"layer {li} o_norm")
+        p["o"], p["o_b"] = a.o_proj.weight, _bias(a.o_proj)
+        return p
+
+    def _moe(self, li, layer):
+        mlp, g = layer.mlp, layer.mlp.gate
+        norm_w, eps = _norm(layer.post_attention_layernorm, f"layer {li} post_attention_layernorm")
+        if getattr(mlp, "w_gu", None) is not None:
+            exp = {"w_gu": mlp.w_gu, "w_d": mlp.w_d, "s_gu": None, "s_d": None}
+        elif getattr(mlp, "q_gu", None) is not None:
+            exp = {"w_gu": mlp.q_gu, "w_d": mlp.q_d, "s_gu": mlp.s_gu, "s_d": mlp.s_d}
+        else:
+            raise ValueError(f"FastThinkerStep: layer {li}: the MoE block has no stacked experts (engine._patch_moe)")
+        bias = getattr(g, "expert_bias", None)
+        return dict(exp, norm_w=norm_w, eps=eps, w32=g.w32, bias=None if bias is None else bias.float().contiguous(),
+                    top_k=int(g.top_k), n_group=int(getattr(g, "n_group", 1) or 1),
+                    topk_group=int(getattr(g, "topk_group", 1) or 1),
+                    scale=float(getattr(g, "routed_scaling_factor", 1.0) or 1.0), inter=exp["w_d"].shape[-1])
+
+    # ----------------------------------------------------------------------------------------------- step
+
+    def embed_token(self):
+        """word_embeddings(tok_buf) -> the step's input row [1, H] (a view of a buffer the step owns)."""
+        return TA.embed_rows(self.embed, self.tok, out=self.h_in)[0]
+
+    def mixer(self, li, h):
+        """The attention half of layer li: h -> h + o(mixer(input_layernorm(h)))."""
+        p = self.L[li]
+        sl = fastlinear.small_linear
+        if p["kind"] == "mla":
+            if self.mla_qkv is not None:
+                q, k, v = self.mla_qkv(li, p, h)
+            else:
+                qkv = sl(h, p["qkv"], b=p["qkv_b"], norm=p["ln1"])
+                nq = p["nh"] * p["dqk"]
+                q, k, v = qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:]
+            o = TA.mla_decode_attn(q, k, v, p["kc"], p["vc"], self.pos, workspace=self.ws)
+            return sl(o.reshape(1, -1), p["o"], b=p["o_b"], residual=h)
+        H, K, V, R = p["heads"], p["K"], p["V"], p["rank"]
+        pr = sl(h, p["proj"], b=p["proj_b"], norm=p["ln1"])
+        ow, oe = p["o_norm"]
+        if self.fused_kda:
+            on = TA.kda_decode_step(pr, p["conv_w"], p["conv"], p["f_b"], p["g_b"], p["A_log"], p["dt_bias"], p["state"],
+                                    ow, heads=H, eps=oe, lower_bound=p["lower_bound"])
+            return sl(on.reshape(1, H * V), p["o"], b=p["o_b"], residual=h)
+        nqk, nv = H * K, H * V
+        qkv = [TA.short_conv(pr[:, a:b], c, w) for (a, b), c, w in
+               zip(((0, nqk), (nqk, 2 * nqk), (2 * nqk, 2 * nqk + nv)), p["conv"], p["conv_w"])]
+        base = 2 * nqk + nv
+        f = sl(pr[:, base:base + R], p["f_b"])
+        gg = sl(pr[:, base + R:base + 2 * R], p["g_b"])
+        beta = pr[:, base + 2 * R:]  # the beta projection: the kernel applies its sigmoid
+        o, _ = TA.fused_recurrent_kda(qkv[0].reshape(1, 1, H, K), qkv[1].reshape(1, 1, H, K), qkv[2].reshape(1, 1, H, V),
+                                      f.reshape(1, 1, H, K), beta.reshape(1, 1, H), A_log=p["A_log"],
+                                      dt_bias=p["dt_bias"], initial_state=p["state"], inplace=True,
+                                      use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True,
+                                      lower_bound=p["lower_bound"])
+        on = TA.rms_norm_gated(o.reshape(H, V), gg.reshape(H, V), ow, oe)
+        return sl(on.reshape(1, H * V), p["o"], b=p["o_b"], residual=h)
+
+    def moe(self, li, h):
+        """The MoE half of layer li with its residual (router outputs in the step's shared buffers)."""
+        b = self.L[li]["blk"]
+        return fused_moe.moe_block_decode(h, b["norm_w"], b["eps"], b["w32"], b["w_gu"], b["w_d"], top_k=b["top_k"],
+                                          bias=b["bias"], scoring=self.scoring, n_group=b["n_group"],
+                                          topk_group=b["topk_group"], scale=b["scale"], s_gu=b["s_gu"], s_d=b["s_d"],
+                                          logits=self.logits[:, :b["w32"].shape[0]], ids=self.ids[:, :b["top_k"] + 1],
+                                          wts=self.wts[:, :b["top_k"] + 1], a_buf=self.a_buf)[0]
+
+    def head_logits(self, h):
+        return fastlinear.small_linear(h, self.head, norm=self.final_norm)
+
+    def __call__(self):
+        h = self.embed_token()
+        for li in range(len(self.L)):
+            h = self.moe(li, self.mixer(li, h))
+        logits = self.head_logits(h)
+        TA.argmax_rows(logits, out=self.tok)
+        self.pos.add_(1)
+        return logits
+
+    def trace(self):
+        """The step run eagerly, keeping per layer (input, mixer output, router ids, weights): returns that list, the
+        last layer's output and the logits. The state advances as in a call."""
+        h, out = self.embed_token(), []
+        for li in range(len(self.L)):
+            h_in = h.clone()
+            hm = self.mixer(li, h)
+            h = self.moe(li, hm)
+            nk = self.L[li]["blk"]["top_k"] + 1
+            out.append((h_in, hm.clone(), self.ids[:, :nk].clone(), self.wts[:, :nk].clone()))
+        logits = self.head_logits(h)
+        TA.argmax_rows(logits, out=self.tok)
+        self.pos.add_(1)
+        return out, h, logits

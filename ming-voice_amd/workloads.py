@@ -250,35 +250,41 @@ KDA_HEADS, KDA_DIM, KDA_CONV, KDA_LORA = 16, 128, 4, 128
 MLA_HEADS, MLA_QK, MLA_V = 16, 192, 128
 
 
+def _ns(**kw):
+    from types import SimpleNamespace
+    return SimpleNamespace(**kw)
+
+
+def _linear_ns(w):
+    return _ns(weight=w, bias=None)
+
+
 class HybridThinkerStep:
-    """One decode token of a synthetic hybrid thinker on the HIP kernels (the layer kinds engine.py:636-648 caches):
-    `layers` layers, every `mla_every`-th an MLA layer and the others KDA layers, each followed by the MoE block of
-    ThinkerDecodeStep; final RMSNorm fused into the LM head; the position advances on the device (engine.py:681-686).
-      KDA layer: RMSNorm fused into one GEMV of [q | k | v (16 x 128 each) | f_a | g_a (rank 128) | b (16)];
-        f = f_b(f_a), gg = g_b(g_a); short convolutions of q | k | v (window 4, SiLU, caches [1, 6144, 4]);
-        fused_recurrent_kda (l2-normalised q, k, in-kernel gate with A_log, dt_bias; beta = sigmoid(b) in the kernel; state
-        [1, 16, 128, 128] fp32 in place); gated RMSNorm with gg; o projection + residual. With fused_kda (the default)
-        the part between the two projections runs as kda_decode_step's one kernel.
-      MLA layer: RMSNorm fused into one GEMV of [q | k (16 x 192) | v (16 x 128)]; attention over the static cache
-        (k [1, 16, max_len, 192], v [1, 16, max_len, 128], rows written at pos); o projection + residual.
-    The real model's projection internals (the rotary part of q / k, the latent kv compression) are not modelled:
-    q, k and v come straight from one GEMV. Shapes beyond the configs' hidden 2048 (head counts, dims, the 3:1 mix)
-    are an assumption. Weights ~ N(0, 0.02) (norm weights 1 + N(0, 0.02), A_log, dt_bias ~ N(0, 0.5), conv ~
-    N(0, 0.5)); the caches hold a context of `pos` tokens (random rows, states ~ N(0, 0.1)).
-    A step is greedy decoding's (engine.py:685-689): the input row is the word embedding [vocab, 2048] (~ N(0, 1))
-    of the token in `tok` [1, 1] (int64, on the device), and the step writes the argmax of its logits back there.
-    Calling the object runs one step and returns the logits [1, vocab]."""
+    """One decode token of a synthetic hybrid thinker (the layer kinds engine.py:636-648 caches): `layers` layers,
+    every `mla_every`-th an MLA layer and the others KDA layers, each followed by the MoE block of ThinkerDecodeStep
+    (softmax top-6 + shared expert); final RMSNorm and LM head; greedy: the word embedding [vocab, 2048] (~ N(0, 1))
+    of the token in `tok` is the input row and the argmax of the logits is written back there, the position advances
+    on the device (engine.py:685-689).
+    The weights and caches are held as engine.Thinker holds them (model.model.word_embeddings, .layers[i] with
+    .attention / .attention_layer_type / .input_layernorm / .post_attention_layernorm / .mlp, .norm, model.lm_head,
+    _KDAState- and _MLAState-like cache layers, tok_buf, pos_buf), and the step is the product's
+    thinker_step.FastThinkerStep built from them.
+      KDA layer: q | k | v (16 x 128 each), f_a | g_a (rank 128), b (16) projections, the q / k / v short convolutions
+        (window 4, caches [1, 2048, 4] each), fused_recurrent_kda's state [1, 16, 128, 128] fp32, o_norm, o_proj.
+      MLA layer: q | k (16 x 192), v (16 x 128) projections, no rotary or latent compression (the remote model code
+        that holds them is not in the reference tree), caches k [1, 16, max_len, 192], v [1, 16, max_len, 128].
+    Shapes beyond the configs' hidden 2048 (head counts, dims, the 3:1 mix) are an assumption. Weights ~ N(0, 0.02)
+    (norm weights 1 + N(0, 0.02), A_log, dt_bias ~ N(0, 0.5), conv ~ N(0, 0.5)); the caches hold a context of `pos`
+    tokens (random rows, states ~ N(0, 0.1)). self.L keeps each layer's tensors by name (views of the same memory)
+    for the checks. Calling the object runs one step and returns the logits [1, vocab]."""
 
     def __init__(self, layers=28, device="cuda", vocab=VOCAB, max_len=1024, pos=512, mla_every=4, seed=5000,
                  fused_kda=True):
-        import thinker_attn as TA
-        self.TA = TA
-        self.fused_kda = fused_kda  # the KDA core as kda_decode_step's one kernel, else the five-call chain
-        self.moe = ThinkerDecodeStep(0, device, vocab=vocab, seed=seed)  # the shared router buffers, head, final norm
+        import thinker_step
         H, dev = HIDDEN, device
         kd = KDA_HEADS * KDA_DIM
         self.max_len = max_len
-        self.L = []
+        self.L, mods, caches = [], [], []
         for li in range(layers):
             s = seed + 64 * li
             w = lambda shape, j, std=0.02, **kw: normal(shape, std, s + j, dev, **kw)  # noqa: E731
@@ -290,6 +296,11 @@ class HybridThinkerStep:
                 p["o"] = w((H, MLA_HEADS * MLA_V), 13)
                 p["kc"] = normal((1, MLA_HEADS, max_len, MLA_QK), 1.0, s + 14, dev)
                 p["vc"] = normal((1, MLA_HEADS, max_len, MLA_V), 1.0, s + 15, dev)
+                nq = MLA_HEADS * MLA_QK
+                q, k, v = p["qkv"][:nq], p["qkv"][nq:2 * nq], p["qkv"][2 * nq:]
+                attn = _ns(q_proj=_linear_ns(q), k_proj=_linear_ns(k), v_proj=_linear_ns(v),
+                           o_proj=_linear_ns(p["o"]), num_heads=MLA_HEADS, qk_head_dim=MLA_QK, v_head_dim=MLA_V)
+                caches.append(_ns(k=p["kc"], v=p["vc"]))
             else:
                 p["kind"] = "kda"
                 p["proj"] = torch.cat([w((3 * kd, H), 20), w((KDA_LORA, H), 21), w((KDA_LORA, H), 22),
@@ -297,61 +308,59 @@ class HybridThinkerStep:
                 p["f_b"] = w((kd, KDA_LORA), 24)
                 p["g_b"] = w((kd, KDA_LORA), 25)
                 p["conv_w"] = w((3 * kd, 1, KDA_CONV), 26, std=0.5)
-                p["conv"] = w((1, 3 * kd, KDA_CONV), 27, std=1.0)
+                p["conv"] = tuple(c.clone() for c in w((1, 3 * kd, KDA_CONV), 27, std=1.0).split(kd, dim=1))
                 p["A_log"] = w((KDA_HEADS,), 28, std=0.5, dtype=torch.float32)
                 p["dt_bias"] = w((kd,), 29, std=0.5, dtype=torch.float32)
                 p["o_norm"] = w((KDA_DIM,), 30, mean=1.0)
                 p["o"] = w((H, kd), 31)
                 p["state"] = w((1, KDA_HEADS, KDA_DIM, KDA_DIM), 32, std=0.1, dtype=torch.float32)
+                pr = p["proj"].split([kd, kd, kd, KDA_LORA, KDA_LORA, KDA_HEADS])
+                cw = p["conv_w"].split(kd)
+                conv = lambda wt: _ns(weight=wt, bias=None, hidden_size=kd, kernel_size=(KDA_CONV,))  # noqa: E731
+                attn = _ns(mode="fused_recurrent", q_proj=_linear_ns(pr[0]), k_proj=_linear_ns(pr[1]),
+                           v_proj=_linear_ns(pr[2]), f_a_proj=_linear_ns(pr[3]), g_a_proj=_linear_ns(pr[4]),
+                           b_proj=_linear_ns(pr[5]), f_b_proj=_linear_ns(p["f_b"]), g_b_proj=_linear_ns(p["g_b"]),
+                           q_conv1d=conv(cw[0]), k_conv1d=conv(cw[1]), v_conv1d=conv(cw[2]),
+                           o_norm=_ns(weight=p["o_norm"], eps=1e-5), o_proj=_linear_ns(p["o"]), A_log=p["A_log"],
+                           dt_bias=p["dt_bias"], lower_bound=None, num_heads=KDA_HEADS, head_k_dim=KDA_DIM,
+                           head_dim=KDA_DIM, no_kda_lora=False)
+                caches.append(_ns(keys=p["state"], values=p["conv"]))
+            b = p["blk"]
+            gate = _ns(weight=None, w32=b["w32"], expert_bias=None, top_k=TOP_K, n_group=1, topk_group=1,
+                       routed_scaling_factor=1.0)
+            mods.append(_ns(attention=attn, attention_layer_type="attention" if p["kind"] == "mla" else "kda",
+                            input_layernorm=_ns(weight=p["ln1"], variance_epsilon=EPS),
+                            post_attention_layernorm=_ns(weight=b["norm_w"], variance_epsilon=EPS),
+                            mlp=_ns(gate=gate, w_gu=b["w_gu"], w_d=b["w_d"])))
             self.L.append(p)
         self.embed = normal((vocab, H), 1.0, seed + 1, dev)
+        self.final_norm = normal((HIDDEN,), 0.02, 999, device, mean=1.0)
+        self.head = normal((vocab, HIDDEN), 0.02, 998, device)
+        self.model = _ns(model=_ns(word_embeddings=_ns(weight=self.embed), layers=mods,
+                                   norm=_ns(weight=self.final_norm, variance_epsilon=EPS)),
+                         lm_head=_linear_ns(self.head))
+        self.cache_layers = caches
         self.tok = torch.tensor([[(seed * 7919) % vocab]], device=dev, dtype=torch.long)
-        self.h_in = torch.empty(1, 1, H, device=dev, dtype=torch.bfloat16)
         self.pos = torch.tensor([pos], device=dev, dtype=torch.long)
-        self.ws = TA.mla_attn_workspace(MLA_HEADS, MLA_V, max_len, dev)
+        self.fast = thinker_step.FastThinkerStep(self.model, caches, self.tok, self.pos, scoring="softmax",
+                                                 fused_kda=fused_kda)
 
-    def mixer(self, p, h):
-        """The attention half of a layer: h -> h + o(mixer(norm(h)))."""
-        from fastlinear import small_linear
-        TA = self.TA
-        kd = KDA_HEADS * KDA_DIM
-        if p["kind"] == "mla":
-            qkv = small_linear(h, p["qkv"], norm=(p["ln1"], EPS))
-            nq = MLA_HEADS * MLA_QK
-            o = TA.mla_decode_attn(qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:], p["kc"], p["vc"], self.pos,
-                                   workspace=self.ws)
-            return small_linear(o.reshape(1, -1), p["o"], residual=h)
-        pr = small_linear(h, p["proj"], norm=(p["ln1"], EPS))
-        if self.fused_kda:
-            on = TA.kda_decode_step(pr, p["conv_w"], p["conv"], p["f_b"], p["g_b"], p["A_log"], p["dt_bias"], p["state"],
-                                    p["o_norm"], heads=KDA_HEADS, eps=1e-5)
-            return small_linear(on.reshape(1, kd), p["o"], residual=h)
-        f = small_linear(pr[:, 3 * kd:3 * kd + KDA_LORA], p["f_b"])
-        gg = small_linear(pr[:, 3 * kd + KDA_LORA:3 * kd + 2 * KDA_LORA], p["g_b"])
-        qkv = TA.short_conv(pr[:, :3 * kd], p["conv"], p["conv_w"])
-        b = pr[:, 3 * kd + 2 * KDA_LORA:]  # the beta projection: the kernel applies its sigmoid
-        shp = (1, 1, KDA_HEADS, KDA_DIM)
-        o, _ = TA.fused_recurrent_kda(qkv[:, :kd].reshape(shp), qkv[:, kd:2 * kd].reshape(shp),
-                                      qkv[:, 2 * kd:].reshape(shp), f.reshape(shp), b.reshape(1, 1, KDA_HEADS),
-                                      A_log=p["A_log"], dt_bias=p["dt_bias"], initial_state=p["state"], inplace=True,
-                                      use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True)
-        on = TA.rms_norm_gated(o.reshape(KDA_HEADS, KDA_DIM), gg.reshape(KDA_HEADS, KDA_DIM), p["o_norm"], 1e-5)
-        return small_linear(on.reshape(1, kd), p["o"], residual=h)
+    @property
+    def fused_kda(self):
+        """The KDA cores as kda_decode_step's one kernel (True) or the chain of calls it replaces."""
+        return self.fast.fused_kda
 
-    def embed_token(self):
-        """word_embeddings(tok) -> the step's input row [1, 2048] (a view of a buffer the step owns)."""
-        return self.TA.embed_rows(self.embed, self.tok, out=self.h_in)[0]
+    @fused_kda.setter
+    def fused_kda(self, v):
+        self.fast.fused_kda = v
 
     def __call__(self):
-        from fastlinear import small_linear
-        m = self.moe
-        h = self.embed_token()
-        for p in self.L:
-            h = m.layer_moe(p["blk"], self.mixer(p, h))
-        logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
-        self.TA.argmax_rows(logits, out=self.tok)
-        self.pos.add_(1)
-        return logits
+        return self.fast()
+
+    def trace(self):
+        """thinker_step.FastThinkerStep.trace: per layer (input, mixer output, router ids, weights), the last
+        output, the logits."""
+        return self.fast.trace()
 
     def bytes_per_step(self, pos=None):
         """HBM bytes one step must read or write at position pos (default: the current one): every weight of the
@@ -359,39 +368,24 @@ class HybridThinkerStep:
         router of every MoE block, the embedding row, the LM head and its logits (written, then read by the
         argmax)."""
         pos = int(self.pos) if pos is None else pos
-        H, kd, total = HIDDEN, KDA_HEADS * KDA_DIM, 0
+        H, total = HIDDEN, 0
         for p in self.L:
             if p["kind"] == "mla":
                 total += (p["qkv"].numel() + p["o"].numel()) * 2
                 total += (pos + 1) * MLA_HEADS * (MLA_QK + MLA_V) * 2
             else:
                 total += (p["proj"].numel() + p["f_b"].numel() + p["g_b"].numel() + p["o"].numel()) * 2
-                total += p["conv_w"].numel() * 2 + 2 * p["conv"].numel() * 2 + 2 * p["state"].numel() * 4
+                total += p["conv_w"].numel() * 2 + 2 * sum(c.numel() for c in p["conv"]) * 2 + 2 * p["state"].numel() * 4
             total += H * 2 + (TOP_K + 1) * expert_bytes() + EXPERTS * H * 4
-        vocab = self.moe.head.shape[0]
-        return total + H * 2 + self.moe.head.numel() * 2 + 2 * vocab * 2
+        vocab = self.head.shape[0]
+        return total + H * 2 + self.head.numel() * 2 + 2 * vocab * 2
 
     def state_copy(self):
         """A copy of the step's mutable state: KDA states and conv caches, MLA caches, the position, the token."""
         keys = ("state", "conv", "kc", "vc")
+        clone = lambda t: tuple(c.clone() for c in t) if isinstance(t, tuple) else t.clone()  # noqa: E731
         return {"pos": self.pos.clone(), "tok": self.tok.clone(),
-                "L": [{k: p[k].clone() for k in keys if k in p} for p in self.L]}
-
-    def trace(self):
-        """The step run eagerly, keeping per layer (input, mixer output, router ids, weights); returns that list
-        and the logits. The state advances as in a call."""
-        from fastlinear import small_linear
-        m = self.moe
-        h, out = self.embed_token(), []
-        for p in self.L:
-            h_in = h.clone()
-            hm = self.mixer(p, h)
-            h = m.layer_moe(p["blk"], hm)
-            out.append((h_in, hm.clone(), m.ids.clone(), m.wts.clone()))
-        logits = small_linear(h, m.head, norm=(m.final_norm, EPS))
-        self.TA.argmax_rows(logits, out=self.tok)
-        self.pos.add_(1)
-        return out, h, logits
+                "L": [{k: clone(p[k]) for k in keys if k in p} for p in self.L]}
 
 
 # ------------------------------------------------------------------------------------------- Talker LLM

@@ -223,7 +223,9 @@ def test_hybrid_step_graph_replays_equal_eager_steps():
         assert torch.equal(a["tok"], b["tok"]) and int(b["tok"]) == int(out.float().cpu().argmax()), i
         for la, lb in zip(a["L"], b["L"]):
             for key in la:
-                assert torch.equal(la[key], lb[key]), (i, key)
+                xa, xb = la[key], lb[key]
+                for ta, tb in zip(xa if isinstance(xa, tuple) else (xa,), xb if isinstance(xb, tuple) else (xb,)):
+                    assert torch.equal(ta, tb), (i, key)
     del eager, graphed, g, out
     torch.cuda.empty_cache()
 
@@ -243,7 +245,8 @@ def _oracle_mixer(p, st, h, pos):
     pr = O.small_linear(h, p["proj"].cpu(), norm=(p["ln1"].cpu(), W.EPS))
     f = O.small_linear(pr[:, 3 * kd:3 * kd + W.KDA_LORA], p["f_b"].cpu())
     gg = O.small_linear(pr[:, 3 * kd + W.KDA_LORA:3 * kd + 2 * W.KDA_LORA], p["g_b"].cpu())
-    qkv, _ = A.short_conv(pr[:, :3 * kd], st["conv"][0].cpu(), p["conv_w"][:, 0].cpu())
+    conv = torch.cat([c[0] for c in st["conv"]]).cpu()  # the q, k and v caches of the layer, [3 kd, 4]
+    qkv, _ = A.short_conv(pr[:, :3 * kd], conv, p["conv_w"][:, 0].cpu())
     qkv = qkv.to(BF)
     beta = torch.sigmoid(pr[:, 3 * kd + 2 * W.KDA_LORA:].double())
     shp = (1, W.KDA_HEADS, W.KDA_DIM)
@@ -412,3 +415,43 @@ def test_embed_rows_matches_index_select(dtype, id_dtype):
     assert torch.equal(bad, torch.zeros(2, H, dtype=dtype))
     with pytest.raises(ValueError, match="int64 or int32"):
         TA.embed_rows(table.to(DEV), torch.zeros(1, device=DEV))
+
+
+def test_fast_thinker_step_from_engine_objects_sigmoid_router_and_int8():
+    """thinker_step.FastThinkerStep built from engine-shaped objects (model.model.layers[i].attention / .mlp / norms,
+    _KDAState- and _MLAState-like caches, tok_buf, pos_buf) with the thinker's own router (sigmoid + expert bias, 8
+    groups, top 4 groups, scale 2.5) and int8 experts (q_gu / q_d / s_gu / s_d, as engine._quantize_moe_int8 leaves a
+    block) on one layer: each layer's MoE half equals rms_norm -> moe_route -> fused_moe_decode(residual) on the
+    layer's own input bit for bit, and the step writes the argmax back and advances the position."""
+    import fused_moe
+    import fused_ops
+    import thinker_step
+    print("[thinker_step] engine objects, sigmoid router, int8 layer", flush=True)
+    h = W.HybridThinkerStep(4, DEV, pos=50, seed=7300)
+    E = W.EXPERTS
+    for li, layer in enumerate(h.model.model.layers):
+        g = layer.mlp.gate
+        g.expert_bias = W.normal((E,), 0.05, 7400 + li, DEV, dtype=torch.float32)
+        g.n_group, g.topk_group, g.routed_scaling_factor = 8, 4, 2.5
+    int8_layer = h.model.model.layers[1]
+    q_gu, s_gu = fused_moe.quantize_rows_int8(int8_layer.mlp.w_gu, scale_dtype=torch.float32)
+    q_d, s_d = fused_moe.quantize_rows_int8(int8_layer.mlp.w_d, scale_dtype=torch.float32)
+    int8_layer.mlp.w_gu = int8_layer.mlp.w_d = None
+    int8_layer.mlp.q_gu, int8_layer.mlp.q_d, int8_layer.mlp.s_gu, int8_layer.mlp.s_d = q_gu, q_d, s_gu, s_d
+    step = thinker_step.FastThinkerStep(h.model, h.cache_layers, h.tok, h.pos, scoring="sigmoid")
+    trace, out, logits = step.trace()
+    assert int(h.pos) == 51 and int(h.tok) == int(logits.float().cpu().argmax())
+    for li, (layer, (h_in, hm, ids, wts)) in enumerate(zip(h.model.model.layers, trace)):
+        mlp, g = layer.mlp, layer.mlp.gate
+        xn = fused_ops.rms_norm(hm, layer.post_attention_layernorm.weight, W.EPS)
+        lg = torch.empty(1, E, device=DEV)
+        i2 = torch.empty(1, W.TOP_K + 1, device=DEV, dtype=torch.long)
+        w2 = torch.empty(1, W.TOP_K + 1, device=DEV)
+        fused_ops.moe_route(xn, g.w32, g.expert_bias, 8, 4, W.TOP_K, 2.5, lg, i2, w2)
+        if mlp.w_gu is not None:
+            y = fused_moe.fused_moe_decode(xn, mlp.w_gu, mlp.w_d, i2, w2, residual=hm)
+        else:
+            y = fused_moe.fused_moe_decode(xn, mlp.q_gu, mlp.q_d, i2, w2, s_gu=mlp.s_gu, s_d=mlp.s_d, residual=hm)
+        assert torch.equal(ids, i2) and torch.equal(wts, w2), li
+        nxt = trace[li + 1][0] if li + 1 < len(trace) else out
+        assert torch.equal(nxt, y), li
