@@ -57,7 +57,10 @@ def log(*a):
 
 
 def graph_of(fn, stream):
-    """Captures fn() once into a hipGraph on `stream` (after one eager warm call)."""
+    """Captures fn() once into a hipGraph on `stream` (after one eager warm call). `stream` first waits for the
+    current stream: the warm call reads (and writes) tensors the current stream made, and the caching allocator may
+    have handed them memory whose previous owner that stream's queued kernels still read."""
+    stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         fn()
     stream.synchronize()
@@ -68,7 +71,9 @@ def graph_of(fn, stream):
 
 
 def time_graph(g, stream, reps, warmup=2):
-    """Average ms per replay, from HIP events recorded on the replay stream."""
+    """Average ms per replay, from HIP events recorded on the replay stream (ordered after the current stream's
+    work, and the current stream after the replays)."""
+    stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             g.replay()
@@ -79,6 +84,7 @@ def time_graph(g, stream, reps, warmup=2):
             g.replay()
         e1.record(stream)
         e1.synchronize()
+    torch.cuda.current_stream().wait_stream(stream)
     return e0.elapsed_time(e1) / reps
 
 
@@ -143,6 +149,7 @@ def prefill_metrics(b, n, bias, steps, warmup, stream, seed=70, slabs=True, int8
     x, sc, st, step = prefill_setup(b, n, bias, seed, slabs, int8)
     wg, wd, sg, sd = st["experts"]
     g = graph_of(step, stream)
+    stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             g.replay()

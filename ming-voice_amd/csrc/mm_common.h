@@ -115,6 +115,27 @@ __device__ __forceinline__ float dot4_i8_bf16(uint32_t w, uint32_t x01, uint32_t
   return acc;
 }
 
+// Two fp32 values whose low 16 bits are zero -> packed bf16 pair (lo in bits 0-15): the high halves, one v_perm_b32.
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 16 int8 -> 16 bf16 (exact), as two uint4 of packed bf16 pairs. |q| <= 127 has at most 7 significant bits, so
+// fp32(q) has a zero low half and its high half is bf16(q): a byte convert per element and one permute per pair
+// (1.5 VALU ops per element, against 3 for a rounding convert of each value and a shift-or to pack).
+__device__ __forceinline__ void widen_i8(const uint4& q, uint4& lo, uint4& hi) {
+  const uint32_t in[4] = {q.x, q.y, q.z, q.w};
+  uint32_t out[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = in[i];
+    out[2 * i] = pack_hi16(sbyte(v, 0), sbyte(v, 1));
+    out[2 * i + 1] = pack_hi16(sbyte(v, 2), sbyte(v, 3));
+  }
+  lo = make_uint4(out[0], out[1], out[2], out[3]);
+  hi = make_uint4(out[4], out[5], out[6], out[7]);
+}
+
 // Dot of 16 int8 weights (uint4) with 16 bf16 activations (two uint4).
 __device__ __forceinline__ float dot16_i8_bf16(const uint4& w, const uint4& xa, const uint4& xb, float acc) {
   acc = dot4_i8_bf16(w.x, xa.x, xa.y, acc);

@@ -197,6 +197,10 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
 
 // Several tokens per expert: their activation rows are staged in LDS (bf16). Each weight row pair is loaded
 // once into registers and dotted with every staged row in turn, so registers hold only the weight chunks.
+// int8 chunks are widened once per row pair to packed bf16 (exact) and dotted with v_dot2_f32_bf16: two products
+// per operation and 8 VGPRs per chunk, where widening to fp32 per token or once and keeping the floats (16 VGPRs
+// per chunk, 111 VGPRs at 8 tokens) took longer (gate/up over 28 cold layers at 2 / 4 / 8 tokens 18.7 / 31.4 /
+// 54.6 -> 18.5 / 30.2 / 53.7 us). Requesting the weights before the staging changed nothing (19.0 / 31.1 / 55.3).
 // Needs the row in one pass (nch <= LPR * NC); the caller takes gate_up_one per token otherwise.
 template <bool Q, int LPR, int NC, int R, int MAXT>
 __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cntp, const int* spid, const char* wbase,
@@ -232,19 +236,28 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
       wg[j] = buf16(wr, ok ? goff + static_cast<uint32_t>(c) * 16u : kPast);
       wu[j] = buf16(wr, ok ? uoff + static_cast<uint32_t>(c) * 16u : kPast);
     }
-    for (int t = 0; t < cntp; ++t) {
-      if (Q && MAXT <= 4) {  // re-widen per token: 64 VGPRs (at 8 tokens hoisting the widening pays)
-        keep_raw(wg);
-        keep_raw(wu);
+    uint4 gl[NC], gh[NC], ul[NC], uh[NC];  // int8: the chunks widened to bf16 (elements 0-7, 8-15)
+    if constexpr (Q) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        widen_i8(wg[j], gl[j], gh[j]);
+        widen_i8(wu[j], ul[j], uh[j]);
       }
+    }
+    for (int t = 0; t < cntp; ++t) {
       float ag = 0.f, au = 0.f;
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         const int64_t c = s + static_cast<int64_t>(LPR) * j;
         Act<Q> xv;
         lds_act<Q>(xv, xs + t * a.H, c, c < nch);
-        ag = dot_chunk<Q>(wg[j], xv, ag);
-        au = dot_chunk<Q>(wu[j], xv, au);
+        if constexpr (Q) {
+          ag = dot8_bf16(gh[j], xv.v[1], dot8_bf16(gl[j], xv.v[0], ag));
+          au = dot8_bf16(uh[j], xv.v[1], dot8_bf16(ul[j], xv.v[0], au));
+        } else {
+          ag = dot_chunk<Q>(wg[j], xv, ag);
+          au = dot_chunk<Q>(wu[j], xv, au);
+        }
       }
       ag = group_sum<LPR>(ag);
       au = group_sum<LPR>(au);
@@ -492,9 +505,9 @@ int dispatch_a_t(const DecodeArgs& a, hipStream_t st) {
   int maxt = a.n_tokens;
   while (maxt > 1 && static_cast<int64_t>(maxt) * a.H * 2 > 65536) maxt /= 2;
   constexpr int R = Q ? MM_GU_R_I8 : MM_GU_R_BF16;  // row pairs per wave, one token
-  // several tokens: two row pairs per wave, except int8 batches of up to 4 tokens, where one row pair (and
-  // the weights widened again per token) keeps the kernel within 64 VGPRs, 8 waves per SIMD: gate/up 3-4 %
-  // faster at 2 and 4 tokens; at 8 tokens that shape is 26 % slower
+  // several tokens: two row pairs per wave, except int8 batches of up to 4 tokens (one row pair, 64 VGPRs, 8 waves
+  // per SIMD: 3-4 % faster at 2 and 4 tokens); at 8 tokens one row pair (also 8 waves per SIMD) took 64.2 us
+  // against 53.7
   constexpr int RS = Q ? 1 : 2;
   if (maxt <= 1) return launch_a<Q, LPR, NC, R, 1>(a, st);
   if (maxt <= 2) return launch_a<Q, LPR, NC, RS, 2>(a, st);
