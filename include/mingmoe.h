@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 11
+#define MM_ABI_VERSION 12
 
 /* status codes */
 #define MM_OK 0
@@ -352,6 +352,20 @@ int64_t mm_mla_attn_workspace(int nh, int dv, int64_t max_len);
 int mm_mla_decode_attn(const void* q, const void* k_new, const void* v_new, int nh, int dqk, int dv, void* k_cache,
                        void* v_cache, int64_t max_len, const void* pos, int pos_dtype, float scale, void* out,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The T tokens of a prompt through an MLA layer's attention (engine.py:936-958 prefill: the StaticHybridCache
+ * index_copy_ of engine.py:537-541 at positions pos .. pos + T - 1, then the causal attention of the mask at
+ * engine.py:679-682): token t's k_new / v_new rows go to cache row pos + t of k_cache [nh, max_len, dqk] and
+ * v_cache [nh, max_len, dv] (bf16), then out_t[h] = softmax(scale * q_t[h] . K[h, 0..pos+t]^T) . V[h, 0..pos+t],
+ * accumulated in fp32 (the probabilities enter the value product as bf16), rounded to bf16. q, k_new: T rows of
+ * [nh, dqk] at token strides q_ts, k_ts; v_new, out: T rows of [nh, dv] at v_ts, out_ts (elements); pos a device
+ * scalar (MM_INT64 / MM_INT32), the first token's position. A prompt outside [0, max_len) (pos < 0 or
+ * pos + T > max_len) writes nothing to the caches and sets out to NaN. dqk a multiple of 8 up to 256, dv a multiple of
+ * 8 up to 128; q, k_new, v_new and the caches 16-byte aligned with rows at 16-byte strides, out 8-byte aligned. With
+ * T = 1 it computes what mm_mla_decode_attn does. */
+int mm_mla_prefill_attn(const void* q, int64_t q_ts, const void* k_new, int64_t k_ts, const void* v_new, int64_t v_ts,
+                        int64_t T, int nh, int dqk, int dv, void* k_cache, void* v_cache, int64_t max_len,
+                        const void* pos, int pos_dtype, float scale, void* out, int64_t out_ts, void* stream);
 
 /* ---- The two ends of a greedy decode step (engine.py:685-689). */
 

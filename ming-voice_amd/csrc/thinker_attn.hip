@@ -705,6 +705,234 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------- MLA prefill (T tokens)
+
+struct MlaPrefillArgs {
+  const uint16_t* q;      // token t's heads at q + t q_ts: [nh, dqk]
+  const uint16_t* k_new;  // [nh, dqk] per token (token stride k_ts)
+  const uint16_t* v_new;  // [nh, dv] per token (token stride v_ts)
+  int64_t q_ts, k_ts, v_ts;
+  uint16_t* kc;  // [nh, max_len, dqk]
+  uint16_t* vc;  // [nh, max_len, dv]
+  const void* pos;  // the first token's position
+  int pos_dtype;
+  int T, nh, dqk, dv;
+  int64_t max_len;
+  float scale;
+  uint16_t* out;  // [nh, dv] per token (token stride out_ts)
+  int64_t out_ts;
+};
+
+__device__ __forceinline__ bool mla_prefill_pos_ok(const MlaPrefillArgs& a, int64_t pos) {
+  return pos >= 0 && pos + a.T <= a.max_len;
+}
+
+// Grid (T, nh) x 64: token t's key and value rows of head h go to cache row pos + t (engine.py:537-541,
+// index_copy_ at the prompt's positions). A prompt that does not fit in [0, max_len) stores nothing.
+__global__ __launch_bounds__(64) void mla_prefill_store_kernel(MlaPrefillArgs a) {
+  const int t = blockIdx.x, h = blockIdx.y;
+  const int64_t pos = load_pos64(a.pos, a.pos_dtype);
+  if (!mla_prefill_pos_ok(a, pos)) return;
+  const int64_t row = static_cast<int64_t>(h) * a.max_len + pos + t;
+  const auto* ks = reinterpret_cast<const uint4*>(a.k_new + t * a.k_ts + static_cast<int64_t>(h) * a.dqk);
+  const auto* vs = reinterpret_cast<const uint4*>(a.v_new + t * a.v_ts + static_cast<int64_t>(h) * a.dv);
+  auto* kd = reinterpret_cast<uint4*>(a.kc + row * a.dqk);
+  auto* vd = reinterpret_cast<uint4*>(a.vc + row * a.dv);
+  for (int i = threadIdx.x; i < a.dqk / 8; i += kWave) kd[i] = ks[i];
+  for (int i = threadIdx.x; i < a.dv / 8; i += kWave) vd[i] = vs[i];
+}
+
+constexpr int kMlaPKeys = 32;  // keys per tile
+constexpr int kMlaPVtRow = 36;  // bf16 per transposed value row in LDS: 32 keys + 4 (72 bytes, see the stores)
+
+// Orders a wave's LDS stores before its later loads (and loads before later stores) without a workgroup barrier:
+// a wave's LDS instructions execute in program order, so only the compiler's reordering has to be fenced.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Causal attention of T prompt tokens over the static cache (the new rows already stored): token t at position
+// pos + t takes softmax(scale q_t . K[0..pos+t]^T) . V[0..pos+t] (engine.py:679-682's mask). Grid (T / 16,
+// nh) x 4 waves: a workgroup holds 16 queries of one head, and its waves take the 32-key tiles round robin
+// (wave w: tiles w, w + 4, ...), each keeping its own running max, sum and output for the 16 queries; the four
+// are merged through LDS at the end. Per tile, on the 16x16x32 bf16 MFMA:
+//   S^T [32 keys, 16 queries] = K Q^T, the key rows read straight from the cache into A fragments and the
+//     queries held as B fragments (lane: query lane % 16, dims 32 kk + 8 (lane / 16) .. + 7);
+//   the masked softmax update per query is lane-local (a lane of the S^T tiles holds 8 keys of its query
+//     column: 4 (lane / 16) + v and 16 + 4 (lane / 16) + v), the tile max summed over the 4 lane quarters;
+//   O^T [dv, 16 queries] += V^T P^T: the B fragment of P comes straight from the S^T registers, its 8 k slots
+//     taking those 8 keys in that order, and the A fragment of V^T (dim lane % 16, the same 8 keys) from a
+//     transposed copy of the value tile the wave stores in its own LDS ([dv][36], two keys per 4-byte store).
+// O^T's lane layout (dims 4 (lane / 16) + v of each 16-dim tile, query lane % 16) keeps the rescaling by the
+// query's exp(m_old - m_new) lane-local as well. Keys past the block's last query are not read (zeros, then
+// masked); queries past T repeat the last token and are not stored. A prompt outside [0, max_len) writes NaN.
+template <int NT>  // dv <= 16 NT
+__global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a) {
+  constexpr int DVM = 16 * NT;
+  constexpr int VT_BYTES = DVM * kMlaPVtRow * 2;
+  constexpr int MERGE_BYTES = 16 * DVM * 4;  // the wave's O [16 queries][DVM] fp32
+  constexpr int WAVE_BYTES = VT_BYTES > MERGE_BYTES ? VT_BYTES : MERGE_BYTES;
+  __shared__ __align__(16) char s_buf[4 * WAVE_BYTES];
+  __shared__ float s_m[4][16], s_l[4][16];
+  const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
+  const int lr = lane & 15, lq = lane >> 4;
+  const int h = blockIdx.y, tq0 = blockIdx.x * 16;
+  const int64_t pos = load_pos64(a.pos, a.pos_dtype);
+  const int n4 = a.dv / 4;
+  if (!mla_prefill_pos_ok(a, pos)) {  // uniform over the workgroup
+    for (int i = tid; i < 16 * a.dv; i += 256) {
+      const int t = tq0 + i / a.dv;
+      if (t < a.T) a.out[t * a.out_ts + static_cast<int64_t>(h) * a.dv + i % a.dv] = 0x7fc0;  // NaN
+    }
+    return;
+  }
+  const int tlast = min(tq0 + 15, a.T - 1);
+  const int tq = min(tq0 + lr, a.T - 1);
+  const int64_t qlim = pos + tq;          // the keys this lane's query attends: 0 .. qlim
+  const int64_t kend = pos + tlast + 1;   // the keys any query of the workgroup attends: 0 .. kend - 1
+  const int ntiles = static_cast<int>((kend + kMlaPKeys - 1) / kMlaPKeys);
+  const int nkq = (a.dqk + 31) / 32;
+  bf16x8_t qf[8];
+  {
+    const uint16_t* qrow = a.q + tq * a.q_ts + static_cast<int64_t>(h) * a.dqk;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int d = 32 * kk + 8 * lq;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (kk < nkq && d < a.dqk) x = *reinterpret_cast<const uint4*>(qrow + d);
+      qf[kk] = __builtin_bit_cast(bf16x8_t, x);
+    }
+  }
+  floatx4 o[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) o[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  uint16_t* vt = reinterpret_cast<uint16_t*>(s_buf + wave * WAVE_BYTES);
+  const int64_t hk = static_cast<int64_t>(h) * a.max_len;
+  constexpr int RV = (DVM + 31) / 32;  // value pieces (2 keys x 8 dims) per lane: 16 key pairs x dv / 8 groups
+  const int ndg = a.dv / 8;
+  for (int kt = wave; kt < ntiles; kt += 4) {
+    const int64_t j0 = static_cast<int64_t>(kt) * kMlaPKeys;
+    // value tile: lane piece i = lane + 64 r -> key pair kp = i % 16, dim group dg = i / 16
+    uint4 va[RV], vb[RV];
+#pragma unroll
+    for (int r = 0; r < RV; ++r) {
+      const int i = lane + kWave * r, kp = i % 16, dg = i / 16;
+      const int64_t ja = j0 + 2 * kp;
+      va[r] = vb[r] = make_uint4(0, 0, 0, 0);
+      if (dg < ndg) {
+        if (ja < kend) va[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + ja) * a.dv + 8 * dg);
+        if (ja + 1 < kend) vb[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + ja + 1) * a.dv + 8 * dg);
+      }
+    }
+    floatx4 s[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t j = j0 + 16 * n + lr;
+      const bool live = j < kend;
+      const uint16_t* krow = a.kc + (hk + (live ? j : 0)) * a.dqk;
+      s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int d = 32 * kk + 8 * lq;
+        if (kk < nkq) {
+          uint4 x = make_uint4(0, 0, 0, 0);
+          if (live && d < a.dqk) x = *reinterpret_cast<const uint4*>(krow + d);
+          s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, x), qf[kk], s[n], 0, 0, 0);
+        }
+      }
+    }
+    // the transposed value tile: dword (dim 8 dg + e, keys 2 kp, 2 kp + 1); 16 consecutive key pairs per dim
+    // row and 4 dim groups 8 x 18 dwords apart per store keep the 64 lanes on distinct banks
+    wave_lds_fence();  // the previous tile's reads of vt are done
+#pragma unroll
+    for (int r = 0; r < RV; ++r) {
+      const int i = lane + kWave * r, kp = i % 16, dg = i / 16;
+      if (dg < ndg) {
+        const uint32_t xa[4] = {va[r].x, va[r].y, va[r].z, va[r].w}, xb[4] = {vb[r].x, vb[r].y, vb[r].z, vb[r].w};
+        auto* dst = reinterpret_cast<uint32_t*>(vt) + (8 * dg) * (kMlaPVtRow / 2) + kp;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dst[(2 * e) * (kMlaPVtRow / 2)] = __builtin_amdgcn_perm(xb[e], xa[e], 0x05040100u);      // low halves
+          dst[(2 * e + 1) * (kMlaPVtRow / 2)] = __builtin_amdgcn_perm(xb[e], xa[e], 0x07060302u);  // high halves
+        }
+      }
+    }
+    // masked online softmax: slot e < 4 is key j0 + 4 lq + e, slot e >= 4 key j0 + 16 + 4 lq + e - 4
+    float sv[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t key = j0 + (e < 4 ? 4 * lq + e : 16 + 4 * lq + e - 4);
+      const float x = e < 4 ? s[0][e] : s[1][e - 4];
+      sv[e] = key <= qlim ? x * a.scale : -INFINITY;
+      tmax = fmaxf(tmax, sv[e]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float mn = fmaxf(m, tmax);
+    const float mu = mn == -INFINITY ? 0.f : mn;  // a query with no key yet in this wave's tiles
+    const float alpha = __expf(m - mu);
+    m = mn;
+    float ps = 0.f;
+    uint32_t pw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p0 = __expf(sv[2 * e] - mu), p1 = __expf(sv[2 * e + 1] - mu);
+      ps += p0 + p1;
+      pw[e] = static_cast<uint32_t>(f32_to_bf16(p0)) | (static_cast<uint32_t>(f32_to_bf16(p1)) << 16);
+    }
+    l = fmaf(l, alpha, ps);
+    const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    wave_lds_fence();  // the stores of vt before the loads
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      o[nt] *= alpha;
+      if (16 * nt < a.dv) {
+        const uint16_t* row = vt + (16 * nt + lr) * kMlaPVtRow;
+        const uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * lq);
+        const uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * lq);
+        o[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y)),
+                                                        pf, o[nt], 0, 0, 0);
+      }
+    }
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  // the wave's state into its own LDS region (its value tile is no longer read), then the merge
+  wave_lds_fence();
+  float* so = reinterpret_cast<float*>(s_buf + wave * WAVE_BYTES);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    if (16 * nt < a.dv) *reinterpret_cast<floatx4*>(so + lr * DVM + 16 * nt + 4 * lq) = o[nt];
+  if (lq == 0) {
+    s_m[wave][lr] = m;
+    s_l[wave][lr] = l;
+  }
+  __syncthreads();
+  for (int i = tid; i < 16 * n4; i += 256) {
+    const int qi = i / n4, d = 4 * (i % n4), t = tq0 + qi;
+    if (t >= a.T) continue;
+    const float mx = fmaxf(fmaxf(s_m[0][qi], s_m[1][qi]), fmaxf(s_m[2][qi], s_m[3][qi]));  // finite: key 0
+    float lt = 0.f;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = __expf(s_m[w][qi] - mx);
+      lt = fmaf(s_l[w][qi], wt, lt);
+      acc += wt * *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(s_buf + w * WAVE_BYTES) +
+                                                    qi * DVM + d);
+    }
+    const float inv = 1.f / lt;
+    uint16_t* dst = a.out + t * a.out_ts + static_cast<int64_t>(h) * a.dv + d;
+    const uint32_t w0 = static_cast<uint32_t>(f32_to_bf16(acc[0] * inv)) | (static_cast<uint32_t>(f32_to_bf16(acc[1] * inv)) << 16);
+    const uint32_t w1 = static_cast<uint32_t>(f32_to_bf16(acc[2] * inv)) | (static_cast<uint32_t>(f32_to_bf16(acc[3] * inv)) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
+  }
+}
+
 template <int K>
 int launch_kda(const KdaArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((kda_recurrent_kernel<K>), dim3(static_cast<unsigned>(a.V / kKdaCols), static_cast<unsigned>(a.H)),
@@ -900,4 +1128,54 @@ extern "C" int mm_mla_decode_attn(const void* q, const void* k_new, const void* 
   else if (dv <= 128) hipLaunchKernelGGL(mla_merge_kernel<2>, dim3(static_cast<unsigned>(nh)), dim3(256), 0, st, a);
   else hipLaunchKernelGGL(mla_merge_kernel<4>, dim3(static_cast<unsigned>(nh)), dim3(256), 0, st, a);
   return mm::check_launch("mla_decode_attn merge");
+}
+
+extern "C" int mm_mla_prefill_attn(const void* q, int64_t q_ts, const void* k_new, int64_t k_ts, const void* v_new,
+                                   int64_t v_ts, int64_t T, int nh, int dqk, int dv, void* k_cache, void* v_cache,
+                                   int64_t max_len, const void* pos, int pos_dtype, float scale, void* out,
+                                   int64_t out_ts, void* stream) {
+  MM_REQUIRE(T >= 0 && T <= (1 << 20), "mla_prefill_attn: bad T=%lld", (long long)T);
+  MM_REQUIRE(nh >= 1 && nh <= 65535 && max_len >= 1 && max_len <= (1LL << 24), "mla_prefill_attn: bad nh or max_len");
+  MM_REQUIRE(dqk % 8 == 0 && dqk >= 8 && dqk <= 256, "mla_prefill_attn: dqk=%d must be a multiple of 8 in [8, 256]",
+             dqk);
+  MM_REQUIRE(dv % 8 == 0 && dv >= 8 && dv <= 128, "mla_prefill_attn: dv=%d must be a multiple of 8 in [8, 128]", dv);
+  MM_REQUIRE(pos_dtype == MM_INT64 || pos_dtype == MM_INT32, "mla_prefill_attn: pos must be int64 or int32");
+  MM_REQUIRE(q && k_new && v_new && k_cache && v_cache && pos && out, "mla_prefill_attn: null pointer");
+  MM_REQUIRE(q_ts >= static_cast<int64_t>(nh) * dqk && k_ts >= static_cast<int64_t>(nh) * dqk &&
+                 v_ts >= static_cast<int64_t>(nh) * dv && out_ts >= static_cast<int64_t>(nh) * dv,
+             "mla_prefill_attn: token strides smaller than a token's heads");
+  MM_REQUIRE(q_ts % 8 == 0 && k_ts % 8 == 0 && v_ts % 8 == 0 && out_ts % 4 == 0,
+             "mla_prefill_attn: token strides must keep rows 16-byte aligned (8-byte for out)");
+  MM_REQUIRE(mm::aligned16(q) && mm::aligned16(k_new) && mm::aligned16(v_new) && mm::aligned16(k_cache) &&
+                 mm::aligned16(v_cache) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
+             "mla_prefill_attn: q, k_new, v_new and the caches must be 16-byte aligned, out 8-byte aligned");
+  if (T == 0) return MM_OK;
+  MlaPrefillArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k_new = static_cast<const uint16_t*>(k_new);
+  a.v_new = static_cast<const uint16_t*>(v_new);
+  a.q_ts = q_ts;
+  a.k_ts = k_ts;
+  a.v_ts = v_ts;
+  a.kc = static_cast<uint16_t*>(k_cache);
+  a.vc = static_cast<uint16_t*>(v_cache);
+  a.pos = pos;
+  a.pos_dtype = pos_dtype;
+  a.T = static_cast<int>(T);
+  a.nh = nh;
+  a.dqk = dqk;
+  a.dv = dv;
+  a.max_len = max_len;
+  a.scale = scale;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_ts = out_ts;
+  hipStream_t st = MM_STREAM(stream);
+  hipLaunchKernelGGL(mla_prefill_store_kernel, dim3(static_cast<unsigned>(T), static_cast<unsigned>(nh)), dim3(kWave),
+                     0, st, a);
+  int rc = mm::check_launch("mla_prefill_attn store");
+  if (rc) return rc;
+  const dim3 grid(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>(nh));
+  if (dv <= 64) hipLaunchKernelGGL(mla_prefill_attn_kernel<4>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(mla_prefill_attn_kernel<8>, grid, dim3(256), 0, st, a);
+  return mm::check_launch("mla_prefill_attn");
 }

@@ -1,6 +1,6 @@
 """The thinker's attention mixers on hand-written gfx950 HIP kernels: the KDA (Kimi delta attention) layers'
-recurrent core, short convolutions and gated output norm, and the MLA layers' single-token attention over the
-static cache.
+recurrent core, short convolutions and gated output norm, and the MLA layers' attention over the static cache (one
+decode token, or a prompt's tokens).
 
   fused_recurrent_kda   drop-in for fla.ops.kda.fused_recurrent_kda (fla-core 0.5.2; engine.py:242-262): same
                         keywords, B = 1; the state is fp32 [1, H, K, V], updated in place with inplace=True
@@ -10,6 +10,8 @@ static cache.
                         recurrence, the gated norm) in one kernel instead of the five calls above
   mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
                         masked softmax attention over positions 0..pos
+  mla_prefill_attn      the T tokens of a prompt through an MLA layer: the update at pos .. pos + T - 1 and the
+                        causal attention, token t over positions 0..pos+t (engine.py:936-958)
   embed_rows            word_embeddings(tok_buf), the input row of a decode step (engine.py:686)
   argmax_rows           logits.argmax(-1), the greedy pick a decode step writes back (engine.py:688)
 Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
@@ -22,7 +24,7 @@ import torch
 import _mingmoe as _mm
 
 __all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
-           "mla_attn_workspace", "embed_rows", "argmax_rows"]
+           "mla_attn_workspace", "mla_prefill_attn", "embed_rows", "argmax_rows"]
 
 
 def _f32_or_bf16(t, name):
@@ -256,6 +258,55 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None
                                          _mm.ptr(v_cache), max_len, _mm.ptr(pos), _mm.dtype_code(pos), sc, _mm.ptr(y),
                                          _mm.ptr(ws), ws.numel() * ws.element_size(), _mm.stream_of(q)),
                   "mla_decode_attn")
+    return y
+
+
+def _token_rows(t, T, n, name):
+    """[T, n] view of a tensor holding T tokens of n contiguous elements (e.g. [1, T, heads, d] or a column slice
+    of a wider projection output) and its token stride; copied when its rows are not 16-byte aligned."""
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"mla_prefill_attn: {name} must be bf16")
+    if t.numel() != T * n:
+        raise ValueError(f"mla_prefill_attn: {name} must hold {T} tokens of {n} elements (got {tuple(t.shape)})")
+    t2 = t.reshape(T, n)
+    if t2.stride(1) != 1 or (T > 1 and t2.stride(0) % 8) or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2, t2.stride(0) if T > 1 else n
+
+
+def mla_prefill_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None):
+    """T prompt tokens of an MLA layer (the engine's prefill over the static cache, engine.py:936-958, 537-541,
+    679-682). q, k_new: T tokens of [nh, dqk] ([T, nh * dqk], [1, T, nh, dqk], or column slices of a projection
+    output); v_new: T tokens of [nh, dv]; k_cache [1, nh, max_len, dqk], v_cache [1, nh, max_len, dv] (bf16);
+    pos: a one-element int64 / int32 device tensor, the first token's position. Writes the new rows at
+    pos .. pos + T - 1 and returns out [T, nh * dv]: token t attends to positions 0 .. pos + t (scale defaults to
+    dqk ** -0.5). A prompt that does not fit in the cache leaves it unchanged and returns NaN."""
+    _mm.require_gpu(q, k_new, v_new, k_cache, v_cache, pos, out)
+    nh, max_len, dqk = k_cache.shape[-3:]
+    dv = v_cache.shape[-1]
+    if tuple(v_cache.shape[-3:-1]) != (nh, max_len) or not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("mla_prefill_attn: caches must be contiguous [1, nh, max_len, d]")
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"mla_prefill_attn: {name} must be bf16")
+    if q.numel() % (nh * dqk):
+        raise ValueError(f"mla_prefill_attn: q must hold tokens of [{nh}, {dqk}]")
+    T = q.numel() // (nh * dqk)
+    qf, qs = _token_rows(q, T, nh * dqk, "q")
+    kf, ks = _token_rows(k_new, T, nh * dqk, "k_new")
+    vf, vs = _token_rows(v_new, T, nh * dv, "v_new")
+    if pos.dtype not in (torch.int64, torch.int32) or pos.numel() != 1:
+        raise ValueError("mla_prefill_attn: pos must be a one-element int64 / int32 device tensor")
+    y = torch.empty(T, nh * dv, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(T, nh * dv)
+    if y.dtype != torch.bfloat16 or y.stride(1) != 1 or y.data_ptr() % 8 or (T > 1 and y.stride(0) % 4):
+        raise ValueError("mla_prefill_attn: out must be bf16 [T, nh * dv] with 8-byte aligned rows")
+    sc = float(scale) if scale is not None else dqk ** -0.5
+    lib = _mm.load()
+    with _mm.on_device(q):
+        _mm.check(lib.mm_mla_prefill_attn(_mm.ptr(qf), qs, _mm.ptr(kf), ks, _mm.ptr(vf), vs, T, nh, dqk, dv,
+                                          _mm.ptr(k_cache), _mm.ptr(v_cache), max_len, _mm.ptr(pos),
+                                          _mm.dtype_code(pos), sc, _mm.ptr(y), y.stride(0) if T > 1 else nh * dv,
+                                          _mm.stream_of(q)), "mla_prefill_attn")
     return y
 
 

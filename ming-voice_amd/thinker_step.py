@@ -36,9 +36,11 @@ Every call enqueues on torch's current stream and can be captured in one hipGrap
 lives in the engine's own buffers, so replays advance it as the engine's decode graphs do.
 """
 import torch
+import torch.nn.functional as F
 
 import fastlinear
 import fused_moe
+import fused_ops
 import thinker_attn as TA
 
 __all__ = ["FastThinkerStep"]
@@ -174,7 +176,7 @@ class FastThinkerStep:
                     topk_group=int(getattr(g, "topk_group", 1) or 1),
                     scale=float(getattr(g, "routed_scaling_factor", 1.0) or 1.0), inter=exp["w_d"].shape[-1])
 
-    # ----------------------------------------------------------------------------------------------- step
+    # ----------------------------------------------------------------------------------------- decode step
 
     def embed_token(self):
         """word_embeddings(tok_buf) -> the step's input row [1, H] (a view of a buffer the step owns)."""
@@ -226,6 +228,103 @@ class FastThinkerStep:
 
     def head_logits(self, h):
         return fastlinear.small_linear(h, self.head, norm=self.final_norm)
+
+    # -------------------------------------------------------------------------------------------- prefill
+
+    @staticmethod
+    def _rows(x, w, b=None, residual=None, norm=None):
+        """A projection of T rows: up to fastlinear.MAX_M rows on the small_linear GEMV (norm and residual fused),
+        more as rms_norm (HIP) -> the library GEMM (torch's linear on hipBLASLt) -> + residual, the form of the
+        reference's own prefill (nn.Linear after the patched norm, engine.py:220-228)."""
+        if x.shape[0] <= fastlinear.MAX_M:
+            return fastlinear.small_linear(x, w, b=b, residual=residual, norm=norm)
+        if norm is not None:
+            x = fused_ops.rms_norm(x, norm[0], norm[1])
+        y = F.linear(x, w, b)
+        return y if residual is None else y.add_(residual)
+
+    def prompt_mixer(self, li, h):
+        """The attention half of layer li over a prompt's T rows h [T, H] at positions pos_buf .. pos_buf + T - 1:
+        h + o(mixer(input_layernorm(h))). KDA: the projection, the q / k / v short convolutions (their caches end
+        on the prompt's last inputs), the f / g LoRA up-projections, fused_recurrent_kda from the layer's state (the
+        recurrent form for any T), rms_norm_gated; MLA: the q | k | v projection and mla_prefill_attn."""
+        p = self.L[li]
+        T = h.shape[0]
+        if p["kind"] == "mla":
+            if self.mla_qkv is not None:
+                q, k, v = self.mla_qkv(li, p, h)
+            else:
+                qkv = self._rows(h, p["qkv"], p["qkv_b"], norm=p["ln1"])
+                nq = p["nh"] * p["dqk"]
+                q, k, v = qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:]
+            o = TA.mla_prefill_attn(q, k, v, p["kc"], p["vc"], self.pos)
+            return self._rows(o, p["o"], p["o_b"], residual=h)
+        H, K, V, R = p["heads"], p["K"], p["V"], p["rank"]
+        pr = self._rows(h, p["proj"], p["proj_b"], norm=p["ln1"])
+        nqk, nv = H * K, H * V
+        q, k, v = (TA.short_conv(pr[:, a:b], c, w) for (a, b), c, w in
+                   zip(((0, nqk), (nqk, 2 * nqk), (2 * nqk, 2 * nqk + nv)), p["conv"], p["conv_w"]))
+        base = 2 * nqk + nv
+        f = self._rows(pr[:, base:base + R], p["f_b"])
+        gg = self._rows(pr[:, base + R:base + 2 * R], p["g_b"])
+        o, _ = TA.fused_recurrent_kda(q.view(1, T, H, K), k.view(1, T, H, K), v.view(1, T, H, V), f.view(1, T, H, K),
+                                      pr[:, base + 2 * R:], A_log=p["A_log"], dt_bias=p["dt_bias"],
+                                      initial_state=p["state"], inplace=True, use_qk_l2norm_in_kernel=True,
+                                      use_gate_in_kernel=True, beta_is_logits=True, lower_bound=p["lower_bound"])
+        ow, oe = p["o_norm"]
+        on = TA.rms_norm_gated(o.reshape(T * H, V), gg.reshape(T * H, V), ow, oe)
+        return self._rows(on.reshape(T, H * V), p["o"], p["o_b"], residual=h)
+
+    def prompt_moe(self, li, h):
+        """The MoE half of layer li over T rows: moe_block_decode up to fused_moe.MAX_DECODE_TOKENS rows (the
+        reference's own split, engine.py:300-310 -> fused_moe.py:13-61), moe_block_prefill beyond.
+        Returns (y, ids, wts)."""
+        b = self.L[li]["blk"]
+        kw = dict(top_k=b["top_k"], bias=b["bias"], scoring=self.scoring, n_group=b["n_group"],
+                  topk_group=b["topk_group"], scale=b["scale"], s_gu=b["s_gu"], s_d=b["s_d"])
+        if h.shape[0] <= fused_moe.MAX_DECODE_TOKENS:
+            y, ids, wts, _ = fused_moe.moe_block_decode(h, b["norm_w"], b["eps"], b["w32"], b["w_gu"], b["w_d"], **kw)
+        else:
+            y, ids, wts, _ = fused_moe.moe_block_prefill(h, b["norm_w"], b["eps"], b["w32"], b["w_gu"], b["w_d"], **kw)
+        return y, ids, wts
+
+    def _prompt_rows(self, ids, h):
+        if (ids is None) == (h is None):
+            raise ValueError("FastThinkerStep.prefill: pass the prompt's token ids or its input rows h")
+        if h is not None:
+            h = h.reshape(-1, self.H)
+            if h.dtype != self.embed.dtype:
+                raise ValueError(f"FastThinkerStep.prefill: h must be {self.embed.dtype} rows of {self.H}")
+            return h.contiguous()
+        ids = ids.reshape(-1)
+        if ids.dtype not in (torch.int64, torch.int32):
+            raise ValueError("FastThinkerStep.prefill: ids must be int64 / int32 device tokens")
+        return TA.embed_rows(self.embed, ids)
+
+    def prefill(self, ids=None, h=None, *, trace=False):
+        """The engine's _prefill (engine.py:921-958) of one prompt at positions pos_buf .. pos_buf + T - 1: ids
+        [1, T] / [T] device token ids (word_embeddings, engine.py:922), or h [1, T, H] / [T, H] input rows (the
+        embeddings with audio features merged in, engine.py:923-927). Per layer h = prompt_moe(prompt_mixer(h)),
+        then logits = lm_head(norm(h[T - 1])), tok_buf = argmax(logits), pos_buf += T: the state (KDA states and
+        conv caches, MLA cache rows) advances as T decode steps would advance it. Returns the last token's logits
+        [1, vocab]; with trace=True also the per-layer (input, mixer output, router ids, weights) list.
+        Eager calls of one T, or a capture per prompt length (the position stays on the device)."""
+        h = self._prompt_rows(ids, h)
+        if h.shape[0] == 0:
+            raise ValueError("FastThinkerStep.prefill: an empty prompt")
+        out = []
+        for li in range(len(self.L)):
+            h_in = h
+            hm = self.prompt_mixer(li, h)
+            h, rid, rw = self.prompt_moe(li, hm)
+            if trace:
+                out.append((h_in.clone(), hm.clone(), rid.clone(), rw.clone()))
+        logits = self.head_logits(h[-1:])
+        TA.argmax_rows(logits, out=self.tok)
+        self.pos.add_(h.shape[0])
+        return (logits, out) if trace else logits
+
+    # ----------------------------------------------------------------------------------------------- step
 
     def __call__(self):
         h = self.embed_token()

@@ -97,3 +97,23 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None):
     p = torch.softmax(s, -1)
     out = (p[:, :, None] * vc[:, : pos + 1].to(F64)).sum(1)
     return out, kc, vc
+
+
+def mla_prefill_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None):
+    """The T tokens of a prompt through an MLA layer (engine.py:936-958 over the static cache): the caches [nh, L, d]
+    take k_new[t] / v_new[t] ([T, nh, d]) at rows pos + t (engine.py:537-541), then token t attends to rows
+    0 .. pos + t (the causal mask of engine.py:679-682): out[t, h] = softmax(scale * q[t, h] . K[h, :pos+t+1]^T) .
+    V[h, :pos+t+1]. Returns (out [T, nh, dv], k_cache, v_cache), float64 (caches in their dtype)."""
+    T = q.shape[0]
+    kc, vc = k_cache.clone(), v_cache.clone()
+    kc[:, pos:pos + T] = k_new.transpose(0, 1).to(kc.dtype)
+    vc[:, pos:pos + T] = v_new.transpose(0, 1).to(vc.dtype)
+    d = q.shape[-1]
+    n = pos + T
+    s = torch.einsum("thd,hjd->htj", q.to(F64), kc[:, :n].to(F64)) * (d ** -0.5 if scale is None else scale)
+    keys = torch.arange(n)
+    mask = keys[None, :] <= (pos + torch.arange(T))[:, None]  # [T, n]
+    s = s.masked_fill(~mask[None], float("-inf"))
+    p = torch.softmax(s, -1)
+    out = torch.einsum("htj,hjd->thd", p, vc[:, :n].to(F64))
+    return out, kc, vc

@@ -3,6 +3,7 @@ attention) against oracle/thinker_attn_oracle.py on seeded inputs. bf16 outputs 
 KDA state within rtol 1e-3 / atol 1e-4 of the float64 oracle; cache rows bit-exact."""
 import pytest
 import torch
+import torch.nn.functional as F
 
 import thinker_attn as TA
 import workloads as W
@@ -182,6 +183,93 @@ def test_mla_graph_replays_follow_the_position():
         assert torch.equal(out, want) and torch.equal(kc, ke) and torch.equal(vc, ve), p
 
 
+def _prompt(nh, dq, dv, T, seed, packed=False):
+    """q, k, v of T tokens; packed: column slices of one [T, nh (2 dq + dv)] projection output (the product's form)."""
+    if packed:
+        qkv = W.normal((T, nh * (2 * dq + dv)), 1.0, seed, DEV)
+        nq = nh * dq
+        return qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:]
+    return (W.normal((T, nh, dq), 1.0, seed, DEV), W.normal((T, nh, dq), 1.0, seed + 1, DEV),
+            W.normal((T, nh, dv), 1.0, seed + 2, DEV))
+
+
+@pytest.mark.parametrize("nh,dq,dv,L,T,pos,packed", [
+    (16, 192, 128, 1024, 128, 512, True), (16, 192, 128, 1024, 17, 0, False), (4, 64, 64, 300, 33, 31, False),
+    (2, 96, 32, 70, 70, 0, True), (3, 72, 40, 100, 5, 95, False), (1, 8, 8, 40, 1, 7, False),
+    (2, 256, 128, 600, 300, 200, True), (2, 200, 48, 64, 16, 16, False), (1, 32, 16, 2100, 64, 2000, False)])
+def test_mla_prefill_attn_matches_oracle(nh, dq, dv, L, T, pos, packed):
+    """Prompts at the cache start and end, lengths off the 16-query and 32-key tiles, head dims off the 32-wide
+    MFMA step, and q / k / v as column slices of a projection output."""
+    print(f"[mla prefill] nh={nh} dq={dq} dv={dv} L={L} T={T} pos={pos} packed={packed}", flush=True)
+    kc = W.normal((1, nh, L, dq), 1.0, 500, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 501, DEV)
+    k0, v0 = kc.clone(), vc.clone()
+    q, kn, vn = _prompt(nh, dq, dv, T, 502, packed)
+    out = TA.mla_prefill_attn(q, kn, vn, kc, vc, torch.tensor([pos], device=DEV))
+    ro, rk, rv = A.mla_prefill_attn(q.reshape(T, nh, dq).cpu(), kn.reshape(T, nh, dq).cpu(),
+                                    vn.reshape(T, nh, dv).cpu(), k0[0].cpu(), v0[0].cpu(), pos)
+    assert out.shape == (T, nh * dv)
+    close(out.reshape(T, nh, dv), ro)
+    assert torch.equal(kc[0].cpu(), rk) and torch.equal(vc[0].cpu(), rv)
+
+
+def test_mla_prefill_rows_past_the_prompt_are_never_read_and_out_of_range_writes_nothing():
+    nh, dq, dv, L = 4, 192, 128, 200
+    for T, pos in ((1, 0), (20, 13), (45, 155)):
+        print(f"[mla prefill nan] T={T} pos={pos}", flush=True)
+        kc = W.normal((1, nh, L, dq), 1.0, 510, DEV)
+        vc = W.normal((1, nh, L, dv), 1.0, 511, DEV)
+        kc[:, :, pos + T:] = float("nan")
+        vc[:, :, pos + T:] = float("nan")
+        k0, v0 = kc.clone(), vc.clone()
+        q, kn, vn = _prompt(nh, dq, dv, T, 512)
+        out = TA.mla_prefill_attn(q, kn, vn, kc, vc, torch.tensor([pos], device=DEV, dtype=torch.int32))
+        ro, _, _ = A.mla_prefill_attn(q.cpu(), kn.cpu(), vn.cpu(), k0[0].cpu(), v0[0].cpu(), pos)
+        assert torch.isfinite(out.float()).all()
+        close(out.reshape(T, nh, dv), ro)
+    kc = W.normal((1, nh, L, dq), 1.0, 513, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 514, DEV)
+    k0, v0 = kc.clone(), vc.clone()
+    q, kn, vn = _prompt(nh, dq, dv, 8, 515)
+    for pos in (L - 7, -1):  # one row past the end; a negative position
+        print(f"[mla prefill out of range] pos={pos}", flush=True)
+        out = TA.mla_prefill_attn(q, kn, vn, kc, vc, torch.tensor([pos], device=DEV))
+        assert torch.isnan(out.float()).all() and torch.equal(kc, k0) and torch.equal(vc, v0)
+
+
+def test_mla_prefill_one_token_equals_decode_and_graph_replays_follow_the_position():
+    nh, dq, dv, L = 16, 192, 128, 512
+    kc = W.normal((1, nh, L, dq), 1.0, 520, DEV)
+    vc = W.normal((1, nh, L, dv), 1.0, 521, DEV)
+    kd, vd = kc.clone(), vc.clone()
+    q, kn, vn = _prompt(nh, dq, dv, 1, 522)
+    pos = torch.tensor([77], device=DEV)
+    a = TA.mla_prefill_attn(q, kn, vn, kc, vc, pos)
+    b = TA.mla_decode_attn(q, kn, vn, kd, vd, pos)
+    close(a.reshape(nh, dv), b, rtol=1e-2, atol=1e-2)
+    assert torch.equal(kc, kd) and torch.equal(vc, vd)
+    # a 40-token prompt captured once, replayed at positions 10, 50, 90 on the graph's cache, against eager calls
+    T = 40
+    q, kn, vn = _prompt(nh, dq, dv, T, 523, packed=True)
+    ke, ve = kc.clone(), vc.clone()
+    pos = torch.tensor([10], device=DEV)
+    out = torch.empty(T, nh * dv, device=DEV, dtype=BF)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        TA.mla_prefill_attn(q, kn, vn, kc, vc, pos, out=out)
+    for p in (10, 50, 90):
+        print(f"[mla prefill graph] pos={p}", flush=True)
+        pos.fill_(p)
+        g.replay()
+        torch.cuda.synchronize()
+        want = TA.mla_prefill_attn(q, kn, vn, ke, ve, torch.tensor([p], device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want) and torch.equal(kc, ke) and torch.equal(vc, ve)
+
+
 def test_kda_beta_logits_apply_the_sigmoid():
     """beta_is_logits=True (the kernel applies the sigmoid of the beta projection) against the oracle given the
     sigmoid's values."""
@@ -283,6 +371,142 @@ def test_hybrid_step_layers_match_the_oracle():
         if nxt is not None:
             d = (nxt.float().cpu() - moe.float()).abs()
             assert float((d <= 1e-2 + 2e-2 * moe.float().abs()).float().mean()) >= 0.995, li
+
+
+def _oracle_prompt_mixer(p, st, h, pos):
+    """One hybrid layer's mixer over a prompt's T rows h [T, H] on the oracle (state st: the layer's state before).
+    Returns (out [T, H], the state after: KDA state and the conv windows, or the MLA caches)."""
+    from oracle import moe_oracle as O
+    T = h.shape[0]
+    kd = W.KDA_HEADS * W.KDA_DIM
+    if p["kind"] == "mla":
+        qkv = O.small_linear(h, p["qkv"].cpu(), norm=(p["ln1"].cpu(), W.EPS))
+        nq = W.MLA_HEADS * W.MLA_QK
+        o, kc, vc = A.mla_prefill_attn(qkv[:, :nq].reshape(T, W.MLA_HEADS, -1),
+                                       qkv[:, nq:2 * nq].reshape(T, W.MLA_HEADS, -1),
+                                       qkv[:, 2 * nq:].reshape(T, W.MLA_HEADS, -1), st["kc"][0].cpu(),
+                                       st["vc"][0].cpu(), pos)
+        return O.small_linear(o.reshape(T, -1).to(BF), p["o"].cpu(), residual=h), {"kc": kc, "vc": vc}
+    pr = O.small_linear(h, p["proj"].cpu(), norm=(p["ln1"].cpu(), W.EPS))
+    f = O.small_linear(pr[:, 3 * kd:3 * kd + W.KDA_LORA], p["f_b"].cpu())
+    gg = O.small_linear(pr[:, 3 * kd + W.KDA_LORA:3 * kd + 2 * W.KDA_LORA], p["g_b"].cpu())
+    conv = torch.cat([c[0] for c in st["conv"]]).cpu()
+    qkv, win = A.short_conv(pr[:, :3 * kd], conv, p["conv_w"][:, 0].cpu())
+    qkv = qkv.to(BF)
+    beta = torch.sigmoid(pr[:, 3 * kd + 2 * W.KDA_LORA:].double())
+    shp = (T, W.KDA_HEADS, W.KDA_DIM)
+    o, S = A.kda_recurrent(qkv[:, :kd].reshape(shp), qkv[:, kd:2 * kd].reshape(shp), qkv[:, 2 * kd:].reshape(shp),
+                           f.reshape(shp), beta, st["state"][0].cpu(), A_log=p["A_log"].cpu(),
+                           dt_bias=p["dt_bias"].cpu())
+    on = A.rms_norm_gated(o.to(BF), gg.reshape(shp), p["o_norm"].cpu(), 1e-5)
+    return O.small_linear(on.reshape(T, kd).to(BF), p["o"].cpu(), residual=h), {"state": S, "conv": win}
+
+
+def _within(got, want, atol=1e-2, rtol=2e-2):
+    d = (got.float().cpu() - want.float()).abs()
+    return float((d <= atol + rtol * want.float().abs()).float().mean()), float(d.max())
+
+
+@pytest.mark.parametrize("T", [40, 5])
+def test_fast_thinker_prefill_layers_match_the_oracle(T):
+    """A T-token prompt through 4 layers (3 KDA, 1 MLA) at full width, each half checked on the GPU's own input: the
+    mixer (projections, convolutions, the KDA recurrence over T tokens or the causal MLA attention) and the MoE
+    block; the layers' states after the prompt (KDA state, conv windows, MLA cache rows); the head on the last
+    token. T = 40 takes the library GEMMs and the prefill MoE block, T = 5 the GEMVs and the decode MoE block."""
+    from oracle import moe_oracle as O
+    pos = 200
+    print(f"[hybrid prefill] T={T} 4 layers vs oracle", flush=True)
+    step = W.HybridThinkerStep(4, DEV, pos=pos, seed=7200)
+    before = step.state_copy()
+    ids = torch.randint(0, step.embed.shape[0], (T,), generator=torch.Generator().manual_seed(T)).to(DEV)
+    logits, trace = step.fast.prefill(ids, trace=True)
+    assert int(step.pos) == pos + T and int(step.tok) == int(logits.float().cpu().argmax())
+    assert torch.equal(trace[0][0].cpu(), step.embed[ids].cpu())
+    after = step.state_copy()
+    for li, (p, st, (h_in, hm, rid, rw)) in enumerate(zip(step.L, before["L"], trace)):
+        want, st_want = _oracle_prompt_mixer(p, st, h_in.cpu(), pos)
+        ok, dmax = _within(hm, want)
+        print(f"[hybrid prefill] T={T} layer {li} ({p['kind']}) mixer: max |d| {dmax:.4f} within-tol {ok:.4f}",
+              flush=True)
+        assert ok >= 0.995, (li, p["kind"], ok)
+        if p["kind"] == "mla":
+            for key in ("kc", "vc"):
+                got = after["L"][li][key][0]
+                assert torch.equal(got[:, :pos].cpu(), st[key][0][:, :pos].cpu())
+                assert torch.equal(got[:, pos + T:].cpu(), st[key][0][:, pos + T:].cpu())
+                ok, _ = _within(got[:, pos:pos + T], st_want[key][:, pos:pos + T])
+                assert ok >= 0.995, (li, key, ok)
+        else:
+            ok, _ = _within(after["L"][li]["state"][0], st_want["state"], atol=2e-3)
+            assert ok >= 0.995, (li, "state", ok)
+            win = torch.cat([c[0] for c in after["L"][li]["conv"]])
+            ok, _ = _within(win, st_want["conv"])
+            assert ok >= 0.995, (li, "conv", ok)
+        b = {k: v.cpu() for k, v in p["blk"].items()}
+        xn = O.rms_norm(hm.cpu(), b["norm_w"], W.EPS)
+        moe = O.moe(xn, b["w_gu"], b["w_d"], rid.cpu(), rw.cpu(), residual=hm.cpu())
+        if li + 1 < len(trace):
+            ok, _ = _within(trace[li + 1][0], moe)
+            assert ok >= 0.995, (li, "moe", ok)
+    del step
+    torch.cuda.empty_cache()
+
+
+def test_fast_thinker_prefill_then_decode_follows_token_by_token_decode():
+    """A 24-token prompt in one prefill, and the same 24 tokens fed one decode step at a time to an identical
+    model: the same position, the layer states and the last logits agree to the bf16 level, and the next decode
+    step from either state picks the same token; a prefill captured in a graph replays bit for bit."""
+    T, pos = 24, 100
+    a = W.HybridThinkerStep(4, DEV, pos=pos, seed=7300)
+    b = W.HybridThinkerStep(4, DEV, pos=pos, seed=7300)
+    ids = torch.randint(0, a.embed.shape[0], (T,), generator=torch.Generator().manual_seed(3)).to(DEV)
+    print("[hybrid prefill] prefill vs 24 decode steps", flush=True)
+    la = a.fast.prefill(ids)
+    for t in range(T):
+        b.tok.fill_(int(ids[t]))
+        lb = b.fast()
+    torch.cuda.synchronize()
+    assert int(a.pos) == int(b.pos) == pos + T
+    cos = F.cosine_similarity(la.float().reshape(-1), lb.float().reshape(-1), dim=0)
+    assert float(cos) > 0.999, float(cos)
+    sa, sb = a.state_copy(), b.state_copy()
+    for li, (x, y) in enumerate(zip(sa["L"], sb["L"])):
+        for key in x:
+            for ta, tb in zip(x[key] if isinstance(x[key], tuple) else (x[key],),
+                              y[key] if isinstance(y[key], tuple) else (y[key],)):
+                c = F.cosine_similarity(ta.float().reshape(-1), tb.float().reshape(-1), dim=0)
+                assert float(c) > 0.999, (li, key, float(c))
+    b.tok.copy_(a.tok)
+    na, nb = a.fast(), b.fast()
+    assert int(a.tok) == int(b.tok) or float(F.cosine_similarity(na.float().reshape(-1), nb.float().reshape(-1),
+                                                                 dim=0)) > 0.999
+    # graph capture: the prompt captured once at the current position, replayed against eager prefills of a copy
+    c = W.HybridThinkerStep(4, DEV, pos=pos, seed=7400)
+    d = W.HybridThinkerStep(4, DEV, pos=pos, seed=7400)
+    c.fast.prefill(ids)  # warm-up (library GEMM plans); both models stay in the same state
+    d.fast.prefill(ids)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = c.fast.prefill(ids)
+    torch.cuda.synchronize()
+    for i in range(3):
+        print(f"[hybrid prefill graph] replay {i}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        want = d.fast.prefill(ids)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        assert int(c.pos) == int(d.pos) and int(c.tok) == int(d.tok)
+        for x, y in zip(c.state_copy()["L"], d.state_copy()["L"]):
+            for key in x:
+                for ta, tb in zip(x[key] if isinstance(x[key], tuple) else (x[key],),
+                                  y[key] if isinstance(y[key], tuple) else (y[key],)):
+                    assert torch.equal(ta, tb), (i, key)
+    del a, b, c, d, g, out
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("H,V,R,lower_bound", [(16, 128, 128, None), (3, 64, 64, None), (5, 128, 32, -5.0),

@@ -140,3 +140,48 @@ def test_mla_decode_attn_equals_sdpa_and_edge_cases():
     assert torch.equal(kc2[:, pos + 1:], kc[:, pos + 1:])
     out0, _, _ = A.mla_decode_attn(q, kn, vn, kc, vc, 0)  # one position: the new value itself
     torch.testing.assert_close(out0, vn, rtol=1e-12, atol=1e-12)
+
+
+def _mla_prompt(T, pos, nh=3, L=24, dq=16, dv=8, seed=80):
+    return (_rand(T, nh, dq, seed=seed), _rand(T, nh, dq, seed=seed + 1), _rand(T, nh, dv, seed=seed + 2),
+            _rand(nh, L, dq, seed=seed + 3), _rand(nh, L, dv, seed=seed + 4))
+
+
+def test_mla_prefill_attn_equals_token_by_token_decode_and_sdpa():
+    T, pos = 6, 9
+    q, kn, vn, kc, vc = _mla_prompt(T, pos)
+    out, kc2, vc2 = A.mla_prefill_attn(q, kn, vn, kc, vc, pos)
+    # the same prompt one token at a time through the decode form
+    kd, vd = kc.clone(), vc.clone()
+    for t in range(T):
+        o, kd, vd = A.mla_decode_attn(q[t], kn[t], vn[t], kd, vd, pos + t)
+        torch.testing.assert_close(out[t], o, rtol=1e-12, atol=1e-12)
+    assert torch.equal(kc2, kd) and torch.equal(vc2, vd)
+    # torch's attention with the causal mask over the updated caches
+    n = pos + T
+    mask = torch.arange(n)[None, :] <= (pos + torch.arange(T))[:, None]
+    ref = F.scaled_dot_product_attention(q.transpose(0, 1), kc2[:, :n], vc2[:, :n], attn_mask=mask)
+    torch.testing.assert_close(out, ref.transpose(0, 1), rtol=1e-12, atol=1e-12)
+    assert torch.equal(kc2[:, n:], kc[:, n:]) and torch.equal(kc2[:, :pos], kc[:, :pos])
+
+
+def test_mla_prefill_attn_edges():
+    q, kn, vn, kc, vc = _mla_prompt(1, 5, seed=90)
+    out, _, _ = A.mla_prefill_attn(q, kn, vn, kc, vc, 5)  # one token: the decode form
+    ref, _, _ = A.mla_decode_attn(q[0], kn[0], vn[0], kc, vc, 5)
+    torch.testing.assert_close(out[0], ref, rtol=1e-12, atol=1e-12)
+    q, kn, vn, kc, vc = _mla_prompt(4, 0, L=4, seed=95)  # a fresh cache filled to the end: token 0 sees itself
+    out, kc2, _ = A.mla_prefill_attn(q, kn, vn, kc, vc, 0)
+    torch.testing.assert_close(out[0], vn[0], rtol=1e-12, atol=1e-12)
+    assert torch.equal(kc2.transpose(0, 1), kn)
+
+
+def test_planted_mask_off_by_one_is_caught():
+    """A mask that hides the token's own key (keys < pos + t) changes every output row."""
+    T, pos = 5, 3
+    q, kn, vn, kc, vc = _mla_prompt(T, pos, seed=100)
+    out, kc2, vc2 = A.mla_prefill_attn(q, kn, vn, kc, vc, pos)
+    n = pos + T
+    wrong = torch.arange(n)[None, :] < (pos + torch.arange(T))[:, None]
+    bad = F.scaled_dot_product_attention(q.transpose(0, 1), kc2[:, :n], vc2[:, :n], attn_mask=wrong).transpose(0, 1)
+    assert all((out[t] - bad[t]).abs().max() > 1e-3 for t in range(T))
