@@ -209,4 +209,20 @@ __device__ __forceinline__ uint4 buf16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+// global_load_lds_dwordx4: lane i copies 16 bytes from src into LDS at lds_wave_base + 16 i (the base is
+// wave-uniform); the data is there once the wave's vector-memory count says the load is done (wait_vmcnt).
+__device__ __forceinline__ void load_lds16(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+// Wait until at most n vector-memory operations of this wave are outstanding (n a compile-time constant).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
 }  // namespace mmd

@@ -167,19 +167,6 @@ __device__ __forceinline__ int pos_row(int r, int c) {
   return r * rowb + ((c ^ ((r / rp) & mask)) << 4);
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
-
-__device__ __forceinline__ void load_lds16(const void* src, char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_wave_base, 16, 0, 0);
-}
-
-// Wait until at most n vector-memory loads of this wave are outstanding (n a compile-time constant).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
 
 // Per-thread source rows of the direct loads: for A instruction j the lane fills tile row ra[j], logical
 // chunk ca[j]; for B instruction j tile row rb[j], logical chunk cb[j].

@@ -3,11 +3,11 @@
 //   kda_recurrent_kernel   Kimi delta attention, the recurrent form fla's fused_recurrent_kda computes (called at
 //                          engine.py:258 and inside the model's KDA layers): per head a [K, V] fp32 state, per token
 //                          q, k l2-normalised (q scaled), a per-key-channel decay exp(g) from the gate, the delta
-//                          rule update and the readout. A workgroup holds 16 value columns of one head's state in
+//                          rule update and the readout. A wave holds 8 value columns of one head's state in
 //                          registers for all T tokens (the columns are independent); the sums over k go through
-//                          lanes, then LDS, in a fixed order.
+//                          lanes in a fixed order, the inputs through LDS 16 tokens at a time.
 //   short_conv_kernel      the depthwise causal convolution of ShortConvolution's step form (a cache of the last W
-//                          inputs per channel), SiLU, T tokens in order.
+//                          inputs per channel), SiLU, T tokens in parallel.
 //   rms_norm_gated_kernel  FusedRMSNormGated with a sigmoid gate: bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)).
 //   kda_token_kernel       one decode token of a KDA layer's core (the three above plus the gate's LoRA
 //                          up-projections) in one launch, one workgroup per head.
@@ -21,6 +21,17 @@
 namespace {
 
 using namespace mmd;
+
+__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// Orders a wave's LDS stores before its later loads (and loads before later stores) without a workgroup barrier:
+// a wave's LDS instructions execute in program order, so only the compiler's reordering has to be fenced.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // ------------------------------------------------------------------------------------------------- KDA
 
@@ -50,137 +61,231 @@ __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
 // softplus with the usual threshold: x above 20 returns x
 __device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-constexpr int kKdaCols = 16;  // value columns per workgroup: 16 lanes read a 64-byte segment of a state row
+constexpr int kKdaCols = 16;   // value columns per workgroup of kda_token_kernel
+constexpr int kKdaChunk = 16;  // tokens kda_recurrent_kernel stages in LDS at a time
 
-// Grid (V / 16, H) x 256 threads: each value column of the recurrence is independent (u and o of column v read
-// only column v of S), so a head's columns spread over V / 16 workgroups. Wave w, lane (rg = lane / 16,
-// c = lane % 16) holds state rows r = 16 i + 4 w + rg (i < K / 16) of column 16 * blockIdx.x + c: one load of a
-// wave reads 4 rows x 64 bytes. Per token the first K threads (whole waves) put each key channel's q, k and decay
-// into LDS, once for the workgroup, with the sums of q^2 and k^2. Sums over rows: lane-internal, then over the
-// 4 row groups of a wave (xor 16, then 32), then over the 4 waves through LDS, in a fixed order.
+// The per-token inputs of the recurrence, prepared for all T tokens in parallel (kda_prep_kernel) into a
+// workspace row per (token, head) of 3 K + 4 floats: q l2-normalised times the scale, k l2-normalised, the
+// per-channel decay exp(gate(g)), then beta (the sigmoid applied when it comes as logits), q . k of the
+// normalised vectors, and 2 zeros.
 template <int K>
-__global__ __launch_bounds__(256) void kda_recurrent_kernel(KdaArgs a) {
-  constexpr int CB = kKdaCols, RPT = K / 16;
-  static_assert(K % kWave == 0 && K <= 256, "kda key dim");
-  __shared__ float s_q[K], s_k[K], s_dec[K];
-  __shared__ float s_red[K / kWave][2];
-  __shared__ float part_u[4][CB], part_o[4][CB];
-  const int h = blockIdx.y;
-  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
-  const int c = lane % CB, rg = lane / CB;
+constexpr int kda_ws_row() { return 3 * K + 4; }
+
+// Grid (T H / 4) x 4 waves: wave w prepares row (t, h) = divmod(4 blockIdx.x + w, H), lane i channels i + 64 j.
+template <int K>
+__global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restrict__ ws) {
+  constexpr int NJ = K / kWave, ROW = kda_ws_row<K>();
+  const int lane = lane_id();
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (idx >= static_cast<int64_t>(a.T) * a.H) return;  // whole waves
+  const int64_t t = idx / a.H;
+  const int h = static_cast<int>(idx % a.H);
+  const int64_t hk = static_cast<int64_t>(h) * K;
+  float qv[NJ], kv[NJ], gv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int64_t ch = hk + lane + kWave * j;
+    qv[j] = bf16_to_f32(a.q[t * a.q_ts + ch]);
+    kv[j] = bf16_to_f32(a.k[t * a.k_ts + ch]);
+    gv[j] = ld_any(a.g, a.g_dtype, t * a.g_ts + ch);
+  }
+  float qs = a.scale, ks = 1.f;
+  if (a.use_l2norm) {
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      sq = fmaf(qv[j], qv[j], sq);
+      sk = fmaf(kv[j], kv[j], sk);
+    }
+    qs = a.scale / sqrtf(wave_sum(sq) + 1e-6f);
+    ks = 1.f / sqrtf(wave_sum(sk) + 1e-6f);
+  }
+  const float nA = a.use_gate ? __expf(a.A_log[h]) : 0.f;
+  float* row = ws + idx * ROW;
+  float qk = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + kWave * j;
+    float gl = gv[j];
+    if (a.use_gate) {
+      const float x = gl + a.dt_bias[hk + c];
+      gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
+    }
+    const float qn = qv[j] * qs, kn = kv[j] * ks;
+    row[c] = qn;
+    row[K + c] = kn;
+    row[2 * K + c] = __expf(gl);
+    qk = fmaf(qn, kn, qk);
+  }
+  qk = wave_sum(qk);
+  if (lane < 4) {
+    float b = 0.f;
+    if (lane == 0) {
+      b = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
+      if (a.beta_logits) b = 1.f / (1.f + __expf(-b));
+    }
+    row[3 * K + lane] = lane == 1 ? qk : b;
+  }
+}
+
+// One wave per (64 / (K / 8) value columns, head): grid (V / CPW, H) x 64 threads. Each value column of the
+// recurrence is independent (u and o of column v read only column v of S), so lane (c = lane / RG, rg = lane % RG,
+// RG = K / 8 row groups) holds the 8 state rows 8 rg .. 8 rg + 7 of column CPW blockIdx.x + c in registers for
+// the whole prompt, and the sums over k are lane-internal, then over the RG lanes of a column by DPP (no LDS, no
+// barrier). The prepared rows of the head come into LDS 16 tokens at a time by global_load_lds, two chunk
+// buffers deep (the next chunk loads while the recurrence runs on this one), and each token's 24 inputs of a lane
+// are read from LDS within the chunk's unrolled token steps. A wave's LDS traffic is ordered by the wave alone.
+// Per token the two sums over k, k . S and q . S of the decayed state, are independent (pairwise within the
+// lane, then their DPP steps interleaved), since o = S'^T q with S' = S + k u^T is q . S + u (q . k), q . k from
+// the workspace: the token's latency is one chain of sums, not two.
+template <int K>
+__global__ __launch_bounds__(64) void kda_recurrent_kernel(KdaArgs a, const float* __restrict__ ws) {
+  constexpr int RG = K / 8, CPW = kWave / RG, ROW = kda_ws_row<K>();
+  constexpr int CHUNK_UNITS = kKdaChunk * ROW / 4;  // 16-byte pieces of a chunk
+  constexpr int NU = (CHUNK_UNITS + kWave - 1) / kWave;
+  constexpr int ROW_UNITS = ROW / 4;
+  static_assert(K == 64 || K == 128, "kda key dim");
+  static_assert(ROW % 4 == 0, "16-byte workspace rows");
+  __shared__ __align__(16) float s_in[2][kKdaChunk * ROW];
+  __shared__ float s_v[kKdaChunk][CPW];
+  const int h = blockIdx.y, lane = lane_id();
+  const int c = lane / RG, rg = lane % RG;
   const int64_t V = a.V;
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
-  float* st = a.state + static_cast<int64_t>(h) * K * V + col;
-  float S[RPT];
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * CPW;
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col0 + c;
+  float S[8];
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
-  const bool chan = tid < K;  // whole waves
-  float nA = 0.f, dtb = 0.f;
-  if (a.use_gate) {
-    nA = __expf(a.A_log[h]);
-    if (chan) dtb = a.dt_bias[static_cast<int64_t>(h) * K + tid];
+  for (int i = 0; i < 8; ++i) S[i] = st[static_cast<int64_t>(8 * rg + i) * V];
+  const float* wsh = ws + static_cast<int64_t>(h) * ROW;
+  const int64_t ts = static_cast<int64_t>(a.H) * ROW;  // workspace token stride
+  constexpr int VPL = kKdaChunk * CPW / kWave;        // v values per lane per chunk
+  float rv[VPL];
+  auto issue = [&](int c0, int b) {
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      const int u = lane + kWave * j, tt = u / ROW_UNITS;
+      if (u < CHUNK_UNITS && c0 + tt < a.T)
+        load_lds16(wsh + (c0 + tt) * ts + (u % ROW_UNITS) * 4, reinterpret_cast<char*>(s_in[b]) + j * kWave * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int i = lane + kWave * j, tt = c0 + i / CPW;
+      rv[j] = tt < a.T ? bf16_to_f32(a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % CPW]) : 0.f;
+    }
+  };
+  issue(0, 0);
+  for (int c0 = 0, b = 0; c0 < a.T; c0 += kKdaChunk, b ^= 1) {
+    wait_vmcnt<0>();  // this chunk's loads (and the stores before them)
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int i = lane + kWave * j;
+      s_v[i / CPW][i % CPW] = rv[j];
+    }
+    wave_lds_fence();
+    if (c0 + kKdaChunk < a.T) issue(c0 + kKdaChunk, b ^ 1);  // in flight during the recurrence below
+    const int n = min(kKdaChunk, a.T - c0);
+    const float* base = s_in[b] + 8 * rg;
+    // lane (c, rg) keeps the output of tokens rg, rg + RG, ... of the chunk (every lane of a column holds each
+    // token's sum) and stores them after the chunk: the token steps have no branch
+    constexpr int OPL = kKdaChunk / RG;
+    float keep[OPL];
+#pragma unroll
+    for (int j = 0; j < OPL; ++j) keep[j] = 0.f;
+    auto step = [&](int t) {
+      const float* r = base + t * ROW;
+      const float4 q0 = *reinterpret_cast<const float4*>(r), q1 = *reinterpret_cast<const float4*>(r + 4);
+      const float4 k0 = *reinterpret_cast<const float4*>(r + K), k1 = *reinterpret_cast<const float4*>(r + K + 4);
+      const float4 d0 = *reinterpret_cast<const float4*>(r + 2 * K), d1 = *reinterpret_cast<const float4*>(r + 2 * K + 4);
+      const float2 bq = *reinterpret_cast<const float2*>(s_in[b] + t * ROW + 3 * K);  // beta, q . k
+      const float vc = s_v[t][c];
+      const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      // decay; the part of v the state already predicts from k, and q . S of the decayed state
+      float pk[8], pq[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        S[i] *= dd[i];
+        pk[i] = kk[i] * S[i];
+        pq[i] = qq[i] * S[i];
+      }
+      float pu = ((pk[0] + pk[1]) + (pk[2] + pk[3])) + ((pk[4] + pk[5]) + (pk[6] + pk[7]));
+      float qs = ((pq[0] + pq[1]) + (pq[2] + pq[3])) + ((pq[4] + pq[5]) + (pq[6] + pq[7]));
+      pu = group_sum<RG>(pu);
+      qs = group_sum<RG>(qs);
+      const float u = (vc - pu) * bq.x;
+      const float po = fmaf(u, bq.y, qs);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], u, S[i]);
+#pragma unroll
+      for (int j = 0; j < OPL; ++j)
+        if (t % RG == rg && t / RG == j) keep[j] = po;  // a select, no branch
+    };
+    if (n == kKdaChunk) {
+#pragma unroll
+      for (int t = 0; t < kKdaChunk; ++t) step(t);
+    } else {
+      for (int t = 0; t < n; ++t) step(t);
+    }
+#pragma unroll
+    for (int j = 0; j < OPL; ++j) {
+      const int t = rg + RG * j;
+      if (t < n) a.o[(c0 + t) * a.o_ts + static_cast<int64_t>(h) * V + col0 + c] = f32_to_bf16(keep[j]);
+    }
+    wave_lds_fence();  // the chunk's reads before the loads two chunks on overwrite its buffer
   }
-  for (int t = 0; t < a.T; ++t) {
-    if (chan) {
-      const int64_t i = static_cast<int64_t>(h) * K + tid;
-      const float qv = bf16_to_f32(a.q[t * a.q_ts + i]);
-      const float kv = bf16_to_f32(a.k[t * a.k_ts + i]);
-      float gl = ld_any(a.g, a.g_dtype, t * a.g_ts + i);
-      if (a.use_gate) {
-        const float x = gl + dtb;
-        gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
-      }
-      s_q[tid] = qv;
-      s_k[tid] = kv;
-      s_dec[tid] = __expf(gl);
-      if (a.use_l2norm) {
-        const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
-        if (lane == 0) {
-          s_red[w][0] = sq;
-          s_red[w][1] = sk;
-        }
-      }
-    }
-    const float vc = bf16_to_f32(a.v[t * a.v_ts + static_cast<int64_t>(h) * V + col]);
-    float beta = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
-    if (a.beta_logits) beta = 1.f / (1.f + __expf(-beta));
-    __syncthreads();
-    float qs = a.scale, ks = 1.f;
-    if (a.use_l2norm) {
-      float sq = s_red[0][0], sk = s_red[0][1];
 #pragma unroll
-      for (int j = 1; j < K / kWave; ++j) {
-        sq += s_red[j][0];
-        sk += s_red[j][1];
-      }
-      qs = a.scale / sqrtf(sq + 1e-6f);
-      ks = 1.f / sqrtf(sk + 1e-6f);
-    }
-    // decay, then the part of v the state already predicts from k
-    float pu = 0.f;
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int r = 16 * i + 4 * w + rg;
-      S[i] *= s_dec[r];
-      pu = fmaf(s_k[r] * ks, S[i], pu);
-    }
-    pu += __shfl_xor(pu, 16, kWave);
-    pu += __shfl_xor(pu, 32, kWave);
-    if (rg == 0) part_u[w][c] = pu;
-    __syncthreads();
-    const float u = (vc - (((part_u[0][c] + part_u[1][c]) + part_u[2][c]) + part_u[3][c])) * beta;
-    float po = 0.f;
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int r = 16 * i + 4 * w + rg;
-      S[i] = fmaf(s_k[r] * ks, u, S[i]);
-      po = fmaf(s_q[r] * qs, S[i], po);
-    }
-    po += __shfl_xor(po, 16, kWave);
-    po += __shfl_xor(po, 32, kWave);
-    if (rg == 0) part_o[w][c] = po;
-    // the next token rewrites s_* after this barrier, when every thread has read them; part_u / part_o are
-    // rewritten after the next token's first and second barriers, when wave 0 has read them
-    __syncthreads();
-    if (w == 0 && rg == 0) {
-      const float o = ((part_o[0][c] + part_o[1][c]) + part_o[2][c]) + part_o[3][c];
-      a.o[t * a.o_ts + static_cast<int64_t>(h) * V + col] = f32_to_bf16(o);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) st[static_cast<int64_t>(16 * i + 4 * w + rg) * V] = S[i];
+  for (int i = 0; i < 8; ++i) st[static_cast<int64_t>(8 * rg + i) * V] = S[i];
 }
 
 // ----------------------------------------------------------------------------------------- short conv
 
-// y[t, ch] = silu(sum_j w[ch, j] * win[j] + b[ch]), win = the last W inputs of the channel (cache[ch, 1..W-1] then
-// x[t, ch]); the cache keeps the window. fp32 math, one rounding of y.
+// y[t, ch] = silu(sum_j w[ch, j] * win_t[j] + b[ch]), win_t = the inputs t - W + 1 .. t of the channel (the cache
+// holds the last W before the prompt, oldest first); the cache keeps the window after the last token. fp32 math,
+// one rounding of y. Grid (C / 64, T / 16) x 64: a thread takes one channel for 16 tokens, all of whose inputs it
+// loads at once; only the first token chunk reads the cache (16 >= W - 1), and its threads write the new window
+// after their own reads of the old one.
+constexpr int kConvTokens = 16;
+
 template <int W>
-__global__ __launch_bounds__(256) void short_conv_kernel(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
-                                                         uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ b, int act,
-                                                         uint16_t* __restrict__ y, int64_t ys) {
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+__global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
+                                                        uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ b, int act,
+                                                        uint16_t* __restrict__ y, int64_t ys) {
+  static_assert(kConvTokens >= W - 1, "only the first chunk may read the cache");
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * kWave + threadIdx.x;
   if (ch >= C) return;
-  float win[W], wt[W];
+  const int t0 = blockIdx.y * kConvTokens;
+  float wt[W], in[kConvTokens + W - 1];  // inputs t0 - W + 1 .. t0 + 15
 #pragma unroll
-  for (int j = 0; j < W; ++j) {
-    win[j] = bf16_to_f32(cache[ch * W + j]);
-    wt[j] = bf16_to_f32(w[ch * W + j]);
+  for (int j = 0; j < W; ++j) wt[j] = bf16_to_f32(w[ch * W + j]);
+#pragma unroll
+  for (int i = 0; i < kConvTokens + W - 1; ++i) {
+    const int t = t0 - (W - 1) + i;
+    in[i] = t < 0 ? bf16_to_f32(cache[ch * W + W + t]) : t < T ? bf16_to_f32(x[t * xs + ch]) : 0.f;
   }
   const float bias = b ? bf16_to_f32(b[ch]) : 0.f;
-  for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int j = 0; j + 1 < W; ++j) win[j] = win[j + 1];
-    win[W - 1] = bf16_to_f32(x[t * xs + ch]);
-    float acc = bias;
+  for (int i = 0; i < kConvTokens; ++i) {
+    if (t0 + i < T) {
+      float acc = bias;
 #pragma unroll
-    for (int j = 0; j < W; ++j) acc = fmaf(wt[j], win[j], acc);
-    if (act) acc = silu(acc);
-    y[t * ys + ch] = f32_to_bf16(acc);
+      for (int j = 0; j < W; ++j) acc = fmaf(wt[j], in[i + j], acc);
+      if (act) acc = silu(acc);
+      y[(t0 + i) * ys + ch] = f32_to_bf16(acc);
+    }
   }
+  if (blockIdx.y == 0) {
+    // the window after the prompt: inputs T - W .. T - 1, from the old cache where they precede the prompt
+    uint16_t nw[W];
 #pragma unroll
-  for (int j = 0; j < W; ++j) cache[ch * W + j] = f32_to_bf16(win[j]);  // inputs are bf16: exact
+    for (int j = 0; j < W; ++j) {
+      const int t = T - W + j;
+      nw[j] = t < 0 ? cache[ch * W + W + t] : x[t * xs + ch];
+    }
+#pragma unroll
+    for (int j = 0; j < W; ++j) cache[ch * W + j] = nw[j];
+  }
 }
 
 // --------------------------------------------------------------------------------------- gated RMSNorm
@@ -527,8 +632,6 @@ __device__ __forceinline__ int64_t load_pos64(const void* p, int dt) {
   return dt == MM_INT64 ? *static_cast<const int64_t*>(p) : static_cast<int64_t>(*static_cast<const int32_t*>(p));
 }
 
-__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
 // Grid (chunks, heads) x 4 waves; wave w owns positions t0 .. t0 + 7 (t0 = 32 chunk + 8 w), the new row standing
 // in for row pos (and stored there by the wave that holds pos). First every lane issues its loads of the wave's
@@ -745,13 +848,6 @@ __global__ __launch_bounds__(64) void mla_prefill_store_kernel(MlaPrefillArgs a)
 constexpr int kMlaPKeys = 32;  // keys per tile
 constexpr int kMlaPVtRow = 36;  // bf16 per transposed value row in LDS: 32 keys + 4 (72 bytes, see the stores)
 
-// Orders a wave's LDS stores before its later loads (and loads before later stores) without a workgroup barrier:
-// a wave's LDS instructions execute in program order, so only the compiler's reordering has to be fenced.
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Causal attention of T prompt tokens over the static cache (the new rows already stored): token t at position
 // pos + t takes softmax(scale q_t . K[0..pos+t]^T) . V[0..pos+t] (engine.py:679-682's mask). Grid (T / 16,
@@ -934,25 +1030,38 @@ __global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a)
 }
 
 template <int K>
-int launch_kda(const KdaArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((kda_recurrent_kernel<K>), dim3(static_cast<unsigned>(a.V / kKdaCols), static_cast<unsigned>(a.H)),
-                     dim3(256), 0, st, a);
+int launch_kda(const KdaArgs& a, float* ws, hipStream_t st) {
+  const int64_t rows = static_cast<int64_t>(a.T) * a.H;
+  hipLaunchKernelGGL((kda_prep_kernel<K>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st, a, ws);
+  int rc = mm::check_launch("kda_recurrent prep");
+  if (rc) return rc;
+  constexpr int cpw = kWave / (K / 8);
+  hipLaunchKernelGGL((kda_recurrent_kernel<K>), dim3(static_cast<unsigned>(a.V / cpw), static_cast<unsigned>(a.H)),
+                     dim3(kWave), 0, st, a, static_cast<const float*>(ws));
   return mm::check_launch("kda_recurrent");
 }
 
 }  // namespace
 
+extern "C" int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K) {
+  if (T < 0 || H < 1 || (K != 64 && K != 128)) return 0;
+  return T * H * (3 * K + 4) * static_cast<int64_t>(sizeof(float));
+}
+
 extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                                 const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
                                 int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound,
                                 int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
-                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, void* stream) {
+                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
   MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535, "kda_recurrent: bad T=%lld or H=%lld", (long long)T,
              (long long)H);
-  // a thread holds K / 16 state values; workgroups of 16 value columns
-  MM_REQUIRE((K == 64 || K == 128) && V % kKdaCols == 0 && V >= kKdaCols && V <= 4096,
-             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 16 up to 4096)", (long long)K,
+  // a lane holds 8 state rows of one column; one wave per 64 / (K / 8) value columns
+  MM_REQUIRE((K == 64 || K == 128) && V % 8 == 0 && V >= 8 && V <= 4096,
+             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096)", (long long)K,
              (long long)V);
+  MM_REQUIRE(T == 0 || (workspace && mm::aligned16(workspace) && workspace_bytes >= mm_kda_recurrent_workspace(T, H, K)),
+             "kda_recurrent: the workspace must be 16-byte aligned and hold mm_kda_recurrent_workspace(T, H, K) bytes");
   MM_REQUIRE(g_dtype == MM_BF16 || g_dtype == MM_FP32, "kda_recurrent: g must be bf16 or fp32");
   MM_REQUIRE(beta_dtype == MM_BF16 || beta_dtype == MM_FP32, "kda_recurrent: beta must be bf16 or fp32");
   MM_REQUIRE(q && k && v && g && beta && state && o, "kda_recurrent: null pointer");
@@ -987,12 +1096,14 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
   a.H = static_cast<int>(H);
   a.V = static_cast<int>(V);
   hipStream_t st = MM_STREAM(stream);
-  return K == 64 ? launch_kda<64>(a, st) : launch_kda<128>(a, st);
+  float* ws = static_cast<float*>(workspace);
+  return K == 64 ? launch_kda<64>(a, ws, st) : launch_kda<128>(a, ws, st);
 }
 
 extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
                              const void* b, int act, void* y, int64_t y_ts, void* stream) {
-  MM_REQUIRE(T >= 0 && C >= 1 && C <= (1LL << 31) / 8, "short_conv: bad T=%lld or C=%lld", (long long)T, (long long)C);
+  MM_REQUIRE(T >= 0 && T <= 65535LL * kConvTokens && C >= 1 && C <= (1LL << 31) / 8, "short_conv: bad T=%lld or C=%lld",
+             (long long)T, (long long)C);
   MM_REQUIRE(W >= 2 && W <= 8, "short_conv: kernel width %lld must be in [2, 8]", (long long)W);
   MM_REQUIRE(x && cache && w && y, "short_conv: null pointer");
   MM_REQUIRE(x_ts >= C && y_ts >= C, "short_conv: token strides smaller than the channels");
@@ -1002,16 +1113,16 @@ extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, 
   const auto* wp = static_cast<const uint16_t*>(w);
   const auto* bp = static_cast<const uint16_t*>(b);
   auto* yp = static_cast<uint16_t*>(y);
-  dim3 grid(static_cast<unsigned>((C + 255) / 256));
+  dim3 grid(static_cast<unsigned>((C + kWave - 1) / kWave), static_cast<unsigned>((T + kConvTokens - 1) / kConvTokens));
   hipStream_t st = MM_STREAM(stream);
   switch (W) {
-    case 2: hipLaunchKernelGGL(short_conv_kernel<2>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 3: hipLaunchKernelGGL(short_conv_kernel<3>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 4: hipLaunchKernelGGL(short_conv_kernel<4>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 5: hipLaunchKernelGGL(short_conv_kernel<5>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 6: hipLaunchKernelGGL(short_conv_kernel<6>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 7: hipLaunchKernelGGL(short_conv_kernel<7>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    default: hipLaunchKernelGGL(short_conv_kernel<8>, grid, dim3(256), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 2: hipLaunchKernelGGL(short_conv_kernel<2>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 3: hipLaunchKernelGGL(short_conv_kernel<3>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 4: hipLaunchKernelGGL(short_conv_kernel<4>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 5: hipLaunchKernelGGL(short_conv_kernel<5>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 6: hipLaunchKernelGGL(short_conv_kernel<6>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 7: hipLaunchKernelGGL(short_conv_kernel<7>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    default: hipLaunchKernelGGL(short_conv_kernel<8>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
   }
   return mm::check_launch("short_conv");
 }

@@ -23,7 +23,7 @@ import torch
 
 import _mingmoe as _mm
 
-__all__ = ["fused_recurrent_kda", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
+__all__ = ["fused_recurrent_kda", "kda_workspace", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
            "mla_attn_workspace", "mla_prefill_attn", "embed_rows", "argmax_rows"]
 
 
@@ -46,15 +46,24 @@ def _tokens(t, name, H, D):
     return t, t.shape[0], t.stride(0)
 
 
+def kda_workspace(T, H, K, device):
+    """The fp32 workspace fused_recurrent_kda needs for T tokens of H heads of key dim K."""
+    n = _mm.load().mm_kda_recurrent_workspace(T, H, K)
+    if n <= 0:
+        raise ValueError(f"kda_workspace: bad T={T}, H={H} or K={K}")
+    return torch.empty(n // 4, device=device, dtype=torch.float32)
+
+
 def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
                         output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
-                        lower_bound=None, inplace=False, out=None, beta_is_logits=False, **unused):
+                        lower_bound=None, inplace=False, out=None, beta_is_logits=False, workspace=None, **unused):
     """q, k [1, T, H, K] bf16; v [1, T, H, V] bf16; g [1, T, H, K] (bf16 / fp32; the raw gate projection when
     use_gate_in_kernel, else a log decay); beta [1, T, H] (fp32 / bf16); A_log [H], dt_bias [H * K] (or [H, K]);
     initial_state [1, H, K, V] fp32 (zeros when None). Returns (o [1, T, H, V] bf16, final_state or None).
     scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor);
-    beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel."""
-    _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out)
+    beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel. workspace: from
+    kda_workspace(T, H, K) (allocated when None)."""
+    _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out, workspace)
     if q.dim() != 4 or q.shape[0] != 1:
         raise ValueError(f"fused_recurrent_kda: q must be [1, T, H, K] (got {tuple(q.shape)})")
     _, T, H, K = q.shape
@@ -96,12 +105,14 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     sc = float(scale) if scale is not None else K ** -0.5
     lb = float("nan") if lower_bound is None else float(lower_bound)
     lib = _mm.load()
+    ws = workspace if workspace is not None else (kda_workspace(T, H, K, q.device) if T else None)
     with _mm.on_device(q):
         _mm.check(lib.mm_kda_recurrent(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts,
                                        _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,
                                        1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0,
-                                       1 if beta_is_logits else 0, sc, T, H, K, V,
-                                       _mm.ptr(state), _mm.ptr(o), o.stride(0), _mm.stream_of(q)), "fused_recurrent_kda")
+                                       1 if beta_is_logits else 0, sc, T, H, K, V, _mm.ptr(state), _mm.ptr(o),
+                                       o.stride(0), _mm.ptr(ws), ws.numel() * 4 if ws is not None else 0,
+                                       _mm.stream_of(q)), "fused_recurrent_kda")
     final = None
     if output_final_state or inplace:
         final = state if (inplace and initial_state is not None) else state.reshape(1, H, K, V)
