@@ -419,6 +419,40 @@ def hybrid_decode_metrics(stream, layers=28, pos=456):
     return out
 
 
+def hybrid_prefill_metrics(stream, layers=28, pos=512, lengths=(32, 128, 512)):
+    """A prompt of T tokens through the synthetic hybrid thinker (thinker_step.FastThinkerStep.prefill, the engine's
+    _prefill: per layer the mixer over the T rows — the projection GEMMs, the short convolutions and the KDA
+    recurrence, or the causal MLA attention over the cache — then the prefill MoE block; the head on the last
+    token), captured in one hipGraph per T and replayed at position 512 of a 2048-row cache (the position set back
+    before each replay; the layer states keep evolving, which changes no amount of work): median of 5 timed
+    replays after one, in ms and prompt tokens/s. The expert stacks take the registered prefill copies."""
+    import workloads as W
+    step = W.HybridThinkerStep(layers, "cuda", pos=pos, max_len=2048, seed=5000)
+    out = {"layers": layers, "kda_layers": sum(p["kind"] == "kda" for p in step.L), "pos": pos}
+    for T in lengths:
+        ids = (torch.arange(T, device="cuda") * 7919 + 11) % step.embed.shape[0]
+        step.pos.fill_(pos)
+        g = graph_of(lambda: step.fast.prefill(ids), stream)
+        ts = []
+        for _ in range(6):
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                step.pos.fill_(pos)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        torch.cuda.current_stream().wait_stream(stream)
+        ms = sorted(ts[1:])[2]
+        out[f"T{T}"] = {"ms": ms, "tokens_per_s": T / ms * 1e3}
+        del g
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
 # ------------------------------------------------------------------------------------------- Talker path
 
 def talker_metrics(stream, layers=24, max_len=1024, pos=512):
@@ -710,6 +744,8 @@ def main():
     if want("hybrid"):
         extra["hybrid_decode_28l"] = hybrid_decode_metrics(stream)
         log(f"[bench] hybrid decode: {extra['hybrid_decode_28l']}")
+        extra["hybrid_prefill_28l"] = hybrid_prefill_metrics(stream)
+        log(f"[bench] hybrid prefill: {extra['hybrid_prefill_28l']}")
     if want("talker"):
         torch.cuda.empty_cache()
         extra["talker"] = talker_metrics(stream)
