@@ -303,15 +303,16 @@ int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stri
  * q, k [T, H, K] bf16, v [T, H, V] bf16, g [T, H, K] (MM_BF16 / MM_FP32), beta [T, H] (MM_BF16 / MM_FP32; the write
  * strength, or with beta_logits the projection whose sigmoid it is), each with its token stride in elements; A_log [H], dt_bias [H * K] fp32 (used when
  * use_gate); state [H, K, V] fp32, read and updated in place; o [T, H, V] bf16 (token stride o_ts).
- * K: 64 or 128; V: a multiple of 8 up to 4096. workspace: at least mm_kda_recurrent_workspace(T, H, K) bytes,
- * 16-byte aligned (the per-token inputs prepared for all tokens at once, then read by the sequential part). */
+ * K: 64 or 128; V: a multiple of 8 up to 4096 (of 16 for T <= 2). workspace: at least
+ * mm_kda_recurrent_workspace(T, H, K) bytes, 16-byte aligned (the per-token inputs prepared for all tokens at once,
+ * then read by the sequential part); T <= 2 (a decode step) runs in one launch and needs none (NULL allowed). */
 int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                      const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
                      const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm, int use_gate,
                      int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V, float* state, void* o,
                      int64_t o_ts, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Bytes of fp32 workspace mm_kda_recurrent needs: T * H * (3 K + 4) * 4 (0 if invalid). */
+/* Bytes of fp32 workspace mm_kda_recurrent needs: T * H * (3 K + 4) * 4, 0 for T <= 2 (-1 if invalid). */
 int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K);
 
 /* Depthwise causal convolution over time, the step form of fla's ShortConvolution (the q / k / v convolutions of a

@@ -1,11 +1,15 @@
 // The thinker's attention mixers for decode and short prefills on gfx950:
 //
-//   kda_recurrent_kernel   Kimi delta attention, the recurrent form fla's fused_recurrent_kda computes (called at
+//   kda_prep_kernel / kda_recurrent_kernel
+//                          Kimi delta attention, the recurrent form fla's fused_recurrent_kda computes (called at
 //                          engine.py:258 and inside the model's KDA layers): per head a [K, V] fp32 state, per token
 //                          q, k l2-normalised (q scaled), a per-key-channel decay exp(g) from the gate, the delta
-//                          rule update and the readout. A wave holds 8 value columns of one head's state in
-//                          registers for all T tokens (the columns are independent); the sums over k go through
-//                          lanes in a fixed order, the inputs through LDS 16 tokens at a time.
+//                          rule update and the readout. The per-token inputs are prepared for all tokens at once
+//                          into a workspace; then a wave holds 4 value columns of one head's state in registers
+//                          for all T tokens (the columns are independent), the sums over k go through lanes in a
+//                          fixed order and the inputs through LDS 16 tokens at a time.
+//   kda_short_kernel       the same recurrence for up to 2 tokens (a decode step) in one launch: a workgroup holds
+//                          16 value columns, the sums over k go through lanes, then LDS.
 //   short_conv_kernel      the depthwise causal convolution of ShortConvolution's step form (a cache of the last W
 //                          inputs per channel), SiLU, T tokens in parallel.
 //   rms_norm_gated_kernel  FusedRMSNormGated with a sigmoid gate: bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)).
@@ -61,8 +65,109 @@ __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
 // softplus with the usual threshold: x above 20 returns x
 __device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-constexpr int kKdaCols = 16;   // value columns per workgroup of kda_token_kernel
+constexpr int kKdaCols = 16;   // value columns per workgroup of kda_short_kernel and kda_token_kernel
 constexpr int kKdaChunk = 16;  // tokens kda_recurrent_kernel stages in LDS at a time
+constexpr int kKdaShortT = 2;  // prompts up to this long take kda_short_kernel (one launch, no workspace)
+
+// Prompts of up to kKdaShortT tokens (a decode step) in one launch, without the workspace: grid (V / 16, H) x 256
+// threads; each value column of the recurrence is independent (u and o of column v read
+// only column v of S), so a head's columns spread over V / 16 workgroups. Wave w, lane (rg = lane / 16,
+// c = lane % 16) holds state rows r = 16 i + 4 w + rg (i < K / 16) of column 16 * blockIdx.x + c: one load of a
+// wave reads 4 rows x 64 bytes. Per token the first K threads (whole waves) put each key channel's q, k and decay
+// into LDS, once for the workgroup, with the sums of q^2 and k^2. Sums over rows: lane-internal, then over the
+// 4 row groups of a wave (xor 16, then 32), then over the 4 waves through LDS, in a fixed order.
+template <int K>
+__global__ __launch_bounds__(256) void kda_short_kernel(KdaArgs a) {
+  constexpr int CB = kKdaCols, RPT = K / 16;
+  static_assert(K % kWave == 0 && K <= 256, "kda key dim");
+  __shared__ float s_q[K], s_k[K], s_dec[K];
+  __shared__ float s_red[K / kWave][2];
+  __shared__ float part_u[4][CB], part_o[4][CB];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, w = tid / kWave, lane = lane_id();
+  const int c = lane % CB, rg = lane / CB;
+  const int64_t V = a.V;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * CB + c;
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col;
+  float S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) S[i] = st[static_cast<int64_t>(16 * i + 4 * w + rg) * V];
+  const bool chan = tid < K;  // whole waves
+  float nA = 0.f, dtb = 0.f;
+  if (a.use_gate) {
+    nA = __expf(a.A_log[h]);
+    if (chan) dtb = a.dt_bias[static_cast<int64_t>(h) * K + tid];
+  }
+  for (int t = 0; t < a.T; ++t) {
+    if (chan) {
+      const int64_t i = static_cast<int64_t>(h) * K + tid;
+      const float qv = bf16_to_f32(a.q[t * a.q_ts + i]);
+      const float kv = bf16_to_f32(a.k[t * a.k_ts + i]);
+      float gl = ld_any(a.g, a.g_dtype, t * a.g_ts + i);
+      if (a.use_gate) {
+        const float x = gl + dtb;
+        gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
+      }
+      s_q[tid] = qv;
+      s_k[tid] = kv;
+      s_dec[tid] = __expf(gl);
+      if (a.use_l2norm) {
+        const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+        if (lane == 0) {
+          s_red[w][0] = sq;
+          s_red[w][1] = sk;
+        }
+      }
+    }
+    const float vc = bf16_to_f32(a.v[t * a.v_ts + static_cast<int64_t>(h) * V + col]);
+    float beta = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
+    if (a.beta_logits) beta = 1.f / (1.f + __expf(-beta));
+    __syncthreads();
+    float qs = a.scale, ks = 1.f;
+    if (a.use_l2norm) {
+      float sq = s_red[0][0], sk = s_red[0][1];
+#pragma unroll
+      for (int j = 1; j < K / kWave; ++j) {
+        sq += s_red[j][0];
+        sk += s_red[j][1];
+      }
+      qs = a.scale / sqrtf(sq + 1e-6f);
+      ks = 1.f / sqrtf(sk + 1e-6f);
+    }
+    // decay, then the part of v the state already predicts from k
+    float pu = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w + rg;
+      S[i] *= s_dec[r];
+      pu = fmaf(s_k[r] * ks, S[i], pu);
+    }
+    pu += __shfl_xor(pu, 16, kWave);
+    pu += __shfl_xor(pu, 32, kWave);
+    if (rg == 0) part_u[w][c] = pu;
+    __syncthreads();
+    const float u = (vc - (((part_u[0][c] + part_u[1][c]) + part_u[2][c]) + part_u[3][c])) * beta;
+    float po = 0.f;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = 16 * i + 4 * w + rg;
+      S[i] = fmaf(s_k[r] * ks, u, S[i]);
+      po = fmaf(s_q[r] * qs, S[i], po);
+    }
+    po += __shfl_xor(po, 16, kWave);
+    po += __shfl_xor(po, 32, kWave);
+    if (rg == 0) part_o[w][c] = po;
+    // the next token rewrites s_* after this barrier, when every thread has read them; part_u / part_o are
+    // rewritten after the next token's first and second barriers, when wave 0 has read them
+    __syncthreads();
+    if (w == 0 && rg == 0) {
+      const float o = ((part_o[0][c] + part_o[1][c]) + part_o[2][c]) + part_o[3][c];
+      a.o[t * a.o_ts + static_cast<int64_t>(h) * V + col] = f32_to_bf16(o);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) st[static_cast<int64_t>(16 * i + 4 * w + rg) * V] = S[i];
+}
 
 // The per-token inputs of the recurrence, prepared for all T tokens in parallel (kda_prep_kernel) into a
 // workspace row per (token, head) of 3 K + 4 floats: q l2-normalised times the scale, k l2-normalised, the
@@ -328,8 +433,8 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
 //     bf16 as short_conv_kernel stores them) and the windows shift in this token's inputs;
 //   - f = bf16(sum_r f_b[ch, r] fa[r]) per key channel and g = bf16(sum_r g_b[ch, r] ga[r]) per value column
 //     (two lanes per LoRA row, each over its half of R in order, one shuffle);
-//   - one token of kda_recurrent_kernel's recurrence, column block by column block (four waves per block of 16
-//     value columns, the sums over key rows in kda_recurrent_kernel's order);
+//   - one token of kda_short_kernel's recurrence, column block by column block (four waves per block of 16
+//     value columns, the sums over key rows in kda_short_kernel's order);
 //   - y = rms_norm_gated(bf16(o), g).
 // Same arithmetic as the five kernels except the order of the f and g dots (small_linear reduces over more
 // lanes), so f and g can differ in the last bf16 place.
@@ -431,7 +536,7 @@ constexpr int kKdaThreads = 512;
 
 // Grid H x 512 threads, K = 128, V <= 128 NP. Wave w, lane (rg = lane / 16, c4 = lane % 16): row group w4 = w % 4
 // and column half hf = w / 4; in pass p the lane holds state rows r = 16 i + 4 w4 + rg (i < 8) of the four columns
-// 128 p + 64 hf + 4 c4 .. + 3 (one 16-byte load per row). Each column's sums over rows keep kda_recurrent_kernel's
+// 128 p + 64 hf + 4 c4 .. + 3 (one 16-byte load per row). Each column's sums over rows keep kda_short_kernel's
 // order: lane-internal over i, then over the 4 row groups of a wave (xor 16, then 32), then over the 4 waves of
 // its half through LDS. Threads 0..255 take the f rows (K of them, a lane pair each), threads 256..511 the g rows,
 // 128 per pass; threads < K the q and k channels, threads < V the v channels. Every global load is issued before
@@ -1031,6 +1136,11 @@ __global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a)
 
 template <int K>
 int launch_kda(const KdaArgs& a, float* ws, hipStream_t st) {
+  if (a.T <= kKdaShortT) {
+    hipLaunchKernelGGL((kda_short_kernel<K>), dim3(static_cast<unsigned>(a.V / kKdaCols), static_cast<unsigned>(a.H)),
+                       dim3(256), 0, st, a);
+    return mm::check_launch("kda_recurrent");
+  }
   const int64_t rows = static_cast<int64_t>(a.T) * a.H;
   hipLaunchKernelGGL((kda_prep_kernel<K>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st, a, ws);
   int rc = mm::check_launch("kda_recurrent prep");
@@ -1044,7 +1154,8 @@ int launch_kda(const KdaArgs& a, float* ws, hipStream_t st) {
 }  // namespace
 
 extern "C" int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K) {
-  if (T < 0 || H < 1 || (K != 64 && K != 128)) return 0;
+  if (T < 0 || H < 1 || (K != 64 && K != 128)) return -1;
+  if (T <= kKdaShortT) return 0;
   return T * H * (3 * K + 4) * static_cast<int64_t>(sizeof(float));
 }
 
@@ -1057,10 +1168,11 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
   MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535, "kda_recurrent: bad T=%lld or H=%lld", (long long)T,
              (long long)H);
   // a lane holds 8 state rows of one column; one wave per 64 / (K / 8) value columns
-  MM_REQUIRE((K == 64 || K == 128) && V % 8 == 0 && V >= 8 && V <= 4096,
-             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096)", (long long)K,
-             (long long)V);
-  MM_REQUIRE(T == 0 || (workspace && mm::aligned16(workspace) && workspace_bytes >= mm_kda_recurrent_workspace(T, H, K)),
+  MM_REQUIRE((K == 64 || K == 128) && V % (T <= kKdaShortT ? kKdaCols : 8) == 0 && V >= 8 && V <= 4096,
+             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096; of 16 for T <= %d)",
+             (long long)K, (long long)V, kKdaShortT);
+  MM_REQUIRE(T <= kKdaShortT || (workspace && mm::aligned16(workspace) &&
+                                 workspace_bytes >= mm_kda_recurrent_workspace(T, H, K)),
              "kda_recurrent: the workspace must be 16-byte aligned and hold mm_kda_recurrent_workspace(T, H, K) bytes");
   MM_REQUIRE(g_dtype == MM_BF16 || g_dtype == MM_FP32, "kda_recurrent: g must be bf16 or fp32");
   MM_REQUIRE(beta_dtype == MM_BF16 || beta_dtype == MM_FP32, "kda_recurrent: beta must be bf16 or fp32");

@@ -49,9 +49,9 @@ def _tokens(t, name, H, D):
 def kda_workspace(T, H, K, device):
     """The fp32 workspace fused_recurrent_kda needs for T tokens of H heads of key dim K."""
     n = _mm.load().mm_kda_recurrent_workspace(T, H, K)
-    if n <= 0:
+    if n < 0:
         raise ValueError(f"kda_workspace: bad T={T}, H={H} or K={K}")
-    return torch.empty(n // 4, device=device, dtype=torch.float32)
+    return torch.empty(max(n, 16) // 4, device=device, dtype=torch.float32)
 
 
 def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
@@ -105,7 +105,9 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     sc = float(scale) if scale is not None else K ** -0.5
     lb = float("nan") if lower_bound is None else float(lower_bound)
     lib = _mm.load()
-    ws = workspace if workspace is not None else (kda_workspace(T, H, K, q.device) if T else None)
+    ws = workspace
+    if ws is None and lib.mm_kda_recurrent_workspace(T, H, K) > 0:
+        ws = kda_workspace(T, H, K, q.device)
     with _mm.on_device(q):
         _mm.check(lib.mm_kda_recurrent(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts,
                                        _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,

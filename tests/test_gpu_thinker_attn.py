@@ -1,5 +1,5 @@
-"""GPU parity of the thinker's attention mixers (KDA recurrent core, short convolution, gated norm, MLA decode
-attention) against oracle/thinker_attn_oracle.py on seeded inputs. bf16 outputs within rtol 2e-2 / atol 1e-2; the fp32
+"""GPU parity of the thinker's attention mixers (KDA recurrent core, short convolution, gated norm, MLA decode and
+prompt attention, the hybrid step's decode and prefill) against oracle/thinker_attn_oracle.py on seeded inputs. bf16 outputs within rtol 2e-2 / atol 1e-2; the fp32
 KDA state within rtol 1e-3 / atol 1e-4 of the float64 oracle; cache rows bit-exact."""
 import pytest
 import torch
@@ -31,7 +31,8 @@ def _kda_inputs(T, H, K, V, seed, gdt=torch.float32):
 
 
 @pytest.mark.parametrize("T,H,K,V", [(1, 16, 128, 128), (7, 4, 128, 128), (64, 2, 128, 128), (3, 5, 64, 64),
-                                     (9, 3, 128, 64), (4, 2, 64, 128), (3, 2, 64, 48), (2, 3, 128, 32)])
+                                     (9, 3, 128, 64), (4, 2, 64, 128), (3, 2, 64, 48), (2, 3, 128, 32),
+                                     (37, 2, 128, 40), (130, 3, 128, 128), (33, 2, 64, 56), (16, 1, 128, 8)])
 @pytest.mark.parametrize("gate", ["softplus", "lower_bound", "none"])
 def test_kda_recurrent_matches_oracle(T, H, K, V, gate):
     print(f"[kda] T={T} H={H} K={K} V={V} gate={gate}", flush=True)
@@ -90,7 +91,8 @@ def test_kda_zero_write_strength_keeps_the_state():
     assert torch.equal(fin, S0)
 
 
-@pytest.mark.parametrize("T,C,Wd", [(1, 6144, 4), (5, 6144, 4), (3, 1000, 2), (2, 77, 8)])
+@pytest.mark.parametrize("T,C,Wd", [(1, 6144, 4), (5, 6144, 4), (3, 1000, 2), (2, 77, 8), (40, 2048, 4), (17, 77, 8),
+                                    (100, 130, 3), (16, 64, 4)])
 def test_short_conv_matches_oracle(T, C, Wd):
     x = W.normal((1, T, C), 1.0, 400 + T, DEV)
     cache = W.normal((1, C, Wd), 1.0, 401, DEV)
