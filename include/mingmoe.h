@@ -305,12 +305,15 @@ int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stri
  * use_gate); state [H, K, V] fp32, read and updated in place; o [T, H, V] bf16 (token stride o_ts).
  * K: 64 or 128; V: a multiple of 8 up to 4096 (of 16 for T <= 2). workspace: at least
  * mm_kda_recurrent_workspace(T, H, K) bytes, 16-byte aligned (the per-token inputs prepared for all tokens at once,
- * then read by the sequential part); T <= 2 (a decode step) runs in one launch and needs none (NULL allowed). */
+ * then read by the sequential part); T <= 2 (a decode step) runs in one launch and needs none (NULL allowed).
+ * n_valid: NULL, or an int64 device scalar n: tokens n .. T - 1 are padding and leave the state exactly unchanged
+ * (decay 1, write strength 0: the padded prefill of engine.py:234-256, where the gate is -1e30 and beta 0); their
+ * outputs are unspecified. */
 int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                      const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
                      const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm, int use_gate,
                      int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V, float* state, void* o,
-                     int64_t o_ts, void* workspace, int64_t workspace_bytes, void* stream);
+                     int64_t o_ts, const int64_t* n_valid, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of fp32 workspace mm_kda_recurrent needs: T * H * (3 K + 4) * 4, 0 for T <= 2 (-1 if invalid). */
 int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K);
@@ -319,9 +322,10 @@ int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K);
  * KDA layer, engine.py:247-249, caches engine.py:645-647): per channel, for each of T tokens in order, the window
  * (cache[ch, 1..W-1], x[t, ch]) replaces the cache and y[t, ch] = act(sum_j w[ch, j] * window[j] + b[ch]) (act 1:
  * SiLU, 0: none; fp32, one rounding). x, y [T, C] bf16 with token strides; cache [C, W], w [C, W] (a conv1d weight
- * [C, 1, W]) bf16; b [C] bf16 or NULL. 2 <= W <= 8. */
+ * [C, 1, W]) bf16; b [C] bf16 or NULL. 2 <= W <= 8. n_valid: NULL, or an int64 device scalar n: the cache ends on
+ * the first n tokens' inputs (the padded prefill's conv_idx, engine.py:254-256); every y row is still computed. */
 int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
-                  const void* b, int act, void* y, int64_t y_ts, void* stream);
+                  const void* b, int act, void* y, int64_t y_ts, const int64_t* n_valid, void* stream);
 
 /* y = bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)) per row of n <= 512 elements: fla's FusedRMSNormGated with a
  * sigmoid gate, the output norm of a KDA layer (o_norm, engine.py:265). x, g, y [rows, n] bf16 with row strides;

@@ -77,9 +77,9 @@ SIGNATURES = {
     "mm_silu_mul": ([_P, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
     "mm_cfg_update": ([_P, _P, _I64, _I64, _F32, _P, _I32, _P, _P], ctypes.c_int),
     "mm_kda_recurrent": ([_P, _I64, _P, _I64, _P, _I64, _P, _I32, _I64, _P, _I32, _I64, _P, _P, _F32, _I32, _I32, _I32,
-                          _F32, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P], ctypes.c_int),
+                          _F32, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P], ctypes.c_int),
     "mm_kda_recurrent_workspace": ([_I64, _I64, _I64], ctypes.c_int64),
-    "mm_short_conv": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _P], ctypes.c_int),
+    "mm_short_conv": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _P, _P], ctypes.c_int),
     "mm_rms_norm_gated": ([_P, _I64, _P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P], ctypes.c_int),
     "mm_mla_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),
     "mm_kda_decode_step": ([_P, _I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), _I64, _P, _P,

@@ -56,7 +56,16 @@ struct KdaArgs {
   uint16_t* o;                             // [T, H, V] bf16
   int64_t o_ts;
   int T, H, V;
+  const int64_t* n_valid;                  // device scalar or null: tokens from n_valid on are padding
 };
+
+// The prompt's real tokens: the first n_valid (clamped to [0, T]) when given, else all T. A padding token leaves the
+// state exactly as it is: its decay is 1 and its write strength 0 (engine.py:234-256's padded prefill).
+__device__ __forceinline__ int kda_valid(const KdaArgs& a) {
+  if (!a.n_valid) return a.T;
+  const int64_t n = *a.n_valid;
+  return static_cast<int>(n < 0 ? 0 : n > a.T ? a.T : n);
+}
 
 __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
   return dt == MM_BF16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
@@ -98,6 +107,7 @@ __global__ __launch_bounds__(256) void kda_short_kernel(KdaArgs a) {
     nA = __expf(a.A_log[h]);
     if (chan) dtb = a.dt_bias[static_cast<int64_t>(h) * K + tid];
   }
+  const int nv = kda_valid(a);
   for (int t = 0; t < a.T; ++t) {
     if (chan) {
       const int64_t i = static_cast<int64_t>(h) * K + tid;
@@ -110,7 +120,7 @@ __global__ __launch_bounds__(256) void kda_short_kernel(KdaArgs a) {
       }
       s_q[tid] = qv;
       s_k[tid] = kv;
-      s_dec[tid] = __expf(gl);
+      s_dec[tid] = t < nv ? __expf(gl) : 1.f;
       if (a.use_l2norm) {
         const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
         if (lane == 0) {
@@ -122,6 +132,7 @@ __global__ __launch_bounds__(256) void kda_short_kernel(KdaArgs a) {
     const float vc = bf16_to_f32(a.v[t * a.v_ts + static_cast<int64_t>(h) * V + col]);
     float beta = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
     if (a.beta_logits) beta = 1.f / (1.f + __expf(-beta));
+    if (t >= nv) beta = 0.f;
     __syncthreads();
     float qs = a.scale, ks = 1.f;
     if (a.use_l2norm) {
@@ -186,6 +197,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
   const int64_t t = idx / a.H;
   const int h = static_cast<int>(idx % a.H);
   const int64_t hk = static_cast<int64_t>(h) * K;
+  const bool pad = t >= kda_valid(a);
   float qv[NJ], kv[NJ], gv[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -219,7 +231,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
     const float qn = qv[j] * qs, kn = kv[j] * ks;
     row[c] = qn;
     row[K + c] = kn;
-    row[2 * K + c] = __expf(gl);
+    row[2 * K + c] = pad ? 1.f : __expf(gl);
     qk = fmaf(qn, kn, qk);
   }
   qk = wave_sum(qk);
@@ -228,6 +240,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
     if (lane == 0) {
       b = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
       if (a.beta_logits) b = 1.f / (1.f + __expf(-b));
+      if (pad) b = 0.f;
     }
     row[3 * K + lane] = lane == 1 ? qk : b;
   }
@@ -356,7 +369,8 @@ template <int W>
 __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
                                                         uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
                                                         const uint16_t* __restrict__ b, int act,
-                                                        uint16_t* __restrict__ y, int64_t ys) {
+                                                        uint16_t* __restrict__ y, int64_t ys,
+                                                        const int64_t* __restrict__ n_valid) {
   static_assert(kConvTokens >= W - 1, "only the first chunk may read the cache");
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * kWave + threadIdx.x;
   if (ch >= C) return;
@@ -381,11 +395,14 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
     }
   }
   if (blockIdx.y == 0) {
-    // the window after the prompt: inputs T - W .. T - 1, from the old cache where they precede the prompt
+    // the window after the prompt's real tokens (the first n_valid, clamped to [0, T], when given: the padded
+    // prefill's conv_idx, engine.py:254-256): inputs nv - W .. nv - 1, from the old cache where they precede it
+    int nv = T;
+    if (n_valid) nv = static_cast<int>(*n_valid < 0 ? 0 : *n_valid > T ? T : *n_valid);
     uint16_t nw[W];
 #pragma unroll
     for (int j = 0; j < W; ++j) {
-      const int t = T - W + j;
+      const int t = nv - W + j;
       nw[j] = t < 0 ? cache[ch * W + W + t] : x[t * xs + ch];
     }
 #pragma unroll
@@ -1163,8 +1180,8 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
                                 const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
                                 int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound,
                                 int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
-                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, void* workspace,
-                                int64_t workspace_bytes, void* stream) {
+                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, const int64_t* n_valid,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535, "kda_recurrent: bad T=%lld or H=%lld", (long long)T,
              (long long)H);
   // a lane holds 8 state rows of one column; one wave per 64 / (K / 8) value columns
@@ -1207,13 +1224,14 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
   a.T = static_cast<int>(T);
   a.H = static_cast<int>(H);
   a.V = static_cast<int>(V);
+  a.n_valid = n_valid;
   hipStream_t st = MM_STREAM(stream);
   float* ws = static_cast<float*>(workspace);
   return K == 64 ? launch_kda<64>(a, ws, st) : launch_kda<128>(a, ws, st);
 }
 
 extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
-                             const void* b, int act, void* y, int64_t y_ts, void* stream) {
+                             const void* b, int act, void* y, int64_t y_ts, const int64_t* n_valid, void* stream) {
   MM_REQUIRE(T >= 0 && T <= 65535LL * kConvTokens && C >= 1 && C <= (1LL << 31) / 8, "short_conv: bad T=%lld or C=%lld",
              (long long)T, (long long)C);
   MM_REQUIRE(W >= 2 && W <= 8, "short_conv: kernel width %lld must be in [2, 8]", (long long)W);
@@ -1225,16 +1243,17 @@ extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, 
   const auto* wp = static_cast<const uint16_t*>(w);
   const auto* bp = static_cast<const uint16_t*>(b);
   auto* yp = static_cast<uint16_t*>(y);
+  const int64_t* nv = n_valid;
   dim3 grid(static_cast<unsigned>((C + kWave - 1) / kWave), static_cast<unsigned>((T + kConvTokens - 1) / kConvTokens));
   hipStream_t st = MM_STREAM(stream);
   switch (W) {
-    case 2: hipLaunchKernelGGL(short_conv_kernel<2>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 3: hipLaunchKernelGGL(short_conv_kernel<3>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 4: hipLaunchKernelGGL(short_conv_kernel<4>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 5: hipLaunchKernelGGL(short_conv_kernel<5>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 6: hipLaunchKernelGGL(short_conv_kernel<6>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    case 7: hipLaunchKernelGGL(short_conv_kernel<7>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
-    default: hipLaunchKernelGGL(short_conv_kernel<8>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts); break;
+    case 2: hipLaunchKernelGGL(short_conv_kernel<2>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    case 3: hipLaunchKernelGGL(short_conv_kernel<3>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    case 4: hipLaunchKernelGGL(short_conv_kernel<4>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    case 5: hipLaunchKernelGGL(short_conv_kernel<5>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    case 6: hipLaunchKernelGGL(short_conv_kernel<6>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    case 7: hipLaunchKernelGGL(short_conv_kernel<7>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
+    default: hipLaunchKernelGGL(short_conv_kernel<8>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
   }
   return mm::check_launch("short_conv");
 }

@@ -56,14 +56,17 @@ def kda_workspace(T, H, K, device):
 
 def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
                         output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
-                        lower_bound=None, inplace=False, out=None, beta_is_logits=False, workspace=None, **unused):
+                        lower_bound=None, inplace=False, out=None, beta_is_logits=False, workspace=None, n_valid=None,
+                        **unused):
     """q, k [1, T, H, K] bf16; v [1, T, H, V] bf16; g [1, T, H, K] (bf16 / fp32; the raw gate projection when
     use_gate_in_kernel, else a log decay); beta [1, T, H] (fp32 / bf16); A_log [H], dt_bias [H * K] (or [H, K]);
     initial_state [1, H, K, V] fp32 (zeros when None). Returns (o [1, T, H, V] bf16, final_state or None).
     scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor);
     beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel. workspace: from
-    kda_workspace(T, H, K) (allocated when None)."""
-    _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out, workspace)
+    kda_workspace(T, H, K) (allocated when None). n_valid: a one-element int64 device tensor n, or None: tokens
+    n .. T - 1 are padding and leave the state exactly unchanged (the engine's padded prefill, engine.py:234-256)."""
+    _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out, workspace, n_valid)
+    _check_count(n_valid, "fused_recurrent_kda")
     if q.dim() != 4 or q.shape[0] != 1:
         raise ValueError(f"fused_recurrent_kda: q must be [1, T, H, K] (got {tuple(q.shape)})")
     _, T, H, K = q.shape
@@ -113,18 +116,25 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
                                        _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,
                                        1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0,
                                        1 if beta_is_logits else 0, sc, T, H, K, V, _mm.ptr(state), _mm.ptr(o),
-                                       o.stride(0), _mm.ptr(ws), ws.numel() * 4 if ws is not None else 0,
-                                       _mm.stream_of(q)), "fused_recurrent_kda")
+                                       o.stride(0), _mm.ptr(n_valid), _mm.ptr(ws),
+                                       ws.numel() * 4 if ws is not None else 0, _mm.stream_of(q)), "fused_recurrent_kda")
     final = None
     if output_final_state or inplace:
         final = state if (inplace and initial_state is not None) else state.reshape(1, H, K, V)
     return o.reshape(1, T, H, V), final
 
 
-def short_conv(x, cache, weight, bias=None, activation="silu", out=None):
+def _check_count(n, what):
+    if n is not None and (n.dtype != torch.int64 or n.numel() != 1):
+        raise ValueError(f"{what}: n_valid must be a one-element int64 device tensor")
+
+
+def short_conv(x, cache, weight, bias=None, activation="silu", out=None, n_valid=None):
     """x [1, T, C] or [T, C] bf16; cache [1, C, W] bf16 (the last W inputs per channel, updated in place); weight
-    [C, 1, W] or [C, W] bf16; bias [C] or None. Returns y with x's shape: act(conv over the window) per token."""
-    _mm.require_gpu(x, cache, weight, bias, out)
+    [C, 1, W] or [C, W] bf16; bias [C] or None. Returns y with x's shape: act(conv over the window) per token.
+    n_valid: a one-element int64 device tensor n, or None: the cache ends on the first n tokens' inputs."""
+    _mm.require_gpu(x, cache, weight, bias, out, n_valid)
+    _check_count(n_valid, "short_conv")
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
@@ -144,7 +154,8 @@ def short_conv(x, cache, weight, bias=None, activation="silu", out=None):
     lib = _mm.load()
     with _mm.on_device(x):
         _mm.check(lib.mm_short_conv(_mm.ptr(x2), x2.stride(0), T, C, _mm.ptr(cache), W, _mm.ptr(w2), _mm.ptr(bias),
-                                    0 if activation is None else 1, _mm.ptr(y), y.stride(0), _mm.stream_of(x)),
+                                    0 if activation is None else 1, _mm.ptr(y), y.stride(0), _mm.ptr(n_valid),
+                                    _mm.stream_of(x)),
                   "short_conv")
     return y.reshape(x.shape)
 

@@ -243,11 +243,13 @@ class FastThinkerStep:
         y = F.linear(x, w, b)
         return y if residual is None else y.add_(residual)
 
-    def prompt_mixer(self, li, h):
+    def prompt_mixer(self, li, h, n_valid=None):
         """The attention half of layer li over a prompt's T rows h [T, H] at positions pos_buf .. pos_buf + T - 1:
         h + o(mixer(input_layernorm(h))). KDA: the projection, the q / k / v short convolutions (their caches end
-        on the prompt's last inputs), the f / g LoRA up-projections, fused_recurrent_kda from the layer's state (the
-        recurrent form for any T), rms_norm_gated; MLA: the q | k | v projection and mla_prefill_attn."""
+        on the prompt's last real inputs), the f / g LoRA up-projections, fused_recurrent_kda from the layer's state
+        (the recurrent form for any T; padding rows past n_valid leave it unchanged), rms_norm_gated; MLA: the
+        q | k | v projection and mla_prefill_attn (padding rows are stored past the real ones, where the next
+        decode steps overwrite them before any query reads them)."""
         p = self.L[li]
         T = h.shape[0]
         if p["kind"] == "mla":
@@ -262,7 +264,7 @@ class FastThinkerStep:
         H, K, V, R = p["heads"], p["K"], p["V"], p["rank"]
         pr = self._rows(h, p["proj"], p["proj_b"], norm=p["ln1"])
         nqk, nv = H * K, H * V
-        q, k, v = (TA.short_conv(pr[:, a:b], c, w) for (a, b), c, w in
+        q, k, v = (TA.short_conv(pr[:, a:b], c, w, n_valid=n_valid) for (a, b), c, w in
                    zip(((0, nqk), (nqk, 2 * nqk), (2 * nqk, 2 * nqk + nv)), p["conv"], p["conv_w"]))
         base = 2 * nqk + nv
         f = self._rows(pr[:, base:base + R], p["f_b"])
@@ -270,7 +272,8 @@ class FastThinkerStep:
         o, _ = TA.fused_recurrent_kda(q.view(1, T, H, K), k.view(1, T, H, K), v.view(1, T, H, V), f.view(1, T, H, K),
                                       pr[:, base + 2 * R:], A_log=p["A_log"], dt_bias=p["dt_bias"],
                                       initial_state=p["state"], inplace=True, use_qk_l2norm_in_kernel=True,
-                                      use_gate_in_kernel=True, beta_is_logits=True, lower_bound=p["lower_bound"])
+                                      use_gate_in_kernel=True, beta_is_logits=True, lower_bound=p["lower_bound"],
+                                      n_valid=n_valid)
         ow, oe = p["o_norm"]
         on = TA.rms_norm_gated(o.reshape(T * H, V), gg.reshape(T * H, V), ow, oe)
         return self._rows(on.reshape(T, H * V), p["o"], p["o_b"], residual=h)
@@ -301,27 +304,37 @@ class FastThinkerStep:
             raise ValueError("FastThinkerStep.prefill: ids must be int64 / int32 device tokens")
         return TA.embed_rows(self.embed, ids)
 
-    def prefill(self, ids=None, h=None, *, trace=False):
+    def prefill(self, ids=None, h=None, *, n_valid=None, trace=False):
         """The engine's _prefill (engine.py:921-958) of one prompt at positions pos_buf .. pos_buf + T - 1: ids
         [1, T] / [T] device token ids (word_embeddings, engine.py:922), or h [1, T, H] / [T, H] input rows (the
         embeddings with audio features merged in, engine.py:923-927). Per layer h = prompt_moe(prompt_mixer(h)),
         then logits = lm_head(norm(h[T - 1])), tok_buf = argmax(logits), pos_buf += T: the state (KDA states and
         conv caches, MLA cache rows) advances as T decode steps would advance it. Returns the last token's logits
         [1, vocab]; with trace=True also the per-layer (input, mixer output, router ids, weights) list.
-        Eager calls of one T, or a capture per prompt length (the position stays on the device)."""
+        n_valid: a one-element int64 device tensor n (the engine's prefill graphs, engine.py:716-757, 936-945: a
+        prompt padded to a bucket length T, p_valid / p_conv_idx / p_last): the first n rows are the prompt, the rest
+        padding that leaves the KDA states and conv caches as the n real tokens leave them; the logits are row
+        n - 1's and pos_buf advances by n. Eager calls, or one capture per (padded) length: the position and n stay
+        on the device, so a graph captured for T serves every prompt of up to T tokens (pos_buf + T <= max_len)."""
         h = self._prompt_rows(ids, h)
-        if h.shape[0] == 0:
+        T = h.shape[0]
+        if T == 0:
             raise ValueError("FastThinkerStep.prefill: an empty prompt")
+        if n_valid is not None and (n_valid.dtype != torch.int64 or n_valid.numel() != 1 or
+                                    n_valid.device != h.device):
+            raise ValueError("FastThinkerStep.prefill: n_valid must be a one-element int64 tensor on the device")
+        nv = None if n_valid is None else n_valid.reshape(1).clamp(0, T)
         out = []
         for li in range(len(self.L)):
             h_in = h
-            hm = self.prompt_mixer(li, h)
+            hm = self.prompt_mixer(li, h, nv)
             h, rid, rw = self.prompt_moe(li, hm)
             if trace:
                 out.append((h_in.clone(), hm.clone(), rid.clone(), rw.clone()))
-        logits = self.head_logits(h[-1:])
+        last = h[-1:] if nv is None else TA.embed_rows(h, (nv - 1).clamp_(min=0))
+        logits = self.head_logits(last)
         TA.argmax_rows(logits, out=self.tok)
-        self.pos.add_(h.shape[0])
+        self.pos.add_(T if nv is None else nv)
         return (logits, out) if trace else logits
 
     # ----------------------------------------------------------------------------------------------- step

@@ -91,6 +91,39 @@ def test_kda_zero_write_strength_keeps_the_state():
     assert torch.equal(fin, S0)
 
 
+@pytest.mark.parametrize("T,n,H,V", [(32, 20, 3, 128), (40, 33, 2, 64), (2, 1, 4, 128), (17, 0, 2, 128), (16, 16, 1, 32)])
+def test_kda_padding_tokens_leave_the_state_unchanged(T, n, H, V):
+    """A prompt padded from n to T tokens with n_valid = n (the engine's prefill graphs): the state after it and the
+    first n outputs equal those of the n-token prompt bit for bit, whatever the padding rows hold."""
+    K = 128
+    print(f"[kda pad] T={T} n={n} H={H} V={V}", flush=True)
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 600 + T)
+    beta = W.normal((1, T, H), 1.0, 610, DEV)  # logits
+    kw = dict(A_log=A_log, dt_bias=dt, inplace=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              beta_is_logits=True)
+    s_pad, s_ref = S0.clone(), S0.clone()
+    o_pad, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=s_pad,
+                                      n_valid=torch.tensor([n], device=DEV), **kw)
+    if n:
+        o_ref, _ = TA.fused_recurrent_kda(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], initial_state=s_ref,
+                                          **kw)
+        assert torch.equal(o_pad[:, :n], o_ref)
+    assert torch.equal(s_pad, s_ref)
+
+
+@pytest.mark.parametrize("T,n,C,Wd", [(40, 23, 2048, 4), (32, 2, 77, 4), (16, 0, 130, 3), (5, 5, 64, 8)])
+def test_short_conv_cache_ends_on_the_real_tokens(T, n, C, Wd):
+    x = W.normal((T, C), 1.0, 620 + T, DEV)
+    cache = W.normal((1, C, Wd), 1.0, 621, DEV)
+    w = W.normal((C, 1, Wd), 0.5, 622, DEV)
+    c_pad, c_ref = cache.clone(), cache.clone()
+    y_pad = TA.short_conv(x, c_pad, w, n_valid=torch.tensor([n], device=DEV))
+    if n:
+        y_ref = TA.short_conv(x[:n], c_ref, w)
+        assert torch.equal(y_pad[:n], y_ref)
+    assert torch.equal(c_pad, c_ref)
+
+
 @pytest.mark.parametrize("T,C,Wd", [(1, 6144, 4), (5, 6144, 4), (3, 1000, 2), (2, 77, 8), (40, 2048, 4), (17, 77, 8),
                                     (100, 130, 3), (16, 64, 4)])
 def test_short_conv_matches_oracle(T, C, Wd):
@@ -508,6 +541,81 @@ def test_fast_thinker_prefill_then_decode_follows_token_by_token_decode():
                                   y[key] if isinstance(y[key], tuple) else (y[key],)):
                     assert torch.equal(ta, tb), (i, key)
     del a, b, c, d, g, out
+    torch.cuda.empty_cache()
+
+
+def _states_close(a, b, what, rows=None, exact=False, min_cos=0.999, keys=("state", "conv", "kc", "vc")):
+    """KDA states and conv caches, and the MLA cache rows `rows` (a slice; all when None), of two state copies."""
+    for li, (x, y) in enumerate(zip(a["L"], b["L"])):
+        for key in (kk for kk in x if kk in keys):
+            for ta, tb in zip(x[key] if isinstance(x[key], tuple) else (x[key],),
+                              y[key] if isinstance(y[key], tuple) else (y[key],)):
+                if key in ("kc", "vc") and rows is not None:
+                    ta, tb = ta[:, :, rows], tb[:, :, rows]
+                if exact:
+                    assert torch.equal(ta, tb), (what, li, key)
+                    continue
+                c = float(F.cosine_similarity(ta.float().reshape(-1), tb.float().reshape(-1), dim=0))
+                assert c > min_cos, (what, li, key, c)
+
+
+def test_fast_thinker_prefill_graph_for_a_bucket_serves_shorter_prompts():
+    """The engine's prefill graphs (engine.py:716-757, 936-945): one capture for a 32-token bucket, replayed for
+    prompts of 20, 7 and 32 tokens padded with token 0 (n_valid on the device), against eager prefills of the
+    unpadded prompts on an identical model: the same position and next token, the layer states and logits
+    agree (bit for bit at the full length, to the bf16 level otherwise: the projection GEMMs see another row count)."""
+    Tb, pos = 32, 300
+    a = W.HybridThinkerStep(4, DEV, pos=pos, seed=7500)
+    b = W.HybridThinkerStep(4, DEV, pos=pos, seed=7500)
+    vocab = a.embed.shape[0]
+    prompt = torch.randint(0, vocab, (Tb,), generator=torch.Generator().manual_seed(11)).to(DEV)
+    ids = torch.zeros(Tb, device=DEV, dtype=torch.long)
+    nv = torch.tensor([Tb], device=DEV)
+    ids.copy_(prompt)
+    a.fast.prefill(ids, n_valid=nv)  # warm-up on both models, which stay identical
+    b.fast.prefill(prompt)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        logits = a.fast.prefill(ids, n_valid=nv)
+    torch.cuda.synchronize()
+    for n in (20, 7, 32):
+        print(f"[hybrid prefill bucket] n={n} of {Tb}", flush=True)
+        p = torch.randint(0, vocab, (n,), generator=torch.Generator().manual_seed(100 + n)).to(DEV)
+        ids.zero_()
+        ids[:n] = p
+        nv.fill_(n)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = b.fast.prefill(p)
+        torch.cuda.synchronize()
+        sa, sb = a.state_copy(), b.state_copy()
+        p0 = int(sa["pos"]) - n
+        assert int(sa["pos"]) == int(sb["pos"])
+        if n == Tb:
+            assert torch.equal(logits, want) and int(a.tok) == int(b.tok)
+            _states_close(sa, sb, n, exact=True)
+        else:
+            c = float(F.cosine_similarity(logits.float().reshape(-1), want.float().reshape(-1), dim=0))
+            assert c > 0.999, (n, c)
+            _states_close(sa, sb, n, rows=slice(0, p0 + n))  # rows past the prompt hold the padding in a
+            _states_close(sa, sb, n, rows=slice(p0 + Tb, None), exact=True, keys=("kc", "vc"))
+        # the next decode steps write over the padding rows of the MLA caches before any query reads them
+        a.tok.copy_(b.tok)
+        for key in ("kc", "vc"):
+            for pa, pb in zip(a.L, b.L):
+                if key in pa:
+                    pa[key].copy_(pb[key])
+        for pa, pb in zip(a.L, b.L):  # realign the two models for the next prompt
+            for key in ("state", "conv"):
+                if key in pa:
+                    for ta, tb in zip(pa[key] if isinstance(pa[key], tuple) else (pa[key],),
+                                      pb[key] if isinstance(pb[key], tuple) else (pb[key],)):
+                        ta.copy_(tb)
+    del a, b, g
     torch.cuda.empty_cache()
 
 
