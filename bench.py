@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline line only (no extra workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run (decode,int8,zipf,full,hybrid,talker,ingest)")
+                    help="comma list of extra workloads to run (decode,int8,zipf,full,hybrid,hybrid_prefill,talker,ingest)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the rocprofv3 counter passes (traffic = null)")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
@@ -744,6 +744,7 @@ def main():
     if want("hybrid"):
         extra["hybrid_decode_28l"] = hybrid_decode_metrics(stream)
         log(f"[bench] hybrid decode: {extra['hybrid_decode_28l']}")
+    if want("hybrid") or want("hybrid_prefill"):
         extra["hybrid_prefill_28l"] = hybrid_prefill_metrics(stream)
         log(f"[bench] hybrid prefill: {extra['hybrid_prefill_28l']}")
     if want("talker"):

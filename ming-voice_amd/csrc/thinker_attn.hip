@@ -378,10 +378,18 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
   float wt[W], in[kConvTokens + W - 1];  // inputs t0 - W + 1 .. t0 + 15
 #pragma unroll
   for (int j = 0; j < W; ++j) wt[j] = bf16_to_f32(w[ch * W + j]);
+  // every load unconditional (rows clamped into range, the value chosen after), so they all issue before the
+  // first wait
 #pragma unroll
   for (int i = 0; i < kConvTokens + W - 1; ++i) {
     const int t = t0 - (W - 1) + i;
-    in[i] = t < 0 ? bf16_to_f32(cache[ch * W + W + t]) : t < T ? bf16_to_f32(x[t * xs + ch]) : 0.f;
+    const float xv = bf16_to_f32(x[static_cast<int64_t>(t < 0 ? 0 : t < T ? t : T - 1) * xs + ch]);
+    if (i < W - 1) {  // only these can precede the prompt (chunk 0)
+      const float cv = bf16_to_f32(cache[ch * W + W + (t < 0 ? t : -1)]);
+      in[i] = t < 0 ? cv : t < T ? xv : 0.f;
+    } else {
+      in[i] = t < T ? xv : 0.f;
+    }
   }
   const float bias = b ? bf16_to_f32(b[ch]) : 0.f;
 #pragma unroll
@@ -403,7 +411,9 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
 #pragma unroll
     for (int j = 0; j < W; ++j) {
       const int t = nv - W + j;
-      nw[j] = t < 0 ? cache[ch * W + W + t] : x[t * xs + ch];
+      const uint16_t cv = cache[ch * W + (t < 0 ? W + t : j)];
+      const uint16_t xv = x[static_cast<int64_t>(t < 0 ? 0 : t) * xs + ch];
+      nw[j] = t < 0 ? cv : xv;
     }
 #pragma unroll
     for (int j = 0; j < W; ++j) cache[ch * W + j] = nw[j];
@@ -973,9 +983,9 @@ constexpr int kMlaPVtRow = 36;  // bf16 per transposed value row in LDS: 32 keys
 
 // Causal attention of T prompt tokens over the static cache (the new rows already stored): token t at position
 // pos + t takes softmax(scale q_t . K[0..pos+t]^T) . V[0..pos+t] (engine.py:679-682's mask). Grid (T / 16,
-// nh) x 4 waves: a workgroup holds 16 queries of one head, and its waves take the 32-key tiles round robin
-// (wave w: tiles w, w + 4, ...), each keeping its own running max, sum and output for the 16 queries; the four
-// are merged through LDS at the end. Per tile, on the 16x16x32 bf16 MFMA:
+// nh) x NW waves (8 when the grid is small, else 4): a workgroup holds 16 queries of one head, and its waves take
+// the 32-key tiles round robin (wave w: tiles w, w + NW, ...), each keeping its own running max, sum and output for
+// the 16 queries; they are merged through LDS at the end. Per tile, on the 16x16x32 bf16 MFMA:
 //   S^T [32 keys, 16 queries] = K Q^T, the key rows read straight from the cache into A fragments and the
 //     queries held as B fragments (lane: query lane % 16, dims 32 kk + 8 (lane / 16) .. + 7);
 //   the masked softmax update per query is lane-local (a lane of the S^T tiles holds 8 keys of its query
@@ -986,21 +996,21 @@ constexpr int kMlaPVtRow = 36;  // bf16 per transposed value row in LDS: 32 keys
 // O^T's lane layout (dims 4 (lane / 16) + v of each 16-dim tile, query lane % 16) keeps the rescaling by the
 // query's exp(m_old - m_new) lane-local as well. Keys past the block's last query are not read (zeros, then
 // masked); queries past T repeat the last token and are not stored. A prompt outside [0, max_len) writes NaN.
-template <int NT>  // dv <= 16 NT
-__global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a) {
+template <int NT, int NW>  // dv <= 16 NT; NW waves per workgroup
+__global__ __launch_bounds__(NW * 64) void mla_prefill_attn_kernel(MlaPrefillArgs a) {
   constexpr int DVM = 16 * NT;
   constexpr int VT_BYTES = DVM * kMlaPVtRow * 2;
   constexpr int MERGE_BYTES = 16 * DVM * 4;  // the wave's O [16 queries][DVM] fp32
   constexpr int WAVE_BYTES = VT_BYTES > MERGE_BYTES ? VT_BYTES : MERGE_BYTES;
-  __shared__ __align__(16) char s_buf[4 * WAVE_BYTES];
-  __shared__ float s_m[4][16], s_l[4][16];
+  __shared__ __align__(16) char s_buf[NW * WAVE_BYTES];
+  __shared__ float s_m[NW][16], s_l[NW][16];
   const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int lr = lane & 15, lq = lane >> 4;
   const int h = blockIdx.y, tq0 = blockIdx.x * 16;
   const int64_t pos = load_pos64(a.pos, a.pos_dtype);
   const int n4 = a.dv / 4;
   if (!mla_prefill_pos_ok(a, pos)) {  // uniform over the workgroup
-    for (int i = tid; i < 16 * a.dv; i += 256) {
+    for (int i = tid; i < 16 * a.dv; i += NW * kWave) {
       const int t = tq0 + i / a.dv;
       if (t < a.T) a.out[t * a.out_ts + static_cast<int64_t>(h) * a.dv + i % a.dv] = 0x7fc0;  // NaN
     }
@@ -1031,7 +1041,7 @@ __global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a)
   const int64_t hk = static_cast<int64_t>(h) * a.max_len;
   constexpr int RV = (DVM + 31) / 32;  // value pieces (2 keys x 8 dims) per lane: 16 key pairs x dv / 8 groups
   const int ndg = a.dv / 8;
-  for (int kt = wave; kt < ntiles; kt += 4) {
+  for (int kt = wave; kt < ntiles; kt += NW) {
     const int64_t j0 = static_cast<int64_t>(kt) * kMlaPKeys;
     // value tile: lane piece i = lane + 64 r -> key pair kp = i % 16, dim group dg = i / 16
     uint4 va[RV], vb[RV];
@@ -1130,14 +1140,16 @@ __global__ __launch_bounds__(256) void mla_prefill_attn_kernel(MlaPrefillArgs a)
     s_l[wave][lr] = l;
   }
   __syncthreads();
-  for (int i = tid; i < 16 * n4; i += 256) {
+  for (int i = tid; i < 16 * n4; i += NW * kWave) {
     const int qi = i / n4, d = 4 * (i % n4), t = tq0 + qi;
     if (t >= a.T) continue;
-    const float mx = fmaxf(fmaxf(s_m[0][qi], s_m[1][qi]), fmaxf(s_m[2][qi], s_m[3][qi]));  // finite: key 0
+    float mx = s_m[0][qi];  // finite: wave 0 holds key 0
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_m[w][qi]);
     float lt = 0.f;
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float wt = __expf(s_m[w][qi] - mx);
       lt = fmaf(s_l[w][qi], wt, lt);
       acc += wt * *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(s_buf + w * WAVE_BYTES) +
@@ -1417,7 +1429,14 @@ extern "C" int mm_mla_prefill_attn(const void* q, int64_t q_ts, const void* k_ne
   int rc = mm::check_launch("mla_prefill_attn store");
   if (rc) return rc;
   const dim3 grid(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>(nh));
-  if (dv <= 64) hipLaunchKernelGGL(mla_prefill_attn_kernel<4>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(mla_prefill_attn_kernel<8>, grid, dim3(256), 0, st, a);
+  // fewer workgroups than two per CU: 8 waves each, so that each wave walks half as many key tiles
+  const bool wide = static_cast<int64_t>(grid.x) * grid.y < 2 * mm::cu_count();
+  if (dv <= 64) {
+    if (wide) hipLaunchKernelGGL((mla_prefill_attn_kernel<4, 8>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((mla_prefill_attn_kernel<4, 4>), grid, dim3(256), 0, st, a);
+  } else {
+    if (wide) hipLaunchKernelGGL((mla_prefill_attn_kernel<8, 8>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((mla_prefill_attn_kernel<8, 4>), grid, dim3(256), 0, st, a);
+  }
   return mm::check_launch("mla_prefill_attn");
 }

@@ -234,12 +234,14 @@ class FastThinkerStep:
     @staticmethod
     def _rows(x, w, b=None, residual=None, norm=None):
         """A projection of T rows: up to fastlinear.MAX_M rows on the small_linear GEMV (norm and residual fused),
-        more as rms_norm (HIP) -> the library GEMM (torch's linear on hipBLASLt) -> + residual, the form of the
-        reference's own prefill (nn.Linear after the patched norm, engine.py:220-228)."""
+        more as rms_norm (HIP) -> the library GEMM (hipBLASLt through torch; the residual, without a bias, as its C
+        operand), the form of the reference's own prefill (nn.Linear after the patched norm, engine.py:220-228)."""
         if x.shape[0] <= fastlinear.MAX_M:
             return fastlinear.small_linear(x, w, b=b, residual=residual, norm=norm)
         if norm is not None:
             x = fused_ops.rms_norm(x, norm[0], norm[1])
+        if residual is not None and b is None:
+            return torch.addmm(residual, x, w.t())
         y = F.linear(x, w, b)
         return y if residual is None else y.add_(residual)
 

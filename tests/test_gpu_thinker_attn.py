@@ -231,10 +231,12 @@ def _prompt(nh, dq, dv, T, seed, packed=False):
 @pytest.mark.parametrize("nh,dq,dv,L,T,pos,packed", [
     (16, 192, 128, 1024, 128, 512, True), (16, 192, 128, 1024, 17, 0, False), (4, 64, 64, 300, 33, 31, False),
     (2, 96, 32, 70, 70, 0, True), (3, 72, 40, 100, 5, 95, False), (1, 8, 8, 40, 1, 7, False),
-    (2, 256, 128, 600, 300, 200, True), (2, 200, 48, 64, 16, 16, False), (1, 32, 16, 2100, 64, 2000, False)])
+    (2, 256, 128, 600, 300, 200, True), (2, 200, 48, 64, 16, 16, False), (1, 32, 16, 2100, 64, 2000, False),
+    (16, 192, 128, 1100, 520, 300, False), (16, 64, 64, 700, 530, 100, True)])
 def test_mla_prefill_attn_matches_oracle(nh, dq, dv, L, T, pos, packed):
     """Prompts at the cache start and end, lengths off the 16-query and 32-key tiles, head dims off the 32-wide
-    MFMA step, and q / k / v as column slices of a projection output."""
+    MFMA step, and q / k / v as column slices of a projection output; grids of 512 workgroups and more (the last
+    two) take 4 waves per workgroup, smaller ones 8."""
     print(f"[mla prefill] nh={nh} dq={dq} dv={dv} L={L} T={T} pos={pos} packed={packed}", flush=True)
     kc = W.normal((1, nh, L, dq), 1.0, 500, DEV)
     vc = W.normal((1, nh, L, dv), 1.0, 501, DEV)
