@@ -307,7 +307,7 @@ int mm_silu_mul(const void* gu, int64_t rows, int64_t inter, int64_t gu_row_stri
  * mm_kda_recurrent_workspace(T, H, K) bytes, 16-byte aligned (the per-token inputs prepared for all tokens at once,
  * then read by the sequential part); T <= 2 (a decode step) runs in one launch and needs none (NULL allowed).
  * n_valid: NULL, or an int64 device scalar n: tokens n .. T - 1 are padding and leave the state exactly unchanged
- * (decay 1, write strength 0: the padded prefill of engine.py:234-256, where the gate is -1e30 and beta 0); their
+ * (decay 1, write strength 0: the padded prefill of engine.py:252-253, where the gate is -1e30 and beta 0); their
  * outputs are unspecified. */
 int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
                      const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
@@ -323,7 +323,7 @@ int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K);
  * (cache[ch, 1..W-1], x[t, ch]) replaces the cache and y[t, ch] = act(sum_j w[ch, j] * window[j] + b[ch]) (act 1:
  * SiLU, 0: none; fp32, one rounding). x, y [T, C] bf16 with token strides; cache [C, W], w [C, W] (a conv1d weight
  * [C, 1, W]) bf16; b [C] bf16 or NULL. 2 <= W <= 8. n_valid: NULL, or an int64 device scalar n: the cache ends on
- * the first n tokens' inputs (the padded prefill's conv_idx, engine.py:254-256); every y row is still computed. */
+ * the first n tokens' inputs (the padded prefill's conv_idx, engine.py:261-262); every y row is still computed. */
 int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
                   const void* b, int act, void* y, int64_t y_ts, const int64_t* n_valid, void* stream);
 
@@ -362,7 +362,7 @@ int mm_mla_decode_attn(const void* q, const void* k_new, const void* v_new, int 
                        void* v_cache, int64_t max_len, const void* pos, int pos_dtype, float scale, void* out,
                        void* workspace, int64_t workspace_bytes, void* stream);
 
-/* The T tokens of a prompt through an MLA layer's attention (engine.py:936-958 prefill: the StaticHybridCache
+/* The T tokens of a prompt through an MLA layer's attention (engine.py:938-972 prefill: the StaticHybridCache
  * index_copy_ of engine.py:537-541 at positions pos .. pos + T - 1, then the causal attention of the mask at
  * engine.py:679-682): token t's k_new / v_new rows go to cache row pos + t of k_cache [nh, max_len, dqk] and
  * v_cache [nh, max_len, dv] (bf16), then out_t[h] = softmax(scale * q_t[h] . K[h, 0..pos+t]^T) . V[h, 0..pos+t],

@@ -60,7 +60,7 @@ struct KdaArgs {
 };
 
 // The prompt's real tokens: the first n_valid (clamped to [0, T]) when given, else all T. A padding token leaves the
-// state exactly as it is: its decay is 1 and its write strength 0 (engine.py:234-256's padded prefill).
+// state exactly as it is: its decay is 1 and its write strength 0 (engine.py:252-253, the padded prefill).
 __device__ __forceinline__ int kda_valid(const KdaArgs& a) {
   if (!a.n_valid) return a.T;
   const int64_t n = *a.n_valid;
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
   }
   if (blockIdx.y == 0) {
     // the window after the prompt's real tokens (the first n_valid, clamped to [0, T], when given: the padded
-    // prefill's conv_idx, engine.py:254-256): inputs nv - W .. nv - 1, from the old cache where they precede it
+    // prefill's conv_idx, engine.py:261-262): inputs nv - W .. nv - 1, from the old cache where they precede it
     int nv = T;
     if (n_valid) nv = static_cast<int>(*n_valid < 0 ? 0 : *n_valid > T ? T : *n_valid);
     uint16_t nw[W];

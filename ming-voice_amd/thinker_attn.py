@@ -11,7 +11,7 @@ decode token, or a prompt's tokens).
   mla_decode_attn       one token of an MLA layer: the StaticHybridCache update at pos (engine.py:537-548) and the
                         masked softmax attention over positions 0..pos
   mla_prefill_attn      the T tokens of a prompt through an MLA layer: the update at pos .. pos + T - 1 and the
-                        causal attention, token t over positions 0..pos+t (engine.py:936-958)
+                        causal attention, token t over positions 0..pos+t (engine.py:938-972)
   embed_rows            word_embeddings(tok_buf), the input row of a decode step (engine.py:686)
   argmax_rows           logits.argmax(-1), the greedy pick a decode step writes back (engine.py:688)
 Every call enqueues on torch's current stream and can be captured in a hipGraph (the workspace and outputs can be
@@ -64,7 +64,7 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     scale defaults to K ** -0.5. inplace=True updates initial_state itself (final_state is then that tensor);
     beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel. workspace: from
     kda_workspace(T, H, K) (allocated when None). n_valid: a one-element int64 device tensor n, or None: tokens
-    n .. T - 1 are padding and leave the state exactly unchanged (the engine's padded prefill, engine.py:234-256)."""
+    n .. T - 1 are padding and leave the state exactly unchanged (the engine's padded prefill, engine.py:252-253)."""
     _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out, workspace, n_valid)
     _check_count(n_valid, "fused_recurrent_kda")
     if q.dim() != 4 or q.shape[0] != 1:
@@ -299,7 +299,7 @@ def _token_rows(t, T, n, name):
 
 
 def mla_prefill_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None):
-    """T prompt tokens of an MLA layer (the engine's prefill over the static cache, engine.py:936-958, 537-541,
+    """T prompt tokens of an MLA layer (the engine's prefill over the static cache, engine.py:938-972, 537-541,
     679-682). q, k_new: T tokens of [nh, dqk] ([T, nh * dqk], [1, T, nh, dqk], or column slices of a projection
     output); v_new: T tokens of [nh, dv]; k_cache [1, nh, max_len, dqk], v_cache [1, nh, max_len, dv] (bf16);
     pos: a one-element int64 / int32 device tensor, the first token's position. Writes the new rows at

@@ -1,4 +1,5 @@
-"""The hybrid thinker's greedy decode step (engine.py:665-689) on this build's kernels, built from the engine's objects.
+"""The hybrid thinker's greedy decode step (engine.py:665-689) and its prefill (engine.py:938-972, with the padded
+prefill graphs of engine.py:716-757) on this build's kernels, built from the engine's objects.
 
 FastThinkerStep(model, cache_layers, tok_buf, pos_buf) takes what engine.Thinker holds once it is loaded and patched
 (engine.py:570-660): `model` is Thinker.model, `cache_layers` Thinker._layers, `tok_buf` / `pos_buf` its [1, 1] token
@@ -34,6 +35,11 @@ them fused with the input norm, with no rotary part (the synthetic thinker of th
 
 Every call enqueues on torch's current stream and can be captured in one hipGraph (engine.py:694-713); the state
 lives in the engine's own buffers, so replays advance it as the engine's decode graphs do.
+
+A prefill (FastThinkerStep.prefill) runs the same layers over a prompt's T rows: the projections as GEMMs, the KDA
+recurrence over the T tokens from the layer's state, the MLA layers' causal attention over the cache (rows stored at
+pos .. pos + T - 1), the prefill MoE block, then the head on the last real row; with n_valid on the device, one
+capture per bucket length serves shorter prompts padded to it.
 """
 import torch
 import torch.nn.functional as F
@@ -307,13 +313,13 @@ class FastThinkerStep:
         return TA.embed_rows(self.embed, ids)
 
     def prefill(self, ids=None, h=None, *, n_valid=None, trace=False):
-        """The engine's _prefill (engine.py:921-958) of one prompt at positions pos_buf .. pos_buf + T - 1: ids
-        [1, T] / [T] device token ids (word_embeddings, engine.py:922), or h [1, T, H] / [T, H] input rows (the
-        embeddings with audio features merged in, engine.py:923-927). Per layer h = prompt_moe(prompt_mixer(h)),
+        """The engine's _prefill (engine.py:938-972) of one prompt at positions pos_buf .. pos_buf + T - 1: ids
+        [1, T] / [T] device token ids (word_embeddings, engine.py:940), or h [1, T, H] / [T, H] input rows (the
+        embeddings with audio features merged in, engine.py:941-944). Per layer h = prompt_moe(prompt_mixer(h)),
         then logits = lm_head(norm(h[T - 1])), tok_buf = argmax(logits), pos_buf += T: the state (KDA states and
         conv caches, MLA cache rows) advances as T decode steps would advance it. Returns the last token's logits
         [1, vocab]; with trace=True also the per-layer (input, mixer output, router ids, weights) list.
-        n_valid: a one-element int64 device tensor n (the engine's prefill graphs, engine.py:716-757, 936-945: a
+        n_valid: a one-element int64 device tensor n (the engine's prefill graphs, engine.py:716-757, 950-961: a
         prompt padded to a bucket length T, p_valid / p_conv_idx / p_last): the first n rows are the prompt, the rest
         padding that leaves the KDA states and conv caches as the n real tokens leave them; the logits are row
         n - 1's and pos_buf advances by n. Eager calls, or one capture per (padded) length: the position and n stay

@@ -100,7 +100,7 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None):
 
 
 def mla_prefill_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None):
-    """The T tokens of a prompt through an MLA layer (engine.py:936-958 over the static cache): the caches [nh, L, d]
+    """The T tokens of a prompt through an MLA layer (engine.py:938-972 over the static cache): the caches [nh, L, d]
     take k_new[t] / v_new[t] ([T, nh, d]) at rows pos + t (engine.py:537-541), then token t attends to rows
     0 .. pos + t (the causal mask of engine.py:679-682): out[t, h] = softmax(scale * q[t, h] . K[h, :pos+t+1]^T) .
     V[h, :pos+t+1]. Returns (out [T, nh, dv], k_cache, v_cache), float64 (caches in their dtype)."""

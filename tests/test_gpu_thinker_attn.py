@@ -562,7 +562,7 @@ def _states_close(a, b, what, rows=None, exact=False, min_cos=0.999, keys=("stat
 
 
 def test_fast_thinker_prefill_graph_for_a_bucket_serves_shorter_prompts():
-    """The engine's prefill graphs (engine.py:716-757, 936-945): one capture for a 32-token bucket, replayed for
+    """The engine's prefill graphs (engine.py:716-757, 950-961): one capture for a 32-token bucket, replayed for
     prompts of 20, 7 and 32 tokens padded with token 0 (n_valid on the device), against eager prefills of the
     unpadded prompts on an identical model: the same position and next token, the layer states and logits
     agree (bit for bit at the full length, to the bf16 level otherwise: the projection GEMMs see another row count)."""
