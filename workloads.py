@@ -1,4 +1,5 @@
-"""Seeded synthetic inputs of the thinker MoE block and the composed block forward.
+"""Seeded synthetic inputs of the thinker MoE block and the composed block forward: the harness of bench.py, the GPU
+tests and the smoke run, outside the product package (ming-voice_amd/ never imports it).
 
 Shapes of the benchmarked block (a Ling-lite-like thinker): hidden 2048, 64 routed experts of
 intermediate 1408 plus one always-on shared expert (slot 64), softmax top-6 router. Weights ~ N(0, 0.02)
