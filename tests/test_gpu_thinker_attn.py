@@ -791,3 +791,44 @@ def test_fast_thinker_step_from_engine_objects_sigmoid_router_and_int8():
         assert torch.equal(ids, i2) and torch.equal(wts, w2), li
         nxt = trace[li + 1][0] if li + 1 < len(trace) else out
         assert torch.equal(nxt, y), li
+
+
+def test_fast_thinker_prefill_from_engine_objects_sigmoid_router_and_int8():
+    """FastThinkerStep.prefill on engine-shaped objects with the thinker's own router (sigmoid + expert bias, 8
+    groups, top 4 groups, scale 2.5) and int8 experts on one layer, a 40-token prompt: each layer's MoE half equals
+    rms_norm -> route -> fused_moe_prefill(residual) on the layer's own input bit for bit (ids, weights, outputs),
+    and the prefill writes the last row's argmax back and advances the position by 40."""
+    import fused_moe
+    import fused_ops
+    import thinker_step
+    print("[thinker_step] prefill, engine objects, sigmoid router, int8 layer", flush=True)
+    T = 40
+    h = W.HybridThinkerStep(4, DEV, pos=50, seed=7600)
+    E = W.EXPERTS
+    for li, layer in enumerate(h.model.model.layers):
+        g = layer.mlp.gate
+        g.expert_bias = W.normal((E,), 0.05, 7700 + li, DEV, dtype=torch.float32)
+        g.n_group, g.topk_group, g.routed_scaling_factor = 8, 4, 2.5
+    int8_layer = h.model.model.layers[2]
+    q_gu, s_gu = fused_moe.quantize_rows_int8(int8_layer.mlp.w_gu, scale_dtype=torch.float32)
+    q_d, s_d = fused_moe.quantize_rows_int8(int8_layer.mlp.w_d, scale_dtype=torch.float32)
+    int8_layer.mlp.w_gu = int8_layer.mlp.w_d = None
+    int8_layer.mlp.q_gu, int8_layer.mlp.q_d, int8_layer.mlp.s_gu, int8_layer.mlp.s_d = q_gu, q_d, s_gu, s_d
+    step = thinker_step.FastThinkerStep(h.model, h.cache_layers, h.tok, h.pos, scoring="sigmoid")
+    ids = torch.randint(0, h.embed.shape[0], (T,), generator=torch.Generator().manual_seed(21)).to(DEV)
+    logits, trace = step.prefill(ids, trace=True)
+    assert int(h.pos) == 50 + T and int(h.tok) == int(logits.float().cpu().argmax())
+    for li, (layer, (h_in, hm, rid, rw)) in enumerate(zip(h.model.model.layers, trace)):
+        mlp, g = layer.mlp, layer.mlp.gate
+        xn = fused_ops.rms_norm(hm, layer.post_attention_layernorm.weight, W.EPS)
+        i2, w2, _ = fused_ops.route(xn, g.w32, g.expert_bias, top_k=W.TOP_K, scoring="sigmoid", n_group=8,
+                                    topk_group=4, scale=2.5)
+        assert torch.equal(rid, i2.long()) and torch.equal(rw, w2), li
+        if mlp.w_gu is not None:
+            y = fused_moe.fused_moe_prefill(xn, mlp.w_gu, mlp.w_d, i2, w2, residual=hm)
+        else:
+            y = fused_moe.fused_moe_prefill(xn, mlp.q_gu, mlp.q_d, i2, w2, s_gu=mlp.s_gu, s_d=mlp.s_d, residual=hm)
+        if li + 1 < len(trace):
+            assert torch.equal(trace[li + 1][0], y), li
+    del h, step
+    torch.cuda.empty_cache()
