@@ -77,6 +77,11 @@ __device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log
 constexpr int kKdaCols = 16;   // value columns per workgroup of kda_short_kernel and kda_token_kernel
 constexpr int kKdaChunk = 16;  // tokens kda_recurrent_kernel stages in LDS at a time
 constexpr int kKdaShortT = 2;  // prompts up to this long take kda_short_kernel (one launch, no workspace)
+// kda_recurrent_kernel's shape: 4 state rows per lane, 4 waves per workgroup. At 16 heads of 128 x 128 that is 256
+// workgroups of 4 waves, one per CU and one wave per SIMD (graph-timed over 21 states, 512 / 128 / 16 tokens:
+// 114 / 36 / 11 us per call, against 146 / 44 / 13 with 8 rows per lane and one wave per workgroup, 125-133 / 38-41
+// with 8 rows and 2 or 4 waves or 4 rows and 2 waves).
+constexpr int kKdaRpl = 4, kKdaNwb = 4;
 
 // Prompts of up to kKdaShortT tokens (a decode step) in one launch, without the workspace: grid (V / 16, H) x 256
 // threads; each value column of the recurrence is independent (u and o of column v read
@@ -246,95 +251,111 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
   }
 }
 
-// One wave per (64 / (K / 8) value columns, head): grid (V / CPW, H) x 64 threads. Each value column of the
-// recurrence is independent (u and o of column v read only column v of S), so lane (c = lane / RG, rg = lane % RG,
-// RG = K / 8 row groups) holds the 8 state rows 8 rg .. 8 rg + 7 of column CPW blockIdx.x + c in registers for
-// the whole prompt, and the sums over k are lane-internal, then over the RG lanes of a column by DPP (no LDS, no
-// barrier). The prepared rows of the head come into LDS 16 tokens at a time by global_load_lds, two chunk
-// buffers deep (the next chunk loads while the recurrence runs on this one), and each token's 24 inputs of a lane
-// are read from LDS within the chunk's unrolled token steps. A wave's LDS traffic is ordered by the wave alone.
+// NWB waves per (NWB CPW value columns, head): grid (V / (NWB CPW), H) x 64 NWB threads, CPW = 64 / RG with
+// RG = K / RPL row groups. Each value column of the recurrence is independent (u and o of column v read only column
+// v of S), so lane (c = lane / RG, rg = lane % RG) holds the RPL state rows rg RPL .. rg RPL + RPL - 1 of one
+// column in registers for the whole prompt, and the sums over k are lane-internal, then over the RG lanes of a
+// column (DPP steps, and one swizzle across rows of 16 lanes when RG = 32). The prepared rows of the head come into
+// LDS 16 tokens at a time by global_load_lds, shared by the workgroup's waves and two chunk buffers deep (the
+// next chunk loads while the recurrence runs on this one; one barrier per chunk), and each token's inputs of a lane
+// are read from LDS within the chunk's unrolled token steps.
 // Per token the two sums over k, k . S and q . S of the decayed state, are independent (pairwise within the
-// lane, then their DPP steps interleaved), since o = S'^T q with S' = S + k u^T is q . S + u (q . k), q . k from
-// the workspace: the token's latency is one chain of sums, not two.
-template <int K>
-__global__ __launch_bounds__(64) void kda_recurrent_kernel(KdaArgs a, const float* __restrict__ ws) {
-  constexpr int RG = K / 8, CPW = kWave / RG, ROW = kda_ws_row<K>();
+// lane, then their cross-lane steps interleaved), since o = S'^T q with S' = S + k u^T is q . S + u (q . k), q . k
+// from the workspace: the token's latency is one chain of sums, not two.
+template <int K, int RPL, int NWB>
+__global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, const float* __restrict__ ws) {
+  constexpr int RG = K / RPL, CPW = kWave / RG, COLS = NWB * CPW, ROW = kda_ws_row<K>();
+  constexpr int NT = NWB * kWave;
   constexpr int CHUNK_UNITS = kKdaChunk * ROW / 4;  // 16-byte pieces of a chunk
-  constexpr int NU = (CHUNK_UNITS + kWave - 1) / kWave;
+  constexpr int NU = (CHUNK_UNITS + NT - 1) / NT;
   constexpr int ROW_UNITS = ROW / 4;
+  constexpr int VPT = (kKdaChunk * COLS + NT - 1) / NT;  // v values per thread per chunk
   static_assert(K == 64 || K == 128, "kda key dim");
+  static_assert(RPL % 4 == 0 && RG <= kWave && (RG & (RG - 1)) == 0, "rows per lane");
   static_assert(ROW % 4 == 0, "16-byte workspace rows");
   __shared__ __align__(16) float s_in[2][kKdaChunk * ROW];
-  __shared__ float s_v[kKdaChunk][CPW];
-  const int h = blockIdx.y, lane = lane_id();
+  __shared__ float s_v[kKdaChunk][COLS];
+  const int h = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int c = lane / RG, rg = lane % RG;
   const int64_t V = a.V;
-  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * CPW;
-  float* st = a.state + static_cast<int64_t>(h) * K * V + col0 + c;
-  float S[8];
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * COLS;
+  const int cw = wave * CPW + c;  // the lane's column within the workgroup
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col0 + cw;
+  float S[RPL];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) S[i] = st[static_cast<int64_t>(8 * rg + i) * V];
+  for (int i = 0; i < RPL; ++i) S[i] = st[static_cast<int64_t>(RPL * rg + i) * V];
   const float* wsh = ws + static_cast<int64_t>(h) * ROW;
   const int64_t ts = static_cast<int64_t>(a.H) * ROW;  // workspace token stride
-  constexpr int VPL = kKdaChunk * CPW / kWave;        // v values per lane per chunk
-  float rv[VPL];
+  float rv[VPT];
   auto issue = [&](int c0, int b) {
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
-      const int u = lane + kWave * j, tt = u / ROW_UNITS;
+      const int u = tid + NT * j, tt = u / ROW_UNITS;
       if (u < CHUNK_UNITS && c0 + tt < a.T)
-        load_lds16(wsh + (c0 + tt) * ts + (u % ROW_UNITS) * 4, reinterpret_cast<char*>(s_in[b]) + j * kWave * 16);
+        load_lds16(wsh + (c0 + tt) * ts + (u % ROW_UNITS) * 4,
+                   reinterpret_cast<char*>(s_in[b]) + (wave * kWave + NT * j) * 16);
     }
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int i = lane + kWave * j, tt = c0 + i / CPW;
-      rv[j] = tt < a.T ? bf16_to_f32(a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % CPW]) : 0.f;
+    for (int j = 0; j < VPT; ++j) {
+      const int i = tid + NT * j, tt = c0 + i / COLS;
+      rv[j] = i < kKdaChunk * COLS && tt < a.T
+                  ? bf16_to_f32(a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % COLS]) : 0.f;
     }
   };
   issue(0, 0);
   for (int c0 = 0, b = 0; c0 < a.T; c0 += kKdaChunk, b ^= 1) {
-    wait_vmcnt<0>();  // this chunk's loads (and the stores before them)
+    wait_vmcnt<0>();  // this wave's loads of the chunk (and the stores before them)
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int i = lane + kWave * j;
-      s_v[i / CPW][i % CPW] = rv[j];
+    for (int j = 0; j < VPT; ++j) {
+      const int i = tid + NT * j;
+      if (i < kKdaChunk * COLS) s_v[i / COLS][i % COLS] = rv[j];
     }
-    wave_lds_fence();
+    // every wave's loads of this chunk are in LDS, and every wave is done with the other buffer
+    if constexpr (NWB == 1) wave_lds_fence(); else __syncthreads();
     if (c0 + kKdaChunk < a.T) issue(c0 + kKdaChunk, b ^ 1);  // in flight during the recurrence below
     const int n = min(kKdaChunk, a.T - c0);
-    const float* base = s_in[b] + 8 * rg;
+    const float* base = s_in[b] + RPL * rg;
     // lane (c, rg) keeps the output of tokens rg, rg + RG, ... of the chunk (every lane of a column holds each
     // token's sum) and stores them after the chunk: the token steps have no branch
-    constexpr int OPL = kKdaChunk / RG;
+    constexpr int OPL = (kKdaChunk + RG - 1) / RG;
     float keep[OPL];
 #pragma unroll
     for (int j = 0; j < OPL; ++j) keep[j] = 0.f;
     auto step = [&](int t) {
       const float* r = base + t * ROW;
-      const float4 q0 = *reinterpret_cast<const float4*>(r), q1 = *reinterpret_cast<const float4*>(r + 4);
-      const float4 k0 = *reinterpret_cast<const float4*>(r + K), k1 = *reinterpret_cast<const float4*>(r + K + 4);
-      const float4 d0 = *reinterpret_cast<const float4*>(r + 2 * K), d1 = *reinterpret_cast<const float4*>(r + 2 * K + 4);
-      const float2 bq = *reinterpret_cast<const float2*>(s_in[b] + t * ROW + 3 * K);  // beta, q . k
-      const float vc = s_v[t][c];
-      const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-      // decay; the part of v the state already predicts from k, and q . S of the decayed state
-      float pk[8], pq[8];
+      float qq[RPL], kk[RPL], dd[RPL];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < RPL; i += 4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(r + i);
+        const float4 k4 = *reinterpret_cast<const float4*>(r + K + i);
+        const float4 d4 = *reinterpret_cast<const float4*>(r + 2 * K + i);
+        qq[i] = q4.x, qq[i + 1] = q4.y, qq[i + 2] = q4.z, qq[i + 3] = q4.w;
+        kk[i] = k4.x, kk[i + 1] = k4.y, kk[i + 2] = k4.z, kk[i + 3] = k4.w;
+        dd[i] = d4.x, dd[i + 1] = d4.y, dd[i + 2] = d4.z, dd[i + 3] = d4.w;
+      }
+      const float2 bq = *reinterpret_cast<const float2*>(s_in[b] + t * ROW + 3 * K);  // beta, q . k
+      const float vc = s_v[t][cw];
+      // decay; the part of v the state already predicts from k, and q . S of the decayed state
+      float pk[RPL], pq[RPL];
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) {
         S[i] *= dd[i];
         pk[i] = kk[i] * S[i];
         pq[i] = qq[i] * S[i];
       }
-      float pu = ((pk[0] + pk[1]) + (pk[2] + pk[3])) + ((pk[4] + pk[5]) + (pk[6] + pk[7]));
-      float qs = ((pq[0] + pq[1]) + (pq[2] + pq[3])) + ((pq[4] + pq[5]) + (pq[6] + pq[7]));
-      pu = group_sum<RG>(pu);
-      qs = group_sum<RG>(qs);
+#pragma unroll
+      for (int w = 1; w < RPL; w *= 2)  // pairwise: (0 + 1) + (2 + 3), ...
+#pragma unroll
+        for (int i = 0; i < RPL; i += 2 * w) {
+          pk[i] += pk[i + w];
+          pq[i] += pq[i + w];
+        }
+      const float pu = group_sum<RG>(pk[0]);
+      const float qs = group_sum<RG>(pq[0]);
       const float u = (vc - pu) * bq.x;
       const float po = fmaf(u, bq.y, qs);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) S[i] = fmaf(kk[i], u, S[i]);
+      for (int i = 0; i < RPL; ++i) S[i] = fmaf(kk[i], u, S[i]);
 #pragma unroll
       for (int j = 0; j < OPL; ++j)
         if (t % RG == rg && t / RG == j) keep[j] = po;  // a select, no branch
@@ -348,12 +369,12 @@ __global__ __launch_bounds__(64) void kda_recurrent_kernel(KdaArgs a, const floa
 #pragma unroll
     for (int j = 0; j < OPL; ++j) {
       const int t = rg + RG * j;
-      if (t < n) a.o[(c0 + t) * a.o_ts + static_cast<int64_t>(h) * V + col0 + c] = f32_to_bf16(keep[j]);
+      if (t < n) a.o[(c0 + t) * a.o_ts + static_cast<int64_t>(h) * V + col0 + cw] = f32_to_bf16(keep[j]);
     }
-    wave_lds_fence();  // the chunk's reads before the loads two chunks on overwrite its buffer
+    if constexpr (NWB == 1) wave_lds_fence();  // the chunk's reads before the loads two chunks on
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) st[static_cast<int64_t>(8 * rg + i) * V] = S[i];
+  for (int i = 0; i < RPL; ++i) st[static_cast<int64_t>(RPL * rg + i) * V] = S[i];
 }
 
 // ----------------------------------------------------------------------------------------- short conv
@@ -1174,9 +1195,14 @@ int launch_kda(const KdaArgs& a, float* ws, hipStream_t st) {
   hipLaunchKernelGGL((kda_prep_kernel<K>), dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st, a, ws);
   int rc = mm::check_launch("kda_recurrent prep");
   if (rc) return rc;
-  constexpr int cpw = kWave / (K / 8);
-  hipLaunchKernelGGL((kda_recurrent_kernel<K>), dim3(static_cast<unsigned>(a.V / cpw), static_cast<unsigned>(a.H)),
-                     dim3(kWave), 0, st, a, static_cast<const float*>(ws));
+  constexpr int RPL = kKdaRpl, NWB = kKdaNwb, cols = NWB * kWave / (K / RPL);
+  if (a.V % cols == 0) {
+    hipLaunchKernelGGL((kda_recurrent_kernel<K, RPL, NWB>), dim3(static_cast<unsigned>(a.V / cols),
+                       static_cast<unsigned>(a.H)), dim3(kWave * NWB), 0, st, a, static_cast<const float*>(ws));
+  } else {  // V a multiple of 8 only: one wave of 8 rows per lane per workgroup
+    hipLaunchKernelGGL((kda_recurrent_kernel<K, 8, 1>), dim3(static_cast<unsigned>(a.V / (kWave / (K / 8))),
+                       static_cast<unsigned>(a.H)), dim3(kWave), 0, st, a, static_cast<const float*>(ws));
+  }
   return mm::check_launch("kda_recurrent");
 }
 
