@@ -168,7 +168,11 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (width >= 8) v += dpp_f32<kDppHalfMirror>(v);
   if constexpr (width >= 16) v += dpp_f32<kDppMirror>(v);
   if constexpr (width == 32) {
-    v += __shfl_xor(v, 16, kWave);
+    // v_permlane16_swap_b32 of v with itself: the first result holds rows (0, 0, 2, 2) of v, the second rows
+    // (1, 1, 3, 3), so their sum is each lane's 32-lane group total (checked lane by lane on the device), with no
+    // trip through the LDS crossbar that a lane shuffle takes
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   } else if constexpr (width == 64) {
     const int b = __float_as_int(v);
     const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));

@@ -274,7 +274,8 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
   static_assert(RPL % 4 == 0 && RG <= kWave && (RG & (RG - 1)) == 0, "rows per lane");
   static_assert(ROW % 4 == 0, "16-byte workspace rows");
   __shared__ __align__(16) float s_in[2][kKdaChunk * ROW];
-  __shared__ float s_v[kKdaChunk][COLS];
+  __shared__ float s_v[2][kKdaChunk][COLS];  // two deep like s_in: a wave writes the next chunk's values while
+                                             // the workgroup's other waves may still read this chunk's
   const int h = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int c = lane / RG, rg = lane % RG;
   const int64_t V = a.V;
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + NT * j;
-      if (i < kKdaChunk * COLS) s_v[i / COLS][i % COLS] = rv[j];
+      if (i < kKdaChunk * COLS) s_v[b][i / COLS][i % COLS] = rv[j];
     }
     // every wave's loads of this chunk are in LDS, and every wave is done with the other buffer
     if constexpr (NWB == 1) wave_lds_fence(); else __syncthreads();
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
         dd[i] = d4.x, dd[i + 1] = d4.y, dd[i + 2] = d4.z, dd[i + 3] = d4.w;
       }
       const float2 bq = *reinterpret_cast<const float2*>(s_in[b] + t * ROW + 3 * K);  // beta, q . k
-      const float vc = s_v[t][cw];
+      const float vc = s_v[b][t][cw];
       // decay; the part of v the state already predicts from k, and q . S of the decayed state
       float pk[RPL], pq[RPL];
 #pragma unroll

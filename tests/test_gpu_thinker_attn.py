@@ -91,6 +91,38 @@ def test_kda_zero_write_strength_keeps_the_state():
     assert torch.equal(fin, S0)
 
 
+def test_kda_prompt_recurrence_is_deterministic():
+    """The prompt form's waves share each staged chunk (and its v values) through LDS; a wave running ahead into the
+    next chunk must not overwrite what the others still read. Five runs of a 300-token prompt (19 chunks) over 16
+    heads from one state, eagerly and from a graph, give the same outputs and states bit for bit."""
+    H, K, V, T = 16, 128, 128, 300
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 640)
+    beta = W.normal((1, T, H), 1.0, 641, DEV)
+    kw = dict(A_log=A_log, dt_bias=dt, inplace=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              beta_is_logits=True)
+    st = S0.clone()
+    o_ref, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, **kw)
+    s_ref = st.clone()
+    ws = TA.kda_workspace(T, H, K, DEV)
+    out = torch.empty_like(o_ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, out=out, workspace=ws, **kw)
+    for i in range(5):
+        st.copy_(S0)
+        o, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(st, s_ref), ("eager", i)
+        st.copy_(S0)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, o_ref) and torch.equal(st, s_ref), ("graph", i)
+
+
 @pytest.mark.parametrize("T,n,H,V", [(32, 20, 3, 128), (40, 33, 2, 64), (2, 1, 4, 128), (17, 0, 2, 128), (16, 16, 1, 32)])
 def test_kda_padding_tokens_leave_the_state_unchanged(T, n, H, V):
     """A prompt padded from n to T tokens with n_valid = n (the engine's prefill graphs): the state after it and the
