@@ -398,7 +398,8 @@ def full_decode_metrics(step, stream):
 def hybrid_decode_metrics(stream, layers=28, pos=456):
     """One decode token of the synthetic hybrid thinker (workloads.HybridThinkerStep: 21 KDA + 7 MLA layers, each
     with its MoE block, final norm + LM head) replayed from one hipGraph, and the same with the KDA cores as the
-    five-call chain (`us_per_token_kda_chain`). Every replay advances the position on
+    five-call chain (`us_per_token_kda_chain`), and on int8 experts (fp32 row scales, `int8`). Every replay
+    advances the position on
     the device: one eager call at pos, then replays at pos + 1, pos + 2, ...; the timed ones (5 x 20 after 2
     warm-up replays each) lie in pos + 3 .. pos + 110 of a 1024-row cache, mean pos + 56.5 (512.5 by default)."""
     import workloads as W
@@ -414,6 +415,14 @@ def hybrid_decode_metrics(stream, layers=28, pos=456):
     out = {"layers": layers, "kda_layers": kda, "mla_layers": layers - kda, "positions": [pos + 3, pos + 110],
            "us_per_token": ms * 1e3, "bytes_per_token": total, "TBs": total / ms / 1e9,
            "hbm_pct": total / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100, "us_per_token_kda_chain": ms_chain * 1e3}
+    # the same step on int8 experts with fp32 row scales (the reference's int8 stacks), same masters
+    step.fused_kda = True
+    step.use_int8_experts(torch.float32)
+    step.pos.fill_(pos)
+    ms8 = median_graph_ms(graph_of(step, stream), stream)
+    total8 = step.bytes_per_step(pos + 56)
+    out["int8"] = {"us_per_token": ms8 * 1e3, "bytes_per_token": total8, "TBs": total8 / ms8 / 1e9,
+                   "hbm_pct": total8 / (ms8 * 1e-3) / (HBM_PEAK_GBS * 1e9) * 100}
     del step
     torch.cuda.empty_cache()
     return out
@@ -425,10 +434,22 @@ def hybrid_prefill_metrics(stream, layers=28, pos=512, lengths=(32, 128, 512)):
     recurrence, or the causal MLA attention over the cache — then the prefill MoE block; the head on the last
     token), captured in one hipGraph per T and replayed at position 512 of a 2048-row cache (the position set back
     before each replay; the layer states keep evolving, which changes no amount of work): median of 5 timed
-    replays after one, in ms and prompt tokens/s. The expert stacks take the registered prefill copies."""
+    replays after one, in ms and prompt tokens/s; then the same on int8 experts (fp32 row scales). The expert
+    stacks take the registered prefill copies."""
     import workloads as W
     step = W.HybridThinkerStep(layers, "cuda", pos=pos, max_len=2048, seed=5000)
     out = {"layers": layers, "kda_layers": sum(p["kind"] == "kda" for p in step.L), "pos": pos}
+    _prompts(step, stream, pos, lengths, out)
+    # the same prompts on int8 experts with fp32 row scales (the reference's int8 stacks), same masters
+    step.use_int8_experts(torch.float32)
+    out["int8"] = {}
+    _prompts(step, stream, pos, lengths, out["int8"])
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
+def _prompts(step, stream, pos, lengths, out):
     for T in lengths:
         ids = (torch.arange(T, device="cuda") * 7919 + 11) % step.embed.shape[0]
         step.pos.fill_(pos)
@@ -448,9 +469,6 @@ def hybrid_prefill_metrics(stream, layers=28, pos=512, lengths=(32, 128, 512)):
         ms = sorted(ts[1:])[2]
         out[f"T{T}"] = {"ms": ms, "tokens_per_s": T / ms * 1e3}
         del g
-    del step
-    torch.cuda.empty_cache()
-    return out
 
 
 # ------------------------------------------------------------------------------------------- Talker path

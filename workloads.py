@@ -346,6 +346,20 @@ class HybridThinkerStep:
         self.fast = thinker_step.FastThinkerStep(self.model, caches, self.tok, self.pos, scoring="softmax",
                                                  fused_kda=fused_kda)
 
+    def use_int8_experts(self, scale_dtype=torch.float32):
+        """Every layer's experts as int8 + row scales from the same bf16 masters, the way engine._quantize_moe_int8
+        leaves a block (mlp.q_gu / q_d / s_gu / s_d, no bf16 stacks); the step is rebuilt on them."""
+        import thinker_step
+        for p, layer in zip(self.L, self.model.model.layers):
+            b = quantize_block(p["blk"], scale_dtype)
+            b.pop("w_gu"), b.pop("w_d")
+            mlp = layer.mlp
+            mlp.w_gu = mlp.w_d = None
+            mlp.q_gu, mlp.q_d, mlp.s_gu, mlp.s_d = b["q_gu"], b["q_d"], b["s_gu"], b["s_d"]
+        self.int8_scale_bytes = torch.finfo(scale_dtype).bits // 8
+        self.fast = thinker_step.FastThinkerStep(self.model, self.cache_layers, self.tok, self.pos, scoring="softmax",
+                                                 fused_kda=self.fast.fused_kda)
+
     @property
     def fused_kda(self):
         """The KDA cores as kda_decode_step's one kernel (True) or the chain of calls it replaces."""
@@ -377,7 +391,8 @@ class HybridThinkerStep:
             else:
                 total += (p["proj"].numel() + p["f_b"].numel() + p["g_b"].numel() + p["o"].numel()) * 2
                 total += p["conv_w"].numel() * 2 + 2 * sum(c.numel() for c in p["conv"]) * 2 + 2 * p["state"].numel() * 4
-            total += H * 2 + (TOP_K + 1) * expert_bytes() + EXPERTS * H * 4
+            sb = getattr(self, "int8_scale_bytes", None)
+            total += H * 2 + (TOP_K + 1) * expert_bytes(int8=sb is not None, scale_bytes=sb or 2) + EXPERTS * H * 4
         vocab = self.head.shape[0]
         return total + H * 2 + self.head.numel() * 2 + 2 * vocab * 2
 
