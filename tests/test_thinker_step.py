@@ -124,3 +124,24 @@ def test_refuses_what_it_cannot_run():
         thinker_step.FastThinkerStep(_model([]), [], *_bufs(), scoring="relu")
     with pytest.raises(ValueError, match="cache layers"):
         thinker_step.FastThinkerStep(_model([_layer(_kda(33), "kda", _moe())]), [], *_bufs())
+
+
+def test_prefill_refuses_bad_prompts():
+    """The prompt checks of FastThinkerStep.prefill come before any kernel: ids or rows (one of them), their types,
+    an empty prompt, and n_valid's form."""
+    kda_c, _ = _caches()
+    st = thinker_step.FastThinkerStep(_model([_layer(_kda(40), "kda", _moe())]), [kda_c], *_bufs())
+    with pytest.raises(ValueError, match="ids or its input rows"):
+        st.prefill()
+    with pytest.raises(ValueError, match="ids or its input rows"):
+        st.prefill(torch.zeros(3, dtype=torch.long), h=torch.zeros(3, H, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="h must be"):
+        st.prefill(h=torch.zeros(3, H, dtype=torch.float32))
+    with pytest.raises(ValueError, match="ids must be"):
+        st.prefill(torch.zeros(3, dtype=torch.float32))
+    with pytest.raises(ValueError, match="empty prompt"):
+        st.prefill(h=torch.zeros(0, H, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="n_valid"):
+        st.prefill(h=torch.zeros(4, H, dtype=torch.bfloat16), n_valid=torch.tensor([2], dtype=torch.int32))
+    with pytest.raises(ValueError, match="n_valid"):
+        st.prefill(h=torch.zeros(4, H, dtype=torch.bfloat16), n_valid=torch.tensor([1, 2]))
