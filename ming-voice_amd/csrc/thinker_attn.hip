@@ -590,9 +590,39 @@ constexpr int kKdaThreads = 512;
 // its half through LDS. Threads 0..255 take the f rows (K of them, a lane pair each), threads 256..511 the g rows,
 // 128 per pass; threads < K the q and k channels, threads < V the v channels. Every global load is issued before
 // the first barrier; column groups past V read zeros and write nothing (buffer bounds).
+// prefetching workgroups per head: kda_token_kernel traced at 11.26 / 9.86 / 9.51 / 9.44 us per call with 0 / 3 / 7 /
+// 15 of them (16 heads of 128 x 128, R = 128, inside the 28-layer hybrid step)
+constexpr int kKdaHelpers = 7;
+
+// A helper workgroup of kda_token_kernel (blockIdx.x >= H): part `part` of kKdaHelpers of the head's state block
+// and LoRA rows, read and dropped, so that the lines come into L2 through more CUs than the one running the head
+// (whose own loads of them then find them there or in flight): one CU alone keeps too few misses outstanding to
+// pull the head's 128 KB at HBM speed.
+__device__ __forceinline__ void kda_token_prefetch(const KdaStepArgs& a, int h, int part) {
+  constexpr int K = 128;
+  const int64_t V = a.V;
+  const char* blocks[3] = {reinterpret_cast<const char*>(a.state + static_cast<int64_t>(h) * K * V),
+                           reinterpret_cast<const char*>(a.f_b + static_cast<int64_t>(h) * K * a.R),
+                           reinterpret_cast<const char*>(a.g_b + static_cast<int64_t>(h) * V * a.R)};
+  const int64_t bytes[3] = {K * V * 4, static_cast<int64_t>(K) * a.R * 2, V * a.R * 2};
+  uint32_t acc = 0;
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    const int64_t n = bytes[b] / 16;  // whole 16-byte pieces (rows are 16-byte multiples)
+    for (int64_t i = threadIdx.x + static_cast<int64_t>(part) * kKdaThreads; i < n; i += kKdaThreads * kKdaHelpers)
+      acc ^= reinterpret_cast<const uint4*>(blocks[b])[i].x;
+  }
+  asm volatile("" ::"v"(acc));  // keeps the loads; nothing is written
+}
+
 template <int NP>
 __global__ __launch_bounds__(kKdaThreads) void kda_token_kernel(KdaStepArgs a) {
   constexpr int K = 128, RPT = K / 16, NV = 128 * NP;
+  if (kKdaHelpers > 0 && static_cast<int>(blockIdx.x) >= a.H) {  // uniform: a helper workgroup
+    const int hb = static_cast<int>(blockIdx.x) - a.H;
+    kda_token_prefetch(a, hb % a.H, hb / a.H);
+    return;
+  }
   __shared__ float s_fga[2 * kKdaMaxR], s_f[K], s_q[K], s_k[K], s_dec[K], s_g[NV], s_vc[NV], s_nr[NV];
   __shared__ float s_red[K / kWave][2];
   __shared__ float4 part_u[NP][2][4][16], part_o[NP][2][4][16];
@@ -1349,7 +1379,7 @@ extern "C" int mm_kda_decode_step(const void* pr, int64_t pr_len, const void* co
   a.V = static_cast<int>(V);
   a.R = static_cast<int>(R);
   hipStream_t st = MM_STREAM(stream);
-  const dim3 grid(static_cast<unsigned>(H)), block(kKdaThreads);
+  const dim3 grid(static_cast<unsigned>(H * (1 + kKdaHelpers))), block(kKdaThreads);
   if (V <= 128) hipLaunchKernelGGL(kda_token_kernel<1>, grid, block, 0, st, a);
   else if (V <= 256) hipLaunchKernelGGL(kda_token_kernel<2>, grid, block, 0, st, a);
   else hipLaunchKernelGGL(kda_token_kernel<4>, grid, block, 0, st, a);
