@@ -161,7 +161,7 @@ def gate_up_silu(x, wgu, norm=None, out=None):
         g = g.contiguous()
     I = wgu.shape[0] // 2
     M = x2.shape[0]
-    y = torch.empty(M, I, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(M, I)
+    y = torch.empty(M, I, device=x.device, dtype=torch.bfloat16) if out is None else out.view(M, I)
     lib = _mm.load()
     with _mm.on_device(x):
         _mm.check(lib.mm_small_linear_glu(_mm.ptr(x2), M, K, x2.stride(0), _mm.ptr(wgu), I, wgu.stride(0), _mm.ptr(g),

@@ -99,7 +99,7 @@ def small_linear(x, w, b=None, act=0, residual=None, out=None, norm=None):
             r2 = residual.expand(*shape[:-1], N).reshape(M, N)
         if not r2.is_contiguous():
             r2 = r2.contiguous()
-    y = torch.empty(M, N, device=x.device, dtype=x.dtype) if out is None else out.reshape(M, N)
+    y = torch.empty(M, N, device=x.device, dtype=x.dtype) if out is None else out.view(M, N)
     # the library fuses the norm into the GEMV for K <= 8192 and needs the scratch row only beyond that
     xn = torch.empty(min(M, MAX_M), K, device=x.device, dtype=torch.bfloat16) if norm is not None and K > 8192 else None
     if M > MAX_M and norm is not None:

@@ -102,7 +102,7 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
             state = initial_state
         else:
             state = initial_state.reshape(H, K, V).clone()
-    o = torch.empty(T, H, V, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(T, H, V)
+    o = torch.empty(T, H, V, device=q.device, dtype=torch.bfloat16) if out is None else out.view(T, H, V)
     if o.dtype != torch.bfloat16 or o.stride(2) != 1 or o.stride(1) != V:
         raise ValueError("fused_recurrent_kda: out must be bf16 [1, T, H, V] with contiguous heads")
     sc = float(scale) if scale is not None else K ** -0.5
@@ -150,7 +150,7 @@ def short_conv(x, cache, weight, bias=None, activation="silu", out=None, n_valid
         bias = bias.to(torch.bfloat16).contiguous()
     if activation not in ("silu", "swish", None):
         raise ValueError(f"short_conv: activation {activation!r} (silu or None)")
-    y = torch.empty(T, C, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(T, C)
+    y = torch.empty(T, C, device=x.device, dtype=torch.bfloat16) if out is None else out.view(T, C)
     lib = _mm.load()
     with _mm.on_device(x):
         _mm.check(lib.mm_short_conv(_mm.ptr(x2), x2.stride(0), T, C, _mm.ptr(cache), W, _mm.ptr(w2), _mm.ptr(bias),
@@ -172,7 +172,7 @@ def rms_norm_gated(x, g, weight, eps=1e-5, out=None):
         g2 = g2.contiguous()
     if x2.shape != g2.shape:
         raise ValueError("rms_norm_gated: x and g must have one shape")
-    y = torch.empty(x2.shape, device=x.device, dtype=torch.bfloat16) if out is None else out.reshape(x2.shape)
+    y = torch.empty(x2.shape, device=x.device, dtype=torch.bfloat16) if out is None else out.view(x2.shape)
     w = weight.to(torch.bfloat16).contiguous()
     lib = _mm.load()
     with _mm.on_device(x):
@@ -273,7 +273,7 @@ def mla_decode_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=None
             raise ValueError(f"mla_decode_attn: {name} must be bf16")
     if pos.dtype not in (torch.int64, torch.int32) or pos.numel() != 1:
         raise ValueError("mla_decode_attn: pos must be a one-element int64 / int32 device tensor")
-    y = torch.empty(nh, dv, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(nh, dv)
+    y = torch.empty(nh, dv, device=q.device, dtype=torch.bfloat16) if out is None else out.view(nh, dv)
     ws = mla_attn_workspace(nh, dv, max_len, q.device) if workspace is None else workspace
     sc = float(scale) if scale is not None else dqk ** -0.5
     lib = _mm.load()
@@ -321,7 +321,7 @@ def mla_prefill_attn(q, k_new, v_new, k_cache, v_cache, pos, scale=None, out=Non
     vf, vs = _token_rows(v_new, T, nh * dv, "v_new")
     if pos.dtype not in (torch.int64, torch.int32) or pos.numel() != 1:
         raise ValueError("mla_prefill_attn: pos must be a one-element int64 / int32 device tensor")
-    y = torch.empty(T, nh * dv, device=q.device, dtype=torch.bfloat16) if out is None else out.reshape(T, nh * dv)
+    y = torch.empty(T, nh * dv, device=q.device, dtype=torch.bfloat16) if out is None else out.view(T, nh * dv)
     if y.dtype != torch.bfloat16 or y.stride(1) != 1 or y.data_ptr() % 8 or (T > 1 and y.stride(0) % 4):
         raise ValueError("mla_prefill_attn: out must be bf16 [T, nh * dv] with 8-byte aligned rows")
     sc = float(scale) if scale is not None else dqk ** -0.5
