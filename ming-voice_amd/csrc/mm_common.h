@@ -160,6 +160,19 @@ constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
 // Sum over aligned groups of `width` lanes (a power of two <= 64); every lane of a group gets the group's
 // total, with one fixed association: pairs, then quads, then halves and rows of 16 (each step adds a lane
 // of the partner group, whose lanes hold equal values by then), then the row totals as (r0 + r1) + (r2 + r3).
+// The steps across rows use gfx950's v_permlane16_swap / v_permlane32_swap of a register with itself: the first
+// result holds rows (0, 0, 2, 2) of it, the second rows (1, 1, 3, 3) (16-swap), or the low and high 32 lanes
+// in both halves (32-swap), so their sum is the pair's total in every lane (lane layouts checked on the device),
+// all in the VALU with no trip through the LDS crossbar or the scalar unit.
+__device__ __forceinline__ float row_pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float half_pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(width >= 1 && width <= 64 && (width & (width - 1)) == 0, "group width");
@@ -167,20 +180,8 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (width >= 4) v += dpp_f32<kDppXor2>(v);
   if constexpr (width >= 8) v += dpp_f32<kDppHalfMirror>(v);
   if constexpr (width >= 16) v += dpp_f32<kDppMirror>(v);
-  if constexpr (width == 32) {
-    // v_permlane16_swap_b32 of v with itself: the first result holds rows (0, 0, 2, 2) of v, the second rows
-    // (1, 1, 3, 3), so their sum is each lane's 32-lane group total (checked lane by lane on the device), with no
-    // trip through the LDS crossbar that a lane shuffle takes
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  } else if constexpr (width == 64) {
-    const int b = __float_as_int(v);
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
-    v = (r0 + r1) + (r2 + r3);
-  }
+  if constexpr (width >= 32) v = row_pair_sum(v);   // r0 + r1 | r2 + r3
+  if constexpr (width == 64) v = half_pair_sum(v);  // (r0 + r1) + (r2 + r3)
   return v;
 }
 
@@ -192,9 +193,10 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f32<kDppXor2>(v));
   v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
   v = fmaxf(v, dpp_f32<kDppMirror>(v));
-  const int b = __float_as_int(v);
-  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)), __int_as_float(__builtin_amdgcn_readlane(b, 16))),
-               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
