@@ -1251,8 +1251,8 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
                                 int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
                                 int64_t K, int64_t V, float* state, void* o, int64_t o_ts, const int64_t* n_valid,
                                 void* workspace, int64_t workspace_bytes, void* stream) {
-  MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535, "kda_recurrent: bad T=%lld or H=%lld", (long long)T,
-             (long long)H);
+  MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535 && T * H <= (1LL << 31),
+             "kda_recurrent: bad T=%lld or H=%lld (T <= 2^20, H <= 65535, T H <= 2^31)", (long long)T, (long long)H);
   // a lane holds 8 state rows of one column; one wave per 64 / (K / 8) value columns
   MM_REQUIRE((K == 64 || K == 128) && V % (T <= kKdaShortT ? kKdaCols : 8) == 0 && V >= 8 && V <= 4096,
              "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096; of 16 for T <= %d)",
