@@ -273,9 +273,11 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
   static_assert(K == 64 || K == 128, "kda key dim");
   static_assert(RPL % 4 == 0 && RG <= kWave && (RG & (RG - 1)) == 0, "rows per lane");
   static_assert(ROW % 4 == 0, "16-byte workspace rows");
-  __shared__ __align__(16) float s_in[2][kKdaChunk * ROW];
-  __shared__ float s_v[2][kKdaChunk][COLS];  // two deep like s_in: a wave writes the next chunk's values while
-                                             // the workgroup's other waves may still read this chunk's
+  // two chunk buffers (and v buffers: a wave writes the next chunk's values while the workgroup's other waves may
+  // still read this chunk's), as separate arrays so that the compiler can tell a chunk's LDS reads from the next
+  // chunk's loads in flight into the other buffer, and need not wait for those loads before the reads
+  __shared__ __align__(16) float s_in0[kKdaChunk * ROW], s_in1[kKdaChunk * ROW];
+  __shared__ float s_v0[kKdaChunk][COLS], s_v1[kKdaChunk][COLS];
   const int h = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int c = lane / RG, rg = lane % RG;
   const int64_t V = a.V;
@@ -287,35 +289,34 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
   for (int i = 0; i < RPL; ++i) S[i] = st[static_cast<int64_t>(RPL * rg + i) * V];
   const float* wsh = ws + static_cast<int64_t>(h) * ROW;
   const int64_t ts = static_cast<int64_t>(a.H) * ROW;  // workspace token stride
-  float rv[VPT];
-  auto issue = [&](int c0, int b) {
+  uint16_t rv[VPT];  // raw bf16: converted once the chunk's loads are waited for, so the load needs no wait here
+  auto issue = [&](int c0, float* dst) {
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
       const int u = tid + NT * j, tt = u / ROW_UNITS;
       if (u < CHUNK_UNITS && c0 + tt < a.T)
         load_lds16(wsh + (c0 + tt) * ts + (u % ROW_UNITS) * 4,
-                   reinterpret_cast<char*>(s_in[b]) + (wave * kWave + NT * j) * 16);
+                   reinterpret_cast<char*>(dst) + (wave * kWave + NT * j) * 16);
     }
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int i = tid + NT * j, tt = c0 + i / COLS;
-      rv[j] = i < kKdaChunk * COLS && tt < a.T
-                  ? bf16_to_f32(a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % COLS]) : 0.f;
+    for (int j = 0; j < VPT; ++j) {  // no branch: rows past the prompt (never read) load its last token's row
+      const int i = tid + NT * j, tt = min(c0 + i / COLS, a.T - 1);
+      rv[j] = a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % COLS];
     }
   };
-  issue(0, 0);
-  for (int c0 = 0, b = 0; c0 < a.T; c0 += kKdaChunk, b ^= 1) {
+  // one chunk from buffers (in, vb) while the next one loads into (in_next); called with the arrays themselves
+  auto chunk = [&](int c0, const float* in, float (*vb)[COLS], float* in_next) {
     wait_vmcnt<0>();  // this wave's loads of the chunk (and the stores before them)
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int i = tid + NT * j;
-      if (i < kKdaChunk * COLS) s_v[b][i / COLS][i % COLS] = rv[j];
+      if (i < kKdaChunk * COLS) vb[i / COLS][i % COLS] = bf16_to_f32(rv[j]);
     }
     // every wave's loads of this chunk are in LDS, and every wave is done with the other buffer
     if constexpr (NWB == 1) wave_lds_fence(); else __syncthreads();
-    if (c0 + kKdaChunk < a.T) issue(c0 + kKdaChunk, b ^ 1);  // in flight during the recurrence below
+    if (c0 + kKdaChunk < a.T) issue(c0 + kKdaChunk, in_next);  // in flight during the recurrence below
     const int n = min(kKdaChunk, a.T - c0);
-    const float* base = s_in[b] + RPL * rg;
+    const float* base = in + RPL * rg;
     // lane (c, rg) keeps the output of tokens rg, rg + RG, ... of the chunk (every lane of a column holds each
     // token's sum) and stores them after the chunk: the token steps have no branch
     constexpr int OPL = (kKdaChunk + RG - 1) / RG;
@@ -334,8 +335,8 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
         kk[i] = k4.x, kk[i + 1] = k4.y, kk[i + 2] = k4.z, kk[i + 3] = k4.w;
         dd[i] = d4.x, dd[i + 1] = d4.y, dd[i + 2] = d4.z, dd[i + 3] = d4.w;
       }
-      const float2 bq = *reinterpret_cast<const float2*>(s_in[b] + t * ROW + 3 * K);  // beta, q . k
-      const float vc = s_v[b][t][cw];
+      const float2 bq = *reinterpret_cast<const float2*>(in + t * ROW + 3 * K);  // beta, q . k
+      const float vc = vb[t][cw];
       // decay; the part of v the state already predicts from k, and q . S of the decayed state
       float pk[RPL], pq[RPL];
 #pragma unroll
@@ -373,6 +374,11 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
       if (t < n) a.o[(c0 + t) * a.o_ts + static_cast<int64_t>(h) * V + col0 + cw] = f32_to_bf16(keep[j]);
     }
     if constexpr (NWB == 1) wave_lds_fence();  // the chunk's reads before the loads two chunks on
+  };
+  issue(0, s_in0);
+  for (int c0 = 0; c0 < a.T; c0 += 2 * kKdaChunk) {
+    chunk(c0, s_in0, s_v0, s_in1);
+    if (c0 + kKdaChunk < a.T) chunk(c0 + kKdaChunk, s_in1, s_v1, s_in0);
   }
 #pragma unroll
   for (int i = 0; i < RPL; ++i) st[static_cast<int64_t>(RPL * rg + i) * V] = S[i];
