@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 12
+#define MM_ABI_VERSION 13
 
 /* status codes */
 #define MM_OK 0
@@ -317,6 +317,22 @@ int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, c
 
 /* Bytes of fp32 workspace mm_kda_recurrent needs: T * H * (3 K + 4) * 4, 0 for T <= 2 (-1 if invalid). */
 int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K);
+
+/* The same recurrence in chunked form: what fla's chunk_kda (fla-core 0.5.2) computes, which the engine's eager
+ * prefill selects for prompt pieces of more than 192 tokens (engine.py:946-949, 964-967; the model's KDA layers call
+ * it). Same arguments, checks and outputs as mm_kda_recurrent up to the order of fp32 sums: the tokens go 16 at a
+ * time, each chunk in closed form (the decay products and the chunk's k-k and q-k products computed for all chunks
+ * at once, then a forward substitution per chunk), so a token no longer waits for the sums of the token before it.
+ * workspace: at least mm_kda_chunk_workspace(T, H, K) bytes, 16-byte aligned; T <= 2 runs as mm_kda_recurrent. */
+int mm_kda_chunk(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
+                 const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
+                 const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm, int use_gate,
+                 int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V, float* state, void* o,
+                 int64_t o_ts, const int64_t* n_valid, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of fp32 workspace mm_kda_chunk needs: ceil(T / 16) * H * (49 K + 512) * 4 (one block per 16-token chunk and
+ * head), 0 for T <= 2 (-1 if invalid). */
+int64_t mm_kda_chunk_workspace(int64_t T, int64_t H, int64_t K);
 
 /* Depthwise causal convolution over time, the step form of fla's ShortConvolution (the q / k / v convolutions of a
  * KDA layer, engine.py:247-249, caches engine.py:645-647): per channel, for each of T tokens in order, the window

@@ -192,17 +192,16 @@ __global__ __launch_bounds__(256) void kda_short_kernel(KdaArgs a) {
 template <int K>
 constexpr int kda_ws_row() { return 3 * K + 4; }
 
-// Grid (T H / 4) x 4 waves: wave w prepares row (t, h) = divmod(4 blockIdx.x + w, H), lane i channels i + 64 j.
+// The prepared inputs of token t, head h for the lane's channels lane + 64 j (one wave): q l2-normalised times the
+// scale, k l2-normalised, the decay exp(gate(g)) (1 for a padding token), and, the same in every lane, beta (the
+// sigmoid applied when it comes as logits; 0 for padding) and q . k of the normalised vectors.
 template <int K>
-__global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restrict__ ws) {
-  constexpr int NJ = K / kWave, ROW = kda_ws_row<K>();
+__device__ __forceinline__ void kda_prep_token(const KdaArgs& a, int64_t t, int h, bool pad, float (&qn)[K / kWave],
+                                               float (&kn)[K / kWave], float (&dv)[K / kWave], float& beta,
+                                               float& qk) {
+  constexpr int NJ = K / kWave;
   const int lane = lane_id();
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-  if (idx >= static_cast<int64_t>(a.T) * a.H) return;  // whole waves
-  const int64_t t = idx / a.H;
-  const int h = static_cast<int>(idx % a.H);
   const int64_t hk = static_cast<int64_t>(h) * K;
-  const bool pad = t >= kda_valid(a);
   float qv[NJ], kv[NJ], gv[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -211,6 +210,7 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
     kv[j] = bf16_to_f32(a.k[t * a.k_ts + ch]);
     gv[j] = ld_any(a.g, a.g_dtype, t * a.g_ts + ch);
   }
+  float b = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
   float qs = a.scale, ks = 1.f;
   if (a.use_l2norm) {
     float sq = 0.f, sk = 0.f;
@@ -223,32 +223,44 @@ __global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restr
     ks = 1.f / sqrtf(wave_sum(sk) + 1e-6f);
   }
   const float nA = a.use_gate ? __expf(a.A_log[h]) : 0.f;
+  float d = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    float gl = gv[j];
+    if (a.use_gate) {
+      const float x = gl + a.dt_bias[hk + lane + kWave * j];
+      gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
+    }
+    qn[j] = qv[j] * qs;
+    kn[j] = kv[j] * ks;
+    dv[j] = pad ? 1.f : __expf(gl);
+    d = fmaf(qn[j], kn[j], d);
+  }
+  qk = wave_sum(d);
+  if (a.beta_logits) b = 1.f / (1.f + __expf(-b));
+  beta = pad ? 0.f : b;
+}
+
+// Grid (T H / 4) x 4 waves: wave w prepares row (t, h) = divmod(4 blockIdx.x + w, H), lane i channels i + 64 j.
+template <int K>
+__global__ __launch_bounds__(256) void kda_prep_kernel(KdaArgs a, float* __restrict__ ws) {
+  constexpr int NJ = K / kWave, ROW = kda_ws_row<K>();
+  const int lane = lane_id();
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  if (idx >= static_cast<int64_t>(a.T) * a.H) return;  // whole waves
+  const int64_t t = idx / a.H;
+  const int h = static_cast<int>(idx % a.H);
+  float qn[NJ], kn[NJ], dv[NJ], beta, qk;
+  kda_prep_token<K>(a, t, h, t >= kda_valid(a), qn, kn, dv, beta, qk);
   float* row = ws + idx * ROW;
-  float qk = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int c = lane + kWave * j;
-    float gl = gv[j];
-    if (a.use_gate) {
-      const float x = gl + a.dt_bias[hk + c];
-      gl = isnan(a.lower_bound) ? -nA * softplus20(x) : a.lower_bound / (1.f + __expf(-nA * x));
-    }
-    const float qn = qv[j] * qs, kn = kv[j] * ks;
-    row[c] = qn;
-    row[K + c] = kn;
-    row[2 * K + c] = pad ? 1.f : __expf(gl);
-    qk = fmaf(qn, kn, qk);
+    row[c] = qn[j];
+    row[K + c] = kn[j];
+    row[2 * K + c] = dv[j];
   }
-  qk = wave_sum(qk);
-  if (lane < 4) {
-    float b = 0.f;
-    if (lane == 0) {
-      b = ld_any(a.beta, a.beta_dtype, t * a.b_ts + h);
-      if (a.beta_logits) b = 1.f / (1.f + __expf(-b));
-      if (pad) b = 0.f;
-    }
-    row[3 * K + lane] = lane == 1 ? qk : b;
-  }
+  if (lane < 4) row[3 * K + lane] = lane == 0 ? beta : lane == 1 ? qk : 0.f;
 }
 
 // NWB waves per (NWB CPW value columns, head): grid (V / (NWB CPW), H) x 64 NWB threads, CPW = 64 / RG with
@@ -382,6 +394,282 @@ __global__ __launch_bounds__(64 * NWB) void kda_recurrent_kernel(KdaArgs a, cons
   }
 #pragma unroll
   for (int i = 0; i < RPL; ++i) st[static_cast<int64_t>(RPL * rg + i) * V] = S[i];
+}
+
+// -------------------------------------------------------------------------------------- KDA, chunked form
+//
+// The same recurrence over a chunk of C = 16 tokens in closed form (the chunked form of fla's chunk_kda, which the
+// engine selects past 192 tokens: engine.py:946-949, 964-967). With chunk-local tokens t = 0 .. C-1, S0 the state
+// at the chunk start, d_t the per-channel decay of token t, P_t = d_0 ... d_t and D(j, t) = d_{j+1} ... d_t
+// (per-channel products taken directly, never as ratios, so a strong decay underflows to zero instead of 0 / 0):
+//   k_t . (the decayed state before token t's write) = a_t + sum_{j<t} A[t][j] u_j,
+//       a_t = (k_t P_t) . S0,  A[t][j] = sum_c k_tc k_jc D(j, t)_c
+//   u_t = beta_t (v_t - a_t - sum_{j<t} A[t][j] u_j)        (forward substitution, j in order)
+//   o_t = q_t . S_t = b_t + sum_{j<=t} B[t][j] u_j,
+//       b_t = (q_t P_t) . S0,  B[t][j] = sum_c q_tc k_jc D(j, t)_c (j < t),  B[t][t] = q_t . k_t
+//   S_end = P_{C-1} S0 + sum_j (k_j D(j, C-1)) u_j^T
+// Everything but S0 and v depends on the head alone, not on the value columns: kda_chunk_prep_kernel computes it
+// for every (chunk, head) at once into a block of the workspace; kda_chunk_kernel then carries its value columns'
+// state from chunk to chunk, and no token waits for a sum over k of the token before it. Padding tokens (past
+// n_valid, or past T in the last chunk) have decay 1 and beta 0, so their u is 0 and the state passes them unchanged.
+
+// A (chunk, head) block of the workspace, in floats: k P [C][K], q P [C][K], W = k D(., C-1) [C][K], P_{C-1} [K],
+// A [C][C] with beta_t on its diagonal, B [C][C] (zero above the diagonal).
+template <int K>
+struct KdaBlk {
+  static constexpr int C = kKdaChunk;
+  static constexpr int KP = 0, QP = C * K, W = 2 * C * K, PC = 3 * C * K, A = PC + K, B = A + C * C;
+  static constexpr int SIZE = B + C * C;
+  static_assert(SIZE % 4 == 0, "blocks stay 16-byte aligned");
+};
+
+// 32 values over the 64 lanes of a wave: x[0] becomes the wave's total of value lane % 32 (the halves summed by
+// v_permlane32_swap, then transposed over the rows and within them: 63 exchanges, against 192 for 32 separate sums).
+__device__ __forceinline__ void wave_sums32(float (&x)[32]);
+
+// Grid (chunks, H) x 16 waves. Wave w prepares token w of the chunk (kda_prep_token: q and k normalised, the decay,
+// beta, q . k; a token past T gets q = k = 0, decay 1, beta 0) into LDS, then writes its rows: k P, q P and W of token
+// w (the decay products over the other tokens' channels read back from LDS, taken as predicated products so that no
+// register array is indexed at run time), P_{C-1} (wave C-1), and row w of A and B (entry j a wave sum over the
+// channels, the 32 entries summed together by wave_sums32).
+template <int K>
+__global__ __launch_bounds__(64 * kKdaChunk) void kda_chunk_prep_kernel(KdaArgs a, float* __restrict__ blk) {
+  using L = KdaBlk<K>;
+  constexpr int C = L::C, NJ = K / kWave;
+  __shared__ float s_k[C][K], s_d[C][K];
+  const int ci = blockIdx.x, h = blockIdx.y;
+  const int w = threadIdx.x / kWave, lane = lane_id();
+  const int t0 = ci * C;
+  const bool in = t0 + w < a.T;
+  float qn[NJ], kn[NJ], dv[NJ], beta, qk;
+  kda_prep_token<K>(a, in ? t0 + w : t0, h, t0 + w >= kda_valid(a), qn, kn, dv, beta, qk);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    qn[j] = in ? qn[j] : 0.f;
+    kn[j] = in ? kn[j] : 0.f;
+    dv[j] = in ? dv[j] : 1.f;
+    s_k[w][lane + kWave * j] = kn[j];
+    s_d[w][lane + kWave * j] = dv[j];
+  }
+  beta = in ? beta : 0.f;
+  qk = in ? qk : 0.f;
+  __syncthreads();
+  // P_w = d_0 ... d_w and R_w = D(w, C-1) = d_{w+1} ... d_{C-1}; then, j running down, D(j, w) = d_{j+1} ... d_w
+  float P[NJ], R[NJ], D[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) P[j] = R[j] = D[j] = 1.f;
+  float x[32];  // the lane's parts of A[w][j] (x[j]) and B[w][j] (x[16 + j]), j < w
+#pragma unroll
+  for (int s2 = C - 1; s2 >= 0; --s2) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float ds = s_d[s2][lane + kWave * j];
+      P[j] = s2 <= w ? P[j] * ds : P[j];
+      R[j] = s2 > w ? R[j] * ds : R[j];
+    }
+  }
+#pragma unroll
+  for (int jj = C - 1; jj >= 0; --jj) {
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int ch = lane + kWave * j;
+      if (jj + 1 < C) D[j] = jj + 1 <= w ? D[j] * s_d[jj + 1][ch] : D[j];
+      const float kd = s_k[jj][ch] * D[j];
+      sa = fmaf(kn[j], kd, sa);
+      sb = fmaf(qn[j], kd, sb);
+    }
+    x[jj] = jj < w ? sa : 0.f;
+    x[C + jj] = jj < w ? sb : 0.f;
+  }
+  float* out = blk + (static_cast<int64_t>(ci) * a.H + h) * L::SIZE;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int ch = lane + kWave * j;
+    out[L::KP + w * K + ch] = kn[j] * P[j];
+    out[L::QP + w * K + ch] = qn[j] * P[j];
+    out[L::W + w * K + ch] = kn[j] * R[j];
+    if (w == C - 1) out[L::PC + ch] = P[j];
+  }
+  wave_sums32(x);
+  if (lane < 2 * C) {
+    const int jj = lane % C;
+    const float diag = lane < C ? beta : qk;
+    out[(lane < C ? L::A : L::B) + w * C + jj] = jj < w ? x[0] : jj == w ? diag : 0.f;
+  }
+}
+
+// Transposed sums over the lanes of a column. In a step the two lanes of a pair each keep the half of their values
+// whose index has their lane bit, adding the partner's copy of it; the pairs are those of group_sum (v_permlane16_swap
+// across rows of 16 for lane bit 4, then the DPP mirror, half mirror, xor 2 and xor 1 for bits 3 .. 0: a partner
+// differs in the step's bit and agrees in every bit split before), so the lane's last value sums all the lanes.
+// One step of 16-lane sums on x[0 .. 2H): pairs (v, v + H) split on lane bit `bit`.
+template <int ctrl, int H>
+__device__ __forceinline__ void col_step(float* x, int bit) {
+  const bool hi = (lane_id() >> bit) & 1;
+#pragma unroll
+  for (int v = 0; v < H; ++v) {
+    const float keep = hi ? x[v + H] : x[v], send = hi ? x[v] : x[v + H];
+    x[v] = keep + dpp_f32<ctrl>(send);
+  }
+}
+
+// 16 values over the 16 lanes of a row: x[0] becomes the row's total of value lane % 16 (15 exchanges, against 64
+// for 16 separate sums).
+__device__ __forceinline__ void row_sums16(float* x) {
+  col_step<kDppMirror, 8>(x, 3);
+  col_step<kDppHalfMirror, 4>(x, 2);
+  col_step<kDppXor2, 2>(x, 1);
+  col_step<kDppXor1, 1>(x, 0);
+}
+
+__device__ __forceinline__ void wave_sums32(float (&x)[32]) {
+#pragma unroll
+  for (int v = 0; v < 32; ++v) x[v] = half_pair_sum(x[v]);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[v]), __float_as_uint(x[v + 16]), false, false);
+    x[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  row_sums16(x);
+}
+
+// 32 values over the RG lanes of a column: RG = 32, x[0] = total of value rg; RG = 16, x[0] and x[16] = totals of
+// values rg and 16 + rg.
+template <int RG>
+__device__ __forceinline__ void column_sums(float (&x)[32]) {
+  if constexpr (RG == 32) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {  // row 0 keeps v, row 1 keeps v + 16, both at index v
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[v]), __float_as_uint(x[v + 16]), false, false);
+      x[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    row_sums16(x);
+  } else {
+    row_sums16(x);
+    row_sums16(x + 16);
+  }
+}
+
+// Grid (V / COLS, H) x NWB waves, the layout of kda_recurrent_kernel: lane (c = lane / RG, rg = lane % RG) holds
+// state rows 4 rg .. 4 rg + 3 of one value column. A chunk's block comes into LDS by global_load_lds (two buffers,
+// the next chunk loading during this one). Per chunk a lane forms its parts of a_t and b_t for the 16 tokens and the
+// column's lanes sum them transposed, so that one lane holds a_t ("A lane" of token t) and one b_t ("B lane"; for
+// RG = 32 lanes 0-15 and 16-31, for RG = 16 every lane is both). The forward substitution then runs across the
+// lanes: at step j the A lane of token j has all of its terms, forms u_j = beta_j r_j, and u_j goes to the column's
+// lanes by readlane; every A lane of a later token subtracts A[t][j] u_j, every B lane adds B[t][j] u_j. Each lane
+// keeps the 16 u for its rows of the state update; the B lanes store the outputs.
+template <int K, int NWB>
+__global__ __launch_bounds__(64 * NWB) void kda_chunk_kernel(KdaArgs a, const float* __restrict__ blk) {
+  using L = KdaBlk<K>;
+  constexpr int C = L::C, RPL = 4, RG = K / RPL, CPW = kWave / RG, COLS = NWB * CPW;
+  constexpr int NT = NWB * kWave, UNITS = L::SIZE / 4, NU = (UNITS + NT - 1) / NT;
+  constexpr int VPT = (C * COLS + NT - 1) / NT;
+  constexpr bool DUAL = RG == C;  // every lane both an A and a B lane
+  static_assert((RG == 32 || RG == 16) && C == 16, "column lanes");
+  // separate arrays, so that a chunk's LDS reads need not wait for the next chunk's loads into the other one
+  __shared__ __align__(16) float s_b0[L::SIZE], s_b1[L::SIZE];
+  __shared__ float s_v0[C][COLS], s_v1[C][COLS];
+  const int h = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
+  const int c = lane / RG, rg = lane % RG, r0 = RPL * rg;
+  const int64_t V = a.V;
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * COLS;
+  const int cw = wave * CPW + c;
+  const int tA = rg % C;                       // token of the lane's A role (RG = 32: lanes rg < 16)
+  const bool isA = DUAL || rg < C, isB = DUAL || rg >= C;
+  float* st = a.state + static_cast<int64_t>(h) * K * V + col0 + cw;
+  float S[RPL];
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) S[i] = st[static_cast<int64_t>(r0 + i) * V];
+  const int nch = (a.T + C - 1) / C;
+  const float* bh = blk + static_cast<int64_t>(h) * L::SIZE;
+  const int64_t cs = static_cast<int64_t>(a.H) * L::SIZE;  // between the chunks of a head
+  uint16_t rv[VPT];  // raw bf16 v, converted once the chunk's loads are waited for
+  auto issue = [&](int ci, float* dst) {
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+      const int u = tid + NT * j;
+      if (u < UNITS) load_lds16(bh + ci * cs + u * 4, reinterpret_cast<char*>(dst) + (wave * kWave + NT * j) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {  // rows past the prompt (never used: beta 0) load its last token's row
+      const int i = tid + NT * j, tt = min(ci * C + i / COLS, a.T - 1);
+      rv[j] = a.v[tt * a.v_ts + static_cast<int64_t>(h) * V + col0 + i % COLS];
+    }
+  };
+  // u_j of this lane's column: the value of its lane j (j wave-uniform)
+  auto col_bcast = [&](float x, int j) {
+    float r = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), j));
+#pragma unroll
+    for (int cc = 1; cc < CPW; ++cc) {
+      const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(x), cc * RG + j));
+      r = c == cc ? o : r;
+    }
+    return r;
+  };
+  auto chunk = [&](int ci, const float* in, float (*vb)[COLS], float* in_next) {
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int i = tid + NT * j;
+      if (i < C * COLS) vb[i / COLS][i % COLS] = bf16_to_f32(rv[j]);
+    }
+    if constexpr (NWB == 1) wave_lds_fence(); else __syncthreads();
+    if (ci + 1 < nch) issue(ci + 1, in_next);
+    float x[32];  // the lane's parts of a_t (x[t]) and b_t (x[16 + t])
+#pragma unroll
+    for (int t = 0; t < C; ++t) {
+      const float4 kp = *reinterpret_cast<const float4*>(in + L::KP + t * K + r0);
+      const float4 qp = *reinterpret_cast<const float4*>(in + L::QP + t * K + r0);
+      x[t] = fmaf(kp.x, S[0], kp.y * S[1]) + fmaf(kp.z, S[2], kp.w * S[3]);
+      x[C + t] = fmaf(qp.x, S[0], qp.y * S[1]) + fmaf(qp.z, S[2], qp.w * S[3]);
+    }
+    column_sums<RG>(x);  // RG = 32: x[0] = a_rg or b_(rg-16); RG = 16: x[0] = a_rg, x[16] = b_rg
+    // the lane's rows of A and B (A's diagonal holds beta)
+    const float* arow = in + L::A + tA * C;
+    const float* brow = in + L::B + (DUAL ? rg : (rg >= C ? rg - C : 0)) * C;
+    float ca[C], cb[C];
+#pragma unroll
+    for (int j = 0; j < C; j += 4) {
+      const float4 av = *reinterpret_cast<const float4*>(arow + j);
+      const float4 bv = *reinterpret_cast<const float4*>(brow + j);
+      ca[j] = av.x, ca[j + 1] = av.y, ca[j + 2] = av.z, ca[j + 3] = av.w;
+      cb[j] = bv.x, cb[j + 1] = bv.y, cb[j + 2] = bv.z, cb[j + 3] = bv.w;
+    }
+    const float beta = arow[tA];
+    float ra = isA ? vb[tA][cw] - x[0] : 0.f;  // v_t - a_t, less the earlier u's terms as they come
+    float rb = DUAL ? x[16] : x[0];            // b_t, plus B[t][j] u_j
+    float uall[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      uall[j] = col_bcast(ra * beta, j);
+      ra = tA > j ? fmaf(-ca[j], uall[j], ra) : ra;
+      rb = fmaf(cb[j], uall[j], rb);
+    }
+    const float4 pc = *reinterpret_cast<const float4*>(in + L::PC + r0);
+    S[0] *= pc.x;
+    S[1] *= pc.y;
+    S[2] *= pc.z;
+    S[3] *= pc.w;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const float4 wv = *reinterpret_cast<const float4*>(in + L::W + j * K + r0);
+      S[0] = fmaf(wv.x, uall[j], S[0]);
+      S[1] = fmaf(wv.y, uall[j], S[1]);
+      S[2] = fmaf(wv.z, uall[j], S[2]);
+      S[3] = fmaf(wv.w, uall[j], S[3]);
+    }
+    const int t = ci * C + (DUAL ? rg : rg - C);
+    if (isB && t < a.T) a.o[t * a.o_ts + static_cast<int64_t>(h) * V + col0 + cw] = f32_to_bf16(rb);
+    if constexpr (NWB == 1) wave_lds_fence();  // the chunk's reads before the loads two chunks on
+  };
+  issue(0, s_b0);
+  for (int ci = 0; ci < nch; ci += 2) {
+    chunk(ci, s_b0, s_v0, s_b1);
+    if (ci + 1 < nch) chunk(ci + 1, s_b1, s_v1, s_b0);
+  }
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) st[static_cast<int64_t>(r0 + i) * V] = S[i];
 }
 
 // ----------------------------------------------------------------------------------------- short conv
@@ -1243,6 +1531,27 @@ int launch_kda(const KdaArgs& a, float* ws, hipStream_t st) {
   return mm::check_launch("kda_recurrent");
 }
 
+// The chunked form: token preparation, the (chunk, head) blocks after the token rows, then the chunk recurrence.
+template <int K>
+int launch_kda_chunk(const KdaArgs& a, float* ws, hipStream_t st) {
+  if (a.T <= kKdaShortT) return launch_kda<K>(a, ws, st);  // a decode step: one launch, no workspace
+  float* blk = ws;
+  const unsigned nch = static_cast<unsigned>((a.T + kKdaChunk - 1) / kKdaChunk);
+  hipLaunchKernelGGL((kda_chunk_prep_kernel<K>), dim3(nch, static_cast<unsigned>(a.H)), dim3(64 * kKdaChunk), 0, st, a,
+                     blk);
+  int rc = mm::check_launch("kda_chunk prep");
+  if (rc) return rc;
+  constexpr int NWB = kKdaNwb, cols = NWB * kWave / (K / 4);
+  if (a.V % cols == 0) {
+    hipLaunchKernelGGL((kda_chunk_kernel<K, NWB>), dim3(static_cast<unsigned>(a.V / cols), static_cast<unsigned>(a.H)),
+                       dim3(kWave * NWB), 0, st, a, static_cast<const float*>(blk));
+  } else {  // V a multiple of 8 only: one wave per workgroup
+    hipLaunchKernelGGL((kda_chunk_kernel<K, 1>), dim3(static_cast<unsigned>(a.V / (cols / NWB)),
+                       static_cast<unsigned>(a.H)), dim3(kWave), 0, st, a, static_cast<const float*>(blk));
+  }
+  return mm::check_launch("kda_chunk");
+}
+
 }  // namespace
 
 extern "C" int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K) {
@@ -1251,27 +1560,37 @@ extern "C" int64_t mm_kda_recurrent_workspace(int64_t T, int64_t H, int64_t K) {
   return T * H * (3 * K + 4) * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
-                                const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
-                                int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound,
-                                int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
-                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, const int64_t* n_valid,
-                                void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int64_t mm_kda_chunk_workspace(int64_t T, int64_t H, int64_t K) {
+  if (T < 0 || H < 1 || (K != 64 && K != 128)) return -1;
+  if (T <= kKdaShortT) return 0;
+  const int64_t blk = K == 64 ? KdaBlk<64>::SIZE : KdaBlk<128>::SIZE;
+  return (T + kKdaChunk - 1) / kKdaChunk * H * blk * static_cast<int64_t>(sizeof(float));
+}
+
+// The argument checks and launches of mm_kda_recurrent and mm_kda_chunk (same arguments, same results up to the
+// order of fp32 sums).
+static int kda_entry(bool chunked, const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v,
+                     int64_t v_ts, const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
+                     int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm,
+                     int use_gate, int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V,
+                     float* state, void* o, int64_t o_ts, const int64_t* n_valid, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
+  const char* who = chunked ? "kda_chunk" : "kda_recurrent";
   MM_REQUIRE(T >= 0 && T <= (1 << 20) && H >= 1 && H <= 65535 && T * H <= (1LL << 31),
-             "kda_recurrent: bad T=%lld or H=%lld (T <= 2^20, H <= 65535, T H <= 2^31)", (long long)T, (long long)H);
+             "%s: bad T=%lld or H=%lld (T <= 2^20, H <= 65535, T H <= 2^31)", who, (long long)T, (long long)H);
   // a lane holds 8 state rows of one column; one wave per 64 / (K / 8) value columns
   MM_REQUIRE((K == 64 || K == 128) && V % (T <= kKdaShortT ? kKdaCols : 8) == 0 && V >= 8 && V <= 4096,
-             "kda_recurrent: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096; of 16 for T <= %d)",
+             "%s: head dims K=%lld (64 or 128), V=%lld (a multiple of 8 up to 4096; of 16 for T <= %d)", who,
              (long long)K, (long long)V, kKdaShortT);
-  MM_REQUIRE(T <= kKdaShortT || (workspace && mm::aligned16(workspace) &&
-                                 workspace_bytes >= mm_kda_recurrent_workspace(T, H, K)),
-             "kda_recurrent: the workspace must be 16-byte aligned and hold mm_kda_recurrent_workspace(T, H, K) bytes");
-  MM_REQUIRE(g_dtype == MM_BF16 || g_dtype == MM_FP32, "kda_recurrent: g must be bf16 or fp32");
-  MM_REQUIRE(beta_dtype == MM_BF16 || beta_dtype == MM_FP32, "kda_recurrent: beta must be bf16 or fp32");
-  MM_REQUIRE(q && k && v && g && beta && state && o, "kda_recurrent: null pointer");
-  MM_REQUIRE(!use_gate || (A_log && dt_bias), "kda_recurrent: the gate needs A_log and dt_bias");
+  const int64_t need = chunked ? mm_kda_chunk_workspace(T, H, K) : mm_kda_recurrent_workspace(T, H, K);
+  MM_REQUIRE(T <= kKdaShortT || (workspace && mm::aligned16(workspace) && workspace_bytes >= need),
+             "%s: the workspace must be 16-byte aligned and hold mm_%s_workspace(T, H, K) bytes", who, who);
+  MM_REQUIRE(g_dtype == MM_BF16 || g_dtype == MM_FP32, "%s: g must be bf16 or fp32", who);
+  MM_REQUIRE(beta_dtype == MM_BF16 || beta_dtype == MM_FP32, "%s: beta must be bf16 or fp32", who);
+  MM_REQUIRE(q && k && v && g && beta && state && o, "%s: null pointer", who);
+  MM_REQUIRE(!use_gate || (A_log && dt_bias), "%s: the gate needs A_log and dt_bias", who);
   MM_REQUIRE(q_ts >= H * K && k_ts >= H * K && g_ts >= H * K && v_ts >= H * V && beta_ts >= H && o_ts >= H * V,
-             "kda_recurrent: token strides smaller than a token's heads");
+             "%s: token strides smaller than a token's heads", who);
   if (T == 0) return MM_OK;
   KdaArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -1302,7 +1621,30 @@ extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int6
   a.n_valid = n_valid;
   hipStream_t st = MM_STREAM(stream);
   float* ws = static_cast<float*>(workspace);
+  if (chunked) return K == 64 ? launch_kda_chunk<64>(a, ws, st) : launch_kda_chunk<128>(a, ws, st);
   return K == 64 ? launch_kda<64>(a, ws, st) : launch_kda<128>(a, ws, st);
+}
+
+extern "C" int mm_kda_recurrent(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
+                                const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype,
+                                int64_t beta_ts, const float* A_log, const float* dt_bias, float lower_bound,
+                                int use_qk_l2norm, int use_gate, int beta_logits, float scale, int64_t T, int64_t H,
+                                int64_t K, int64_t V, float* state, void* o, int64_t o_ts, const int64_t* n_valid,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
+  return kda_entry(false, q, q_ts, k, k_ts, v, v_ts, g, g_dtype, g_ts, beta, beta_dtype, beta_ts, A_log, dt_bias,
+                   lower_bound, use_qk_l2norm, use_gate, beta_logits, scale, T, H, K, V, state, o, o_ts, n_valid,
+                   workspace, workspace_bytes, stream);
+}
+
+extern "C" int mm_kda_chunk(const void* q, int64_t q_ts, const void* k, int64_t k_ts, const void* v, int64_t v_ts,
+                            const void* g, int g_dtype, int64_t g_ts, const void* beta, int beta_dtype, int64_t beta_ts,
+                            const float* A_log, const float* dt_bias, float lower_bound, int use_qk_l2norm,
+                            int use_gate, int beta_logits, float scale, int64_t T, int64_t H, int64_t K, int64_t V,
+                            float* state, void* o, int64_t o_ts, const int64_t* n_valid, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  return kda_entry(true, q, q_ts, k, k_ts, v, v_ts, g, g_dtype, g_ts, beta, beta_dtype, beta_ts, A_log, dt_bias,
+                   lower_bound, use_qk_l2norm, use_gate, beta_logits, scale, T, H, K, V, state, o, o_ts, n_valid,
+                   workspace, workspace_bytes, stream);
 }
 
 extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,

@@ -54,6 +54,14 @@ def kda_workspace(T, H, K, device):
     return torch.empty(max(n, 16) // 4, device=device, dtype=torch.float32)
 
 
+def kda_chunk_workspace(T, H, K, device):
+    """The fp32 workspace chunk_kda needs for T tokens of H heads of key dim K."""
+    n = _mm.load().mm_kda_chunk_workspace(T, H, K)
+    if n < 0:
+        raise ValueError(f"kda_chunk_workspace: bad T={T}, H={H} or K={K}")
+    return torch.empty(max(n, 16) // 4, device=device, dtype=torch.float32)
+
+
 def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None,
                         output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
                         lower_bound=None, inplace=False, out=None, beta_is_logits=False, workspace=None, n_valid=None,
@@ -65,15 +73,33 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     beta_is_logits=True takes the beta projection itself and applies the sigmoid in the kernel. workspace: from
     kda_workspace(T, H, K) (allocated when None). n_valid: a one-element int64 device tensor n, or None: tokens
     n .. T - 1 are padding and leave the state exactly unchanged (the engine's padded prefill, engine.py:252-253)."""
+    return _kda("fused_recurrent_kda", False, q, k, v, g, beta, A_log, dt_bias, scale, initial_state,
+                output_final_state, use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound, inplace, out,
+                beta_is_logits, workspace, n_valid)
+
+
+def chunk_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, initial_state=None, output_final_state=False,
+              use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False, lower_bound=None, inplace=False, out=None,
+              beta_is_logits=False, workspace=None, n_valid=None, **unused):
+    """fla's chunk_kda (the form the engine's eager prefill selects past 192 tokens, engine.py:946-949): the
+    arguments, outputs and state update of fused_recurrent_kda, computed 16 tokens at a time in closed form (the
+    same values up to the order of fp32 sums). workspace: from kda_chunk_workspace(T, H, K) (allocated when None)."""
+    return _kda("chunk_kda", True, q, k, v, g, beta, A_log, dt_bias, scale, initial_state, output_final_state,
+                use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound, inplace, out, beta_is_logits, workspace,
+                n_valid)
+
+
+def _kda(name, chunked, q, k, v, g, beta, A_log, dt_bias, scale, initial_state, output_final_state,
+         use_qk_l2norm_in_kernel, use_gate_in_kernel, lower_bound, inplace, out, beta_is_logits, workspace, n_valid):
     _mm.require_gpu(q, k, v, g, beta, A_log, dt_bias, initial_state, out, workspace, n_valid)
-    _check_count(n_valid, "fused_recurrent_kda")
+    _check_count(n_valid, name)
     if q.dim() != 4 or q.shape[0] != 1:
-        raise ValueError(f"fused_recurrent_kda: q must be [1, T, H, K] (got {tuple(q.shape)})")
+        raise ValueError(f"{name}: q must be [1, T, H, K] (got {tuple(q.shape)})")
     _, T, H, K = q.shape
     V = v.shape[-1]
-    for name, t in (("q", q), ("k", k), ("v", v)):
+    for nm, t in (("q", q), ("k", k), ("v", v)):
         if t.dtype != torch.bfloat16:
-            raise ValueError(f"fused_recurrent_kda: {name} must be bf16 (got {t.dtype})")
+            raise ValueError(f"{name}: {nm} must be bf16 (got {t.dtype})")
     q2, _, qts = _tokens(q, "q", H, K)
     k2, _, kts = _tokens(k, "k", H, K)
     v2, _, vts = _tokens(v, "v", H, V)
@@ -81,43 +107,43 @@ def fused_recurrent_kda(q, k, v, g, beta, A_log=None, dt_bias=None, scale=None, 
     gdt = _f32_or_bf16(g2, "g")
     b2 = beta[0] if beta.dim() == 3 else beta
     if tuple(b2.shape) != (T, H):
-        raise ValueError(f"fused_recurrent_kda: beta must be [1, T, H] (got {tuple(beta.shape)})")
+        raise ValueError(f"{name}: beta must be [1, T, H] (got {tuple(beta.shape)})")
     if b2.stride(1) != 1:
         b2 = b2.contiguous()
     bdt = _f32_or_bf16(b2, "beta")
     use_gate = bool(use_gate_in_kernel)
     if use_gate:
         if A_log is None or dt_bias is None:
-            raise ValueError("fused_recurrent_kda: use_gate_in_kernel needs A_log and dt_bias")
+            raise ValueError(f"{name}: use_gate_in_kernel needs A_log and dt_bias")
         A_log = A_log.float().reshape(H).contiguous()
         dt_bias = dt_bias.float().reshape(H * K).contiguous()
     if initial_state is None:
         state = torch.zeros(H, K, V, device=q.device, dtype=torch.float32)
     else:
         if initial_state.dtype != torch.float32 or tuple(initial_state.shape[-3:]) != (H, K, V):
-            raise ValueError(f"fused_recurrent_kda: initial_state must be fp32 [1, {H}, {K}, {V}]")
+            raise ValueError(f"{name}: initial_state must be fp32 [1, {H}, {K}, {V}]")
         if inplace:
             if not initial_state.is_contiguous():
-                raise ValueError("fused_recurrent_kda: inplace needs a contiguous initial_state")
+                raise ValueError(f"{name}: inplace needs a contiguous initial_state")
             state = initial_state
         else:
             state = initial_state.reshape(H, K, V).clone()
     o = torch.empty(T, H, V, device=q.device, dtype=torch.bfloat16) if out is None else out.view(T, H, V)
     if o.dtype != torch.bfloat16 or o.stride(2) != 1 or o.stride(1) != V:
-        raise ValueError("fused_recurrent_kda: out must be bf16 [1, T, H, V] with contiguous heads")
+        raise ValueError(f"{name}: out must be bf16 [1, T, H, V] with contiguous heads")
     sc = float(scale) if scale is not None else K ** -0.5
     lb = float("nan") if lower_bound is None else float(lower_bound)
     lib = _mm.load()
     ws = workspace
-    if ws is None and lib.mm_kda_recurrent_workspace(T, H, K) > 0:
-        ws = kda_workspace(T, H, K, q.device)
+    if ws is None and (lib.mm_kda_chunk_workspace if chunked else lib.mm_kda_recurrent_workspace)(T, H, K) > 0:
+        ws = (kda_chunk_workspace if chunked else kda_workspace)(T, H, K, q.device)
+    fn = lib.mm_kda_chunk if chunked else lib.mm_kda_recurrent
     with _mm.on_device(q):
-        _mm.check(lib.mm_kda_recurrent(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts,
-                                       _mm.ptr(b2), bdt, b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb,
-                                       1 if use_qk_l2norm_in_kernel else 0, 1 if use_gate else 0,
-                                       1 if beta_is_logits else 0, sc, T, H, K, V, _mm.ptr(state), _mm.ptr(o),
-                                       o.stride(0), _mm.ptr(n_valid), _mm.ptr(ws),
-                                       ws.numel() * 4 if ws is not None else 0, _mm.stream_of(q)), "fused_recurrent_kda")
+        _mm.check(fn(_mm.ptr(q2), qts, _mm.ptr(k2), kts, _mm.ptr(v2), vts, _mm.ptr(g2), gdt, gts, _mm.ptr(b2), bdt,
+                     b2.stride(0), _mm.ptr(A_log), _mm.ptr(dt_bias), lb, 1 if use_qk_l2norm_in_kernel else 0,
+                     1 if use_gate else 0, 1 if beta_is_logits else 0, sc, T, H, K, V, _mm.ptr(state), _mm.ptr(o),
+                     o.stride(0), _mm.ptr(n_valid), _mm.ptr(ws), ws.numel() * 4 if ws is not None else 0,
+                     _mm.stream_of(q)), name)
     final = None
     if output_final_state or inplace:
         final = state if (inplace and initial_state is not None) else state.reshape(1, H, K, V)

@@ -52,6 +52,10 @@ import thinker_attn as TA
 __all__ = ["FastThinkerStep"]
 
 _SCORING = ("sigmoid", "softmax")
+# Prompts longer than this take the KDA recurrence in chunked form (chunk_kda), as the engine switches its KDA layers'
+# mode (engine.py:946-949, 964-967). Measured per call over 16 heads of 128 x 128 (graph replays): 200 / 256 / 384 /
+# 512 tokens 42.1 / 48.2 / 71.2 / 87.1 us chunked against 43.2 / 51.7 / 72.7 / 93.4 us recurrent.
+KDA_CHUNK_ABOVE = 192
 
 
 def _norm(mod, what):
@@ -254,8 +258,9 @@ class FastThinkerStep:
     def prompt_mixer(self, li, h, n_valid=None):
         """The attention half of layer li over a prompt's T rows h [T, H] at positions pos_buf .. pos_buf + T - 1:
         h + o(mixer(input_layernorm(h))). KDA: the projection, the q / k / v short convolutions (their caches end
-        on the prompt's last real inputs), the f / g LoRA up-projections, fused_recurrent_kda from the layer's state
-        (the recurrent form for any T; padding rows past n_valid leave it unchanged), rms_norm_gated; MLA: the
+        on the prompt's last real inputs), the f / g LoRA up-projections, the recurrence from the layer's state
+        (fused_recurrent_kda up to KDA_CHUNK_ABOVE rows, chunk_kda beyond: the engine's mode switch,
+        engine.py:946-949; padding rows past n_valid leave the state unchanged), rms_norm_gated; MLA: the
         q | k | v projection and mla_prefill_attn (padding rows are stored past the real ones, where the next
         decode steps overwrite them before any query reads them)."""
         p = self.L[li]
@@ -277,11 +282,11 @@ class FastThinkerStep:
         base = 2 * nqk + nv
         f = self._rows(pr[:, base:base + R], p["f_b"])
         gg = self._rows(pr[:, base + R:base + 2 * R], p["g_b"])
-        o, _ = TA.fused_recurrent_kda(q.view(1, T, H, K), k.view(1, T, H, K), v.view(1, T, H, V), f.view(1, T, H, K),
-                                      pr[:, base + 2 * R:], A_log=p["A_log"], dt_bias=p["dt_bias"],
-                                      initial_state=p["state"], inplace=True, use_qk_l2norm_in_kernel=True,
-                                      use_gate_in_kernel=True, beta_is_logits=True, lower_bound=p["lower_bound"],
-                                      n_valid=n_valid)
+        kda = TA.chunk_kda if T > KDA_CHUNK_ABOVE else TA.fused_recurrent_kda
+        o, _ = kda(q.view(1, T, H, K), k.view(1, T, H, K), v.view(1, T, H, V), f.view(1, T, H, K), pr[:, base + 2 * R:],
+                   A_log=p["A_log"], dt_bias=p["dt_bias"], initial_state=p["state"], inplace=True,
+                   use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True, beta_is_logits=True,
+                   lower_bound=p["lower_bound"], n_valid=n_valid)
         ow, oe = p["o_norm"]
         on = TA.rms_norm_gated(o.reshape(T * H, V), gg.reshape(T * H, V), ow, oe)
         return self._rows(on.reshape(T, H * V), p["o"], p["o_b"], residual=h)

@@ -213,3 +213,23 @@ def test_decode_refuses_expert_spans_beyond_32_bit_offsets():
     ex.d_stride_n = 16384
     assert "n_tokens * nk" in _err(lib.mm_moe_decode(P, 10, 32768, ctypes.byref(ex), P, mm.MM_INT64, 7, 7, P, 7, None,
                                                      0, P, P, 32768, 0, None))
+
+
+def test_kda_chunk_workspace_and_argument_checks():
+    """mm_kda_chunk_workspace: one block of 49 K + 512 floats per (16-token chunk, head); mm_kda_chunk refuses a
+    short workspace before any launch, naming itself."""
+    lib = mm.load()
+    assert lib.mm_kda_chunk_workspace(2, 16, 128) == 0 == lib.mm_kda_recurrent_workspace(2, 16, 128)
+    assert lib.mm_kda_chunk_workspace(5, 16, 96) == -1
+    for T, H, K in ((512, 16, 128), (17, 3, 64), (3, 1, 128)):
+        rows = T * H * (3 * K + 4) * 4
+        assert lib.mm_kda_recurrent_workspace(T, H, K) == rows
+        assert lib.mm_kda_chunk_workspace(T, H, K) == (T + 15) // 16 * H * (49 * K + 512) * 4
+    rc = lib.mm_kda_chunk(16, 2048, 16, 2048, 16, 2048, 16, mm.MM_FP32, 2048, 16, mm.MM_FP32, 16, None, None,
+                          float("nan"), 1, 0, 0, 1.0, 40, 16, 128, 128, 16, 16, 2048, None, 16,
+                          lib.mm_kda_chunk_workspace(40, 16, 128) - 16, None)
+    assert rc == mm.MM_ERR_ARG and "kda_chunk" in mm.last_error() and "workspace" in mm.last_error()
+    with pytest.raises(ValueError, match="no CPU path"):
+        import thinker_attn
+        z = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)
+        thinker_attn.chunk_kda(z, z, z, z, torch.zeros(1, 4, 2))

@@ -51,6 +51,51 @@ def test_kda_recurrent_matches_oracle(T, H, K, V, gate):
     torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
 
 
+@pytest.mark.parametrize("T,H,K,V", [(2, 3, 128, 32), (3, 5, 64, 64), (9, 3, 128, 64), (16, 1, 128, 8), (17, 2, 128, 128),
+                                     (33, 2, 64, 56), (37, 2, 128, 40), (130, 3, 128, 128), (200, 2, 128, 128)])
+@pytest.mark.parametrize("gate", ["softplus", "lower_bound", "none"])
+def test_kda_chunk_matches_oracle(T, H, K, V, gate):
+    """chunk_kda (16-token chunks in closed form) against the float64 recurrence, chunk boundaries and partial last
+    chunks included; T <= 2 takes the one-launch decode kernel."""
+    print(f"[kda chunk] T={T} H={H} K={K} V={V} gate={gate}", flush=True)
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 700 + T + K, torch.bfloat16 if gate == "none" else torch.float32)
+    if gate == "none":
+        g = (-0.1 * g.float().abs()).to(BF)
+    lb = -5.0 if gate == "lower_bound" else None
+    o, fin = TA.chunk_kda(q, k, v, g, beta, A_log=A_log, dt_bias=dt, initial_state=S0, output_final_state=True,
+                          use_qk_l2norm_in_kernel=True, use_gate_in_kernel=gate != "none", lower_bound=lb)
+    ro, rS = A.kda_recurrent(q[0].cpu(), k[0].cpu(), v[0].cpu(), g[0].cpu(), beta[0].cpu(), S0[0].cpu(),
+                             A_log=A_log.cpu(), dt_bias=dt.cpu(), use_gate=gate != "none", lower_bound=lb)
+    close(o[0], ro)
+    torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
+
+
+def test_kda_chunk_full_prompt_and_strong_decay():
+    """The hybrid thinker's shape, 512 tokens over 16 heads of 128 x 128, against the float64 recurrence; then decays
+    of e^-30 .. e^-80 per token, whose products over a chunk underflow: the chunk form takes them as products, never
+    as ratios, so the outputs stay finite and match."""
+    H, K, V, T = 16, 128, 128, 512
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 720)
+    beta = W.normal((1, T, H), 1.0, 721, DEV)
+    kw = dict(A_log=A_log, dt_bias=dt, output_final_state=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+              beta_is_logits=True)
+    print("[kda chunk] 512 tokens x 16 heads", flush=True)
+    o, fin = TA.chunk_kda(q, k, v, g, beta, initial_state=S0, **kw)
+    ro, rS = A.kda_recurrent(q[0].cpu(), k[0].cpu(), v[0].cpu(), g[0].cpu(), torch.sigmoid(beta[0].float()).cpu(),
+                             S0[0].cpu(), A_log=A_log.cpu(), dt_bias=dt.cpu())
+    close(o[0], ro)
+    torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
+    T = 48
+    q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, 2, K, V, 730, torch.bfloat16)
+    g = (-30.0 - 50.0 * torch.rand(g.shape, generator=torch.Generator().manual_seed(731))).to(DEV, BF)  # log decays
+    print("[kda chunk] strong decay", flush=True)
+    o, fin = TA.chunk_kda(q, k, v, g, beta, initial_state=S0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert torch.isfinite(o).all() and torch.isfinite(fin).all()
+    ro, rS = A.kda_recurrent(q[0].cpu(), k[0].cpu(), v[0].cpu(), g[0].cpu(), beta[0].cpu(), S0[0].cpu(), use_gate=False)
+    close(o[0], ro)
+    torch.testing.assert_close(fin[0].cpu().double(), rS, rtol=1e-3, atol=1e-4)
+
+
 def test_kda_inplace_decode_steps_and_graph_replays():
     """A decode step (T = 1) updates the state in place; a captured step replayed with new tokens advances it
     exactly as eager steps do."""
@@ -91,29 +136,32 @@ def test_kda_zero_write_strength_keeps_the_state():
     assert torch.equal(fin, S0)
 
 
-def test_kda_prompt_recurrence_is_deterministic():
-    """The prompt form's waves share each staged chunk (and its v values) through LDS; a wave running ahead into the
+@pytest.mark.parametrize("chunked", [False, True])
+def test_kda_prompt_recurrence_is_deterministic(chunked):
+    """The prompt forms' waves share each staged chunk (and its v values) through LDS; a wave running ahead into the
     next chunk must not overwrite what the others still read. Five runs of a 300-token prompt (19 chunks) over 16
-    heads from one state, eagerly and from a graph, give the same outputs and states bit for bit."""
+    heads from one state, eagerly and from a graph, give the same outputs and states bit for bit (fused_recurrent_kda
+    and chunk_kda)."""
     H, K, V, T = 16, 128, 128, 300
+    fn = TA.chunk_kda if chunked else TA.fused_recurrent_kda
     q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 640)
     beta = W.normal((1, T, H), 1.0, 641, DEV)
     kw = dict(A_log=A_log, dt_bias=dt, inplace=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
               beta_is_logits=True)
     st = S0.clone()
-    o_ref, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, **kw)
+    o_ref, _ = fn(q, k, v, g, beta, initial_state=st, **kw)
     s_ref = st.clone()
-    ws = TA.kda_workspace(T, H, K, DEV)
+    ws = (TA.kda_chunk_workspace if chunked else TA.kda_workspace)(T, H, K, DEV)
     out = torch.empty_like(o_ref)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr, stream=s):
-        TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, out=out, workspace=ws, **kw)
+        fn(q, k, v, g, beta, initial_state=st, out=out, workspace=ws, **kw)
     for i in range(5):
         st.copy_(S0)
-        o, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=st, **kw)
+        o, _ = fn(q, k, v, g, beta, initial_state=st, **kw)
         torch.cuda.synchronize()
         assert torch.equal(o, o_ref) and torch.equal(st, s_ref), ("eager", i)
         st.copy_(S0)
@@ -123,22 +171,24 @@ def test_kda_prompt_recurrence_is_deterministic():
         assert torch.equal(out, o_ref) and torch.equal(st, s_ref), ("graph", i)
 
 
-@pytest.mark.parametrize("T,n,H,V", [(32, 20, 3, 128), (40, 33, 2, 64), (2, 1, 4, 128), (17, 0, 2, 128), (16, 16, 1, 32)])
-def test_kda_padding_tokens_leave_the_state_unchanged(T, n, H, V):
+@pytest.mark.parametrize("T,n,H,V", [(32, 20, 3, 128), (40, 33, 2, 64), (2, 1, 4, 128), (17, 0, 2, 128), (16, 16, 1, 32),
+                                     (64, 23, 2, 128)])
+@pytest.mark.parametrize("chunked", [False, True])
+def test_kda_padding_tokens_leave_the_state_unchanged(T, n, H, V, chunked):
     """A prompt padded from n to T tokens with n_valid = n (the engine's prefill graphs): the state after it and the
-    first n outputs equal those of the n-token prompt bit for bit, whatever the padding rows hold."""
+    first n outputs equal those of the n-token prompt bit for bit, whatever the padding rows hold (both forms: in the
+    chunk form a padding token's u is 0 and its decay 1, so it adds exact zeros and multiplies by exact ones)."""
     K = 128
-    print(f"[kda pad] T={T} n={n} H={H} V={V}", flush=True)
+    fn = TA.chunk_kda if chunked else TA.fused_recurrent_kda
+    print(f"[kda pad] T={T} n={n} H={H} V={V} chunked={chunked}", flush=True)
     q, k, v, g, beta, A_log, dt, S0 = _kda_inputs(T, H, K, V, 600 + T)
     beta = W.normal((1, T, H), 1.0, 610, DEV)  # logits
     kw = dict(A_log=A_log, dt_bias=dt, inplace=True, use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
               beta_is_logits=True)
     s_pad, s_ref = S0.clone(), S0.clone()
-    o_pad, _ = TA.fused_recurrent_kda(q, k, v, g, beta, initial_state=s_pad,
-                                      n_valid=torch.tensor([n], device=DEV), **kw)
+    o_pad, _ = fn(q, k, v, g, beta, initial_state=s_pad, n_valid=torch.tensor([n], device=DEV), **kw)
     if n:
-        o_ref, _ = TA.fused_recurrent_kda(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], initial_state=s_ref,
-                                          **kw)
+        o_ref, _ = fn(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], initial_state=s_ref, **kw)
         assert torch.equal(o_pad[:, :n], o_ref)
     assert torch.equal(s_pad, s_ref)
 
@@ -591,6 +641,29 @@ def _states_close(a, b, what, rows=None, exact=False, min_cos=0.999, keys=("stat
                     continue
                 c = float(F.cosine_similarity(ta.float().reshape(-1), tb.float().reshape(-1), dim=0))
                 assert c > min_cos, (what, li, key, c)
+
+
+def test_fast_thinker_long_prompt_takes_the_chunked_recurrence(monkeypatch):
+    """Past KDA_CHUNK_ABOVE rows the prompt's KDA layers run chunk_kda (the engine's chunk mode, engine.py:946-949);
+    the same 200-token prompt with the recurrent form in every layer gives the same logits and layer states to the
+    fp32 level (the two forms differ only in the order of their fp32 sums)."""
+    import thinker_step
+    T, pos = 200, 300
+    a = W.HybridThinkerStep(4, DEV, pos=pos, seed=7500)
+    b = W.HybridThinkerStep(4, DEV, pos=pos, seed=7500)
+    ids = torch.randint(0, a.embed.shape[0], (T,), generator=torch.Generator().manual_seed(7501)).to(DEV)
+    calls, orig = [], TA.chunk_kda
+    monkeypatch.setattr(TA, "chunk_kda", lambda *x, **kw: (calls.append(1), orig(*x, **kw))[1])
+    print("[hybrid prefill] 200 tokens, chunked KDA", flush=True)
+    la = a.fast.prefill(ids)
+    assert len(calls) == 3  # the 3 KDA layers
+    monkeypatch.setattr(thinker_step, "KDA_CHUNK_ABOVE", 1 << 30)
+    print("[hybrid prefill] 200 tokens, recurrent KDA", flush=True)
+    lb = b.fast.prefill(ids)
+    torch.cuda.synchronize()
+    assert len(calls) == 3 and int(a.pos) == int(b.pos) == pos + T
+    assert float(F.cosine_similarity(la.float().reshape(-1), lb.float().reshape(-1), dim=0)) > 0.999
+    _states_close(a.state_copy(), b.state_copy(), "chunked vs recurrent", rows=slice(0, pos + T))
 
 
 def test_fast_thinker_prefill_graph_for_a_bucket_serves_shorter_prompts():
