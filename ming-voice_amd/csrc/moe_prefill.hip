@@ -52,6 +52,12 @@ constexpr int kXcds = 8;
 #ifndef MM_PREFILL_DOWN_WAVES_BF16
 #define MM_PREFILL_DOWN_WAVES_BF16 8
 #endif
+#ifndef MM_PREFILL_GU_WAVES_INT8
+#define MM_PREFILL_GU_WAVES_INT8 4
+#endif
+#ifndef MM_PREFILL_DOWN_WAVES_INT8
+#define MM_PREFILL_DOWN_WAVES_INT8 4
+#endif
 
 // Rows per piece of the prefill copy of w_gu: [E1][2I/R][H/64][R][64], so a 64-k slab of R consecutive rows is
 // one piece of R * 64 weights. bf16: R = 8 makes a piece the 1 KB that one direct-load instruction of a wave fills
@@ -547,8 +553,8 @@ template <bool Q, int BM>
 int launch_gemms(const PrefillArgs& a, int64_t nb, int phases, hipStream_t st) {
   constexpr int GU_BN = Q ? MM_PREFILL_GU_BN_INT8 : MM_PREFILL_GU_BN_BF16;
   constexpr int DOWN_BN = Q ? MM_PREFILL_DOWN_BN_INT8 : MM_PREFILL_DOWN_BN_BF16;
-  constexpr int GU_NW = Q ? 4 : MM_PREFILL_GU_WAVES_BF16;
-  constexpr int DOWN_NW = Q ? 4 : MM_PREFILL_DOWN_WAVES_BF16;
+  constexpr int GU_NW = Q ? MM_PREFILL_GU_WAVES_INT8 : MM_PREFILL_GU_WAVES_BF16;
+  constexpr int DOWN_NW = Q ? MM_PREFILL_DOWN_WAVES_INT8 : MM_PREFILL_DOWN_WAVES_BF16;
   int rc;
   if (phases & MM_PHASE_GATE_UP) {
     rc = a.gu_slabs ? launch_gate_up<Q, GU_BN, GU_NW, BM, true>(a, nb, st) : launch_gate_up<Q, GU_BN, GU_NW, BM, false>(a, nb, st);
