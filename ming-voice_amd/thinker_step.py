@@ -242,27 +242,30 @@ class FastThinkerStep:
     # -------------------------------------------------------------------------------------------- prefill
 
     @staticmethod
-    def _rows(x, w, b=None, residual=None, norm=None):
+    def _rows(x, w, b=None, residual=None, norm=None, in_place=False):
         """A projection of T rows: up to fastlinear.MAX_M rows on the small_linear GEMV (norm and residual fused),
         more as rms_norm (HIP) -> the library GEMM (hipBLASLt through torch; the residual, without a bias, as its C
-        operand), the form of the reference's own prefill (nn.Linear after the patched norm, engine.py:220-228)."""
+        operand), the form of the reference's own prefill (nn.Linear after the patched norm, engine.py:220-228).
+        in_place: the residual is a buffer nobody reads afterwards, so the GEMM accumulates into it (beta = 1 on C = D,
+        the same single rounding) instead of first copying it into a new output."""
         if x.shape[0] <= fastlinear.MAX_M:
             return fastlinear.small_linear(x, w, b=b, residual=residual, norm=norm)
         if norm is not None:
             x = fused_ops.rms_norm(x, norm[0], norm[1])
         if residual is not None and b is None:
-            return torch.addmm(residual, x, w.t())
+            return residual.addmm_(x, w.t()) if in_place else torch.addmm(residual, x, w.t())
         y = F.linear(x, w, b)
         return y if residual is None else y.add_(residual)
 
-    def prompt_mixer(self, li, h, n_valid=None):
+    def prompt_mixer(self, li, h, n_valid=None, own=False):
         """The attention half of layer li over a prompt's T rows h [T, H] at positions pos_buf .. pos_buf + T - 1:
         h + o(mixer(input_layernorm(h))). KDA: the projection, the q / k / v short convolutions (their caches end
         on the prompt's last real inputs), the f / g LoRA up-projections, the recurrence from the layer's state
         (fused_recurrent_kda up to KDA_CHUNK_ABOVE rows, chunk_kda beyond: the engine's mode switch,
         engine.py:946-949; padding rows past n_valid leave the state unchanged), rms_norm_gated; MLA: the
         q | k | v projection and mla_prefill_attn (padding rows are stored past the real ones, where the next
-        decode steps overwrite them before any query reads them)."""
+        decode steps overwrite them before any query reads them). own: h is the step's and dead after this call, so
+        the o projection past fastlinear.MAX_M rows adds into it in place."""
         p = self.L[li]
         T = h.shape[0]
         if p["kind"] == "mla":
@@ -273,7 +276,7 @@ class FastThinkerStep:
                 nq = p["nh"] * p["dqk"]
                 q, k, v = qkv[:, :nq], qkv[:, nq:2 * nq], qkv[:, 2 * nq:]
             o = TA.mla_prefill_attn(q, k, v, p["kc"], p["vc"], self.pos)
-            return self._rows(o, p["o"], p["o_b"], residual=h)
+            return self._rows(o, p["o"], p["o_b"], residual=h, in_place=own)
         H, K, V, R = p["heads"], p["K"], p["V"], p["rank"]
         pr = self._rows(h, p["proj"], p["proj_b"], norm=p["ln1"])
         nqk, nv = H * K, H * V
@@ -289,7 +292,7 @@ class FastThinkerStep:
                    lower_bound=p["lower_bound"], n_valid=n_valid)
         ow, oe = p["o_norm"]
         on = TA.rms_norm_gated(o.reshape(T * H, V), gg.reshape(T * H, V), ow, oe)
-        return self._rows(on.reshape(T, H * V), p["o"], p["o_b"], residual=h)
+        return self._rows(on.reshape(T, H * V), p["o"], p["o_b"], residual=h, in_place=own)
 
     def prompt_moe(self, li, h):
         """The MoE half of layer li over T rows: moe_block_decode up to fused_moe.MAX_DECODE_TOKENS rows (the
@@ -338,12 +341,14 @@ class FastThinkerStep:
             raise ValueError("FastThinkerStep.prefill: n_valid must be a one-element int64 tensor on the device")
         nv = None if n_valid is None else n_valid.reshape(1).clamp(0, T)
         out = []
+        owned = ids is not None  # the embedding rows are the step's own; rows handed in are the caller's
         for li in range(len(self.L)):
-            h_in = h
-            hm = self.prompt_mixer(li, h, nv)
+            h_in = h.clone() if trace else None
+            # a layer's input is dead after its mixer unless it is the caller's: the o projection then adds into it
+            hm = self.prompt_mixer(li, h, nv, own=owned or li > 0)
             h, rid, rw = self.prompt_moe(li, hm)
             if trace:
-                out.append((h_in.clone(), hm.clone(), rid.clone(), rw.clone()))
+                out.append((h_in, hm.clone(), rid.clone(), rw.clone()))
         last = h[-1:] if nv is None else TA.embed_rows(h, (nv - 1).clamp_(min=0))
         logits = self.head_logits(last)
         TA.argmax_rows(logits, out=self.tok)
