@@ -480,7 +480,11 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
 
 // -------------------------------------------------------------------------------------------- combine
 
-// One thread per 8 consecutive outputs of a token: y = bf16(sum_k w_k * part_k) (+ residual, rounded again).
+// One thread per 8 consecutive outputs of a token: y = bf16(sum_k w_k * part_k) (+ residual, rounded again), slots
+// in order. MAXK > 0: up to MAXK slots, every slot's id, weight and part chunk loaded before the first sum (a dropped
+// pair's part row is never written: its term is skipped by a select, not multiplied by zero), so the thread waits
+// for memory once; MAXK = 0: any number of slots, one at a time.
+template <int MAXK, bool I64>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   const int64_t H8 = a.H / 8;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -489,17 +493,49 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int k = 0; k < a.nk; ++k) {
-    const int64_t p = t * a.nk + k;
-    const int64_t id = load_id(a.ids, a.ids_dtype, p);
-    if (id < 0 || id >= a.E1) continue;  // dropped pairs have no row
-    const float w = a.wts[p];
-    const uint4 v = *reinterpret_cast<const uint4*>(a.part + p * a.H + h);
+  auto add = [&](bool ok, float w, const uint4& v) {
     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(w, __uint_as_float(u[i] << 16), acc[2 * i]);
-      acc[2 * i + 1] = fmaf(w, __uint_as_float(u[i] & 0xffff0000u), acc[2 * i + 1]);
+      acc[2 * i] = ok ? fmaf(w, __uint_as_float(u[i] << 16), acc[2 * i]) : acc[2 * i];
+      acc[2 * i + 1] = ok ? fmaf(w, __uint_as_float(u[i] & 0xffff0000u), acc[2 * i + 1]) : acc[2 * i + 1];
+    }
+  };
+  uint16_t rraw[8];  // the residual, fetched with the slots' loads
+  if (a.res) {
+    const uint16_t* rr = a.res + t * a.res_rs + h;
+    if ((reinterpret_cast<uintptr_t>(a.res) & 15) == 0 && (a.res_rs & 7) == 0) {  // uniform
+      const uint4 r = *reinterpret_cast<const uint4*>(rr);
+      const uint32_t ru[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rraw[2 * i] = static_cast<uint16_t>(ru[i] & 0xffff);
+        rraw[2 * i + 1] = static_cast<uint16_t>(ru[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rraw[i] = rr[i];
+    }
+  }
+  if constexpr (MAXK > 0) {
+    int64_t id[MAXK];
+    float w[MAXK];
+    uint4 v[MAXK];
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {  // slots past nk load the last slot again (not used)
+      const int64_t p = t * a.nk + min(k, a.nk - 1);
+      id[k] = I64 ? static_cast<const int64_t*>(a.ids)[p] : static_cast<const int32_t*>(a.ids)[p];
+      w[k] = a.wts[p];
+      v[k] = *reinterpret_cast<const uint4*>(a.part + p * a.H + h);
+    }
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) add(k < a.nk && id[k] >= 0 && id[k] < a.E1, w[k], v[k]);
+  } else {
+    for (int k = 0; k < a.nk; ++k) {
+      const int64_t p = t * a.nk + k;
+      const int64_t id = load_id(a.ids, a.ids_dtype, p);
+      if (id < 0 || id >= a.E1) continue;  // dropped pairs have no row
+      add(true, a.wts[p], *reinterpret_cast<const uint4*>(a.part + p * a.H + h));
     }
   }
   uint32_t o[4];
@@ -507,8 +543,8 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   for (int i = 0; i < 4; ++i) {
     float lo = round_bf16(acc[2 * i]), hi = round_bf16(acc[2 * i + 1]);
     if (a.res) {
-      lo += bf16_to_f32(a.res[t * a.res_rs + h + 2 * i]);
-      hi += bf16_to_f32(a.res[t * a.res_rs + h + 2 * i + 1]);
+      lo += bf16_to_f32(rraw[2 * i]);
+      hi += bf16_to_f32(rraw[2 * i + 1]);
     }
     o[i] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
   }
@@ -524,6 +560,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
   }
 }
 
+constexpr int kCombineMaxK = 16;
 
 template <bool Q, int BN, int NW, int BM, bool SL>
 int launch_gate_up(const PrefillArgs& a, int64_t nb, hipStream_t st) {
@@ -728,7 +765,13 @@ extern "C" int mm_moe_prefill(const void* x, int64_t n_tokens, int64_t x_row_str
   }
   if (!(phases & MM_PHASE_COMBINE)) return MM_OK;
   const int64_t total = n_tokens * (a.H / 8);
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, st, a);
+  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+  const bool i64 = ids_dtype == MM_INT64;
+  if (nk <= 8 && i64) hipLaunchKernelGGL((prefill_combine_kernel<8, true>), grid, dim3(256), 0, st, a);
+  else if (nk <= 8) hipLaunchKernelGGL((prefill_combine_kernel<8, false>), grid, dim3(256), 0, st, a);
+  else if (nk <= kCombineMaxK && i64) hipLaunchKernelGGL((prefill_combine_kernel<kCombineMaxK, true>), grid, dim3(256), 0, st, a);
+  else if (nk <= kCombineMaxK) hipLaunchKernelGGL((prefill_combine_kernel<kCombineMaxK, false>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((prefill_combine_kernel<0, false>), grid, dim3(256), 0, st, a);
   return mm::check_launch("moe_prefill combine");
 }
 
