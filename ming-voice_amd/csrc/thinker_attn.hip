@@ -27,6 +27,11 @@ namespace {
 using namespace mmd;
 
 __device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+// v, or zero when !ok (a select per dword, no branch)
+__device__ __forceinline__ uint4 and_mask16(const uint4& v, bool ok) {
+  const uint32_t m = ok ? ~0u : 0u;
+  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
 __device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
 // Orders a wave's LDS stores before its later loads (and loads before later stores) without a workgroup barrier:
@@ -1389,34 +1394,48 @@ __global__ __launch_bounds__(NW * 64) void mla_prefill_attn_kernel(MlaPrefillArg
   const int ndg = a.dv / 8;
   for (int kt = wave; kt < ntiles; kt += NW) {
     const int64_t j0 = static_cast<int64_t>(kt) * kMlaPKeys;
+    // every load of the tile first, unconditionally (rows and dims past the ends read the row's first piece and are
+    // zeroed after), so the tile costs one trip to memory: where each load sat behind its own range test, the
+    // compiler waited for each before the next (16 round trips per tile)
     // value tile: lane piece i = lane + 64 r -> key pair kp = i % 16, dim group dg = i / 16
     uint4 va[RV], vb[RV];
+    bool oka[RV], okb[RV];
 #pragma unroll
     for (int r = 0; r < RV; ++r) {
       const int i = lane + kWave * r, kp = i % 16, dg = i / 16;
       const int64_t ja = j0 + 2 * kp;
-      va[r] = vb[r] = make_uint4(0, 0, 0, 0);
-      if (dg < ndg) {
-        if (ja < kend) va[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + ja) * a.dv + 8 * dg);
-        if (ja + 1 < kend) vb[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + ja + 1) * a.dv + 8 * dg);
-      }
+      const bool dok = dg < ndg;
+      oka[r] = dok && ja < kend;
+      okb[r] = dok && ja + 1 < kend;
+      va[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + (oka[r] ? ja : 0)) * a.dv + (oka[r] ? 8 * dg : 0));
+      vb[r] = *reinterpret_cast<const uint4*>(a.vc + (hk + (okb[r] ? ja + 1 : 0)) * a.dv + (okb[r] ? 8 * dg : 0));
     }
-    floatx4 s[2];
+    uint4 kx[2][8];
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const int64_t j = j0 + 16 * n + lr;
       const bool live = j < kend;
       const uint16_t* krow = a.kc + (hk + (live ? j : 0)) * a.dqk;
-      s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
         const int d = 32 * kk + 8 * lq;
-        if (kk < nkq) {
-          uint4 x = make_uint4(0, 0, 0, 0);
-          if (live && d < a.dqk) x = *reinterpret_cast<const uint4*>(krow + d);
-          s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, x), qf[kk], s[n], 0, 0, 0);
-        }
+        const bool ok = live && d < a.dqk;
+        kx[n][kk] = and_mask16(*reinterpret_cast<const uint4*>(krow + (ok ? d : 0)), ok);
       }
+    }
+#pragma unroll
+    for (int r = 0; r < RV; ++r) {
+      va[r] = and_mask16(va[r], oka[r]);
+      vb[r] = and_mask16(vb[r], okb[r]);
+    }
+    floatx4 s[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        if (kk < nkq)
+          s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kx[n][kk]), qf[kk], s[n], 0, 0, 0);
     }
     // the transposed value tile: dword (dim 8 dg + e, keys 2 kp, 2 kp + 1); 16 consecutive key pairs per dim
     // row and 4 dim groups 8 x 18 dwords apart per store keep the 64 lanes on distinct banks
