@@ -188,6 +188,88 @@ __device__ __forceinline__ float group_sum(float v) {
 // Sum over the lanes of a wave (all lanes get the total).
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Transposed sums (group_sums below) keep, in their step on lane bit B of groups of W lanes, the half of a lane's
+// values that this bit selects (1: the upper half). It is the lane bit itself, xor a higher bit that the later
+// mirror steps flip along with it: 0, 1 take bit 2 (flipped by the half mirror and the mirror), 2 takes bit 3
+// (the mirror), so that the half mirror (lane i <-> 7 - i) and mirror (i <-> 15 - i) partners of group_sum hold the
+// same values' partials as the lane.
+template <int B, int W>
+__device__ __forceinline__ int sums_hi(int lane) {
+  const int b = (lane >> B) & 1;
+  if constexpr (B <= 1) return b ^ (W > 4 ? (lane >> 2) & 1 : 0);
+  else if constexpr (B == 2) return b ^ (W > 8 ? (lane >> 3) & 1 : 0);
+  else return b;
+}
+
+// group_sum's pair step on lane bit B: partner xor 1, xor 2, half mirror, mirror, across rows, across halves.
+template <int B>
+__device__ __forceinline__ float pair_sum_bit(float v) {
+  if constexpr (B == 0) return v + dpp_f32<kDppXor1>(v);
+  else if constexpr (B == 1) return v + dpp_f32<kDppXor2>(v);
+  else if constexpr (B == 2) return v + dpp_f32<kDppHalfMirror>(v);
+  else if constexpr (B == 3) return v + dpp_f32<kDppMirror>(v);
+  else if constexpr (B == 4) return row_pair_sum(v);
+  else return half_pair_sum(v);
+}
+
+// One transposed step on lane bit B: 2H values -> H, each lane of a pair keeping the half its select bit names and
+// adding the partner's copy of it.
+template <int B, int W, int H>
+__device__ __forceinline__ void group_sums_step(float* x) {
+  if constexpr (B < 4) {
+    const bool hi = sums_hi<B, W>(lane_id());
+#pragma unroll
+    for (int v = 0; v < H; ++v) {
+      const float keep = hi ? x[v + H] : x[v], send = hi ? x[v] : x[v + H];
+      constexpr int ctrl = B == 0 ? kDppXor1 : B == 1 ? kDppXor2 : B == 2 ? kDppHalfMirror : kDppMirror;
+      x[v] = keep + dpp_f32<ctrl>(send);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < H; ++v) {  // rows 0 / 2 (bit 4) or lanes 0-31 (bit 5) keep v, the others v + H
+      const auto r = B == 4 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x[v]), __float_as_uint(x[v + H]), false, false)
+                            : __builtin_amdgcn_permlane32_swap(__float_as_uint(x[v]), __float_as_uint(x[v + H]), false, false);
+      x[v] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  }
+}
+
+template <int B, int W, int N>
+__device__ __forceinline__ void group_sums_from(float* x) {
+  if constexpr ((1 << B) < W) {
+    if constexpr (N > 1) group_sums_step<B, W, N / 2>(x);
+    else x[0] = pair_sum_bit<B>(x[0]);
+    group_sums_from<B + 1, W, (N > 1 ? N / 2 : 1)>(x);
+  }
+}
+
+// Sums of N values over aligned groups of W lanes (powers of two, N <= W <= 64), transposed: on lane bits 0, 1, ...
+// in turn, the lanes of each pair split their values in half while more than one is left (group_sums_step), then
+// sum the last one (pair_sum_bit). Every step pairs the lanes as group_sum's does and adds the partials of one value
+// over the same two lane sets, so each total is group_sum's of that value, bit for bit; a lane makes N - 1 +
+// log2 W - log2 N exchanges, where N group_sum calls take N log2 W. Lane l's x[0] ends as the total of value
+// sums_index<W, N>(l).
+template <int W, int N>
+__device__ __forceinline__ void group_sums(float (&x)[N]) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0 && N >= 1 && N <= W && (N & (N - 1)) == 0, "group sums");
+  group_sums_from<0, W, N>(x);
+}
+
+template <int B, int W, int N>
+__device__ __forceinline__ int sums_index_from(int lane) {
+  if constexpr ((1 << B) < N) return sums_hi<B, W>(lane) * (N >> (B + 1)) + sums_index_from<B + 1, W, N>(lane);
+  else return 0;
+}
+
+// The value whose total lane `lane` holds after group_sums<W, N>: sum over b < log2 N of its select bit b times
+// N / 2^(b+1). Lane ^ 1 holds value index +- N / 2 (only select bit 0 differs).
+template <int W, int N>
+__device__ __forceinline__ int sums_index(int lane) {
+  return sums_index_from<0, W, N>(lane);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f32<kDppXor1>(v));
   v = fmaxf(v, dpp_f32<kDppXor2>(v));
@@ -199,7 +281,6 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
 // Global operands of the latency-bound kernels are read through buffer resources (a wave-uniform base and
 // byte size): a load at an offset past the end returns zero, so a lane past a row's end is given kPast as

@@ -78,19 +78,6 @@ struct Act {
   uint4 v[Q ? 2 : 1];
 };
 
-__device__ __forceinline__ uint4 and_mask(const uint4& v, uint32_t m) {
-  return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-}
-
-// Chunk c of an LDS row; a lane past the row (ok false) reads the row's first chunk and zeroes it.
-template <bool Q>
-__device__ __forceinline__ void lds_act(Act<Q>& o, const uint16_t* row, int64_t c, bool ok) {
-  const uint4* p = reinterpret_cast<const uint4*>(row) + (ok ? c : 0) * (Q ? 2 : 1);
-  const uint32_t m = ok ? ~0u : 0u;
-  o.v[0] = and_mask(p[0], m);
-  if (Q) o.v[Q ? 1 : 0] = and_mask(p[1], m);
-}
-
 // Activation chunk c (CE bf16 values) of the row starting at byte `row` of resource r; kPast when !ok.
 template <bool Q>
 __device__ __forceinline__ void buf_act(Act<Q>& o, rsrc_t r, uint32_t row, int64_t c, bool ok) {
@@ -132,14 +119,26 @@ __device__ __forceinline__ void gate_up_store(const DecodeArgs& a, int64_t r, in
   a.a_buf[static_cast<int64_t>(p) * a.I + r] = f32_to_bf16(act * uu);
 }
 
-// The int8 row scales of gate row r and up row r + I of expert e (1 for bf16 weights).
+// The int8 row scales of gate row r and up row r + I of expert e (1 for bf16 weights). Loaded without a branch on
+// the scale type: through buffer resources over the expert's scale row of both types, the one of the other type
+// empty (its loads read zero and touch no memory), so the bits combine by an or and nothing waits for these loads
+// until the epilogue uses them (a load per type behind a branch made the wave wait for it, and for every load
+// issued before it, on the spot).
 template <bool Q>
 __device__ __forceinline__ void gate_up_scales(const DecodeArgs& a, int e, int64_t r, bool rok, float& sg, float& su) {
   sg = su = 1.f;
   if (Q) {
-    const int64_t base = static_cast<int64_t>(e) * a.sgu_se + (rok ? r : 0);
-    sg = load_scale(a.s_gu, a.s_dtype, base);
-    su = load_scale(a.s_gu, a.s_dtype, base + a.I);
+    const bool b16 = a.s_dtype == MM_BF16;
+    const char* row = static_cast<const char*>(a.s_gu) + static_cast<int64_t>(e) * a.sgu_se * (b16 ? 2 : 4);
+    const rsrc_t r16 = make_rsrc(row, b16 ? 2 * a.I * 2 : 0), r32 = make_rsrc(row, b16 ? 0 : 2 * a.I * 4);
+    const uint32_t i = static_cast<uint32_t>(rok ? r : 0), iu = i + static_cast<uint32_t>(a.I);
+    auto ld = [&](uint32_t k) {
+      const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r16, k * 2, 0, 0));
+      const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r32, k * 4, 0, 0));
+      return __uint_as_float((lo << 16) | w);
+    };
+    sg = ld(i);
+    su = ld(iu);
   }
 }
 
@@ -195,40 +194,45 @@ __device__ __forceinline__ void gate_up_one(const DecodeArgs& a, int e, int p, c
   }
 }
 
-// Several tokens per expert: their activation rows are staged in LDS (bf16). Each weight row pair is loaded
-// once into registers and dotted with every staged row in turn, so registers hold only the weight chunks.
-// int8 chunks are widened once per row pair to packed bf16 (exact) and dotted with v_dot2_f32_bf16: two products
-// per operation and 8 VGPRs per chunk, where widening to fp32 per token or once and keeping the floats (16 VGPRs
-// per chunk, 111 VGPRs at 8 tokens) took longer (gate/up over 28 cold layers at 2 / 4 / 8 tokens 18.7 / 31.4 /
-// 54.6 -> 18.5 / 30.2 / 53.7 us). Requesting the weights before the staging changed nothing (19.0 / 31.1 / 55.3).
+// Several tokens per expert: their activation rows are staged in LDS (bf16), each padded with zeros to the LPR * NC
+// chunks that the lanes of a row cover, so the reads need no mask (a chunk past the row's end adds 0 * 0 products, as
+// the masked reads of the one-token kernel do). The staging issues all of a thread's loads before its stores (one
+// trip to memory; issued one by one behind their range tests, the loads had waited for each other). Each weight row
+// pair is loaded once into registers and dotted with every staged row in turn. int8 chunks are widened once per row
+// pair to packed bf16 (exact) and dotted with v_dot2_f32_bf16: two products per operation and 8 VGPRs per chunk,
+// where widening to fp32 per token or once and keeping the floats (16 VGPRs per chunk, 111 VGPRs at 8 tokens) took
+// longer; the next row pair's int8 weights are requested into the raw registers once these are widened, so they
+// stream during this pair's dots. The gate and up sums of G tokens are reduced over the row's lanes together
+// (group_sums: group_sum's totals, bit for bit) and the lanes then run the epilogue of one token each, where a sum
+// and an epilogue per token and row were three quarters of the wave's instructions.
 // Needs the row in one pass (nch <= LPR * NC); the caller takes gate_up_one per token otherwise.
-template <bool Q, int LPR, int NC, int R, int MAXT>
-__device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cntp, const int* spid, const char* wbase,
-                                             int64_t row0, uint16_t* xs) {
-  constexpr int ES = Q ? 1 : 2;
+template <bool Q, int LPR, int NC>
+constexpr int staged_row_elems() {
+  return LPR * NC * (Q ? 16 : 8);  // bf16 activations per staged row
+}
+
+// Tokens per group: 2 measured best (int8 gate/up over 28 cold layers at 2 / 4 / 8 tokens 17.4 / 30.5 / 45.8 us,
+// against 17.4 / 30.8 / 46.9 with 4 and 17.4 / 30.7 / 49.3 with 8).
+#ifndef MM_GU_MANY_G
+#define MM_GU_MANY_G 2
+#endif
+
+// The R row pairs of one wave for the cntp staged tokens, G tokens at a time: the 2 G sums of a group are reduced
+// together and stored by one lane each.
+template <bool Q, int LPR, int NC, int R, int G>
+__device__ __forceinline__ void gate_up_many_rows(const DecodeArgs& a, int e, int cntp, const int* spid,
+                                                  const uint16_t* xs, rsrc_t wr, uint32_t rowb, int64_t row0,
+                                                  uint4 (&wg)[NC], uint4 (&wu)[NC]) {
   constexpr int GPW = kWave / LPR;
+  constexpr int ROW = staged_row_elems<Q, LPR, NC>();
+  constexpr int LOGN = G == 1 ? 1 : G == 2 ? 2 : G == 4 ? 3 : 4;  // log2 of the 2 G sums of a group
+  static_assert(2 * G <= LPR && (G & (G - 1)) == 0 && G <= 8, "token group");
   const int lane = lane_id();
   const int g = lane / LPR, s = lane % LPR;
-  const int64_t nch = a.H * ES / 16;
-  // stage the rows of this group's tokens (whole workgroup; the group is uniform across it)
-  const int64_t row_chunks = a.H / 8;  // 16-byte chunks of one bf16 row
-  for (int64_t i = threadIdx.x; i < cntp * row_chunks; i += blockDim.x) {
-    const int t = static_cast<int>(i / row_chunks);
-    const int64_t c = i % row_chunks;
-    const int tok = spid[t] / a.nk;
-    reinterpret_cast<uint4*>(xs + t * a.H)[c] = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(tok) * a.xs)[c];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+  const int64_t nch = a.H * (Q ? 1 : 2) / 16;
+  auto load_w = [&](int64_t r) {
     const bool rok = r < a.I;
-    float sg, su;
-    gate_up_scales<Q>(a, e, r, rok, sg, su);
-    const uint32_t rowb = static_cast<uint32_t>(a.gu_sn * ES);
-    const rsrc_t wr = make_rsrc(wbase, 2 * a.I * a.gu_sn * ES);
     const uint32_t goff = static_cast<uint32_t>(r) * rowb, uoff = static_cast<uint32_t>(r + a.I) * rowb;
-    uint4 wg[NC], wu[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int64_t c = s + static_cast<int64_t>(LPR) * j;
@@ -236,34 +240,125 @@ __device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cnt
       wg[j] = buf16(wr, ok ? goff + static_cast<uint32_t>(c) * 16u : kPast);
       wu[j] = buf16(wr, ok ? uoff + static_cast<uint32_t>(c) * 16u : kPast);
     }
+  };
+  // after group_sums a lane holds the gate total of the group's token vi < G (its up total, value G + vi, is at
+  // lane ^ 1) or an up total; the G gate lanes among the first 2 G of the row store
+  const int vi = sums_index<LPR, 2 * G>(lane);
+  const bool storer = vi < G && (s >> LOGN) == 0;
+  float sg = 1.f, su = 1.f;
+  gate_up_scales<Q>(a, e, row0 + g, row0 + g < a.I, sg, su);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = row0 + static_cast<int64_t>(GPW) * i + g;
+    const bool rok = r < a.I;
     uint4 gl[NC], gh[NC], ul[NC], uh[NC];  // int8: the chunks widened to bf16 (elements 0-7, 8-15)
+    float sgn = 1.f, sun = 1.f;
     if constexpr (Q) {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
         widen_i8(wg[j], gl[j], gh[j]);
         widen_i8(wu[j], ul[j], uh[j]);
       }
-    }
-    for (int t = 0; t < cntp; ++t) {
-      float ag = 0.f, au = 0.f;
-#pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const int64_t c = s + static_cast<int64_t>(LPR) * j;
-        Act<Q> xv;
-        lds_act<Q>(xv, xs + t * a.H, c, c < nch);
-        if constexpr (Q) {
-          ag = dot8_bf16(gh[j], xv.v[1], dot8_bf16(gl[j], xv.v[0], ag));
-          au = dot8_bf16(uh[j], xv.v[1], dot8_bf16(ul[j], xv.v[0], au));
-        } else {
-          ag = dot_chunk<Q>(wg[j], xv, ag);
-          au = dot_chunk<Q>(wu[j], xv, au);
-        }
+      if (i + 1 < R) {  // the next row pair streams during this one's dots
+        const int64_t rn = r + GPW;
+        load_w(rn);
+        gate_up_scales<Q>(a, e, rn, rn < a.I, sgn, sun);
       }
-      ag = group_sum<LPR>(ag);
-      au = group_sum<LPR>(au);
-      if (s == 0 && rok) gate_up_store<Q>(a, r, spid[t], ag, au, sg, su);
+    }
+    // x[t]: gate sum of token t0 + t, x[G + t]: its up sum. A row past cntp (the last group) holds stale values:
+    // its sums stay in their own lanes through group_sums and are not stored.
+    for (int t0 = 0; t0 < cntp; t0 += G) {
+      float x[2 * G];
+#pragma unroll
+      for (int t = 0; t < G; ++t) {
+        const uint4* row = reinterpret_cast<const uint4*>(xs + (t0 + t) * ROW);
+        float ag = 0.f, au = 0.f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int c = s + LPR * j;
+          if constexpr (Q) {
+            const uint4 x0 = row[2 * c], x1 = row[2 * c + 1];
+            ag = dot8_bf16(gh[j], x1, dot8_bf16(gl[j], x0, ag));
+            au = dot8_bf16(uh[j], x1, dot8_bf16(ul[j], x0, au));
+          } else {
+            const uint4 x0 = row[c];
+            ag = dot8_bf16(wg[j], x0, ag);
+            au = dot8_bf16(wu[j], x0, au);
+          }
+        }
+        x[t] = ag;
+        x[G + t] = au;
+      }
+      group_sums<LPR, 2 * G>(x);
+      const float up = dpp_f32<kDppXor1>(x[0]);
+      if (storer && t0 + vi < cntp && rok) gate_up_store<Q>(a, r, spid[t0 + vi], x[0], up, sg, su);
+    }
+    if constexpr (Q) {
+      sg = sgn;
+      su = sun;
+    } else if (i + 1 < R) {
+      const int64_t rn = r + GPW;
+      load_w(rn);
+      gate_up_scales<Q>(a, e, rn, rn < a.I, sg, su);
     }
   }
+}
+
+template <bool Q, int LPR, int NC, int R, int MAXT>
+__device__ __forceinline__ void gate_up_many(const DecodeArgs& a, int e, int cntp, const int* spid, const char* wbase,
+                                             int64_t row0, uint16_t* xs) {
+  constexpr int ES = Q ? 1 : 2;
+  constexpr int GPW = kWave / LPR;
+  constexpr int ROW = staged_row_elems<Q, LPR, NC>();
+  const int lane = lane_id();
+  const int g = lane / LPR, s = lane % LPR;
+  const int64_t nch = a.H * ES / 16;
+  const uint32_t rowb = static_cast<uint32_t>(a.gu_sn * ES);
+  const rsrc_t wr = make_rsrc(wbase, 2 * a.I * a.gu_sn * ES);
+  // the first row pair's weights, in flight during the staging below
+  uint4 wg[NC], wu[NC];
+  {
+    const int64_t r = row0 + g;
+    const bool rok = r < a.I;
+    const uint32_t goff = static_cast<uint32_t>(r) * rowb, uoff = static_cast<uint32_t>(r + a.I) * rowb;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t c = s + static_cast<int64_t>(LPR) * j;
+      const bool ok = rok && c < nch;
+      wg[j] = buf16(wr, ok ? goff + static_cast<uint32_t>(c) * 16u : kPast);
+      wu[j] = buf16(wr, ok ? uoff + static_cast<uint32_t>(c) * 16u : kPast);
+    }
+  }
+  // stage the rows of this group's tokens and their zero padding (whole workgroup; the group is uniform across it),
+  // every load of a batch issued before its stores, so the staging waits for memory once (up to 8 pieces per thread
+  // and batch)
+  {
+    const int row_chunks = static_cast<int>(a.H / 8);  // 16-byte pieces of one bf16 row
+    constexpr int PAD_CHUNKS = ROW / 8;               // ... of one staged row
+    const int total = cntp * PAD_CHUNKS;
+    constexpr int SB = 8;
+    for (int b0 = threadIdx.x; b0 < total; b0 += SB * static_cast<int>(blockDim.x)) {
+      uint4 v[SB];
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const int i = b0 + j * static_cast<int>(blockDim.x);
+        const int ic = i < total ? i : total - 1;  // clamped: the value is not stored past the end
+        const int t = ic / PAD_CHUNKS, c = ic % PAD_CHUNKS;
+        const int tok = spid[t] / a.nk;
+        v[j] = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(tok) * a.xs)[c < row_chunks ? c : 0];
+        v[j] = c < row_chunks ? v[j] : make_uint4(0u, 0u, 0u, 0u);
+      }
+      keep_raw(v);  // all loads here, not each sunk into its store's branch
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const int i = b0 + j * static_cast<int>(blockDim.x);
+        if (i < total) reinterpret_cast<uint4*>(xs)[i] = v[j];
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int G = MM_GU_MANY_G < MAXT ? MM_GU_MANY_G : MAXT;  // groups never reach past the MAXT staged rows
+  gate_up_many_rows<Q, LPR, NC, R, G>(a, e, cntp, spid, xs, wr, rowb, row0, wg, wu);
   __syncthreads();  // the staging buffer is reused by the next group
 }
 
@@ -462,7 +557,7 @@ template <bool Q, int LPR, int NC, int R, int MAXT>
 int launch_a(const DecodeArgs& a, hipStream_t st) {
   constexpr int rows_per_wg = 4 * (kWave / LPR) * R;
   dim3 grid(static_cast<unsigned>((a.I + rows_per_wg - 1) / rows_per_wg), static_cast<unsigned>(a.P));
-  const size_t lds = MAXT > 1 ? static_cast<size_t>(MAXT) * a.H * 2 : 0;
+  const size_t lds = MAXT > 1 ? static_cast<size_t>(MAXT) * staged_row_elems<Q, LPR, NC>() * 2 : 0;
   if (a.n_tokens == 1 && a.sel_logits)
     hipLaunchKernelGGL((decode_gate_up_kernel<Q, LPR, NC, R, MAXT, true, true>), grid, dim3(256), lds, st, a);
   else if (a.n_tokens == 1)
@@ -503,7 +598,7 @@ int dispatch_a_t(const DecodeArgs& a, hipStream_t st) {
   // tokens staged per group: one per token of the batch (a token naming an expert twice adds groups),
   // bounded so that the staged rows fit 64 KB of LDS
   int maxt = a.n_tokens;
-  while (maxt > 1 && static_cast<int64_t>(maxt) * a.H * 2 > 65536) maxt /= 2;
+  while (maxt > 1 && static_cast<int64_t>(maxt) * staged_row_elems<Q, LPR, NC>() * 2 > 65536) maxt /= 2;
   constexpr int R = Q ? MM_GU_R_I8 : MM_GU_R_BF16;  // row pairs per wave, one token
   // several tokens: two row pairs per wave, except int8 batches of up to 4 tokens (one row pair, 64 VGPRs, 8 waves
   // per SIMD: 3-4 % faster at 2 and 4 tokens); at 8 tokens one row pair (also 8 waves per SIMD) took 64.2 us
