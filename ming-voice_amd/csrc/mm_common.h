@@ -296,6 +296,34 @@ __device__ __forceinline__ uint4 buf16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
 }
 
+__device__ __forceinline__ uint32_t buf4(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0));
+}
+
+__device__ __forceinline__ uint32_t buf2(rsrc_t r, uint32_t off) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0));
+}
+
+// Loads of a tensor whose dtype is one of two, chosen at run time, without a branch on it: one buffer resource per
+// dtype over the same memory, the other dtype's of size zero (its loads read zero and touch no memory), and the
+// two results combined. A load behind a branch makes the wave wait for it, and for every load issued before it,
+// right away; these wait only where their value is used.
+// A row of n fp32 or bf16 scales starting at element `first` of s.
+struct ScaleRow {
+  rsrc_t r16, r32;
+};
+
+__device__ __forceinline__ ScaleRow scale_row(const void* s, int s_dtype, int64_t first, int64_t n) {
+  const bool b16 = s_dtype == MM_BF16;
+  const char* row = static_cast<const char*>(s) + first * (b16 ? 2 : 4);
+  return {make_rsrc(row, b16 ? n * 2 : 0), make_rsrc(row, b16 ? 0 : n * 4)};
+}
+
+__device__ __forceinline__ float scale_at(const ScaleRow& r, uint32_t i) {
+  return __uint_as_float((buf2(r.r16, i * 2u) << 16) | buf4(r.r32, i * 4u));
+}
+
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
 

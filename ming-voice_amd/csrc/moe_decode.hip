@@ -119,26 +119,16 @@ __device__ __forceinline__ void gate_up_store(const DecodeArgs& a, int64_t r, in
   a.a_buf[static_cast<int64_t>(p) * a.I + r] = f32_to_bf16(act * uu);
 }
 
-// The int8 row scales of gate row r and up row r + I of expert e (1 for bf16 weights). Loaded without a branch on
-// the scale type: through buffer resources over the expert's scale row of both types, the one of the other type
-// empty (its loads read zero and touch no memory), so the bits combine by an or and nothing waits for these loads
-// until the epilogue uses them (a load per type behind a branch made the wave wait for it, and for every load
-// issued before it, on the spot).
+// The int8 row scales of gate row r and up row r + I of expert e (1 for bf16 weights), loaded without a branch on the
+// scale type (scale_row), so nothing waits for them before the epilogue uses them.
 template <bool Q>
 __device__ __forceinline__ void gate_up_scales(const DecodeArgs& a, int e, int64_t r, bool rok, float& sg, float& su) {
   sg = su = 1.f;
   if (Q) {
-    const bool b16 = a.s_dtype == MM_BF16;
-    const char* row = static_cast<const char*>(a.s_gu) + static_cast<int64_t>(e) * a.sgu_se * (b16 ? 2 : 4);
-    const rsrc_t r16 = make_rsrc(row, b16 ? 2 * a.I * 2 : 0), r32 = make_rsrc(row, b16 ? 0 : 2 * a.I * 4);
-    const uint32_t i = static_cast<uint32_t>(rok ? r : 0), iu = i + static_cast<uint32_t>(a.I);
-    auto ld = [&](uint32_t k) {
-      const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r16, k * 2, 0, 0));
-      const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r32, k * 4, 0, 0));
-      return __uint_as_float((lo << 16) | w);
-    };
-    sg = ld(i);
-    su = ld(iu);
+    const ScaleRow sr = scale_row(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se, 2 * a.I);
+    const uint32_t i = static_cast<uint32_t>(rok ? r : 0);
+    sg = scale_at(sr, i);
+    su = scale_at(sr, i + static_cast<uint32_t>(a.I));
   }
 }
 
@@ -440,12 +430,21 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeArgs a) {
 // ------------------------------------------------------------------------------------------- kernel B
 
 constexpr int kDownWaves = 8;
+// Largest batch whose down kernel reads each expert row again for every pair (RELOAD below), per weight type:
+// int8 down over 28 cold layers at 2 / 4 / 8 tokens 11.3 / 19.2 / 33.8 us reloading, 11.8 / 18.9 / 31.2 holding the
+// row; bf16 15.4 / 26.5 / 46.5 reloading, 15.2 / 25.0 / 41.3 holding it.
+#ifndef MM_DOWN_RELOAD_I8
+#define MM_DOWN_RELOAD_I8 4
+#endif
+#ifndef MM_DOWN_RELOAD_BF16
+#define MM_DOWN_RELOAD_BF16 1
+#endif
 
 // Grid: row tiles of H (RW = 64 / LPR rows). Wave w takes slots w, w + 8, ... (ONE: each; otherwise the
 // first slot of each distinct expert, with all its pairs), streams the tile's rows of the slot's expert
 // (LPR lanes per row) once, dots them with a[p] of the pairs, rounds to bf16 (after the row scale for int8)
 // into LDS; the workgroup then sums over slots in order per token and adds the residual.
-template <bool Q, int LPR, int NC, bool ONEPASS, bool ONE>
+template <bool Q, int LPR, int NC, bool ONEPASS, bool ONE, bool RELOAD>
 __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs a) {
   constexpr int RW = kWave / LPR;  // output rows per workgroup
   constexpr int CE = Q ? 16 : 8;   // weights per 16-byte chunk
@@ -458,23 +457,30 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
   const bool hok = h < a.H;
   const int64_t nch = a.I / CE;
 
+  // Lane p holds pair p's expert: one load per lane for every slot the wave takes (read back by readlane), issued
+  // first so that waiting for it does not wait for the loads below. One bf16 token (SCALAR_ID): each slot's expert
+  // by a scalar load, as no scale load needs the barrier below (which turns these into vector loads: a scalar load
+  // is used only where no store can reach it, and the barrier counts as one).
+  constexpr bool SCALAR_ID = ONE && !Q;
+  const int myid = SCALAR_ID ? -1 : lane_pair_expert(a);
   // The combine's operands are fetched now, into registers, so their loads overlap the weight stream: the
   // slot weight of pair tid and the residual of this thread's (token, row) output. Nothing waits here.
   const int tid = threadIdx.x;
   const int ct = tid / RW, cr = tid % RW;
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * RW + cr;
   const bool combiner = tid < a.n_tokens * RW && ch < a.H;
-  const uint16_t res_raw = (combiner && a.res) ? a.res[ct * a.res_rs + ch] : 0;
-  float wt = 0.f;
-  if (tid < a.P) {
-    const int t = tid / a.nk, k = tid - t * a.nk;
-    wt = a.wts[t * a.wts_rs + k];
-  }
+  // (buffer loads: no branch on a null residual or on the thread's role sits before them)
+  const rsrc_t rr = make_rsrc(a.res, a.res ? (static_cast<int64_t>(a.n_tokens - 1) * a.res_rs + a.H) * 2 : 0);
+  const uint16_t res_raw =
+      static_cast<uint16_t>(buf2(rr, combiner ? static_cast<uint32_t>((ct * a.res_rs + ch) * 2) : kPast));
+  const rsrc_t wtr = make_rsrc(a.wts, (static_cast<int64_t>(a.n_tokens - 1) * a.wts_rs + a.nk) * 4);
+  const int wt_t = tid / a.nk;
+  const float wt = __uint_as_float(
+      buf4(wtr, tid < a.P ? static_cast<uint32_t>((wt_t * a.wts_rs + tid - wt_t * a.nk) * 4) : kPast));
 
-  const int myid = ONE ? -1 : lane_pair_expert(a);
   const rsrc_t ar = make_rsrc(a.a_buf, static_cast<int64_t>(a.P) * a.I * 2);
   for (int u = wave; u < a.P; u += kDownWaves) {
-    const int e = slot_expert(a, u);
+    const int e = SCALAR_ID ? slot_expert(a, u) : __builtin_amdgcn_readlane(myid, u);
     if (e < 0) {  // a dropped pair contributes nothing
       if (s == 0) part[u][g] = 0.f;
       continue;
@@ -490,34 +496,47 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
     const uint32_t wrow = static_cast<uint32_t>((hok ? h : 0) * a.d_sn * (Q ? 1 : 2));
     float sc = 1.f;
     if constexpr (ONEPASS) {
-      // the whole row in registers, loaded once for every pair of the expert
+      // the whole row in registers. RELOAD (one token, int8 batches of up to 4 tokens): loaded with each pair's
+      // activations, the later pairs reading it again from cache, so that every load of a pass is in flight at
+      // once. Otherwise loaded once before the loop over pairs: the wave then waits for it (and the scale) on
+      // entering the loop, before the first pair's activations are requested, but reads it once (8 int8 tokens:
+      // the shared expert's 8 pairs re-reading it cost 1.2 us more than the wait; at 2 / 4 tokens the reload
+      // saved 0.5 / 0.3 us). Held across the loop, int8 chunks are kept raw (keep_raw) so that their widening (16
+      // floats each, halving the waves per SIMD) is not hoisted out of it.
       uint4 w[NC];
+      auto load_w = [&] {
 #pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const int64_t c = s + static_cast<int64_t>(LPR) * j;
-        w[j] = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
-      }
-      if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + (hok ? h : 0));
+        for (int j = 0; j < NC; ++j) {
+          const int64_t c = s + static_cast<int64_t>(LPR) * j;
+          w[j] = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
+        }
+        if (Q) sc = scale_at(scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, a.H), hok ? h : 0);
+      };
+      if (!RELOAD) load_w();
       do {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
         pairs &= pairs - 1ull;
+        if (RELOAD) load_w();
         const uint32_t arow = static_cast<uint32_t>(p * a.I * 2);
-        Act<Q> av[NC];  // every load issued before the first dot
+        Act<Q> av[NC];
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
           const int64_t c = s + static_cast<int64_t>(LPR) * j;
           buf_act<Q>(av[j], ar, arow, c, c < nch);
         }
-        if (Q && !ONE) keep_raw(w);
+        // every load above is issued before the first wait: a compiler barrier keeps the scheduler from moving the
+        // activation or scale loads past the dots or into the storing lane's branch (a round trip each)
+        if (!SCALAR_ID) asm volatile("" ::: "memory");
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < NC; ++j) acc = dot_chunk<Q>(w[j], av[j], acc);
         acc = group_sum<LPR>(acc);
         if (s == 0 && hok) part[p][g] = round_bf16(Q ? acc * sc : acc);
+        if (Q && !RELOAD) keep_raw(w);
       } while (!ONE && pairs);
     } else {
       // long rows: passes of LPR * NC chunks per pair (weights re-read from cache for later pairs)
-      if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + (hok ? h : 0));
+      if (Q) sc = scale_at(scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, a.H), hok ? h : 0);
       while (pairs) {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
         pairs &= pairs - 1ull;
@@ -573,11 +592,13 @@ int launch_b(const DecodeArgs& a, hipStream_t st) {
   dim3 grid(static_cast<unsigned>((a.H + RW - 1) / RW));
   const bool onepass = a.I * (Q ? 1 : 2) / 16 <= static_cast<int64_t>(LPR) * NC;
   if (onepass && a.n_tokens == 1)
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, true, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+  else if (onepass && a.n_tokens <= (Q ? MM_DOWN_RELOAD_I8 : MM_DOWN_RELOAD_BF16))
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false, true>), grid, dim3(kDownWaves * 64), 0, st, a);
   else if (onepass)
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
   else
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, false, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
   return mm::check_launch("moe_decode down");
 }
 
