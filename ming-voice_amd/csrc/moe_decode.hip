@@ -821,7 +821,8 @@ static int block_decode(const char* who, const void* x, int64_t n_tokens, int64_
   // one token, bf16 experts, at most 64 experts without groups: the gate/up kernel selects (one launch fewer;
   // 31.4 -> 29.0 us per cold layer). int8 keeps the separate selection: its selecting instance holds 105
   // VGPRs (4 waves per SIMD) and the layer ran slower (25.1 -> 28.1 us); held to 8 waves per SIMD
-  // (amdgpu_waves_per_eu, 47 VGPRs, no spills) it only tied (25.12 against 25.10 us).
+  // (amdgpu_waves_per_eu, 47 VGPRs, no spills) it only tied (25.12 against 25.10 us), and tied again after the
+  // branch-free scale loads (23.9 against 23.4-24.2 us).
   const bool fuse_select = n_tokens == 1 && n_experts <= 64 && n_group <= 1 && ex->w_dtype == MM_BF16;
   rc = mm::router_front(x, n_tokens, ex->hidden, x_row_stride, norm_w, eps, w32, sp, logits, ids, ids_dtype, wts, nk,
                         xn, st, !fuse_select);
