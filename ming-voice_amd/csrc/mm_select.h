@@ -46,9 +46,12 @@ __device__ __forceinline__ void select_token64(const SelectParams& a, const floa
   const int E = a.E;
   const bool valid = lane < E;
   float score = 0.f, key = -INFINITY;
+  // the logit and bias of this lane through buffer resources (a null bias has size zero and reads zero), with no
+  // branch before the loads: behind the lane and null tests each load was waited on by itself
+  const rsrc_t lr = make_rsrc(lg, static_cast<int64_t>(E) * 4), br = make_rsrc(a.bias, a.bias ? E * 4 : 0);
+  const uint32_t off = valid ? static_cast<uint32_t>(lane) * 4u : kPast;
+  const float l = __uint_as_float(buf4(lr, off)), b = __uint_as_float(buf4(br, off));
   if (valid) {
-    const float l = lg[lane];
-    const float b = a.bias ? a.bias[lane] : 0.f;
     if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
       score = 1.0f / (1.0f + __expf(-l));
       key = score + b;
@@ -104,14 +107,24 @@ __device__ __forceinline__ void select_token(const SelectParams& a, const float*
   const int E = a.E;
   const int nslots = (E + kWave - 1) / kWave;
   float score[NS], key[NS];  // score: weight source; key: selection value
+  // every slot's logit and bias loaded first, with no branch before them (as in select_token64)
+  const rsrc_t lr = make_rsrc(lg, static_cast<int64_t>(E) * 4), br = make_rsrc(a.bias, a.bias ? E * 4 : 0);
+  float lv[NS], bv[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int e = lane + kWave * j;
+    const uint32_t off = j < nslots && e < E ? static_cast<uint32_t>(e) * 4u : kPast;
+    lv[j] = __uint_as_float(buf4(lr, off));
+    bv[j] = __uint_as_float(buf4(br, off));
+  }
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const int e = lane + kWave * j;
     score[j] = 0.f;
     key[j] = -INFINITY;
     if (j < nslots && e < E) {
-      const float l = lg[e];
-      const float b = a.bias ? a.bias[e] : 0.f;
+      const float l = lv[j];
+      const float b = bv[j];
       if (a.scoring == MM_SCORE_SIGMOID_GROUP) {
         score[j] = 1.0f / (1.0f + __expf(-l));
         key[j] = score[j] + b;

@@ -125,21 +125,21 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(const typename TX::T* 
 // router row, the RMSNorm weight, the token rows) is issued at kernel start through buffer resources.
 // The sum of squares runs over the chunks exactly as row_rstd256 does, so xn matches mm_rms_norm bit for
 // bit; a chunk's logit terms are added in element order, chunks in j order, then the waves in order.
-template <int J>
+template <int J, int NT>
 __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* __restrict__ x, int n_tokens, int64_t H,
                                                                int64_t xs, const float* __restrict__ w32, int E,
                                                                float* __restrict__ logits,
                                                                const uint16_t* __restrict__ norm_w, float eps,
                                                                uint16_t* __restrict__ xn_out) {
-  __shared__ float red_ss[8][4];
-  __shared__ float red[4][8];
+  __shared__ float red_ss[NT][4];
+  __shared__ float red[4][NT];
   const int e = blockIdx.x;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
   const int nch = static_cast<int>(H / 8);
   const rsrc_t wr = make_rsrc(w32 + static_cast<int64_t>(e) * H, H * 4);
   const rsrc_t xr = make_rsrc(x, static_cast<int64_t>(n_tokens) * xs * 2);
   const rsrc_t nr = make_rsrc(norm_w, norm_w ? H * 2 : 0);
-  uint4 wv[J][2], nv[J], xv[J][8];
+  uint4 wv[J][2], nv[J], xv[J][NT];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int c = tid + 256 * j;
@@ -148,15 +148,15 @@ __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* _
     wv[j][1] = buf16(wr, ok ? static_cast<uint32_t>(c) * 32u + 16u : kPast);
     nv[j] = buf16(nr, ok ? static_cast<uint32_t>(c) * 16u : kPast);
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      if (t < n_tokens) xv[j][t] = buf16(xr, ok ? static_cast<uint32_t>(t * xs * 2 + c * 16) : kPast);
+    for (int t = 0; t < NT; ++t)  // a token past n_tokens reads zero (no branch: a load behind one is waited on)
+      xv[j][t] = buf16(xr, ok && t < n_tokens ? static_cast<uint32_t>(t * xs * 2 + c * 16) : kPast);
   }
-  float rstd[8];
+  float rstd[NT];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) rstd[t] = 1.f;
+  for (int t = 0; t < NT; ++t) rstd[t] = 1.f;
   if (norm_w) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < NT; ++t) {
       if (t < n_tokens) {
         float ss = 0.f;
 #pragma unroll
@@ -167,21 +167,21 @@ __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* _
     }
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < NT; ++t)
       if (t < n_tokens)
         rstd[t] = rsqrtf((((red_ss[t][0] + red_ss[t][1]) + red_ss[t][2]) + red_ss[t][3]) / static_cast<float>(H) + eps);
   }
   const bool store_xn = xn_out && e == 0;
-  float acc[8];
+  float acc[NT];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+  for (int t = 0; t < NT; ++t) acc[t] = 0.f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int c = tid + 256 * j;
     const uint32_t wq[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w, wv[j][1].x, wv[j][1].y, wv[j][1].z, wv[j][1].w};
     const uint32_t nq[4] = {nv[j].x, nv[j].y, nv[j].z, nv[j].w};
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < NT; ++t) {
       if (t < n_tokens) {
         const uint32_t xq[4] = {xv[j][t].x, xv[j][t].y, xv[j][t].z, xv[j][t].w};
         uint32_t o[4];
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void router_gemv_bf16_kernel(const uint16_t* _
     }
   }
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < NT; ++t) {
     if (t < n_tokens) {
       const float v = wave_sum(acc[t]);
       if (lane == 0) red[wave][t] = v;
@@ -387,7 +387,7 @@ struct SelectArgs {
 template <int NS>
 __global__ __launch_bounds__(256) void router_select_kernel(SelectArgs a) {
   __shared__ float rbuf[4][NS * kWave];
-  const int wv = threadIdx.x / kWave;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform: the logit row's address too
   const int t = blockIdx.x * 4 + wv;
   if (t >= a.n_tokens) return;
   const int lane = lane_id();
@@ -451,12 +451,16 @@ int launch_logits(const void* x, int64_t n_tokens, int64_t H, int64_t xs, const 
                     n_tokens * xs * 2 < (1LL << 31);
   if (n_tokens <= 8 && fast) {  // the RMSNorm is fused only for up to 8 tokens; larger batches take normalised rows
     const auto* xb = static_cast<const uint16_t*>(x);
-    if (H <= 2048)
-      hipLaunchKernelGGL(router_gemv_bf16_kernel<1>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xb,
-                         static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
+    const dim3 grid(static_cast<unsigned>(E));
+    const int nt = static_cast<int>(n_tokens), e = static_cast<int>(E);
+    if (H <= 2048 && n_tokens == 1)
+      hipLaunchKernelGGL((router_gemv_bf16_kernel<1, 1>), grid, dim3(256), 0, s, xb, nt, H, xs, w32, e, logits, nw, eps, xo);
+    else if (H <= 2048)
+      hipLaunchKernelGGL((router_gemv_bf16_kernel<1, 8>), grid, dim3(256), 0, s, xb, nt, H, xs, w32, e, logits, nw, eps, xo);
+    else if (n_tokens == 1)
+      hipLaunchKernelGGL((router_gemv_bf16_kernel<2, 1>), grid, dim3(256), 0, s, xb, nt, H, xs, w32, e, logits, nw, eps, xo);
     else
-      hipLaunchKernelGGL(router_gemv_bf16_kernel<2>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xb,
-                         static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
+      hipLaunchKernelGGL((router_gemv_bf16_kernel<2, 8>), grid, dim3(256), 0, s, xb, nt, H, xs, w32, e, logits, nw, eps, xo);
   } else if (n_tokens <= 8) {
     hipLaunchKernelGGL(router_gemv_kernel<TX>, dim3(static_cast<unsigned>(E)), dim3(256), 0, s, xp,
                        static_cast<int>(n_tokens), H, xs, w32, static_cast<int>(E), logits, nw, eps, xo);
