@@ -890,26 +890,49 @@ constexpr int kKdaThreads = 512;
 // 128 per pass; threads < K the q and k channels, threads < V the v channels. Every global load is issued before
 // the first barrier; column groups past V read zeros and write nothing (buffer bounds).
 // prefetching workgroups per head: kda_token_kernel traced at 11.26 / 9.86 / 9.51 / 9.44 us per call with 0 / 3 / 7 /
-// 15 of them (16 heads of 128 x 128, R = 128, inside the 28-layer hybrid step)
-constexpr int kKdaHelpers = 7;
+// 15 of them (16 heads of 128 x 128, R = 128, inside the 28-layer hybrid step); with each helper thread's loads
+// issued together (they had waited for one another) the 28-layer step took 1490 / 1484.5 / 1483 us per token with
+// 3 / 7 / 15 helpers, against 1496 before
+#ifndef MM_KDA_HELPERS
+#define MM_KDA_HELPERS 7
+#endif
+constexpr int kKdaHelpers = MM_KDA_HELPERS;
 
 // A helper workgroup of kda_token_kernel (blockIdx.x >= H): part `part` of kKdaHelpers of the head's state block
 // and LoRA rows, read and dropped, so that the lines come into L2 through more CUs than the one running the head
 // (whose own loads of them then find them there or in flight): one CU alone keeps too few misses outstanding to
 // pull the head's 128 KB at HBM speed.
 __device__ __forceinline__ void kda_token_prefetch(const KdaStepArgs& a, int h, int part) {
-  constexpr int K = 128;
+  constexpr int K = 128, B = 4;  // up to B pieces of each block per thread and batch, all blocks' batches at once
   const int64_t V = a.V;
-  const char* blocks[3] = {reinterpret_cast<const char*>(a.state + static_cast<int64_t>(h) * K * V),
-                           reinterpret_cast<const char*>(a.f_b + static_cast<int64_t>(h) * K * a.R),
-                           reinterpret_cast<const char*>(a.g_b + static_cast<int64_t>(h) * V * a.R)};
+  const void* blocks[3] = {a.state + static_cast<int64_t>(h) * K * V, a.f_b + static_cast<int64_t>(h) * K * a.R,
+                           a.g_b + static_cast<int64_t>(h) * V * a.R};
   const int64_t bytes[3] = {K * V * 4, static_cast<int64_t>(K) * a.R * 2, V * a.R * 2};
-  uint32_t acc = 0;
+  rsrc_t r[3];
+  int64_t n[3];
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
-    const int64_t n = bytes[b] / 16;  // whole 16-byte pieces (rows are 16-byte multiples)
-    for (int64_t i = threadIdx.x + static_cast<int64_t>(part) * kKdaThreads; i < n; i += kKdaThreads * kKdaHelpers)
-      acc ^= reinterpret_cast<const uint4*>(blocks[b])[i].x;
+    r[b] = make_rsrc(blocks[b], bytes[b]);
+    n[b] = bytes[b] / 16;  // whole 16-byte pieces (rows are 16-byte multiples)
+  }
+  const int64_t stride = static_cast<int64_t>(kKdaThreads) * kKdaHelpers;
+  const int64_t most = n[0] > n[1] ? (n[0] > n[2] ? n[0] : n[2]) : (n[1] > n[2] ? n[1] : n[2]);
+  uint32_t acc = 0;
+  // every piece of a batch is requested before any is used (a load whose value the next one waits for keeps one
+  // request per thread in flight); pieces past a block's end read nothing
+  for (int64_t i0 = threadIdx.x + static_cast<int64_t>(part) * kKdaThreads; i0 < most; i0 += stride * B) {
+    uint4 v[3][B];
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int64_t i = i0 + stride * j;
+        v[b][j] = buf16(r[b], i < n[b] ? static_cast<uint32_t>(i) * 16u : kPast);
+      }
+#pragma unroll
+    for (int b = 0; b < 3; ++b)
+#pragma unroll
+      for (int j = 0; j < B; ++j) acc ^= v[b][j].x;
   }
   asm volatile("" ::"v"(acc));  // keeps the loads; nothing is written
 }
