@@ -397,16 +397,25 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   constexpr int OS = HALF + 8;  // row stride (elements): rows 4 apart start 64 bytes apart on the banks
   static_assert(static_cast<size_t>(BM) * OS * 2 <= G::LDS, "gate/up output tile must fit in the k-slab LDS");
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds_raw);
+  // int8: the row scales of the wave's columns, all requested before the first is used and without a branch on the
+  // scale type (one trip to memory; loaded per fragment behind that branch, each waited on in turn)
+  float sgv[FG], suv[FG];
+#pragma unroll
+  for (int j = 0; j < FG; ++j) sgv[j] = suv[j] = 1.f;
+  if constexpr (Q) {
+    const ScaleRow sr = scale_row(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se, 2 * I);
+#pragma unroll
+    for (int j = 0; j < FG; ++j) {
+      const uint32_t col = static_cast<uint32_t>(min(n0 + g0 + 16 * j + (lane & 15), I - 1));
+      sgv[j] = scale_at(sr, col);
+      suv[j] = scale_at(sr, col + static_cast<uint32_t>(I));
+    }
+  }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < FG; ++j) {
     const int c = g0 + 16 * j + (lane & 15);  // tile column; columns past I are never stored
-    const int64_t col = min(n0 + c, I - 1);
-    float sg = 1.f, su = 1.f;
-    if (Q) {
-      sg = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + col);
-      su = load_scale(a.s_gu, a.s_dtype, static_cast<int64_t>(e) * a.sgu_se + I + col);
-    }
+    const float sg = sgv[j], su = suv[j];
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
 #pragma unroll
@@ -460,12 +469,19 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   constexpr int OS = G::BN + 8;
   static_assert(static_cast<size_t>(BM) * OS * 2 <= G::LDS, "down output tile must fit in the k-slab LDS");
   uint16_t* ot = reinterpret_cast<uint16_t*>(lds_raw);
+  float scv[G::FN];  // int8: the wave's row scales, requested together (as in gate/up)
+#pragma unroll
+  for (int j = 0; j < G::FN; ++j) scv[j] = 1.f;
+  if constexpr (Q) {
+    const ScaleRow sr = scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, H);
+#pragma unroll
+    for (int j = 0; j < G::FN; ++j) scv[j] = scale_at(sr, static_cast<uint32_t>(min(h0 + c0 + 16 * j + (lane & 15), H - 1)));
+  }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < G::FN; ++j) {
     const int c = c0 + 16 * j + (lane & 15);
-    float sc = 1.f;
-    if (Q) sc = load_scale(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se + min(h0 + c, H - 1));
+    const float sc = scv[j];
 #pragma unroll
     for (int i = 0; i < G::FM; ++i)
 #pragma unroll
