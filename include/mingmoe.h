@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 13
+#define MM_ABI_VERSION 14
 
 /* status codes */
 #define MM_OK 0
@@ -342,6 +342,14 @@ int64_t mm_kda_chunk_workspace(int64_t T, int64_t H, int64_t K);
  * the first n tokens' inputs (the padded prefill's conv_idx, engine.py:261-262); every y row is still computed. */
 int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, void* cache, int64_t W, const void* w,
                   const void* b, int act, void* y, int64_t y_ts, const int64_t* n_valid, void* stream);
+
+/* mm_short_conv (no bias) on n <= 4 convolutions over the same T tokens and width W in one launch: the q, k and v
+ * convolutions of a KDA layer over a prompt (engine.py:247-249), which the reference runs as three ShortConvolution
+ * calls. Host arrays of n entries: x[i], y[i] [T, C[i]] bf16 with token strides x_ts[i], y_ts[i]; cache[i], w[i]
+ * [C[i], W] bf16. act and n_valid as for mm_short_conv; each convolution's results equal its own mm_short_conv. */
+int mm_short_conv_many(int64_t n, const void* const* x, const int64_t* x_ts, const int64_t* C, void* const* cache,
+                       const void* const* w, void* const* y, const int64_t* y_ts, int64_t T, int64_t W, int act,
+                       const int64_t* n_valid, void* stream);
 
 /* y = bf16(x * rsqrt(mean(x^2) + eps) * w * sigmoid(g)) per row of n <= 512 elements: fla's FusedRMSNormGated with a
  * sigmoid gate, the output norm of a KDA layer (o_norm, engine.py:265). x, g, y [rows, n] bf16 with row strides;

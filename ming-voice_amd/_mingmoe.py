@@ -17,7 +17,7 @@ MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
 MM_NORM_ROUND_ONCE = 0x100
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -83,6 +83,7 @@ SIGNATURES = {
                       _F32, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P], ctypes.c_int),
     "mm_kda_chunk_workspace": ([_I64, _I64, _I64], ctypes.c_int64),
     "mm_short_conv": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _P, _P], ctypes.c_int),
+    "mm_short_conv_many": ([_I64, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P], ctypes.c_int),
     "mm_rms_norm_gated": ([_P, _I64, _P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P], ctypes.c_int),
     "mm_mla_attn_workspace": ([_I32, _I32, _I64], ctypes.c_int64),
     "mm_kda_decode_step": ([_P, _I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p), _I64, _P, _P,

@@ -687,15 +687,14 @@ __global__ __launch_bounds__(64 * NWB) void kda_chunk_kernel(KdaArgs a, const fl
 constexpr int kConvTokens = 16;
 
 template <int W>
-__global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
-                                                        uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
-                                                        const uint16_t* __restrict__ b, int act,
-                                                        uint16_t* __restrict__ y, int64_t ys,
-                                                        const int64_t* __restrict__ n_valid) {
+__device__ __forceinline__ void short_conv_tile(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
+                                                uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
+                                                const uint16_t* __restrict__ b, int act, uint16_t* __restrict__ y,
+                                                int64_t ys, const int64_t* __restrict__ n_valid, int bx, int by) {
   static_assert(kConvTokens >= W - 1, "only the first chunk may read the cache");
-  const int64_t ch = static_cast<int64_t>(blockIdx.x) * kWave + threadIdx.x;
+  const int64_t ch = static_cast<int64_t>(bx) * kWave + threadIdx.x;
   if (ch >= C) return;
-  const int t0 = blockIdx.y * kConvTokens;
+  const int t0 = by * kConvTokens;
   float wt[W], in[kConvTokens + W - 1];  // inputs t0 - W + 1 .. t0 + 15
 #pragma unroll
   for (int j = 0; j < W; ++j) wt[j] = bf16_to_f32(w[ch * W + j]);
@@ -723,7 +722,7 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
       y[(t0 + i) * ys + ch] = f32_to_bf16(acc);
     }
   }
-  if (blockIdx.y == 0) {
+  if (by == 0) {
     // the window after the prompt's real tokens (the first n_valid, clamped to [0, T], when given: the padded
     // prefill's conv_idx, engine.py:261-262): inputs nv - W .. nv - 1, from the old cache where they precede it
     int nv = T;
@@ -739,6 +738,38 @@ __global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restri
 #pragma unroll
     for (int j = 0; j < W; ++j) cache[ch * W + j] = nw[j];
   }
+}
+
+
+template <int W>
+__global__ __launch_bounds__(64) void short_conv_kernel(const uint16_t* __restrict__ x, int64_t xs, int T, int64_t C,
+                                                        uint16_t* __restrict__ cache, const uint16_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ b, int act,
+                                                        uint16_t* __restrict__ y, int64_t ys,
+                                                        const int64_t* __restrict__ n_valid) {
+  short_conv_tile<W>(x, xs, T, C, cache, w, b, act, y, ys, n_valid, blockIdx.x, blockIdx.y);
+}
+
+// Up to kConvMany convolutions over the same tokens and width in one launch (a KDA layer's q, k and v):
+// grid (channel blocks of the widest, token chunks, problems); a block past its problem's channels does nothing.
+constexpr int kConvMany = 4;
+
+struct ConvMany {
+  const uint16_t* x[kConvMany];
+  int64_t xs[kConvMany], C[kConvMany];
+  uint16_t* cache[kConvMany];
+  const uint16_t* w[kConvMany];
+  uint16_t* y[kConvMany];
+  int64_t ys[kConvMany];
+  int T, act;
+  const int64_t* n_valid;
+};
+
+template <int W>
+__global__ __launch_bounds__(64) void short_conv_many_kernel(ConvMany m) {
+  const int z = blockIdx.z;
+  short_conv_tile<W>(m.x[z], m.xs[z], m.T, m.C[z], m.cache[z], m.w[z], nullptr, m.act, m.y[z], m.ys[z], m.n_valid,
+                     blockIdx.x, blockIdx.y);
 }
 
 // --------------------------------------------------------------------------------------- gated RMSNorm
@@ -1715,6 +1746,49 @@ extern "C" int mm_short_conv(const void* x, int64_t x_ts, int64_t T, int64_t C, 
     default: hipLaunchKernelGGL(short_conv_kernel<8>, grid, dim3(kWave), 0, st, xp, x_ts, (int)T, C, cp, wp, bp, act, yp, y_ts, nv); break;
   }
   return mm::check_launch("short_conv");
+}
+
+extern "C" int mm_short_conv_many(int64_t n, const void* const* x, const int64_t* x_ts, const int64_t* C,
+                                  void* const* cache, const void* const* w, void* const* y, const int64_t* y_ts,
+                                  int64_t T, int64_t W, int act, const int64_t* n_valid, void* stream) {
+  MM_REQUIRE(n >= 1 && n <= kConvMany, "short_conv_many: %lld convolutions (1 to %d)", (long long)n, kConvMany);
+  MM_REQUIRE(x && x_ts && C && cache && w && y && y_ts, "short_conv_many: null array");
+  MM_REQUIRE(T >= 0 && T <= 65535LL * kConvTokens, "short_conv_many: bad T=%lld", (long long)T);
+  MM_REQUIRE(W >= 2 && W <= 8, "short_conv_many: kernel width %lld must be in [2, 8]", (long long)W);
+  ConvMany m{};
+  int64_t cmax = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    MM_REQUIRE(C[i] >= 1 && C[i] <= (1LL << 31) / 8, "short_conv_many: bad C=%lld (convolution %lld)", (long long)C[i],
+               (long long)i);
+    MM_REQUIRE(x[i] && cache[i] && w[i] && y[i], "short_conv_many: null pointer (convolution %lld)", (long long)i);
+    MM_REQUIRE(x_ts[i] >= C[i] && y_ts[i] >= C[i], "short_conv_many: token strides smaller than the channels "
+               "(convolution %lld)", (long long)i);
+    m.x[i] = static_cast<const uint16_t*>(x[i]);
+    m.xs[i] = x_ts[i];
+    m.C[i] = C[i];
+    m.cache[i] = static_cast<uint16_t*>(cache[i]);
+    m.w[i] = static_cast<const uint16_t*>(w[i]);
+    m.y[i] = static_cast<uint16_t*>(y[i]);
+    m.ys[i] = y_ts[i];
+    cmax = C[i] > cmax ? C[i] : cmax;
+  }
+  if (T == 0) return MM_OK;
+  m.T = static_cast<int>(T);
+  m.act = act;
+  m.n_valid = n_valid;
+  dim3 grid(static_cast<unsigned>((cmax + kWave - 1) / kWave), static_cast<unsigned>((T + kConvTokens - 1) / kConvTokens),
+            static_cast<unsigned>(n));
+  hipStream_t st = MM_STREAM(stream);
+  switch (W) {
+    case 2: hipLaunchKernelGGL(short_conv_many_kernel<2>, grid, dim3(kWave), 0, st, m); break;
+    case 3: hipLaunchKernelGGL(short_conv_many_kernel<3>, grid, dim3(kWave), 0, st, m); break;
+    case 4: hipLaunchKernelGGL(short_conv_many_kernel<4>, grid, dim3(kWave), 0, st, m); break;
+    case 5: hipLaunchKernelGGL(short_conv_many_kernel<5>, grid, dim3(kWave), 0, st, m); break;
+    case 6: hipLaunchKernelGGL(short_conv_many_kernel<6>, grid, dim3(kWave), 0, st, m); break;
+    case 7: hipLaunchKernelGGL(short_conv_many_kernel<7>, grid, dim3(kWave), 0, st, m); break;
+    default: hipLaunchKernelGGL(short_conv_many_kernel<8>, grid, dim3(kWave), 0, st, m); break;
+  }
+  return mm::check_launch("short_conv_many");
 }
 
 extern "C" int mm_rms_norm_gated(const void* x, int64_t x_rs, const void* g, int64_t g_rs, const void* w, int64_t rows,

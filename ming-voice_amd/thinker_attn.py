@@ -23,7 +23,7 @@ import torch
 
 import _mingmoe as _mm
 
-__all__ = ["fused_recurrent_kda", "kda_workspace", "short_conv", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
+__all__ = ["fused_recurrent_kda", "kda_workspace", "short_conv", "short_conv_many", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
            "mla_attn_workspace", "mla_prefill_attn", "embed_rows", "argmax_rows"]
 
 
@@ -184,6 +184,48 @@ def short_conv(x, cache, weight, bias=None, activation="silu", out=None, n_valid
                                     _mm.stream_of(x)),
                   "short_conv")
     return y.reshape(x.shape)
+
+
+def short_conv_many(xs, caches, weights, activation="silu", n_valid=None):
+    """short_conv (no bias) on up to 4 inputs over the same tokens and window width in one launch, each with its own
+    cache (updated in place) and weight: the q, k and v convolutions of a KDA layer's prompt. xs: [T, C_i] bf16 (unit
+    last-dim stride); caches [1, C_i, W]; weights [C_i, 1, W]. Returns [y_i], each equal to short_conv(x_i, ...)."""
+    n = len(xs)
+    if not 1 <= n <= 4 or len(caches) != n or len(weights) != n:
+        raise ValueError("short_conv_many: 1 to 4 inputs, with as many caches and weights")
+    _mm.require_gpu(*xs, *caches, *weights, n_valid)
+    _check_count(n_valid, "short_conv_many")
+    if activation not in ("silu", "swish", None):
+        raise ValueError(f"short_conv_many: activation {activation!r} (silu or None)")
+    x2s, w2s, ys = [], [], []
+    T, W = xs[0].reshape(-1, xs[0].shape[-1]).shape[0], caches[0].shape[-1]
+    for x, cache, weight in zip(xs, caches, weights):
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.stride(-1) != 1:
+            x2 = x2.contiguous()
+        C = x2.shape[1]
+        if x2.shape[0] != T or cache.shape[-1] != W:
+            raise ValueError("short_conv_many: every input needs the same tokens and window width")
+        if cache.numel() != C * W or not cache.is_contiguous() or cache.dtype != torch.bfloat16:
+            raise ValueError(f"short_conv_many: cache must be a contiguous bf16 [1, {C}, W] tensor")
+        w2 = weight.reshape(C, -1)
+        if w2.shape[1] != W or w2.dtype != torch.bfloat16:
+            raise ValueError(f"short_conv_many: weight must be bf16 [{C}, 1, {W}]")
+        x2s.append(x2)
+        w2s.append(w2.contiguous())
+        ys.append(torch.empty(T, C, device=x.device, dtype=torch.bfloat16))
+
+    def arr(ctype, vals):
+        return (ctype * n)(*vals)
+    lib = _mm.load()
+    with _mm.on_device(xs[0]):
+        _mm.check(lib.mm_short_conv_many(
+            n, arr(ctypes.c_void_p, [_mm.ptr(t) for t in x2s]), arr(ctypes.c_int64, [t.stride(0) for t in x2s]),
+            arr(ctypes.c_int64, [t.shape[1] for t in x2s]), arr(ctypes.c_void_p, [_mm.ptr(c) for c in caches]),
+            arr(ctypes.c_void_p, [_mm.ptr(w) for w in w2s]), arr(ctypes.c_void_p, [_mm.ptr(y) for y in ys]),
+            arr(ctypes.c_int64, [y.stride(0) for y in ys]), T, W, 0 if activation is None else 1, _mm.ptr(n_valid),
+            _mm.stream_of(xs[0])), "short_conv_many")
+    return [y.reshape(x.shape) for x, y in zip(xs, ys)]
 
 
 def rms_norm_gated(x, g, weight, eps=1e-5, out=None):

@@ -280,8 +280,8 @@ class FastThinkerStep:
         H, K, V, R = p["heads"], p["K"], p["V"], p["rank"]
         pr = self._rows(h, p["proj"], p["proj_b"], norm=p["ln1"])
         nqk, nv = H * K, H * V
-        q, k, v = (TA.short_conv(pr[:, a:b], c, w, n_valid=n_valid) for (a, b), c, w in
-                   zip(((0, nqk), (nqk, 2 * nqk), (2 * nqk, 2 * nqk + nv)), p["conv"], p["conv_w"]))
+        q, k, v = TA.short_conv_many([pr[:, a:b] for a, b in ((0, nqk), (nqk, 2 * nqk), (2 * nqk, 2 * nqk + nv))],
+                                     p["conv"], p["conv_w"], n_valid=n_valid)
         base = 2 * nqk + nv
         f = self._rows(pr[:, base:base + R], p["f_b"])
         gg = self._rows(pr[:, base + R:base + 2 * R], p["g_b"])

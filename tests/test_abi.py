@@ -77,6 +77,16 @@ def test_argument_validation_reports_messages():
     assert "M=17" in _err(lib.mm_small_linear(P, 17, 64, 64, P, 64, 64, None, 0, None, 0, None, 0.0, None, P, 64, None))
     assert "scale dtype" in _err(lib.mm_quantize_rows_int8(P, mm.MM_BF16, 4, 64, 64, P, 64, P, mm.MM_INT8, None))
     assert "seq=9" in _err(lib.mm_rope_attn(P, 2, 9, 1024, 16, P, P, P, None))
+    arrP, arr64 = (ctypes.c_void_p * 4)(16, 16, 16, 16), (ctypes.c_int64 * 4)(64, 64, 64, 64)
+    assert "convolutions (1 to 4)" in _err(lib.mm_short_conv_many(5, arrP, arr64, arr64, arrP, arrP, arrP, arr64, 8, 4,
+                                                                  1, None, None))
+    assert "kernel width" in _err(lib.mm_short_conv_many(3, arrP, arr64, arr64, arrP, arrP, arrP, arr64, 8, 9, 1, None,
+                                                         None))
+    bad_c = (ctypes.c_int64 * 4)(64, 0, 64, 64)
+    assert "bad C=0 (convolution 1)" in _err(lib.mm_short_conv_many(3, arrP, arr64, bad_c, arrP, arrP, arrP, arr64, 8,
+                                                                    4, 1, None, None))
+    assert "null array" in _err(lib.mm_short_conv_many(3, None, arr64, arr64, arrP, arrP, arrP, arr64, 8, 4, 1, None,
+                                                       None))
     assert "head dim 65" in _err(lib.mm_rope_attn(P, 2, 3, 1040, 16, P, P, P, None))
     assert "head dim 48" in _err(lib.mm_qwen_decode_attn(P, 8, 2, 48, P, P, 64, P, mm.MM_INT64, P, 0.1, P, P, 1 << 20,
                                                          None))

@@ -220,6 +220,29 @@ def test_short_conv_matches_oracle(T, C, Wd):
     assert torch.equal(cache[0].cpu(), rc.to(BF))  # the window holds bf16 inputs exactly
 
 
+@pytest.mark.parametrize("T,Cs,Wd,n", [(1, (2048, 2048, 2048), 4, None), (40, (2048, 2048, 2048), 4, None),
+                                       (17, (77, 300, 64), 3, None), (100, (130, 2048), 8, None), (33, (96,), 2, None),
+                                       (24, (2048, 2048, 2048), 4, 19), (24, (150, 64, 77, 20), 4, 0)])
+def test_short_conv_many_equals_separate_calls(T, Cs, Wd, n):
+    """One launch over several convolutions (the q, k, v of a KDA prompt, and other channel counts, with and without
+    n_valid): every output and every updated cache equals its own short_conv call bit for bit, read through strided
+    column slices of one projection row as the prefill passes them."""
+    pr = W.normal((T, sum(Cs) + 5), 1.0, 630 + T, DEV)
+    xs, o = [], 0
+    for C in Cs:
+        xs.append(pr[:, o:o + C])
+        o += C
+    caches = [W.normal((1, C, Wd), 1.0, 631 + i, DEV) for i, C in enumerate(Cs)]
+    ws = [W.normal((C, 1, Wd), 0.5, 641 + i, DEV) for i, C in enumerate(Cs)]
+    nv = None if n is None else torch.tensor([n], device=DEV)
+    c_one = [c.clone() for c in caches]
+    ys = TA.short_conv_many(xs, caches, ws, n_valid=nv)
+    for x, c, w, y in zip(xs, c_one, ws, ys):
+        assert torch.equal(y, TA.short_conv(x, c, w, n_valid=nv))
+    for c, c1 in zip(caches, c_one):
+        assert torch.equal(c, c1)
+
+
 def test_rms_norm_gated_matches_oracle():
     x = W.normal((7, 16, 128), 2.0, 410, DEV)
     g = W.normal((7, 16, 128), 1.0, 411, DEV)
