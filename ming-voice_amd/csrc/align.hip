@@ -17,8 +17,16 @@ constexpr uint16_t kNoExpert = 0xffff;
 
 // STAGED: the counting pass keeps each pair's expert id in LDS (dynamic, P x 2 bytes), so the scatter pass
 // reads ids from LDS instead of a second, latency-bound pass over global memory.
-template <bool STAGED>
-__global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict__ flat, int flat_dtype, int P, int E1,
+// Id i of the flat ids (int64 or int32 by the template flag: a branch on a run-time dtype put each of a batch's
+// loads behind it, and the wave waited for each in turn).
+template <bool I64>
+__device__ __forceinline__ int64_t flat_id(const void* flat, int64_t i) {
+  if constexpr (I64) return static_cast<const int64_t*>(flat)[i];
+  else return static_cast<int64_t>(static_cast<const int32_t*>(flat)[i]);
+}
+
+template <bool STAGED, bool I64>
+__global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict__ flat, int P, int E1,
                                                          int BM, int32_t* __restrict__ sorted_ids,
                                                          int32_t* __restrict__ bexp, int nb,
                                                          int32_t* __restrict__ expert_offsets) {
@@ -45,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict_
   for (int c0 = beg; c0 < end; c0 += kWave * kIdBatch) {
     int64_t ev[kIdBatch];
 #pragma unroll
-    for (int u = 0; u < kIdBatch; ++u) ev[u] = load_id(flat, flat_dtype, min(c0 + u * kWave + lane, end - 1));
+    for (int u = 0; u < kIdBatch; ++u) ev[u] = flat_id<I64>(flat, min(c0 + u * kWave + lane, end - 1));
 #pragma unroll
     for (int u = 0; u < kIdBatch; ++u) {
       const int p = c0 + u * kWave + lane;
@@ -94,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void align_kernel(const void* __restrict_
     if (STAGED) {
       if (p < end && staged[p] != kNoExpert) e = staged[p];
     } else if (p < end) {
-      e = load_id(flat, flat_dtype, p);
+      e = flat_id<I64>(flat, p);
     }
     const bool valid = e >= 0 && e < E1;
     if (valid) atomicOr(&lanes[wave][e], 1ull << lane);
@@ -150,17 +158,17 @@ extern "C" int mm_align_blocks(const void* flat, int flat_dtype, int64_t P, int3
              (long long)want);
   MM_REQUIRE(nb * block_m <= (1LL << 31) - 1, "align_blocks: too many rows");
   MM_REQUIRE(sorted_ids && bexp && (P == 0 || flat), "align_blocks: null pointer");
+  const bool i64 = flat_dtype == MM_INT64;
+  auto kernel = P <= kMaxStaged ? (i64 ? align_kernel<true, true> : align_kernel<true, false>)
+                                : (i64 ? align_kernel<false, true> : align_kernel<false, false>);
+  size_t lds = 0;
   if (P <= kMaxStaged) {
-    const size_t lds = (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
-    int rc = mm::allow_lds(align_kernel<true>, static_cast<size_t>(kMaxStaged) * 2, "align_blocks");
+    lds = (static_cast<size_t>(P) * 2 + 15) / 16 * 16;
+    int rc = mm::allow_lds(kernel, static_cast<size_t>(kMaxStaged) * 2, "align_blocks");
     if (rc) return rc;
-    hipLaunchKernelGGL(align_kernel<true>, dim3(1), dim3(kThreads), lds, MM_STREAM(stream), flat, flat_dtype,
-                       static_cast<int>(P), static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp,
-                       static_cast<int>(nb), expert_offsets);
-  } else {
-    hipLaunchKernelGGL(align_kernel<false>, dim3(1), dim3(kThreads), 0, MM_STREAM(stream), flat, flat_dtype,
-                       static_cast<int>(P), static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp,
-                       static_cast<int>(nb), expert_offsets);
   }
+  hipLaunchKernelGGL(kernel, dim3(1), dim3(kThreads), lds, MM_STREAM(stream), flat, static_cast<int>(P),
+                     static_cast<int>(n_slots), static_cast<int>(block_m), sorted_ids, bexp, static_cast<int>(nb),
+                     expert_offsets);
   return mm::check_launch("align_blocks");
 }
