@@ -779,24 +779,29 @@ __global__ __launch_bounds__(256) void rms_norm_gated_kernel(const uint16_t* __r
                                                              const uint16_t* __restrict__ g, int64_t gs,
                                                              const uint16_t* __restrict__ w, int64_t rows, int n,
                                                              float eps, uint16_t* __restrict__ y, int64_t ys) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   if (row >= rows) return;
   const int lane = lane_id();
-  float xv[8], ss = 0.f;
+  // x, g and w of the row all requested first, through buffer resources over the row (an element past n reads
+  // zero), so the wave waits for memory once (behind the range tests, each load was waited on in turn)
+  const rsrc_t xr = make_rsrc(x + row * xs, static_cast<int64_t>(n) * 2), gr = make_rsrc(g + row * gs, static_cast<int64_t>(n) * 2),
+               wr = make_rsrc(w, static_cast<int64_t>(n) * 2);
+  float xv[8], gv[8], wv[8], ss = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = lane + kWave * j;
-    xv[j] = i < n ? bf16_to_f32(x[row * xs + i]) : 0.f;
-    ss = fmaf(xv[j], xv[j], ss);
+    const uint32_t off = i < n ? static_cast<uint32_t>(i) * 2u : kPast;
+    xv[j] = bf16_to_f32(static_cast<uint16_t>(buf2(xr, off)));
+    gv[j] = bf16_to_f32(static_cast<uint16_t>(buf2(gr, off)));
+    wv[j] = bf16_to_f32(static_cast<uint16_t>(buf2(wr, off)));
   }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = fmaf(xv[j], xv[j], ss);
   const float rstd = rsqrtf(wave_sum(ss) / static_cast<float>(n) + eps);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = lane + kWave * j;
-    if (i < n) {
-      const float gv = bf16_to_f32(g[row * gs + i]);
-      y[row * ys + i] = f32_to_bf16(xv[j] * rstd * bf16_to_f32(w[i]) / (1.f + __expf(-gv)));
-    }
+    if (i < n) y[row * ys + i] = f32_to_bf16(xv[j] * rstd * wv[j] / (1.f + __expf(-gv[j])));
   }
 }
 
