@@ -439,21 +439,41 @@ constexpr int kDownWaves = 8;
 #ifndef MM_DOWN_RELOAD_BF16
 #define MM_DOWN_RELOAD_BF16 1
 #endif
+// Rows per lane group of the down kernel: one token (RL1), batches that reload the rows per pair (RLR) and
+// batches that hold them (RLH). Two rows dot every activation chunk a lane loads twice, halving the grid's
+// activation reads; over 28 cold layers, down at int8 2 / 4 tokens 11.3 / 19.3 -> 10.5 / 18.1 us, bf16 4 / 8
+// tokens 25.0 / 41.3 -> 24.0 / 37.7. Holding two int8 rows takes 87 instead of 59 VGPRs (8 tokens 31.3 -> 35.4).
+#ifndef MM_DOWN_RL1_I8
+#define MM_DOWN_RL1_I8 2
+#endif
+#ifndef MM_DOWN_RLR_I8
+#define MM_DOWN_RLR_I8 2
+#endif
+#ifndef MM_DOWN_RLH_I8
+#define MM_DOWN_RLH_I8 1
+#endif
+#ifndef MM_DOWN_RL1_BF16
+#define MM_DOWN_RL1_BF16 1
+#endif
+#ifndef MM_DOWN_RLH_BF16
+#define MM_DOWN_RLH_BF16 2
+#endif
 
-// Grid: row tiles of H (RW = 64 / LPR rows). Wave w takes slots w, w + 8, ... (ONE: each; otherwise the
+// Grid: row tiles of H (RW = 64 / LPR * RL rows: lane group g holds rows g * RL ... g * RL + RL - 1). Wave w takes slots w, w + 8, ... (ONE: each; otherwise the
 // first slot of each distinct expert, with all its pairs), streams the tile's rows of the slot's expert
 // (LPR lanes per row) once, dots them with a[p] of the pairs, rounds to bf16 (after the row scale for int8)
 // into LDS; the workgroup then sums over slots in order per token and adds the residual.
-template <bool Q, int LPR, int NC, bool ONEPASS, bool ONE, bool RELOAD>
+template <bool Q, int LPR, int NC, int RL, bool ONEPASS, bool ONE, bool RELOAD>
 __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs a) {
-  constexpr int RW = kWave / LPR;  // output rows per workgroup
+  static_assert(RL == 1 || ONEPASS, "several rows per lane group need one-pass rows");
+  constexpr int RW = kWave / LPR * RL;  // output rows per workgroup
   constexpr int CE = Q ? 16 : 8;   // weights per 16-byte chunk
   __shared__ float part[kMaxPairs][RW];
   __shared__ float swts[kMaxPairs];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / LPR, s = lane % LPR;
-  const int h = static_cast<int>(blockIdx.x) * RW + g;
+  const int h = static_cast<int>(blockIdx.x) * RW + g * RL;  // the lane group's first row (of RL)
   const bool hok = h < a.H;
   const int64_t nch = a.I / CE;
 
@@ -482,7 +502,7 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
   for (int u = wave; u < a.P; u += kDownWaves) {
     const int e = SCALAR_ID ? slot_expert(a, u) : __builtin_amdgcn_readlane(myid, u);
     if (e < 0) {  // a dropped pair contributes nothing
-      if (s == 0) part[u][g] = 0.f;
+      if (s < RL) part[u][g * RL + s] = 0.f;
       continue;
     }
     unsigned long long pairs = 1ull << u;
@@ -493,8 +513,6 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
     // the expert's down matrix as one resource; this lane group's row starts at byte wrow
     const rsrc_t wr = make_rsrc(static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * (Q ? 1 : 2),
                                 a.H * a.d_sn * (Q ? 1 : 2));
-    const uint32_t wrow = static_cast<uint32_t>((hok ? h : 0) * a.d_sn * (Q ? 1 : 2));
-    float sc = 1.f;
     if constexpr (ONEPASS) {
       // the whole row in registers. RELOAD (one token, int8 batches of up to 4 tokens): loaded with each pair's
       // activations, the later pairs reading it again from cache, so that every load of a pass is in flight at
@@ -503,14 +521,26 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
       // the shared expert's 8 pairs re-reading it cost 1.2 us more than the wait; at 2 / 4 tokens the reload
       // saved 0.5 / 0.3 us). Held across the loop, int8 chunks are kept raw (keep_raw) so that their widening (16
       // floats each, halving the waves per SIMD) is not hoisted out of it.
-      uint4 w[NC];
+      // RL > 1: a lane group holds RL adjacent rows, each activation chunk dotted with all of them
+      uint4 w[RL][NC];
+      float sc[RL];
       auto load_w = [&] {
 #pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const int64_t c = s + static_cast<int64_t>(LPR) * j;
-          w[j] = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
+        for (int r = 0; r < RL; ++r) {
+          const uint32_t wrow = static_cast<uint32_t>((h + r < a.H ? h + r : 0) * a.d_sn * (Q ? 1 : 2));
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            const int64_t c = s + static_cast<int64_t>(LPR) * j;
+            w[r][j] = buf16(wr, c < nch ? wrow + static_cast<uint32_t>(c) * 16u : kPast);
+          }
         }
-        if (Q) sc = scale_at(scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, a.H), hok ? h : 0);
+#pragma unroll
+        for (int r = 0; r < RL; ++r) sc[r] = 1.f;
+        if (Q) {
+          const ScaleRow sr = scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, a.H);
+#pragma unroll
+          for (int r = 0; r < RL; ++r) sc[r] = scale_at(sr, static_cast<uint32_t>(h + r < a.H ? h + r : 0));
+        }
       };
       if (!RELOAD) load_w();
       do {
@@ -527,15 +557,40 @@ __global__ __launch_bounds__(kDownWaves * 64) void decode_down_kernel(DecodeArgs
         // every load above is issued before the first wait: a compiler barrier keeps the scheduler from moving the
         // activation or scale loads past the dots or into the storing lane's branch (a round trip each)
         if (!SCALAR_ID) asm volatile("" ::: "memory");
-        float acc = 0.f;
+        float acc[RL];
 #pragma unroll
-        for (int j = 0; j < NC; ++j) acc = dot_chunk<Q>(w[j], av[j], acc);
-        acc = group_sum<LPR>(acc);
-        if (s == 0 && hok) part[p][g] = round_bf16(Q ? acc * sc : acc);
-        if (Q && !RELOAD) keep_raw(w);
+        for (int r = 0; r < RL; ++r) acc[r] = 0.f;
+        if constexpr (RL == 1) {
+#pragma unroll
+          for (int j = 0; j < NC; ++j) acc[0] = dot_chunk<Q>(w[0][j], av[j], acc[0]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {  // chunk by chunk: one chunk's widened activations live at a time
+#pragma unroll
+            for (int r = 0; r < RL; ++r) acc[r] = dot_chunk<Q>(w[r][j], av[j], acc[r]);
+          }
+        }
+        if constexpr (RL == 1) {
+          const float t = group_sum<LPR>(acc[0]);
+          if (s == 0 && hok) part[p][g] = round_bf16(Q ? t * sc[0] : t);
+        } else {
+          // transposed sums (group_sum's totals, bit for bit): lane s < RL of the group ends with row vi's total
+          group_sums<LPR, RL>(acc);
+          const int vi = sums_index<LPR, RL>(lane);
+          float scv = sc[0];
+#pragma unroll
+          for (int r = 1; r < RL; ++r) scv = vi == r ? sc[r] : scv;
+          if (s < RL && h + vi < a.H) part[p][g * RL + vi] = round_bf16(Q ? acc[0] * scv : acc[0]);
+        }
+        if (Q && !RELOAD) {
+#pragma unroll
+          for (int r = 0; r < RL; ++r) keep_raw(w[r]);
+        }
       } while (!ONE && pairs);
     } else {
       // long rows: passes of LPR * NC chunks per pair (weights re-read from cache for later pairs)
+      const uint32_t wrow = static_cast<uint32_t>((hok ? h : 0) * a.d_sn * (Q ? 1 : 2));
+      float sc = 1.f;
       if (Q) sc = scale_at(scale_row(a.s_d, a.s_dtype, static_cast<int64_t>(e) * a.sd_se, a.H), hok ? h : 0);
       while (pairs) {
         const int p = __ffsll(static_cast<long long>(pairs)) - 1;
@@ -586,19 +641,20 @@ int launch_a(const DecodeArgs& a, hipStream_t st) {
   return mm::check_launch("moe_decode gate_up");
 }
 
-template <bool Q, int LPR, int NC>
+template <bool Q, int LPR, int NC, int RL1 = 1, int RLR = 1, int RLH = 1>
 int launch_b(const DecodeArgs& a, hipStream_t st) {
+  const auto grid = [&](int rw) { return dim3(static_cast<unsigned>((a.H + rw - 1) / rw)); };
   constexpr int RW = kWave / LPR;
-  dim3 grid(static_cast<unsigned>((a.H + RW - 1) / RW));
   const bool onepass = a.I * (Q ? 1 : 2) / 16 <= static_cast<int64_t>(LPR) * NC;
+  const dim3 block(kDownWaves * 64);
   if (onepass && a.n_tokens == 1)
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, true, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, RL1, true, true, true>), grid(RW * RL1), block, 0, st, a);
   else if (onepass && a.n_tokens <= (Q ? MM_DOWN_RELOAD_I8 : MM_DOWN_RELOAD_BF16))
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false, true>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, RLR, true, false, true>), grid(RW * RLR), block, 0, st, a);
   else if (onepass)
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, true, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, RLH, true, false, false>), grid(RW * RLH), block, 0, st, a);
   else
-    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, false, false, false>), grid, dim3(kDownWaves * 64), 0, st, a);
+    hipLaunchKernelGGL((decode_down_kernel<Q, LPR, NC, 1, false, false, false>), grid(RW), block, 0, st, a);
   return mm::check_launch("moe_decode down");
 }
 
@@ -656,10 +712,10 @@ template <bool Q>
 int dispatch_b(const DecodeArgs& a, hipStream_t st) {
   const int64_t nch = a.I * (Q ? 1 : 2) / 16;  // down rows run over the intermediate dim
   if constexpr (Q) {  // int8 chunks carry 32-byte activation chunks: fewer chunks per lane
-    if (nch > 48) return launch_b<Q, MM_DOWN_I8_LPR, MM_DOWN_I8_NC>(a, st);
+    if (nch > 48) return launch_b<Q, MM_DOWN_I8_LPR, MM_DOWN_I8_NC, MM_DOWN_RL1_I8, MM_DOWN_RLR_I8, MM_DOWN_RLH_I8>(a, st);
     return launch_b<Q, 8, 6>(a, st);
   } else {
-    if (nch >= 128) return launch_b<Q, MM_DOWN_BF16_LPR, MM_DOWN_BF16_NC>(a, st);
+    if (nch >= 128) return launch_b<Q, MM_DOWN_BF16_LPR, MM_DOWN_BF16_NC, MM_DOWN_RL1_BF16, 1, MM_DOWN_RLH_BF16>(a, st);
     if (nch > 32) return launch_b<Q, 8, 12>(a, st);
     return launch_b<Q, 8, 4>(a, st);
   }
