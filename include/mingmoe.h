@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define MM_ABI_VERSION 14
+#define MM_ABI_VERSION 15
 
 /* status codes */
 #define MM_OK 0
@@ -184,9 +184,10 @@ int mm_moe_block_decode_noalloc(const void* x, int64_t n_tokens, int64_t x_row_s
  * x [n_tokens, hidden] bf16; ids [n_tokens*nk] (MM_INT32 / MM_INT64, the flat ids given to align; pairs
  * p = t*nk + k whose id lies outside [0, n_slots) contribute nothing); wts fp32 [n_tokens*nk];
  * sorted_ids / bexp / expert_offsets / nb / block_m from mm_align_blocks, block_m = 64 or, for bf16 experts,
- * 128 (mm_prefill_block_m gives the faster one for a shape); a_buf bf16
- * [n_tokens*nk, inter] and part_buf bf16 [n_tokens*nk, hidden] (per-pair expert outputs bf16(a . Wd^T),
- * before the slot weight) are scratch; y bf16 [n_tokens, hidden]. */
+ * 128 (mm_prefill_block_m gives the faster one for a shape); a_buf bf16 [nb*block_m, 64*ceil(inter/64)]
+ * (the gated activations of each expert block in 64-column slabs, [nb][ceil(inter/64)][block_m][64], so that the
+ * down GEMM reads each of its activation slabs as one contiguous piece) and part_buf bf16 [n_tokens*nk, hidden]
+ * (per-pair expert outputs bf16(a . Wd^T), before the slot weight) are scratch; y bf16 [n_tokens, hidden]. */
 /* Rows per expert block the prefill kernels take for a shape (the align padding): 128 for bf16 experts
  * (w_dtype MM_BF16) averaging at least 128 pairs (n_tokens * nk >= 128 * n_slots: each weight slab then
  * feeds twice the MFMA rows), else 64. No counterpart in the reference (its grouped kernels take BM = 64,

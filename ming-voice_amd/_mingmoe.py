@@ -17,7 +17,7 @@ MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
 MM_NORM_ROUND_ONCE = 0x100
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}

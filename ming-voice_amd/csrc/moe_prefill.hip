@@ -70,6 +70,13 @@ constexpr int kSlabRows = MM_SLAB_ROWS;
 constexpr int kSlabRowsI8 = 2 * kSlabRows;
 constexpr int slab_rows(bool q) { return q ? kSlabRowsI8 : kSlabRows; }
 
+// The gated activations a (gate/up output, down input) in 64-column slabs per expert block: [nb][ceil(I/64)][BM][64],
+// so that each A slab of a down tile is one contiguous BM x 128-byte piece (read by 1 KB direct loads, as the weight
+// copies are) instead of BM row pieces scattered by pair index. 0: rows by pair index, [P][I].
+#ifndef MM_PREFILL_A_SLABS
+#define MM_PREFILL_A_SLABS 1
+#endif
+
 struct PrefillArgs {
   const uint16_t* x;
   int64_t xs;
@@ -199,10 +206,12 @@ struct LoadMap {
 };
 
 // Issues the direct loads of slab kt into LDS stage `st` (arow/brow: this thread's source row starts,
-// null for masked rows; k counted in elements; slab kt of a weight row starts kt * bslab elements in).
+// null for masked rows; k counted in elements; slab kt of an activation row starts kt * aslab elements in, of a
+// weight row kt * bslab).
 template <class G>
 __device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K, const LoadMap<G>& m,
-                                           const uint16_t* const* arow, const char* const* brow, int64_t bslab) {
+                                           const uint16_t* const* arow, const char* const* brow, int64_t aslab,
+                                           int64_t bslab) {
   constexpr int ES = G::Q ? 1 : 2;
   char* sa = lds + st * G::STAGE;
   char* sb = sa + G::A_BYTES;
@@ -210,8 +219,8 @@ __device__ __forceinline__ void issue_slab(char* lds, int st, int kt, int64_t K,
   const int64_t k0 = static_cast<int64_t>(kt) * G::BK;
 #pragma unroll
   for (int j = 0; j < G::A_INSTR; ++j) {
-    const int64_t k = k0 + m.ca[j] * 8;
-    const void* src = (arow[j] && k < K) ? static_cast<const void*>(arow[j] + k) : static_cast<const void*>(g_zero_chunk);
+    const int64_t k = k0 + m.ca[j] * 8, ka = kt * aslab + m.ca[j] * 8;
+    const void* src = (arow[j] && k < K) ? static_cast<const void*>(arow[j] + ka) : static_cast<const void*>(g_zero_chunk);
     load_lds16(src, sa + (w * G::A_INSTR + j) * 1024);
   }
 #pragma unroll
@@ -237,12 +246,12 @@ __device__ __forceinline__ int valid_rows(const int* spair, int P) {
 }
 
 // The shared GEMM body: acc[i][j] (i: 16-row fragment of the wave's rows starting at tile row r0, j: its
-// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j; wrow(r) is where weight
-// row r's first slab starts and bslab the elements between its slabs. Row fragments at or
+// 16-column fragments) over K; bcol(j) is the tile row (B row) of column fragment j; xrow(r) / wrow(r) is
+// where activation / weight row r's first slab starts and aslab / bslab the elements between its slabs. Row fragments at or
 // past fm_live (wave-uniform) hold only padding rows: their LDS reads and MFMAs are skipped and their
 // accumulators stay zero (the epilogues store no padding row).
 template <class G, class XRowFn, class WRowFn, class BColFn>
-__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t K, XRowFn xrow,
+__device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t K, XRowFn xrow, int64_t aslab,
                                           WRowFn wrow, int64_t bslab, char* lds, int r0, BColFn bcol, int fm_live) {
   constexpr int NS = G::NS, LOADS = G::LOADS, FM = G::FM, FN = G::FN;
   const int lane = lane_id();
@@ -261,7 +270,7 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
   const int nk = static_cast<int>((K + G::BK - 1) / G::BK);
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue_slab<G>(lds, s, s, K, m, arow, brow, bslab);
+    if (s < nk) issue_slab<G>(lds, s, s, K, m, arow, brow, aslab, bslab);
   for (int kt = 0; kt < nk; ++kt) {
     // slabs issued after kt so far: min(nk - 1 - kt, NS - 2); wait for kt's own loads
     const int pending = min(nk - 1 - kt, NS - 2);
@@ -276,7 +285,7 @@ __device__ __forceinline__ void tile_gemm(floatx4 (&acc)[G::FM][G::FN], int64_t 
     // slab kt visible to all waves; every wave is done with slab kt-1. A plain barrier: the loads of
     // slab kt were waited for above, and a memory fence would also wait for the later slabs' loads.
     __builtin_amdgcn_s_barrier();
-    if (kt + NS - 1 < nk) issue_slab<G>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow, bslab);
+    if (kt + NS - 1 < nk) issue_slab<G>(lds, (kt + NS - 1) % NS, kt + NS - 1, K, m, arow, brow, aslab, bslab);
     const char* sa = lds + (kt % NS) * G::STAGE;
     const char* sb = sa + G::A_BYTES;
     if constexpr (G::Q) {
@@ -354,6 +363,25 @@ __device__ __forceinline__ void store_rows(const uint16_t* ot, int os, const int
   }
 }
 
+// The gated activations of a gate/up tile into the block's slabs (dst: the block's first slab; column col of row r at
+// ((col / 64) * BM + r) * 64 + col % 64): consecutive threads write consecutive 16-byte chunks, so 8 rows of a
+// 64-column slab go out as 1 KB. Padding rows (pair >= P) and chunks past ncols are skipped.
+template <int BM, int NC, int NT>
+__device__ __forceinline__ void store_slab_rows(const uint16_t* ot, int os, const int* spair, int P, uint16_t* dst,
+                                                int64_t col0, int64_t ncols) {
+  constexpr int CPR = NC / 8;
+  static_assert(NC % 8 == 0, "whole chunks");
+#pragma unroll
+  for (int q = threadIdx.x; q < BM * CPR; q += NT) {
+    const int r = q / CPR, cc = q % CPR;
+    const int64_t col = col0 + cc * 8;
+    if (spair[r] < P && col < ncols) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ot + r * os + cc * 8);
+      *reinterpret_cast<u32x4_t*>(dst + ((col >> 6) * BM + r) * 64 + (col & 63)) = v;
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------- gate / up
 
 // SL: the weights are the prefill copy of w_gu (kSlabRows-row pieces), else the row layout.
@@ -391,7 +419,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
   const int g0 = wn * FG * 16;       // first gate column of the wave, relative to n0
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, a.H, xrow, wrow, SL ? R * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
+  tile_gemm<G>(acc, a.H, xrow, G::BK, wrow, SL ? R * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
                [&](int j) { return (j < FG ? 0 : HALF) + g0 + 16 * (j % FG); }, fm_live);
   // the output tile [BM][HALF] goes through LDS (free once every wave is past the last slab), then out in rows
   constexpr int OS = HALF + 8;  // row stride (elements): rows 4 apart start 64 bytes apart on the banks
@@ -428,7 +456,11 @@ __global__ __launch_bounds__(NW * 64) void prefill_gate_up_kernel(PrefillArgs a)
       }
   }
   __syncthreads();
-  store_rows<BM, HALF, NW * 64>(ot, OS, spair, a.P, a.a_buf, I, n0, I);
+  if constexpr (MM_PREFILL_A_SLABS)
+    store_slab_rows<BM, HALF, NW * 64>(ot, OS, spair, a.P, a.a_buf + static_cast<int64_t>(blk) * ((I + 63) / 64) * BM * 64,
+                                       n0, I);
+  else
+    store_rows<BM, HALF, NW * 64>(ot, OS, spair, a.P, a.a_buf, I, n0, I);
 }
 
 // ----------------------------------------------------------------------------------------------- down
@@ -446,9 +478,12 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int64_t H = a.H, I = a.I, h0 = static_cast<int64_t>(nt) * G::BN;
   if (threadIdx.x < BM) spair[threadIdx.x] = a.sorted_ids[static_cast<int64_t>(blk) * BM + threadIdx.x];
   __syncthreads();
+  // the block's slabs of a (row r of slab kt at (kt * BM + r) * 64), or rows by pair index
+  const uint16_t* ablk = a.a_buf + static_cast<int64_t>(blk) * ((I + 63) / 64) * BM * 64;
   auto xrow = [&](int r) -> const uint16_t* {
     const int p = spair[r];
-    return p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
+    if constexpr (MM_PREFILL_A_SLABS) return p < a.P ? ablk + r * 64 : nullptr;
+    else return p < a.P ? a.a_buf + static_cast<int64_t>(p) * I : nullptr;
   };
   constexpr int R = slab_rows(Q);
   const char* wbase = static_cast<const char*>(a.w_d) + static_cast<int64_t>(e) * a.d_se * ES;
@@ -463,8 +498,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_down_kernel(PrefillArgs a) {
   const int c0 = wn * G::FN * 16;
   floatx4 acc[G::FM][G::FN];
   const int fm_live = min(max((valid_rows<BM>(spair, a.P) - r0 + 15) / 16, 0), G::FM);
-  tile_gemm<G>(acc, I, xrow, wrow, SL ? R * G::BK : G::BK, reinterpret_cast<char*>(lds_raw), r0,
-               [&](int j) { return c0 + 16 * j; }, fm_live);
+  tile_gemm<G>(acc, I, xrow, MM_PREFILL_A_SLABS ? BM * 64 : G::BK, wrow, SL ? R * G::BK : G::BK,
+               reinterpret_cast<char*>(lds_raw), r0, [&](int j) { return c0 + 16 * j; }, fm_live);
   // the output tile [BM][BN] goes through LDS, then out in rows (as in gate/up)
   constexpr int OS = G::BN + 8;
   static_assert(static_cast<size_t>(BM) * OS * 2 <= G::LDS, "down output tile must fit in the k-slab LDS");

@@ -182,6 +182,10 @@ def prefill_block_m(n_tokens, kp1, n_slots, w_dtype=torch.bfloat16):
     return int(_mm.load().mm_prefill_block_m(int(n_tokens), int(kp1), int(n_slots), code))
 
 
+def _a_cols(I):
+    return 64 * ((I + 63) // 64)
+
+
 class PrefillScratch:
     """Device buffers of one prefill call (align output and intermediates), reusable across calls of the
     same shape and expert dtype so that a caller can keep them outside the timed or captured region."""
@@ -193,7 +197,8 @@ class PrefillScratch:
         self.sorted_ids = torch.empty(self.nb * self.block_m, dtype=torch.int32, device=device)
         self.bexp = torch.empty(self.nb, dtype=torch.int32, device=device)
         self.offsets = torch.empty(E1 + 1, dtype=torch.int32, device=device)
-        self.a = torch.empty(P, I, device=device, dtype=torch.bfloat16)
+        # the gated activations in 64-column slabs per expert block: [nb][ceil(I/64)][block_m][64]
+        self.a = torch.empty(self.nb * self.block_m, _a_cols(I), device=device, dtype=torch.bfloat16)
         self.part = torch.empty(P, H, device=device, dtype=torch.bfloat16)
         self.y = torch.empty(N, H, device=device, dtype=torch.bfloat16)
         if block:  # router outputs and normalised rows of moe_block_prefill
@@ -234,7 +239,7 @@ def fused_moe_prefill(x, w_gu, w_d, ids, weights, s_gu=None, s_d=None, *, residu
         raise ValueError("fused_moe_prefill: ids must be [N, K+1]")
     wts = weights.reshape(-1).float().contiguous()
     sc = scratch if scratch is not None else PrefillScratch(N, KP1, E1, H, I, x.device, w_dtype=w_gu.dtype)
-    if sc.a.shape != (P, I) or sc.y.shape != (N, H) or sc.offsets.numel() != E1 + 1:
+    if sc.a.shape != (sc.nb * sc.block_m, _a_cols(I)) or sc.y.shape != (N, H) or sc.offsets.numel() != E1 + 1:
         raise ValueError("fused_moe_prefill: scratch was made for another shape")
     if sc.block_m != prefill_block_m(N, KP1, E1, w_gu.dtype):
         raise ValueError("fused_moe_prefill: scratch was made for another expert dtype (PrefillScratch w_dtype)")
@@ -289,7 +294,7 @@ def moe_block_prefill(x, norm_w, eps, w32, w_gu, w_d, *, top_k, bias=None, scori
     if sc.block_m != prefill_block_m(N, NK, ex.n_slots, w_gu.dtype):
         raise ValueError("moe_block_prefill: scratch was made for another expert dtype (PrefillScratch w_dtype)")
     if not hasattr(sc, "xn") or sc.xn.shape != (N, H) or sc.ids.shape != (N, NK) or sc.logits.shape != (N, E) \
-            or sc.a.shape != (N * NK, ex.inter) or sc.offsets.numel() != ex.n_slots + 1:
+            or sc.a.shape != (sc.nb * sc.block_m, _a_cols(ex.inter)) or sc.offsets.numel() != ex.n_slots + 1:
         raise ValueError("moe_block_prefill: scratch was made for another shape (or without block=True)")
     if N == 0:
         return sc.y, sc.ids, sc.wts, sc.logits
