@@ -17,7 +17,7 @@ MM_BF16, MM_FP16, MM_FP32, MM_INT8, MM_INT32, MM_INT64 = range(6)
 MM_SCORE_SIGMOID_GROUP, MM_SCORE_SOFTMAX = 0, 1
 MM_PHASE_ALL, MM_PHASE_GATE_UP, MM_PHASE_DOWN, MM_PHASE_COMBINE = 0, 1, 2, 4
 MM_NORM_ROUND_ONCE = 0x100
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _DTYPES = {torch.bfloat16: MM_BF16, torch.float16: MM_FP16, torch.float32: MM_FP32, torch.int8: MM_INT8,
            torch.int32: MM_INT32, torch.int64: MM_INT64}
@@ -93,6 +93,8 @@ SIGNATURES = {
                              _I64, _P], ctypes.c_int),
     "mm_embed_rows": ([_P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _I64, _P], ctypes.c_int),
     "mm_argmax_rows": ([_P, _I32, _I64, _I64, _I64, _P, _P], ctypes.c_int),
+    "mm_argmax_rows_ws": ([_P, _I32, _I64, _I64, _I64, _P, _P, _I64, _P], ctypes.c_int),
+    "mm_argmax_rows_workspace_bytes": ([_I64, _I64, _I32], ctypes.c_int64),
     "mm_gate_up_slabs_bytes": ([ctypes.POINTER(Experts)], _I64),
     "mm_gate_up_slabs": ([ctypes.POINTER(Experts), _P, _P], ctypes.c_int),
     "mm_down_slabs_bytes": ([ctypes.POINTER(Experts)], _I64),

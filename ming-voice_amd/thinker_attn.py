@@ -24,7 +24,7 @@ import torch
 import _mingmoe as _mm
 
 __all__ = ["fused_recurrent_kda", "kda_workspace", "short_conv", "short_conv_many", "rms_norm_gated", "kda_decode_step", "mla_decode_attn",
-           "mla_attn_workspace", "mla_prefill_attn", "embed_rows", "argmax_rows"]
+           "mla_attn_workspace", "mla_prefill_attn", "embed_rows", "argmax_rows", "argmax_workspace"]
 
 
 def _f32_or_bf16(t, name):
@@ -429,10 +429,20 @@ def embed_rows(table, ids, *, out=None):
     return y
 
 
-def argmax_rows(logits, *, out=None):
+def argmax_workspace(rows, n, dtype=torch.bfloat16, device="cuda"):
+    """Device workspace for argmax_rows over `rows` rows of n logits of `dtype` (the split form)."""
+    nb = int(_mm.load().mm_argmax_rows_workspace_bytes(int(rows), int(n), _mm.dtype_code(torch.empty(0, dtype=dtype))))
+    if nb < 0:
+        raise ValueError("argmax_workspace: rows >= 0, n >= 1 and bf16 / fp32 logits")
+    return torch.empty(max(nb, 16), dtype=torch.uint8, device=device)
+
+
+def argmax_rows(logits, *, out=None, workspace=None):
     """logits.argmax(-1) (engine.py:688) over the last dim of bf16 / fp32 logits [..., n] (last dim contiguous):
     torch's order, the largest value, NaN above every number, the lowest index among equals. Returns int64
-    [...]; out: an int64 device tensor with one element per row (e.g. the [1, 1] token buffer), written in place."""
+    [...]; out: an int64 device tensor with one element per row (e.g. the [1, 1] token buffer), written in place.
+    workspace (from argmax_workspace): the row split over many workgroups, the same results (a long row drawn
+    through one CU is slow); calls sharing a workspace must not overlap."""
     _mm.require_gpu(logits, out)
     if logits.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("argmax_rows: logits must be bf16 or fp32")
@@ -446,6 +456,12 @@ def argmax_rows(logits, *, out=None):
         raise ValueError(f"argmax_rows: out must be a contiguous int64 tensor of {rows} elements")
     lib = _mm.load()
     with _mm.on_device(logits):
-        _mm.check(lib.mm_argmax_rows(_mm.ptr(x2), _mm.dtype_code(x2), rows, n, x2.stride(0) if rows > 1 else n,
-                                     _mm.ptr(y), _mm.stream_of(logits)), "argmax_rows")
+        if workspace is None:
+            _mm.check(lib.mm_argmax_rows(_mm.ptr(x2), _mm.dtype_code(x2), rows, n, x2.stride(0) if rows > 1 else n,
+                                         _mm.ptr(y), _mm.stream_of(logits)), "argmax_rows")
+        else:
+            _mm.require_gpu(workspace)
+            _mm.check(lib.mm_argmax_rows_ws(_mm.ptr(x2), _mm.dtype_code(x2), rows, n, x2.stride(0) if rows > 1 else n,
+                                            _mm.ptr(y), _mm.ptr(workspace), workspace.numel() * workspace.element_size(),
+                                            _mm.stream_of(logits)), "argmax_rows")
     return y

@@ -110,6 +110,8 @@ class FastThinkerStep:
         dev = self.embed.device
         self.H = self.embed.shape[1]
         self.h_in = torch.empty(1, 1, self.H, device=dev, dtype=self.embed.dtype)
+        # the argmax of the logits split over many workgroups (sized for fp32 logits, which need the most)
+        self.amx_ws = TA.argmax_workspace(1, self.head.shape[0], torch.float32, dev)
         self.L = [self._layer(li, layer, cache_layers[li]) for li, layer in enumerate(layers)]
         # router outputs and gated activations, shared by the layers (a layer reads them before the next writes)
         nk = max(p["blk"]["top_k"] for p in self.L) + 1 if self.L else 1
@@ -351,7 +353,7 @@ class FastThinkerStep:
                 out.append((h_in, hm.clone(), rid.clone(), rw.clone()))
         last = h[-1:] if nv is None else TA.embed_rows(h, (nv - 1).clamp_(min=0))
         logits = self.head_logits(last)
-        TA.argmax_rows(logits, out=self.tok)
+        TA.argmax_rows(logits, out=self.tok, workspace=self.amx_ws)
         self.pos.add_(T if nv is None else nv)
         return (logits, out) if trace else logits
 
@@ -362,7 +364,7 @@ class FastThinkerStep:
         for li in range(len(self.L)):
             h = self.moe(li, self.mixer(li, h))
         logits = self.head_logits(h)
-        TA.argmax_rows(logits, out=self.tok)
+        TA.argmax_rows(logits, out=self.tok, workspace=self.amx_ws)
         self.pos.add_(1)
         return logits
 
@@ -377,6 +379,6 @@ class FastThinkerStep:
             nk = self.L[li]["blk"]["top_k"] + 1
             out.append((h_in, hm.clone(), self.ids[:, :nk].clone(), self.wts[:, :nk].clone()))
         logits = self.head_logits(h)
-        TA.argmax_rows(logits, out=self.tok)
+        TA.argmax_rows(logits, out=self.tok, workspace=self.amx_ws)
         self.pos.add_(1)
         return out, h, logits

@@ -118,6 +118,10 @@ def test_argument_validation_reports_messages():
     assert "bf16 or fp32" in _err(lib.mm_argmax_rows(P, mm.MM_INT8, 1, 64, 64, P, None))
     assert "n=0" in _err(lib.mm_argmax_rows(P, mm.MM_BF16, 1, 0, 64, P, None))
     assert "row stride" in _err(lib.mm_argmax_rows(P, mm.MM_FP32, 2, 64, 32, P, None))
+    assert lib.mm_argmax_rows_workspace_bytes(1, 126464, mm.MM_BF16) == 31 * 8
+    assert lib.mm_argmax_rows_workspace_bytes(1, 0, mm.MM_BF16) == -1
+    assert "workspace of 8 bytes" in _err(lib.mm_argmax_rows_ws(P, mm.MM_BF16, 1, 126464, 126464, P, P, 8, None))
+    assert "null pointer" in _err(lib.mm_argmax_rows_ws(P, mm.MM_BF16, 1, 126464, 126464, P, None, 1024, None))
     assert "int32 or int64" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 64, 64, P, mm.MM_FP32, 1, P, 64, None))
     assert "16-byte aligned" in _err(lib.mm_embed_rows(P, mm.MM_BF16, 100, 12, 12, P, mm.MM_INT64, 1, P, 12, None))
     assert "bf16, fp16 or fp32" in _err(lib.mm_embed_rows(P, mm.MM_INT8, 100, 64, 64, P, mm.MM_INT64, 1, P, 64, None))

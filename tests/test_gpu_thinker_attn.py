@@ -855,6 +855,9 @@ def test_argmax_rows_matches_torch_argmax(dtype):
         x[4] = 0.5
         got = TA.argmax_rows(x.to(DEV)).cpu()
         assert torch.equal(got, x.argmax(-1)), (n, got, x.argmax(-1))
+        ws = TA.argmax_workspace(5, n, dtype, DEV)  # the split form (one workgroup below 2 x 512 pieces)
+        got = TA.argmax_rows(x.to(DEV), workspace=ws).cpu()
+        assert torch.equal(got, x.argmax(-1)), (n, got, x.argmax(-1))
         if n > 8:  # rows not 16-byte aligned: the scalar path
             xv = x.to(DEV)[:, 1:]
             assert torch.equal(TA.argmax_rows(xv).cpu(), x[:, 1:].argmax(-1)), n
@@ -862,6 +865,14 @@ def test_argmax_rows_matches_torch_argmax(dtype):
     x = torch.randn(1, 126464, generator=g).to(dtype)
     TA.argmax_rows(x.to(DEV), out=tok)
     assert int(tok) == int(x.argmax())
+    # the split form: the maximum planted in each workgroup's range in turn and at both ends, ties across ranges
+    ws = TA.argmax_workspace(1, 126464, dtype, DEV)
+    for pos in (0, 4095, 4096, 4097, 60000, 126463):
+        y = x.clone()
+        y[0, pos] = 100.0
+        y[0, (pos + 70001) % 126464] = 100.0  # a tie: the lower index wins
+        TA.argmax_rows(y.to(DEV), out=tok, workspace=ws)
+        assert int(tok) == int(y.argmax()), pos
 
 
 @pytest.mark.parametrize("dtype,id_dtype", [(torch.bfloat16, torch.int64), (torch.float32, torch.int32)])
