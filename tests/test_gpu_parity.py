@@ -415,6 +415,44 @@ def test_prefill_and_decode_ragged_shapes(int8):
         close(y, ref)
 
 
+@pytest.mark.parametrize("int8", [False, True])
+def test_prefill_phases_and_block_slab_layout(int8):
+    """The prefill run as its three phases on one scratch (gate/up, then down, then combine, each a call of its own)
+    equals the one call bit for bit; and the gated activations sit in the scratch in 64-column slabs per expert
+    block, [nb][ceil(I/64)][block_m][64] with row r of block b holding pair sorted_ids[b * block_m + r]: rebuilt in
+    pair order they match the oracle's, on ragged dims (inter 208: a partial last slab, a partial column tile)."""
+    H, I, E, K, n = 1536, 208, 32, 6, 90
+    w_gu = W.normal((E + 1, 2 * I, H), 0.02, 140, DEV)
+    w_d = W.normal((E + 1, H, I), 0.02, 141, DEV)
+    g = torch.Generator().manual_seed(142)
+    sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
+    ids = torch.cat([sel, torch.full((n, 1), E)], 1).to(DEV)
+    wts = torch.cat([torch.rand(n, K, generator=g), torch.ones(n, 1)], 1).to(DEV)
+    x = W.normal((n, H), 1.0, 143, DEV)
+    kw = {}
+    if int8:
+        w_gu, kw["s_gu"] = fused_moe.quantize_rows_int8(w_gu, scale_dtype=torch.float32)
+        w_d, kw["s_d"] = fused_moe.quantize_rows_int8(w_d, scale_dtype=torch.float32)
+    sc1 = fused_moe.PrefillScratch(n, K + 1, E + 1, H, I, DEV, w_dtype=w_gu.dtype)
+    y1 = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts, scratch=sc1, **kw).clone()
+    sc2 = fused_moe.PrefillScratch(n, K + 1, E + 1, H, I, DEV, w_dtype=w_gu.dtype)
+    for ph, al in ((_mingmoe.MM_PHASE_GATE_UP, True), (_mingmoe.MM_PHASE_DOWN, False),
+                   (_mingmoe.MM_PHASE_COMBINE, False)):
+        y2 = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts, scratch=sc2, phases=ph, align=al, **kw)
+    assert torch.equal(y1, y2)
+    P, BM, nb, nsl = n * (K + 1), sc1.block_m, sc1.nb, (I + 63) // 64
+    assert sc1.a.shape == (nb * BM, nsl * 64)
+    rows = sc1.a.view(nb, nsl, BM, 64).permute(0, 2, 1, 3).reshape(nb * BM, nsl * 64)[:, :I]
+    sid = sc1.sorted_ids.long()
+    valid = sid < P
+    assert int(valid.sum()) == P  # every pair has one row
+    a = torch.zeros(P, I, dtype=BF, device=DEV)
+    a[sid[valid]] = rows[valid]
+    s_gu, s_d = (kw["s_gu"].cpu(), kw["s_d"].cpu()) if int8 else (None, None)
+    _, a_ref = O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu(), s_gu, s_d, return_a=True)
+    close(a, a_ref)
+
+
 def test_prefill_ragged_shapes_128_pair_blocks():
     """The 128-pair blocks (bf16 experts averaging at least 128 pairs: 700 tokens x 7 slots over 33 slots) on
     ragged dims: hidden 1536, inter 208 (a partial 128-column tile and a partial 64-wide k slab), so the
