@@ -204,6 +204,30 @@ def test_decode_int8_batches(blk, n, sdt):
     close(y, _oracle_moe(c, xn, ids, wts, int8=True))
 
 
+@pytest.mark.parametrize("n", [1, 2, 4, 8])
+@pytest.mark.parametrize("int8", [False, True])
+def test_decode_dropped_pairs_contribute_nothing(blk, n, int8):
+    """Pairs whose id lies outside the stack (-1, or the slot count 65) contribute nothing, as the oracle's zero
+    rows, in every form of the down kernel: one token, batches that reload the expert rows per pair and batches
+    that hold them, one or two rows per lane group; one slot of every token dropped, and a whole token's slots."""
+    b, cpu = blk
+    x = W.tokens(n, seed=70 + n, device=DEV)
+    xn, ids, wts = _route_tokens(b, x)
+    ids = ids.clone()
+    ids[:, 1] = -1
+    ids[:, 4] = 65
+    if n > 1:
+        ids[n - 1, :] = -1
+    if int8:
+        y = fused_moe.fused_moe_decode(xn, b["q_gu"], b["q_d"], ids, wts, s_gu=b["s_gu"], s_d=b["s_d"], residual=x)
+    else:
+        y = fused_moe.fused_moe_decode(xn, b["w_gu"], b["w_d"], ids, wts, residual=x)
+    ref = _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu())
+    close(y, ref)
+    if n > 1:  # the token with every slot dropped keeps its residual alone: bf16(0) + x
+        assert torch.equal(y[n - 1].cpu(), x[n - 1].cpu())
+
+
 @pytest.mark.parametrize("n,int8", [(1, False), (3, False), (1, True), (2, True), (4, True), (8, True)])
 def test_moe_block_decode_matches_unfused_and_oracle(blk, n, int8):
     """The three-kernel decode block equals rms_norm -> moe_route -> fused_moe_decode(residual=x) bit for bit
@@ -413,6 +437,27 @@ def test_prefill_and_decode_ragged_shapes(int8):
             y = fused_moe.fused_moe_prefill(x, w_gu, w_d, ids, wts)
             ref = O.moe(x.cpu(), w_gu.cpu(), w_d.cpu(), ids.cpu(), wts.cpu())
         close(y, ref)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_prefill_dropped_pairs_contribute_nothing(blk, int8):
+    """Prefill pairs whose id lies outside the stack (-1, 65) contribute nothing (align leaves them out of every
+    expert block), as the oracle's zero rows; tokens with every slot dropped keep their residual alone."""
+    b, cpu = blk
+    n = 100
+    x = W.tokens(n, seed=80, device=DEV)
+    xn, ids, wts = _route_tokens(b, x)
+    ids = ids.clone()
+    ids[::3, 2] = -1
+    ids[1::4, 5] = 65
+    ids[7, :] = 65
+    ids[50, :] = -1
+    if int8:
+        y = fused_moe.fused_moe_prefill(xn, b["q_gu"], b["q_d"], ids, wts, s_gu=b["s_gu"], s_d=b["s_d"], residual=x)
+    else:
+        y = fused_moe.fused_moe_prefill(xn, b["w_gu"], b["w_d"], ids, wts, residual=x)
+    close(y, _oracle_moe(cpu, xn, ids, wts, int8=int8, residual=x.cpu()))
+    assert torch.equal(y[7].cpu(), x[7].cpu()) and torch.equal(y[50].cpu(), x[50].cpu())
 
 
 @pytest.mark.parametrize("int8", [False, True])
