@@ -418,8 +418,8 @@ int mm_argmax_rows(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t 
 /* mm_argmax_rows with the row split over many workgroups (one CU draws a long row only at the rate its outstanding
  * lines allow; the LM head's 126464 logits take 17 us that way) and a second launch merging their partial results,
  * same results. workspace: device memory of mm_argmax_rows_workspace_bytes(rows, n, x_dtype) bytes, 16-byte aligned
- * (-1: bad arguments); calls that share a workspace must not overlap. Rows that are short, not 16-byte aligned or
- * not a whole number of 16-byte pieces take mm_argmax_rows. No counterpart in the reference beyond
+ * (-1: bad arguments); calls that share a workspace must not overlap; rows <= 65535. Rows that are short, not
+ * 16-byte aligned or not a whole number of 16-byte pieces take mm_argmax_rows. No counterpart in the reference beyond
  * logits.argmax(-1) (engine.py:688). */
 int64_t mm_argmax_rows_workspace_bytes(int64_t rows, int64_t n, int x_dtype);
 int mm_argmax_rows_ws(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t x_row_stride, int64_t* out,
